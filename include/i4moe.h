@@ -1,0 +1,200 @@
+/*
+ * i4moe.h -- C ABI of the MI355X (gfx950) int4 clock-path library.
+ *
+ * One shared library (libi4moe.so) replaces the quantized compute that runs
+ * Qwen3-Omni Thinker layers 0-23 in thecodacus/qwen3-omni-duplex:
+ *
+ *   - the int4 dequant-GEMV   (src/duplex/streaming/triton_dequant_gemv.py:32-113)
+ *   - the packed Linear       (src/duplex/streaming/triton_dequant_gemv.py:125-159)
+ *   - the fused int4 MoE block (src/duplex/streaming/fused_packed_moe.py:83-275)
+ *
+ * Conventions shared by every entry point:
+ *   - all functions are extern "C" and return int: 0 = I4_OK, < 0 = error code
+ *     (i4_strerror() turns it into a static string);
+ *   - the library never allocates, frees or synchronises: outputs and
+ *     workspaces are caller memory, work is only enqueued on `stream`
+ *     (so every call can be captured into a hipGraph);
+ *   - every pointer is a device pointer unless stated otherwise and must be
+ *     16-byte aligned when it points to packed weights or activations;
+ *   - shapes are validated on the host before anything is launched; an
+ *     invalid call launches nothing;
+ *   - an expert id outside [0, E) is never dereferenced: the affected output
+ *     rows are written as NaN (the reference faults with an illegal address,
+ *     src/duplex/streaming/fused_packed_moe.py:227-229).
+ *
+ * Weight formats (W is the logical [N out][K in] matrix of y = W x):
+ *   I4_LAYOUT_CT  -- compressed-tensors "pack-quantized", the reference's own
+ *                    format (src/duplex/quant/dequant.py:23-27,
+ *                    src/duplex/streaming/fused_packed_moe.py:7-11,54-65):
+ *                      packed [E][N][K/8] int32, column k = 8m+i of a row is
+ *                             nibble i (bits 4i..4i+3) of word m;
+ *                      scale  [E][N][NG],  NG = ceil(K/group);
+ *                      zeros  NULL (symmetric, zero point 8, the reference) or
+ *                             [E][N][ceil(NG/8)] int32, group g in nibble g%8
+ *                             of word g/8.
+ *                    value = (nibble - zero) * scale.
+ *   I4_LAYOUT_AWQ -- AutoAWQ GEMM packing:
+ *                      qweight [E][K][N/8] int32, nibble slot i of word w holds
+ *                             column 8w + {0,2,4,6,1,3,5,7}[i];
+ *                      qzeros  [E][NG][N/8] int32, same packing;
+ *                      scales  [E][NG][N].
+ */
+#ifndef I4MOE_H
+#define I4MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define I4_ABI_VERSION 1
+
+/* status codes */
+#define I4_OK               0
+#define I4_ERR_NULL        -1  /* a required pointer is NULL                     */
+#define I4_ERR_SHAPE       -2  /* dimension out of range or inconsistent         */
+#define I4_ERR_DTYPE       -3  /* unsupported element type                       */
+#define I4_ERR_ALIGN       -4  /* pointer not 16-byte aligned                    */
+#define I4_ERR_LAYOUT      -5  /* unsupported packed layout for this entry point */
+#define I4_ERR_GROUP       -6  /* group size not a multiple of 32                */
+#define I4_ERR_WORKSPACE   -7  /* workspace missing or too small                 */
+#define I4_ERR_LAUNCH      -8  /* the HIP runtime rejected a kernel launch       */
+#define I4_ERR_STRIDE      -9  /* expert stride smaller than one expert          */
+
+/* element types */
+#define I4_F32  0
+#define I4_F16  1
+#define I4_BF16 2
+
+/* packed layouts */
+#define I4_LAYOUT_CT  0
+#define I4_LAYOUT_AWQ 1
+
+/* One stacked int4 weight: E experts of a [N][K] matrix.  E = 1 is a plain
+ * Linear.  *_estride are element strides between experts; 0 means densely
+ * stacked.  Mirrors the (packed, scale) pair that
+ * src/duplex/streaming/fused_packed_moe.py:68-80 (_stack_packed) builds, plus
+ * the optional zero points of the AWQ format. */
+typedef struct i4_qweight {
+  const int32_t* packed;
+  const void*    scale;
+  const int32_t* zeros;
+  int64_t        packed_estride;
+  int64_t        scale_estride;
+  int64_t        zeros_estride;
+  int32_t        layout;       /* I4_LAYOUT_*                        */
+  int32_t        group;        /* quantisation group along K, %32==0 */
+  int32_t        scale_dtype;  /* I4_F32 / I4_F16 / I4_BF16          */
+  int32_t        E, N, K;
+} i4_qweight;
+
+/* One Thinker MoE block in the internal (CT) layout, as FusedPackedMoE stores
+ * it (src/duplex/streaming/fused_packed_moe.py:112,117-122,166-169). */
+typedef struct i4_moe_weights {
+  i4_qweight  gate_up;    /* [E][2I][H]: rows [0,I) gate_proj, [I,2I) up_proj */
+  i4_qweight  down;       /* [E][H][I]                                       */
+  const void* router_w;   /* [E][H] dense, in the activation dtype; may be
+                             NULL when logits are passed to i4_moe_forward    */
+} i4_moe_weights;
+
+int         i4_abi_version(void);
+const char* i4_strerror(int code);
+
+/* dequant_gemv (src/duplex/streaming/triton_dequant_gemv.py:85-113):
+ *   out[j][n] = sum_k W[sel[j]][n][k] * x[j * x_stride + k],  j < k_sel
+ * x_stride = 0 shares one activation row across the selected experts (the
+ * gate_up call, fused_packed_moe.py:255); x_stride = K gives each expert its
+ * own row (the down call, fused_packed_moe.py:261).  Accumulation is fp32.
+ * out is [k_sel][N] in out_dtype (I4_F32 matches the reference).  The AWQ
+ * layout needs a workspace of i4_dq_gemv_workspace_bytes(); CT needs none. */
+int    i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride,
+                  const i4_qweight* w, const int32_t* sel, int k_sel,
+                  void* out, int out_dtype,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t i4_dq_gemv_workspace_bytes(const i4_qweight* w, int k_sel);
+
+/* TritonPackedLinear.forward (src/duplex/streaming/triton_dequant_gemv.py:151-159):
+ *   y[m][n] = sum_k W[n][k] * x[m][k] (+ bias[n]),  m < M, expert 0 of w.
+ * One launch for all M rows (the reference launches once per row).  bias is
+ * nullable and in y_dtype. */
+int    i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w,
+                 const void* bias, void* y, int y_dtype,
+                 void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t i4_linear_workspace_bytes(const i4_qweight* w, int M);
+
+/* unpack4 (src/duplex/streaming/fused_packed_moe.py:54-65): raw nibbles of
+ * every expert in logical [E][N][K] order as uint8 0..15 (the reference's
+ * signed value is nibble - 8).  Same device decode as the GEMV kernels. */
+int    i4_unpack(const i4_qweight* w, uint8_t* out, hipStream_t stream);
+
+/* FusedPackedMoE._dequant (src/duplex/streaming/fused_packed_moe.py:183-189):
+ * dense [E][N][K] = (nibble - zero) * scale, computed in fp32 and rounded
+ * once to out_dtype. */
+int    i4_dequant(const i4_qweight* w, void* out, int out_dtype, hipStream_t stream);
+
+/* Load-time repack of an AWQ weight into the CT layout with explicit zeros
+ * (the kernel-native format).  Writes expert e of src into rows
+ * [row_offset, row_offset + src->N) of a CT destination that has dst_rows
+ * rows per expert; dst_scale is in src->scale_dtype.  Used to build the
+ * gate|up concatenation of fused_packed_moe.py:122 from AWQ experts. */
+int    i4_repack_awq_to_ct(const i4_qweight* src, int32_t* dst_packed, void* dst_scale,
+                           int32_t* dst_zeros, int dst_rows, int row_offset,
+                           hipStream_t stream);
+
+/* Router half of FusedPackedMoE.forward (fused_packed_moe.py:195):
+ *   logits[t][e] = sum_h x[t][h] * router_w[e][h], fp32 accumulation,
+ * rounded to x_dtype like the reference's half-precision gate Linear. */
+int    i4_router_logits(const void* x, int x_dtype, int T, int H,
+                        const void* router_w, int E, void* logits, hipStream_t stream);
+
+/* Routing (fused_packed_moe.py:195-199): softmax in fp32 over E logits,
+ * top-k, optional renormalisation.  Ties are broken by the lower expert id.
+ * sel [T][topk] int32 (descending weight); w_f32 [T][topk] (nullable);
+ * w_half [T][topk] in w_half_dtype (nullable; the reference's w.to(x.dtype)). */
+int    i4_route_topk(const void* logits, int logits_dtype, int T, int E, int topk,
+                     int renorm, int32_t* sel, float* w_f32, void* w_half,
+                     int w_half_dtype, hipStream_t stream);
+
+/* FusedPackedMoE.forward (fused_packed_moe.py:191-263), hidden states in and
+ * out, optional residual: out[t] = residual[t] + sum_j w[t][j] * down(
+ * silu(gate(x[t])) * up(x[t]))_{sel[t][j]}.  Routing comes from
+ * weights->router_w, or from `logits` ([T][E], x_dtype) when router_w is
+ * NULL.  The activation is rounded to x_dtype between the two projections as
+ * in the reference (fused_packed_moe.py:257); everything else is fp32 and the
+ * output is rounded once to x_dtype.  sel_out / w_out (nullable) receive the
+ * routing.  Both weights must be in the CT layout. */
+int    i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weights,
+                      int topk, int renorm, const void* logits, const void* residual,
+                      void* out, int32_t* sel_out, float* w_out,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
+
+/* The two expert stages of one decode token with routing already known --
+ * the body of the reference's per-token loop (fused_packed_moe.py:231-263):
+ *   i4_moe_gate_up:      act[j][:] = silu(gate_e(x)) * up_e(x), e = sel[j],
+ *                        rounded to x_dtype (fused_packed_moe.py:255-257);
+ *   i4_moe_down_combine: out = residual + sum_j w[j] * down_{sel[j]}(act[j])
+ *                        (fused_packed_moe.py:261-262), fixed j order.
+ * x, residual and out are [H]; act is [topk][I]; sel [topk]; w [topk] fp32. */
+int    i4_moe_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up,
+                      const int32_t* sel, int topk, void* act, hipStream_t stream);
+int    i4_moe_down_combine(const void* act, int x_dtype, const i4_qweight* down,
+                           const int32_t* sel, const float* w, int topk,
+                           const void* residual, void* out, hipStream_t stream);
+
+/* The Thinker[0:24] MoE stack of src/duplex/streaming/clock.py:168-171 with
+ * only the MoE blocks and residual adds kept: h <- h + moe_l(h) for
+ * l < n_layers.  x and out are [T][H]; x is not modified. */
+int    i4_moe_stack_forward(const void* x, int x_dtype, int T,
+                            const i4_moe_weights* layers, int n_layers, int topk,
+                            int renorm, void* out, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+size_t i4_moe_stack_workspace_bytes(int T, int H, int I, int E, int topk);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* I4MOE_H */

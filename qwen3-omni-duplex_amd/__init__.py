@@ -1,0 +1,26 @@
+"""MI355X (gfx950) int4 clock-path kernels for Qwen3-Omni Thinker layers 0-23.
+
+Drop-in replacements for thecodacus/qwen3-omni-duplex's quantized compute:
+  dequant_gemv           <- src/duplex/streaming/triton_dequant_gemv.py:85
+  PackedLinear           <- TritonPackedLinear (:125), patch_attention (:162)
+  FusedPackedMoE         <- src/duplex/streaming/fused_packed_moe.py:83
+  fuse_packed_moe_blocks <- fused_packed_moe.py:278
+all executed by the hand-written HIP kernels of libi4moe.so (C ABI in
+include/i4moe.h).  There is no fallback: without the built library every op
+raises.
+"""
+from . import _lib
+from .linear import PackedLinear, patch_attention
+from .moe import FusedPackedMoE, fuse_packed_moe_blocks
+from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_forward, moe_gate_up,
+                  moe_stack, route, router_logits, unpack4, unpack_nibbles, Workspace)
+from .weights import QWeight, repack_awq_to_ct
+
+lib = _lib.lib
+
+__all__ = [
+    "QWeight", "repack_awq_to_ct", "dequant_gemv", "linear", "unpack4", "unpack_nibbles",
+    "dequant", "router_logits", "route", "moe_forward", "moe_gate_up", "moe_down_combine",
+    "moe_stack", "Workspace",
+    "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "patch_attention", "lib",
+]

@@ -1,0 +1,251 @@
+// Device helpers shared by every gfx950 kernel of libi4moe.
+//
+// Nibble decode.  A CT word holds columns k0..k0+7 in nibbles 0..7.  The
+// expression (w >> 4p) & 0x000F000F moves nibble p to bits 0..3 and nibble
+// p+4 to bits 16..19; OR-ing the exponent pattern of a half-precision M turns
+// the two 16-bit lanes into the exact values M + q (M = 1024 for fp16, whose
+// ulp there is 1; M = 128 for bf16, whose ulp there is 1 as well).  One
+// v_and_or_b32 (plus a shift for p > 0) therefore yields a (k0+p, k0+p+4)
+// pair ready for v_dot2_f32_{f16,bf16}, which multiplies exactly and
+// accumulates in fp32.  The bias M and the zero point z are removed per
+// 32-column chunk with the chunk's activation sum S:
+//     sum (q - z) x = sum (M + q) x - (M + z) S.
+// Activations are staged once per workgroup in LDS, already permuted into the
+// same (k0+p, k0+p+4) pair order, together with the chunk sums S.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "i4moe.h"
+
+namespace i4 {
+
+typedef unsigned int u32;
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte global load (global_load_dwordx4) of a packed-weight stream
+__device__ inline u32x4 ldg16(const void* p) { return *(const u32x4*)p; }
+
+// ---------------------------------------------------------------------------
+// half-precision codecs, selected by the I4_F16 / I4_BF16 dtype code
+template <int DT> struct Half;
+
+template <> struct Half<I4_F16> {
+  static constexpr u32 MAGIC2 = 0x64006400u;  // two fp16 1024.0
+  static constexpr float MAGIC = 1024.0f;
+  __device__ static inline float to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+  }
+  __device__ static inline uint16_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+  __device__ static inline float dot2(u32 a, u32 b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a),
+                                  __builtin_bit_cast(f16x2, b), c, false);
+  }
+};
+
+template <> struct Half<I4_BF16> {
+  static constexpr u32 MAGIC2 = 0x43004300u;  // two bf16 128.0
+  static constexpr float MAGIC = 128.0f;
+  __device__ static inline float to_f32(uint16_t b) {
+    return __builtin_bit_cast(float, (u32)b << 16);
+  }
+  __device__ static inline uint16_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+  }
+  __device__ static inline float dot2(u32 a, u32 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), c, false);
+  }
+};
+
+// scale element of any supported dtype, widened to fp32
+template <int ST> __device__ inline float load_scale(const void* p, int64_t i) {
+  if constexpr (ST == I4_F32) {
+    return ((const float*)p)[i];
+  } else {
+    return Half<ST>::to_f32(((const uint16_t*)p)[i]);
+  }
+}
+
+// Raw scale bits, loaded now and widened later so that a load never has to
+// be waited for before the next one is issued.
+template <int ST> __device__ inline u32 load_scale_raw(const void* p, int64_t i) {
+  if constexpr (ST == I4_F32) return ((const u32*)p)[i];
+  else return (u32)((const uint16_t*)p)[i];
+}
+template <int ST> __device__ inline float scale_from_raw(u32 r) {
+  if constexpr (ST == I4_F32) return __builtin_bit_cast(float, r);
+  else return Half<ST>::to_f32((uint16_t)r);
+}
+
+// Zero-point words of a symmetric weight (every nibble 8).  Kernels read
+// zeros through a pointer that is either the caller's zeros or this table
+// with zero strides, so the zero load is branch-free.  64 words cover
+// K <= 16384 at group 32.  Kept non-const so it lives in the global address
+// space and a select between it and a kernel argument stays a global load.
+static __device__ u32 kSymZeros[64] = {
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u,
+    0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+
+// One 32-column chunk of one CT row: 4 packed words, its group's raw scale
+// and the zero word holding its group's zero point.
+struct Chunk {
+  u32x4 w;
+  u32 s, z;
+};
+
+// CT row view: packed row, scale row, zero row (already offset to the row)
+struct RowPtr {
+  const int32_t* p;
+  const void* s;
+  const u32* z;
+};
+
+template <int ST> __device__ inline const void* scale_at(const void* p, int64_t i) {
+  return (const char*)p + i * (ST == I4_F32 ? 4 : 2);
+}
+
+template <int ST>
+__device__ inline Chunk load_chunk(const RowPtr& r, int c, int gshift) {
+  Chunk k;
+  const int g = c >> gshift;
+  k.w = *(const u32x4*)(r.p + 4 * c);
+  k.s = load_scale_raw<ST>(r.s, g);
+  k.z = r.z[g >> 3];
+  return k;
+}
+
+// store one fp32 result in the requested output dtype
+template <int OT> __device__ inline void store_out(void* p, int64_t i, float v) {
+  if constexpr (OT == I4_F32) {
+    ((float*)p)[i] = v;
+  } else {
+    ((uint16_t*)p)[i] = Half<OT>::from_f32(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// nibble decode + dot: 8 columns of one CT word against 4 staged x pairs
+template <int XT> __device__ inline float dot8(u32 w, u32x4 xp, float acc) {
+  constexpr u32 MK = 0x000F000Fu, MG = Half<XT>::MAGIC2;
+  acc = Half<XT>::dot2((w & MK) | MG, xp.x, acc);
+  acc = Half<XT>::dot2(((w >> 4) & MK) | MG, xp.y, acc);
+  acc = Half<XT>::dot2(((w >> 8) & MK) | MG, xp.z, acc);
+  acc = Half<XT>::dot2(((w >> 12) & MK) | MG, xp.w, acc);
+  return acc;
+}
+
+// sum over one chunk of (q - z) * s * x given the staged x words of the chunk
+// (xw0..xw3, pair order) and their sum S
+template <int XT, int ST>
+__device__ inline float chunk_dot(const Chunk& k, u32x4 xw0, u32x4 xw1, u32x4 xw2, u32x4 xw3,
+                                  float S, int c, int gshift) {
+  float a = 0.f;
+  a = dot8<XT>(k.w.x, xw0, a);
+  a = dot8<XT>(k.w.y, xw1, a);
+  a = dot8<XT>(k.w.z, xw2, a);
+  a = dot8<XT>(k.w.w, xw3, a);
+  const int g = c >> gshift;
+  const float z = (float)((k.z >> (4 * (g & 7))) & 15u);
+  return scale_from_raw<ST>(k.s) * (a - (Half<XT>::MAGIC + z) * S);
+}
+
+// Permute 8 consecutive half-precision x values (one 16-byte load, dwords
+// d = (x0,x1),(x2,x3),(x4,x5),(x6,x7)) into the decode pair order
+// (x0,x4),(x1,x5),(x2,x6),(x3,x7).  v_perm_b32 picks bytes of {src0:src1}.
+__device__ inline u32x4 pair_order(u32x4 d) {
+  u32x4 r;
+  r.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
+  r.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
+  r.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
+  r.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+  return r;
+}
+
+// fp32 sum of the 8 half values of one 16-byte load
+template <int XT> __device__ inline float sum8(u32x4 d) {
+  float s = 0.f;
+  s += Half<XT>::to_f32((uint16_t)(d.x & 0xFFFF));
+  s += Half<XT>::to_f32((uint16_t)(d.x >> 16));
+  s += Half<XT>::to_f32((uint16_t)(d.y & 0xFFFF));
+  s += Half<XT>::to_f32((uint16_t)(d.y >> 16));
+  s += Half<XT>::to_f32((uint16_t)(d.z & 0xFFFF));
+  s += Half<XT>::to_f32((uint16_t)(d.z >> 16));
+  s += Half<XT>::to_f32((uint16_t)(d.w & 0xFFFF));
+  s += Half<XT>::to_f32((uint16_t)(d.w >> 16));
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// cross-lane sums over aligned groups of L lanes (L a power of two <= 64);
+// every lane of the group ends with the group total.
+template <int CTRL> __device__ inline float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+template <int L> __device__ inline float group_sum(float v) {
+  if constexpr (L >= 2) v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+  if constexpr (L >= 4) v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) v += dpp_mov<0x141>(v);   // row_half_mirror
+  if constexpr (L >= 16) v += dpp_mov<0x140>(v);  // row_mirror
+  if constexpr (L >= 32)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v),
+                                                                0x401F));  // xor 16
+  if constexpr (L >= 64) {
+    const int src = ((int)__lane_id() ^ 32) << 2;
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, v)));
+  }
+  return v;
+}
+
+// Stage nr activation rows (row r starts at row_of(r), K halves each) into
+// LDS in decode pair order with per-chunk sums:
+//   xs [nr][4][C] uint4 (word jw of chunk c of row r at (r*4 + jw)*C + c),
+//   xsum [nr][C].
+// Up to 4 loads per thread are in flight before the first LDS write.
+template <int XT, class RowOf>
+__device__ inline void stage_rows(RowOf row_of, int nr, int K, u32x4* xs, float* xsum) {
+  const int C = K >> 5, words = K >> 3, total = nr * words;
+  const int nt = blockDim.x;
+  for (int i0 = 0; i0 < total; i0 += 4 * nt) {
+    u32x4 d[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = min(i0 + u * nt + (int)threadIdx.x, total - 1);
+      const int r = idx / words, m = idx - r * words;
+      d[u] = ldg16(row_of(r) + 8 * m);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = i0 + u * nt + (int)threadIdx.x;
+      if (idx < total) {  // total and nt are multiples of 4: quads are all in or all out
+        const int r = idx / words, m = idx - r * words;
+        const int c = m >> 2, jw = m & 3;
+        xs[(r * 4 + jw) * C + c] = pair_order(d[u]);
+        const float sm = group_sum<4>(sum8<XT>(d[u]));
+        if (jw == 0) xsum[r * C + c] = sm;
+      }
+    }
+  }
+}
+
+__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+
+
+}  // namespace i4

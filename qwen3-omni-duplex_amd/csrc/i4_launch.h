@@ -1,0 +1,29 @@
+// Host-side helpers shared between the translation units of libi4moe.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "i4moe.h"
+
+// log2(group) - 5: group index of 32-column chunk c is c >> shift
+inline int i4_group_shift(int group) {
+  int sh = 0;
+  while ((32 << sh) < group) ++sh;
+  return sh;
+}
+
+// Validate a weight descriptor; on success *norm holds a copy whose zero
+// expert strides are replaced by the dense ones.
+int i4_check_weight(const i4_qweight* w, i4_qweight* norm);
+
+// Launch the CT dequant-GEMV: out[j][n] = W[sel[j] or 0] x[j*x_stride] (+bias).
+int i4_launch_gemv_ct(const void* x, int xt, int64_t x_stride, const i4_qweight* w,
+                      const int32_t* sel, int k_sel, void* out, int ot, const void* bias,
+                      hipStream_t s);
+
+// Launch router logits / top-k without re-validating (callers validated).
+int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr, int E,
+                            void* logits, hipStream_t s);
+int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
+                   float* wf, void* wh, int wht, hipStream_t s);

@@ -1,0 +1,724 @@
+// Fused int4 MoE block for gfx950 (replaces FusedPackedMoE.forward,
+// src/duplex/streaming/fused_packed_moe.py:191-263).
+//
+// Decode (T = 1), four launches:
+//   router logits -> top-k -> k_moe_gate_up<direct> -> k_moe_down_m1
+// k_moe_gate_up computes gate row n and up row n of one selected expert in
+// the same lanes, so silu(g) * u happens in registers and only the half-
+// precision activation [topk][I] is written (the reference writes fp32
+// [8][1536] and runs split / silu / mul / cast as separate kernels,
+// fused_packed_moe.py:255-257).  k_moe_down_m1 gives each workgroup a slice of
+// output rows across ALL selected experts, so the routing-weighted combine and
+// the residual add happen in LDS in a fixed expert order: no atomics, the
+// result is bit-reproducible run to run.
+//
+// Prefill / chunks (T > 1):
+//   router logits -> top-k -> k_group -> k_moe_gate_up<list> ->
+//   k_moe_down_list -> k_moe_combine
+// k_group sorts the T*topk (token, slot) pairs by expert (stable in token
+// order) and cuts each expert's tokens into entries of at most MT tokens, so
+// each weight row is streamed once per entry instead of once per token (the
+// reference loops over tokens, fused_packed_moe.py:231).
+#include "i4_common.h"
+#include "i4_launch.h"
+
+namespace i4 {
+
+static constexpr int WG = 256;
+static constexpr int MT_LIST = 4;    // tokens per entry in the grouped GEMV path
+static constexpr int TCHUNK = 1024;  // tokens handled by one pass of the pipeline
+static constexpr size_t kMaxLds = 65536;  // dynamic LDS per workgroup
+
+struct QW {  // device view of one CT weight
+  const int32_t* packed;
+  const void* scale;
+  const int32_t* zeros;
+  int64_t pes, ses, zes;
+  int gshift, E, N, K;
+};
+
+// row n of expert e (both already clamped to valid values)
+template <int ST> __device__ inline RowPtr row_ptr(const QW& w, int e, int n) {
+  const int C = w.K >> 5, KW = w.K >> 3;
+  const int NG = (C + (1 << w.gshift) - 1) >> w.gshift, NZW = (NG + 7) >> 3;
+  RowPtr r;
+  r.p = w.packed + e * w.pes + (int64_t)n * KW;
+  r.s = scale_at<ST>(w.scale, e * w.ses + (int64_t)n * NG);
+  r.z = w.zeros ? (const u32*)w.zeros + e * w.zes + (int64_t)n * NZW : kSymZeros;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// gate_up + SiLU.  L lanes per row pair (gate row n, up row I + n); a
+// workgroup owns WG/L consecutive row pairs of one entry (one expert and up
+// to MT of its tokens).  DIRECT: entry j is slot j of token 0 (decode).
+template <int XT, int ST, int L, int MT, bool DIRECT>
+__global__ __launch_bounds__(WG) void k_moe_gate_up(
+    const uint16_t* __restrict__ x, int topk, const int32_t* __restrict__ sel,
+    const int4* __restrict__ entries, const int* __restrict__ n_entries,
+    const int32_t* __restrict__ perm, QW w, int I, uint16_t* __restrict__ act) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  constexpr int RPW = WG / L;
+  constexpr int ROUND = 2;
+  const int H = w.K, C = H >> 5;
+  const int cpl = (C + L - 1) / L;
+  u32x4* xs = (u32x4*)lds;
+  float* xsum = (float*)(lds + (size_t)MT * H * 2);
+
+  int e, pos0, cnt;
+  if constexpr (DIRECT) {
+    e = sel[blockIdx.y];
+    pos0 = blockIdx.y;
+    cnt = 1;
+  } else {
+    if ((int)blockIdx.y >= *n_entries) return;
+    const int4 en = entries[blockIdx.y];
+    e = en.x;
+    pos0 = en.y;
+    cnt = en.z;
+  }
+  const int rl = threadIdx.x / L, cl = threadIdx.x % L;
+  const int n = blockIdx.x * RPW + rl;
+  const bool rv = n < I;
+  if ((unsigned)e >= (unsigned)w.E) {
+    if (rv && cl == 0)
+      for (int t = 0; t < cnt; ++t)
+        act[(int64_t)(pos0 + t) * I + n] = Half<XT>::from_f32(__builtin_nanf(""));
+    return;
+  }
+  const int nn = rv ? n : 0;
+  const RowPtr rg = row_ptr<ST>(w, e, nn), ru = row_ptr<ST>(w, e, I + nn);
+
+  float ag[MT], au[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) ag[t] = au[t] = 0.f;
+  for (int r0 = 0; r0 < cpl; r0 += ROUND) {
+    Chunk cg[ROUND], cu[ROUND];
+#pragma unroll
+    for (int i = 0; i < ROUND; ++i) {
+      const int c = min(cl + (r0 + i) * L, C - 1);
+      cg[i] = load_chunk<ST>(rg, c, w.gshift);
+      cu[i] = load_chunk<ST>(ru, c, w.gshift);
+    }
+    if (r0 == 0) {
+      if constexpr (DIRECT) {
+        stage_rows<XT>([&](int) { return x; }, 1, H, xs, xsum);
+      } else {
+        stage_rows<XT>([&](int t) { return x + (int64_t)(perm[pos0 + min(t, cnt - 1)] / topk) * H; },
+                       MT, H, xs, xsum);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < ROUND; ++i) {
+      const int c = cl + (r0 + i) * L;
+      if (c < C) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if (t < cnt) {
+            const u32x4* xt = xs + (size_t)t * 4 * C;
+            const u32x4 x0 = xt[c], x1 = xt[C + c], x2 = xt[2 * C + c], x3 = xt[3 * C + c];
+            const float S = xsum[t * C + c];
+            ag[t] += chunk_dot<XT, ST>(cg[i], x0, x1, x2, x3, S, c, w.gshift);
+            au[t] += chunk_dot<XT, ST>(cu[i], x0, x1, x2, x3, S, c, w.gshift);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const float g = group_sum<L>(ag[t]);
+    const float u = group_sum<L>(au[t]);
+    if (rv && cl == 0 && t < cnt)
+      act[(int64_t)(pos0 + t) * I + n] = Half<XT>::from_f32(silu(g) * u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode down projection + routing-weighted combine + residual (T = 1).
+// Lane groups of L lanes; RW output rows per workgroup; the GPR groups of a
+// row split the selected experts (j = gi, gi + GPR, ...).  Every weight load
+// of a round (all experts of the group x CR chunks) is issued before the
+// activations are staged, so one HBM latency covers the whole workgroup.
+template <int L> struct DownShape {
+  static constexpr int NGR = 256 / L;
+  static constexpr int GPR = NGR >= 8 ? NGR / 8 : 1;
+  static constexpr int RW = NGR / GPR;
+};
+
+template <int XT, int ST, int L, int JMAX>
+__global__ __launch_bounds__(WG) void k_moe_down_m1(
+    const uint16_t* __restrict__ act, int topk, const int32_t* __restrict__ sel,
+    const float* __restrict__ wts, QW w, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ out) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  constexpr int GPR = DownShape<L>::GPR, RW = DownShape<L>::RW;
+  constexpr int CR = 4;  // chunks per round
+  const int I = w.K, H = w.N, C = I >> 5;
+  const int cpl = (C + L - 1) / L;
+  u32x4* xs = (u32x4*)lds;
+  float* xsum = (float*)(lds + (size_t)topk * I * 2);
+  float* red = xsum + topk * C;  // [topk][RW]
+
+  static_assert(L * RW >= 64, "the expert group must be uniform across a wave");
+  const int gi = threadIdx.x / L, cl = threadIdx.x % L;
+  const int r = gi % RW;
+  const int jg = __builtin_amdgcn_readfirstlane(gi / RW);  // wave-uniform: sel[] via s_load
+  const int n = blockIdx.x * RW + r;
+  const bool rv = n < H;
+  const int nn = rv ? n : 0;
+
+  int ej[JMAX];
+  RowPtr rp[JMAX];
+#pragma unroll
+  for (int jj = 0; jj < JMAX; ++jj) {
+    const int j = jg + jj * GPR;
+    ej[jj] = j < topk ? sel[j] : -1;
+    const int ee = (unsigned)ej[jj] < (unsigned)w.E ? ej[jj] : 0;
+    rp[jj] = row_ptr<ST>(w, ee, nn);
+  }
+  float row[JMAX];
+#pragma unroll
+  for (int jj = 0; jj < JMAX; ++jj) row[jj] = 0.f;
+
+  for (int r0 = 0; r0 < cpl; r0 += CR) {
+    Chunk ch[JMAX][CR];
+#pragma unroll
+    for (int jj = 0; jj < JMAX; ++jj)
+#pragma unroll
+      for (int i = 0; i < CR; ++i)
+        ch[jj][i] = load_chunk<ST>(rp[jj], min(cl + (r0 + i) * L, C - 1), w.gshift);
+    if (r0 == 0) {  // all selected activation rows, contiguous act[j][I]
+      stage_rows<XT>([&](int j) { return act + (int64_t)j * I; }, topk, I, xs, xsum);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int jj = 0; jj < JMAX; ++jj) {
+      const int j = jg + jj * GPR;
+      if (j < topk) {
+        const u32x4* xj = xs + (size_t)j * 4 * C;
+#pragma unroll
+        for (int i = 0; i < CR; ++i) {
+          const int c = cl + (r0 + i) * L;
+          if (c < C)
+            row[jj] += chunk_dot<XT, ST>(ch[jj][i], xj[c], xj[C + c], xj[2 * C + c], xj[3 * C + c],
+                                         xsum[j * C + c], c, w.gshift);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int jj = 0; jj < JMAX; ++jj) {
+    const int j = jg + jj * GPR;
+    const float v = group_sum<L>(row[jj]);
+    if (j < topk && cl == 0)
+      red[j * RW + r] = (unsigned)ej[jj] < (unsigned)w.E ? v : __builtin_nanf("");
+  }
+  __syncthreads();
+  if (threadIdx.x < RW) {
+    const int rr = threadIdx.x, on = blockIdx.x * RW + rr;
+    if (on < H) {
+      const float res = residual ? Half<XT>::to_f32(residual[on]) : 0.f;
+      float y = 0.f;
+      for (int j = 0; j < topk; ++j) y += wts[j] * red[j * RW + rr];
+      out[on] = Half<XT>::from_f32(res + y);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// grouped down projection: ys[slot][n] (fp32) for the tokens of one entry
+template <int XT, int ST, int L, int MT>
+__global__ __launch_bounds__(WG) void k_moe_down_list(
+    const uint16_t* __restrict__ act, const int4* __restrict__ entries,
+    const int* __restrict__ n_entries, const int32_t* __restrict__ perm, QW w,
+    float* __restrict__ ys) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  constexpr int RPW = WG / L;
+  constexpr int ROUND = 4;
+  const int I = w.K, H = w.N, C = I >> 5;
+  const int cpl = (C + L - 1) / L;
+  u32x4* xs = (u32x4*)lds;
+  float* xsum = (float*)(lds + (size_t)MT * I * 2);
+  if ((int)blockIdx.y >= *n_entries) return;
+  const int4 en = entries[blockIdx.y];
+  const int e = en.x, pos0 = en.y, cnt = en.z;
+  const int rl = threadIdx.x / L, cl = threadIdx.x % L;
+  const int n = blockIdx.x * RPW + rl;
+  const bool rv = n < H;
+  if ((unsigned)e >= (unsigned)w.E) {
+    if (rv && cl == 0)
+      for (int t = 0; t < cnt; ++t) ys[(int64_t)perm[pos0 + t] * H + n] = __builtin_nanf("");
+    return;
+  }
+  const RowPtr rp = row_ptr<ST>(w, e, rv ? n : 0);
+  float acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = 0.f;
+  for (int r0 = 0; r0 < cpl; r0 += ROUND) {
+    Chunk ch[ROUND];
+#pragma unroll
+    for (int i = 0; i < ROUND; ++i) ch[i] = load_chunk<ST>(rp, min(cl + (r0 + i) * L, C - 1), w.gshift);
+    if (r0 == 0) {
+      stage_rows<XT>([&](int t) { return act + (int64_t)(pos0 + min(t, cnt - 1)) * I; }, MT, I, xs,
+                     xsum);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < ROUND; ++i) {
+      const int c = cl + (r0 + i) * L;
+      if (c < C) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if (t < cnt) {
+            const u32x4* xt = xs + (size_t)t * 4 * C;
+            acc[t] += chunk_dot<XT, ST>(ch[i], xt[c], xt[C + c], xt[2 * C + c], xt[3 * C + c],
+                                        xsum[t * C + c], c, w.gshift);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const float y = group_sum<L>(acc[t]);
+    if (rv && cl == 0 && t < cnt) ys[(int64_t)perm[pos0 + t] * H + n] = y;
+  }
+}
+
+// out[t][n] = residual[t][n] + sum_j w[t][j] * ys[t*topk + j][n], j ascending
+template <int XT>
+__global__ __launch_bounds__(WG) void k_moe_combine(const float* __restrict__ ys,
+                                                    const float* __restrict__ wts,
+                                                    const int32_t* __restrict__ sel, int T,
+                                                    int topk, int E, int H,
+                                                    const uint16_t* __restrict__ residual,
+                                                    uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
+  if (i >= (int64_t)T * H) return;
+  const int t = (int)(i / H), n = (int)(i - (int64_t)t * H);
+  float y = 0.f;
+  for (int j = 0; j < topk; ++j) {
+    const int s = t * topk + j;
+    const float v = (unsigned)sel[s] < (unsigned)E ? ys[(int64_t)s * H + n] : __builtin_nanf("");
+    y += wts[s] * v;
+  }
+  const float r = residual ? Half<XT>::to_f32(residual[i]) : 0.f;
+  out[i] = Half<XT>::from_f32(r + y);
+}
+
+// ---------------------------------------------------------------------------
+// Sort (token, slot) pairs by expert, stable in token order, and cut them
+// into entries of <= mt tokens.  One workgroup of 1024 threads.
+//   bits[e][w]: bit b set <=> token 32w + b selected expert e
+//   pre [e][w]: popcount of bits[e][0..w)
+__global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel, int T, int topk,
+                                                int E, int mt, int32_t* __restrict__ perm,
+                                                int4* __restrict__ entries,
+                                                int* __restrict__ n_entries) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int TW = (T + 31) >> 5;
+  u32* bits = (u32*)lds;
+  u32* pre = bits + E * TW;
+  int* cnt = (int*)(pre + E * TW);
+  int* off = cnt + E;       // [E + 1]
+  int* eoff = off + E + 1;  // [E + 1]
+  const int tid = threadIdx.x, nt = blockDim.x;
+  for (int i = tid; i < E * TW; i += nt) bits[i] = 0u;
+  __syncthreads();
+  for (int s = tid; s < T * topk; s += nt) {
+    const int e = sel[s], t = s / topk;
+    if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * TW + (t >> 5)], 1u << (t & 31));
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += nt) {
+    int run = 0;
+    for (int wd = 0; wd < TW; ++wd) {
+      pre[e * TW + wd] = (u32)run;
+      run += __popc(bits[e * TW + wd]);
+    }
+    cnt[e] = run;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int o = 0, eo = 0;
+    for (int e = 0; e < E; ++e) {
+      off[e] = o;
+      eoff[e] = eo;
+      o += cnt[e];
+      eo += (cnt[e] + mt - 1) / mt;
+    }
+    off[E] = o;
+    eoff[E] = eo;
+    *n_entries = eo;
+  }
+  __syncthreads();
+  for (int s = tid; s < T * topk; s += nt) {
+    const int e = sel[s], t = s / topk;
+    if ((unsigned)e < (unsigned)E) {
+      const u32 word = bits[e * TW + (t >> 5)];
+      const int below = __popc(word & ((1u << (t & 31)) - 1u));
+      perm[off[e] + (int)pre[e * TW + (t >> 5)] + below] = s;
+    }
+  }
+  for (int e = tid; e < E; e += nt) {
+    const int c = cnt[e];
+    for (int q = 0; q * mt < c; ++q)
+      entries[eoff[e] + q] = int4{e, off[e] + q * mt, min(mt, c - q * mt), 0};
+  }
+}
+
+}  // namespace i4
+
+// ===========================================================================
+// host side
+using namespace i4;
+
+namespace {
+
+inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct MoeWs {
+  void* logits;
+  int32_t* sel;
+  float* w;
+  uint16_t* act;
+  float* ys;
+  int32_t* perm;
+  int4* entries;
+  int* n_entries;
+  size_t bytes;
+};
+
+MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
+  const int Tc = T < TCHUNK ? T : TCHUNK;
+  const size_t Tk = (size_t)Tc * topk;
+  MoeWs m;
+  size_t o = 0;
+  auto take = [&](size_t b) {
+    void* p = base ? (char*)base + o : nullptr;
+    o += al256(b);
+    return p;
+  };
+  m.logits = take((size_t)Tc * E * 2);
+  m.sel = (int32_t*)take(Tk * 4);
+  m.w = (float*)take(Tk * 4);
+  m.act = (uint16_t*)take(Tk * I * 2);
+  m.ys = Tc > 1 ? (float*)take(Tk * H * 4) : nullptr;
+  m.perm = (int32_t*)take(Tk * 4);
+  m.entries = (int4*)take((E + Tk) * sizeof(int4));
+  m.n_entries = (int*)take(4);
+  m.bytes = o;
+  return m;
+}
+
+// lanes per output row of the down projections (8..64, 3+ chunks per lane
+// when the row is long enough)
+inline int lanes_per_row(int C) {
+  int L = 8;
+  while (L * 2 <= C && L < 64) L *= 2;
+  while (L > 8 && C < 3 * L) L /= 2;
+  return L;
+}
+
+QW to_qw(const i4_qweight& w) {
+  QW q;
+  q.packed = w.packed;
+  q.scale = w.scale;
+  q.zeros = w.zeros;
+  q.pes = w.packed_estride;
+  q.ses = w.scale_estride;
+  q.zes = w.zeros_estride;
+  q.gshift = i4_group_shift(w.group);
+  q.E = w.E;
+  q.N = w.N;
+  q.K = w.K;
+  return q;
+}
+
+// gate_up lanes: prefer 2 chunks per lane so a decode layer spreads over
+// ~3 workgroups per CU (H = 2048: L = 32, 8 row pairs per workgroup)
+inline int gate_up_lanes(int C) {
+  int L = 8;
+  while (L < 64 && C >= 4 * L) L *= 2;
+  return L;
+}
+
+template <int XT, int ST, int MT, bool DIRECT>
+int launch_gate_up_t(int L, dim3 grid, size_t lds, hipStream_t s, const uint16_t* x, int topk,
+                     const int32_t* sel, const int4* ent, const int* nent, const int32_t* perm,
+                     const QW& w, int I, uint16_t* act) {
+#define I4_GU_CASE(L_)                                                                           \
+  if (L == L_) {                                                                                 \
+    hipLaunchKernelGGL((k_moe_gate_up<XT, ST, L_, MT, DIRECT>), grid, dim3(WG), lds, s, x, topk, \
+                       sel, ent, nent, perm, w, I, act);                                         \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                              \
+  }
+  I4_GU_CASE(8) I4_GU_CASE(16) I4_GU_CASE(32) I4_GU_CASE(64)
+#undef I4_GU_CASE
+  return I4_ERR_SHAPE;
+}
+
+template <int XT, int ST>
+int launch_gate_up_dt(bool direct, int n_entries, const void* x, int topk, const int32_t* sel,
+                      const int4* ent, const int* nent, const int32_t* perm, const QW& w, int I,
+                      void* act, hipStream_t s) {
+  const int H = w.K, C = H / 32;
+  const int L = gate_up_lanes(C);
+  const int rpw = WG / L;
+  dim3 grid((I + rpw - 1) / rpw, n_entries);
+  const size_t lds = (size_t)(direct ? 1 : MT_LIST) * (H * 2 + C * 4);
+  if (lds > kMaxLds) return I4_ERR_SHAPE;
+  if (direct)
+    return launch_gate_up_t<XT, ST, 1, true>(L, grid, (size_t)H * 2 + C * 4, s,
+                                             (const uint16_t*)x, topk, sel, ent, nent, perm, w,
+                                             I, (uint16_t*)act);
+  return launch_gate_up_t<XT, ST, MT_LIST, false>(L, grid, (size_t)MT_LIST * (H * 2 + C * 4), s,
+                                                  (const uint16_t*)x, topk, sel, ent, nent, perm,
+                                                  w, I, (uint16_t*)act);
+}
+
+template <int XT, int ST>
+int launch_down_m1_t(const void* act, int topk, const int32_t* sel, const float* wts,
+                     const QW& w, const void* res, void* out, hipStream_t s) {
+  const int I = w.K, C = I / 32;
+  const int L = lanes_per_row(C);
+  const size_t lds_base = (size_t)topk * (I * 2 + C * 4);
+#define I4_DN_CASE(L_, J_)                                                                     \
+  if (L == L_ && (topk + DownShape<L_>::GPR - 1) / DownShape<L_>::GPR <= J_) {                 \
+    constexpr int RW = DownShape<L_>::RW;                                                      \
+    const size_t lds = lds_base + (size_t)topk * RW * 4;                                       \
+    if (lds > kMaxLds) return I4_ERR_SHAPE;                                                    \
+    hipLaunchKernelGGL((k_moe_down_m1<XT, ST, L_, J_>), dim3((w.N + RW - 1) / RW), dim3(WG),   \
+                       lds, s, (const uint16_t*)act, topk, sel, wts, w, (const uint16_t*)res,  \
+                       (uint16_t*)out);                                                        \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                            \
+  }
+  I4_DN_CASE(8, 2) I4_DN_CASE(16, 2) I4_DN_CASE(8, 4) I4_DN_CASE(16, 4) I4_DN_CASE(32, 8)
+  I4_DN_CASE(64, 8)
+#undef I4_DN_CASE
+  return I4_ERR_SHAPE;
+}
+
+template <int XT, int ST>
+int launch_down_list_t(int max_entries, const void* act, const int4* ent, const int* nent,
+                       const int32_t* perm, const QW& w, float* ys, hipStream_t s) {
+  const int I = w.K, C = I / 32;
+  const int L = lanes_per_row(C);
+  const size_t lds = (size_t)MT_LIST * (I * 2 + C * 4);
+  if (lds > kMaxLds) return I4_ERR_SHAPE;
+  const int rpw = WG / L;
+  dim3 grid((w.N + rpw - 1) / rpw, max_entries);
+#define I4_DL_CASE(L_)                                                                      \
+  if (L == L_) {                                                                            \
+    hipLaunchKernelGGL((k_moe_down_list<XT, ST, L_, MT_LIST>), grid, dim3(WG), lds, s,      \
+                       (const uint16_t*)act, ent, nent, perm, w, ys);                       \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                         \
+  }
+  I4_DL_CASE(8) I4_DL_CASE(16) I4_DL_CASE(32) I4_DL_CASE(64)
+#undef I4_DL_CASE
+  return I4_ERR_SHAPE;
+}
+
+// the three MoE projections dispatched on (activation dtype, scale dtype)
+struct MoeOps {
+  int (*gate_up)(bool, int, const void*, int, const int32_t*, const int4*, const int*,
+                 const int32_t*, const QW&, int, void*, hipStream_t);
+  int (*down_m1)(const void*, int, const int32_t*, const float*, const QW&, const void*, void*,
+                 hipStream_t);
+  int (*down_list)(int, const void*, const int4*, const int*, const int32_t*, const QW&, float*,
+                   hipStream_t);
+};
+
+template <int XT, int ST> constexpr MoeOps moe_ops() {
+  return MoeOps{&launch_gate_up_dt<XT, ST>, &launch_down_m1_t<XT, ST>,
+                &launch_down_list_t<XT, ST>};
+}
+
+bool pick_ops(int xt, int gst, int dst, MoeOps* ops) {
+  if (gst != dst) return false;
+#define I4_OPS(XT_, ST_)                 \
+  if (xt == XT_ && gst == ST_) {         \
+    *ops = moe_ops<XT_, ST_>();          \
+    return true;                         \
+  }
+  I4_OPS(I4_F16, I4_F32) I4_OPS(I4_F16, I4_F16) I4_OPS(I4_F16, I4_BF16)
+  I4_OPS(I4_BF16, I4_F32) I4_OPS(I4_BF16, I4_F16) I4_OPS(I4_BF16, I4_BF16)
+#undef I4_OPS
+  return false;
+}
+
+int check_moe(const i4_moe_weights* mw, int x_dtype, int T, int topk, i4_qweight* gu,
+              i4_qweight* dn) {
+  if (!mw) return I4_ERR_NULL;
+  int rc = i4_check_weight(&mw->gate_up, gu);
+  if (rc) return rc;
+  rc = i4_check_weight(&mw->down, dn);
+  if (rc) return rc;
+  if (gu->layout != I4_LAYOUT_CT || dn->layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  const int H = gu->K, I = dn->K, E = gu->E;
+  if (gu->N != 2 * I || dn->N != H || dn->E != E) return I4_ERR_SHAPE;
+  if (T < 1 || E > 512 || topk < 1 || topk > E || topk > 16) return I4_ERR_SHAPE;
+  if (H > 4096 || I > 4096) return I4_ERR_SHAPE;
+  return I4_OK;
+}
+
+int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_qweight& gu,
+              const i4_qweight& dn, int topk, int renorm, const void* logits, const void* residual,
+              void* out, int32_t* sel_out, float* w_out, const MoeWs& ws, hipStream_t s) {
+  const int H = gu.K, I = dn.K, E = gu.E;
+  MoeOps ops;
+  if (!pick_ops(xt, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
+  int rc;
+  const void* lg = logits;
+  if (mw->router_w) {
+    rc = i4_launch_router_logits(x, xt, T, H, mw->router_w, E, ws.logits, s);
+    if (rc) return rc;
+    lg = ws.logits;
+  }
+  int32_t* sel = sel_out ? sel_out : ws.sel;
+  float* wts = w_out ? w_out : ws.w;
+  rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
+  if (rc) return rc;
+  const QW qgu = to_qw(gu), qdn = to_qw(dn);
+  if (T == 1) {
+    rc = ops.gate_up(true, topk, x, topk, sel, nullptr, nullptr, nullptr, qgu, I, ws.act, s);
+    if (rc) return rc;
+    return ops.down_m1(ws.act, topk, sel, wts, qdn, residual, out, s);
+  }
+  const int Tk = T * topk;
+  const int TW = (T + 31) / 32;
+  const size_t glds = (size_t)2 * E * TW * 4 + (size_t)(3 * E + 2) * 4;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E, MT_LIST, ws.perm,
+                     ws.entries, ws.n_entries);
+  if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
+  const int max_entries = (E < Tk ? E : Tk) + Tk / MT_LIST;
+  rc = ops.gate_up(false, max_entries, x, topk, sel, ws.entries, ws.n_entries, ws.perm, qgu, I,
+                   ws.act, s);
+  if (rc) return rc;
+  rc = ops.down_list(max_entries, ws.act, ws.entries, ws.n_entries, ws.perm, qdn, ws.ys, s);
+  if (rc) return rc;
+  const int64_t tot = (int64_t)T * H;
+  dim3 cg((unsigned)((tot + WG - 1) / WG));
+  if (xt == I4_F16)
+    hipLaunchKernelGGL(k_moe_combine<I4_F16>, cg, dim3(WG), 0, s, ws.ys, wts, sel, T, topk, E, H,
+                       (const uint16_t*)residual, (uint16_t*)out);
+  else
+    hipLaunchKernelGGL(k_moe_combine<I4_BF16>, cg, dim3(WG), 0, s, ws.ys, wts, sel, T, topk, E,
+                       H, (const uint16_t*)residual, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk) {
+  if (T < 1 || H < 1 || I < 1 || E < 1 || topk < 1) return 0;
+  return carve(nullptr, T, H, I, E, topk).bytes;
+}
+
+int i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weights, int topk,
+                   int renorm, const void* logits, const void* residual, void* out,
+                   int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
+  i4_qweight gu, dn;
+  int rc = check_moe(weights, x_dtype, T, topk, &gu, &dn);
+  if (rc) return rc;
+  if (!x || !out) return I4_ERR_NULL;
+  if (!weights->router_w && !logits) return I4_ERR_NULL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)out & 15) || ((uintptr_t)residual & 15))
+    return I4_ERR_ALIGN;
+  const int H = gu.K, I = dn.K, E = gu.E;
+  if (H % 8 || I % 8) return I4_ERR_SHAPE;
+  const MoeWs need = carve(nullptr, T, H, I, E, topk);
+  if (!workspace || workspace_bytes < need.bytes) return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  const MoeWs ws = carve(workspace, T, H, I, E, topk);
+  for (int t0 = 0; t0 < T; t0 += TCHUNK) {
+    const int Tc = T - t0 < TCHUNK ? T - t0 : TCHUNK;
+    const char* xs = (const char*)x + (size_t)t0 * H * 2;
+    const void* lg = logits ? (const char*)logits + (size_t)t0 * E * 2 : nullptr;
+    const void* rs = residual ? (const char*)residual + (size_t)t0 * H * 2 : nullptr;
+    void* os = (char*)out + (size_t)t0 * H * 2;
+    rc = moe_chunk(xs, x_dtype, Tc, weights, gu, dn, topk, renorm, lg, rs, os,
+                   sel_out ? sel_out + (size_t)t0 * topk : nullptr,
+                   w_out ? w_out + (size_t)t0 * topk : nullptr, ws, stream);
+    if (rc) return rc;
+  }
+  return I4_OK;
+}
+
+int i4_moe_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up, const int32_t* sel,
+                   int topk, void* act, hipStream_t stream) {
+  i4_qweight gu;
+  int rc = i4_check_weight(gate_up, &gu);
+  if (rc) return rc;
+  if (gu.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (!x || !sel || !act) return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  if (topk < 1 || topk > 65535 || gu.N % 2 || gu.K > 4096) return I4_ERR_SHAPE;
+  if (((uintptr_t)x & 15) || ((uintptr_t)act & 15)) return I4_ERR_ALIGN;
+  MoeOps ops;
+  if (!pick_ops(x_dtype, gu.scale_dtype, gu.scale_dtype, &ops)) return I4_ERR_DTYPE;
+  return ops.gate_up(true, topk, x, topk, sel, nullptr, nullptr, nullptr, to_qw(gu), gu.N / 2,
+                     act, stream);
+}
+
+int i4_moe_down_combine(const void* act, int x_dtype, const i4_qweight* down, const int32_t* sel,
+                        const float* w, int topk, const void* residual, void* out,
+                        hipStream_t stream) {
+  i4_qweight dn;
+  int rc = i4_check_weight(down, &dn);
+  if (rc) return rc;
+  if (dn.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (!act || !sel || !w || !out) return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  if (topk < 1 || topk > 16 || dn.K > 4096) return I4_ERR_SHAPE;
+  if (((uintptr_t)act & 15) || ((uintptr_t)out & 15) || ((uintptr_t)residual & 15))
+    return I4_ERR_ALIGN;
+  MoeOps ops;
+  if (!pick_ops(x_dtype, dn.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
+  return ops.down_m1(act, topk, sel, w, to_qw(dn), residual, out, stream);
+}
+
+size_t i4_moe_stack_workspace_bytes(int T, int H, int I, int E, int topk) {
+  const size_t m = i4_moe_workspace_bytes(T, H, I, E, topk);
+  if (!m) return 0;
+  return m + al256((size_t)T * H * 2);
+}
+
+int i4_moe_stack_forward(const void* x, int x_dtype, int T, const i4_moe_weights* layers,
+                         int n_layers, int topk, int renorm, void* out, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
+  if (!layers || !x || !out) return I4_ERR_NULL;
+  if (n_layers < 1) return I4_ERR_SHAPE;
+  i4_qweight gu, dn;
+  for (int l = 0; l < n_layers; ++l) {
+    int rc = check_moe(&layers[l], x_dtype, T, topk, &gu, &dn);
+    if (rc) return rc;
+    if (!layers[l].router_w) return I4_ERR_NULL;
+  }
+  int rc = check_moe(&layers[0], x_dtype, T, topk, &gu, &dn);
+  const int H = gu.K, I = dn.K, E = gu.E;
+  for (int l = 1; l < n_layers; ++l)
+    if (layers[l].gate_up.K != H || layers[l].down.K != I || layers[l].gate_up.E != E)
+      return I4_ERR_SHAPE;
+  const size_t mbytes = i4_moe_workspace_bytes(T, H, I, E, topk);
+  if (!workspace || workspace_bytes < mbytes + al256((size_t)T * H * 2)) return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  void* buf = (char*)workspace + mbytes;
+  const void* h = x;
+  for (int l = 0; l < n_layers; ++l) {
+    void* dst = ((n_layers - 1 - l) % 2 == 0) ? out : buf;
+    rc = i4_moe_forward(h, x_dtype, T, &layers[l], topk, renorm, nullptr, h, dst, nullptr,
+                        nullptr, workspace, mbytes, stream);
+    if (rc) return rc;
+    h = dst;
+  }
+  return I4_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,131 @@
+"""FusedPackedMoE drop-in: the int4 SparseMoeBlock replacement on libi4moe.
+
+Mirrors src/duplex/streaming/fused_packed_moe.py:83-319:
+  - FusedPackedMoE(block, dtype, device) stacks a transformers block's packed
+    experts (weight_packed / weight_scale / weight_shape per Linear) into
+    gate|up [E, 2I, H/8] and down [E, H, I/8] with scales cast to `dtype`
+    (:68-80, :112-122);
+  - forward(hidden_states) routes and runs the experts (:191-263) in four
+    launches at T = 1 (router, top-k, gate_up+SiLU, down+combine);
+  - fuse_packed_moe_blocks(model, ...) swaps every matching block (:278-319).
+
+Host-resident experts and CPU compute (:86-164, :202-220) exist in the
+reference only because its 12 GB card cannot hold the Thinker; on a 288 GB
+MI355X every layer stays resident, so those modes are rejected.
+Extra constructors build the module from already-stacked CT tensors or from
+AutoAWQ tensors (repacked once, on the device, into CT with zero points).
+"""
+from __future__ import annotations
+
+import gc
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .weights import QWeight, repack_awq_to_ct
+
+
+def _stack_ct(linears, dtype, device):
+    """Stack packed Linears into (packed [E, N, K/8], scale [E, N, NG], N, K)."""
+    l0 = linears[0]
+    out_f, in_f = (int(v) for v in l0.weight_shape.tolist())
+    E = len(linears)
+    packed = torch.empty(E, out_f, l0.weight_packed.shape[1], dtype=torch.int32, device=device)
+    scale = torch.empty(E, out_f, l0.weight_scale.shape[1], dtype=dtype, device=device)
+    for i, lin in enumerate(linears):
+        packed[i] = lin.weight_packed.to(device)
+        scale[i] = lin.weight_scale.to(device, dtype)
+    return packed, scale, out_f, in_f
+
+
+class FusedPackedMoE(nn.Module):
+    """SparseMoeBlock replacement for int4-packed experts."""
+
+    def __init__(self, block: nn.Module | None = None, dtype=torch.bfloat16, device="cuda",
+                 host_resident: bool = False, cpu_compute: bool = False, group: int = 32):
+        super().__init__()
+        if host_resident or cpu_compute:
+            raise NotImplementedError(
+                "host-resident / CPU-computed experts are not provided: every layer is resident "
+                "in HBM on MI355X")
+        self.workspace = ops.Workspace()
+        if block is None:  # filled by a classmethod constructor
+            return
+        experts = block.experts
+        self.num_experts = len(experts)
+        self.top_k = int(block.top_k)
+        self.norm_topk_prob = bool(getattr(block, "norm_topk_prob", True))
+        gw = block.gate.weight.detach().to(device=device, dtype=dtype).contiguous()
+        gp, gs, inter, hidden = _stack_ct([e.gate_proj for e in experts], dtype, device)
+        up, us, _, _ = _stack_ct([e.up_proj for e in experts], dtype, device)
+        dp, ds, hid_out, inter_in = _stack_ct([e.down_proj for e in experts], dtype, device)
+        gu_p, gu_s = torch.cat([gp, up], dim=1), torch.cat([gs, us], dim=1)
+        del gp, up, gs, us
+        self._install(QWeight(gu_p, gu_s, None, "ct", group, 2 * inter, hidden),
+                      QWeight(dp, ds, None, "ct", group, hid_out, inter_in), gw)
+
+    def _install(self, gate_up: QWeight, down: QWeight, router_w: torch.Tensor) -> None:
+        if gate_up.layout != "ct" or down.layout != "ct":
+            raise ValueError("FusedPackedMoE stores CT weights (convert AWQ with from_awq)")
+        self.gate_up, self.down = gate_up, down
+        self.num_experts = gate_up.E
+        self.inter = gate_up.N // 2
+        self.hidden = gate_up.K
+        self.hid_out, self.inter_in = down.N, down.K
+        self.register_buffer("router_w", router_w, persistent=False)
+        for name, t in (("gu_packed", gate_up.packed), ("gu_scale", gate_up.scale),
+                        ("gu_zeros", gate_up.zeros), ("down_packed", down.packed),
+                        ("down_scale", down.scale), ("down_zeros", down.zeros)):
+            self.register_buffer(name, t, persistent=False)
+
+    @classmethod
+    def from_stacked(cls, gate_up: QWeight, down: QWeight, router_w: torch.Tensor, top_k: int,
+                     norm_topk_prob: bool = True) -> "FusedPackedMoE":
+        m = cls()
+        m.top_k, m.norm_topk_prob = int(top_k), bool(norm_topk_prob)
+        m._install(gate_up, down, router_w.contiguous())
+        return m
+
+    @classmethod
+    def from_awq(cls, gate: QWeight, up: QWeight, down: QWeight, router_w: torch.Tensor,
+                 top_k: int, norm_topk_prob: bool = True) -> "FusedPackedMoE":
+        """Experts in AutoAWQ packing; gate|up and down are repacked to CT+zeros."""
+        gu = repack_awq_to_ct([gate, up])
+        dn = repack_awq_to_ct([down])
+        return cls.from_stacked(gu, dn, router_w, top_k, norm_topk_prob)
+
+    def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor | None = None):
+        return ops.moe_forward(hidden_states, self.gate_up, self.down, self.top_k,
+                               router_w=self.router_w, norm_topk_prob=self.norm_topk_prob,
+                               residual=residual, workspace=self.workspace)
+
+    def route(self, hidden_states: torch.Tensor):
+        """(w, sel) exactly as forward() routes: router Linear, softmax, top-k, renorm."""
+        lg = ops.router_logits(hidden_states.reshape(-1, self.hidden), self.router_w)
+        return ops.route(lg, self.top_k, self.norm_topk_prob)
+
+
+def fuse_packed_moe_blocks(model: nn.Module, dtype=torch.bfloat16, device="cuda",
+                           n_pinned: int | None = None, cpu_compute: bool = False,
+                           verbose: bool = True) -> int:
+    """Replace every packed *SparseMoeBlock with a FusedPackedMoE (all resident)."""
+    if cpu_compute:
+        raise NotImplementedError("CPU-computed experts are not provided")
+    del n_pinned  # every block is resident in HBM
+    sites = []
+    for parent in model.modules():
+        for name, child in list(parent.named_children()):
+            if type(child).__name__.endswith("SparseMoeBlock") and hasattr(child, "experts"):
+                gp = getattr(child.experts[0], "gate_proj", None)
+                if gp is not None and hasattr(gp, "weight_packed"):
+                    sites.append((parent, name))
+    for parent, name in sites:
+        child = getattr(parent, name)
+        setattr(parent, name, FusedPackedMoE(child, dtype, device))
+        child.experts = None
+        del child
+        gc.collect()
+    if verbose:
+        print(f"fused {len(sites)} packed MoE blocks, all HBM-resident")
+    return len(sites)

@@ -1,0 +1,262 @@
+"""Functional ops with the reference's signatures, executed by libi4moe.
+
+    dequant_gemv   src/duplex/streaming/triton_dequant_gemv.py:85-113
+    reference_gemv is not provided here: it is the checker's job (oracle/)
+    unpack4        src/duplex/streaming/fused_packed_moe.py:54-65 (device)
+    dequant        FusedPackedMoE._dequant, fused_packed_moe.py:183-189 (device)
+    route          fused_packed_moe.py:195-199
+    moe_forward    FusedPackedMoE.forward, fused_packed_moe.py:191-263
+    moe_stack      Thinker[0:24] MoE stack with residual adds (clock.py:168-171)
+
+Every op enqueues on torch's current stream of the tensors' device and never
+synchronises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .weights import QWeight
+
+
+def _ws(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def dequant_gemv(x, packed, scale, sel, group=32, block_r=64, nw_blk=8, *, zeros=None,
+                 layout="ct", out_dtype=torch.float32):
+    """y[j, r] = sum_c W[sel[j], r, c] * x[j, c], W dequantised from int4 on the fly.
+
+    Same contract as the reference's dequant_gemv: x [K] (shared by every
+    selected expert) or [k, K] (one row per expert); packed/scale in the CT
+    layout [E, R, K/8] / [E, R, K/group] (or AWQ with layout="awq" and zeros);
+    sel [k] expert ids; returns [k, R] float32.  block_r and nw_blk are the
+    reference's Triton tile sizes and have no meaning here.
+    """
+    del block_r, nw_blk
+    dev = _lib.require_device(x, packed, scale, sel, zeros)
+    xt = _lib.half_code(x.dtype)
+    sel32 = sel.to(torch.int32).contiguous()
+    k = sel32.numel()
+    if layout == "ct":
+        w = QWeight(packed, scale, zeros, "ct", group, packed.shape[-2], packed.shape[-1] * 8)
+    else:
+        w = QWeight(packed, scale, zeros, "awq", group, packed.shape[-1] * 8, packed.shape[-2])
+    K = w.K
+    if x.dim() == 1:
+        if x.numel() != K:
+            raise RuntimeError(f"x has {x.numel()} elements, weights have K={K}")
+        xc, s_x = x.contiguous(), 0
+    else:
+        if x.shape[-1] != K or x.shape[0] != k:
+            raise RuntimeError(f"x shape {tuple(x.shape)} does not match [k={k}, K={K}]")
+        xc = x.contiguous()
+        s_x = K
+    out = torch.empty(k, w.N, dtype=out_dtype, device=dev)
+    lb = _lib.lib()
+    cw = w.c()
+    ws = _ws(lb.i4_dq_gemv_workspace_bytes(ctypes.byref(cw), k), dev)
+    _lib.check(lb.i4_dq_gemv(xc.data_ptr(), xt, s_x, ctypes.byref(cw), sel32.data_ptr(), k,
+                             out.data_ptr(), _lib.dtype_code(out_dtype),
+                             None if ws is None else ws.data_ptr(),
+                             0 if ws is None else ws.numel(), _lib.stream(dev)))
+    return out
+
+
+def linear(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
+           out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """y = x W^T (+ bias) for every row of x in one launch (E = 1 weight)."""
+    dev = _lib.require_device(x, w.packed, bias)
+    xt = _lib.half_code(x.dtype)
+    lead = x.shape[:-1]
+    if x.shape[-1] != w.K:
+        raise RuntimeError(f"x has K={x.shape[-1]}, weight has K={w.K}")
+    flat = x.reshape(-1, w.K).contiguous()
+    M = flat.shape[0]
+    od = out_dtype or x.dtype
+    y = torch.empty(M, w.N, dtype=od, device=dev)
+    b = None
+    if bias is not None:
+        b = bias.to(od).contiguous()
+        if b.numel() != w.N:
+            raise RuntimeError("bias length != out_features")
+    lb = _lib.lib()
+    cw = w.c()
+    ws = _ws(lb.i4_linear_workspace_bytes(ctypes.byref(cw), M), dev)
+    _lib.check(lb.i4_linear(flat.data_ptr(), xt, M, ctypes.byref(cw), _lib.ptr(b), y.data_ptr(),
+                            _lib.dtype_code(od), None if ws is None else ws.data_ptr(),
+                            0 if ws is None else ws.numel(), _lib.stream(dev)))
+    return y.view(*lead, w.N)
+
+
+def unpack_nibbles(w: QWeight) -> torch.Tensor:
+    """Raw nibbles 0..15 of every expert in logical [E, N, K] order (uint8)."""
+    dev = _lib.require_device(w.packed)
+    out = torch.empty(w.E, w.N, w.K, dtype=torch.uint8, device=dev)
+    cw = w.c()
+    _lib.check(_lib.lib().i4_unpack(ctypes.byref(cw), out.data_ptr(), _lib.stream(dev)))
+    return out
+
+
+def unpack4(packed: torch.Tensor, out_cols: int) -> torch.Tensor:
+    """The reference's unpack4 on a CT tensor: signed nibble - 8, [..., out_cols]."""
+    lead = packed.shape[:-2]
+    p = packed.reshape(-1, packed.shape[-2], packed.shape[-1])
+    G = 32
+    ng = -(-p.shape[-1] * 8 // G)
+    dummy_scale = torch.ones(p.shape[0], p.shape[1], ng, dtype=torch.float16, device=p.device)
+    w = QWeight(p, dummy_scale, None, "ct", G, p.shape[1], p.shape[2] * 8)
+    q = unpack_nibbles(w).to(torch.int32) - 8
+    return q[..., :out_cols].reshape(*lead, p.shape[1], out_cols)
+
+
+def dequant(w: QWeight, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Dense [E, N, K] = (nibble - zero) * scale (FusedPackedMoE._dequant)."""
+    dev = _lib.require_device(w.packed)
+    out = torch.empty(w.E, w.N, w.K, dtype=out_dtype, device=dev)
+    cw = w.c()
+    _lib.check(_lib.lib().i4_dequant(ctypes.byref(cw), out.data_ptr(), _lib.dtype_code(out_dtype),
+                                     _lib.stream(dev)))
+    return out
+
+
+def router_logits(x: torch.Tensor, router_w: torch.Tensor) -> torch.Tensor:
+    """gate(x): [T, H] x [E, H]^T -> [T, E] in x.dtype, fp32 accumulation."""
+    dev = _lib.require_device(x, router_w)
+    xt = _lib.half_code(x.dtype)
+    if router_w.dtype != x.dtype:
+        raise RuntimeError("router weight must have the activation dtype")
+    xf = x.reshape(-1, x.shape[-1]).contiguous()
+    T, H = xf.shape
+    E = router_w.shape[0]
+    wr = router_w.contiguous()
+    out = torch.empty(T, E, dtype=x.dtype, device=dev)
+    _lib.check(_lib.lib().i4_router_logits(xf.data_ptr(), xt, T, H, wr.data_ptr(), E,
+                                           out.data_ptr(), _lib.stream(dev)))
+    return out
+
+
+def route(logits: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
+          w_dtype: torch.dtype | None = None):
+    """softmax (fp32) -> top-k -> renorm, from [T, E] logits.
+
+    Returns (w, sel): w [T, top_k] in w_dtype (default logits.dtype, the
+    reference's w.to(x.dtype)), sel [T, top_k] int32 in descending-weight
+    order; exact ties go to the lower expert id.
+    """
+    dev = _lib.require_device(logits)
+    lt = _lib.dtype_code(logits.dtype)
+    lg = logits.reshape(-1, logits.shape[-1]).contiguous()
+    T, E = lg.shape
+    wd = w_dtype or logits.dtype
+    sel = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    w = torch.empty(T, top_k, dtype=wd, device=dev)
+    _lib.check(_lib.lib().i4_route_topk(lg.data_ptr(), lt, T, E, top_k, int(norm_topk_prob),
+                                        sel.data_ptr(), None, w.data_ptr(),
+                                        _lib.dtype_code(wd), _lib.stream(dev)))
+    return w, sel
+
+
+def moe_weights_c(gate_up: QWeight, down: QWeight,
+                  router_w: torch.Tensor | None) -> _lib.MoeWeightsC:
+    return _lib.MoeWeightsC(gate_up=gate_up.c(), down=down.c(),
+                            router_w=None if router_w is None else router_w.data_ptr())
+
+
+class Workspace:
+    """Grow-only device scratch for the MoE entry points (one per module)."""
+
+    def __init__(self) -> None:
+        self.buf: torch.Tensor | None = None
+
+    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
+            self.buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        return self.buf
+
+
+def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
+                router_w: torch.Tensor | None = None, logits: torch.Tensor | None = None,
+                norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
+                return_routing: bool = False, workspace: Workspace | None = None):
+    """One int4 MoE block: out = residual + sum_j w_j down_e(silu(gate_e x) * up_e x)."""
+    dev = _lib.require_device(x, gate_up.packed, down.packed, router_w, logits, residual)
+    xt = _lib.half_code(x.dtype)
+    shape = x.shape
+    xf = x.reshape(-1, shape[-1]).contiguous()
+    T, H = xf.shape
+    E, I = gate_up.E, down.K
+    if router_w is None and logits is None:
+        raise RuntimeError("need router_w or logits")
+    lg = None
+    if router_w is None:
+        lg = logits.reshape(T, E).to(x.dtype).contiguous()
+    rs = None if residual is None else residual.reshape(T, H).to(x.dtype).contiguous()
+    out = torch.empty(T, H, dtype=x.dtype, device=dev)
+    sel = torch.empty(T, top_k, dtype=torch.int32, device=dev) if return_routing else None
+    wts = torch.empty(T, top_k, dtype=torch.float32, device=dev) if return_routing else None
+    lb = _lib.lib()
+    nbytes = lb.i4_moe_workspace_bytes(T, H, I, E, top_k)
+    ws = (workspace or Workspace()).get(nbytes, dev)
+    mw = moe_weights_c(gate_up, down, router_w)
+    _lib.check(lb.i4_moe_forward(xf.data_ptr(), xt, T, ctypes.byref(mw), top_k,
+                                 int(norm_topk_prob), _lib.ptr(lg), _lib.ptr(rs), out.data_ptr(),
+                                 _lib.ptr(sel), _lib.ptr(wts), ws.data_ptr(), ws.numel(),
+                                 _lib.stream(dev)))
+    out = out.view(shape)
+    if return_routing:
+        return out, sel, wts
+    return out
+
+
+def moe_gate_up(x: torch.Tensor, gate_up: QWeight, sel: torch.Tensor) -> torch.Tensor:
+    """Decode gate_up stage: act [k, I] = silu(gate_e x) * up_e x for e = sel (x is [H])."""
+    dev = _lib.require_device(x, gate_up.packed, sel)
+    xt = _lib.half_code(x.dtype)
+    xc = x.reshape(-1).contiguous()
+    s32 = sel.reshape(-1).to(torch.int32).contiguous()
+    act = torch.empty(s32.numel(), gate_up.N // 2, dtype=x.dtype, device=dev)
+    cw = gate_up.c()
+    _lib.check(_lib.lib().i4_moe_gate_up(xc.data_ptr(), xt, ctypes.byref(cw), s32.data_ptr(),
+                                         s32.numel(), act.data_ptr(), _lib.stream(dev)))
+    return act
+
+
+def moe_down_combine(act: torch.Tensor, down: QWeight, sel: torch.Tensor, w: torch.Tensor,
+                     residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode down stage: residual + sum_j w[j] down_{sel[j]}(act[j]) -> [H]."""
+    dev = _lib.require_device(act, down.packed, sel, w, residual)
+    xt = _lib.half_code(act.dtype)
+    s32 = sel.reshape(-1).to(torch.int32).contiguous()
+    wf = w.reshape(-1).to(torch.float32).contiguous()
+    rs = None if residual is None else residual.reshape(-1).to(act.dtype).contiguous()
+    out = torch.empty(down.N, dtype=act.dtype, device=dev)
+    cw = down.c()
+    _lib.check(_lib.lib().i4_moe_down_combine(act.contiguous().data_ptr(), xt, ctypes.byref(cw),
+                                              s32.data_ptr(), wf.data_ptr(), s32.numel(),
+                                              _lib.ptr(rs), out.data_ptr(), _lib.stream(dev)))
+    return out
+
+
+def moe_stack(x: torch.Tensor, layers: list[tuple[QWeight, QWeight, torch.Tensor]], top_k: int,
+              norm_topk_prob: bool = True, workspace: Workspace | None = None) -> torch.Tensor:
+    """h <- h + moe_l(h) over layers [(gate_up, down, router_w), ...]."""
+    dev = _lib.require_device(x)
+    xt = _lib.half_code(x.dtype)
+    shape = x.shape
+    xf = x.reshape(-1, shape[-1]).contiguous()
+    T, H = xf.shape
+    gu0, dn0, _ = layers[0]
+    arr = (_lib.MoeWeightsC * len(layers))(*[moe_weights_c(g, d, r) for g, d, r in layers])
+    lb = _lib.lib()
+    nbytes = lb.i4_moe_stack_workspace_bytes(T, H, dn0.K, gu0.E, top_k)
+    ws = (workspace or Workspace()).get(nbytes, dev)
+    out = torch.empty_like(xf)
+    _lib.check(lb.i4_moe_stack_forward(xf.data_ptr(), xt, T, arr, len(layers), top_k,
+                                       int(norm_topk_prob), out.data_ptr(), ws.data_ptr(),
+                                       ws.numel(), _lib.stream(dev)))
+    return out.view(shape)

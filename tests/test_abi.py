@@ -1,0 +1,125 @@
+"""The C ABI: libi4moe.so loads without a GPU, exports every function that
+include/i4moe.h declares, and rejects invalid calls on the host before any
+launch (no compute call is made here)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "i4moe.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(i4_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    assert "i4_dq_gemv" in names and "i4_moe_forward" in names and len(names) >= 15
+
+
+def test_every_declared_symbol_is_exported_and_bound(pkg):
+    lib = pkg.lib()
+    from qwen3_omni_duplex_amd import _lib
+
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+
+
+def test_version_and_errors(pkg):
+    lib = pkg.lib()
+    assert lib.i4_abi_version() == 1
+    codes = {0: b"ok", -1: b"NULL", -2: b"dimension", -3: b"element type", -4: b"aligned",
+             -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride"}
+    for c, frag in codes.items():
+        assert frag in lib.i4_strerror(c)
+    assert b"unknown" in lib.i4_strerror(-99)
+
+
+def _qw(_lib, **kw):
+    base = dict(packed=0x10000, scale=0x20000, zeros=None, packed_estride=0, scale_estride=0,
+                zeros_estride=0, layout=0, group=32, scale_dtype=1, E=4, N=64, K=256)
+    base.update(kw)
+    return _lib.QWeightC(**base)
+
+
+@pytest.mark.parametrize("bad,code", [
+    (dict(packed=None), -1),
+    (dict(K=100), -2),
+    (dict(K=16), -2),
+    (dict(group=48), -6),
+    (dict(group=16), -6),
+    (dict(layout=7), -5),
+    (dict(scale_dtype=9), -3),
+    (dict(packed=0x10004), -4),
+    (dict(packed_estride=10), -9),
+    (dict(layout=1, N=60), -2),
+])
+def test_weight_validation_codes(pkg, bad, code):
+    pkg.lib()
+    from qwen3_omni_duplex_amd import _lib
+
+    lib = pkg.lib()
+    w = _qw(_lib, **bad)
+    rc = lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(w), 0x40000, 8, 0x50000, 0, None, 0, None)
+    assert rc == code
+
+
+def test_call_validation_codes(pkg):
+    from qwen3_omni_duplex_amd import _lib
+
+    lib = pkg.lib()
+    w = _qw(_lib)
+    # activations must be half precision, aligned, with a sane stride
+    assert lib.i4_dq_gemv(0x30000, 0, 0, ctypes.byref(w), 0x40000, 8, 0x50000, 0, None, 0, None) == -3
+    assert lib.i4_dq_gemv(0x30002, 1, 0, ctypes.byref(w), 0x40000, 8, 0x50000, 0, None, 0, None) == -4
+    assert lib.i4_dq_gemv(0x30000, 1, 100, ctypes.byref(w), 0x40000, 8, 0x50000, 0, None, 0, None) == -9
+    assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(w), None, 8, 0x50000, 0, None, 0, None) == -1
+    assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(w), 0x40000, 0, 0x50000, 0, None, 0, None) == -2
+    # AWQ needs its split-K workspace
+    wa = _qw(_lib, layout=1)
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wa), 8) > 0
+    assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(wa), 0x40000, 8, 0x50000, 0, None, 0, None) == -7
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(w), 8) == 0
+    # routing limits
+    assert lib.i4_route_topk(0x30000, 1, 1, 128, 0, 1, 0x40000, None, None, 0, None) == -2
+    assert lib.i4_route_topk(0x30000, 1, 1, 1024, 8, 1, 0x40000, None, None, 0, None) == -2
+    assert lib.i4_route_topk(0x30000, 5, 1, 128, 8, 1, 0x40000, None, None, 0, None) == -3
+    assert lib.i4_router_logits(0x30000, 1, 1, 2047, 0x40000, 128, 0x50000, None) == -2
+
+
+def test_moe_validation_codes(pkg):
+    from qwen3_omni_duplex_amd import _lib
+
+    lib = pkg.lib()
+    gu = _qw(_lib, E=128, N=1536, K=2048, group=128)
+    dn = _qw(_lib, E=128, N=2048, K=768, group=128)
+    mw = _lib.MoeWeightsC(gate_up=gu, down=dn, router_w=0x60000)
+    ws = lib.i4_moe_workspace_bytes(1, 2048, 768, 128, 8)
+    assert ws > 0
+    call = lambda **kw: lib.i4_moe_forward(
+        kw.get("x", 0x30000), kw.get("xt", 1), kw.get("T", 1), ctypes.byref(kw.get("mw", mw)),
+        kw.get("k", 8), 1, None, None, 0x70000, None, None, kw.get("ws", 0x100000),
+        kw.get("wsb", ws), None)
+    assert call(wsb=ws - 1) == -7
+    assert call(ws=0x100010) == -4
+    assert call(k=0) == -2
+    assert call(T=0) == -2
+    assert call(xt=0) == -3
+    bad = _lib.MoeWeightsC(gate_up=_qw(_lib, E=128, N=1500, K=2048, group=128), down=dn,
+                           router_w=0x60000)
+    assert call(mw=bad) == -2
+    awq = _lib.MoeWeightsC(gate_up=_qw(_lib, E=128, N=1536, K=2048, group=128, layout=1),
+                           down=dn, router_w=0x60000)
+    assert call(mw=awq) == -5
+    nor = _lib.MoeWeightsC(gate_up=gu, down=dn, router_w=None)
+    assert call(mw=nor) == -1
+    assert lib.i4_moe_stack_workspace_bytes(1, 2048, 768, 128, 8) > ws

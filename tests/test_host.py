@@ -1,0 +1,54 @@
+"""Host-side logic of the package (no GPU needed): descriptor validation and
+the refusal to run anything off the HIP device."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+
+def test_qweight_shape_checks(pkg):
+    p = torch.zeros(2, 16, 32, dtype=torch.int32)
+    s = torch.zeros(2, 16, 8, dtype=torch.float16)
+    w = pkg.QWeight(p, s, None, "ct", 32, 16, 256)
+    assert (w.E, w.N, w.K) == (2, 16, 256)
+    c = w.c()
+    assert (c.E, c.N, c.K, c.group, c.layout, c.scale_dtype) == (2, 16, 256, 32, 0, 1)
+    with pytest.raises(ValueError):
+        pkg.QWeight(p, s[:, :, :4], None, "ct", 32, 16, 256)
+    with pytest.raises(ValueError):
+        pkg.QWeight(p.float(), s, None, "ct", 32, 16, 256)
+    with pytest.raises(ValueError):
+        pkg.QWeight(p, s, None, "gptq", 32, 16, 256)
+    qa = torch.zeros(2, 256, 2, dtype=torch.int32)
+    sa = torch.zeros(2, 2, 16, dtype=torch.float16)
+    za = torch.zeros(2, 2, 2, dtype=torch.int32)
+    wa = pkg.QWeight.awq(qa, sa, za, group=128)
+    assert (wa.N, wa.K, wa.layout) == (16, 256, "awq")
+    # 2-D tensors are one expert
+    w1 = pkg.QWeight.ct(p[0], s[0], group=32)
+    assert w1.E == 1
+
+
+def test_ops_refuse_cpu_tensors(pkg):
+    x = torch.zeros(256, dtype=torch.float16)
+    p = torch.zeros(2, 16, 32, dtype=torch.int32)
+    s = torch.zeros(2, 16, 8, dtype=torch.float16)
+    sel = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        pkg.dequant_gemv(x, p, s, sel)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        pkg.route(torch.zeros(1, 8), 2)
+
+
+def test_reference_only_modes_are_rejected(pkg):
+    with pytest.raises(NotImplementedError):
+        pkg.FusedPackedMoE(None, host_resident=True)
+    with pytest.raises(NotImplementedError):
+        pkg.fuse_packed_moe_blocks(torch.nn.Linear(2, 2), cpu_compute=True)
+
+
+def test_library_path_is_in_tree(pkg):
+    from qwen3_omni_duplex_amd import _lib
+
+    assert _lib.LIB_PATH.parent.name == "qwen3-omni-duplex_amd"
+    assert _lib.LIB_PATH.exists()

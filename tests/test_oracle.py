@@ -1,0 +1,300 @@
+"""Pins of the CPU oracle (oracle/i4ref.py) -- runs on CPU.
+
+Every oracle function is checked against at least one of: the known-answer
+vectors of tests/golden/known_answers.json (written by an independent
+pure-Python script), a closed form or invariant, or a library routine
+(torch.topk / torch.softmax / torch's bf16 cast / numpy matmul).  The
+mutation tests at the end plant plausible mistakes in the oracle and show
+that these checks catch them.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import i4ref
+
+GOLD = json.loads((Path(__file__).parent / "golden" / "known_answers.json").read_text())
+
+
+# ---------------------------------------------------------------- packing
+def check_ct_words():
+    for case in GOLD["ct_words"]:
+        w = np.array([case["word"]], dtype=np.int32)
+        assert i4ref.ct_nibbles(w).tolist() == case["nibbles"]
+        assert i4ref.ct_pack(np.array(case["nibbles"])).tolist() == [case["word"]]
+    rw = np.array(GOLD["random_words"]["words"], dtype=np.int32)
+    assert i4ref.ct_nibbles(rw).reshape(-1, 8).tolist() == GOLD["random_words"]["ct_nibbles"]
+
+
+def check_awq_words():
+    for case in GOLD["awq_words"]:
+        w = np.array([case["word"]], dtype=np.int32)
+        assert i4ref.awq_nibbles(w).tolist() == case["cols"]
+        assert i4ref.awq_pack(np.array(case["cols"])).tolist() == [case["word"]]
+    rw = np.array(GOLD["random_words"]["words"], dtype=np.int32)
+    assert i4ref.awq_nibbles(rw).reshape(-1, 8).tolist() == GOLD["random_words"]["awq_cols"]
+
+
+def test_ct_known_words():
+    check_ct_words()
+
+
+def test_awq_known_words():
+    check_awq_words()
+    # the published AutoAWQ example: columns 0..7 -> 0x75316420
+    assert int(i4ref.awq_pack(np.arange(8))[0]) == 0x75316420
+
+
+def test_brute_force_every_value_every_position():
+    for pos in range(8):
+        for v in range(16):
+            q = np.zeros(8, dtype=np.int64)
+            q[pos] = v
+            w = int(i4ref.ct_pack(q)[0]) & 0xFFFFFFFF
+            assert w == v << (4 * pos)
+            assert i4ref.ct_nibbles(np.array([w]).astype(np.uint32).view(np.int32))[pos] == v
+            wa = int(i4ref.awq_pack(q)[0]) & 0xFFFFFFFF
+            assert wa == v << (4 * i4ref.AWQ_SLOT[pos])
+
+
+def test_round_trips():
+    rng = np.random.default_rng(0)
+    q = rng.integers(0, 16, size=(3, 5, 64))
+    assert np.array_equal(i4ref.ct_nibbles(i4ref.ct_pack(q)), q)
+    assert np.array_equal(i4ref.awq_nibbles(i4ref.awq_pack(q)), q)
+    w = rng.integers(-2**31, 2**31, size=(4, 7), dtype=np.int64).astype(np.int32)
+    assert np.array_equal(i4ref.ct_pack(i4ref.ct_nibbles(w)), w)
+    assert np.array_equal(i4ref.awq_pack(i4ref.awq_nibbles(w)), w)
+
+
+def test_unpack4_is_signed_nibble():
+    rng = np.random.default_rng(1)
+    w = rng.integers(-2**31, 2**31, size=(2, 3, 4), dtype=np.int64).astype(np.int32)
+    s = i4ref.unpack4(w, 32)
+    assert s.min() >= -8 and s.max() <= 7
+    assert np.array_equal(s, i4ref.ct_nibbles(w).astype(np.int32) - 8)
+    # out_cols truncates like the reference's [..., :out_cols]
+    assert np.array_equal(i4ref.unpack4(w, 20), s[..., :20])
+
+
+def test_unpack_matches_torch_bit_ops():
+    """The reference's own torch expression (fused_packed_moe.py:62-65) on CPU tensors."""
+    rng = np.random.default_rng(2)
+    w = rng.integers(-2**31, 2**31, size=(3, 16), dtype=np.int64).astype(np.int32)
+    t = torch.from_numpy(w)
+    shifts = torch.arange(8, dtype=torch.int32) * 4
+    u = ((t.unsqueeze(-1) >> shifts) & 0xF).flatten(-2) - 8
+    assert np.array_equal(u.numpy(), i4ref.unpack4(w, 128))
+
+
+# ---------------------------------------------------------------- dequant + gemv
+def test_ct_gemv_known_answer():
+    g = GOLD["ct_gemv"]
+    packed = np.array(g["packed"], dtype=np.int32)[None]
+    scale = np.array(g["scale"])[None]
+    W = i4ref.ct_dequant(packed, scale, g["K"], g["group"])
+    y = i4ref.dq_gemv(np.array(g["x"]), W, [0])[0]
+    np.testing.assert_allclose(y, g["y"], rtol=0, atol=1e-12)
+
+
+def test_awq_gemv_known_answer():
+    g = GOLD["awq_gemv"]
+    W = i4ref.awq_dequant(np.array(g["qweight"], np.int32)[None], np.array(g["qzeros"], np.int32)[None],
+                          np.array(g["scales"])[None], g["group"])
+    y = i4ref.dq_gemv(np.array(g["x"]), W, [0])[0]
+    np.testing.assert_allclose(y, g["y"], rtol=0, atol=1e-12)
+
+
+def test_zero_point_8_reduces_to_symmetric():
+    rng = np.random.default_rng(3)
+    E, N, K, G = 2, 16, 256, 64
+    p = rng.integers(-2**31, 2**31, size=(E, N, K // 8), dtype=np.int64).astype(np.int32)
+    s = rng.uniform(0.002, 0.02, size=(E, N, K // G))
+    z8 = i4ref.ct_pack(np.full((E, N, 8), 8))
+    np.testing.assert_array_equal(i4ref.ct_dequant(p, s, K, G, zeros=z8), i4ref.ct_dequant(p, s, K, G))
+
+
+def test_ct_awq_layout_equivalence():
+    """One logical int4 matrix packed both ways dequantises identically; awq_to_ct agrees."""
+    rng = np.random.default_rng(4)
+    E, N, K, G = 2, 24, 256, 128
+    Q = rng.integers(0, 16, size=(E, N, K))
+    Z = rng.integers(0, 16, size=(E, N, K // G))
+    S = rng.uniform(0.002, 0.02, size=(E, N, K // G)).astype(np.float16)
+    qw = i4ref.awq_pack(np.swapaxes(Q, 1, 2))                 # [E, K, N/8]
+    qz = i4ref.awq_pack(np.swapaxes(Z, 1, 2))                 # [E, NG, N/8]
+    sc = np.swapaxes(S, 1, 2)                                 # [E, NG, N]
+    W_awq = i4ref.awq_dequant(qw, qz, sc, G)
+    zpad = np.concatenate([Z, np.zeros((E, N, 6), np.int64)], axis=-1)
+    W_ct = i4ref.ct_dequant(i4ref.ct_pack(Q), S, K, G, zeros=i4ref.ct_pack(zpad))
+    np.testing.assert_array_equal(W_awq, W_ct)
+    cp, cs, cz = i4ref.awq_to_ct(qw, qz, sc, G)
+    np.testing.assert_array_equal(i4ref.ct_dequant(cp, cs, K, G, zeros=cz), W_awq)
+    # direct element check against the definition
+    e, n, k = 1, 5, 200
+    assert W_awq[e, n, k] == (Q[e, n, k] - Z[e, n, k // G]) * np.float64(S[e, n, k // G])
+
+
+def test_dq_gemv_vs_loops():
+    rng = np.random.default_rng(5)
+    E, N, K = 3, 5, 64
+    W = rng.standard_normal((E, N, K))
+    x1 = rng.standard_normal(K)
+    x2 = rng.standard_normal((2, K))
+    sel = [2, 0]
+    y1 = i4ref.dq_gemv(x1, W, sel)
+    y2 = i4ref.dq_gemv(x2, W, sel)
+    for j, e in enumerate(sel):
+        for r in range(N):
+            assert abs(y1[j, r] - sum(W[e, r, c] * x1[c] for c in range(K))) < 1e-10
+            assert abs(y2[j, r] - sum(W[e, r, c] * x2[j, c] for c in range(K))) < 1e-10
+
+
+# ---------------------------------------------------------------- routing
+def test_route_known_answers():
+    for case in GOLD["routing"]:
+        sel, w = i4ref.route(np.array([case["logits"]]), case["k"])
+        assert sel[0].tolist() == case["sel"]
+        np.testing.assert_allclose(w[0], case["w"], rtol=1e-12)
+
+
+def test_route_matches_torch_on_tie_free_rows():
+    torch.manual_seed(6)
+    for dt in (torch.float16, torch.bfloat16):
+        lg = torch.randn(256, 128).to(dt)
+        lgf = lg.float()
+        # keep rows whose 8th and 9th largest logits differ
+        srt = lgf.sort(dim=-1, descending=True).values
+        keep = srt[:, 7] != srt[:, 8]
+        p = torch.softmax(lgf, dim=-1, dtype=torch.float32)
+        w_t, sel_t = torch.topk(p, 8, dim=-1)
+        w_t = w_t / w_t.sum(-1, keepdim=True)
+        sel, w = i4ref.route(lgf.double().numpy(), 8)
+        assert keep.sum() > 200
+        # index sets agree on tie-free rows (order may differ only inside exact ties above the cut)
+        for t in np.nonzero(keep.numpy())[0]:
+            assert set(sel[t].tolist()) == set(sel_t[t].tolist())
+            np.testing.assert_allclose(np.sort(w[t]), np.sort(w_t[t].double().numpy()), rtol=2e-6)
+
+
+def test_route_ties_go_to_lower_id():
+    sel, w = i4ref.route(np.zeros((1, 16)), 5)
+    assert sel[0].tolist() == [0, 1, 2, 3, 4]
+    np.testing.assert_allclose(w[0], 0.2)
+
+
+def test_route_without_renorm_is_softmax():
+    lg = np.array([[0.0, 1.0, 2.0, 3.0]])
+    sel, w = i4ref.route(lg, 2, renorm=False)
+    p = np.exp(lg[0] - 3) / np.exp(lg[0] - 3).sum()
+    np.testing.assert_allclose(w[0], p[[3, 2]])
+
+
+def test_bf16_rounding_matches_torch():
+    a = np.random.default_rng(7).standard_normal(10000).astype(np.float32) * 100
+    a[:4] = [np.inf, -np.inf, 0.0, -0.0]
+    bits = i4ref.f32_to_bf16_bits(a)
+    tb = torch.from_numpy(a).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(bits, tb)
+    np.testing.assert_array_equal(i4ref.round_half(a, "f16"), a.astype(np.float16).astype(np.float64))
+
+
+# ---------------------------------------------------------------- MoE layer
+def _golden_moe():
+    g = GOLD["moe_layer"]
+    Wgu = i4ref.ct_dequant(np.array(g["gu_packed"], np.int32), np.array(g["gu_scale"]), g["H"], 32)
+    Wdn = i4ref.ct_dequant(np.array(g["dn_packed"], np.int32), np.array(g["dn_scale"]), g["I"], 32)
+    return g, Wgu, Wdn
+
+
+def test_moe_layer_known_answer():
+    g, Wgu, Wdn = _golden_moe()
+    sel, w = i4ref.route(np.array([g["logits"]]), g["k"])
+    assert sel[0].tolist() == g["sel"]
+    out = i4ref.moe_layer(np.array([g["x"]]), sel, w, Wgu, Wdn, act_dtype=None)
+    np.testing.assert_allclose(out[0], g["out"], rtol=1e-10, atol=1e-12)
+
+
+def test_moe_grouped_equals_per_token():
+    rng = np.random.default_rng(8)
+    E, H, I, T, k = 6, 32, 16, 9, 3
+    Wgu = rng.standard_normal((E, 2 * I, H)) * 0.1
+    Wdn = rng.standard_normal((E, H, I)) * 0.1
+    x = rng.standard_normal((T, H))
+    sel, w = i4ref.route(rng.standard_normal((T, E)), k)
+    a = i4ref.moe_layer(x, sel, w, Wgu, Wdn, "f16", residual=x)
+    b = i4ref.moe_layer_grouped(x, sel, w, lambda e: Wgu[e], lambda e: Wdn[e], "f16", residual=x)
+    np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_moe_identical_experts_ignore_routing():
+    """With every expert equal and renormalised weights, routing cannot matter."""
+    rng = np.random.default_rng(9)
+    E, H, I, T = 5, 16, 8, 4
+    Wg = rng.standard_normal((2 * I, H))
+    Wd = rng.standard_normal((H, I))
+    Wgu, Wdn = np.stack([Wg] * E), np.stack([Wd] * E)
+    x = rng.standard_normal((T, H))
+    sel, w = i4ref.route(rng.standard_normal((T, E)), 3)
+    out = i4ref.moe_layer(x, sel, w, Wgu, Wdn, None)
+    gu = x @ Wg.T
+    ref = (i4ref.silu(gu[:, :I]) * gu[:, I:]) @ Wd.T
+    np.testing.assert_allclose(out, ref, rtol=1e-10)
+
+
+# ---------------------------------------------------------------- mutation tests
+def test_mutation_wrong_awq_order_is_caught(monkeypatch):
+    monkeypatch.setattr(i4ref, "AWQ_ORDER", tuple(range(8)))
+    monkeypatch.setattr(i4ref, "AWQ_SLOT", tuple(range(8)))
+    with pytest.raises(AssertionError):
+        check_awq_words()
+
+
+def test_mutation_wrong_nibble_shift_is_caught(monkeypatch):
+    real = i4ref.ct_nibbles
+
+    def shifted(packed, cols=None):  # nibble i read from bits 4i+1: a plausible off-by-one
+        u = np.asarray(packed).astype(np.int64) & 0xFFFFFFFF
+        q = ((u[..., None] >> (np.arange(8) * 4 + 1)) & 0xF).astype(np.uint8)
+        q = q.reshape(*u.shape[:-1], u.shape[-1] * 8)
+        return q if cols is None else q[..., :cols]
+
+    monkeypatch.setattr(i4ref, "ct_nibbles", shifted)
+    with pytest.raises(AssertionError):
+        check_ct_words()
+    monkeypatch.setattr(i4ref, "ct_nibbles", real)
+
+
+def test_mutation_missing_renorm_or_wrong_tie_rule_is_caught(monkeypatch):
+    real = i4ref.route
+
+    def no_renorm(logits, k, renorm=True):
+        return real(logits, k, renorm=False)
+
+    monkeypatch.setattr(i4ref, "route", no_renorm)
+    with pytest.raises(AssertionError):
+        test_route_known_answers()
+    monkeypatch.setattr(i4ref, "route", real)
+
+    def high_id_ties(logits, k):
+        lg = np.asarray(logits, np.float64)
+        E = lg.shape[-1]
+        return np.stack([np.lexsort((-np.arange(E), -row))[:k] for row in lg.reshape(-1, E)])
+
+    monkeypatch.setattr(i4ref, "topk_sel", high_id_ties)
+    with pytest.raises(AssertionError):
+        test_route_known_answers()
+
+
+def test_mutation_wrong_zero_point_is_caught():
+    g = GOLD["ct_gemv"]
+    packed = np.array(g["packed"], dtype=np.int32)[None]
+    z7 = i4ref.ct_pack(np.full((1, g["N"], 8), 7))
+    W = i4ref.ct_dequant(packed, np.array(g["scale"])[None], g["K"], g["group"], zeros=z7)
+    y = i4ref.dq_gemv(np.array(g["x"]), W, [0])[0]
+    assert np.max(np.abs(y - np.array(g["y"]))) > 1e-3
