@@ -2,7 +2,10 @@
 """Headline benchmark: microseconds per int4 Thinker MoE layer at M = 1.
 
 Workload (one step = one decode token through the 24-layer MoE stack,
-Thinker[0:24] with residual adds, src/duplex/streaming/clock.py:168-171):
+Thinker[0:24] with residual adds, src/duplex/streaming/clock.py:168-171; each
+layer is h <- h + MoE(RMSNorm(h)), the decoder's pre-MoE norm being fused into
+the router kernel -- without it these synthetic weights overflow fp16 within
+three layers):
   128 experts, top-8 (softmax, renormalised), hidden 2048, expert FFN 768,
   gate/up/down in AutoAWQ int4 g128 with zero points and fp16 scales
   (scales ~ U[0.002, 0.02], int4 values and zeros ~ U{0..15}), router weight
@@ -62,8 +65,10 @@ def make_layers(pkg, torch, n_layers, dev, seed=1234, keep_first_awq=False):
     for li in range(n_layers):
         g, u, d = awq(H, I), awq(H, I), awq(I, H)
         wr = (torch.randn(E, H, device=dev, generator=gen) * 0.02).half()
+        nw = (torch.rand(H, device=dev, generator=gen) * 0.4 + 0.8).half()
         q = lambda p: pkg.QWeight.awq(p[0], p[2], p[1], group=G)
-        mods.append(pkg.FusedPackedMoE.from_awq(q(g), q(u), q(d), wr, top_k=TOPK))
+        mods.append(pkg.FusedPackedMoE.from_awq(q(g), q(u), q(d), wr, top_k=TOPK,
+                                                norm_weight=nw, norm_eps=1e-6))
         if keep_first_awq and li == 0:
             first = (g, u, d, wr)
         del g, u, d
@@ -201,14 +206,14 @@ def main() -> int:
     gen.manual_seed(99)
     P = 64
     xs = [torch.randn(1, H, device=dev, generator=gen).half() for _ in range(P)]
-    layers = [(m.gate_up, m.down, m.router_w) for m in mods]
+    layers = [m.stack_entry() for m in mods]
     ws = pkg.Workspace()
 
     # ---- eager: one C call per token (96 launches)
     lb = pkg.lib()
     from qwen3_omni_duplex_amd import _lib, ops
 
-    arr = (_lib.MoeWeightsC * len(layers))(*[ops.moe_weights_c(g, d, r) for g, d, r in layers])
+    arr = (_lib.MoeWeightsC * len(layers))(*[ops.moe_weights_c(*layer) for layer in layers])
     nbytes = lb.i4_moe_stack_workspace_bytes(1, H, I, E, TOPK)
     wbuf = ws.get(nbytes, dev)
     out = torch.empty(1, H, dtype=torch.float16, device=dev)
@@ -245,6 +250,8 @@ def main() -> int:
         graph_step(5)
         eager_step(5)
         torch.cuda.synchronize()
+        if not torch.isfinite(out).all():
+            raise RuntimeError("the stack produced non-finite values")
         if not torch.equal(g_out, out):
             raise RuntimeError("graph replay differs from the eager stack")
         log(f"graph: {ms_graph:.3f} ms/token ({ms_graph * 1e3 / args.layers:.2f} us/layer)")
@@ -257,7 +264,8 @@ def main() -> int:
     h = xs[1]
     for m in mods:
         o, sel, _ = ops.moe_forward(h, m.gate_up, m.down, TOPK, router_w=m.router_w,
-                                    residual=h, return_routing=True, workspace=ws)
+                                    residual=h, return_routing=True, workspace=ws,
+                                    norm_w=m.norm_weight, norm_eps=m.norm_eps)
         routing.append(sel.reshape(-1).contiguous())
         h = o
     torch.cuda.synchronize()
@@ -292,7 +300,7 @@ def main() -> int:
         "config": {
             "workload": "Thinker[0:24] int4 MoE stack, decode M=1: 128 experts, top-8, hidden 2048, "
                         "expert FFN 768, AWQ g128 + zeros (fp16 scales) repacked to CT+zeros, "
-                        "residual adds; one step = one token through 24 layers",
+                        "pre-MoE RMSNorm + residual adds; one step = one token through 24 layers",
             "layers": args.layers, "tokens_per_step": 1,
             "timing": "eager" if ms_graph is None else "hipGraph replay",
         },

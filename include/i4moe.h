@@ -98,6 +98,14 @@ typedef struct i4_moe_weights {
   i4_qweight  down;       /* [E][H][I]                                       */
   const void* router_w;   /* [E][H] dense, in the activation dtype; may be
                              NULL when logits are passed to i4_moe_forward    */
+  const void* norm_w;     /* [H] in the activation dtype, or NULL.  When set,
+                             the block runs on RMSNorm(x) -- the decoder
+                             layer's post_attention_layernorm in front of the
+                             MoE (transformers Qwen3OmniMoeThinkerTextRMSNorm:
+                             w * (x * rsqrt(mean(x^2) + eps)).to(dtype)) --
+                             while the residual stays the un-normalised input.
+                             Requires router_w.                               */
+  float       norm_eps;
 } i4_moe_weights;
 
 int         i4_abi_version(void);
@@ -145,10 +153,13 @@ int    i4_repack_awq_to_ct(const i4_qweight* src, int32_t* dst_packed, void* dst
                            hipStream_t stream);
 
 /* Router half of FusedPackedMoE.forward (fused_packed_moe.py:195):
- *   logits[t][e] = sum_h x[t][h] * router_w[e][h], fp32 accumulation,
- * rounded to x_dtype like the reference's half-precision gate Linear. */
+ *   logits[t][e] = sum_h xn[t][h] * router_w[e][h], fp32 accumulation,
+ * rounded to x_dtype like the reference's half-precision gate Linear.
+ * xn = x, or RMSNorm(x) with weight norm_w when norm_w is not NULL; xn_out
+ * ([T][H], nullable) receives xn. */
 int    i4_router_logits(const void* x, int x_dtype, int T, int H,
-                        const void* router_w, int E, void* logits, hipStream_t stream);
+                        const void* router_w, int E, const void* norm_w, float norm_eps,
+                        void* xn_out, void* logits, hipStream_t stream);
 
 /* Routing (fused_packed_moe.py:195-199): softmax in fp32 over E logits,
  * top-k, optional renormalisation.  Ties are broken by the lower expert id.

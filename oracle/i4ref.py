@@ -196,6 +196,18 @@ def router_logits(x, router_w, dtype: str) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# pre-MoE RMSNorm of the Thinker decoder layer (post_attention_layernorm; the
+# caller in front of FusedPackedMoE).  transformers 5.15
+# Qwen3OmniMoeThinkerTextRMSNorm.forward (modeling_qwen3_omni_moe.py:1388-1393):
+#   h = x.float(); h = h * rsqrt(mean(h^2) + eps); return weight * h.to(dtype)
+def rmsnorm(x, weight, eps: float, dtype: str) -> np.ndarray:
+    xf = np.asarray(x, np.float64)
+    var = np.mean(xf * xf, axis=-1, keepdims=True)
+    xn = round_half(xf / np.sqrt(var + eps), dtype)
+    return round_half(xn * np.asarray(weight, np.float64), dtype)
+
+
+# ---------------------------------------------------------------------------
 # MoE block: Triton branch of FusedPackedMoE.forward (fused_packed_moe.py:222-263)
 # with the CPU branch's fp32-everywhere arithmetic (:202-220); act is rounded to
 # the activation dtype between the projections exactly as :257 does.

@@ -46,7 +46,8 @@ class QWeightC(ctypes.Structure):
 class MoeWeightsC(ctypes.Structure):
     """struct i4_moe_weights"""
 
-    _fields_ = [("gate_up", QWeightC), ("down", QWeightC), ("router_w", c_void_p)]
+    _fields_ = [("gate_up", QWeightC), ("down", QWeightC), ("router_w", c_void_p),
+                ("norm_w", c_void_p), ("norm_eps", ctypes.c_float)]
 
 
 # name -> (restype, argtypes); every function declared in include/i4moe.h
@@ -64,7 +65,7 @@ SIGNATURES = {
     "i4_repack_awq_to_ct": (c_int, [POINTER(QWeightC), c_void_p, c_void_p, c_void_p, c_int, c_int,
                                     c_void_p]),
     "i4_router_logits": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p,
-                                 c_void_p]),
+                                 ctypes.c_float, c_void_p, c_void_p, c_void_p]),
     "i4_route_topk": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                               c_void_p, c_int, c_void_p]),
     "i4_moe_forward": (c_int, [c_void_p, c_int, c_int, POINTER(MoeWeightsC), c_int, c_int,

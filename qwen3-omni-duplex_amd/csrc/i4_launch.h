@@ -24,6 +24,6 @@ int i4_launch_gemv_ct(const void* x, int xt, int64_t x_stride, const i4_qweight*
 
 // Launch router logits / top-k without re-validating (callers validated).
 int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr, int E,
-                            void* logits, hipStream_t s);
+                            const void* norm_w, float eps, void* xn, void* logits, hipStream_t s);
 int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
                    float* wf, void* wh, int wht, hipStream_t s);

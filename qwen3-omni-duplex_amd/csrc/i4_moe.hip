@@ -381,6 +381,7 @@ inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct MoeWs {
   void* logits;
+  uint16_t* xn;
   int32_t* sel;
   float* w;
   uint16_t* act;
@@ -402,6 +403,7 @@ MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
     return p;
   };
   m.logits = take((size_t)Tc * E * 2);
+  m.xn = (uint16_t*)take((size_t)Tc * H * 2);
   m.sel = (int32_t*)take(Tk * 4);
   m.w = (float*)take(Tk * 4);
   m.act = (uint16_t*)take(Tk * I * 2);
@@ -574,9 +576,11 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   int rc;
   const void* lg = logits;
   if (mw->router_w) {
-    rc = i4_launch_router_logits(x, xt, T, H, mw->router_w, E, ws.logits, s);
+    rc = i4_launch_router_logits(x, xt, T, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
+                                 mw->norm_w ? ws.xn : nullptr, ws.logits, s);
     if (rc) return rc;
     lg = ws.logits;
+    if (mw->norm_w) x = ws.xn;  // the experts run on RMSNorm(x); residual is untouched
   }
   int32_t* sel = sel_out ? sel_out : ws.sel;
   float* wts = w_out ? w_out : ws.w;
@@ -629,6 +633,8 @@ int i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weig
   if (rc) return rc;
   if (!x || !out) return I4_ERR_NULL;
   if (!weights->router_w && !logits) return I4_ERR_NULL;
+  if (weights->norm_w && !weights->router_w) return I4_ERR_NULL;
+  if ((uintptr_t)weights->norm_w & 15) return I4_ERR_ALIGN;
   if (((uintptr_t)x & 15) || ((uintptr_t)out & 15) || ((uintptr_t)residual & 15))
     return I4_ERR_ALIGN;
   const int H = gu.K, I = dn.K, E = gu.E;

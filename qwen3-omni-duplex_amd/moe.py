@@ -65,7 +65,8 @@ class FusedPackedMoE(nn.Module):
         self._install(QWeight(gu_p, gu_s, None, "ct", group, 2 * inter, hidden),
                       QWeight(dp, ds, None, "ct", group, hid_out, inter_in), gw)
 
-    def _install(self, gate_up: QWeight, down: QWeight, router_w: torch.Tensor) -> None:
+    def _install(self, gate_up: QWeight, down: QWeight, router_w: torch.Tensor,
+                 norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6) -> None:
         if gate_up.layout != "ct" or down.layout != "ct":
             raise ValueError("FusedPackedMoE stores CT weights (convert AWQ with from_awq)")
         self.gate_up, self.down = gate_up, down
@@ -74,6 +75,8 @@ class FusedPackedMoE(nn.Module):
         self.hidden = gate_up.K
         self.hid_out, self.inter_in = down.N, down.K
         self.register_buffer("router_w", router_w, persistent=False)
+        self.register_buffer("norm_weight", norm_weight, persistent=False)
+        self.norm_eps = float(norm_eps)
         for name, t in (("gu_packed", gate_up.packed), ("gu_scale", gate_up.scale),
                         ("gu_zeros", gate_up.zeros), ("down_packed", down.packed),
                         ("down_scale", down.scale), ("down_zeros", down.zeros)):
@@ -81,28 +84,39 @@ class FusedPackedMoE(nn.Module):
 
     @classmethod
     def from_stacked(cls, gate_up: QWeight, down: QWeight, router_w: torch.Tensor, top_k: int,
-                     norm_topk_prob: bool = True) -> "FusedPackedMoE":
+                     norm_topk_prob: bool = True, norm_weight: torch.Tensor | None = None,
+                     norm_eps: float = 1e-6) -> "FusedPackedMoE":
+        """From CT weights.  norm_weight fuses the decoder's pre-MoE RMSNorm (optional)."""
         m = cls()
         m.top_k, m.norm_topk_prob = int(top_k), bool(norm_topk_prob)
-        m._install(gate_up, down, router_w.contiguous())
+        m._install(gate_up, down, router_w.contiguous(),
+                   None if norm_weight is None else norm_weight.contiguous(), norm_eps)
         return m
 
     @classmethod
     def from_awq(cls, gate: QWeight, up: QWeight, down: QWeight, router_w: torch.Tensor,
-                 top_k: int, norm_topk_prob: bool = True) -> "FusedPackedMoE":
+                 top_k: int, norm_topk_prob: bool = True, norm_weight: torch.Tensor | None = None,
+                 norm_eps: float = 1e-6) -> "FusedPackedMoE":
         """Experts in AutoAWQ packing; gate|up and down are repacked to CT+zeros."""
         gu = repack_awq_to_ct([gate, up])
         dn = repack_awq_to_ct([down])
-        return cls.from_stacked(gu, dn, router_w, top_k, norm_topk_prob)
+        return cls.from_stacked(gu, dn, router_w, top_k, norm_topk_prob, norm_weight, norm_eps)
 
     def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor | None = None):
+        """MoE(hidden_states) (+ residual); with a fused norm, MoE(RMSNorm(hidden_states))."""
         return ops.moe_forward(hidden_states, self.gate_up, self.down, self.top_k,
                                router_w=self.router_w, norm_topk_prob=self.norm_topk_prob,
-                               residual=residual, workspace=self.workspace)
+                               residual=residual, workspace=self.workspace,
+                               norm_w=self.norm_weight, norm_eps=self.norm_eps)
+
+    def stack_entry(self) -> tuple:
+        """(gate_up, down, router_w, norm_w, eps) for ops.moe_stack."""
+        return (self.gate_up, self.down, self.router_w, self.norm_weight, self.norm_eps)
 
     def route(self, hidden_states: torch.Tensor):
-        """(w, sel) exactly as forward() routes: router Linear, softmax, top-k, renorm."""
-        lg = ops.router_logits(hidden_states.reshape(-1, self.hidden), self.router_w)
+        """(w, sel) exactly as forward() routes: [norm,] router Linear, softmax, top-k, renorm."""
+        lg = ops.router_logits(hidden_states.reshape(-1, self.hidden), self.router_w,
+                               self.norm_weight, self.norm_eps)
         return ops.route(lg, self.top_k, self.norm_topk_prob)
 
 

@@ -124,19 +124,28 @@ def dequant(w: QWeight, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     return out
 
 
-def router_logits(x: torch.Tensor, router_w: torch.Tensor) -> torch.Tensor:
-    """gate(x): [T, H] x [E, H]^T -> [T, E] in x.dtype, fp32 accumulation."""
-    dev = _lib.require_device(x, router_w)
+def router_logits(x: torch.Tensor, router_w: torch.Tensor, norm_w: torch.Tensor | None = None,
+                  norm_eps: float = 1e-6, return_xn: bool = False):
+    """gate(x): [T, H] x [E, H]^T -> [T, E] in x.dtype, fp32 accumulation.
+
+    With norm_w the router runs on RMSNorm(x) (and return_xn gives it back).
+    """
+    dev = _lib.require_device(x, router_w, norm_w)
     xt = _lib.half_code(x.dtype)
-    if router_w.dtype != x.dtype:
-        raise RuntimeError("router weight must have the activation dtype")
+    if router_w.dtype != x.dtype or (norm_w is not None and norm_w.dtype != x.dtype):
+        raise RuntimeError("router and norm weights must have the activation dtype")
     xf = x.reshape(-1, x.shape[-1]).contiguous()
     T, H = xf.shape
     E = router_w.shape[0]
     wr = router_w.contiguous()
+    nw = None if norm_w is None else norm_w.contiguous()
     out = torch.empty(T, E, dtype=x.dtype, device=dev)
+    xn = torch.empty_like(xf) if (return_xn and nw is not None) else None
     _lib.check(_lib.lib().i4_router_logits(xf.data_ptr(), xt, T, H, wr.data_ptr(), E,
+                                           _lib.ptr(nw), float(norm_eps), _lib.ptr(xn),
                                            out.data_ptr(), _lib.stream(dev)))
+    if return_xn:
+        return out, (xn if xn is not None else xf)
     return out
 
 
@@ -161,10 +170,12 @@ def route(logits: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
     return w, sel
 
 
-def moe_weights_c(gate_up: QWeight, down: QWeight,
-                  router_w: torch.Tensor | None) -> _lib.MoeWeightsC:
+def moe_weights_c(gate_up: QWeight, down: QWeight, router_w: torch.Tensor | None,
+                  norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6) -> _lib.MoeWeightsC:
     return _lib.MoeWeightsC(gate_up=gate_up.c(), down=down.c(),
-                            router_w=None if router_w is None else router_w.data_ptr())
+                            router_w=None if router_w is None else router_w.data_ptr(),
+                            norm_w=None if norm_w is None else norm_w.data_ptr(),
+                            norm_eps=float(norm_eps))
 
 
 class Workspace:
@@ -182,9 +193,13 @@ class Workspace:
 def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
                 router_w: torch.Tensor | None = None, logits: torch.Tensor | None = None,
                 norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
-                return_routing: bool = False, workspace: Workspace | None = None):
-    """One int4 MoE block: out = residual + sum_j w_j down_e(silu(gate_e x) * up_e x)."""
-    dev = _lib.require_device(x, gate_up.packed, down.packed, router_w, logits, residual)
+                return_routing: bool = False, workspace: Workspace | None = None,
+                norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6):
+    """One int4 MoE block: out = residual + sum_j w_j down_e(silu(gate_e xn) * up_e xn).
+
+    xn = x, or RMSNorm(x) with weight norm_w (the decoder's post-attention norm).
+    """
+    dev = _lib.require_device(x, gate_up.packed, down.packed, router_w, logits, residual, norm_w)
     xt = _lib.half_code(x.dtype)
     shape = x.shape
     xf = x.reshape(-1, shape[-1]).contiguous()
@@ -202,7 +217,7 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
     lb = _lib.lib()
     nbytes = lb.i4_moe_workspace_bytes(T, H, I, E, top_k)
     ws = (workspace or Workspace()).get(nbytes, dev)
-    mw = moe_weights_c(gate_up, down, router_w)
+    mw = moe_weights_c(gate_up, down, router_w, norm_w, norm_eps)
     _lib.check(lb.i4_moe_forward(xf.data_ptr(), xt, T, ctypes.byref(mw), top_k,
                                  int(norm_topk_prob), _lib.ptr(lg), _lib.ptr(rs), out.data_ptr(),
                                  _lib.ptr(sel), _lib.ptr(wts), ws.data_ptr(), ws.numel(),
@@ -242,16 +257,16 @@ def moe_down_combine(act: torch.Tensor, down: QWeight, sel: torch.Tensor, w: tor
     return out
 
 
-def moe_stack(x: torch.Tensor, layers: list[tuple[QWeight, QWeight, torch.Tensor]], top_k: int,
+def moe_stack(x: torch.Tensor, layers: list[tuple], top_k: int,
               norm_topk_prob: bool = True, workspace: Workspace | None = None) -> torch.Tensor:
-    """h <- h + moe_l(h) over layers [(gate_up, down, router_w), ...]."""
+    """h <- h + moe_l(norm_l(h)) over layers [(gate_up, down, router_w[, norm_w[, eps]]), ...]."""
     dev = _lib.require_device(x)
     xt = _lib.half_code(x.dtype)
     shape = x.shape
     xf = x.reshape(-1, shape[-1]).contiguous()
     T, H = xf.shape
-    gu0, dn0, _ = layers[0]
-    arr = (_lib.MoeWeightsC * len(layers))(*[moe_weights_c(g, d, r) for g, d, r in layers])
+    gu0, dn0 = layers[0][0], layers[0][1]
+    arr = (_lib.MoeWeightsC * len(layers))(*[moe_weights_c(*layer) for layer in layers])
     lb = _lib.lib()
     nbytes = lb.i4_moe_stack_workspace_bytes(T, H, dn0.K, gu0.E, top_k)
     ws = (workspace or Workspace()).get(nbytes, dev)

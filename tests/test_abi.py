@@ -93,7 +93,13 @@ def test_call_validation_codes(pkg):
     assert lib.i4_route_topk(0x30000, 1, 1, 128, 0, 1, 0x40000, None, None, 0, None) == -2
     assert lib.i4_route_topk(0x30000, 1, 1, 1024, 8, 1, 0x40000, None, None, 0, None) == -2
     assert lib.i4_route_topk(0x30000, 5, 1, 128, 8, 1, 0x40000, None, None, 0, None) == -3
-    assert lib.i4_router_logits(0x30000, 1, 1, 2047, 0x40000, 128, 0x50000, None) == -2
+    assert lib.i4_router_logits(0x30000, 1, 1, 2047, 0x40000, 128, None, 1e-6, None, 0x50000,
+                                None) == -2
+    # xn output needs a norm weight; norm weight must be aligned
+    assert lib.i4_router_logits(0x30000, 1, 1, 2048, 0x40000, 128, None, 1e-6, 0x60000, 0x50000,
+                                None) == -1
+    assert lib.i4_router_logits(0x30000, 1, 1, 2048, 0x40000, 128, 0x60002, 1e-6, None, 0x50000,
+                                None) == -4
 
 
 def test_moe_validation_codes(pkg):
@@ -122,4 +128,8 @@ def test_moe_validation_codes(pkg):
     assert call(mw=awq) == -5
     nor = _lib.MoeWeightsC(gate_up=gu, down=dn, router_w=None)
     assert call(mw=nor) == -1
+    # a fused norm needs the router weight (it produces the normalised input)
+    nrm = _lib.MoeWeightsC(gate_up=gu, down=dn, router_w=None, norm_w=0x80000, norm_eps=1e-6)
+    assert lib.i4_moe_forward(0x30000, 1, 1, ctypes.byref(nrm), 8, 1, 0x90000, None, 0x70000,
+                              None, None, 0x100000, ws, None) == -1
     assert lib.i4_moe_stack_workspace_bytes(1, 2048, 768, 128, 8) > ws

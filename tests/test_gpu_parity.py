@@ -271,21 +271,39 @@ def _awq_moe(pkg, dev, rng, E=128, H=2048, I=768, G=128, sdt=np.float16):
     return moe, dgu, ddn, wr
 
 
-def _check_moe(pkg, moe, dgu, ddn, x_np, xdt, dev, logits=None, residual=None):
+def _check_moe(pkg, moe, dgu, ddn, x_np, xdt, dev, logits=None, residual=None, norm=None):
+    """Run one block on the GPU and check it against the oracle on the same inputs.
+
+    norm = (weight_np, eps): the block normalises x first; routing is checked
+    bit-exactly against the oracle's top-k of the GPU's own logits, and the
+    GPU's normalised input is checked against the oracle's RMSNorm.
+    """
     x = t_(x_np, dev)
     kw = dict(router_w=moe.router_w) if logits is None else dict(logits=t_(logits, dev))
+    if norm is not None:
+        kw.update(norm_w=t_(norm[0], dev), norm_eps=norm[1])
     out, sel, w = pkg.moe_forward(x, moe.gate_up, moe.down, moe.top_k, return_routing=True,
                                   residual=None if residual is None else t_(residual, dev), **kw)
+    xin = f_(x_np)
     if logits is None:
-        lg = host(pkg.router_logits(x, moe.router_w))
+        if norm is None:
+            lg = host(pkg.router_logits(x, moe.router_w))
+        else:
+            lg_t, xn_t = pkg.router_logits(x, moe.router_w, t_(norm[0], dev), norm[1],
+                                           return_xn=True)
+            lg, xin = host(lg_t), host(xn_t)
+            ref_xn = i4ref.rmsnorm(f_(x_np), f_(norm[0]), norm[1], half_name(xdt))
+            ulp = np.abs(ref_xn) * (2.0 ** (-10 if xdt == "f16" else -7)) + 1e-7
+            assert np.all(np.abs(xin - ref_xn) <= 2 * ulp)
     else:
         lg = f_(logits)
     sel_ref, w_ref = i4ref.route(lg, moe.top_k)
     np.testing.assert_array_equal(sel.cpu().numpy(), sel_ref)          # bit-exact routing
     np.testing.assert_allclose(host(w), w_ref, rtol=1e-5, atol=1e-7)
-    ref = i4ref.moe_layer_grouped(f_(x_np), sel_ref, w_ref, dgu, ddn, half_name(xdt),
+    ref = i4ref.moe_layer_grouped(xin, sel_ref, w_ref, dgu, ddn, half_name(xdt),
                                   residual=None if residual is None else f_(residual))
     got = host(out)
+    assert np.all(np.isfinite(got))
     err = i4ref.rel_err(got, ref)
     assert err <= TOL, err
     return got, err
@@ -355,19 +373,44 @@ def test_moe_is_deterministic(pkg, dev):
 
 
 def test_stack_matches_layer_loop_and_oracle(pkg, dev):
-    """h <- h + moe_l(h) for 3 layers; each layer checked against the oracle on the GPU's input."""
+    """h <- h + moe_l(RMSNorm_l(h)) for 4 layers; each layer checked against the oracle on the
+    GPU's own input, and the one-call stack equals the layer-by-layer loop bit for bit."""
     rng = np.random.default_rng(27)
-    layers = [_awq_moe(pkg, dev, rng, E=32) for _ in range(3)]
+    layers = []
+    for _ in range(4):
+        m, dgu, ddn, _ = _awq_moe(pkg, dev, rng, E=32)
+        nw = rng.uniform(0.5, 1.5, 2048).astype(np.float16)
+        m.register_buffer("norm_weight", t_(nw, dev), persistent=False)
+        m.norm_eps = 1e-6
+        layers.append((m, dgu, ddn, nw))
     x = make_x(rng, (1, 2048), "f16")
     xt = t_(x, dev)
-    stack = pkg.moe_stack(xt, [(m.gate_up, m.down, m.router_w) for m, _, _, _ in layers], 8)
+    stack = pkg.moe_stack(xt, [m.stack_entry() for m, _, _, _ in layers], 8)
     h = xt
-    for m, dgu, ddn, _ in layers:
+    for m, dgu, ddn, nw in layers:
         h_np = host(h).astype(np.float16)
         h_next = m(h, residual=h)
-        _check_moe(pkg, m, dgu, ddn, h_np, "f16", dev, residual=h_np)
+        _check_moe(pkg, m, dgu, ddn, h_np, "f16", dev, residual=h_np, norm=(nw, 1e-6))
         h = h_next
+    assert torch.isfinite(stack).all()
     assert torch.equal(stack, h)
+
+
+@pytest.mark.parametrize("T", [1, 9])
+def test_router_logits_with_norm(pkg, dev, T):
+    rng = np.random.default_rng(29 + T)
+    E, H = 128, 2048
+    wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float16)
+    nw = rng.uniform(0.5, 1.5, H).astype(np.float16)
+    x = (rng.standard_normal((T, H)) * 40).astype(np.float16)
+    lg, xn = pkg.router_logits(t_(x, dev), t_(wr, dev), t_(nw, dev), 1e-6, return_xn=True)
+    ref_xn = i4ref.rmsnorm(f_(x), f_(nw), 1e-6, "f16")
+    got_xn = host(xn).astype(np.float64)
+    assert np.all(np.abs(got_xn - ref_xn) <= 2 * np.abs(ref_xn) * 2.0 ** -10 + 1e-7)
+    assert np.mean(got_xn == ref_xn) > 0.99
+    ref = i4ref.router_logits(got_xn, f_(wr), "f16")
+    got = host(lg).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -10 + 1e-6)
 
 
 def test_graph_replays_match_eager(pkg, dev):

@@ -204,6 +204,29 @@ def test_bf16_rounding_matches_torch():
     np.testing.assert_array_equal(i4ref.round_half(a, "f16"), a.astype(np.float16).astype(np.float64))
 
 
+# ---------------------------------------------------------------- RMSNorm
+@pytest.mark.parametrize("dt,tdt", [("f16", torch.float16), ("bf16", torch.bfloat16)])
+def test_rmsnorm_matches_torch(dt, tdt):
+    """Against torch's own rms_norm followed by the transformers cast-and-scale order."""
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(16, 2048, generator=g) * 30).to(tdt)
+    w = (torch.rand(2048, generator=g) + 0.5).to(tdt)
+    ref = (w * torch.nn.functional.rms_norm(x.float(), (2048,), eps=1e-6).to(tdt)).float().numpy()
+    got = i4ref.rmsnorm(x.float().numpy(), w.float().numpy(), 1e-6, dt)
+    ulp = np.abs(ref) * (2.0 ** (-10 if dt == "f16" else -7))
+    assert np.all(np.abs(got - ref) <= 2 * ulp + 1e-12)
+    assert np.mean(got == ref) > 0.99
+
+
+def test_rmsnorm_invariants():
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((4, 256)) * 7
+    ones = np.ones(256)
+    y = i4ref.rmsnorm(x, ones, 1e-6, "f16")
+    np.testing.assert_allclose(np.sqrt(np.mean(y * y, axis=-1)), 1.0, rtol=2e-3)
+    np.testing.assert_array_equal(i4ref.rmsnorm(4 * x, ones, 0.0, "f16"), i4ref.rmsnorm(x, ones, 0.0, "f16"))
+
+
 # ---------------------------------------------------------------- MoE layer
 def _golden_moe():
     g = GOLD["moe_layer"]
