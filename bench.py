@@ -105,23 +105,25 @@ def gpu_backlog(torch, dev, ms=20.0):
     return c
 
 
-def time_gate_up(pkg, torch, dev, mods, xs, routing, rounds):
-    """Per-launch HIP-event duration of the decode gate_up+SiLU kernel (and batched)."""
+def time_gate_up(pkg, torch, dev, mods, xns, logits, rounds):
+    """HIP-event timing of the dominant kernel, the decode route + gate_up + SiLU launch, on
+    each layer's own normalised input and logits: back-to-back launches over the layers
+    between one pair of events (average per launch), and each launch bracketed by its own
+    events behind a queued backlog (includes the event overhead)."""
     lb = pkg.lib()
     from qwen3_omni_duplex_amd import _lib
 
     stream = torch.cuda.current_stream(dev)
     s_ptr = stream.cuda_stream
     acts = [torch.empty(TOPK, I, dtype=torch.float16, device=dev) for _ in mods]
+    sel = torch.empty(TOPK, dtype=torch.int32, device=dev)
+    wts = torch.empty(TOPK, dtype=torch.float32, device=dev)
     cws = [m.gate_up.c() for m in mods]
-    args = []
-    for li in range(len(mods)):
-        x = xs[li % len(xs)]
-        args.append((x.data_ptr(), _lib.F16, ctypes.byref(cws[li]), routing[li].data_ptr(), TOPK,
-                     acts[li].data_ptr(), s_ptr))
+    args = [(xns[li].data_ptr(), _lib.F16, ctypes.byref(cws[li]), logits[li].data_ptr(), E, TOPK, 1,
+             sel.data_ptr(), wts.data_ptr(), acts[li].data_ptr(), s_ptr) for li in range(len(mods))]
 
     def launch(li):
-        rc = lb.i4_moe_gate_up(*args[li])
+        rc = lb.i4_moe_route_gate_up(*args[li])
         if rc:
             raise RuntimeError(lb.i4_strerror(rc).decode())
 
@@ -129,7 +131,15 @@ def time_gate_up(pkg, torch, dev, mods, xs, routing, rounds):
     for li in range(n):  # warm
         launch(li)
     torch.cuda.synchronize()
-    # (a) every launch bracketed by its own events, behind a backlog
+    gpu_backlog(torch, dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(rounds):
+        for li in range(n):
+            launch(li)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    batched = e0.elapsed_time(e1) * 1e3 / (n * rounds)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(n * rounds)]
     gpu_backlog(torch, dev)
@@ -141,19 +151,8 @@ def time_gate_up(pkg, torch, dev, mods, xs, routing, rounds):
             evs[k][1].record(stream)
             k += 1
     torch.cuda.synchronize()
-    per = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
-    # (b) back-to-back launches between one pair of events
-    gpu_backlog(torch, dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(rounds):
-        for li in range(n):
-            launch(li)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    batched = e0.elapsed_time(e1) * 1e3 / (n * rounds)
-    mean = sum(per) / len(per)
-    return mean, per[len(per) // 2], batched
+    per = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    return batched, sum(per) / len(per)
 
 
 def cpu_baseline(torch, first, xs, seconds):
@@ -259,20 +258,19 @@ def main() -> int:
     ms = ms_graph if ms_graph is not None else ms_eager
     us_layer = ms * 1e3 / args.layers
 
-    # ---- dominant kernel: decode gate_up + SiLU, per-launch HIP events
-    routing = []
+    # ---- dominant kernel: decode route + gate_up + SiLU, HIP events on its stream
+    xns, lgs = [], []
     h = xs[1]
     for m in mods:
-        o, sel, _ = ops.moe_forward(h, m.gate_up, m.down, TOPK, router_w=m.router_w,
-                                    residual=h, return_routing=True, workspace=ws,
-                                    norm_w=m.norm_weight, norm_eps=m.norm_eps)
-        routing.append(sel.reshape(-1).contiguous())
-        h = o
+        lg, xn = ops.router_logits(h, m.router_w, m.norm_weight, m.norm_eps, return_xn=True)
+        xns.append(xn.reshape(-1).contiguous())
+        lgs.append(lg.reshape(-1).contiguous())
+        h = m(h, residual=h)
     torch.cuda.synchronize()
-    k_mean, k_med, k_batched = time_gate_up(pkg, torch, dev, mods, xs, routing, args.kernel_rounds)
-    achieved = B_GATE_UP_LAUNCH / (k_mean * 1e-6) / 1e9
-    log(f"gate_up kernel: mean {k_mean:.2f} us, median {k_med:.2f} us, back-to-back {k_batched:.2f}"
-        f" us -> {achieved:.0f} GB/s")
+    k_us, k_evt = time_gate_up(pkg, torch, dev, mods, xns, lgs, args.kernel_rounds)
+    achieved = B_GATE_UP_LAUNCH / (k_us * 1e-6) / 1e9
+    log(f"route+gate_up kernel: {k_us:.2f} us/launch back-to-back ({k_evt:.2f} with per-launch "
+        f"events) -> {achieved:.0f} GB/s")
 
     # ---- CPU baseline
     cpu = None
@@ -309,11 +307,11 @@ def main() -> int:
         "layer_GBps": round(B_LAYER / (us_layer * 1e-6) / 1e9, 1),
         "layer_hbm_frac": round(B_LAYER / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": "k_moe_gate_up (decode gate+up+SiLU, 8 experts)",
+            "kernel": "k_moe_gate_up<route> (decode top-8 routing + gate/up + SiLU, 8 experts)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "bytes_per_launch": B_GATE_UP_LAUNCH, "us_per_launch": round(k_mean, 3),
-            "us_per_launch_back_to_back": round(k_batched, 3),
+            "bytes_per_launch": B_GATE_UP_LAUNCH, "us_per_launch": round(k_us, 3),
+            "us_per_launch_own_events": round(k_evt, 3),
         },
         "cpu_baseline": cpu,
     }

@@ -181,6 +181,10 @@ int    i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* w
                       int topk, int renorm, const void* logits, const void* residual,
                       void* out, int32_t* sel_out, float* w_out,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* Workspace of i4_moe_forward.  Its bytes must be zero before the first call
+ * that uses it (e.g. hipMemset once at allocation); every call leaves the
+ * small handoff-counter region zero again, so no per-call clearing is needed.
+ * Calls that share one workspace must not overlap. */
 size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
 
 /* The two expert stages of one decode token with routing already known --
@@ -192,6 +196,13 @@ size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
  * x, residual and out are [H]; act is [topk][I]; sel [topk]; w [topk] fp32. */
 int    i4_moe_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up,
                       const int32_t* sel, int topk, void* act, hipStream_t stream);
+/* Routing (fused_packed_moe.py:195-199) and the gate_up stage of one decode
+ * token in one launch: every workgroup ranks the E_r half-precision logits
+ * itself; sel_out / w_out ([topk], fp32) receive the routing for the down
+ * stage.  This is the decode path i4_moe_forward takes at T = 1. */
+int    i4_moe_route_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up,
+                            const void* logits, int E_r, int topk, int renorm,
+                            int32_t* sel_out, float* w_out, void* act, hipStream_t stream);
 int    i4_moe_down_combine(const void* act, int x_dtype, const i4_qweight* down,
                            const int32_t* sel, const float* w, int topk,
                            const void* residual, void* out, hipStream_t stream);

@@ -13,14 +13,16 @@ from . import _lib
 from .linear import PackedLinear, patch_attention
 from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_forward, moe_gate_up,
-                  moe_stack, route, router_logits, unpack4, unpack_nibbles, Workspace)
+                  moe_route_gate_up, moe_stack, route, router_logits, unpack4, unpack_nibbles,
+                  Workspace)
 from .weights import QWeight, repack_awq_to_ct
 
 lib = _lib.lib
 
 __all__ = [
     "QWeight", "repack_awq_to_ct", "dequant_gemv", "linear", "unpack4", "unpack_nibbles",
-    "dequant", "router_logits", "route", "moe_forward", "moe_gate_up", "moe_down_combine",
+    "dequant", "router_logits", "route", "moe_forward", "moe_gate_up", "moe_route_gate_up",
+    "moe_down_combine",
     "moe_stack", "Workspace",
     "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "patch_attention", "lib",
 ]

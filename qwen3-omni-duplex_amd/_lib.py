@@ -74,6 +74,8 @@ SIGNATURES = {
     "i4_moe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "i4_moe_gate_up": (c_int, [c_void_p, c_int, POINTER(QWeightC), c_void_p, c_int, c_void_p,
                                c_void_p]),
+    "i4_moe_route_gate_up": (c_int, [c_void_p, c_int, POINTER(QWeightC), c_void_p, c_int, c_int,
+                                     c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "i4_moe_down_combine": (c_int, [c_void_p, c_int, POINTER(QWeightC), c_void_p, c_void_p, c_int,
                                     c_void_p, c_void_p, c_void_p]),
     "i4_moe_stack_forward": (c_int, [c_void_p, c_int, c_int, POINTER(MoeWeightsC), c_int, c_int,

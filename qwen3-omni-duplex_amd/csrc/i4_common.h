@@ -5,13 +5,17 @@
 // p+4 to bits 16..19; OR-ing the exponent pattern of a half-precision M turns
 // the two 16-bit lanes into the exact values M + q (M = 1024 for fp16, whose
 // ulp there is 1; M = 128 for bf16, whose ulp there is 1 as well).  One
-// v_and_or_b32 (plus a shift for p > 0) therefore yields a (k0+p, k0+p+4)
-// pair ready for v_dot2_f32_{f16,bf16}, which multiplies exactly and
-// accumulates in fp32.  The bias M and the zero point z are removed per
-// 32-column chunk with the chunk's activation sum S:
-//     sum (q - z) x = sum (M + q) x - (M + z) S.
+// v_and_or_b32 (plus a shift) therefore yields a (k0+p, k0+p+4) pair ready
+// for v_dot2_f32_{f16,bf16}, which multiplies exactly and accumulates in fp32.
+// fp16 saves two shifts per word: w & 0x00F000F0 reads nibbles 1 and 5 in
+// place as the exact values M + 16q (< 2048); those pairs accumulate
+// separately and enter the chunk sum divided by 16.
+// The bias M and the zero point z are removed per 32-column chunk with the
+// chunk's activation sums: with S the plain sum and Sb the bias coefficient
+// (S for bf16; S_lo + S_hi / 16 for fp16, lo = pairs 0 and 2),
+//     sum (q - z) x = (lo + hi / 16) - M Sb - z S.
 // Activations are staged once per workgroup in LDS, already permuted into the
-// same (k0+p, k0+p+4) pair order, together with the chunk sums S.
+// (k0+p, k0+p+4) pair order, together with (Sb, S) per chunk.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -140,29 +144,41 @@ template <int OT> __device__ inline void store_out(void* p, int64_t i, float v) 
 }
 
 // ---------------------------------------------------------------------------
-// nibble decode + dot: 8 columns of one CT word against 4 staged x pairs
-template <int XT> __device__ inline float dot8(u32 w, u32x4 xp, float acc) {
+// nibble decode + dot of one CT word (8 columns) against its 4 staged x pairs;
+// lo / hi accumulate the pairs as described at the top of this file.
+template <int XT> __device__ inline void dot8(u32 w, u32x4 xp, float& lo, float& hi) {
   constexpr u32 MK = 0x000F000Fu, MG = Half<XT>::MAGIC2;
-  acc = Half<XT>::dot2((w & MK) | MG, xp.x, acc);
-  acc = Half<XT>::dot2(((w >> 4) & MK) | MG, xp.y, acc);
-  acc = Half<XT>::dot2(((w >> 8) & MK) | MG, xp.z, acc);
-  acc = Half<XT>::dot2(((w >> 12) & MK) | MG, xp.w, acc);
-  return acc;
+  if constexpr (XT == I4_F16) {
+    const u32 t = w >> 8;
+    lo = Half<XT>::dot2((w & MK) | MG, xp.x, lo);
+    hi = Half<XT>::dot2((w & 0x00F000F0u) | MG, xp.y, hi);
+    lo = Half<XT>::dot2((t & MK) | MG, xp.z, lo);
+    hi = Half<XT>::dot2((t & 0x00F000F0u) | MG, xp.w, hi);
+  } else {
+    lo = Half<XT>::dot2((w & MK) | MG, xp.x, lo);
+    hi = Half<XT>::dot2(((w >> 4) & MK) | MG, xp.y, hi);
+    lo = Half<XT>::dot2(((w >> 8) & MK) | MG, xp.z, lo);
+    hi = Half<XT>::dot2(((w >> 12) & MK) | MG, xp.w, hi);
+  }
 }
 
-// sum over one chunk of (q - z) * s * x given the staged x words of the chunk
-// (xw0..xw3, pair order) and their sum S
+// hi-pair weight of the fp16 decode (its pairs carry 16q)
+template <int XT> constexpr float hi_scale() { return XT == I4_F16 ? 1.0f / 16.0f : 1.0f; }
+
+// sum over one chunk of (q - z) * s * x given the chunk's staged x words
+// (xw0..xw3, pair order) and its sums (Sb, S)
 template <int XT, int ST>
 __device__ inline float chunk_dot(const Chunk& k, u32x4 xw0, u32x4 xw1, u32x4 xw2, u32x4 xw3,
-                                  float S, int c, int gshift) {
-  float a = 0.f;
-  a = dot8<XT>(k.w.x, xw0, a);
-  a = dot8<XT>(k.w.y, xw1, a);
-  a = dot8<XT>(k.w.z, xw2, a);
-  a = dot8<XT>(k.w.w, xw3, a);
+                                  float2 sums, int c, int gshift) {
+  float lo = 0.f, hi = 0.f;
+  dot8<XT>(k.w.x, xw0, lo, hi);
+  dot8<XT>(k.w.y, xw1, lo, hi);
+  dot8<XT>(k.w.z, xw2, lo, hi);
+  dot8<XT>(k.w.w, xw3, lo, hi);
   const int g = c >> gshift;
   const float z = (float)((k.z >> (4 * (g & 7))) & 15u);
-  return scale_from_raw<ST>(k.s) * (a - (Half<XT>::MAGIC + z) * S);
+  const float a = fmaf(hi, hi_scale<XT>(), lo);
+  return scale_from_raw<ST>(k.s) * (a - Half<XT>::MAGIC * sums.x - z * sums.y);
 }
 
 // Permute 8 consecutive half-precision x values (one 16-byte load, dwords
@@ -177,18 +193,14 @@ __device__ inline u32x4 pair_order(u32x4 d) {
   return r;
 }
 
-// fp32 sum of the 8 half values of one 16-byte load
-template <int XT> __device__ inline float sum8(u32x4 d) {
-  float s = 0.f;
-  s += Half<XT>::to_f32((uint16_t)(d.x & 0xFFFF));
-  s += Half<XT>::to_f32((uint16_t)(d.x >> 16));
-  s += Half<XT>::to_f32((uint16_t)(d.y & 0xFFFF));
-  s += Half<XT>::to_f32((uint16_t)(d.y >> 16));
-  s += Half<XT>::to_f32((uint16_t)(d.z & 0xFFFF));
-  s += Half<XT>::to_f32((uint16_t)(d.z >> 16));
-  s += Half<XT>::to_f32((uint16_t)(d.w & 0xFFFF));
-  s += Half<XT>::to_f32((uint16_t)(d.w >> 16));
-  return s;
+// (Sb, S) contribution of the 8 half values of one 16-byte load (see top)
+template <int XT> __device__ inline float2 sum8(u32x4 d) {
+  const float x0 = Half<XT>::to_f32((uint16_t)(d.x & 0xFFFF)), x1 = Half<XT>::to_f32((uint16_t)(d.x >> 16));
+  const float x2 = Half<XT>::to_f32((uint16_t)(d.y & 0xFFFF)), x3 = Half<XT>::to_f32((uint16_t)(d.y >> 16));
+  const float x4 = Half<XT>::to_f32((uint16_t)(d.z & 0xFFFF)), x5 = Half<XT>::to_f32((uint16_t)(d.z >> 16));
+  const float x6 = Half<XT>::to_f32((uint16_t)(d.w & 0xFFFF)), x7 = Half<XT>::to_f32((uint16_t)(d.w >> 16));
+  const float slo = ((x0 + x4) + (x2 + x6)), shi = ((x1 + x5) + (x3 + x7));
+  return make_float2(fmaf(shi, hi_scale<XT>(), slo), slo + shi);
 }
 
 // ---------------------------------------------------------------------------
@@ -214,23 +226,28 @@ template <int L> __device__ inline float group_sum(float v) {
   return v;
 }
 
-// Stage nr activation rows (row r starts at row_of(r), K halves each) into
-// LDS in decode pair order with per-chunk sums:
-//   xs [nr][4][C] uint4 (word jw of chunk c of row r at (r*4 + jw)*C + c),
-//   xsum [nr][C].
-// Up to 4 loads per thread are in flight before the first LDS write.
-template <int XT, class RowOf>
-__device__ inline void stage_rows(RowOf row_of, int nr, int K, u32x4* xs, float* xsum) {
-  const int C = K >> 5, words = K >> 3, total = nr * words;
-  const int nt = blockDim.x;
-  for (int i0 = 0; i0 < total; i0 += 4 * nt) {
-    u32x4 d[4];
+// Two-phase staging of nr activation rows (row r starts at row_of(r), K
+// halves each) into LDS in decode pair order with per-chunk sums:
+//   xs  [nr][4][C] uint4 (word jw of chunk c of row r at (r*4 + jw)*C + c),
+//   sums[nr][C] float2 (Sb, S).
+// issue() puts up to 4 loads per thread in flight and returns; the caller
+// issues its weight loads next and only then commit()s, so the LDS writes
+// wait for the activations alone (loads retire in issue order).
+template <int XT> struct Stager {
+  u32x4 d[4];
+  int total, words, C;
+  __device__ inline Stager(int nr, int K) : total(nr * (K >> 3)), words(K >> 3), C(K >> 5) {}
+  template <class RowOf> __device__ inline void issue(RowOf row_of, int i0) {
+    const int nt = blockDim.x;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int idx = min(i0 + u * nt + (int)threadIdx.x, total - 1);
       const int r = idx / words, m = idx - r * words;
       d[u] = ldg16(row_of(r) + 8 * m);
     }
+  }
+  __device__ inline void commit(int i0, u32x4* xs, float2* sums) {
+    const int nt = blockDim.x;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int idx = i0 + u * nt + (int)threadIdx.x;
@@ -238,12 +255,21 @@ __device__ inline void stage_rows(RowOf row_of, int nr, int K, u32x4* xs, float*
         const int r = idx / words, m = idx - r * words;
         const int c = m >> 2, jw = m & 3;
         xs[(r * 4 + jw) * C + c] = pair_order(d[u]);
-        const float sm = group_sum<4>(sum8<XT>(d[u]));
-        if (jw == 0) xsum[r * C + c] = sm;
+        float2 sm = sum8<XT>(d[u]);
+        sm.x = group_sum<4>(sm.x);
+        sm.y = group_sum<4>(sm.y);
+        if (jw == 0) sums[r * C + c] = sm;
       }
     }
   }
-}
+  // everything beyond the first round (rows longer than 4 * blockDim words)
+  template <class RowOf> __device__ inline void rest(RowOf row_of, u32x4* xs, float2* sums) {
+    for (int i0 = 4 * (int)blockDim.x; i0 < total; i0 += 4 * (int)blockDim.x) {
+      issue(row_of, i0);
+      commit(i0, xs, sums);
+    }
+  }
+};
 
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 

@@ -35,7 +35,7 @@ __global__ __launch_bounds__(WG) void k_gemv_ct(
   const int NG = (C + (1 << gshift) - 1) >> gshift, NZW = (NG + 7) >> 3;
   const int cpl = (C + L - 1) / L;
   u32x4* xs = (u32x4*)lds;
-  float* xsum = (float*)(lds + (size_t)K * 2);
+  float2* sums = (float2*)(lds + (size_t)K * 2);
 
   const int j = blockIdx.y;
   const int rl = threadIdx.x / L, cl = threadIdx.x % L;
@@ -56,6 +56,9 @@ __global__ __launch_bounds__(WG) void k_gemv_ct(
   rp.s = scale_at<ST>(scale, e * s_es + (int64_t)nn * NG);
   rp.z = zeros ? (const u32*)zeros + e * z_es + (int64_t)nn * NZW : kSymZeros;
   const uint16_t* xrow = x + (int64_t)j * x_stride;
+  Stager<XT> st(1, K);  // activation loads first, weight loads behind them
+  auto row_of = [&](int) { return xrow; };
+  st.issue(row_of, 0);
 
   float row = 0.f;
   for (int r0 = 0; r0 < cpl; r0 += ROUND) {
@@ -63,14 +66,15 @@ __global__ __launch_bounds__(WG) void k_gemv_ct(
 #pragma unroll
     for (int i = 0; i < ROUND; ++i) ch[i] = load_chunk<ST>(rp, min(cl + (r0 + i) * L, C - 1), gshift);
     if (r0 == 0) {
-      stage_rows<XT>([&](int) { return xrow; }, 1, K, xs, xsum);
+      st.commit(0, xs, sums);
+      st.rest(row_of, xs, sums);
       __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < ROUND; ++i) {
       const int c = cl + (r0 + i) * L;
       if (c < C)
-        row += chunk_dot<XT, ST>(ch[i], xs[c], xs[C + c], xs[2 * C + c], xs[3 * C + c], xsum[c], c,
+        row += chunk_dot<XT, ST>(ch[i], xs[c], xs[C + c], xs[2 * C + c], xs[3 * C + c], sums[c], c,
                                  gshift);
     }
   }
@@ -399,7 +403,7 @@ static int launch_gemv_ct_t(const void* x, int64_t x_stride, const i4_qweight* w
   const int L = lanes_per_row(C);
   const int rpw = WG / L;
   dim3 grid((w->N + rpw - 1) / rpw, k_sel);
-  const size_t lds = (size_t)w->K * 2 + (size_t)C * 4;
+  const size_t lds = (size_t)w->K * 2 + (size_t)C * 8;
   const int gshift = i4_group_shift(w->group);
 #define I4_GEMV_CASE(L_)                                                                        \
   if (L == L_) {                                                                                \

@@ -21,6 +21,7 @@
 // reference loops over tokens, fused_packed_moe.py:231).
 #include "i4_common.h"
 #include "i4_launch.h"
+#include "i4_topk.h"
 
 namespace i4 {
 
@@ -51,10 +52,18 @@ template <int ST> __device__ inline RowPtr row_ptr(const QW& w, int e, int n) {
 // ---------------------------------------------------------------------------
 // gate_up + SiLU.  L lanes per row pair (gate row n, up row I + n); a
 // workgroup owns WG/L consecutive row pairs of one entry (one expert and up
-// to MT of its tokens).  DIRECT: entry j is slot j of token 0 (decode).
-template <int XT, int ST, int L, int MT, bool DIRECT>
+// to MT of its tokens).
+//   GU_SEL:   decode, entry j is slot j of token 0, experts from sel[]
+//   GU_ROUTE: decode, every wave ranks the E logits itself (top-k + softmax,
+//             bit-identical in every wave) and takes slot j; workgroup
+//             (0, 0) writes sel[] / wts[] for the down projection
+//   GU_LIST:  grouped entries {expert, first position, count} from k_group
+enum { GU_SEL = 0, GU_ROUTE = 1, GU_LIST = 2 };
+
+template <int XT, int ST, int L, int MT, int MODE>
 __global__ __launch_bounds__(WG) void k_moe_gate_up(
-    const uint16_t* __restrict__ x, int topk, const int32_t* __restrict__ sel,
+    const uint16_t* __restrict__ x, int topk, int32_t* __restrict__ sel,
+    const uint16_t* __restrict__ logits, int E_r, int renorm, float* __restrict__ wts,
     const int4* __restrict__ entries, const int* __restrict__ n_entries,
     const int32_t* __restrict__ perm, QW w, int I, uint16_t* __restrict__ act) {
   extern __shared__ __align__(16) unsigned char lds[];
@@ -63,31 +72,47 @@ __global__ __launch_bounds__(WG) void k_moe_gate_up(
   const int H = w.K, C = H >> 5;
   const int cpl = (C + L - 1) / L;
   u32x4* xs = (u32x4*)lds;
-  float* xsum = (float*)(lds + (size_t)MT * H * 2);
+  float2* sums = (float2*)(lds + (size_t)MT * H * 2);
 
-  int e, pos0, cnt;
-  if constexpr (DIRECT) {
-    e = sel[blockIdx.y];
-    pos0 = blockIdx.y;
-    cnt = 1;
-  } else {
+  int pos0 = blockIdx.y, cnt = 1;
+  if constexpr (MODE == GU_LIST) {
     if ((int)blockIdx.y >= *n_entries) return;
+  }
+  // activations first: their loads retire before the weight loads below
+  Stager<XT> st(MT, H);
+  auto row_of = [&](int t) -> const uint16_t* {
+    if constexpr (MODE == GU_LIST) return x + (int64_t)(perm[pos0 + min(t, cnt - 1)] / topk) * H;
+    else return x;
+  };
+  int e;
+  if constexpr (MODE == GU_LIST) {
     const int4 en = entries[blockIdx.y];
     e = en.x;
     pos0 = en.y;
     cnt = en.z;
+    st.issue(row_of, 0);
+  } else if constexpr (MODE == GU_ROUTE) {
+    st.issue(row_of, 0);
+    int my_sel = 0;
+    float my_w = 0.f;
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64;
+    if (E_r <= 128)
+      wave_topk_row<XT, 2>(logits, 0, E_r, topk, renorm, writer ? sel : nullptr,
+                           writer ? wts : nullptr, nullptr, 0, &my_sel, &my_w);
+    else
+      wave_topk_row<XT, 8>(logits, 0, E_r, topk, renorm, writer ? sel : nullptr,
+                           writer ? wts : nullptr, nullptr, 0, &my_sel, &my_w);
+    e = __builtin_amdgcn_readlane(my_sel, blockIdx.y);
+  } else {
+    st.issue(row_of, 0);
+    e = sel[blockIdx.y];
   }
   const int rl = threadIdx.x / L, cl = threadIdx.x % L;
   const int n = blockIdx.x * RPW + rl;
   const bool rv = n < I;
-  if ((unsigned)e >= (unsigned)w.E) {
-    if (rv && cl == 0)
-      for (int t = 0; t < cnt; ++t)
-        act[(int64_t)(pos0 + t) * I + n] = Half<XT>::from_f32(__builtin_nanf(""));
-    return;
-  }
-  const int nn = rv ? n : 0;
-  const RowPtr rg = row_ptr<ST>(w, e, nn), ru = row_ptr<ST>(w, e, I + nn);
+  const bool ev = (unsigned)e < (unsigned)w.E;
+  const int nn = rv ? n : 0, ee = ev ? e : 0;
+  const RowPtr rg = row_ptr<ST>(w, ee, nn), ru = row_ptr<ST>(w, ee, I + nn);
 
   float ag[MT], au[MT];
 #pragma unroll
@@ -101,12 +126,8 @@ __global__ __launch_bounds__(WG) void k_moe_gate_up(
       cu[i] = load_chunk<ST>(ru, c, w.gshift);
     }
     if (r0 == 0) {
-      if constexpr (DIRECT) {
-        stage_rows<XT>([&](int) { return x; }, 1, H, xs, xsum);
-      } else {
-        stage_rows<XT>([&](int t) { return x + (int64_t)(perm[pos0 + min(t, cnt - 1)] / topk) * H; },
-                       MT, H, xs, xsum);
-      }
+      st.commit(0, xs, sums);
+      st.rest(row_of, xs, sums);
       __syncthreads();
     }
 #pragma unroll
@@ -118,9 +139,9 @@ __global__ __launch_bounds__(WG) void k_moe_gate_up(
           if (t < cnt) {
             const u32x4* xt = xs + (size_t)t * 4 * C;
             const u32x4 x0 = xt[c], x1 = xt[C + c], x2 = xt[2 * C + c], x3 = xt[3 * C + c];
-            const float S = xsum[t * C + c];
-            ag[t] += chunk_dot<XT, ST>(cg[i], x0, x1, x2, x3, S, c, w.gshift);
-            au[t] += chunk_dot<XT, ST>(cu[i], x0, x1, x2, x3, S, c, w.gshift);
+            const float2 sm = sums[t * C + c];
+            ag[t] += chunk_dot<XT, ST>(cg[i], x0, x1, x2, x3, sm, c, w.gshift);
+            au[t] += chunk_dot<XT, ST>(cu[i], x0, x1, x2, x3, sm, c, w.gshift);
           }
         }
       }
@@ -131,7 +152,8 @@ __global__ __launch_bounds__(WG) void k_moe_gate_up(
     const float g = group_sum<L>(ag[t]);
     const float u = group_sum<L>(au[t]);
     if (rv && cl == 0 && t < cnt)
-      act[(int64_t)(pos0 + t) * I + n] = Half<XT>::from_f32(silu(g) * u);
+      act[(int64_t)(pos0 + t) * I + n] =
+          Half<XT>::from_f32(ev ? silu(g) * u : __builtin_nanf(""));
   }
 }
 
@@ -158,10 +180,14 @@ __global__ __launch_bounds__(WG) void k_moe_down_m1(
   const int I = w.K, H = w.N, C = I >> 5;
   const int cpl = (C + L - 1) / L;
   u32x4* xs = (u32x4*)lds;
-  float* xsum = (float*)(lds + (size_t)topk * I * 2);
-  float* red = xsum + topk * C;  // [topk][RW]
+  float2* sums = (float2*)(lds + (size_t)topk * I * 2);
+  float* red = (float*)(sums + topk * C);  // [topk][RW]
 
   static_assert(L * RW >= 64, "the expert group must be uniform across a wave");
+  // activations first (all selected rows, contiguous act[j][I])
+  Stager<XT> st(topk, I);
+  auto row_of = [&](int j) { return act + (int64_t)j * I; };
+  st.issue(row_of, 0);
   const int gi = threadIdx.x / L, cl = threadIdx.x % L;
   const int r = gi % RW;
   const int jg = __builtin_amdgcn_readfirstlane(gi / RW);  // wave-uniform: sel[] via s_load
@@ -189,8 +215,9 @@ __global__ __launch_bounds__(WG) void k_moe_down_m1(
 #pragma unroll
       for (int i = 0; i < CR; ++i)
         ch[jj][i] = load_chunk<ST>(rp[jj], min(cl + (r0 + i) * L, C - 1), w.gshift);
-    if (r0 == 0) {  // all selected activation rows, contiguous act[j][I]
-      stage_rows<XT>([&](int j) { return act + (int64_t)j * I; }, topk, I, xs, xsum);
+    if (r0 == 0) {
+      st.commit(0, xs, sums);
+      st.rest(row_of, xs, sums);
       __syncthreads();
     }
 #pragma unroll
@@ -203,7 +230,7 @@ __global__ __launch_bounds__(WG) void k_moe_down_m1(
           const int c = cl + (r0 + i) * L;
           if (c < C)
             row[jj] += chunk_dot<XT, ST>(ch[jj][i], xj[c], xj[C + c], xj[2 * C + c], xj[3 * C + c],
-                                         xsum[j * C + c], c, w.gshift);
+                                         sums[j * C + c], c, w.gshift);
         }
       }
     }
@@ -240,10 +267,13 @@ __global__ __launch_bounds__(WG) void k_moe_down_list(
   const int I = w.K, H = w.N, C = I >> 5;
   const int cpl = (C + L - 1) / L;
   u32x4* xs = (u32x4*)lds;
-  float* xsum = (float*)(lds + (size_t)MT * I * 2);
+  float2* sums = (float2*)(lds + (size_t)MT * I * 2);
   if ((int)blockIdx.y >= *n_entries) return;
   const int4 en = entries[blockIdx.y];
   const int e = en.x, pos0 = en.y, cnt = en.z;
+  Stager<XT> st(MT, I);
+  auto row_of = [&](int t) { return act + (int64_t)(pos0 + min(t, cnt - 1)) * I; };
+  st.issue(row_of, 0);
   const int rl = threadIdx.x / L, cl = threadIdx.x % L;
   const int n = blockIdx.x * RPW + rl;
   const bool rv = n < H;
@@ -261,8 +291,8 @@ __global__ __launch_bounds__(WG) void k_moe_down_list(
 #pragma unroll
     for (int i = 0; i < ROUND; ++i) ch[i] = load_chunk<ST>(rp, min(cl + (r0 + i) * L, C - 1), w.gshift);
     if (r0 == 0) {
-      stage_rows<XT>([&](int t) { return act + (int64_t)(pos0 + min(t, cnt - 1)) * I; }, MT, I, xs,
-                     xsum);
+      st.commit(0, xs, sums);
+      st.rest(row_of, xs, sums);
       __syncthreads();
     }
 #pragma unroll
@@ -274,7 +304,7 @@ __global__ __launch_bounds__(WG) void k_moe_down_list(
           if (t < cnt) {
             const u32x4* xt = xs + (size_t)t * 4 * C;
             acc[t] += chunk_dot<XT, ST>(ch[i], xt[c], xt[C + c], xt[2 * C + c], xt[3 * C + c],
-                                        xsum[t * C + c], c, w.gshift);
+                                        sums[t * C + c], c, w.gshift);
           }
         }
       }
@@ -389,6 +419,7 @@ struct MoeWs {
   int32_t* perm;
   int4* entries;
   int* n_entries;
+  unsigned* counters;  // router/top-k handoff, one per token tile; zero between calls
   size_t bytes;
 };
 
@@ -411,6 +442,7 @@ MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
   m.perm = (int32_t*)take(Tk * 4);
   m.entries = (int4*)take((E + Tk) * sizeof(int4));
   m.n_entries = (int*)take(4);
+  m.counters = (unsigned*)take(((size_t)(Tc + 3) / 4 + 1) * 4);
   m.bytes = o;
   return m;
 }
@@ -447,15 +479,29 @@ inline int gate_up_lanes(int C) {
   return L;
 }
 
-template <int XT, int ST, int MT, bool DIRECT>
-int launch_gate_up_t(int L, dim3 grid, size_t lds, hipStream_t s, const uint16_t* x, int topk,
-                     const int32_t* sel, const int4* ent, const int* nent, const int32_t* perm,
-                     const QW& w, int I, uint16_t* act) {
-#define I4_GU_CASE(L_)                                                                           \
-  if (L == L_) {                                                                                 \
-    hipLaunchKernelGGL((k_moe_gate_up<XT, ST, L_, MT, DIRECT>), grid, dim3(WG), lds, s, x, topk, \
-                       sel, ent, nent, perm, w, I, act);                                         \
-    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                              \
+// decode / grouped gate_up launch.  mode GU_SEL / GU_ROUTE (one token) or
+// GU_LIST (n_entries = upper bound on the grouped entries)
+struct GateUpArgs {
+  int mode, n_entries, topk, E_r, renorm;
+  const void* x;
+  int32_t* sel;
+  const void* logits;
+  float* wts;
+  const int4* ent;
+  const int* nent;
+  const int32_t* perm;
+  void* act;
+};
+
+template <int XT, int ST, int MT, int MODE>
+int launch_gate_up_t(int L, dim3 grid, size_t lds, hipStream_t s, const GateUpArgs& a,
+                     const QW& w, int I) {
+#define I4_GU_CASE(L_)                                                                          \
+  if (L == L_) {                                                                                \
+    hipLaunchKernelGGL((k_moe_gate_up<XT, ST, L_, MT, MODE>), grid, dim3(WG), lds, s,           \
+                       (const uint16_t*)a.x, a.topk, a.sel, (const uint16_t*)a.logits, a.E_r,   \
+                       a.renorm, a.wts, a.ent, a.nent, a.perm, w, I, (uint16_t*)a.act);         \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
   }
   I4_GU_CASE(8) I4_GU_CASE(16) I4_GU_CASE(32) I4_GU_CASE(64)
 #undef I4_GU_CASE
@@ -463,22 +509,17 @@ int launch_gate_up_t(int L, dim3 grid, size_t lds, hipStream_t s, const uint16_t
 }
 
 template <int XT, int ST>
-int launch_gate_up_dt(bool direct, int n_entries, const void* x, int topk, const int32_t* sel,
-                      const int4* ent, const int* nent, const int32_t* perm, const QW& w, int I,
-                      void* act, hipStream_t s) {
+int launch_gate_up_dt(const GateUpArgs& a, const QW& w, int I, hipStream_t s) {
   const int H = w.K, C = H / 32;
   const int L = gate_up_lanes(C);
   const int rpw = WG / L;
-  dim3 grid((I + rpw - 1) / rpw, n_entries);
-  const size_t lds = (size_t)(direct ? 1 : MT_LIST) * (H * 2 + C * 4);
+  dim3 grid((I + rpw - 1) / rpw, a.n_entries);
+  const int MT = a.mode == GU_LIST ? MT_LIST : 1;
+  const size_t lds = (size_t)MT * (H * 2 + C * 8);
   if (lds > kMaxLds) return I4_ERR_SHAPE;
-  if (direct)
-    return launch_gate_up_t<XT, ST, 1, true>(L, grid, (size_t)H * 2 + C * 4, s,
-                                             (const uint16_t*)x, topk, sel, ent, nent, perm, w,
-                                             I, (uint16_t*)act);
-  return launch_gate_up_t<XT, ST, MT_LIST, false>(L, grid, (size_t)MT_LIST * (H * 2 + C * 4), s,
-                                                  (const uint16_t*)x, topk, sel, ent, nent, perm,
-                                                  w, I, (uint16_t*)act);
+  if (a.mode == GU_SEL) return launch_gate_up_t<XT, ST, 1, GU_SEL>(L, grid, lds, s, a, w, I);
+  if (a.mode == GU_ROUTE) return launch_gate_up_t<XT, ST, 1, GU_ROUTE>(L, grid, lds, s, a, w, I);
+  return launch_gate_up_t<XT, ST, MT_LIST, GU_LIST>(L, grid, lds, s, a, w, I);
 }
 
 template <int XT, int ST>
@@ -486,7 +527,7 @@ int launch_down_m1_t(const void* act, int topk, const int32_t* sel, const float*
                      const QW& w, const void* res, void* out, hipStream_t s) {
   const int I = w.K, C = I / 32;
   const int L = lanes_per_row(C);
-  const size_t lds_base = (size_t)topk * (I * 2 + C * 4);
+  const size_t lds_base = (size_t)topk * (I * 2 + C * 8);
 #define I4_DN_CASE(L_, J_)                                                                     \
   if (L == L_ && (topk + DownShape<L_>::GPR - 1) / DownShape<L_>::GPR <= J_) {                 \
     constexpr int RW = DownShape<L_>::RW;                                                      \
@@ -508,7 +549,7 @@ int launch_down_list_t(int max_entries, const void* act, const int4* ent, const 
                        const int32_t* perm, const QW& w, float* ys, hipStream_t s) {
   const int I = w.K, C = I / 32;
   const int L = lanes_per_row(C);
-  const size_t lds = (size_t)MT_LIST * (I * 2 + C * 4);
+  const size_t lds = (size_t)MT_LIST * (I * 2 + C * 8);
   if (lds > kMaxLds) return I4_ERR_SHAPE;
   const int rpw = WG / L;
   dim3 grid((w.N + rpw - 1) / rpw, max_entries);
@@ -525,8 +566,7 @@ int launch_down_list_t(int max_entries, const void* act, const int4* ent, const 
 
 // the three MoE projections dispatched on (activation dtype, scale dtype)
 struct MoeOps {
-  int (*gate_up)(bool, int, const void*, int, const int32_t*, const int4*, const int*,
-                 const int32_t*, const QW&, int, void*, hipStream_t);
+  int (*gate_up)(const GateUpArgs&, const QW&, int, hipStream_t);
   int (*down_m1)(const void*, int, const int32_t*, const float*, const QW&, const void*, void*,
                  hipStream_t);
   int (*down_list)(int, const void*, const int4*, const int*, const int32_t*, const QW&, float*,
@@ -574,23 +614,33 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   MoeOps ops;
   if (!pick_ops(xt, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
   int rc;
-  const void* lg = logits;
-  if (mw->router_w) {
-    rc = i4_launch_router_logits(x, xt, T, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
-                                 mw->norm_w ? ws.xn : nullptr, ws.logits, s);
-    if (rc) return rc;
-    lg = ws.logits;
-    if (mw->norm_w) x = ws.xn;  // the experts run on RMSNorm(x); residual is untouched
-  }
   int32_t* sel = sel_out ? sel_out : ws.sel;
   float* wts = w_out ? w_out : ws.w;
-  rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
-  if (rc) return rc;
   const QW qgu = to_qw(gu), qdn = to_qw(dn);
-  if (T == 1) {
-    rc = ops.gate_up(true, topk, x, topk, sel, nullptr, nullptr, nullptr, qgu, I, ws.act, s);
+  if (T == 1) {  // decode: router -> gate_up (ranks the logits itself) -> down + combine
+    const void* lg = logits;
+    if (mw->router_w) {
+      rc = i4_launch_router_logits(x, xt, 1, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
+                                   mw->norm_w ? ws.xn : nullptr, ws.logits, s);
+      if (rc) return rc;
+      lg = ws.logits;
+      if (mw->norm_w) x = ws.xn;  // the experts run on RMSNorm(x); residual is untouched
+    }
+    const GateUpArgs a{GU_ROUTE, topk, topk, E, renorm, x, sel, lg, wts,
+                       nullptr, nullptr, nullptr, ws.act};
+    rc = ops.gate_up(a, qgu, I, s);
     if (rc) return rc;
     return ops.down_m1(ws.act, topk, sel, wts, qdn, residual, out, s);
+  }
+  if (mw->router_w) {
+    rc = i4_launch_router_topk(x, xt, T, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
+                               mw->norm_w ? ws.xn : nullptr, ws.logits, topk, renorm, sel, wts,
+                               ws.counters, s);
+    if (rc) return rc;
+    if (mw->norm_w) x = ws.xn;
+  } else {
+    rc = i4_launch_topk(logits, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
+    if (rc) return rc;
   }
   const int Tk = T * topk;
   const int TW = (T + 31) / 32;
@@ -599,8 +649,9 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
                      ws.entries, ws.n_entries);
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
   const int max_entries = (E < Tk ? E : Tk) + Tk / MT_LIST;
-  rc = ops.gate_up(false, max_entries, x, topk, sel, ws.entries, ws.n_entries, ws.perm, qgu, I,
-                   ws.act, s);
+  const GateUpArgs a{GU_LIST, max_entries, topk, E, renorm, x, sel, nullptr, wts,
+                     ws.entries, ws.n_entries, ws.perm, ws.act};
+  rc = ops.gate_up(a, qgu, I, s);
   if (rc) return rc;
   rc = ops.down_list(max_entries, ws.act, ws.entries, ws.n_entries, ws.perm, qdn, ws.ys, s);
   if (rc) return rc;
@@ -669,8 +720,29 @@ int i4_moe_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up, const 
   if (((uintptr_t)x & 15) || ((uintptr_t)act & 15)) return I4_ERR_ALIGN;
   MoeOps ops;
   if (!pick_ops(x_dtype, gu.scale_dtype, gu.scale_dtype, &ops)) return I4_ERR_DTYPE;
-  return ops.gate_up(true, topk, x, topk, sel, nullptr, nullptr, nullptr, to_qw(gu), gu.N / 2,
-                     act, stream);
+  const GateUpArgs a{GU_SEL, topk, topk, 0, 0, x, const_cast<int32_t*>(sel), nullptr, nullptr,
+                     nullptr, nullptr, nullptr, act};
+  return ops.gate_up(a, to_qw(gu), gu.N / 2, stream);
+}
+
+int i4_moe_route_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up,
+                         const void* logits, int E_r, int topk, int renorm, int32_t* sel_out,
+                         float* w_out, void* act, hipStream_t stream) {
+  i4_qweight gu;
+  int rc = i4_check_weight(gate_up, &gu);
+  if (rc) return rc;
+  if (gu.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (!x || !logits || !sel_out || !w_out || !act) return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  if (E_r < 1 || E_r > 512 || E_r > gu.E || topk < 1 || topk > E_r || topk > 64 || gu.N % 2 ||
+      gu.K > 4096)
+    return I4_ERR_SHAPE;
+  if (((uintptr_t)x & 15) || ((uintptr_t)act & 15)) return I4_ERR_ALIGN;
+  MoeOps ops;
+  if (!pick_ops(x_dtype, gu.scale_dtype, gu.scale_dtype, &ops)) return I4_ERR_DTYPE;
+  const GateUpArgs a{GU_ROUTE, topk, topk, E_r, renorm, x, sel_out, logits, w_out,
+                     nullptr, nullptr, nullptr, act};
+  return ops.gate_up(a, to_qw(gu), gu.N / 2, stream);
 }
 
 int i4_moe_down_combine(const void* act, int x_dtype, const i4_qweight* down, const int32_t* sel,

@@ -9,6 +9,7 @@
 // (torch.topk leaves that order unspecified).
 #include "i4_common.h"
 #include "i4_launch.h"
+#include "i4_topk.h"
 
 namespace i4 {
 
@@ -36,140 +37,125 @@ template <int XT> __device__ inline float sumsq8(u32x4 d) {
 }
 
 // logits[t][e] = round(sum_h xn[t][h] * wr[e][h]); one wave per expert row,
-// TT tokens per workgroup column.  Lane l covers h = 8l + 512i.  With NORM
-// every wave computes r = 1 / sqrt(mean(x^2) + eps) for its tokens in the
-// same order (so all waves agree bit for bit), and wave 0 of column 0
+// TT tokens per workgroup column.  Lane l covers h = 8l + 512i (H <= 2048 *
+// RL).  The router-row loads are issued before the norm reduction.  With
+// NORM every wave computes r = 1 / sqrt(mean(x^2) + eps) for its tokens in
+// the same order (so all waves agree bit for bit), and wave 0 of column 0
 // writes xn for the expert kernels.
+template <int XT, int TT, bool NORM>
+__device__ inline void router_rows(const uint16_t* __restrict__ x, int T, int H,
+                                   const uint16_t* __restrict__ wr, int E,
+                                   const uint16_t* __restrict__ nw, float eps,
+                                   uint16_t* __restrict__ xn_out, uint16_t* __restrict__ logits) {
+  constexpr int RL = 8;  // 512-element rounds held in registers (H <= 4096)
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + wave;
+  const int t0 = blockIdx.y * TT;
+  if (e >= E) return;
+  const int rounds = (H + 511) / 512;
+  const uint16_t* wrow = wr + (int64_t)e * H;
+  u32x4 wv[RL];
+#pragma unroll
+  for (int i = 0; i < RL; ++i) {
+    const int h = min(8 * lane + 512 * i, H - 8);
+    wv[i] = i < rounds ? ldg16(wrow + h) : u32x4{0u, 0u, 0u, 0u};
+  }
+  const bool write_xn = NORM && xn_out != nullptr && blockIdx.x == 0 && wave == 0;
+  u32x4 gv[RL];
+  if constexpr (NORM) {  // norm weights with the router rows, ahead of any dependency
+#pragma unroll
+    for (int i = 0; i < RL; ++i) {
+      const int h = min(8 * lane + 512 * i, H - 8);
+      gv[i] = i < rounds ? ldg16(nw + h) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    if (t0 + t >= T) break;
+    const uint16_t* xr = x + (int64_t)(t0 + t) * H;
+    u32x4 xv[RL];
+#pragma unroll
+    for (int i = 0; i < RL; ++i) {
+      const int h = min(8 * lane + 512 * i, H - 8);
+      xv[i] = i < rounds ? ldg16(xr + h) : u32x4{0u, 0u, 0u, 0u};
+    }
+    if constexpr (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < RL; ++i)
+        if (i < rounds && 8 * lane + 512 * i < H) ss += sumsq8<XT>(xv[i]);
+      ss = group_sum<64>(ss);
+      const float r = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+      for (int i = 0; i < RL; ++i) {
+        const int h = 8 * lane + 512 * i;
+        if (i < rounds && h < H) {
+          xv[i].x = norm_pair<XT>(xv[i].x, gv[i].x, r);
+          xv[i].y = norm_pair<XT>(xv[i].y, gv[i].y, r);
+          xv[i].z = norm_pair<XT>(xv[i].z, gv[i].z, r);
+          xv[i].w = norm_pair<XT>(xv[i].w, gv[i].w, r);
+          if (write_xn) *(u32x4*)(xn_out + (int64_t)(t0 + t) * H + h) = xv[i];
+        }
+      }
+    }
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < RL; ++i) {
+      if (i < rounds && 8 * lane + 512 * i < H) {
+        a = Half<XT>::dot2(wv[i].x, xv[i].x, a);
+        a = Half<XT>::dot2(wv[i].y, xv[i].y, a);
+        a = Half<XT>::dot2(wv[i].z, xv[i].z, a);
+        a = Half<XT>::dot2(wv[i].w, xv[i].w, a);
+      }
+    }
+    a = group_sum<64>(a);
+    if (lane == 0) logits[(int64_t)(t0 + t) * E + e] = Half<XT>::from_f32(a);
+  }
+}
+
 template <int XT, int TT, bool NORM>
 __global__ __launch_bounds__(256) void k_router_logits(
     const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ wr, int E,
     const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
     uint16_t* __restrict__ logits) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int e = blockIdx.x * 4 + wave;
-  const int t0 = blockIdx.y * TT;
-  if (e >= E) return;
-  float r[TT];
-#pragma unroll
-  for (int t = 0; t < TT; ++t) r[t] = 1.f;
-  if constexpr (NORM) {
-#pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      float ss = 0.f;
-      if (t0 + t < T)
-        for (int h = 8 * lane; h < H; h += 512) ss += sumsq8<XT>(ldg16(x + (int64_t)(t0 + t) * H + h));
-      ss = group_sum<64>(ss);
-      r[t] = 1.0f / sqrtf(ss / (float)H + eps);
-    }
-  }
-  const bool write_xn = NORM && xn_out != nullptr && blockIdx.x == 0 && wave == 0;
-  float acc[TT];
-#pragma unroll
-  for (int t = 0; t < TT; ++t) acc[t] = 0.f;
-  const uint16_t* wrow = wr + (int64_t)e * H;
-  for (int h = 8 * lane; h < H; h += 512) {
-    const u32x4 wv = ldg16(wrow + h);
-    u32x4 gv = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (NORM) gv = ldg16(nw + h);
-#pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      if (t0 + t < T) {
-        u32x4 xv = ldg16(x + (int64_t)(t0 + t) * H + h);
-        if constexpr (NORM) {
-          xv.x = norm_pair<XT>(xv.x, gv.x, r[t]);
-          xv.y = norm_pair<XT>(xv.y, gv.y, r[t]);
-          xv.z = norm_pair<XT>(xv.z, gv.z, r[t]);
-          xv.w = norm_pair<XT>(xv.w, gv.w, r[t]);
-          if (write_xn) *(u32x4*)(xn_out + (int64_t)(t0 + t) * H + h) = xv;
-        }
-        float a = acc[t];
-        a = Half<XT>::dot2(wv.x, xv.x, a);
-        a = Half<XT>::dot2(wv.y, xv.y, a);
-        a = Half<XT>::dot2(wv.z, xv.z, a);
-        a = Half<XT>::dot2(wv.w, xv.w, a);
-        acc[t] = a;
-      }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    const float s = group_sum<64>(acc[t]);
-    if (lane == 0 && t0 + t < T) logits[(int64_t)(t0 + t) * E + e] = Half<XT>::from_f32(s);
-  }
+  router_rows<XT, TT, NORM>(x, T, H, wr, E, nw, eps, xn_out, logits);
 }
 
-struct Cand {
-  float v;
-  int i;
-};
-__device__ inline bool better(Cand a, Cand b) { return a.v > b.v || (a.v == b.v && a.i < b.i); }
-
-template <int LT> __device__ inline float load_logit(const void* p, int64_t i) {
-  if constexpr (LT == I4_F32) return ((const float*)p)[i];
-  else return Half<LT>::to_f32(((const uint16_t*)p)[i]);
-}
-
-// one wave per token, E <= 64 * VPL
+// one wave per token
 template <int LT, int VPL>
 __global__ __launch_bounds__(256) void k_topk(const void* __restrict__ logits, int T, int E,
                                               int topk, int renorm, int32_t* __restrict__ sel,
                                               float* __restrict__ wf, void* __restrict__ wh,
                                               int wht) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float v[VPL];
-  unsigned taken = 0;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = e < E ? load_logit<LT>(logits, (int64_t)t * E + e) : -__builtin_inff();
-    if (e >= E) taken |= 1u << i;  // padding never competes
+  wave_topk_row<LT, VPL>(logits, t, E, topk, renorm, sel, wf, wh, wht);
+}
+
+// Router logits + top-k in one launch.  Every workgroup of token tile y
+// computes 4 expert rows of logits; the last one to finish (device-scope
+// counter per tile) ranks the tile's tokens and resets the counter, so the
+// counters are zero again after every launch.
+template <int XT, int TT, bool NORM>
+__global__ __launch_bounds__(256) void k_router_topk(
+    const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ wr, int E,
+    const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
+    uint16_t* __restrict__ logits, int topk, int renorm, int32_t* __restrict__ sel,
+    float* __restrict__ wf, unsigned* __restrict__ counters) {
+  router_rows<XT, TT, NORM>(x, T, H, wr, E, nw, eps, xn_out, logits);
+  __threadfence();
+  __syncthreads();
+  __shared__ bool last;
+  if (threadIdx.x == 0) last = atomicAdd(&counters[blockIdx.y], 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  const int wave = threadIdx.x >> 6, t = blockIdx.y * TT + wave;
+  if (wave < TT && t < T) {
+    if (E <= 128) wave_topk_row<XT, 2>(logits, t, E, topk, renorm, sel, wf, nullptr, 0);
+    else wave_topk_row<XT, 8>(logits, t, E, topk, renorm, sel, wf, nullptr, 0);
   }
-  int my_sel = 0;
-  float my_val = 0.f, top_val = 0.f;
-  for (int r = 0; r < topk; ++r) {
-    Cand b{-__builtin_inff(), 0x7fffffff};
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const Cand c{v[i], lane + 64 * i};
-      if (!((taken >> i) & 1u) && (b.i == 0x7fffffff || better(c, b))) b = c;
-    }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-      Cand o;
-      o.v = __shfl_xor(b.v, m, 64);
-      o.i = __shfl_xor(b.i, m, 64);
-      if (o.i != 0x7fffffff && (b.i == 0x7fffffff || better(o, b))) b = o;
-    }
-    if ((b.i & 63) == lane) taken |= 1u << (b.i >> 6);
-    if (r == 0) top_val = b.v;
-    if (lane == r) {
-      my_sel = b.i;
-      my_val = b.v;
-    }
-  }
-  // softmax denominator over all E logits, max = top-1 logit
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i)
-    if (lane + 64 * i < E) s += expf(v[i] - top_val);
-  s = group_sum<64>(s);
-  float p = lane < topk ? expf(my_val - top_val) / s : 0.f;
-  if (renorm) {
-    const float ps = group_sum<64>(p);
-    p = p / ps;
-  }
-  if (lane < topk) {
-    const int64_t o = (int64_t)t * topk + lane;
-    sel[o] = my_sel;
-    if (wf) wf[o] = p;
-    if (wh) {
-      if (wht == I4_F16) ((uint16_t*)wh)[o] = Half<I4_F16>::from_f32(p);
-      else if (wht == I4_BF16) ((uint16_t*)wh)[o] = Half<I4_BF16>::from_f32(p);
-      else ((float*)wh)[o] = p;
-    }
-  }
+  if (threadIdx.x == 0) counters[blockIdx.y] = 0u;
 }
 
 }  // namespace i4
@@ -203,6 +189,26 @@ int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr,
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
+int i4_launch_router_topk(const void* x, int xt, int T, int H, const void* wr, int E,
+                          const void* norm_w, float eps, void* xn, void* logits, int topk,
+                          int renorm, int32_t* sel, float* wf, unsigned* counters,
+                          hipStream_t s) {
+  const int TT = T == 1 ? 1 : 4;
+  dim3 grid((E + 3) / 4, (T + TT - 1) / TT);
+#define I4_RT_CASE(XT_, TT_, N_)                                                                \
+  if (xt == XT_ && TT == TT_ && (norm_w != nullptr) == N_) {                                    \
+    hipLaunchKernelGGL((k_router_topk<XT_, TT_, N_>), grid, dim3(256), 0, s, (const uint16_t*)x, \
+                       T, H, (const uint16_t*)wr, E, (const uint16_t*)norm_w, eps,             \
+                       (uint16_t*)xn, (uint16_t*)logits, topk, renorm, sel, wf, counters);     \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
+  }
+  I4_RT_CASE(I4_F16, 1, true) I4_RT_CASE(I4_F16, 1, false) I4_RT_CASE(I4_F16, 4, true)
+  I4_RT_CASE(I4_F16, 4, false) I4_RT_CASE(I4_BF16, 1, true) I4_RT_CASE(I4_BF16, 1, false)
+  I4_RT_CASE(I4_BF16, 4, true) I4_RT_CASE(I4_BF16, 4, false)
+#undef I4_RT_CASE
+  return I4_ERR_DTYPE;
+}
+
 int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
                    float* wf, void* wh, int wht, hipStream_t s) {
   dim3 grid((T + 3) / 4);
@@ -228,7 +234,7 @@ int i4_router_logits(const void* x, int x_dtype, int T, int H, const void* route
   if (xn_out && !norm_w) return I4_ERR_NULL;
   if (((uintptr_t)norm_w & 15) || ((uintptr_t)xn_out & 15)) return I4_ERR_ALIGN;
   if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
-  if (T < 1 || T > 65535 * 4 || H < 8 || H % 8 != 0 || E < 1 || E > 65535 * 4)
+  if (T < 1 || T > 65535 * 4 || H < 8 || H % 8 != 0 || H > 4096 || E < 1 || E > 65535 * 4)
     return I4_ERR_SHAPE;
   if (((uintptr_t)x & 15) || ((uintptr_t)router_w & 15)) return I4_ERR_ALIGN;
   return i4_launch_router_logits(x, x_dtype, T, H, router_w, E, norm_w, norm_eps, xn_out, logits,

@@ -185,8 +185,9 @@ class Workspace:
         self.buf: torch.Tensor | None = None
 
     def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+        # zero-filled once: the library keeps its handoff counters zero between calls
         if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
-            self.buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+            self.buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
         return self.buf
 
 
@@ -239,6 +240,24 @@ def moe_gate_up(x: torch.Tensor, gate_up: QWeight, sel: torch.Tensor) -> torch.T
     _lib.check(_lib.lib().i4_moe_gate_up(xc.data_ptr(), xt, ctypes.byref(cw), s32.data_ptr(),
                                          s32.numel(), act.data_ptr(), _lib.stream(dev)))
     return act
+
+
+def moe_route_gate_up(x: torch.Tensor, gate_up: QWeight, logits: torch.Tensor, top_k: int,
+                      norm_topk_prob: bool = True):
+    """Decode routing + gate_up stage in one launch: (act [k, I], sel [k] int32, w [k] fp32)."""
+    dev = _lib.require_device(x, gate_up.packed, logits)
+    xt = _lib.half_code(x.dtype)
+    xc = x.reshape(-1).contiguous()
+    lg = logits.reshape(-1).to(x.dtype).contiguous()
+    act = torch.empty(top_k, gate_up.N // 2, dtype=x.dtype, device=dev)
+    sel = torch.empty(top_k, dtype=torch.int32, device=dev)
+    w = torch.empty(top_k, dtype=torch.float32, device=dev)
+    cw = gate_up.c()
+    _lib.check(_lib.lib().i4_moe_route_gate_up(xc.data_ptr(), xt, ctypes.byref(cw), lg.data_ptr(),
+                                               lg.numel(), top_k, int(norm_topk_prob),
+                                               sel.data_ptr(), w.data_ptr(), act.data_ptr(),
+                                               _lib.stream(dev)))
+    return act, sel, w
 
 
 def moe_down_combine(act: torch.Tensor, down: QWeight, sel: torch.Tensor, w: torch.Tensor,

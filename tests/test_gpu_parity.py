@@ -320,6 +320,30 @@ def test_moe_decode_m1(pkg, dev):
         assert err <= 1e-3
 
 
+def test_decode_stages_compose_to_the_block(pkg, dev):
+    """route+gate_up, gate_up(sel) and down+combine reproduce moe_forward at T=1 bit for bit,
+    and the stage outputs match the oracle."""
+    rng = np.random.default_rng(31)
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, E=64)
+    x = t_(make_x(rng, (1, 2048), "f16"), dev)
+    res = t_(make_x(rng, (1, 2048), "f16"), dev)
+    full, sel_f, w_f = pkg.moe_forward(x, moe.gate_up, moe.down, 8, router_w=moe.router_w,
+                                       residual=res, return_routing=True)
+    lg = pkg.router_logits(x, moe.router_w)
+    act, sel, w = pkg.moe_route_gate_up(x, moe.gate_up, lg, 8)
+    assert torch.equal(sel, sel_f.reshape(-1)) and torch.equal(w, w_f.reshape(-1))
+    act2 = pkg.moe_gate_up(x, moe.gate_up, sel)
+    assert torch.equal(act, act2)
+    out = pkg.moe_down_combine(act, moe.down, sel, w, residual=res)
+    assert torch.equal(out.reshape(1, -1), full)
+    # stage values against the oracle
+    xs = host(x)[0]
+    for j, e in enumerate(sel.cpu().numpy()):
+        gu = dgu(int(e)) @ xs
+        ref_act = i4ref.round_half(i4ref.silu(gu[:768]) * gu[768:], "f16")
+        assert i4ref.rel_err(host(act[j]).astype(np.float64), ref_act) <= 1e-3
+
+
 def test_moe_decode_reference_format(pkg, dev):
     """The reference checkpoint's own format: CT g32 symmetric, bf16 scales and activations."""
     rng = np.random.default_rng(22)
