@@ -185,6 +185,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time without a hipGraph")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 10 device copies of 64 MiB (calibrates the FETCH_SIZE / "
+                         "WRITE_SIZE counters against a copy of known size) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU decode path only: run it with --gpus 1 "
@@ -193,6 +196,16 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": 64 << 20,
+                          "bytes_written": 64 << 20, "dispatches": 10}))
+        return 0
 
     from __graft_entry__ import load_package
 
