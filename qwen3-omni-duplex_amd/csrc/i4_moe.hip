@@ -339,21 +339,205 @@ __global__ __launch_bounds__(WG) void k_moe_combine(const float* __restrict__ ys
 }
 
 // ---------------------------------------------------------------------------
+// MFMA tile path for experts that received many tokens (T > 1).
+//
+// One workgroup = 64 tokens of one expert (4 m-blocks of 16) x a column tile;
+// wave w owns NB n-blocks of 16 weight rows.  v_mfma_f32_16x16x32_{f16,bf16}:
+// lane l supplies A[m = l%16][8 k] and B[8 k][n = l%16] for its k-group
+// kb = l/16 and receives D[4 kb + i][l%16], i < 4.  K is walked in 128-column
+// superchunks (one quantisation group, G = 128): lane group kb loads chunk
+// 4s + kb of its weight row with one 16-byte load, and MFMA step t uses word t
+// of that chunk -- a permutation of k that A (the staged activations, read in
+// the same order) follows, so the contraction is unchanged.  B holds the exact
+// half values M + q; after the group's 4 steps the accumulator D is corrected
+// per output with the group's scale s, zero z and activation sum S_m:
+//     res += s * D - s (M + z) S_m,
+// so every product is exact and accumulation is fp32, as in the GEMV path.
+// Activation tiles are double buffered in LDS (token stride 272 B keeps the 16
+// tokens of an MFMA on distinct banks); the next superchunk's weights and
+// activations are loaded while the current one is multiplied.
+//   GATEUP: NB = 2 (16 gate rows, the same 16 up rows), SiLU in the epilogue,
+//           act[pos] in the activation dtype.  Column tile 64 row pairs.
+//   DOWN:   NB = 2 (32 output rows), ys[slot] in fp32.  Column tile 128 rows.
+static constexpr int MF_TOK = 64;   // tokens per MFMA entry
+static constexpr int MF_MIN = 16;   // experts with at least this many tokens use MFMA
+static constexpr int MF_TSTRIDE = 17;  // uint4 per staged token row (16 + 1 pad)
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <int XT> __device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (XT == I4_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// 8 exact halves M + q of one CT word, in the staged pair order
+template <int XT> __device__ inline u32x4 decode8(u32 w) {
+  constexpr u32 MK = 0x000F000Fu, MG = Half<XT>::MAGIC2;
+  return u32x4{(w & MK) | MG, ((w >> 4) & MK) | MG, ((w >> 8) & MK) | MG, ((w >> 12) & MK) | MG};
+}
+
+template <int XT, int ST, bool GATEUP>
+__global__ __launch_bounds__(WG) void k_moe_mfma(
+    const uint16_t* __restrict__ src, int topk, const int4* __restrict__ entries,
+    const int* __restrict__ n_entries, const int32_t* __restrict__ perm, QW w, int I,
+    uint16_t* __restrict__ act, float* __restrict__ ys) {
+  constexpr int NB = 2;
+  constexpr int COLS = GATEUP ? 64 : 128;  // weight rows (pairs for GATEUP) per workgroup
+  __shared__ u32x4 xs[2][MF_TOK * MF_TSTRIDE];
+  __shared__ float xsum[2][MF_TOK];
+  if ((int)blockIdx.y >= *n_entries) return;
+  const int4 en = entries[blockIdx.y];
+  const int e = en.x, pos0 = en.y, cnt = en.z;
+  const int K = w.K, SC = K >> 7;  // superchunks
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ln = lane & 15, kb = lane >> 4;
+  const bool ev = (unsigned)e < (unsigned)w.E;
+  const int ee = ev ? e : 0;
+
+  // weight rows of this lane (column ln of each n-block)
+  RowPtr rp[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    int row;
+    if constexpr (GATEUP) row = blockIdx.x * COLS + 16 * wave + ln + (nb ? I : 0);
+    else row = blockIdx.x * COLS + 32 * wave + 16 * nb + ln;
+    rp[nb] = row_ptr<ST>(w, ee, row);
+  }
+  // staging role: token tk, chunk kc of the superchunk
+  const int tk = threadIdx.x >> 2, kc = threadIdx.x & 3;
+  const bool tv = tk < cnt;
+  const uint16_t* xrow;
+  if constexpr (GATEUP) xrow = src + (int64_t)(perm[pos0 + min(tk, cnt - 1)] / topk) * K;
+  else xrow = src + (int64_t)(pos0 + min(tk, cnt - 1)) * K;
+
+  u32x4 xd[4];
+  auto issue_x = [&](int sc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xd[j] = ldg16(xrow + 128 * sc + 32 * kc + 8 * j);
+  };
+  auto commit_x = [&](int sc, int buf) {
+    float sm = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 d = tv ? xd[j] : u32x4{0u, 0u, 0u, 0u};
+      xs[buf][tk * MF_TSTRIDE + kc * 4 + j] = pair_order(d);
+      sm += sum8<XT>(d).y;
+    }
+    sm = group_sum<4>(sm);
+    if (kc == 0) xsum[buf][tk] = sm;
+    (void)sc;
+  };
+  Chunk cur[NB], nxt[NB];  // weights of this superchunk / the next one
+  auto issue_w = [&](int sc, Chunk* dst) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) dst[nb] = load_chunk<ST>(rp[nb], 4 * sc + kb, w.gshift);
+  };
+
+  f32x4 res[4][NB];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) res[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nmb = (cnt + 15) >> 4;
+
+  issue_w(0, cur);
+  issue_x(0);
+  for (int sc = 0; sc < SC; ++sc) {
+    const int buf = sc & 1;
+    commit_x(sc, buf);
+    __syncthreads();
+    if (sc + 1 < SC) {
+      issue_w(sc + 1, nxt);
+      issue_x(sc + 1);
+    }
+    f32x4 d[4][NB];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) d[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      u32x4 b[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const u32x4 cw = cur[nb].w;
+        b[nb] = decode8<XT>(t == 0 ? cw.x : t == 1 ? cw.y : t == 2 ? cw.z : cw.w);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        if (mb < nmb) {
+          const u32x4 a = xs[buf][(16 * mb + ln) * MF_TSTRIDE + kb * 4 + t];
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) d[mb][nb] = mfma16<XT>(a, b[nb], d[mb][nb]);
+        }
+      }
+    }
+    // per-group correction: res += s D - s (M + z) S_m
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const Chunk& c = cur[nb];
+      const int g = (4 * sc + kb) >> w.gshift;
+      const float sv = scale_from_raw<ST>(c.s);
+      const float z = (float)((c.z >> (4 * (g & 7))) & 15u);
+      const float bv = -sv * (Half<XT>::MAGIC + z);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        if (mb < nmb) {
+          const float* sp = &xsum[buf][16 * mb + 4 * kb];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) res[mb][nb][i] = fmaf(sv, d[mb][nb][i], fmaf(bv, sp[i], res[mb][nb][i]));
+        }
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) cur[nb] = nxt[nb];
+  }
+  // epilogue: lane holds rows m = 16 mb + 4 kb + i of column ln
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * mb + 4 * kb + i;
+      if (m < cnt) {
+        if constexpr (GATEUP) {
+          const int n = blockIdx.x * COLS + 16 * wave + ln;
+          const float v = ev ? silu(res[mb][0][i]) * res[mb][1][i] : __builtin_nanf("");
+          act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
+        } else {
+          const int64_t o = (int64_t)perm[pos0 + m] * w.N + blockIdx.x * COLS + 32 * wave + ln;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) ys[o + 16 * nb] = ev ? res[mb][nb][i] : __builtin_nanf("");
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Sort (token, slot) pairs by expert, stable in token order, and cut them
 // into entries of <= mt tokens.  One workgroup of 1024 threads.
 //   bits[e][w]: bit b set <=> token 32w + b selected expert e
 //   pre [e][w]: popcount of bits[e][0..w)
 __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel, int T, int topk,
-                                                int E, int mt, int32_t* __restrict__ perm,
+                                                int E, int mt, int mf_min,
+                                                int32_t* __restrict__ perm,
                                                 int4* __restrict__ entries,
-                                                int* __restrict__ n_entries) {
+                                                int* __restrict__ n_entries,
+                                                int4* __restrict__ mf_entries,
+                                                int* __restrict__ n_mf_entries) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int TW = (T + 31) >> 5;
   u32* bits = (u32*)lds;
   u32* pre = bits + E * TW;
   int* cnt = (int*)(pre + E * TW);
   int* off = cnt + E;       // [E + 1]
-  int* eoff = off + E + 1;  // [E + 1]
+  int* eoff = off + E + 1;  // [E + 1] GEMV entries
+  int* moff = eoff + E + 1; // [E + 1] MFMA entries
   const int tid = threadIdx.x, nt = blockDim.x;
   for (int i = tid; i < E * TW; i += nt) bits[i] = 0u;
   __syncthreads();
@@ -372,16 +556,20 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
   }
   __syncthreads();
   if (tid == 0) {
-    int o = 0, eo = 0;
+    int o = 0, eo = 0, mo = 0;
     for (int e = 0; e < E; ++e) {
       off[e] = o;
       eoff[e] = eo;
+      moff[e] = mo;
       o += cnt[e];
-      eo += (cnt[e] + mt - 1) / mt;
+      if (cnt[e] >= mf_min) mo += (cnt[e] + MF_TOK - 1) / MF_TOK;
+      else eo += (cnt[e] + mt - 1) / mt;
     }
     off[E] = o;
     eoff[E] = eo;
+    moff[E] = mo;
     *n_entries = eo;
+    *n_mf_entries = mo;
   }
   __syncthreads();
   for (int s = tid; s < T * topk; s += nt) {
@@ -394,8 +582,13 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
   }
   for (int e = tid; e < E; e += nt) {
     const int c = cnt[e];
-    for (int q = 0; q * mt < c; ++q)
-      entries[eoff[e] + q] = int4{e, off[e] + q * mt, min(mt, c - q * mt), 0};
+    if (c >= mf_min) {
+      for (int q = 0; q * MF_TOK < c; ++q)
+        mf_entries[moff[e] + q] = int4{e, off[e] + q * MF_TOK, min(MF_TOK, c - q * MF_TOK), 0};
+    } else {
+      for (int q = 0; q * mt < c; ++q)
+        entries[eoff[e] + q] = int4{e, off[e] + q * mt, min(mt, c - q * mt), 0};
+    }
   }
 }
 
@@ -419,6 +612,8 @@ struct MoeWs {
   int32_t* perm;
   int4* entries;
   int* n_entries;
+  int4* mf_entries;
+  int* n_mf_entries;
   unsigned* counters;  // router/top-k handoff, one per token tile; zero between calls
   size_t bytes;
 };
@@ -442,6 +637,8 @@ MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
   m.perm = (int32_t*)take(Tk * 4);
   m.entries = (int4*)take((E + Tk) * sizeof(int4));
   m.n_entries = (int*)take(4);
+  m.mf_entries = (int4*)take((E + Tk / MF_MIN + 1) * sizeof(int4));
+  m.n_mf_entries = (int*)take(4);
   m.counters = (unsigned*)take(((size_t)(Tc + 3) / 4 + 1) * 4);
   m.bytes = o;
   return m;
@@ -571,11 +768,34 @@ struct MoeOps {
                  hipStream_t);
   int (*down_list)(int, const void*, const int4*, const int*, const int32_t*, const QW&, float*,
                    hipStream_t);
+  int (*mfma_gate_up)(int, const void*, int, const int4*, const int*, const int32_t*, const QW&,
+                      int, void*, hipStream_t);
+  int (*mfma_down)(int, const void*, const int4*, const int*, const int32_t*, const QW&, float*,
+                   hipStream_t);
 };
+
+template <int XT, int ST>
+int launch_mfma_gate_up_t(int max_entries, const void* x, int topk, const int4* ent,
+                          const int* nent, const int32_t* perm, const QW& w, int I, void* act,
+                          hipStream_t s) {
+  hipLaunchKernelGGL((k_moe_mfma<XT, ST, true>), dim3(I / 64, max_entries), dim3(WG), 0, s,
+                     (const uint16_t*)x, topk, ent, nent, perm, w, I, (uint16_t*)act,
+                     (float*)nullptr);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+template <int XT, int ST>
+int launch_mfma_down_t(int max_entries, const void* act, const int4* ent, const int* nent,
+                       const int32_t* perm, const QW& w, float* ys, hipStream_t s) {
+  hipLaunchKernelGGL((k_moe_mfma<XT, ST, false>), dim3(w.N / 128, max_entries), dim3(WG), 0, s,
+                     (const uint16_t*)act, 0, ent, nent, perm, w, 0, (uint16_t*)nullptr, ys);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
   return MoeOps{&launch_gate_up_dt<XT, ST>, &launch_down_m1_t<XT, ST>,
-                &launch_down_list_t<XT, ST>};
+                &launch_down_list_t<XT, ST>, &launch_mfma_gate_up_t<XT, ST>,
+                &launch_mfma_down_t<XT, ST>};
 }
 
 bool pick_ops(int xt, int gst, int dst, MoeOps* ops) {
@@ -644,17 +864,30 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   }
   const int Tk = T * topk;
   const int TW = (T + 31) / 32;
-  const size_t glds = (size_t)2 * E * TW * 4 + (size_t)(3 * E + 2) * 4;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E, MT_LIST, ws.perm,
-                     ws.entries, ws.n_entries);
+  // experts with >= MF_MIN tokens go to the MFMA tile kernels (G = 128 weights)
+  const bool mfma = gu.group == 128 && dn.group == 128 && I % 128 == 0 && H % 128 == 0;
+  const size_t glds = (size_t)2 * E * TW * 4 + (size_t)(4 * E + 3) * 4;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E, MT_LIST,
+                     mfma ? MF_MIN : 0x7fffffff, ws.perm, ws.entries, ws.n_entries, ws.mf_entries,
+                     ws.n_mf_entries);
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
   const int max_entries = (E < Tk ? E : Tk) + Tk / MT_LIST;
   const GateUpArgs a{GU_LIST, max_entries, topk, E, renorm, x, sel, nullptr, wts,
                      ws.entries, ws.n_entries, ws.perm, ws.act};
   rc = ops.gate_up(a, qgu, I, s);
   if (rc) return rc;
+  const int max_mf = (E < Tk / MF_MIN ? E : Tk / MF_MIN) + Tk / MF_TOK + 1;
+  if (mfma) {
+    rc = ops.mfma_gate_up(max_mf, x, topk, ws.mf_entries, ws.n_mf_entries, ws.perm, qgu, I, ws.act,
+                          s);
+    if (rc) return rc;
+  }
   rc = ops.down_list(max_entries, ws.act, ws.entries, ws.n_entries, ws.perm, qdn, ws.ys, s);
   if (rc) return rc;
+  if (mfma) {
+    rc = ops.mfma_down(max_mf, ws.act, ws.mf_entries, ws.n_mf_entries, ws.perm, qdn, ws.ys, s);
+    if (rc) return rc;
+  }
   const int64_t tot = (int64_t)T * H;
   dim3 cg((unsigned)((tot + WG - 1) / WG));
   if (xt == I4_F16)

@@ -377,6 +377,24 @@ def test_moe_m512_zipf_logits(pkg, dev):
     _check_moe(pkg, moe, dgu, ddn, x, "f16", dev, logits=lg)
 
 
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+def test_moe_mfma_tiles(pkg, dev, xdt):
+    """Few experts, many tokens each: every expert takes the MFMA tile path (>= 16 tokens),
+    including partial 64-token tiles and ragged m-blocks."""
+    rng = np.random.default_rng(32)
+    E, H, I, G, T = 12, 2048, 768, 128, 181
+    sdt = "bf16" if xdt == "bf16" else np.float16
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, E=E, sdt=sdt)
+    if xdt == "bf16":
+        moe.register_buffer("router_w", moe.router_w.to(torch.bfloat16), persistent=False)
+    x = make_x(rng, (T, H), xdt)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg = i4ref.f32_to_bf16_bits(lg) if xdt == "bf16" else lg.astype(np.float16)
+    counts = np.bincount(i4ref.route(f_(lg), 8)[0].ravel(), minlength=E)
+    assert counts.min() >= 16  # all MFMA
+    _check_moe(pkg, moe, dgu, ddn, x, xdt, dev, logits=lg, residual=x)
+
+
 def test_moe_tokens_are_independent(pkg, dev):
     rng = np.random.default_rng(25)
     moe, _, _, _ = _awq_moe(pkg, dev, rng, E=32)
