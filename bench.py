@@ -184,6 +184,8 @@ def main() -> int:
     ap.add_argument("--kernel-rounds", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the M=32 and M=512 workloads (reported as extra fields)")
     ap.add_argument("--eager", action="store_true", help="time without a hipGraph")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 device copies of 64 MiB (calibrates the FETCH_SIZE / "
@@ -285,6 +287,41 @@ def main() -> int:
     log(f"route+gate_up kernel: {k_us:.2f} us/launch back-to-back ({k_evt:.2f} with per-launch "
         f"events) -> {achieved:.0f} GB/s")
 
+    # ---- other workloads of the same layer: M=32 (router from weights) and M=512 prefill
+    # with Zipf(1.1)-skewed logits (MFMA tiles for hot experts), rotating over the layers
+    prefill = {}
+    if args.prefill:
+        gen2 = torch.Generator(device=dev)
+        gen2.manual_seed(7)
+        for T in (32, 512):
+            xT = [torch.randn(T, H, device=dev, generator=gen2).half() for _ in range(4)]
+            lgT = None
+            if T == 512:
+                rank = torch.randperm(E, device=dev, generator=gen2).float() + 1
+                lgT = [(-1.1 * 2.0 * torch.log(rank)[None, :]
+                        - torch.log(-torch.log(torch.rand(T, E, device=dev, generator=gen2))))
+                       .half() for _ in range(4)]
+            wsT = pkg.Workspace()
+
+            def run_T(i, T=T, xT=xT, lgT=lgT, wsT=wsT):
+                m = mods[i % len(mods)]
+                if lgT is None:
+                    ops.moe_forward(xT[i % 4], m.gate_up, m.down, TOPK, router_w=m.router_w,
+                                    residual=xT[i % 4], workspace=wsT)
+                else:
+                    ops.moe_forward(xT[i % 4], m.gate_up, m.down, TOPK, logits=lgT[i % 4],
+                                    residual=xT[i % 4], workspace=wsT)
+
+            reps = 48
+            ms_T, _ = time_stack(torch, run_T, reps, 8)
+            flops = T * TOPK * 3 * 2 * H * I
+            prefill[f"M{T}"] = {"us_per_layer": round(ms_T * 1e3, 2),
+                                "tokens_per_s": round(T / (ms_T * 1e-3), 1),
+                                "expert_TFLOPs": round(flops / (ms_T * 1e-3) / 1e12, 2),
+                                "routing": "router weights" if lgT is None else
+                                           "Zipf(1.1), tau 2 logits"}
+            log(f"M={T}: {ms_T * 1e3:.1f} us/layer, {flops / (ms_T * 1e-3) / 1e12:.1f} TFLOP/s")
+
     # ---- CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -327,6 +364,7 @@ def main() -> int:
             "us_per_launch_own_events": round(k_evt, 3),
         },
         "cpu_baseline": cpu,
+        "other_workloads": prefill,
     }
     print(json.dumps(res), flush=True)
     return 0
