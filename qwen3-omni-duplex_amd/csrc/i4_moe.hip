@@ -92,17 +92,22 @@ __global__ __launch_bounds__(WG) void k_moe_gate_up(
     cnt = en.z;
     st.issue(row_of, 0);
   } else if constexpr (MODE == GU_ROUTE) {
-    st.issue(row_of, 0);
-    int my_sel = 0;
-    float my_w = 0.f;
-    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64;
-    if (E_r <= 128)
-      wave_topk_row<XT, 2>(logits, 0, E_r, topk, renorm, writer ? sel : nullptr,
-                           writer ? wts : nullptr, nullptr, 0, &my_sel, &my_w);
-    else
-      wave_topk_row<XT, 8>(logits, 0, E_r, topk, renorm, writer ? sel : nullptr,
-                           writer ? wts : nullptr, nullptr, 0, &my_sel, &my_w);
-    e = __builtin_amdgcn_readlane(my_sel, blockIdx.y);
+    // the logits are the critical path: load them before the activations
+    auto route = [&](auto vpl) -> int {
+      constexpr int VPL = decltype(vpl)::value;
+      u32 raw[VPL];
+      load_row<XT, VPL>(logits, 0, E_r, raw);
+      st.issue(row_of, 0);
+      if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
+        int my_sel = 0;
+        float my_w = 0.f;
+        topk_row<XT, VPL>(raw, 0, E_r, topk, renorm, sel, wts, nullptr, 0, &my_sel, &my_w);
+        return __builtin_amdgcn_readlane(my_sel, 0);
+      }
+      return topk_slot<XT, VPL>(raw, E_r, blockIdx.y);
+    };
+    e = E_r <= 128 ? route(std::integral_constant<int, 2>{})
+                   : route(std::integral_constant<int, 8>{});
   } else {
     st.issue(row_of, 0);
     e = sel[blockIdx.y];
