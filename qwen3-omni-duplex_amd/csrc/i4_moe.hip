@@ -122,19 +122,16 @@ __global__ __launch_bounds__(WG) void k_moe_gate_up(
   float ag[MT], au[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) ag[t] = au[t] = 0.f;
-  for (int r0 = 0; r0 < cpl; r0 += ROUND) {
-    Chunk cg[ROUND], cu[ROUND];
+  Chunk cg[ROUND], cu[ROUND];
+  auto load_round = [&](int r0) {
 #pragma unroll
     for (int i = 0; i < ROUND; ++i) {
       const int c = min(cl + (r0 + i) * L, C - 1);
       cg[i] = load_chunk<ST>(rg, c, w.gshift);
       cu[i] = load_chunk<ST>(ru, c, w.gshift);
     }
-    if (r0 == 0) {
-      st.commit(0, xs, sums);
-      st.rest(row_of, xs, sums);
-      __syncthreads();
-    }
+  };
+  auto dot_round = [&](int r0) {
 #pragma unroll
     for (int i = 0; i < ROUND; ++i) {
       const int c = cl + (r0 + i) * L;
@@ -151,6 +148,17 @@ __global__ __launch_bounds__(WG) void k_moe_gate_up(
         }
       }
     }
+  };
+  // round 0 is peeled: a loop-header wait would hold its weight loads behind
+  // the activation loads
+  load_round(0);
+  st.commit(0, xs, sums);
+  st.rest(row_of, xs, sums);
+  __syncthreads();
+  dot_round(0);
+  for (int r0 = ROUND; r0 < cpl; r0 += ROUND) {
+    load_round(r0);
+    dot_round(r0);
   }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
@@ -189,7 +197,14 @@ __global__ __launch_bounds__(WG) void k_moe_down_m1(
   float* red = (float*)(sums + topk * C);  // [topk][RW]
 
   static_assert(L * RW >= 64, "the expert group must be uniform across a wave");
-  // activations first (all selected rows, contiguous act[j][I])
+  __shared__ float s_w[16];  // routing weights, loaded with the first wave of loads
+  // unconditional loads (clamped indices): a guarded load would be waited for
+  // where its branch joins, before anything else is issued
+  const float wv = wts[min((int)threadIdx.x, topk - 1)];
+  const int on = blockIdx.x * RW + (int)threadIdx.x;  // output row of the combine threads
+  const bool comb = (int)threadIdx.x < RW && on < H;
+  const uint16_t res_raw = *(residual ? residual + min(on, H - 1) : act);
+  // activations next (all selected rows, contiguous act[j][I])
   Stager<XT> st(topk, I);
   auto row_of = [&](int j) { return act + (int64_t)j * I; };
   st.issue(row_of, 0);
@@ -212,19 +227,16 @@ __global__ __launch_bounds__(WG) void k_moe_down_m1(
   float row[JMAX];
 #pragma unroll
   for (int jj = 0; jj < JMAX; ++jj) row[jj] = 0.f;
-
-  for (int r0 = 0; r0 < cpl; r0 += CR) {
-    Chunk ch[JMAX][CR];
+  Chunk ch[JMAX][CR];
+  auto load_round = [&](int r0) {
 #pragma unroll
     for (int jj = 0; jj < JMAX; ++jj)
 #pragma unroll
       for (int i = 0; i < CR; ++i)
-        ch[jj][i] = load_chunk<ST>(rp[jj], min(cl + (r0 + i) * L, C - 1), w.gshift);
-    if (r0 == 0) {
-      st.commit(0, xs, sums);
-      st.rest(row_of, xs, sums);
-      __syncthreads();
-    }
+        if (i == 0 || (r0 + i) * L < C)  // wave-uniform: skips rounds past the row's end
+          ch[jj][i] = load_chunk<ST>(rp[jj], min(cl + (r0 + i) * L, C - 1), w.gshift);
+  };
+  auto dot_round = [&](int r0) {
 #pragma unroll
     for (int jj = 0; jj < JMAX; ++jj) {
       const int j = jg + jj * GPR;
@@ -239,6 +251,18 @@ __global__ __launch_bounds__(WG) void k_moe_down_m1(
         }
       }
     }
+  };
+  // round 0 is peeled: a loop-header wait would hold its weight loads behind
+  // the activation loads
+  load_round(0);
+  st.commit(0, xs, sums);
+  st.rest(row_of, xs, sums);
+  if ((int)threadIdx.x < topk) s_w[threadIdx.x] = wv;
+  __syncthreads();
+  dot_round(0);
+  for (int r0 = CR; r0 < cpl; r0 += CR) {
+    load_round(r0);
+    dot_round(r0);
   }
 #pragma unroll
   for (int jj = 0; jj < JMAX; ++jj) {
@@ -248,14 +272,10 @@ __global__ __launch_bounds__(WG) void k_moe_down_m1(
       red[j * RW + r] = (unsigned)ej[jj] < (unsigned)w.E ? v : __builtin_nanf("");
   }
   __syncthreads();
-  if (threadIdx.x < RW) {
-    const int rr = threadIdx.x, on = blockIdx.x * RW + rr;
-    if (on < H) {
-      const float res = residual ? Half<XT>::to_f32(residual[on]) : 0.f;
-      float y = 0.f;
-      for (int j = 0; j < topk; ++j) y += wts[j] * red[j * RW + rr];
-      out[on] = Half<XT>::from_f32(res + y);
-    }
+  if (comb) {
+    float y = 0.f;
+    for (int j = 0; j < topk; ++j) y += s_w[j] * red[j * RW + (int)threadIdx.x];
+    out[on] = Half<XT>::from_f32((residual ? Half<XT>::to_f32(res_raw) : 0.f) + y);
   }
 }
 

@@ -121,6 +121,76 @@ __global__ __launch_bounds__(256) void k_router_logits(
   router_rows<XT, TT, NORM>(x, T, H, wr, E, nw, eps, xn_out, logits);
 }
 
+// T = 1: the workgroup normalises x once (8 values per thread, x and the norm
+// weights loaded ahead of the router rows), shares xn through LDS, and each
+// wave dots one expert row.  The sum of squares is reduced in the same fixed
+// order in every workgroup, so all of them use the same r bit for bit.
+template <int XT, bool NORM>
+__global__ __launch_bounds__(256) void k_router_m1(
+    const uint16_t* __restrict__ x, int H, const uint16_t* __restrict__ wr, int E,
+    const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
+    uint16_t* __restrict__ logits) {
+  constexpr int RL = 8;  // 512-element rounds of a router row (H <= 4096)
+  __shared__ u32x4 s_xn[512];
+  __shared__ float s_ss[4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int words = H >> 3, rounds = (H + 511) / 512;
+  u32x4 xv[2], gv[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int m = min((int)threadIdx.x + 256 * u, words - 1);
+    xv[u] = ldg16(x + 8 * m);
+    if constexpr (NORM) gv[u] = ldg16(nw + 8 * m);
+  }
+  const int e = blockIdx.x * 4 + wave;
+  const uint16_t* wrow = wr + (int64_t)min(e, E - 1) * H;
+  u32x4 wv[RL];
+#pragma unroll
+  for (int i = 0; i < RL; ++i)
+    wv[i] = i < rounds ? ldg16(wrow + min(8 * lane + 512 * i, H - 8)) : u32x4{0u, 0u, 0u, 0u};
+  float r = 1.f;
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if ((int)threadIdx.x + 256 * u < words) ss += sumsq8<XT>(xv[u]);
+    ss = group_sum<64>(ss);
+    if (lane == 0) s_ss[wave] = ss;
+    __syncthreads();
+    r = 1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)H + eps);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int m = (int)threadIdx.x + 256 * u;
+    if (m < words) {
+      u32x4 v = xv[u];
+      if constexpr (NORM) {
+        v.x = norm_pair<XT>(v.x, gv[u].x, r);
+        v.y = norm_pair<XT>(v.y, gv[u].y, r);
+        v.z = norm_pair<XT>(v.z, gv[u].z, r);
+        v.w = norm_pair<XT>(v.w, gv[u].w, r);
+        if (xn_out && blockIdx.x == 0) *(u32x4*)(xn_out + 8 * m) = v;
+      }
+      s_xn[m] = v;
+    }
+  }
+  __syncthreads();
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < RL; ++i) {
+    const int h = 8 * lane + 512 * i;
+    if (i < rounds && h < H) {
+      const u32x4 xw = s_xn[h >> 3];
+      a = Half<XT>::dot2(wv[i].x, xw.x, a);
+      a = Half<XT>::dot2(wv[i].y, xw.y, a);
+      a = Half<XT>::dot2(wv[i].z, xw.z, a);
+      a = Half<XT>::dot2(wv[i].w, xw.w, a);
+    }
+  }
+  a = group_sum<64>(a);
+  if (lane == 0 && e < E) logits[e] = Half<XT>::from_f32(a);
+}
+
 // one wave per token
 template <int LT, int VPL>
 __global__ __launch_bounds__(256) void k_topk(const void* __restrict__ logits, int T, int E,
@@ -179,8 +249,14 @@ int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr,
                             const void* norm_w, float eps, void* xn, void* logits, hipStream_t s) {
   dim3 grid((E + 3) / 4, 1);
   if (T == 1) {
-    if (xt == I4_F16) launch_router_t<I4_F16, 1>(grid, s, x, T, H, wr, E, norm_w, eps, xn, logits);
-    else launch_router_t<I4_BF16, 1>(grid, s, x, T, H, wr, E, norm_w, eps, xn, logits);
+#define I4_RM1_CASE(XT_, N_)                                                                  \
+  if (xt == XT_ && (norm_w != nullptr) == N_)                                                 \
+    hipLaunchKernelGGL((k_router_m1<XT_, N_>), grid, dim3(256), 0, s, (const uint16_t*)x, H,  \
+                       (const uint16_t*)wr, E, (const uint16_t*)norm_w, eps, (uint16_t*)xn,   \
+                       (uint16_t*)logits);
+    I4_RM1_CASE(I4_F16, true) else I4_RM1_CASE(I4_F16, false) else I4_RM1_CASE(I4_BF16, true)
+    else I4_RM1_CASE(I4_BF16, false)
+#undef I4_RM1_CASE
   } else {
     grid.y = (T + 3) / 4;
     if (xt == I4_F16) launch_router_t<I4_F16, 4>(grid, s, x, T, H, wr, E, norm_w, eps, xn, logits);
