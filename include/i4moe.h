@@ -156,7 +156,8 @@ int    i4_repack_awq_to_ct(const i4_qweight* src, int32_t* dst_packed, void* dst
  *   logits[t][e] = sum_h xn[t][h] * router_w[e][h], fp32 accumulation,
  * rounded to x_dtype like the reference's half-precision gate Linear.
  * xn = x, or RMSNorm(x) with weight norm_w when norm_w is not NULL; xn_out
- * ([T][H], nullable) receives xn. */
+ * ([T][H]) receives xn.  xn_out may be NULL when T == 1 (the norm then stays
+ * in registers); with norm_w and T > 1 it is required (I4_ERR_NULL). */
 int    i4_router_logits(const void* x, int x_dtype, int T, int H,
                         const void* router_w, int E, const void* norm_w, float norm_eps,
                         void* xn_out, void* logits, hipStream_t stream);

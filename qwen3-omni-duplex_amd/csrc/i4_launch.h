@@ -27,11 +27,3 @@ int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr,
                             const void* norm_w, float eps, void* xn, void* logits, hipStream_t s);
 int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
                    float* wf, void* wh, int wht, hipStream_t s);
-
-// Router logits and top-k in one launch (last workgroup of each token tile
-// ranks it).  counters: one per tile of 1 (T == 1) or 4 tokens, zero on entry
-// and left zero.
-int i4_launch_router_topk(const void* x, int xt, int T, int H, const void* wr, int E,
-                          const void* norm_w, float eps, void* xn, void* logits, int topk,
-                          int renorm, int32_t* sel, float* wf, unsigned* counters,
-                          hipStream_t s);

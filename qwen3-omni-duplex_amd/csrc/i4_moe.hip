@@ -343,24 +343,34 @@ __global__ __launch_bounds__(WG) void k_moe_down_list(
 }
 
 // out[t][n] = residual[t][n] + sum_j w[t][j] * ys[t*topk + j][n], j ascending
-template <int XT>
+// out[t] = residual[t] + sum_j w[t][j] ys[t][j] in slot order.  KMAX >= topk
+// slots are loaded unconditionally (indices clamped) so that all loads of a
+// thread are in flight together.
+template <int XT, int KMAX>
 __global__ __launch_bounds__(WG) void k_moe_combine(const float* __restrict__ ys,
                                                     const float* __restrict__ wts,
                                                     const int32_t* __restrict__ sel, int T,
                                                     int topk, int E, int H,
                                                     const uint16_t* __restrict__ residual,
                                                     uint16_t* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
-  if (i >= (int64_t)T * H) return;
+  const int64_t i = min((int64_t)blockIdx.x * WG + threadIdx.x, (int64_t)T * H - 1);
   const int t = (int)(i / H), n = (int)(i - (int64_t)t * H);
-  float y = 0.f;
-  for (int j = 0; j < topk; ++j) {
-    const int s = t * topk + j;
-    const float v = (unsigned)sel[s] < (unsigned)E ? ys[(int64_t)s * H + n] : __builtin_nanf("");
-    y += wts[s] * v;
+  const uint16_t rraw = *(residual ? residual + i : (const uint16_t*)sel);
+  int sl[KMAX];
+  float wv[KMAX], yv[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    const int s = t * topk + min(j, topk - 1);
+    sl[j] = sel[s];
+    wv[j] = wts[s];
+    yv[j] = ys[(int64_t)s * H + n];
   }
-  const float r = residual ? Half<XT>::to_f32(residual[i]) : 0.f;
-  out[i] = Half<XT>::from_f32(r + y);
+  float y = 0.f;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j)
+    if (j < topk) y += wv[j] * ((unsigned)sl[j] < (unsigned)E ? yv[j] : __builtin_nanf(""));
+  const float r = residual ? Half<XT>::to_f32(rraw) : 0.f;
+  if ((int64_t)blockIdx.x * WG + threadIdx.x < (int64_t)T * H) out[i] = Half<XT>::from_f32(r + y);
 }
 
 // ---------------------------------------------------------------------------
@@ -545,25 +555,37 @@ __global__ __launch_bounds__(WG) void k_moe_mfma(
 
 // ---------------------------------------------------------------------------
 // Sort (token, slot) pairs by expert, stable in token order, and cut them
-// into entries of <= mt tokens.  One workgroup of 1024 threads.
+// into entries: experts with >= mf_min tokens get MFMA entries of <= MF_TOK
+// tokens, the others GEMV entries of <= MT_LIST.  One workgroup of 1024
+// threads (E <= 1024):
 //   bits[e][w]: bit b set <=> token 32w + b selected expert e
 //   pre [e][w]: popcount of bits[e][0..w)
+// and thread e owns expert e for the three exclusive prefix sums (tokens,
+// GEMV entries, MFMA entries), done as wave scans plus a scan of the wave
+// totals.
+__device__ inline int wave_incl_scan(int v) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+
 __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel, int T, int topk,
-                                                int E, int mt, int mf_min,
+                                                int E, int mf_min,
                                                 int32_t* __restrict__ perm,
                                                 int4* __restrict__ entries,
                                                 int* __restrict__ n_entries,
                                                 int4* __restrict__ mf_entries,
                                                 int* __restrict__ n_mf_entries) {
   extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ int s_wsum[16][3];
   const int TW = (T + 31) >> 5;
   u32* bits = (u32*)lds;
   u32* pre = bits + E * TW;
-  int* cnt = (int*)(pre + E * TW);
-  int* off = cnt + E;       // [E + 1]
-  int* eoff = off + E + 1;  // [E + 1] GEMV entries
-  int* moff = eoff + E + 1; // [E + 1] MFMA entries
-  const int tid = threadIdx.x, nt = blockDim.x;
+  const int tid = threadIdx.x, nt = blockDim.x, wave = tid >> 6, lane = tid & 63;
   for (int i = tid; i < E * TW; i += nt) bits[i] = 0u;
   __syncthreads();
   for (int s = tid; s < T * topk; s += nt) {
@@ -571,48 +593,52 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
     if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * TW + (t >> 5)], 1u << (t & 31));
   }
   __syncthreads();
-  for (int e = tid; e < E; e += nt) {
-    int run = 0;
+  int c = 0;
+  if (tid < E) {
     for (int wd = 0; wd < TW; ++wd) {
-      pre[e * TW + wd] = (u32)run;
-      run += __popc(bits[e * TW + wd]);
+      pre[tid * TW + wd] = (u32)c;
+      c += __popc(bits[tid * TW + wd]);
     }
-    cnt[e] = run;
+  }
+  const bool big = c >= mf_min;
+  const int ne = big ? 0 : (c + MT_LIST - 1) / MT_LIST;
+  const int nm = big ? (c + MF_TOK - 1) / MF_TOK : 0;
+  const int ic = wave_incl_scan(c), ie = wave_incl_scan(ne), im = wave_incl_scan(nm);
+  if (lane == 63) {
+    s_wsum[wave][0] = ic;
+    s_wsum[wave][1] = ie;
+    s_wsum[wave][2] = im;
   }
   __syncthreads();
-  if (tid == 0) {
-    int o = 0, eo = 0, mo = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = o;
-      eoff[e] = eo;
-      moff[e] = mo;
-      o += cnt[e];
-      if (cnt[e] >= mf_min) mo += (cnt[e] + MF_TOK - 1) / MF_TOK;
-      else eo += (cnt[e] + mt - 1) / mt;
-    }
-    off[E] = o;
-    eoff[E] = eo;
-    moff[E] = mo;
-    *n_entries = eo;
-    *n_mf_entries = mo;
+  int bc = 0, be = 0, bm = 0;  // totals of the waves before this one
+  for (int v = 0; v < wave; ++v) {
+    bc += s_wsum[v][0];
+    be += s_wsum[v][1];
+    bm += s_wsum[v][2];
   }
+  const int off = bc + ic - c, eoff = be + ie - ne, moff = bm + im - nm;
+  if (tid == nt - 1) {  // the last thread's inclusive sums are the totals
+    *n_entries = be + ie;
+    *n_mf_entries = bm + im;
+  }
+  int* s_off = (int*)(pre + E * TW);  // [E]
+  if (tid < E) s_off[tid] = off;
   __syncthreads();
   for (int s = tid; s < T * topk; s += nt) {
     const int e = sel[s], t = s / topk;
     if ((unsigned)e < (unsigned)E) {
       const u32 word = bits[e * TW + (t >> 5)];
       const int below = __popc(word & ((1u << (t & 31)) - 1u));
-      perm[off[e] + (int)pre[e * TW + (t >> 5)] + below] = s;
+      perm[s_off[e] + (int)pre[e * TW + (t >> 5)] + below] = s;
     }
   }
-  for (int e = tid; e < E; e += nt) {
-    const int c = cnt[e];
-    if (c >= mf_min) {
-      for (int q = 0; q * MF_TOK < c; ++q)
-        mf_entries[moff[e] + q] = int4{e, off[e] + q * MF_TOK, min(MF_TOK, c - q * MF_TOK), 0};
+  if (tid < E) {
+    if (big) {
+      for (int q = 0; q < nm; ++q)
+        mf_entries[moff + q] = int4{tid, off + q * MF_TOK, min(MF_TOK, c - q * MF_TOK), 0};
     } else {
-      for (int q = 0; q * mt < c; ++q)
-        entries[eoff[e] + q] = int4{e, off[e] + q * mt, min(mt, c - q * mt), 0};
+      for (int q = 0; q < ne; ++q)
+        entries[eoff + q] = int4{tid, off + q * MT_LIST, min(MT_LIST, c - q * MT_LIST), 0};
     }
   }
 }
@@ -639,7 +665,6 @@ struct MoeWs {
   int* n_entries;
   int4* mf_entries;
   int* n_mf_entries;
-  unsigned* counters;  // router/top-k handoff, one per token tile; zero between calls
   size_t bytes;
 };
 
@@ -664,7 +689,6 @@ MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
   m.n_entries = (int*)take(4);
   m.mf_entries = (int4*)take((E + Tk / MF_MIN + 1) * sizeof(int4));
   m.n_mf_entries = (int*)take(4);
-  m.counters = (unsigned*)take(((size_t)(Tc + 3) / 4 + 1) * 4);
   m.bytes = o;
   return m;
 }
@@ -877,22 +901,22 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
     if (rc) return rc;
     return ops.down_m1(ws.act, topk, sel, wts, qdn, residual, out, s);
   }
+  const void* lg = logits;
   if (mw->router_w) {
-    rc = i4_launch_router_topk(x, xt, T, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
-                               mw->norm_w ? ws.xn : nullptr, ws.logits, topk, renorm, sel, wts,
-                               ws.counters, s);
+    rc = i4_launch_router_logits(x, xt, T, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
+                                 mw->norm_w ? ws.xn : nullptr, ws.logits, s);
     if (rc) return rc;
+    lg = ws.logits;
     if (mw->norm_w) x = ws.xn;
-  } else {
-    rc = i4_launch_topk(logits, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
-    if (rc) return rc;
   }
+  rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
+  if (rc) return rc;
   const int Tk = T * topk;
   const int TW = (T + 31) / 32;
   // experts with >= MF_MIN tokens go to the MFMA tile kernels (G = 128 weights)
   const bool mfma = gu.group == 128 && dn.group == 128 && I % 128 == 0 && H % 128 == 0;
-  const size_t glds = (size_t)2 * E * TW * 4 + (size_t)(4 * E + 3) * 4;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E, MT_LIST,
+  const size_t glds = (size_t)2 * E * TW * 4 + (size_t)E * 4;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E,
                      mfma ? MF_MIN : 0x7fffffff, ws.perm, ws.entries, ws.n_entries, ws.mf_entries,
                      ws.n_mf_entries);
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
@@ -915,12 +939,17 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   }
   const int64_t tot = (int64_t)T * H;
   dim3 cg((unsigned)((tot + WG - 1) / WG));
-  if (xt == I4_F16)
-    hipLaunchKernelGGL(k_moe_combine<I4_F16>, cg, dim3(WG), 0, s, ws.ys, wts, sel, T, topk, E, H,
-                       (const uint16_t*)residual, (uint16_t*)out);
-  else
-    hipLaunchKernelGGL(k_moe_combine<I4_BF16>, cg, dim3(WG), 0, s, ws.ys, wts, sel, T, topk, E,
-                       H, (const uint16_t*)residual, (uint16_t*)out);
+#define I4_COMB_CASE(XT_, KM_)                                                                 \
+  hipLaunchKernelGGL((k_moe_combine<XT_, KM_>), cg, dim3(WG), 0, s, ws.ys, wts, sel, T, topk, E, \
+                     H, (const uint16_t*)residual, (uint16_t*)out)
+  if (xt == I4_F16) {
+    if (topk <= 8) I4_COMB_CASE(I4_F16, 8);
+    else I4_COMB_CASE(I4_F16, 16);
+  } else {
+    if (topk <= 8) I4_COMB_CASE(I4_BF16, 8);
+    else I4_COMB_CASE(I4_BF16, 16);
+  }
+#undef I4_COMB_CASE
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 

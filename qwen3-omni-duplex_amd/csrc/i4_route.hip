@@ -36,91 +36,6 @@ template <int XT> __device__ inline float sumsq8(u32x4 d) {
   return s;
 }
 
-// logits[t][e] = round(sum_h xn[t][h] * wr[e][h]); one wave per expert row,
-// TT tokens per workgroup column.  Lane l covers h = 8l + 512i (H <= 2048 *
-// RL).  The router-row loads are issued before the norm reduction.  With
-// NORM every wave computes r = 1 / sqrt(mean(x^2) + eps) for its tokens in
-// the same order (so all waves agree bit for bit), and wave 0 of column 0
-// writes xn for the expert kernels.
-template <int XT, int TT, bool NORM>
-__device__ inline void router_rows(const uint16_t* __restrict__ x, int T, int H,
-                                   const uint16_t* __restrict__ wr, int E,
-                                   const uint16_t* __restrict__ nw, float eps,
-                                   uint16_t* __restrict__ xn_out, uint16_t* __restrict__ logits) {
-  constexpr int RL = 8;  // 512-element rounds held in registers (H <= 4096)
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int e = blockIdx.x * 4 + wave;
-  const int t0 = blockIdx.y * TT;
-  if (e >= E) return;
-  const int rounds = (H + 511) / 512;
-  const uint16_t* wrow = wr + (int64_t)e * H;
-  u32x4 wv[RL];
-#pragma unroll
-  for (int i = 0; i < RL; ++i) {
-    const int h = min(8 * lane + 512 * i, H - 8);
-    wv[i] = i < rounds ? ldg16(wrow + h) : u32x4{0u, 0u, 0u, 0u};
-  }
-  const bool write_xn = NORM && xn_out != nullptr && blockIdx.x == 0 && wave == 0;
-  u32x4 gv[RL];
-  if constexpr (NORM) {  // norm weights with the router rows, ahead of any dependency
-#pragma unroll
-    for (int i = 0; i < RL; ++i) {
-      const int h = min(8 * lane + 512 * i, H - 8);
-      gv[i] = i < rounds ? ldg16(nw + h) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    if (t0 + t >= T) break;
-    const uint16_t* xr = x + (int64_t)(t0 + t) * H;
-    u32x4 xv[RL];
-#pragma unroll
-    for (int i = 0; i < RL; ++i) {
-      const int h = min(8 * lane + 512 * i, H - 8);
-      xv[i] = i < rounds ? ldg16(xr + h) : u32x4{0u, 0u, 0u, 0u};
-    }
-    if constexpr (NORM) {
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < RL; ++i)
-        if (i < rounds && 8 * lane + 512 * i < H) ss += sumsq8<XT>(xv[i]);
-      ss = group_sum<64>(ss);
-      const float r = 1.0f / sqrtf(ss / (float)H + eps);
-#pragma unroll
-      for (int i = 0; i < RL; ++i) {
-        const int h = 8 * lane + 512 * i;
-        if (i < rounds && h < H) {
-          xv[i].x = norm_pair<XT>(xv[i].x, gv[i].x, r);
-          xv[i].y = norm_pair<XT>(xv[i].y, gv[i].y, r);
-          xv[i].z = norm_pair<XT>(xv[i].z, gv[i].z, r);
-          xv[i].w = norm_pair<XT>(xv[i].w, gv[i].w, r);
-          if (write_xn) *(u32x4*)(xn_out + (int64_t)(t0 + t) * H + h) = xv[i];
-        }
-      }
-    }
-    float a = 0.f;
-#pragma unroll
-    for (int i = 0; i < RL; ++i) {
-      if (i < rounds && 8 * lane + 512 * i < H) {
-        a = Half<XT>::dot2(wv[i].x, xv[i].x, a);
-        a = Half<XT>::dot2(wv[i].y, xv[i].y, a);
-        a = Half<XT>::dot2(wv[i].z, xv[i].z, a);
-        a = Half<XT>::dot2(wv[i].w, xv[i].w, a);
-      }
-    }
-    a = group_sum<64>(a);
-    if (lane == 0) logits[(int64_t)(t0 + t) * E + e] = Half<XT>::from_f32(a);
-  }
-}
-
-template <int XT, int TT, bool NORM>
-__global__ __launch_bounds__(256) void k_router_logits(
-    const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ wr, int E,
-    const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
-    uint16_t* __restrict__ logits) {
-  router_rows<XT, TT, NORM>(x, T, H, wr, E, nw, eps, xn_out, logits);
-}
-
 // T = 1: the workgroup normalises x once (8 values per thread, x and the norm
 // weights loaded ahead of the router rows), shares xn through LDS, and each
 // wave dots one expert row.  The sum of squares is reduced in the same fixed
@@ -191,6 +106,118 @@ __global__ __launch_bounds__(256) void k_router_m1(
   if (lane == 0 && e < E) logits[e] = Half<XT>::from_f32(a);
 }
 
+// T > 1, pass 1: RMSNorm of one token per workgroup with exactly the
+// arithmetic of k_router_m1 (same thread -> word map, same reduction order),
+// so each token's xn is bit for bit the one it gets alone.
+template <int XT>
+__global__ __launch_bounds__(256) void k_rmsnorm_t(const uint16_t* __restrict__ x, int H,
+                                                   const uint16_t* __restrict__ nw, float eps,
+                                                   uint16_t* __restrict__ xn) {
+  __shared__ float s_ss[4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int words = H >> 3;
+  const uint16_t* xr = x + (int64_t)blockIdx.x * H;
+  u32x4 xv[2], gv[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int m = min((int)threadIdx.x + 256 * u, words - 1);
+    xv[u] = ldg16(xr + 8 * m);
+    gv[u] = ldg16(nw + 8 * m);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if ((int)threadIdx.x + 256 * u < words) ss += sumsq8<XT>(xv[u]);
+  ss = group_sum<64>(ss);
+  if (lane == 0) s_ss[wave] = ss;
+  __syncthreads();
+  const float r =
+      1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)H + eps);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int m = (int)threadIdx.x + 256 * u;
+    if (m < words) {
+      u32x4 v = xv[u];
+      v.x = norm_pair<XT>(v.x, gv[u].x, r);
+      v.y = norm_pair<XT>(v.y, gv[u].y, r);
+      v.z = norm_pair<XT>(v.z, gv[u].z, r);
+      v.w = norm_pair<XT>(v.w, gv[u].w, r);
+      *(u32x4*)(xn + (int64_t)blockIdx.x * H + 8 * m) = v;
+    }
+  }
+}
+
+// T > 1, pass 2: logits of TT tokens (staged in LDS) x 4 * EPW experts per
+// workgroup.  Each logit is the per-lane dot2 chain and wave sum of
+// k_router_m1, so a token's logits do not depend on the batch.  Wave w owns
+// experts EPW * w .. of the tile; the TT sums of one expert are formed
+// together so their wave reductions overlap.
+template <int XT, int TT, int EPW>
+__global__ __launch_bounds__(256) void k_router_t(const uint16_t* __restrict__ x, int T, int H,
+                                                  const uint16_t* __restrict__ wr, int E,
+                                                  uint16_t* __restrict__ logits) {
+  constexpr int RL = 8;  // 512-element rounds of a router row (H <= 4096)
+  extern __shared__ __align__(16) unsigned char lds[];
+  u32x4* s_x = (u32x4*)lds;  // [TT][words]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int words = H >> 3, rounds = (H + 511) / 512;
+  const int t0 = blockIdx.y * TT, e0 = (blockIdx.x * 4 + wave) * EPW;
+  u32x4 wv[EPW][RL];
+#pragma unroll
+  for (int j = 0; j < EPW; ++j) {
+    const uint16_t* wrow = wr + (int64_t)min(e0 + j, E - 1) * H;
+#pragma unroll
+    for (int i = 0; i < RL; ++i)
+      wv[j][i] = i < rounds ? ldg16(wrow + min(8 * lane + 512 * i, H - 8)) : u32x4{0u, 0u, 0u, 0u};
+  }
+  // all staging loads in flight before the first LDS write (a load / wait /
+  // write loop would pay one memory latency per round)
+  constexpr int NS = TT * 512 / 256;  // 16-byte words per thread at H = 4096
+  const int total = TT * words;
+  u32x4 sv[NS];
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    if (256 * u < total) {
+      const int idx = min((int)threadIdx.x + 256 * u, total - 1);
+      const int tk = idx / words, m = idx - tk * words;
+      sv[u] = ldg16(x + (int64_t)min(t0 + tk, T - 1) * H + 8 * m);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    const int idx = (int)threadIdx.x + 256 * u;
+    if (256 * u < total && idx < total) s_x[idx] = sv[u];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < EPW; ++j) {
+    float a[TT];
+#pragma unroll
+    for (int tk = 0; tk < TT; ++tk) {
+      a[tk] = 0.f;
+#pragma unroll
+      for (int i = 0; i < RL; ++i) {
+        const int h = 8 * lane + 512 * i;
+        if (i < rounds && h < H) {
+          const u32x4 xw = s_x[tk * words + (h >> 3)];
+          a[tk] = Half<XT>::dot2(wv[j][i].x, xw.x, a[tk]);
+          a[tk] = Half<XT>::dot2(wv[j][i].y, xw.y, a[tk]);
+          a[tk] = Half<XT>::dot2(wv[j][i].z, xw.z, a[tk]);
+          a[tk] = Half<XT>::dot2(wv[j][i].w, xw.w, a[tk]);
+        }
+      }
+    }
+#pragma unroll
+    for (int tk = 0; tk < TT; ++tk) a[tk] = group_sum<64>(a[tk]);
+    const int e = e0 + j;
+    if (lane == 0 && e < E) {
+#pragma unroll
+      for (int tk = 0; tk < TT; ++tk)
+        if (t0 + tk < T) logits[(int64_t)(t0 + tk) * E + e] = Half<XT>::from_f32(a[tk]);
+    }
+  }
+}
+
 // one wave per token
 template <int LT, int VPL>
 __global__ __launch_bounds__(256) void k_topk(const void* __restrict__ logits, int T, int E,
@@ -202,48 +229,9 @@ __global__ __launch_bounds__(256) void k_topk(const void* __restrict__ logits, i
   wave_topk_row<LT, VPL>(logits, t, E, topk, renorm, sel, wf, wh, wht);
 }
 
-// Router logits + top-k in one launch.  Every workgroup of token tile y
-// computes 4 expert rows of logits; the last one to finish (device-scope
-// counter per tile) ranks the tile's tokens and resets the counter, so the
-// counters are zero again after every launch.
-template <int XT, int TT, bool NORM>
-__global__ __launch_bounds__(256) void k_router_topk(
-    const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ wr, int E,
-    const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
-    uint16_t* __restrict__ logits, int topk, int renorm, int32_t* __restrict__ sel,
-    float* __restrict__ wf, unsigned* __restrict__ counters) {
-  router_rows<XT, TT, NORM>(x, T, H, wr, E, nw, eps, xn_out, logits);
-  __threadfence();
-  __syncthreads();
-  __shared__ bool last;
-  if (threadIdx.x == 0) last = atomicAdd(&counters[blockIdx.y], 1u) == gridDim.x - 1;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  const int wave = threadIdx.x >> 6, t = blockIdx.y * TT + wave;
-  if (wave < TT && t < T) {
-    if (E <= 128) wave_topk_row<XT, 2>(logits, t, E, topk, renorm, sel, wf, nullptr, 0);
-    else wave_topk_row<XT, 8>(logits, t, E, topk, renorm, sel, wf, nullptr, 0);
-  }
-  if (threadIdx.x == 0) counters[blockIdx.y] = 0u;
-}
-
 }  // namespace i4
 
 using namespace i4;
-
-template <int XT, int TT>
-static void launch_router_t(dim3 grid, hipStream_t s, const void* x, int T, int H, const void* wr,
-                            int E, const void* nw, float eps, void* xn, void* logits) {
-  if (nw)
-    hipLaunchKernelGGL((k_router_logits<XT, TT, true>), grid, dim3(256), 0, s, (const uint16_t*)x,
-                       T, H, (const uint16_t*)wr, E, (const uint16_t*)nw, eps, (uint16_t*)xn,
-                       (uint16_t*)logits);
-  else
-    hipLaunchKernelGGL((k_router_logits<XT, TT, false>), grid, dim3(256), 0, s,
-                       (const uint16_t*)x, T, H, (const uint16_t*)wr, E, (const uint16_t*)nullptr,
-                       eps, (uint16_t*)nullptr, (uint16_t*)logits);
-}
 
 int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr, int E,
                             const void* norm_w, float eps, void* xn, void* logits, hipStream_t s) {
@@ -258,31 +246,27 @@ int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr,
     else I4_RM1_CASE(I4_BF16, false)
 #undef I4_RM1_CASE
   } else {
-    grid.y = (T + 3) / 4;
-    if (xt == I4_F16) launch_router_t<I4_F16, 4>(grid, s, x, T, H, wr, E, norm_w, eps, xn, logits);
-    else launch_router_t<I4_BF16, 4>(grid, s, x, T, H, wr, E, norm_w, eps, xn, logits);
+    const uint16_t* xin = (const uint16_t*)x;
+    if (norm_w) {
+      if (xt == I4_F16)
+        hipLaunchKernelGGL(k_rmsnorm_t<I4_F16>, dim3(T), dim3(256), 0, s, xin, H,
+                           (const uint16_t*)norm_w, eps, (uint16_t*)xn);
+      else
+        hipLaunchKernelGGL(k_rmsnorm_t<I4_BF16>, dim3(T), dim3(256), 0, s, xin, H,
+                           (const uint16_t*)norm_w, eps, (uint16_t*)xn);
+      xin = (const uint16_t*)xn;
+    }
+    constexpr int TT = 8, EPW = 2;
+    const dim3 g2((E + 4 * EPW - 1) / (4 * EPW), (T + TT - 1) / TT);
+    const size_t lds = (size_t)TT * (H / 8) * 16;  // <= 64 KB for H <= 4096
+#define I4_RT_CASE(XT_)                                                                       \
+  if (xt == XT_)                                                                              \
+    hipLaunchKernelGGL((k_router_t<XT_, TT, EPW>), g2, dim3(256), lds, s, xin, T, H,           \
+                       (const uint16_t*)wr, E, (uint16_t*)logits);
+    I4_RT_CASE(I4_F16) else I4_RT_CASE(I4_BF16)
+#undef I4_RT_CASE
   }
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
-}
-
-int i4_launch_router_topk(const void* x, int xt, int T, int H, const void* wr, int E,
-                          const void* norm_w, float eps, void* xn, void* logits, int topk,
-                          int renorm, int32_t* sel, float* wf, unsigned* counters,
-                          hipStream_t s) {
-  const int TT = T == 1 ? 1 : 4;
-  dim3 grid((E + 3) / 4, (T + TT - 1) / TT);
-#define I4_RT_CASE(XT_, TT_, N_)                                                                \
-  if (xt == XT_ && TT == TT_ && (norm_w != nullptr) == N_) {                                    \
-    hipLaunchKernelGGL((k_router_topk<XT_, TT_, N_>), grid, dim3(256), 0, s, (const uint16_t*)x, \
-                       T, H, (const uint16_t*)wr, E, (const uint16_t*)norm_w, eps,             \
-                       (uint16_t*)xn, (uint16_t*)logits, topk, renorm, sel, wf, counters);     \
-    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
-  }
-  I4_RT_CASE(I4_F16, 1, true) I4_RT_CASE(I4_F16, 1, false) I4_RT_CASE(I4_F16, 4, true)
-  I4_RT_CASE(I4_F16, 4, false) I4_RT_CASE(I4_BF16, 1, true) I4_RT_CASE(I4_BF16, 1, false)
-  I4_RT_CASE(I4_BF16, 4, true) I4_RT_CASE(I4_BF16, 4, false)
-#undef I4_RT_CASE
-  return I4_ERR_DTYPE;
 }
 
 int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
@@ -308,6 +292,7 @@ int i4_router_logits(const void* x, int x_dtype, int T, int H, const void* route
                      hipStream_t stream) {
   if (!x || !router_w || !logits) return I4_ERR_NULL;
   if (xn_out && !norm_w) return I4_ERR_NULL;
+  if (norm_w && T > 1 && !xn_out) return I4_ERR_NULL;  // the norm pass writes xn there
   if (((uintptr_t)norm_w & 15) || ((uintptr_t)xn_out & 15)) return I4_ERR_ALIGN;
   if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
   if (T < 1 || T > 65535 * 4 || H < 8 || H % 8 != 0 || H > 4096 || E < 1 || E > 65535 * 4)

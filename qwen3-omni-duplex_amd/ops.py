@@ -140,7 +140,8 @@ def router_logits(x: torch.Tensor, router_w: torch.Tensor, norm_w: torch.Tensor 
     wr = router_w.contiguous()
     nw = None if norm_w is None else norm_w.contiguous()
     out = torch.empty(T, E, dtype=x.dtype, device=dev)
-    xn = torch.empty_like(xf) if (return_xn and nw is not None) else None
+    # with a norm and T > 1 the library writes xn (its first pass) even if not returned
+    xn = torch.empty_like(xf) if (nw is not None and (return_xn or T > 1)) else None
     _lib.check(_lib.lib().i4_router_logits(xf.data_ptr(), xt, T, H, wr.data_ptr(), E,
                                            _lib.ptr(nw), float(norm_eps), _lib.ptr(xn),
                                            out.data_ptr(), _lib.stream(dev)))

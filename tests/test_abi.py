@@ -100,6 +100,9 @@ def test_call_validation_codes(pkg):
                                 None) == -1
     assert lib.i4_router_logits(0x30000, 1, 1, 2048, 0x40000, 128, 0x60002, 1e-6, None, 0x50000,
                                 None) == -4
+    # with a norm and more than one token the normalised rows must have somewhere to go
+    assert lib.i4_router_logits(0x30000, 1, 2, 2048, 0x40000, 128, 0x60000, 1e-6, None, 0x50000,
+                                None) == -1
 
 
 def test_moe_validation_codes(pkg):

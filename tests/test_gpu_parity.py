@@ -455,6 +455,30 @@ def test_router_logits_with_norm(pkg, dev, T):
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -10 + 1e-6)
 
 
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+@pytest.mark.parametrize("norm", [False, True])
+def test_router_tokens_match_single_token_bits(pkg, dev, xdt, norm):
+    """The multi-token router gives every token the logits and RMSNorm output it gets alone,
+    bit for bit (so routing never depends on the batch), including a ragged last tile."""
+    rng = np.random.default_rng(41)
+    E, H, T = 128, 2048, 19
+    wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    wr = i4ref.f32_to_bf16_bits(wr) if xdt == "bf16" else wr.astype(np.float16)
+    x = t_(make_x(rng, (T, H), xdt), dev)
+    w_t = t_(wr, dev)
+    nw = t_(rng.uniform(0.5, 1.5, H).astype(np.float16), dev) if norm else None
+    if nw is not None and xdt == "bf16":
+        nw = nw.to(torch.bfloat16)
+    kw = dict(norm_w=nw, norm_eps=1e-6, return_xn=True) if norm else {}
+    full = pkg.router_logits(x, w_t, **kw)
+    for t in range(T):
+        one = pkg.router_logits(x[t:t + 1], w_t, **kw)
+        if norm:
+            assert torch.equal(one[0][0], full[0][t]) and torch.equal(one[1][0], full[1][t])
+        else:
+            assert torch.equal(one[0], full[t])
+
+
 def test_graph_replays_match_eager(pkg, dev):
     rng = np.random.default_rng(28)
     moe, _, _, _ = _awq_moe(pkg, dev, rng, E=32)
