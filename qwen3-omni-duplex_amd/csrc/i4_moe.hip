@@ -374,32 +374,40 @@ __global__ __launch_bounds__(WG) void k_moe_combine(const float* __restrict__ ys
 }
 
 // ---------------------------------------------------------------------------
-// MFMA tile path for experts that received many tokens (T > 1).
+// MFMA tile path for the grouped experts (T > 1).
 //
-// One workgroup = 64 tokens of one expert (4 m-blocks of 16) x a column tile;
-// wave w owns NB n-blocks of 16 weight rows.  v_mfma_f32_16x16x32_{f16,bf16}:
-// lane l supplies A[m = l%16][8 k] and B[8 k][n = l%16] for its k-group
-// kb = l/16 and receives D[4 kb + i][l%16], i < 4.  K is walked in 128-column
-// superchunks (one quantisation group, G = 128): lane group kb loads chunk
-// 4s + kb of its weight row with one 16-byte load, and MFMA step t uses word t
-// of that chunk -- a permutation of k that A (the staged activations, read in
-// the same order) follows, so the contraction is unchanged.  B holds the exact
-// half values M + q; after the group's 4 steps the accumulator D is corrected
-// per output with the group's scale s, zero z and activation sum S_m:
-//     res += s * D - s (M + z) S_m,
-// so every product is exact and accumulation is fp32, as in the GEMV path.
+// One workgroup = up to 64 tokens of one expert (m-blocks of 16) x a column
+// tile; wave w owns NB n-blocks of 16 weight rows.  v_mfma_f32_16x16x32_{f16,
+// bf16}: lane l supplies A[m = l%16][8 k] and B[8 k][n = l%16] for its
+// k-group kb = l/16 and receives D[4 kb + i][l%16], i < 4.  K is walked in
+// 128-column superchunks (one quantisation group, G = 128): lane group kb
+// loads chunk 4s + kb of its weight row with one 16-byte load, and MFMA step
+// t uses word t of that chunk -- a permutation of k that A (the staged
+// activations, read in the same order) follows, so the contraction is
+// unchanged.
+//   fp16: B holds q - z exactly ((M + q) - (M + z), one packed half add per
+//         pair), so after the group's 4 steps res += s * D.
+//   bf16: B holds M + q exactly (no packed bf16 add on gfx950) and the group
+//         correction is res += s * D - s (M + z) S_m with S_m the staged
+//         activation sum of token m over the group.
+// Every product is exact and accumulation is fp32, as in the GEMV path.
 // Activation tiles are double buffered in LDS (token stride 272 B keeps the 16
-// tokens of an MFMA on distinct banks); the next superchunk's weights and
-// activations are loaded while the current one is multiplied.
-//   GATEUP: NB = 2 (16 gate rows, the same 16 up rows), SiLU in the epilogue,
-//           act[pos] in the activation dtype.  Column tile 64 row pairs.
-//   DOWN:   NB = 2 (32 output rows), ys[slot] in fp32.  Column tile 128 rows.
+// tokens of an MFMA on distinct banks), only the m-blocks the entry uses are
+// staged, and the next superchunk's weights and activations are loaded while
+// the current one is multiplied.
+//   GATEUP: NB/2 blocks of gate rows and the same up rows per wave, SiLU in
+//           the epilogue, act[pos] in the activation dtype; 32 NB row pairs
+//           per workgroup.
+//   DOWN:   NB blocks of output rows per wave, ys[slot] in fp32; 64 NB rows
+//           per workgroup.
 static constexpr int MF_TOK = 64;   // tokens per MFMA entry
-static constexpr int MF_MIN = 16;   // experts with at least this many tokens use MFMA
+static constexpr int MF_SMALL = 16; // experts with at most this many tokens: k_moe_mfma_s
 static constexpr int MF_TSTRIDE = 17;  // uint4 per staged token row (16 + 1 pad)
+static constexpr int MF_NB = 2;     // n-blocks per wave
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 template <int XT> __device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
   if constexpr (XT == I4_F16)
@@ -416,13 +424,19 @@ template <int XT> __device__ inline u32x4 decode8(u32 w) {
   return u32x4{(w & MK) | MG, ((w >> 4) & MK) | MG, ((w >> 8) & MK) | MG, ((w >> 12) & MK) | MG};
 }
 
-template <int XT, int ST, bool GATEUP>
+// fp16 pair (M + q0, M + q1) + nz, nz = (-(M + z), -(M + z)): exactly (q0 - z, q1 - z)
+__device__ inline u32 sub_zero(u32 p, u32 nz) {
+  return __builtin_bit_cast(u32, __builtin_bit_cast(f16x2, p) + __builtin_bit_cast(f16x2, nz));
+}
+
+template <int XT, int ST, bool GATEUP, int NB>
 __global__ __launch_bounds__(WG) void k_moe_mfma(
     const uint16_t* __restrict__ src, int topk, const int4* __restrict__ entries,
     const int* __restrict__ n_entries, const int32_t* __restrict__ perm, QW w, int I,
     uint16_t* __restrict__ act, float* __restrict__ ys) {
-  constexpr int NB = 2;
-  constexpr int COLS = GATEUP ? 64 : 128;  // weight rows (pairs for GATEUP) per workgroup
+  constexpr bool EXACT = XT == I4_F16;
+  constexpr int COLS = GATEUP ? 32 * NB : 64 * NB;  // row pairs (GATEUP) / rows per workgroup
+  static_assert(!GATEUP || NB % 2 == 0, "gate_up pairs gate and up blocks");
   __shared__ u32x4 xs[2][MF_TOK * MF_TSTRIDE];
   __shared__ float xsum[2][MF_TOK];
   if ((int)blockIdx.y >= *n_entries) return;
@@ -433,39 +447,47 @@ __global__ __launch_bounds__(WG) void k_moe_mfma(
   const int ln = lane & 15, kb = lane >> 4;
   const bool ev = (unsigned)e < (unsigned)w.E;
   const int ee = ev ? e : 0;
+  const int nmb = (cnt + 15) >> 4;
 
   // weight rows of this lane (column ln of each n-block)
   RowPtr rp[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     int row;
-    if constexpr (GATEUP) row = blockIdx.x * COLS + 16 * wave + ln + (nb ? I : 0);
-    else row = blockIdx.x * COLS + 32 * wave + 16 * nb + ln;
+    if constexpr (GATEUP)
+      row = blockIdx.x * COLS + 16 * (NB / 2) * wave + 16 * (nb % (NB / 2)) + ln +
+            (nb >= NB / 2 ? I : 0);
+    else
+      row = blockIdx.x * COLS + 16 * NB * wave + 16 * nb + ln;
     rp[nb] = row_ptr<ST>(w, ee, row);
   }
-  // staging role: token tk, chunk kc of the superchunk
+  // staging role: token tk, chunk kc of the superchunk; wave w stages m-block w
   const int tk = threadIdx.x >> 2, kc = threadIdx.x & 3;
-  const bool tv = tk < cnt;
+  const bool stager = wave < nmb;  // wave-uniform
   const uint16_t* xrow;
   if constexpr (GATEUP) xrow = src + (int64_t)(perm[pos0 + min(tk, cnt - 1)] / topk) * K;
   else xrow = src + (int64_t)(pos0 + min(tk, cnt - 1)) * K;
 
   u32x4 xd[4];
   auto issue_x = [&](int sc) {
+    if (stager) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xd[j] = ldg16(xrow + 128 * sc + 32 * kc + 8 * j);
-  };
-  auto commit_x = [&](int sc, int buf) {
-    float sm = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u32x4 d = tv ? xd[j] : u32x4{0u, 0u, 0u, 0u};
-      xs[buf][tk * MF_TSTRIDE + kc * 4 + j] = pair_order(d);
-      sm += sum8<XT>(d).y;
+      for (int j = 0; j < 4; ++j) xd[j] = ldg16(xrow + 128 * sc + 32 * kc + 8 * j);
     }
-    sm = group_sum<4>(sm);
-    if (kc == 0) xsum[buf][tk] = sm;
-    (void)sc;
+  };
+  auto commit_x = [&](int buf) {
+    if (stager) {
+      float sm = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xs[buf][tk * MF_TSTRIDE + kc * 4 + j] = pair_order(xd[j]);
+        if constexpr (!EXACT) sm += sum8<XT>(xd[j]).y;
+      }
+      if constexpr (!EXACT) {
+        sm = group_sum<4>(sm);
+        if (kc == 0) xsum[buf][tk] = sm;
+      }
+    }
   };
   Chunk cur[NB], nxt[NB];  // weights of this superchunk / the next one
   auto issue_w = [&](int sc, Chunk* dst) {
@@ -478,17 +500,25 @@ __global__ __launch_bounds__(WG) void k_moe_mfma(
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) res[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int nmb = (cnt + 15) >> 4;
 
   issue_w(0, cur);
   issue_x(0);
   for (int sc = 0; sc < SC; ++sc) {
     const int buf = sc & 1;
-    commit_x(sc, buf);
+    commit_x(buf);
     __syncthreads();
     if (sc + 1 < SC) {
       issue_w(sc + 1, nxt);
       issue_x(sc + 1);
+    }
+    const int g = (4 * sc + kb) >> w.gshift;
+    u32 nz[NB];  // fp16: -(M + z) in both halves
+    if constexpr (EXACT) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const u32 z = (cur[nb].z >> (4 * (g & 7))) & 15u;
+        nz[nb] = (0xE400u | z) * 0x00010001u;
+      }
     }
     f32x4 d[4][NB];
 #pragma unroll
@@ -502,6 +532,12 @@ __global__ __launch_bounds__(WG) void k_moe_mfma(
       for (int nb = 0; nb < NB; ++nb) {
         const u32x4 cw = cur[nb].w;
         b[nb] = decode8<XT>(t == 0 ? cw.x : t == 1 ? cw.y : t == 2 ? cw.z : cw.w);
+        if constexpr (EXACT) {
+          b[nb].x = sub_zero(b[nb].x, nz[nb]);
+          b[nb].y = sub_zero(b[nb].y, nz[nb]);
+          b[nb].z = sub_zero(b[nb].z, nz[nb]);
+          b[nb].w = sub_zero(b[nb].w, nz[nb]);
+        }
       }
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
@@ -512,20 +548,24 @@ __global__ __launch_bounds__(WG) void k_moe_mfma(
         }
       }
     }
-    // per-group correction: res += s D - s (M + z) S_m
+    // per-group correction
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const Chunk& c = cur[nb];
-      const int g = (4 * sc + kb) >> w.gshift;
       const float sv = scale_from_raw<ST>(c.s);
-      const float z = (float)((c.z >> (4 * (g & 7))) & 15u);
-      const float bv = -sv * (Half<XT>::MAGIC + z);
+      float bv = 0.f;
+      if constexpr (!EXACT) bv = -sv * (Half<XT>::MAGIC + (float)((c.z >> (4 * (g & 7))) & 15u));
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         if (mb < nmb) {
-          const float* sp = &xsum[buf][16 * mb + 4 * kb];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) res[mb][nb][i] = fmaf(sv, d[mb][nb][i], fmaf(bv, sp[i], res[mb][nb][i]));
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (EXACT)
+              res[mb][nb][i] = fmaf(sv, d[mb][nb][i], res[mb][nb][i]);
+            else
+              res[mb][nb][i] = fmaf(sv, d[mb][nb][i],
+                                    fmaf(bv, xsum[buf][16 * mb + 4 * kb + i], res[mb][nb][i]));
+          }
         }
       }
     }
@@ -540,11 +580,15 @@ __global__ __launch_bounds__(WG) void k_moe_mfma(
       const int m = 16 * mb + 4 * kb + i;
       if (m < cnt) {
         if constexpr (GATEUP) {
-          const int n = blockIdx.x * COLS + 16 * wave + ln;
-          const float v = ev ? silu(res[mb][0][i]) * res[mb][1][i] : __builtin_nanf("");
-          act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
+#pragma unroll
+          for (int nb = 0; nb < NB / 2; ++nb) {
+            const int n = blockIdx.x * COLS + 16 * (NB / 2) * wave + 16 * nb + ln;
+            const float v =
+                ev ? silu(res[mb][nb][i]) * res[mb][nb + NB / 2][i] : __builtin_nanf("");
+            act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
+          }
         } else {
-          const int64_t o = (int64_t)perm[pos0 + m] * w.N + blockIdx.x * COLS + 32 * wave + ln;
+          const int64_t o = (int64_t)perm[pos0 + m] * w.N + blockIdx.x * COLS + 16 * NB * wave + ln;
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) ys[o + 16 * nb] = ev ? res[mb][nb][i] : __builtin_nanf("");
         }
@@ -553,16 +597,159 @@ __global__ __launch_bounds__(WG) void k_moe_mfma(
   }
 }
 
+// Small entries (<= 16 tokens: one m-block) take k_moe_mfma_s: the same
+// contraction and corrections, but each lane loads its own A words straight
+// from global memory (16 bytes per MFMA step, the 4 waves of a workgroup hit
+// the same L1 lines), so there is no LDS staging and no barrier, and the
+// weights and activations of the next two superchunks are in flight while one
+// is multiplied (a three-slot register ring, unrolled so every slot index is
+// static).
+template <int XT, int ST, int NB> struct MfSlot {
+  Chunk w[NB];
+  u32x4 a[4];
+};
+
+template <int XT, int ST, bool GATEUP, int NB>
+__global__ __launch_bounds__(WG) void k_moe_mfma_s(
+    const uint16_t* __restrict__ src, int topk, const int4* __restrict__ entries,
+    const int* __restrict__ n_entries, const int32_t* __restrict__ perm, QW w, int I,
+    uint16_t* __restrict__ act, float* __restrict__ ys) {
+  constexpr bool EXACT = XT == I4_F16;
+  constexpr int COLS = GATEUP ? 32 * NB : 64 * NB;
+  static_assert(!GATEUP || NB % 2 == 0, "gate_up pairs gate and up blocks");
+  if ((int)blockIdx.y >= *n_entries) return;
+  const int4 en = entries[blockIdx.y];
+  const int e = en.x, pos0 = en.y, cnt = en.z;
+  const int K = w.K, SC = K >> 7;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ln = lane & 15, kb = lane >> 4;
+  const bool ev = (unsigned)e < (unsigned)w.E;
+  const int ee = ev ? e : 0;
+  RowPtr rp[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    int row;
+    if constexpr (GATEUP)
+      row = blockIdx.x * COLS + 16 * (NB / 2) * wave + 16 * (nb % (NB / 2)) + ln +
+            (nb >= NB / 2 ? I : 0);
+    else
+      row = blockIdx.x * COLS + 16 * NB * wave + 16 * nb + ln;
+    rp[nb] = row_ptr<ST>(w, ee, row);
+  }
+  // A row of this lane: token ln of the entry (clamped; rows >= cnt are not stored)
+  const uint16_t* xrow;
+  if constexpr (GATEUP) xrow = src + (int64_t)(perm[pos0 + min(ln, cnt - 1)] / topk) * K;
+  else xrow = src + (int64_t)(pos0 + min(ln, cnt - 1)) * K;
+  xrow += 32 * kb;
+
+  using Slot = MfSlot<XT, ST, NB>;
+  // unconditional (past the end it reloads the last superchunk, an L2 hit), so
+  // that the number of loads in flight is the same on every path and the
+  // waits before each slot's use stay partial
+  auto issue = [&](int sc, Slot& sl) {
+    sc = min(sc, SC - 1);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) sl.w[nb] = load_chunk<ST>(rp[nb], 4 * sc + kb, w.gshift);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) sl.a[t] = ldg16(xrow + 128 * sc + 8 * t);
+  };
+  f32x4 res[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) res[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int sc, const Slot& sl) {
+    const int g = (4 * sc + kb) >> w.gshift;
+    f32x4 d[NB];
+    u32 nz[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      d[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      nz[nb] = (0xE400u | ((sl.w[nb].z >> (4 * (g & 7))) & 15u)) * 0x00010001u;
+    }
+    float sm = 0.f;  // bf16: this lane's part of the activation sum of token ln
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u32x4 a = pair_order(sl.a[t]);
+      if constexpr (!EXACT) sm += sum8<XT>(sl.a[t]).y;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const u32x4 cw = sl.w[nb].w;
+        u32x4 b = decode8<XT>(t == 0 ? cw.x : t == 1 ? cw.y : t == 2 ? cw.z : cw.w);
+        if constexpr (EXACT) {
+          b.x = sub_zero(b.x, nz[nb]);
+          b.y = sub_zero(b.y, nz[nb]);
+          b.z = sub_zero(b.z, nz[nb]);
+          b.w = sub_zero(b.w, nz[nb]);
+        }
+        d[nb] = mfma16<XT>(a, b, d[nb]);
+      }
+    }
+    // S_m for the rows this lane holds (m = 4 kb + i): total over the 4 lane
+    // groups of lane m, gathered with bpermute
+    float sr[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (!EXACT) {
+      float tot = sm;
+      tot += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((lane + 16) & 63) << 2, __builtin_bit_cast(int, sm)));
+      tot += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((lane + 32) & 63) << 2, __builtin_bit_cast(int, sm)));
+      tot += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((lane + 48) & 63) << 2, __builtin_bit_cast(int, sm)));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sr[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((4 * kb + i) << 2, __builtin_bit_cast(int, tot)));
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const float sv = scale_from_raw<ST>(sl.w[nb].s);
+      float bv = 0.f;
+      if constexpr (!EXACT)
+        bv = -sv * (Half<XT>::MAGIC + (float)((sl.w[nb].z >> (4 * (g & 7))) & 15u));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (EXACT) res[nb][i] = fmaf(sv, d[nb][i], res[nb][i]);
+        else res[nb][i] = fmaf(sv, d[nb][i], fmaf(bv, sr[i], res[nb][i]));
+      }
+    }
+  };
+  Slot s0, s1, s2;
+  issue(0, s0);
+  issue(1, s1);
+  issue(2, s2);
+  for (int sc = 0; sc < SC; sc += 3) {
+    compute(sc, s0);
+    issue(sc + 3, s0);
+    if (sc + 1 < SC) compute(sc + 1, s1);
+    issue(sc + 4, s1);
+    if (sc + 2 < SC) compute(sc + 2, s2);
+    issue(sc + 5, s2);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 4 * kb + i;
+    if (m < cnt) {
+      if constexpr (GATEUP) {
+#pragma unroll
+        for (int nb = 0; nb < NB / 2; ++nb) {
+          const int n = blockIdx.x * COLS + 16 * (NB / 2) * wave + 16 * nb + ln;
+          const float v = ev ? silu(res[nb][i]) * res[nb + NB / 2][i] : __builtin_nanf("");
+          act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
+        }
+      } else {
+        const int64_t o = (int64_t)perm[pos0 + m] * w.N + blockIdx.x * COLS + 16 * NB * wave + ln;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) ys[o + 16 * nb] = ev ? res[nb][i] : __builtin_nanf("");
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Sort (token, slot) pairs by expert, stable in token order, and cut them
-// into entries: experts with >= mf_min tokens get MFMA entries of <= MF_TOK
-// tokens, the others GEMV entries of <= MT_LIST.  One workgroup of 1024
-// threads (E <= 1024):
+// into two lists: experts with <= lo_max tokens get entries of <= lo_chunk
+// tokens in `entries`, the others entries of <= MF_TOK tokens in
+// `mf_entries`.  One workgroup of 1024 threads (E <= 1024):
 //   bits[e][w]: bit b set <=> token 32w + b selected expert e
 //   pre [e][w]: popcount of bits[e][0..w)
 // and thread e owns expert e for the three exclusive prefix sums (tokens,
-// GEMV entries, MFMA entries), done as wave scans plus a scan of the wave
-// totals.
+// first-list entries, second-list entries), done as wave scans plus a scan of
+// the wave totals.
 __device__ inline int wave_incl_scan(int v) {
   const int lane = __lane_id();
 #pragma unroll
@@ -574,7 +761,7 @@ __device__ inline int wave_incl_scan(int v) {
 }
 
 __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel, int T, int topk,
-                                                int E, int mf_min,
+                                                int E, int lo_max, int lo_chunk,
                                                 int32_t* __restrict__ perm,
                                                 int4* __restrict__ entries,
                                                 int* __restrict__ n_entries,
@@ -600,8 +787,8 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
       c += __popc(bits[tid * TW + wd]);
     }
   }
-  const bool big = c >= mf_min;
-  const int ne = big ? 0 : (c + MT_LIST - 1) / MT_LIST;
+  const bool big = c > lo_max;
+  const int ne = big ? 0 : (c + lo_chunk - 1) / lo_chunk;
   const int nm = big ? (c + MF_TOK - 1) / MF_TOK : 0;
   const int ic = wave_incl_scan(c), ie = wave_incl_scan(ne), im = wave_incl_scan(nm);
   if (lane == 63) {
@@ -638,7 +825,7 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
         mf_entries[moff + q] = int4{tid, off + q * MF_TOK, min(MF_TOK, c - q * MF_TOK), 0};
     } else {
       for (int q = 0; q < ne; ++q)
-        entries[eoff + q] = int4{tid, off + q * MT_LIST, min(MT_LIST, c - q * MT_LIST), 0};
+        entries[eoff + q] = int4{tid, off + q * lo_chunk, min(lo_chunk, c - q * lo_chunk), 0};
     }
   }
 }
@@ -687,7 +874,7 @@ MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
   m.perm = (int32_t*)take(Tk * 4);
   m.entries = (int4*)take((E + Tk) * sizeof(int4));
   m.n_entries = (int*)take(4);
-  m.mf_entries = (int4*)take((E + Tk / MF_MIN + 1) * sizeof(int4));
+  m.mf_entries = (int4*)take((E + Tk / MF_TOK + 1) * sizeof(int4));
   m.n_mf_entries = (int*)take(4);
   m.bytes = o;
   return m;
@@ -821,13 +1008,18 @@ struct MoeOps {
                       int, void*, hipStream_t);
   int (*mfma_down)(int, const void*, const int4*, const int*, const int32_t*, const QW&, float*,
                    hipStream_t);
+  int (*mfma_gate_up_s)(int, const void*, int, const int4*, const int*, const int32_t*, const QW&,
+                        int, void*, hipStream_t);
+  int (*mfma_down_s)(int, const void*, const int4*, const int*, const int32_t*, const QW&, float*,
+                     hipStream_t);
 };
 
 template <int XT, int ST>
 int launch_mfma_gate_up_t(int max_entries, const void* x, int topk, const int4* ent,
                           const int* nent, const int32_t* perm, const QW& w, int I, void* act,
                           hipStream_t s) {
-  hipLaunchKernelGGL((k_moe_mfma<XT, ST, true>), dim3(I / 64, max_entries), dim3(WG), 0, s,
+  hipLaunchKernelGGL((k_moe_mfma<XT, ST, true, MF_NB>), dim3(I / (32 * MF_NB), max_entries),
+                     dim3(WG), 0, s,
                      (const uint16_t*)x, topk, ent, nent, perm, w, I, (uint16_t*)act,
                      (float*)nullptr);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
@@ -836,15 +1028,36 @@ int launch_mfma_gate_up_t(int max_entries, const void* x, int topk, const int4* 
 template <int XT, int ST>
 int launch_mfma_down_t(int max_entries, const void* act, const int4* ent, const int* nent,
                        const int32_t* perm, const QW& w, float* ys, hipStream_t s) {
-  hipLaunchKernelGGL((k_moe_mfma<XT, ST, false>), dim3(w.N / 128, max_entries), dim3(WG), 0, s,
+  hipLaunchKernelGGL((k_moe_mfma<XT, ST, false, MF_NB>), dim3(w.N / (64 * MF_NB), max_entries),
+                     dim3(WG), 0, s,
                      (const uint16_t*)act, 0, ent, nent, perm, w, 0, (uint16_t*)nullptr, ys);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+template <int XT, int ST>
+int launch_mfma_gate_up_s_t(int max_entries, const void* x, int topk, const int4* ent,
+                            const int* nent, const int32_t* perm, const QW& w, int I, void* act,
+                            hipStream_t s) {
+  hipLaunchKernelGGL((k_moe_mfma_s<XT, ST, true, MF_NB>), dim3(I / (32 * MF_NB), max_entries),
+                     dim3(WG), 0, s, (const uint16_t*)x, topk, ent, nent, perm, w, I,
+                     (uint16_t*)act, (float*)nullptr);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+template <int XT, int ST>
+int launch_mfma_down_s_t(int max_entries, const void* act, const int4* ent, const int* nent,
+                         const int32_t* perm, const QW& w, float* ys, hipStream_t s) {
+  hipLaunchKernelGGL((k_moe_mfma_s<XT, ST, false, MF_NB>), dim3(w.N / (64 * MF_NB), max_entries),
+                     dim3(WG), 0, s, (const uint16_t*)act, 0, ent, nent, perm, w, 0,
+                     (uint16_t*)nullptr, ys);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
   return MoeOps{&launch_gate_up_dt<XT, ST>, &launch_down_m1_t<XT, ST>,
                 &launch_down_list_t<XT, ST>, &launch_mfma_gate_up_t<XT, ST>,
-                &launch_mfma_down_t<XT, ST>};
+                &launch_mfma_down_t<XT, ST>, &launch_mfma_gate_up_s_t<XT, ST>,
+                &launch_mfma_down_s_t<XT, ST>};
 }
 
 bool pick_ops(int xt, int gst, int dst, MoeOps* ops) {
@@ -913,28 +1126,35 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   if (rc) return rc;
   const int Tk = T * topk;
   const int TW = (T + 31) / 32;
-  // experts with >= MF_MIN tokens go to the MFMA tile kernels (G = 128 weights)
-  const bool mfma = gu.group == 128 && dn.group == 128 && I % 128 == 0 && H % 128 == 0;
+  // G = 128 weights take the MFMA kernels: experts with <= MF_SMALL tokens
+  // (one m-block) k_moe_mfma_s, the others k_moe_mfma in entries of <= MF_TOK.
+  // Other group sizes take the dot2 GEMV list kernels (entries of <= MT_LIST).
+  const bool mfma = gu.group == 128 && dn.group == 128 && I % (32 * MF_NB) == 0 &&
+                    H % (64 * MF_NB) == 0;
   const size_t glds = (size_t)2 * E * TW * 4 + (size_t)E * 4;
   hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E,
-                     mfma ? MF_MIN : 0x7fffffff, ws.perm, ws.entries, ws.n_entries, ws.mf_entries,
-                     ws.n_mf_entries);
+                     mfma ? MF_SMALL : 0x7fffffff, mfma ? MF_SMALL : MT_LIST, ws.perm, ws.entries,
+                     ws.n_entries, ws.mf_entries, ws.n_mf_entries);
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
-  const int max_entries = (E < Tk ? E : Tk) + Tk / MT_LIST;
-  const GateUpArgs a{GU_LIST, max_entries, topk, E, renorm, x, sel, nullptr, wts,
-                     ws.entries, ws.n_entries, ws.perm, ws.act};
-  rc = ops.gate_up(a, qgu, I, s);
-  if (rc) return rc;
-  const int max_mf = (E < Tk / MF_MIN ? E : Tk / MF_MIN) + Tk / MF_TOK + 1;
   if (mfma) {
-    rc = ops.mfma_gate_up(max_mf, x, topk, ws.mf_entries, ws.n_mf_entries, ws.perm, qgu, I, ws.act,
+    const int max_s = E < Tk ? E : Tk;                                    // one per expert
+    const int max_b = (E < Tk / (MF_SMALL + 1) ? E : Tk / (MF_SMALL + 1)) + Tk / MF_TOK + 1;
+    rc = ops.mfma_gate_up_s(max_s, x, topk, ws.entries, ws.n_entries, ws.perm, qgu, I, ws.act, s);
+    if (rc) return rc;
+    rc = ops.mfma_gate_up(max_b, x, topk, ws.mf_entries, ws.n_mf_entries, ws.perm, qgu, I, ws.act,
                           s);
     if (rc) return rc;
-  }
-  rc = ops.down_list(max_entries, ws.act, ws.entries, ws.n_entries, ws.perm, qdn, ws.ys, s);
-  if (rc) return rc;
-  if (mfma) {
-    rc = ops.mfma_down(max_mf, ws.act, ws.mf_entries, ws.n_mf_entries, ws.perm, qdn, ws.ys, s);
+    rc = ops.mfma_down_s(max_s, ws.act, ws.entries, ws.n_entries, ws.perm, qdn, ws.ys, s);
+    if (rc) return rc;
+    rc = ops.mfma_down(max_b, ws.act, ws.mf_entries, ws.n_mf_entries, ws.perm, qdn, ws.ys, s);
+    if (rc) return rc;
+  } else {
+    const int max_entries = (E < Tk ? E : Tk) + Tk / MT_LIST;
+    const GateUpArgs a{GU_LIST, max_entries, topk, E, renorm, x, sel, nullptr, wts,
+                       ws.entries, ws.n_entries, ws.perm, ws.act};
+    rc = ops.gate_up(a, qgu, I, s);
+    if (rc) return rc;
+    rc = ops.down_list(max_entries, ws.act, ws.entries, ws.n_entries, ws.perm, qdn, ws.ys, s);
     if (rc) return rc;
   }
   const int64_t tot = (int64_t)T * H;
