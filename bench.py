@@ -305,12 +305,13 @@ def main() -> int:
 
             def run_T(i, T=T, xT=xT, lgT=lgT, wsT=wsT):
                 m = mods[i % len(mods)]
+                tiles = dict(gate_up_tile=m.gate_up_tile, down_tile=m.down_tile)
                 if lgT is None:
                     ops.moe_forward(xT[i % 4], m.gate_up, m.down, TOPK, router_w=m.router_w,
-                                    residual=xT[i % 4], workspace=wsT)
+                                    residual=xT[i % 4], workspace=wsT, **tiles)
                 else:
                     ops.moe_forward(xT[i % 4], m.gate_up, m.down, TOPK, logits=lgT[i % 4],
-                                    residual=xT[i % 4], workspace=wsT)
+                                    residual=xT[i % 4], workspace=wsT, **tiles)
 
             reps = 48
             ms_T, _ = time_stack(torch, run_T, reps, 8)

@@ -38,6 +38,20 @@
  *                             column 8w + {0,2,4,6,1,3,5,7}[i];
  *                      qzeros  [E][NG][N/8] int32, same packing;
  *                      scales  [E][NG][N].
+ *   I4_LAYOUT_TILE -- this library's load-time layout for the MoE kernels (no
+ *                    reference counterpart; built by i4_repack_tile).  The CT
+ *                    words regrouped so that one 16-byte load of lane (row r,
+ *                    k-group j) holds word j of the four 32-column chunks of a
+ *                    128-column superchunk, and one wavefront load is 1 KB of
+ *                    contiguous memory (16 rows x 4 k-groups):
+ *                      packed [E][N/16][K/128][16][4][4] int32, element
+ *                             [e][b][s][r][j][t] = CT word 4 (4s + t) + j of
+ *                             row 16b + r;
+ *                      scale  [E][N/16][NG][16], element [e][b][g][r] = CT
+ *                             scale of row 16b + r, group g;
+ *                      zeros  NULL or [E][N/16][ceil(NG/8)][16] int32, the CT
+ *                             zero words of row 16b + r.
+ *                    Needs N % 16 == 0 and K % 128 == 0.
  */
 #ifndef I4MOE_H
 #define I4MOE_H
@@ -50,7 +64,7 @@
 extern "C" {
 #endif
 
-#define I4_ABI_VERSION 1
+#define I4_ABI_VERSION 2
 
 /* status codes */
 #define I4_OK               0
@@ -70,8 +84,9 @@ extern "C" {
 #define I4_BF16 2
 
 /* packed layouts */
-#define I4_LAYOUT_CT  0
-#define I4_LAYOUT_AWQ 1
+#define I4_LAYOUT_CT   0
+#define I4_LAYOUT_AWQ  1
+#define I4_LAYOUT_TILE 2
 
 /* One stacked int4 weight: E experts of a [N][K] matrix.  E = 1 is a plain
  * Linear.  *_estride are element strides between experts; 0 means densely
@@ -91,8 +106,13 @@ typedef struct i4_qweight {
   int32_t        E, N, K;
 } i4_qweight;
 
-/* One Thinker MoE block in the internal (CT) layout, as FusedPackedMoE stores
- * it (src/duplex/streaming/fused_packed_moe.py:112,117-122,166-169). */
+/* One Thinker MoE block, as FusedPackedMoE stores it
+ * (src/duplex/streaming/fused_packed_moe.py:112,117-122,166-169).
+ * gate_up / down are in I4_LAYOUT_CT (the decode kernels read whole rows) or
+ * I4_LAYOUT_TILE; gate_up_tile / down_tile are optional tile copies of the
+ * same weights (packed == NULL: absent) for the T > 1 MFMA kernels, which read
+ * tiles only.  T = 1 uses gate_up / down; T > 1 uses the tile copies, or
+ * gate_up / down when those are tiles (else I4_ERR_LAYOUT). */
 typedef struct i4_moe_weights {
   i4_qweight  gate_up;    /* [E][2I][H]: rows [0,I) gate_proj, [I,2I) up_proj */
   i4_qweight  down;       /* [E][H][I]                                       */
@@ -106,6 +126,8 @@ typedef struct i4_moe_weights {
                              while the residual stays the un-normalised input.
                              Requires router_w.                               */
   float       norm_eps;
+  i4_qweight  gate_up_tile;
+  i4_qweight  down_tile;
 } i4_moe_weights;
 
 int         i4_abi_version(void);
@@ -152,6 +174,16 @@ int    i4_repack_awq_to_ct(const i4_qweight* src, int32_t* dst_packed, void* dst
                            int32_t* dst_zeros, int dst_rows, int row_offset,
                            hipStream_t stream);
 
+/* Load-time repack of a CT or AWQ weight into I4_LAYOUT_TILE (no reference
+ * counterpart: it replaces the stacking of _stack_packed,
+ * fused_packed_moe.py:68-80, for the MoE kernels).  Expert e of src goes to
+ * rows [row_offset, row_offset + src->N) of a destination with dst_rows rows
+ * per expert (dst_rows and row_offset multiples of 16, so gate and up can be
+ * concatenated); dst_scale is in src->scale_dtype.  dst_zeros may be NULL only
+ * when src has no zeros (the symmetric zero point 8 is then implied). */
+int    i4_repack_tile(const i4_qweight* src, int32_t* dst_packed, void* dst_scale,
+                      int32_t* dst_zeros, int dst_rows, int row_offset, hipStream_t stream);
+
 /* Router half of FusedPackedMoE.forward (fused_packed_moe.py:195):
  *   logits[t][e] = sum_h xn[t][h] * router_w[e][h], fp32 accumulation,
  * rounded to x_dtype like the reference's half-precision gate Linear.
@@ -177,15 +209,14 @@ int    i4_route_topk(const void* logits, int logits_dtype, int T, int E, int top
  * NULL.  The activation is rounded to x_dtype between the two projections as
  * in the reference (fused_packed_moe.py:257); everything else is fp32 and the
  * output is rounded once to x_dtype.  sel_out / w_out (nullable) receive the
- * routing.  Both weights must be in the CT layout. */
+ * routing. */
 int    i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weights,
                       int topk, int renorm, const void* logits, const void* residual,
                       void* out, int32_t* sel_out, float* w_out,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
-/* Workspace of i4_moe_forward.  Its bytes must be zero before the first call
- * that uses it (e.g. hipMemset once at allocation); every call leaves the
- * small handoff-counter region zero again, so no per-call clearing is needed.
- * Calls that share one workspace must not overlap. */
+/* Workspace of i4_moe_forward (scratch for logits, routing, expert lists and
+ * intermediate activations; no state is kept between calls).  Calls that
+ * share one workspace must not overlap. */
 size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
 
 /* The two expert stages of one decode token with routing already known --
@@ -194,7 +225,8 @@ size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
  *                        rounded to x_dtype (fused_packed_moe.py:255-257);
  *   i4_moe_down_combine: out = residual + sum_j w[j] * down_{sel[j]}(act[j])
  *                        (fused_packed_moe.py:261-262), fixed j order.
- * x, residual and out are [H]; act is [topk][I]; sel [topk]; w [topk] fp32. */
+ * x, residual and out are [H]; act is [topk][I]; sel [topk]; w [topk] fp32.
+ * The weights are in I4_LAYOUT_CT or I4_LAYOUT_TILE. */
 int    i4_moe_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up,
                       const int32_t* sel, int topk, void* act, hipStream_t stream);
 /* Routing (fused_packed_moe.py:195-199) and the gate_up stage of one decode

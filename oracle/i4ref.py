@@ -145,6 +145,43 @@ def awq_to_ct(qweight, qzeros, scales, group):
 
 
 # ---------------------------------------------------------------------------
+# The library's tile layout (I4_LAYOUT_TILE in include/i4moe.h).  No reference
+# counterpart: a permutation of the CT words, pinned by its closed form
+# (test_tile_index_closed_form) and its round trip.
+def tile_pack(packed, scale, zeros=None):
+    """CT (packed [E, N, K/8], scale [E, N, NG], zeros [E, N, NZW] or None) -> tile.
+
+    packed -> [E, N/16, K/128, 16, 16]: element [e, b, s, r, 4j + t] is CT word
+    4 (4s + t) + j of row 16b + r; scale -> [E, N/16, NG, 16]; zeros ->
+    [E, N/16, NZW, 16] (element [e, b, g, r] = CT element [e, 16b + r, g]).
+    """
+    p = np.asarray(packed)
+    E, N, KW = p.shape
+    SC = KW // 16
+    t = p.reshape(E, N // 16, 16, SC, 4, 4)            # [e, b, r, s, t, j]
+    t = t.transpose(0, 1, 3, 2, 5, 4).reshape(E, N // 16, SC, 16, 16)
+
+    def rows(a):
+        a = np.asarray(a)
+        return a.reshape(E, N // 16, 16, a.shape[-1]).transpose(0, 1, 3, 2).copy()
+
+    return t.copy(), rows(scale), None if zeros is None else rows(zeros)
+
+
+def tile_unpack(packed, scale, zeros=None):
+    """Inverse of tile_pack: tile -> CT."""
+    p = np.asarray(packed)
+    E, NB, SC = p.shape[:3]
+    c = p.reshape(E, NB, SC, 16, 4, 4).transpose(0, 1, 3, 2, 5, 4).reshape(E, NB * 16, SC * 16)
+
+    def rows(a):
+        a = np.asarray(a)
+        return a.transpose(0, 1, 3, 2).reshape(E, NB * 16, a.shape[2]).copy()
+
+    return c.copy(), rows(scale), None if zeros is None else rows(zeros)
+
+
+# ---------------------------------------------------------------------------
 # GEMV: _dq_gemv_kernel / dequant_gemv / reference_gemv
 # (triton_dequant_gemv.py:43-82, 85-113, 116-122)
 def dq_gemv(x, W, sel) -> np.ndarray:

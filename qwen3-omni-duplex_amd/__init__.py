@@ -15,12 +15,12 @@ from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_forward, moe_gate_up,
                   moe_route_gate_up, moe_stack, route, router_logits, unpack4, unpack_nibbles,
                   Workspace)
-from .weights import QWeight, repack_awq_to_ct
+from .weights import QWeight, repack_awq_to_ct, repack_tile
 
 lib = _lib.lib
 
 __all__ = [
-    "QWeight", "repack_awq_to_ct", "dequant_gemv", "linear", "unpack4", "unpack_nibbles",
+    "QWeight", "repack_awq_to_ct", "repack_tile", "dequant_gemv", "linear", "unpack4", "unpack_nibbles",
     "dequant", "router_logits", "route", "moe_forward", "moe_gate_up", "moe_route_gate_up",
     "moe_down_combine",
     "moe_stack", "Workspace",

@@ -14,12 +14,12 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libi4moe.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # element types and layouts (include/i4moe.h)
 F32, F16, BF16 = 0, 1, 2
-LAYOUT_CT, LAYOUT_AWQ = 0, 1
-LAYOUTS = {"ct": LAYOUT_CT, "awq": LAYOUT_AWQ}
+LAYOUT_CT, LAYOUT_AWQ, LAYOUT_TILE = 0, 1, 2
+LAYOUTS = {"ct": LAYOUT_CT, "awq": LAYOUT_AWQ, "tile": LAYOUT_TILE}
 
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -47,7 +47,8 @@ class MoeWeightsC(ctypes.Structure):
     """struct i4_moe_weights"""
 
     _fields_ = [("gate_up", QWeightC), ("down", QWeightC), ("router_w", c_void_p),
-                ("norm_w", c_void_p), ("norm_eps", ctypes.c_float)]
+                ("norm_w", c_void_p), ("norm_eps", ctypes.c_float),
+                ("gate_up_tile", QWeightC), ("down_tile", QWeightC)]
 
 
 # name -> (restype, argtypes); every function declared in include/i4moe.h
@@ -64,6 +65,8 @@ SIGNATURES = {
     "i4_dequant": (c_int, [POINTER(QWeightC), c_void_p, c_int, c_void_p]),
     "i4_repack_awq_to_ct": (c_int, [POINTER(QWeightC), c_void_p, c_void_p, c_void_p, c_int, c_int,
                                     c_void_p]),
+    "i4_repack_tile": (c_int, [POINTER(QWeightC), c_void_p, c_void_p, c_void_p, c_int, c_int,
+                               c_void_p]),
     "i4_router_logits": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p,
                                  ctypes.c_float, c_void_p, c_void_p, c_void_p]),
     "i4_route_topk": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,

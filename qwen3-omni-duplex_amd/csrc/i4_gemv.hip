@@ -230,7 +230,19 @@ __device__ inline void nib_and_zero(const WView& w, int e, int n, int k, int& q,
                                     float& s) {
   const int NG = (w.K + w.group - 1) / w.group;
   const int g = k / w.group;
-  if (w.layout == I4_LAYOUT_CT) {
+  if (w.layout == I4_LAYOUT_TILE) {
+    const int SC = w.K >> 7, NZW = (NG + 7) >> 3, b = n >> 4, r = n & 15, c = k >> 5;
+    const u32 word = (u32)w.packed[e * w.pes + (((int64_t)b * SC + (c >> 2)) * 16 + r) * 16 +
+                                   ((k >> 3) & 3) * 4 + (c & 3)];
+    q = (word >> (4 * (k & 7))) & 15;
+    z = w.zeros ? ((u32)w.zeros[e * w.zes + ((int64_t)b * NZW + (g >> 3)) * 16 + r] >>
+                   (4 * (g & 7))) & 15
+                : 8;
+    const int64_t si = e * w.ses + ((int64_t)b * NG + g) * 16 + r;
+    s = w.st == I4_F32 ? load_scale<I4_F32>(w.scale, si)
+      : w.st == I4_F16 ? load_scale<I4_F16>(w.scale, si)
+                       : load_scale<I4_BF16>(w.scale, si);
+  } else if (w.layout == I4_LAYOUT_CT) {
     const u32 word = (u32)w.packed[e * w.pes + (int64_t)n * (w.K >> 3) + (k >> 3)];
     q = (word >> (4 * (k & 7))) & 15;
     if (w.zeros) {
@@ -335,6 +347,63 @@ __global__ __launch_bounds__(WG) void k_repack_awq(WView w, int32_t* __restrict_
   }
 }
 
+// CT or AWQ -> TILE, one thread per destination-ordered source item: the
+// CT word m of (e, n), then the scales and the zero words of (e, n).
+__global__ __launch_bounds__(WG) void k_repack_tile(WView w, int32_t* __restrict__ dp,
+                                                    void* __restrict__ ds,
+                                                    int32_t* __restrict__ dz, int dst_rows,
+                                                    int row_off) {
+  const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
+  const int KW = w.K >> 3, SC = w.K >> 7;
+  const int NG = (w.K + w.group - 1) / w.group, NZW = (NG + 7) >> 3;
+  const int DB = dst_rows >> 4;  // destination row blocks per expert
+  const int64_t tot_w = (int64_t)w.E * w.N * KW;
+  const int64_t tot_s = (int64_t)w.E * w.N * NG;
+  const int64_t tot_z = dz ? (int64_t)w.E * w.N * NZW : 0;
+  if (i < tot_w) {
+    const int m = (int)(i % KW);
+    const int64_t en = i / KW;
+    const int n = (int)(en % w.N), e = (int)(en / w.N);
+    u32 word = 0;
+    for (int b = 0; b < 8; ++b) {
+      int q, z;
+      float s;
+      nib_and_zero(w, e, n, 8 * m + b, q, z, s);
+      word |= (u32)q << (4 * b);
+    }
+    const int dn = row_off + n, c = m >> 2, j = m & 3;
+    dp[((((int64_t)e * DB + (dn >> 4)) * SC + (c >> 2)) * 16 + (dn & 15)) * 16 + j * 4 + (c & 3)] =
+        (int32_t)word;
+  } else if (i < tot_w + tot_s) {
+    const int64_t r = i - tot_w;
+    const int g = (int)(r % NG);
+    const int64_t en = r / NG;
+    const int n = (int)(en % w.N), e = (int)(en / w.N);
+    const int64_t src = w.layout == I4_LAYOUT_AWQ ? e * w.ses + (int64_t)g * w.N + n
+                                                  : e * w.ses + (int64_t)n * NG + g;
+    const int dn = row_off + n;
+    const int64_t dst = (((int64_t)e * DB + (dn >> 4)) * NG + g) * 16 + (dn & 15);
+    if (w.st == I4_F32) ((float*)ds)[dst] = ((const float*)w.scale)[src];
+    else ((uint16_t*)ds)[dst] = ((const uint16_t*)w.scale)[src];
+  } else if (i < tot_w + tot_s + tot_z) {
+    const int64_t r = i - tot_w - tot_s;
+    const int zw = (int)(r % NZW);
+    const int64_t en = r / NZW;
+    const int n = (int)(en % w.N), e = (int)(en / w.N);
+    u32 word = 0;
+    for (int b = 0; b < 8; ++b) {
+      const int g = 8 * zw + b;
+      if (g >= NG) break;
+      int q, z;
+      float s;
+      nib_and_zero(w, e, n, g * w.group, q, z, s);
+      word |= (u32)z << (4 * b);
+    }
+    const int dn = row_off + n;
+    dz[(((int64_t)e * DB + (dn >> 4)) * NZW + zw) * 16 + (dn & 15)] = (int32_t)word;
+  }
+}
+
 }  // namespace i4
 
 // ===========================================================================
@@ -358,9 +427,9 @@ inline int64_t scale_ng(const i4_qweight* w) { return (w->K + w->group - 1) / w-
 
 inline int64_t dense_pes(const i4_qweight* w) { return (int64_t)w->N * w->K / 8; }
 inline int64_t dense_ses(const i4_qweight* w) { return (int64_t)w->N * scale_ng(w); }
-inline int64_t dense_zes(const i4_qweight* w) {
-  return w->layout == I4_LAYOUT_CT ? (int64_t)w->N * ((scale_ng(w) + 7) / 8)
-                                   : scale_ng(w) * (w->N / 8);
+inline int64_t dense_zes(const i4_qweight* w) {  // CT and TILE hold the same words
+  return w->layout == I4_LAYOUT_AWQ ? scale_ng(w) * (w->N / 8)
+                                    : (int64_t)w->N * ((scale_ng(w) + 7) / 8);
 }
 
 inline int awq_split_rows(const i4_qweight* w) {
@@ -376,11 +445,13 @@ inline int awq_split_rows(const i4_qweight* w) {
 // validate an i4_qweight; fills dense strides when they are 0
 int i4_check_weight(const i4_qweight* w, i4_qweight* norm) {
   if (!w || !w->packed || !w->scale) return I4_ERR_NULL;
-  if (w->layout != I4_LAYOUT_CT && w->layout != I4_LAYOUT_AWQ) return I4_ERR_LAYOUT;
+  if (w->layout != I4_LAYOUT_CT && w->layout != I4_LAYOUT_AWQ && w->layout != I4_LAYOUT_TILE)
+    return I4_ERR_LAYOUT;
   if (!any_dt(w->scale_dtype)) return I4_ERR_DTYPE;
   if (w->E < 1 || w->N < 1 || w->K < 32) return I4_ERR_SHAPE;
   if (w->K % 32 != 0 || w->K > 16384) return I4_ERR_SHAPE;
   if (w->layout == I4_LAYOUT_AWQ && w->N % 8 != 0) return I4_ERR_SHAPE;
+  if (w->layout == I4_LAYOUT_TILE && (w->N % 16 != 0 || w->K % 128 != 0)) return I4_ERR_SHAPE;
   if (w->group < 32 || (w->group & (w->group - 1)) != 0) return I4_ERR_GROUP;
   if (!al16(w->packed)) return I4_ERR_ALIGN;
   *norm = *w;
@@ -475,6 +546,7 @@ int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w
   if (k_sel < 1 || k_sel > 65535 || x_stride < 0) return I4_ERR_SHAPE;
   if (x_stride != 0 && x_stride < nw.K) return I4_ERR_STRIDE;
   if (!al16(x) || (x_stride * 2) % 16 != 0) return I4_ERR_ALIGN;
+  if (nw.layout == I4_LAYOUT_TILE) return I4_ERR_LAYOUT;  // the MoE kernels' layout
   if (nw.layout == I4_LAYOUT_CT)
     return i4_launch_gemv_ct(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr,
                              stream);
@@ -495,6 +567,7 @@ int i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w, const void
   if (!half_dt(x_dtype) || !any_dt(y_dtype)) return I4_ERR_DTYPE;
   if (M < 1 || M > 65535) return I4_ERR_SHAPE;
   if (!al16(x)) return I4_ERR_ALIGN;
+  if (nw.layout == I4_LAYOUT_TILE) return I4_ERR_LAYOUT;
   nw.E = 1;
   if (nw.layout == I4_LAYOUT_CT)
     return i4_launch_gemv_ct(x, x_dtype, nw.K, &nw, nullptr, M, y, y_dtype, bias, stream);
@@ -553,6 +626,24 @@ int i4_repack_awq_to_ct(const i4_qweight* src, int32_t* dst_packed, void* dst_sc
   const int NG = (nw.K + nw.group - 1) / nw.group;
   const int64_t total = (int64_t)nw.E * nw.N * (nw.K / 8 + NG + (NG + 7) / 8);
   hipLaunchKernelGGL(k_repack_awq, dim3((unsigned)((total + WG - 1) / WG)), dim3(WG), 0, stream,
+                     make_view(nw), dst_packed, dst_scale, dst_zeros, dst_rows, row_offset);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+int i4_repack_tile(const i4_qweight* src, int32_t* dst_packed, void* dst_scale,
+                   int32_t* dst_zeros, int dst_rows, int row_offset, hipStream_t stream) {
+  i4_qweight nw;
+  int rc = i4_check_weight(src, &nw);
+  if (rc) return rc;
+  if (nw.layout == I4_LAYOUT_TILE) return I4_ERR_LAYOUT;
+  if (!dst_packed || !dst_scale || (nw.zeros && !dst_zeros)) return I4_ERR_NULL;
+  if (nw.K % 128 != 0 || dst_rows % 16 != 0 || row_offset % 16 != 0) return I4_ERR_SHAPE;
+  if (row_offset < 0 || dst_rows < row_offset + nw.N) return I4_ERR_SHAPE;
+  if (!al16(dst_packed)) return I4_ERR_ALIGN;
+  const int NG = (nw.K + nw.group - 1) / nw.group;
+  const int64_t total =
+      (int64_t)nw.E * nw.N * (nw.K / 8 + NG + (dst_zeros ? (NG + 7) / 8 : 0));
+  hipLaunchKernelGGL(k_repack_tile, dim3((unsigned)((total + WG - 1) / WG)), dim3(WG), 0, stream,
                      make_view(nw), dst_packed, dst_scale, dst_zeros, dst_rows, row_offset);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }

@@ -1,0 +1,344 @@
+// Decode (T = 1) expert kernels on CT rows (I4_LAYOUT_CT weights), the
+// decode path of i4_moe_forward when the block carries CT weights; the tile
+// kernels of i4_moe_decode.hip serve blocks that only carry the tile copy.
+//
+// Rows are read whole: L lanes share one row and each lane loads 16-byte
+// chunks along it, so a wavefront streams two to eight full rows (the 1 KB
+// rows of the Thinker's gate_up at L = 32).  Decode is latency-bound, and
+// these narrow workgroups (8 row pairs of gate_up, 8 output rows of down)
+// give the most workgroups per layer.
+//   k_ct_gate_up: gate row n and up row I + n of one selected expert in the
+//     same lanes, so silu(g) * u happens in registers and only the half-
+//     precision activation [topk][I] is written (the reference writes fp32
+//     [8][1536] and runs split / silu / mul / cast as separate kernels,
+//     fused_packed_moe.py:255-257).
+//   k_ct_down_m1: a workgroup owns a slice of output rows across ALL selected
+//     experts, so the routing-weighted combine and the residual add happen in
+//     LDS in a fixed slot order: no atomics, bit-reproducible run to run.
+#include "i4_launch.h"
+#include "i4_moe_launch.h"
+#include "i4_topk.h"
+
+namespace i4 {
+
+static constexpr int WG = 256;
+static constexpr size_t kMaxLds = 65536;  // dynamic LDS per workgroup
+enum { GU_SEL = 0, GU_ROUTE = 1 };
+
+struct QW {  // device view of one CT weight
+  const int32_t* packed;
+  const void* scale;
+  const int32_t* zeros;
+  int64_t pes, ses, zes;
+  int gshift, E, N, K;
+};
+
+// row n of expert e (both already clamped to valid values)
+template <int ST> __device__ inline RowPtr row_ptr(const QW& w, int e, int n) {
+  const int C = w.K >> 5, KW = w.K >> 3;
+  const int NG = (C + (1 << w.gshift) - 1) >> w.gshift, NZW = (NG + 7) >> 3;
+  RowPtr r;
+  r.p = w.packed + e * w.pes + (int64_t)n * KW;
+  r.s = scale_at<ST>(w.scale, e * w.ses + (int64_t)n * NG);
+  r.z = w.zeros ? (const u32*)w.zeros + e * w.zes + (int64_t)n * NZW : kSymZeros;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// gate_up + SiLU.  L lanes per row pair (gate row n, up row I + n); a
+// workgroup owns WG/L consecutive row pairs of slot blockIdx.y.
+//   GU_SEL:   experts from sel[]
+//   GU_ROUTE: every wave ranks the E logits itself (top-k + softmax,
+//             bit-identical in every wave) and takes its slot; workgroup
+//             (0, 0) writes sel[] / wts[] for the down projection
+
+template <int XT, int ST, int L, int MODE>
+__global__ __launch_bounds__(WG) void k_ct_gate_up(
+    const uint16_t* __restrict__ x, int topk, int32_t* __restrict__ sel,
+    const uint16_t* __restrict__ logits, int E_r, int renorm, float* __restrict__ wts, QW w,
+    int I, uint16_t* __restrict__ act) {
+  constexpr int MT = 1;
+  extern __shared__ __align__(16) unsigned char lds[];
+  constexpr int RPW = WG / L;
+  constexpr int ROUND = 2;
+  const int H = w.K, C = H >> 5;
+  const int cpl = (C + L - 1) / L;
+  u32x4* xs = (u32x4*)lds;
+  float2* sums = (float2*)(lds + (size_t)MT * H * 2);
+
+  const int pos0 = blockIdx.y, cnt = 1;
+  Stager<XT> st(MT, H);
+  auto row_of = [&](int) -> const uint16_t* { return x; };
+  int e;
+  if constexpr (MODE == GU_ROUTE) {
+    // the logits are the critical path: load them before the activations
+    auto route = [&](auto vpl) -> int {
+      constexpr int VPL = decltype(vpl)::value;
+      u32 raw[VPL];
+      load_row<XT, VPL>(logits, 0, E_r, raw);
+      st.issue(row_of, 0);
+      if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
+        int my_sel = 0;
+        float my_w = 0.f;
+        topk_row<XT, VPL>(raw, 0, E_r, topk, renorm, sel, wts, nullptr, 0, &my_sel, &my_w);
+        return __builtin_amdgcn_readlane(my_sel, 0);
+      }
+      return topk_slot<XT, VPL>(raw, E_r, blockIdx.y);
+    };
+    e = E_r <= 128 ? route(std::integral_constant<int, 2>{})
+                   : route(std::integral_constant<int, 8>{});
+  } else {
+    st.issue(row_of, 0);
+    e = sel[blockIdx.y];
+  }
+  const int rl = threadIdx.x / L, cl = threadIdx.x % L;
+  const int n = blockIdx.x * RPW + rl;
+  const bool rv = n < I;
+  const bool ev = (unsigned)e < (unsigned)w.E;
+  const int nn = rv ? n : 0, ee = ev ? e : 0;
+  const RowPtr rg = row_ptr<ST>(w, ee, nn), ru = row_ptr<ST>(w, ee, I + nn);
+
+  float ag[MT], au[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) ag[t] = au[t] = 0.f;
+  Chunk cg[ROUND], cu[ROUND];
+  auto load_round = [&](int r0) {
+#pragma unroll
+    for (int i = 0; i < ROUND; ++i) {
+      const int c = min(cl + (r0 + i) * L, C - 1);
+      cg[i] = load_chunk<ST>(rg, c, w.gshift);
+      cu[i] = load_chunk<ST>(ru, c, w.gshift);
+    }
+  };
+  auto dot_round = [&](int r0) {
+#pragma unroll
+    for (int i = 0; i < ROUND; ++i) {
+      const int c = cl + (r0 + i) * L;
+      if (c < C) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if (t < cnt) {
+            const u32x4* xt = xs + (size_t)t * 4 * C;
+            const u32x4 x0 = xt[c], x1 = xt[C + c], x2 = xt[2 * C + c], x3 = xt[3 * C + c];
+            const float2 sm = sums[t * C + c];
+            ag[t] += chunk_dot<XT, ST>(cg[i], x0, x1, x2, x3, sm, c, w.gshift);
+            au[t] += chunk_dot<XT, ST>(cu[i], x0, x1, x2, x3, sm, c, w.gshift);
+          }
+        }
+      }
+    }
+  };
+  // round 0 is peeled: a loop-header wait would hold its weight loads behind
+  // the activation loads
+  load_round(0);
+  st.commit(0, xs, sums);
+  st.rest(row_of, xs, sums);
+  __syncthreads();
+  dot_round(0);
+  for (int r0 = ROUND; r0 < cpl; r0 += ROUND) {
+    load_round(r0);
+    dot_round(r0);
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const float g = group_sum<L>(ag[t]);
+    const float u = group_sum<L>(au[t]);
+    if (rv && cl == 0 && t < cnt)
+      act[(int64_t)(pos0 + t) * I + n] =
+          Half<XT>::from_f32(ev ? silu(g) * u : __builtin_nanf(""));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode down projection + routing-weighted combine + residual (T = 1).
+// Lane groups of L lanes; RW output rows per workgroup; the GPR groups of a
+// row split the selected experts (j = gi, gi + GPR, ...).  Every weight load
+// of a round (all experts of the group x CR chunks) is issued before the
+// activations are staged, so one HBM latency covers the whole workgroup.
+template <int L> struct DownShape {
+  static constexpr int NGR = 256 / L;
+  static constexpr int GPR = NGR >= 8 ? NGR / 8 : 1;
+  static constexpr int RW = NGR / GPR;
+};
+
+template <int XT, int ST, int L, int JMAX>
+__global__ __launch_bounds__(WG) void k_ct_down_m1(
+    const uint16_t* __restrict__ act, int topk, const int32_t* __restrict__ sel,
+    const float* __restrict__ wts, QW w, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ out) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  constexpr int GPR = DownShape<L>::GPR, RW = DownShape<L>::RW;
+  constexpr int CR = 4;  // chunks per round
+  const int I = w.K, H = w.N, C = I >> 5;
+  const int cpl = (C + L - 1) / L;
+  u32x4* xs = (u32x4*)lds;
+  float2* sums = (float2*)(lds + (size_t)topk * I * 2);
+  float* red = (float*)(sums + topk * C);  // [topk][RW]
+
+  static_assert(L * RW >= 64, "the expert group must be uniform across a wave");
+  __shared__ float s_w[16];  // routing weights, loaded with the first wave of loads
+  // unconditional loads (clamped indices): a guarded load would be waited for
+  // where its branch joins, before anything else is issued
+  const float wv = wts[min((int)threadIdx.x, topk - 1)];
+  const int on = blockIdx.x * RW + (int)threadIdx.x;  // output row of the combine threads
+  const bool comb = (int)threadIdx.x < RW && on < H;
+  const uint16_t res_raw = *(residual ? residual + min(on, H - 1) : act);
+  // activations next (all selected rows, contiguous act[j][I])
+  Stager<XT> st(topk, I);
+  auto row_of = [&](int j) { return act + (int64_t)j * I; };
+  st.issue(row_of, 0);
+  const int gi = threadIdx.x / L, cl = threadIdx.x % L;
+  const int r = gi % RW;
+  const int jg = __builtin_amdgcn_readfirstlane(gi / RW);  // wave-uniform: sel[] via s_load
+  const int n = blockIdx.x * RW + r;
+  const bool rv = n < H;
+  const int nn = rv ? n : 0;
+
+  int ej[JMAX];
+  RowPtr rp[JMAX];
+#pragma unroll
+  for (int jj = 0; jj < JMAX; ++jj) {
+    const int j = jg + jj * GPR;
+    ej[jj] = j < topk ? sel[j] : -1;
+    const int ee = (unsigned)ej[jj] < (unsigned)w.E ? ej[jj] : 0;
+    rp[jj] = row_ptr<ST>(w, ee, nn);
+  }
+  float row[JMAX];
+#pragma unroll
+  for (int jj = 0; jj < JMAX; ++jj) row[jj] = 0.f;
+  Chunk ch[JMAX][CR];
+  auto load_round = [&](int r0) {
+#pragma unroll
+    for (int jj = 0; jj < JMAX; ++jj)
+#pragma unroll
+      for (int i = 0; i < CR; ++i)
+        if (i == 0 || (r0 + i) * L < C)  // wave-uniform: skips rounds past the row's end
+          ch[jj][i] = load_chunk<ST>(rp[jj], min(cl + (r0 + i) * L, C - 1), w.gshift);
+  };
+  auto dot_round = [&](int r0) {
+#pragma unroll
+    for (int jj = 0; jj < JMAX; ++jj) {
+      const int j = jg + jj * GPR;
+      if (j < topk) {
+        const u32x4* xj = xs + (size_t)j * 4 * C;
+#pragma unroll
+        for (int i = 0; i < CR; ++i) {
+          const int c = cl + (r0 + i) * L;
+          if (c < C)
+            row[jj] += chunk_dot<XT, ST>(ch[jj][i], xj[c], xj[C + c], xj[2 * C + c], xj[3 * C + c],
+                                         sums[j * C + c], c, w.gshift);
+        }
+      }
+    }
+  };
+  // round 0 is peeled: a loop-header wait would hold its weight loads behind
+  // the activation loads
+  load_round(0);
+  st.commit(0, xs, sums);
+  st.rest(row_of, xs, sums);
+  if ((int)threadIdx.x < topk) s_w[threadIdx.x] = wv;
+  __syncthreads();
+  dot_round(0);
+  for (int r0 = CR; r0 < cpl; r0 += CR) {
+    load_round(r0);
+    dot_round(r0);
+  }
+#pragma unroll
+  for (int jj = 0; jj < JMAX; ++jj) {
+    const int j = jg + jj * GPR;
+    const float v = group_sum<L>(row[jj]);
+    if (j < topk && cl == 0)
+      red[j * RW + r] = (unsigned)ej[jj] < (unsigned)w.E ? v : __builtin_nanf("");
+  }
+  __syncthreads();
+  if (comb) {
+    float y = 0.f;
+    for (int j = 0; j < topk; ++j) y += s_w[j] * red[j * RW + (int)threadIdx.x];
+    out[on] = Half<XT>::from_f32((residual ? Half<XT>::to_f32(res_raw) : 0.f) + y);
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// launchers
+// gate_up lanes: prefer 2 chunks per lane so a decode layer spreads over
+// ~3 workgroups per CU (H = 2048: L = 32, 8 row pairs per workgroup)
+inline int gate_up_lanes(int C) {
+  int L = 8;
+  while (L < 64 && C >= 4 * L) L *= 2;
+  return L;
+}
+
+// lanes per output row of the down projection (8..64, 3+ chunks per lane
+// when the row is long enough)
+inline int lanes_per_row(int C) {
+  int L = 8;
+  while (L * 2 <= C && L < 64) L *= 2;
+  while (L > 8 && C < 3 * L) L /= 2;
+  return L;
+}
+
+inline QW to_qw(const TW& t) {
+  return QW{t.packed, t.scale, t.zeros, t.pes, t.ses, t.zes, t.gshift, t.E, t.N, t.K};
+}
+
+template <int XT, int ST, int MODE>
+static int ct_gate_up_t(int L, dim3 grid, size_t lds, hipStream_t s, const GateUpArgs& a,
+                        const QW& w, int I) {
+#define I4_GU_CASE(L_)                                                                          \
+  if (L == L_) {                                                                                \
+    hipLaunchKernelGGL((k_ct_gate_up<XT, ST, L_, MODE>), grid, dim3(WG), lds, s,                \
+                       (const uint16_t*)a.x, a.topk, a.sel, (const uint16_t*)a.logits, a.E_r,   \
+                       a.renorm, a.wts, w, I, (uint16_t*)a.act);                                \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
+  }
+  I4_GU_CASE(8) I4_GU_CASE(16) I4_GU_CASE(32) I4_GU_CASE(64)
+#undef I4_GU_CASE
+  return I4_ERR_SHAPE;
+}
+
+template <int XT, int ST>
+int launch_gate_up_ct(const GateUpArgs& a, const TW& tw, int I, hipStream_t s) {
+  const QW w = to_qw(tw);
+  const int H = w.K, C = H / 32;
+  const int L = gate_up_lanes(C);
+  const int rpw = WG / L;
+  dim3 grid((I + rpw - 1) / rpw, a.n_slots);
+  const size_t lds = (size_t)H * 2 + C * 8;
+  if (lds > kMaxLds) return I4_ERR_SHAPE;
+  return a.route ? ct_gate_up_t<XT, ST, GU_ROUTE>(L, grid, lds, s, a, w, I)
+                 : ct_gate_up_t<XT, ST, GU_SEL>(L, grid, lds, s, a, w, I);
+}
+
+template <int XT, int ST>
+int launch_down_m1_ct(const void* act, int topk, const int32_t* sel, const float* wts,
+                      const TW& tw, const void* res, void* out, hipStream_t s) {
+  const QW w = to_qw(tw);
+  const int I = w.K, C = I / 32;
+  const int L = lanes_per_row(C);
+  const size_t lds_base = (size_t)topk * (I * 2 + C * 8);
+#define I4_DN_CASE(L_, J_)                                                                     \
+  if (L == L_ && (topk + DownShape<L_>::GPR - 1) / DownShape<L_>::GPR <= J_) {                 \
+    constexpr int RW = DownShape<L_>::RW;                                                      \
+    const size_t lds = lds_base + (size_t)topk * RW * 4;                                       \
+    if (lds > kMaxLds) return I4_ERR_SHAPE;                                                    \
+    hipLaunchKernelGGL((k_ct_down_m1<XT, ST, L_, J_>), dim3((w.N + RW - 1) / RW), dim3(WG),    \
+                       lds, s, (const uint16_t*)act, topk, sel, wts, w, (const uint16_t*)res,  \
+                       (uint16_t*)out);                                                        \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                            \
+  }
+  I4_DN_CASE(8, 2) I4_DN_CASE(16, 2) I4_DN_CASE(8, 4) I4_DN_CASE(16, 4) I4_DN_CASE(32, 8)
+  I4_DN_CASE(64, 8)
+#undef I4_DN_CASE
+  return I4_ERR_SHAPE;
+}
+
+#define I4_INST(XT_, ST_)                                                                      \
+  template int launch_gate_up_ct<XT_, ST_>(const GateUpArgs&, const TW&, int, hipStream_t);    \
+  template int launch_down_m1_ct<XT_, ST_>(const void*, int, const int32_t*, const float*,     \
+                                           const TW&, const void*, void*, hipStream_t);
+I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
+I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)
+#undef I4_INST
+
+}  // namespace i4

@@ -1,0 +1,57 @@
+// Launchers of the MoE kernels (I4_LAYOUT_TILE weights), shared between the
+// translation units of libi4moe.  Callers have validated every argument.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "i4_tile.h"
+
+namespace i4 {
+
+static constexpr int MF_TOK = 64;    // tokens per entry of the large-entry MFMA kernel
+static constexpr int MF_SMALL = 16;  // experts with at most this many tokens: one m-block
+static constexpr int MF_NB = 2;      // n-blocks of 16 weight rows per wave
+
+// decode gate_up + SiLU: slot j of token 0 (route: ranked from logits in the
+// kernel, sel / wts written for the down stage; else expert sel[j])
+struct GateUpArgs {
+  bool route;
+  int n_slots;  // grid rows: slots computed
+  int topk;
+  int E_r;      // logits per row (route)
+  int renorm;
+  const void* x;
+  int32_t* sel;
+  const void* logits;
+  float* wts;
+  void* act;
+};
+
+// tile weights (i4_moe_decode.hip)
+template <int XT, int ST>
+int launch_gate_up(const GateUpArgs& a, const TW& w, int I, hipStream_t s);
+template <int XT, int ST>
+int launch_down_m1(const void* act, int topk, const int32_t* sel, const float* wts, const TW& w,
+                   const void* residual, void* out, hipStream_t s);
+// CT weights (i4_moe_ct.hip); TW carries the CT pointers and strides
+template <int XT, int ST>
+int launch_gate_up_ct(const GateUpArgs& a, const TW& w, int I, hipStream_t s);
+template <int XT, int ST>
+int launch_down_m1_ct(const void* act, int topk, const int32_t* sel, const float* wts,
+                      const TW& w, const void* residual, void* out, hipStream_t s);
+
+// Grouped (T > 1) expert projections on MFMA.  entries[i] = {expert, first
+// position, tokens, 0} of the expert-sorted (token, slot) list perm; small
+// entries have <= MF_SMALL tokens, large ones <= MF_TOK.
+//   gate_up: act[pos] = silu(gate(x[perm[pos] / topk])) * up(...)
+//   down:    ys[perm[pos]] = down(act[pos]) (fp32)
+template <int XT, int ST>
+int launch_mfma_gate_up(bool small, int max_entries, const void* x, int topk, const int4* ent,
+                        const int* nent, const int32_t* perm, const TW& w, int I, void* act,
+                        hipStream_t s);
+template <int XT, int ST>
+int launch_mfma_down(bool small, int max_entries, const void* act, const int4* ent,
+                     const int* nent, const int32_t* perm, const TW& w, float* ys, hipStream_t s);
+
+}  // namespace i4

@@ -13,7 +13,11 @@ Host-resident experts and CPU compute (:86-164, :202-220) exist in the
 reference only because its 12 GB card cannot hold the Thinker; on a 288 GB
 MI355X every layer stays resident, so those modes are rejected.
 Extra constructors build the module from already-stacked CT tensors or from
-AutoAWQ tensors (repacked once, on the device, into CT with zero points).
+AutoAWQ tensors.  The module keeps the experts as CT rows (AWQ repacked with
+explicit zeros), which the latency-bound decode kernels stream row by row, and
+a copy in the library's tile layout for the MFMA kernels of T > 1
+(layouts="both", the default); layouts="tile" keeps only the tile copy and
+decodes from it (one copy of the weights, slower decode).
 """
 from __future__ import annotations
 
@@ -23,11 +27,11 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .weights import QWeight, repack_awq_to_ct
+from .weights import QWeight, repack_awq_to_ct, repack_tile
 
 
 def _stack_ct(linears, dtype, device):
-    """Stack packed Linears into (packed [E, N, K/8], scale [E, N, NG], N, K)."""
+    """Stack packed Linears into CT (packed [E, N, K/8], scale [E, N, NG], N, K)."""
     l0 = linears[0]
     out_f, in_f = (int(v) for v in l0.weight_shape.tolist())
     E = len(linears)
@@ -43,8 +47,12 @@ class FusedPackedMoE(nn.Module):
     """SparseMoeBlock replacement for int4-packed experts."""
 
     def __init__(self, block: nn.Module | None = None, dtype=torch.bfloat16, device="cuda",
-                 host_resident: bool = False, cpu_compute: bool = False, group: int = 32):
+                 host_resident: bool = False, cpu_compute: bool = False, group: int = 32,
+                 layouts: str = "both"):
         super().__init__()
+        if layouts not in ("both", "tile"):
+            raise ValueError("layouts is 'both' (CT rows for decode + tiles) or 'tile'")
+        self.layouts = layouts
         if host_resident or cpu_compute:
             raise NotImplementedError(
                 "host-resident / CPU-computed experts are not provided: every layer is resident "
@@ -60,16 +68,24 @@ class FusedPackedMoE(nn.Module):
         gp, gs, inter, hidden = _stack_ct([e.gate_proj for e in experts], dtype, device)
         up, us, _, _ = _stack_ct([e.up_proj for e in experts], dtype, device)
         dp, ds, hid_out, inter_in = _stack_ct([e.down_proj for e in experts], dtype, device)
-        gu_p, gu_s = torch.cat([gp, up], dim=1), torch.cat([gs, us], dim=1)
+        gu = QWeight(torch.cat([gp, up], dim=1), torch.cat([gs, us], dim=1), None, "ct", group,
+                     2 * inter, hidden)
         del gp, up, gs, us
-        self._install(QWeight(gu_p, gu_s, None, "ct", group, 2 * inter, hidden),
-                      QWeight(dp, ds, None, "ct", group, hid_out, inter_in), gw)
+        self._install(gu, QWeight(dp, ds, None, "ct", group, hid_out, inter_in), gw)
 
     def _install(self, gate_up: QWeight, down: QWeight, router_w: torch.Tensor,
-                 norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6) -> None:
-        if gate_up.layout != "ct" or down.layout != "ct":
-            raise ValueError("FusedPackedMoE stores CT weights (convert AWQ with from_awq)")
+                 norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6,
+                 gate_up_tile: QWeight | None = None, down_tile: QWeight | None = None) -> None:
+        """gate_up / down in any layout; tile copies are built here unless given."""
+        if self.layouts == "tile" or gate_up.layout == "tile":
+            gate_up, down = gate_up.to_tile(), down.to_tile()  # tiles cannot become CT rows
+            gate_up_tile = down_tile = None
+        else:
+            if gate_up_tile is None:
+                gate_up_tile, down_tile = gate_up.to_tile(), down.to_tile()
+            gate_up, down = gate_up.to_ct(), down.to_ct()
         self.gate_up, self.down = gate_up, down
+        self.gate_up_tile, self.down_tile = gate_up_tile, down_tile
         self.num_experts = gate_up.E
         self.inter = gate_up.N // 2
         self.hidden = gate_up.K
@@ -77,17 +93,25 @@ class FusedPackedMoE(nn.Module):
         self.register_buffer("router_w", router_w, persistent=False)
         self.register_buffer("norm_weight", norm_weight, persistent=False)
         self.norm_eps = float(norm_eps)
-        for name, t in (("gu_packed", gate_up.packed), ("gu_scale", gate_up.scale),
-                        ("gu_zeros", gate_up.zeros), ("down_packed", down.packed),
-                        ("down_scale", down.scale), ("down_zeros", down.zeros)):
+        bufs = [("gu_packed", gate_up.packed), ("gu_scale", gate_up.scale),
+                ("gu_zeros", gate_up.zeros), ("down_packed", down.packed),
+                ("down_scale", down.scale), ("down_zeros", down.zeros)]
+        if gate_up_tile is not None:
+            bufs += [("gu_tile_packed", gate_up_tile.packed), ("gu_tile_scale", gate_up_tile.scale),
+                     ("gu_tile_zeros", gate_up_tile.zeros), ("down_tile_packed", down_tile.packed),
+                     ("down_tile_scale", down_tile.scale), ("down_tile_zeros", down_tile.zeros)]
+        for name, t in bufs:
             self.register_buffer(name, t, persistent=False)
 
     @classmethod
     def from_stacked(cls, gate_up: QWeight, down: QWeight, router_w: torch.Tensor, top_k: int,
                      norm_topk_prob: bool = True, norm_weight: torch.Tensor | None = None,
-                     norm_eps: float = 1e-6) -> "FusedPackedMoE":
-        """From CT weights.  norm_weight fuses the decoder's pre-MoE RMSNorm (optional)."""
-        m = cls()
+                     norm_eps: float = 1e-6, layouts: str = "both") -> "FusedPackedMoE":
+        """From stacked weights in any layout (gate_up = gate rows then up rows).
+
+        norm_weight fuses the decoder's pre-MoE RMSNorm (optional).
+        """
+        m = cls(layouts=layouts)
         m.top_k, m.norm_topk_prob = int(top_k), bool(norm_topk_prob)
         m._install(gate_up, down, router_w.contiguous(),
                    None if norm_weight is None else norm_weight.contiguous(), norm_eps)
@@ -96,22 +120,33 @@ class FusedPackedMoE(nn.Module):
     @classmethod
     def from_awq(cls, gate: QWeight, up: QWeight, down: QWeight, router_w: torch.Tensor,
                  top_k: int, norm_topk_prob: bool = True, norm_weight: torch.Tensor | None = None,
-                 norm_eps: float = 1e-6) -> "FusedPackedMoE":
-        """Experts in AutoAWQ packing; gate|up and down are repacked to CT+zeros."""
-        gu = repack_awq_to_ct([gate, up])
-        dn = repack_awq_to_ct([down])
-        return cls.from_stacked(gu, dn, router_w, top_k, norm_topk_prob, norm_weight, norm_eps)
+                 norm_eps: float = 1e-6, layouts: str = "both") -> "FusedPackedMoE":
+        """Experts in AutoAWQ packing: gate|up and down repacked (CT + zeros, and tiles)."""
+        m = cls(layouts=layouts)
+        m.top_k, m.norm_topk_prob = int(top_k), bool(norm_topk_prob)
+        gu_t, dn_t = repack_tile([gate, up]), repack_tile([down])
+        if layouts == "tile":
+            m._install(gu_t, dn_t, router_w.contiguous(),
+                       None if norm_weight is None else norm_weight.contiguous(), norm_eps)
+        else:
+            m._install(repack_awq_to_ct([gate, up]), repack_awq_to_ct([down]),
+                       router_w.contiguous(),
+                       None if norm_weight is None else norm_weight.contiguous(), norm_eps,
+                       gu_t, dn_t)
+        return m
 
     def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor | None = None):
         """MoE(hidden_states) (+ residual); with a fused norm, MoE(RMSNorm(hidden_states))."""
         return ops.moe_forward(hidden_states, self.gate_up, self.down, self.top_k,
                                router_w=self.router_w, norm_topk_prob=self.norm_topk_prob,
                                residual=residual, workspace=self.workspace,
-                               norm_w=self.norm_weight, norm_eps=self.norm_eps)
+                               norm_w=self.norm_weight, norm_eps=self.norm_eps,
+                               gate_up_tile=self.gate_up_tile, down_tile=self.down_tile)
 
     def stack_entry(self) -> tuple:
-        """(gate_up, down, router_w, norm_w, eps) for ops.moe_stack."""
-        return (self.gate_up, self.down, self.router_w, self.norm_weight, self.norm_eps)
+        """(gate_up, down, router_w, norm_w, eps, gate_up_tile, down_tile) for ops.moe_stack."""
+        return (self.gate_up, self.down, self.router_w, self.norm_weight, self.norm_eps,
+                self.gate_up_tile, self.down_tile)
 
     def route(self, hidden_states: torch.Tensor):
         """(w, sel) exactly as forward() routes: [norm,] router Linear, softmax, top-k, renorm."""
@@ -122,7 +157,7 @@ class FusedPackedMoE(nn.Module):
 
 def fuse_packed_moe_blocks(model: nn.Module, dtype=torch.bfloat16, device="cuda",
                            n_pinned: int | None = None, cpu_compute: bool = False,
-                           verbose: bool = True) -> int:
+                           verbose: bool = True, layouts: str = "both") -> int:
     """Replace every packed *SparseMoeBlock with a FusedPackedMoE (all resident)."""
     if cpu_compute:
         raise NotImplementedError("CPU-computed experts are not provided")
@@ -136,7 +171,7 @@ def fuse_packed_moe_blocks(model: nn.Module, dtype=torch.bfloat16, device="cuda"
                     sites.append((parent, name))
     for parent, name in sites:
         child = getattr(parent, name)
-        setattr(parent, name, FusedPackedMoE(child, dtype, device))
+        setattr(parent, name, FusedPackedMoE(child, dtype, device, layouts=layouts))
         child.experts = None
         del child
         gc.collect()

@@ -171,12 +171,30 @@ def route(logits: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
     return w, sel
 
 
+def _decode_layout(*ws: QWeight) -> None:
+    for w in ws:
+        if w.layout not in ("ct", "tile"):
+            raise ValueError(f"the MoE kernels read CT rows or tiles, got {w.layout!r}: "
+                             "convert once with QWeight.to_ct() / to_tile()")
+
+
 def moe_weights_c(gate_up: QWeight, down: QWeight, router_w: torch.Tensor | None,
-                  norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6) -> _lib.MoeWeightsC:
-    return _lib.MoeWeightsC(gate_up=gate_up.c(), down=down.c(),
-                            router_w=None if router_w is None else router_w.data_ptr(),
-                            norm_w=None if norm_w is None else norm_w.data_ptr(),
-                            norm_eps=float(norm_eps))
+                  norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
+                  gate_up_tile: QWeight | None = None,
+                  down_tile: QWeight | None = None) -> _lib.MoeWeightsC:
+    """struct i4_moe_weights: decode weights (CT or tile) and optional tile copies (T > 1)."""
+    _decode_layout(gate_up, down)
+    if (gate_up_tile is None) != (down_tile is None):
+        raise ValueError("give both tile copies or neither")
+    mw = _lib.MoeWeightsC(gate_up=gate_up.c(), down=down.c(),
+                          router_w=None if router_w is None else router_w.data_ptr(),
+                          norm_w=None if norm_w is None else norm_w.data_ptr(),
+                          norm_eps=float(norm_eps))
+    if gate_up_tile is not None:
+        if gate_up_tile.layout != "tile" or down_tile.layout != "tile":
+            raise ValueError("the tile copies must be in the tile layout")
+        mw.gate_up_tile, mw.down_tile = gate_up_tile.c(), down_tile.c()
+    return mw
 
 
 class Workspace:
@@ -186,9 +204,8 @@ class Workspace:
         self.buf: torch.Tensor | None = None
 
     def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
-        # zero-filled once: the library keeps its handoff counters zero between calls
         if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
-            self.buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+            self.buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
         return self.buf
 
 
@@ -196,10 +213,13 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
                 router_w: torch.Tensor | None = None, logits: torch.Tensor | None = None,
                 norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
                 return_routing: bool = False, workspace: Workspace | None = None,
-                norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6):
+                norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
+                gate_up_tile: QWeight | None = None, down_tile: QWeight | None = None):
     """One int4 MoE block: out = residual + sum_j w_j down_e(silu(gate_e xn) * up_e xn).
 
     xn = x, or RMSNorm(x) with weight norm_w (the decoder's post-attention norm).
+    gate_up / down (CT or tile) serve one token; more tokens run on tiles: the
+    tile copies, or gate_up / down themselves when they are tiles.
     """
     dev = _lib.require_device(x, gate_up.packed, down.packed, router_w, logits, residual, norm_w)
     xt = _lib.half_code(x.dtype)
@@ -219,7 +239,7 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
     lb = _lib.lib()
     nbytes = lb.i4_moe_workspace_bytes(T, H, I, E, top_k)
     ws = (workspace or Workspace()).get(nbytes, dev)
-    mw = moe_weights_c(gate_up, down, router_w, norm_w, norm_eps)
+    mw = moe_weights_c(gate_up, down, router_w, norm_w, norm_eps, gate_up_tile, down_tile)
     _lib.check(lb.i4_moe_forward(xf.data_ptr(), xt, T, ctypes.byref(mw), top_k,
                                  int(norm_topk_prob), _lib.ptr(lg), _lib.ptr(rs), out.data_ptr(),
                                  _lib.ptr(sel), _lib.ptr(wts), ws.data_ptr(), ws.numel(),
@@ -232,6 +252,7 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
 
 def moe_gate_up(x: torch.Tensor, gate_up: QWeight, sel: torch.Tensor) -> torch.Tensor:
     """Decode gate_up stage: act [k, I] = silu(gate_e x) * up_e x for e = sel (x is [H])."""
+    _decode_layout(gate_up)
     dev = _lib.require_device(x, gate_up.packed, sel)
     xt = _lib.half_code(x.dtype)
     xc = x.reshape(-1).contiguous()
@@ -246,6 +267,7 @@ def moe_gate_up(x: torch.Tensor, gate_up: QWeight, sel: torch.Tensor) -> torch.T
 def moe_route_gate_up(x: torch.Tensor, gate_up: QWeight, logits: torch.Tensor, top_k: int,
                       norm_topk_prob: bool = True):
     """Decode routing + gate_up stage in one launch: (act [k, I], sel [k] int32, w [k] fp32)."""
+    _decode_layout(gate_up)
     dev = _lib.require_device(x, gate_up.packed, logits)
     xt = _lib.half_code(x.dtype)
     xc = x.reshape(-1).contiguous()
@@ -264,6 +286,7 @@ def moe_route_gate_up(x: torch.Tensor, gate_up: QWeight, logits: torch.Tensor, t
 def moe_down_combine(act: torch.Tensor, down: QWeight, sel: torch.Tensor, w: torch.Tensor,
                      residual: torch.Tensor | None = None) -> torch.Tensor:
     """Decode down stage: residual + sum_j w[j] down_{sel[j]}(act[j]) -> [H]."""
+    _decode_layout(down)
     dev = _lib.require_device(act, down.packed, sel, w, residual)
     xt = _lib.half_code(act.dtype)
     s32 = sel.reshape(-1).to(torch.int32).contiguous()
@@ -279,7 +302,8 @@ def moe_down_combine(act: torch.Tensor, down: QWeight, sel: torch.Tensor, w: tor
 
 def moe_stack(x: torch.Tensor, layers: list[tuple], top_k: int,
               norm_topk_prob: bool = True, workspace: Workspace | None = None) -> torch.Tensor:
-    """h <- h + moe_l(norm_l(h)) over layers [(gate_up, down, router_w[, norm_w[, eps]]), ...]."""
+    """h <- h + moe_l(norm_l(h)) over layers
+    [(gate_up, down, router_w[, norm_w[, eps[, gate_up_tile, down_tile]]]), ...]."""
     dev = _lib.require_device(x)
     xt = _lib.half_code(x.dtype)
     shape = x.shape

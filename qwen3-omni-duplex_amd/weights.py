@@ -13,8 +13,16 @@ packed formats:
         word w holding column 8w + (0, 2, 4, 6, 1, 3, 5, 7)[i]; qzeros
         [E, NG, N/8] packed the same way; scales [E, NG, N].
 
-The fused kernels run on "ct" (optionally with zeros); AWQ weights are
-converted once with to_ct(), on the device, by the library.
+  "tile" the library's load-time layout for the MoE kernels (no reference
+        counterpart): packed [E, N/16, K/128, 16, 16] int32, element
+        [e, b, s, r, 4j + t] = CT word 4(4s + t) + j of row 16b + r, so one
+        wavefront load of lanes (r, j) reads 1 KB of contiguous memory;
+        scale [E, N/16, NG, 16] and zeros [E, N/16, ceil(NG/8), 16] hold the CT
+        values of row 16b + r.  Needs N % 16 == 0 and K % 128 == 0.
+
+The dequant-GEMV entry points take "ct" or "awq"; the fused MoE kernels take
+"tile", built once on the device with to_tile() / repack_tile() (AWQ can also
+be converted to "ct" with explicit zeros by to_ct()).
 """
 from __future__ import annotations
 
@@ -56,6 +64,12 @@ class QWeight:
             want_p = (E, self.N, self.K // 8)
             want_s = (E, self.N, NG)
             want_z = (E, self.N, -(-NG // 8))
+        elif self.layout == "tile":
+            if self.N % 16 or self.K % 128:
+                raise ValueError("the tile layout needs N % 16 == 0 and K % 128 == 0")
+            want_p = (E, self.N // 16, self.K // 128, 16, 16)
+            want_s = (E, self.N // 16, NG, 16)
+            want_z = (E, self.N // 16, -(-NG // 8), 16)
         else:
             want_p = (E, self.K, self.N // 8)
             want_s = (E, NG, self.N)
@@ -90,6 +104,12 @@ class QWeight:
         if self.layout == "ct":
             return self
         return repack_awq_to_ct([self])
+
+    def to_tile(self) -> "QWeight":
+        """Tile-layout copy for the MoE kernels (identity for a tile weight)."""
+        if self.layout == "tile":
+            return self
+        return repack_tile([self])
 
     @staticmethod
     def ct(packed, scale, group=32, zeros=None, N=None, K=None) -> "QWeight":
@@ -130,3 +150,37 @@ def repack_awq_to_ct(parts: list[QWeight]) -> QWeight:
                                           zeros.data_ptr(), N, off, _lib.stream(dev)))
         off += p.N
     return QWeight(packed, scale, zeros, "ct", G, N, K)
+
+
+def repack_tile(parts: list[QWeight]) -> QWeight:
+    """Concatenate CT / AWQ weights along N into one tile-layout weight, on the device.
+
+    parts share E, K, group and scale dtype, and each part's N is a multiple of
+    16; the result has N = sum of parts' N (the gate|up concatenation of
+    fused_packed_moe.py:122 when parts = [gate, up]).  Zero points are kept
+    explicit when any part has them (a symmetric part then gets 8s).
+    """
+    p0 = parts[0]
+    dev = _lib.require_device(*[p.packed for p in parts])
+    E, K, G = p0.E, p0.K, p0.group
+    for p in parts:
+        if (p.layout == "tile" or p.E != E or p.K != K or p.group != G
+                or p.scale.dtype != p0.scale.dtype or p.N % 16):
+            raise ValueError("repack parts must be CT/AWQ weights with equal E, K, group, scale "
+                             "dtype and N % 16 == 0")
+    N = sum(p.N for p in parts)
+    NG = -(-K // G)
+    packed = torch.empty(E, N // 16, K // 128, 16, 16, dtype=torch.int32, device=dev)
+    scale = torch.empty(E, N // 16, NG, 16, dtype=p0.scale.dtype, device=dev)
+    with_z = any(p.zeros is not None for p in parts)
+    zeros = (torch.empty(E, N // 16, -(-NG // 8), 16, dtype=torch.int32, device=dev)
+             if with_z else None)
+    lb = _lib.lib()
+    off = 0
+    for p in parts:
+        cw = p.c()
+        _lib.check(lb.i4_repack_tile(ctypes.byref(cw), packed.data_ptr(), scale.data_ptr(),
+                                     None if zeros is None else zeros.data_ptr(), N, off,
+                                     _lib.stream(dev)))
+        off += p.N
+    return QWeight(packed, scale, zeros, "tile", G, N, K)

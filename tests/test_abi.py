@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported_and_bound(pkg):
 
 def test_version_and_errors(pkg):
     lib = pkg.lib()
-    assert lib.i4_abi_version() == 1
+    assert lib.i4_abi_version() == 2
     codes = {0: b"ok", -1: b"NULL", -2: b"dimension", -3: b"element type", -4: b"aligned",
              -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride"}
     for c, frag in codes.items():
@@ -109,8 +109,8 @@ def test_moe_validation_codes(pkg):
     from qwen3_omni_duplex_amd import _lib
 
     lib = pkg.lib()
-    gu = _qw(_lib, E=128, N=1536, K=2048, group=128)
-    dn = _qw(_lib, E=128, N=2048, K=768, group=128)
+    gu = _qw(_lib, E=128, N=1536, K=2048, group=128, layout=2)
+    dn = _qw(_lib, E=128, N=2048, K=768, group=128, layout=2)
     mw = _lib.MoeWeightsC(gate_up=gu, down=dn, router_w=0x60000)
     ws = lib.i4_moe_workspace_bytes(1, 2048, 768, 128, 8)
     assert ws > 0
@@ -123,12 +123,43 @@ def test_moe_validation_codes(pkg):
     assert call(k=0) == -2
     assert call(T=0) == -2
     assert call(xt=0) == -3
-    bad = _lib.MoeWeightsC(gate_up=_qw(_lib, E=128, N=1500, K=2048, group=128), down=dn,
-                           router_w=0x60000)
+    bad = _lib.MoeWeightsC(gate_up=_qw(_lib, E=128, N=1504, K=2048, group=128, layout=2),
+                           down=dn, router_w=0x60000)
     assert call(mw=bad) == -2
+    # the tile layout needs N % 16 == 0 and K % 128 == 0
+    ragged = _lib.MoeWeightsC(gate_up=_qw(_lib, E=128, N=1528, K=2048, group=128, layout=2),
+                              down=dn, router_w=0x60000)
+    assert call(mw=ragged) == -2
+    # decode reads CT rows or tiles (the same layout for both weights), more tokens need tiles
+    # (only validation failures here: a valid call would launch on the fake pointers)
+    ct_gu = _qw(_lib, E=128, N=1536, K=2048, group=128, layout=0)
+    ct_dn = _qw(_lib, E=128, N=2048, K=768, group=128, layout=0)
+    ctw = _lib.MoeWeightsC(gate_up=ct_gu, down=ct_dn, router_w=0x60000)
+    assert call(mw=ctw, T=2) == -5
+    mixed = _lib.MoeWeightsC(gate_up=ct_gu, down=dn, router_w=0x60000)
+    assert call(mw=mixed) == -5
     awq = _lib.MoeWeightsC(gate_up=_qw(_lib, E=128, N=1536, K=2048, group=128, layout=1),
                            down=dn, router_w=0x60000)
     assert call(mw=awq) == -5
+    # tile copies: both or neither, in the tile layout, the block's shapes
+    half = _lib.MoeWeightsC(gate_up=ct_gu, down=ct_dn, router_w=0x60000, gate_up_tile=gu)
+    assert call(mw=half) == -1
+    wrong = _lib.MoeWeightsC(gate_up=ct_gu, down=ct_dn, router_w=0x60000, gate_up_tile=ct_gu,
+                             down_tile=ct_dn)
+    assert call(mw=wrong) == -5
+    small = _lib.MoeWeightsC(gate_up=ct_gu, down=ct_dn, router_w=0x60000,
+                             gate_up_tile=_qw(_lib, E=64, N=1536, K=2048, group=128, layout=2),
+                             down_tile=dn)
+    assert call(mw=small) == -2
+    # and the dequant-GEMV entry points do not take it
+    tw = _qw(_lib, E=8, N=768, K=2048, group=128, layout=2)
+    assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(tw), 0x40000, 8, 0x50000, 0, None, 0,
+                          None) == -5
+    # repack into tiles: row offsets in whole 16-row blocks, a source in CT or AWQ
+    src = _qw(_lib, E=8, N=768, K=2048, group=128)
+    assert lib.i4_repack_tile(ctypes.byref(src), 0x40000, 0x50000, None, 1536, 8, None) == -2
+    assert lib.i4_repack_tile(ctypes.byref(src), 0x40000, 0x50000, None, 1536, 1024, None) == -2
+    assert lib.i4_repack_tile(ctypes.byref(tw), 0x40000, 0x50000, None, 768, 0, None) == -5
     nor = _lib.MoeWeightsC(gate_up=gu, down=dn, router_w=None)
     assert call(mw=nor) == -1
     # a fused norm needs the router weight (it produces the normalised input)

@@ -100,6 +100,63 @@ def test_repack_concatenates_gate_up(pkg, dev):
     np.testing.assert_array_equal(gu.packed.cpu().numpy(), ref)
 
 
+def canon_zeros(z, NG):
+    """CT zero words with the nibbles past the last group cleared (what a repack writes)."""
+    z = np.ascontiguousarray(z).view(np.uint32).copy()
+    last = NG - 8 * (z.shape[-1] - 1)
+    if last < 8:
+        z[..., -1] &= np.uint32((1 << (4 * last)) - 1)
+    return z.view(np.int32)
+
+
+@pytest.mark.parametrize("src,G,zeros", [("ct", 32, False), ("ct", 128, True), ("ct", 64, True),
+                                          ("awq", 128, True)])
+def test_repack_tile_bit_exact(pkg, dev, src, G, zeros):
+    """CT / AWQ -> tile layout on the device equals the oracle's tile_pack of the CT words,
+    and the tile weight dequantises to the same values as its source."""
+    rng = np.random.default_rng(15)
+    E, N, K = 3, 96, 768
+    if src == "ct":
+        p, s, z = _gen.ct_weight(rng, E, N, K, G, zeros=zeros)
+        z = None if z is None else canon_zeros(z, -(-K // G))
+        w = pkg.QWeight(t_(p, dev), t_(s, dev), None if z is None else t_(z, dev), "ct", G, N, K)
+        cp, cs, cz = p, s, z
+    else:
+        qw, qz, s = _gen.awq_weight(rng, E, K, N, G)
+        w = pkg.QWeight(t_(qw, dev), t_(s, dev), t_(qz, dev), "awq", G, N, K)
+        cp, cs, cz = i4ref.awq_to_ct(qw, qz, s, G)
+    t = w.to_tile()
+    rp, rs, rz = i4ref.tile_pack(cp, cs, cz)
+    np.testing.assert_array_equal(t.packed.cpu().numpy(), rp)
+    np.testing.assert_array_equal(t.scale.cpu().numpy(), rs)
+    if rz is None:
+        assert t.zeros is None
+    else:
+        np.testing.assert_array_equal(t.zeros.cpu().numpy(), rz)
+    np.testing.assert_array_equal(host(pkg.dequant(t, torch.float32)),
+                                  host(pkg.dequant(w, torch.float32)))
+
+
+def test_repack_tile_concatenates_gate_up(pkg, dev):
+    """gate | up into one tile weight: rows [0, N) from gate, [N, 2N) from up; a symmetric
+    part next to one with zeros gets explicit 8s."""
+    rng = np.random.default_rng(16)
+    E, K, N, G = 2, 256, 64, 128
+    g = _gen.ct_weight(rng, E, N, K, G, zeros=True)
+    u = _gen.ct_weight(rng, E, N, K, G, zeros=False)
+    gz = canon_zeros(g[2], K // G)
+    ws = [pkg.QWeight(t_(g[0], dev), t_(g[1], dev), t_(gz, dev), "ct", G, N, K),
+          pkg.QWeight(t_(u[0], dev), t_(u[1], dev), None, "ct", G, N, K)]
+    gu = pkg.repack_tile(ws)
+    u_z = np.full((E, N, 1), 0x88, dtype=np.int32)  # two groups, zero point 8
+    rp, rs, rz = i4ref.tile_pack(np.concatenate([g[0], u[0]], axis=1),
+                                 np.concatenate([g[1], u[1]], axis=1),
+                                 np.concatenate([gz, u_z], axis=1))
+    np.testing.assert_array_equal(gu.packed.cpu().numpy(), rp)
+    np.testing.assert_array_equal(gu.scale.cpu().numpy(), rs)
+    np.testing.assert_array_equal(gu.zeros.cpu().numpy(), rz)
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 def test_dequant_matches_oracle(pkg, dev, out_dtype):
     rng = np.random.default_rng(14)
@@ -254,7 +311,7 @@ def test_router_logits(pkg, dev, xdt, T):
 
 
 # ---------------------------------------------------------------- MoE block
-def _awq_moe(pkg, dev, rng, E=128, H=2048, I=768, G=128, sdt=np.float16):
+def _awq_moe(pkg, dev, rng, E=128, H=2048, I=768, G=128, sdt=np.float16, layouts="both"):
     g = _gen.awq_weight(rng, E, H, I, G, sdt)
     u = _gen.awq_weight(rng, E, H, I, G, sdt)
     d = _gen.awq_weight(rng, E, I, H, G, sdt)
@@ -264,7 +321,7 @@ def _awq_moe(pkg, dev, rng, E=128, H=2048, I=768, G=128, sdt=np.float16):
         return pkg.QWeight(t_(part[0], dev), t_(part[2], dev), t_(part[1], dev), "awq", G,
                            part[0].shape[2] * 8, part[0].shape[1])
 
-    moe = pkg.FusedPackedMoE.from_awq(q(g), q(u), q(d), t_(wr, dev), top_k=8)
+    moe = pkg.FusedPackedMoE.from_awq(q(g), q(u), q(d), t_(wr, dev), top_k=8, layouts=layouts)
     dgu = lambda e: np.concatenate([i4ref.awq_dequant(g[0][e], g[1][e], f_(g[2][e]), G),
                                     i4ref.awq_dequant(u[0][e], u[1][e], f_(u[2][e]), G)], axis=0)
     ddn = lambda e: i4ref.awq_dequant(d[0][e], d[1][e], f_(d[2][e]), G)
@@ -283,7 +340,8 @@ def _check_moe(pkg, moe, dgu, ddn, x_np, xdt, dev, logits=None, residual=None, n
     if norm is not None:
         kw.update(norm_w=t_(norm[0], dev), norm_eps=norm[1])
     out, sel, w = pkg.moe_forward(x, moe.gate_up, moe.down, moe.top_k, return_routing=True,
-                                  residual=None if residual is None else t_(residual, dev), **kw)
+                                  residual=None if residual is None else t_(residual, dev),
+                                  gate_up_tile=moe.gate_up_tile, down_tile=moe.down_tile, **kw)
     xin = f_(x_np)
     if logits is None:
         if norm is None:
@@ -309,10 +367,13 @@ def _check_moe(pkg, moe, dgu, ddn, x_np, xdt, dev, logits=None, residual=None, n
     return got, err
 
 
-def test_moe_decode_m1(pkg, dev):
-    """One int4 MoE layer at M=1: 128 experts, top-8, hidden 2048, FFN 768, AWQ g128."""
+@pytest.mark.parametrize("layouts", ["both", "tile"])
+def test_moe_decode_m1(pkg, dev, layouts):
+    """One int4 MoE layer at M=1: 128 experts, top-8, hidden 2048, FFN 768, AWQ g128; decode
+    on CT rows (layouts="both") or on the tile copy alone (layouts="tile")."""
     rng = np.random.default_rng(21)
-    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng)
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, layouts=layouts)
+    assert moe.gate_up.layout == ("ct" if layouts == "both" else "tile")
     for rep in range(3):
         x = make_x(rng, (1, 2048), "f16")
         _, err = _check_moe(pkg, moe, dgu, ddn, x, "f16", dev,
@@ -320,11 +381,12 @@ def test_moe_decode_m1(pkg, dev):
         assert err <= 1e-3
 
 
-def test_decode_stages_compose_to_the_block(pkg, dev):
+@pytest.mark.parametrize("layouts", ["both", "tile"])
+def test_decode_stages_compose_to_the_block(pkg, dev, layouts):
     """route+gate_up, gate_up(sel) and down+combine reproduce moe_forward at T=1 bit for bit,
     and the stage outputs match the oracle."""
     rng = np.random.default_rng(31)
-    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, E=64)
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, E=64, layouts=layouts)
     x = t_(make_x(rng, (1, 2048), "f16"), dev)
     res = t_(make_x(rng, (1, 2048), "f16"), dev)
     full, sel_f, w_f = pkg.moe_forward(x, moe.gate_up, moe.down, 8, router_w=moe.router_w,
@@ -344,7 +406,8 @@ def test_decode_stages_compose_to_the_block(pkg, dev):
         assert i4ref.rel_err(host(act[j]).astype(np.float64), ref_act) <= 1e-3
 
 
-def test_moe_decode_reference_format(pkg, dev):
+@pytest.mark.parametrize("layouts", ["both", "tile"])
+def test_moe_decode_reference_format(pkg, dev, layouts):
     """The reference checkpoint's own format: CT g32 symmetric, bf16 scales and activations."""
     rng = np.random.default_rng(22)
     E, H, I, G = 128, 2048, 768, 32
@@ -353,7 +416,7 @@ def test_moe_decode_reference_format(pkg, dev):
     wr = i4ref.f32_to_bf16_bits((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
     gu = pkg.QWeight(t_(gp, dev), t_(gs, dev), None, "ct", G, 2 * I, H)
     dn = pkg.QWeight(t_(dp, dev), t_(ds, dev), None, "ct", G, H, I)
-    moe = pkg.FusedPackedMoE.from_stacked(gu, dn, t_(wr, dev), top_k=8)
+    moe = pkg.FusedPackedMoE.from_stacked(gu, dn, t_(wr, dev), top_k=8, layouts=layouts)
     dgu = lambda e: i4ref.ct_dequant(gp[e], f_(gs[e]), H, G)
     ddn = lambda e: i4ref.ct_dequant(dp[e], f_(ds[e]), I, G)
     for _ in range(2):
@@ -393,6 +456,35 @@ def test_moe_mfma_tiles(pkg, dev, xdt):
     counts = np.bincount(i4ref.route(f_(lg), 8)[0].ravel(), minlength=E)
     assert counts.min() >= 16  # all MFMA
     _check_moe(pkg, moe, dgu, ddn, x, xdt, dev, logits=lg, residual=x)
+
+
+@pytest.mark.parametrize("E,T", [(16, 40), (128, 24)])
+def test_moe_prefill_reference_format(pkg, dev, E, T):
+    """The reference checkpoint's own format (CT g32 symmetric, bf16) at T > 1: per-chunk
+    group corrections on the MFMA path, large entries (E = 16: ~20 tokens per expert) and
+    small ones (E = 128)."""
+    rng = np.random.default_rng(33 + E)
+    H, I, G = 2048, 768, 32
+    gp, gs, _ = _gen.ct_weight(rng, E, 2 * I, H, G, sdt="bf16")
+    dp, ds, _ = _gen.ct_weight(rng, E, H, I, G, sdt="bf16")
+    wr = i4ref.f32_to_bf16_bits((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    gu = pkg.QWeight(t_(gp, dev), t_(gs, dev), None, "ct", G, 2 * I, H)
+    dn = pkg.QWeight(t_(dp, dev), t_(ds, dev), None, "ct", G, H, I)
+    moe = pkg.FusedPackedMoE.from_stacked(gu, dn, t_(wr, dev), top_k=8)
+    dgu = lambda e: i4ref.ct_dequant(gp[e], f_(gs[e]), H, G)
+    ddn = lambda e: i4ref.ct_dequant(dp[e], f_(ds[e]), I, G)
+    x = make_x(rng, (T, H), "bf16")
+    _check_moe(pkg, moe, dgu, ddn, x, "bf16", dev, residual=x)
+
+
+def test_moe_prefill_bf16_small_entries(pkg, dev):
+    """bf16 activations with AWQ g128 weights and <= 16 tokens per expert: the small-entry
+    MFMA kernel's activation-sum correction."""
+    rng = np.random.default_rng(35)
+    moe, dgu, ddn, wr = _awq_moe(pkg, dev, rng, sdt="bf16")
+    moe.register_buffer("router_w", moe.router_w.to(torch.bfloat16), persistent=False)
+    x = make_x(rng, (24, 2048), "bf16")
+    _check_moe(pkg, moe, dgu, ddn, x, "bf16", dev)
 
 
 def test_moe_tokens_are_independent(pkg, dev):

@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from oracle import i4ref
+from tests import _gen
 
 GOLD = json.loads((Path(__file__).parent / "golden" / "known_answers.json").read_text())
 
@@ -138,6 +139,37 @@ def test_ct_awq_layout_equivalence():
     # direct element check against the definition
     e, n, k = 1, 5, 200
     assert W_awq[e, n, k] == (Q[e, n, k] - Z[e, n, k // G]) * np.float64(S[e, n, k // G])
+
+
+def test_tile_index_closed_form():
+    """Tile element [e, b, s, r, 4j + t] is CT word 4 (4s + t) + j of row 16b + r."""
+    E, N, K = 2, 32, 256
+    idx = np.arange(E * N * K // 8, dtype=np.int64).reshape(E, N, K // 8).astype(np.int32)
+    sc = np.arange(E * N * 2, dtype=np.float32).reshape(E, N, 2)
+    t, ts, tz = i4ref.tile_pack(idx, sc, sc.astype(np.int32))
+    assert t.shape == (E, N // 16, K // 128, 16, 16) and ts.shape == (E, N // 16, 2, 16)
+    for e, b, s_, r, j, tt in [(0, 0, 0, 0, 0, 0), (1, 1, 1, 15, 3, 3), (0, 1, 0, 7, 2, 1),
+                               (1, 0, 1, 3, 1, 2)]:
+        assert t[e, b, s_, r, 4 * j + tt] == idx[e, 16 * b + r, 4 * (4 * s_ + tt) + j]
+    for e, b, g, r in [(0, 0, 0, 0), (1, 1, 1, 15), (0, 1, 0, 9)]:
+        assert ts[e, b, g, r] == sc[e, 16 * b + r, g] and tz[e, b, g, r] == int(sc[e, 16 * b + r, g])
+    # a lane (r, j) of one 16-byte load holds word j of the four chunks of a superchunk
+    lane = t[0, 0, 1, 5, 8:12]
+    assert list(lane) == [idx[0, 5, 4 * (4 + c) + 2] for c in range(4)]
+
+
+def test_tile_round_trip_and_dequant():
+    rng = np.random.default_rng(5)
+    E, N, K, G = 3, 48, 384, 128
+    p = _gen.words(rng, (E, N, K // 8))
+    sc = rng.uniform(0.002, 0.02, (E, N, K // G)).astype(np.float16)
+    z = _gen.words(rng, (E, N, 1))
+    t = i4ref.tile_pack(p, sc, z)
+    back = i4ref.tile_unpack(*t)
+    np.testing.assert_array_equal(back[0], p)
+    np.testing.assert_array_equal(back[1], sc)
+    np.testing.assert_array_equal(back[2], z)
+    assert i4ref.tile_unpack(*i4ref.tile_pack(p, sc))[2] is None
 
 
 def test_dq_gemv_vs_loops():
