@@ -16,10 +16,15 @@ three layers):
   the stack touches ~470 MB of weights per token out of 7.5 GB resident, well
   beyond the 256 MB Infinity Cache.
 
-Printed: one JSON line with value = us per layer (stack time / 24), plus the
-roofline of the dominant kernel (the decode gate_up + SiLU launch) timed with
-HIP events on the stream it runs on, and a CPU baseline (the reference's CPU
-expert path restated in torch, oracle/cpu_baseline.py) timed on this host.
+Printed: one JSON line with value = us per layer (stack time / 24, median and
+p99 of the per-token times beside it), plus the roofline of the dominant
+kernel (the decode gate_up + SiLU launch) timed with HIP events on the stream
+it runs on, and a CPU baseline (the reference's CPU expert path restated in
+torch, oracle/cpu_baseline.py) timed on this host.  Extra fields time the same
+layer at M = 32 (router from weights) and M = 512 (Zipf-skewed logits) with
+their realised expert histograms, HBM and MFMA fractions, and the dequant-GEMV
+workloads (a 2048 -> 768 GEMV and the four attention projections, individually
+and back to back).
 """
 from __future__ import annotations
 
@@ -37,12 +42,16 @@ sys.path.insert(0, str(ROOT))
 
 E, H, I, TOPK, G = 128, 2048, 768, 8, 128
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
 # algorithmic bytes (AWQ g128 + zeros, fp16 scales)
 B_GATE_UP_EXPERT = 2 * (H * I // 2 + (H // G) * I * 2 + (H // G) * (I // 8) * 4)  # 1,634,304
 B_DOWN_EXPERT = I * H // 2 + (I // G) * H * 2 + (I // G) * (H // 8) * 4            # 817,152
 B_ROUTER = E * H * 2
 B_LAYER = TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + B_ROUTER + 2 * H * 2        # 20,144,128
 B_GATE_UP_LAUNCH = TOPK * B_GATE_UP_EXPERT + H * 2 + TOPK * I * 2
+# HBM bytes per decode gate_up launch measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (calibrated against a device copy; summary under profiles/)
+GATE_UP_TRAFFIC_BYTES = 13_424_000
 
 
 def log(msg: str) -> None:
@@ -76,7 +85,9 @@ def make_layers(pkg, torch, n_layers, dev, seed=1234, keep_first_awq=False):
     return mods, first
 
 
-def time_stack(torch, step, steps, warmup):
+def time_stack(torch, step, steps, warmup, per_step=None):
+    """Mean ms per step between one pair of HIP events around `steps` steps (and the wall
+    clock); with per_step a list, a second pass appends each step's own event time (ms)."""
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -88,6 +99,15 @@ def time_stack(torch, step, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if per_step is not None:
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+        for i, (a, b) in enumerate(evs):
+            a.record()
+            step(warmup + steps + i)
+            b.record()
+        torch.cuda.synchronize()
+        per_step.extend(a.elapsed_time(b) for a, b in evs)
     return e0.elapsed_time(e1) / steps, wall / steps * 1e3
 
 
@@ -155,6 +175,162 @@ def time_gate_up(pkg, torch, dev, mods, xns, logits, rounds):
     return batched, sum(per) / len(per)
 
 
+def awq_gemv_bytes(K, N):
+    """algorithmic bytes of one AWQ g128 GEMV: weights + fp16 scales + zeros + x + fp16 y"""
+    return K * N // 2 + (K // G) * N * 2 + (K // G) * (N // 8) * 4 + 2 * K + 2 * N
+
+
+def graph_times(torch, launches, replays):
+    """Capture launches() (which enqueues on the current stream) in one hipGraph and replay
+    it; returns the per-replay times in microseconds, each from a pair of HIP events on the
+    replay stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launches()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launches()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(replays)]
+    for a, b in evs:
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e3 for a, b in evs]
+
+
+def pct(vals, q):
+    v = sorted(vals)
+    return v[min(len(v) - 1, int(round(q / 100 * (len(v) - 1))))]
+
+
+def time_gemvs(pkg, torch, dev, replays=20):
+    """The dequant-GEMV workloads at decode M = 1, AWQ g128 + zeros, fp16 scales ~ U[0.002,
+    0.02], x ~ N(0, 1), fp16 out:
+      single:    K=2048 -> N=768, 640 distinct weight copies (526 MB, twice the Infinity
+                 Cache) launched back to back;
+      attention: q 2048->4096, k/v 2048->512, o 4096->2048, 64 distinct layer sets (628 MB),
+                 each projection timed on its own (all 64 copies back to back) and the four
+                 of a layer back to back.
+    Each workload runs on the AWQ tensors as the checkpoint holds them (split-K kernel +
+    reduction) and on their CT+zeros repack (one launch, what PackedLinear installs).
+    Times are per GEMV (or per layer of four), mean / median / p99 over graph replays."""
+    from qwen3_omni_duplex_amd import _lib
+
+    lb = pkg.lib()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+
+    def awq_copies(K, N, n):
+        qw = torch.randint(-2**31, 2**31, (n, K, N // 8), dtype=torch.int32, device=dev,
+                           generator=gen)
+        qz = torch.randint(-2**31, 2**31, (n, K // G, N // 8), dtype=torch.int32, device=dev,
+                           generator=gen)
+        sc = (torch.rand(n, K // G, N, device=dev, generator=gen) * 0.018 + 0.002).half()
+        return pkg.QWeight.awq(qw, sc, qz, group=G)
+
+    def per_copy(w):
+        """i4_qweight descriptors of each copy as an E = 1 Linear weight"""
+        c = w.c()
+        pes, ses = w.packed[0].numel() * 4, w.scale[0].numel() * 2
+        zes = w.zeros[0].numel() * 4
+        return [_lib.QWeightC(packed=c.packed + i * pes, scale=c.scale + i * ses,
+                              zeros=c.zeros + i * zes, packed_estride=0, scale_estride=0,
+                              zeros_estride=0, layout=c.layout, group=c.group,
+                              scale_dtype=c.scale_dtype, E=1, N=c.N, K=c.K)
+                for i in range(w.E)]
+
+    class Proj:
+        def __init__(self, K, N, n):
+            self.K, self.N = K, N
+            awq = awq_copies(K, N, n)
+            ct = awq.to_ct()
+            self.desc = {"awq": per_copy(awq), "ct": per_copy(ct)}
+            self.keep = (awq, ct)
+            self.x = torch.randn(1, K, device=dev, generator=gen).half()
+            self.y = torch.empty(1, N, dtype=torch.float16, device=dev)
+            nb = lb.i4_linear_workspace_bytes(ctypes.byref(self.desc["awq"][0]), 1)
+            self.ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
+
+        def launch(self, layout, i):
+            d = self.desc[layout][i]
+            rc = lb.i4_linear(self.x.data_ptr(), _lib.F16, 1, ctypes.byref(d), None,
+                              self.y.data_ptr(), _lib.F16, self.ws.data_ptr(), self.ws.numel(),
+                              torch.cuda.current_stream().cuda_stream)
+            if rc:
+                raise RuntimeError(lb.i4_strerror(rc).decode())
+
+    def stats(times, per, nbytes):
+        t = [v / per for v in times]
+        mean = sum(t) / len(t)
+        return {"us": round(mean, 3), "us_median": round(pct(t, 50), 3),
+                "us_p99": round(pct(t, 99), 3), "GBps": round(nbytes / (mean * 1e-6) / 1e9, 1),
+                "hbm_frac": round(nbytes / (mean * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "bytes": nbytes}
+
+    out = {}
+    n1 = 640
+    single = Proj(2048, 768, n1)
+    nbytes = awq_gemv_bytes(2048, 768)
+    for layout in ("ct", "awq"):
+        ts = graph_times(torch, lambda: [single.launch(layout, i) for i in range(n1)], replays)
+        out[f"single_{layout}"] = stats(ts, n1, nbytes)
+        log(f"GEMV 2048->768 ({layout}): {out[f'single_{layout}']['us']:.2f} us")
+    del single
+    n2 = 64
+    projs = {"q": Proj(2048, 4096, n2), "k": Proj(2048, 512, n2), "v": Proj(2048, 512, n2),
+             "o": Proj(4096, 2048, n2)}
+    for layout in ("ct", "awq"):
+        att = {}
+        for name, p in projs.items():
+            ts = graph_times(torch, lambda p=p: [p.launch(layout, i) for i in range(n2)], replays)
+            att[name] = stats(ts, n2, awq_gemv_bytes(p.K, p.N))
+
+        def layer_seq():
+            for i in range(n2):
+                for p in projs.values():
+                    p.launch(layout, i)
+
+        ts = graph_times(torch, layer_seq, replays)
+        att["qkvo_back_to_back"] = stats(ts, n2, sum(awq_gemv_bytes(p.K, p.N)
+                                                    for p in projs.values()))
+        out[f"attention_{layout}"] = att
+        log(f"attention q/k/v/o ({layout}): " + ", ".join(
+            f"{k} {v['us']:.2f}" for k, v in att.items()) + " us")
+    out["timing"] = ("hipGraph of all copies back to back, HIP events per replay; per-GEMV "
+                     "time = replay / copies; bytes = AWQ g128 weights + scales + zeros + x + y")
+    return out
+
+
+def routing_stats(sels, per_expert_bytes, extra_bytes):
+    """Realised expert histogram of a list of [T, k] selections: distinct experts hit,
+    tokens per hit expert, and the layer's algorithmic bytes (distinct experts' weights)."""
+    import torch
+
+    hits, mx, over64, over16, low = [], [], [], [], []
+    for sel in sels:
+        cnt = torch.bincount(sel.reshape(-1).long().cpu(), minlength=E)
+        hits.append(int((cnt > 0).sum()))
+        mx.append(int(cnt.max()))
+        over64.append(int((cnt > 64).sum()))
+        over16.append(int((cnt > 16).sum()))
+        low.append(int((cnt <= 2).sum()))
+    n = len(sels)
+    avg = lambda v: round(sum(v) / n, 2)
+    d = avg(hits)
+    return {"experts_hit": d, "max_tokens_per_expert": avg(mx), "experts_over_64": avg(over64),
+            "experts_over_16": avg(over16), "experts_0_to_2": avg(low),
+            "bytes": int(d * per_expert_bytes + extra_bytes)}
+
+
 def cpu_baseline(torch, first, xs, seconds):
     from oracle import cpu_baseline as cb
 
@@ -187,6 +363,10 @@ def main() -> int:
     ap.add_argument("--prefill", action=argparse.BooleanOptionalAction, default=True,
                     help="also time the M=32 and M=512 workloads (reported as extra fields)")
     ap.add_argument("--eager", action="store_true", help="time without a hipGraph")
+    ap.add_argument("--gemv", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the single and attention-projection dequant-GEMVs")
+    ap.add_argument("--replays", type=int, default=20,
+                    help="graph replays per timed GEMV / prefill workload")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 device copies of 64 MiB (calibrates the FETCH_SIZE / "
                          "WRITE_SIZE counters against a copy of known size) and exit")
@@ -239,7 +419,9 @@ def main() -> int:
         if rc:
             raise RuntimeError(lb.i4_strerror(rc).decode())
 
-    ms_eager, wall_eager = time_stack(torch, eager_step, args.steps, args.warmup)
+    per_token = []  # ms of each token through the stack (the timed path's own events)
+    ms_eager, wall_eager = time_stack(torch, eager_step, args.steps, args.warmup,
+                                      per_token if args.eager else None)
     log(f"eager: {ms_eager:.3f} ms/token ({ms_eager * 1e3 / args.layers:.2f} us/layer)")
 
     # ---- hipGraph: the 96 launches of one token captured once, replayed per token
@@ -259,7 +441,7 @@ def main() -> int:
             static_x.copy_(xs[i % P])
             graph.replay()
 
-        ms_graph, _ = time_stack(torch, graph_step, args.steps, args.warmup)
+        ms_graph, _ = time_stack(torch, graph_step, args.steps, args.warmup, per_token)
         # the replay computes what the eager path computes
         graph_step(5)
         eager_step(5)
@@ -302,26 +484,47 @@ def main() -> int:
                         - torch.log(-torch.log(torch.rand(T, E, device=dev, generator=gen2))))
                        .half() for _ in range(4)]
             wsT = pkg.Workspace()
+            nl = len(mods)
+            # layer li takes input li % 4: one replay = every layer once, routing and hence
+            # the expert histogram differ from layer to layer
+            sels = []
+            for li, m in enumerate(mods):
+                lg = (ops.router_logits(xT[li % 4], m.router_w) if lgT is None else lgT[li % 4])
+                sels.append(ops.route(lg, TOPK)[1])
+            rs = routing_stats(sels, B_GATE_UP_EXPERT + B_DOWN_EXPERT,
+                               (B_ROUTER if lgT is None else 0) + 2 * 2 * H * T)
 
-            def run_T(i, T=T, xT=xT, lgT=lgT, wsT=wsT):
-                m = mods[i % len(mods)]
-                tiles = dict(gate_up_tile=m.gate_up_tile, down_tile=m.down_tile)
-                if lgT is None:
-                    ops.moe_forward(xT[i % 4], m.gate_up, m.down, TOPK, router_w=m.router_w,
-                                    residual=xT[i % 4], workspace=wsT, **tiles)
-                else:
-                    ops.moe_forward(xT[i % 4], m.gate_up, m.down, TOPK, logits=lgT[i % 4],
-                                    residual=xT[i % 4], workspace=wsT, **tiles)
+            def run_all(T=T, xT=xT, lgT=lgT, wsT=wsT):
+                for li, m in enumerate(mods):
+                    tiles = dict(gate_up_tile=m.gate_up_tile, down_tile=m.down_tile)
+                    x = xT[li % 4]
+                    if lgT is None:
+                        ops.moe_forward(x, m.gate_up, m.down, TOPK, router_w=m.router_w,
+                                        residual=x, workspace=wsT, **tiles)
+                    else:
+                        ops.moe_forward(x, m.gate_up, m.down, TOPK, logits=lgT[li % 4],
+                                        residual=x, workspace=wsT, **tiles)
 
-            reps = 48
-            ms_T, _ = time_stack(torch, run_T, reps, 8)
+            ts = [t / nl for t in graph_times(torch, run_all, args.replays)]
+            us_T = sum(ts) / len(ts)
             flops = T * TOPK * 3 * 2 * H * I
-            prefill[f"M{T}"] = {"us_per_layer": round(ms_T * 1e3, 2),
-                                "tokens_per_s": round(T / (ms_T * 1e-3), 1),
-                                "expert_TFLOPs": round(flops / (ms_T * 1e-3) / 1e12, 2),
-                                "routing": "router weights" if lgT is None else
-                                           "Zipf(1.1), tau 2 logits"}
-            log(f"M={T}: {ms_T * 1e3:.1f} us/layer, {flops / (ms_T * 1e-3) / 1e12:.1f} TFLOP/s")
+            tf = flops / (us_T * 1e-6) / 1e12
+            gbs = rs["bytes"] / (us_T * 1e-6) / 1e9
+            prefill[f"M{T}"] = {
+                "us_per_layer": round(us_T, 2), "us_median": round(pct(ts, 50), 2),
+                "us_p99": round(pct(ts, 99), 2),
+                "tokens_per_s": round(T / (us_T * 1e-6), 1),
+                "expert_TFLOPs": round(tf, 2), "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                "routing": ("router weights, x ~ N(0, 1)" if lgT is None else
+                            "logits -1.1 tau ln(rank) + Gumbel, tau 2"),
+                "realised": rs,
+                "timing": f"hipGraph of the {nl} layers (input li % 4), mean over "
+                          f"{args.replays} replays"}
+            log(f"M={T}: {us_T:.1f} us/layer, {tf:.1f} TFLOP/s, {gbs:.0f} GB/s, "
+                f"{rs['experts_hit']} experts hit")
+
+    gemv = time_gemvs(pkg, torch, dev, args.replays) if args.gemv else None
 
     # ---- CPU baseline
     cpu = None
@@ -355,17 +558,20 @@ def main() -> int:
         },
         "tokens_per_s": round(1e3 / ms, 1),
         "us_per_layer_eager": round(ms_eager * 1e3 / args.layers, 3),
+        "us_per_layer_median": round(pct(per_token, 50) * 1e3 / args.layers, 3),
+        "us_per_layer_p99": round(pct(per_token, 99) * 1e3 / args.layers, 3),
         "layer_GBps": round(B_LAYER / (us_layer * 1e-6) / 1e9, 1),
         "layer_hbm_frac": round(B_LAYER / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": "k_moe_gate_up<route> (decode top-8 routing + gate/up + SiLU, 8 experts)",
+            "kernel": "k_ct_gate_up<route> (decode top-8 routing + gate/up + SiLU, 8 experts)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
             "bytes_per_launch": B_GATE_UP_LAUNCH, "us_per_launch": round(k_us, 3),
             "us_per_launch_own_events": round(k_evt, 3),
         },
         "cpu_baseline": cpu,
         "other_workloads": prefill,
+        "gemv": gemv,
     }
     print(json.dumps(res), flush=True)
     return 0
