@@ -46,7 +46,10 @@
  *                    contiguous memory (16 rows x 4 k-groups):
  *                      packed [E][N/16][K/128][16][4][4] int32, element
  *                             [e][b][s][r][j][t] = CT word 4 (4s + t) + j of
- *                             row 16b + r;
+ *                             row 16b + r with its nibbles interleaved: slot
+ *                             i holds column 8m + {0,2,4,6,1,3,5,7}[i] (the
+ *                             AWQ order), so nibbles i and i + 4 are two
+ *                             adjacent columns;
  *                      scale  [E][N/16][NG][16], element [e][b][g][r] = CT
  *                             scale of row 16b + r, group g;
  *                      zeros  NULL or [E][N/16][ceil(NG/8)][16] int32, the CT
@@ -64,7 +67,7 @@
 extern "C" {
 #endif
 
-#define I4_ABI_VERSION 2
+#define I4_ABI_VERSION 3
 
 /* status codes */
 #define I4_OK               0

@@ -148,17 +148,40 @@ def awq_to_ct(qweight, qzeros, scales, group):
 # The library's tile layout (I4_LAYOUT_TILE in include/i4moe.h).  No reference
 # counterpart: a permutation of the CT words, pinned by its closed form
 # (test_tile_index_closed_form) and its round trip.
+TILE_NIBBLE_ORDER = AWQ_ORDER  # tile word nibble slot i holds column 8m + order[i]
+
+
+def interleave_words(words, order=TILE_NIBBLE_ORDER) -> np.ndarray:
+    """CT words (nibble i = column 8m + i) -> words whose slot i holds column 8m + order[i]."""
+    w = np.asarray(words).astype(np.int64) & 0xFFFFFFFF
+    out = np.zeros_like(w)
+    for i, c in enumerate(order):
+        out |= ((w >> (4 * c)) & 0xF) << (4 * i)
+    return out.astype(np.uint32).view(np.int32)
+
+
+def deinterleave_words(words, order=TILE_NIBBLE_ORDER) -> np.ndarray:
+    """Inverse of interleave_words."""
+    w = np.asarray(words).astype(np.int64) & 0xFFFFFFFF
+    out = np.zeros_like(w)
+    for i, c in enumerate(order):
+        out |= ((w >> (4 * i)) & 0xF) << (4 * c)
+    return out.astype(np.uint32).view(np.int32)
+
+
 def tile_pack(packed, scale, zeros=None):
     """CT (packed [E, N, K/8], scale [E, N, NG], zeros [E, N, NZW] or None) -> tile.
 
     packed -> [E, N/16, K/128, 16, 16]: element [e, b, s, r, 4j + t] is CT word
-    4 (4s + t) + j of row 16b + r; scale -> [E, N/16, NG, 16]; zeros ->
-    [E, N/16, NZW, 16] (element [e, b, g, r] = CT element [e, 16b + r, g]).
+    4 (4s + t) + j of row 16b + r with its nibbles interleaved (slot i holds
+    column 8m + (0, 2, 4, 6, 1, 3, 5, 7)[i]); scale -> [E, N/16, NG, 16]; zeros
+    -> [E, N/16, NZW, 16] (element [e, b, g, r] = CT element [e, 16b + r, g],
+    zero words unchanged).
     """
     p = np.asarray(packed)
     E, N, KW = p.shape
     SC = KW // 16
-    t = p.reshape(E, N // 16, 16, SC, 4, 4)            # [e, b, r, s, t, j]
+    t = interleave_words(p).reshape(E, N // 16, 16, SC, 4, 4)   # [e, b, r, s, t, j]
     t = t.transpose(0, 1, 3, 2, 5, 4).reshape(E, N // 16, SC, 16, 16)
 
     def rows(a):
@@ -173,6 +196,7 @@ def tile_unpack(packed, scale, zeros=None):
     p = np.asarray(packed)
     E, NB, SC = p.shape[:3]
     c = p.reshape(E, NB, SC, 16, 4, 4).transpose(0, 1, 3, 2, 5, 4).reshape(E, NB * 16, SC * 16)
+    c = deinterleave_words(c)
 
     def rows(a):
         a = np.asarray(a)

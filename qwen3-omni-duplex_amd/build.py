@@ -30,13 +30,18 @@ FLAGS = [
 ]
 
 
+# per-source flags: the MFMA kernels keep their accumulators in VGPRs (the
+# group corrections read them every superchunk; AGPRs would need a move each way)
+EXTRA = {"i4_moe_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")

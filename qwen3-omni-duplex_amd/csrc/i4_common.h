@@ -34,6 +34,18 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // 16-byte global load (global_load_dwordx4) of a packed-weight stream
 __device__ inline u32x4 ldg16(const void* p) { return *(const u32x4*)p; }
 
+// The nibble decode computes (w & mask) | magic.  A gfx9 VOP3 instruction
+// reads at most one SGPR and takes no literal, so with both operands constant
+// the compiler emits v_and_b32 + v_or_b32; with the magic in a VGPR it is one
+// v_and_or_b32.  magic_v() puts it there once, at kernel entry, in a way the
+// optimizer cannot fold back into a constant; the decode itself stays plain
+// code, so the compiler tracks every hazard around it.
+__device__ inline u32 vgpr_const(u32 c) {
+  u32 r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(c));
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // half-precision codecs, selected by the I4_F16 / I4_BF16 dtype code
 template <int DT> struct Half;
@@ -146,21 +158,24 @@ template <int OT> __device__ inline void store_out(void* p, int64_t i, float v) 
 // ---------------------------------------------------------------------------
 // nibble decode + dot of one CT word (8 columns) against its 4 staged x pairs;
 // lo / hi accumulate the pairs as described at the top of this file.
-template <int XT> __device__ inline void dot8(u32 w, u32x4 xp, float& lo, float& hi) {
-  constexpr u32 MK = 0x000F000Fu, MG = Half<XT>::MAGIC2;
+template <int XT> __device__ inline void dot8(u32 w, u32x4 xp, float& lo, float& hi, u32 mg) {
+  constexpr u32 MK = 0x000F000Fu;
   if constexpr (XT == I4_F16) {
     const u32 t = w >> 8;
-    lo = Half<XT>::dot2((w & MK) | MG, xp.x, lo);
-    hi = Half<XT>::dot2((w & 0x00F000F0u) | MG, xp.y, hi);
-    lo = Half<XT>::dot2((t & MK) | MG, xp.z, lo);
-    hi = Half<XT>::dot2((t & 0x00F000F0u) | MG, xp.w, hi);
+    lo = Half<XT>::dot2((w & MK) | mg, xp.x, lo);
+    hi = Half<XT>::dot2((w & 0x00F000F0u) | mg, xp.y, hi);
+    lo = Half<XT>::dot2((t & MK) | mg, xp.z, lo);
+    hi = Half<XT>::dot2((t & 0x00F000F0u) | mg, xp.w, hi);
   } else {
-    lo = Half<XT>::dot2((w & MK) | MG, xp.x, lo);
-    hi = Half<XT>::dot2(((w >> 4) & MK) | MG, xp.y, hi);
-    lo = Half<XT>::dot2(((w >> 8) & MK) | MG, xp.z, lo);
-    hi = Half<XT>::dot2(((w >> 12) & MK) | MG, xp.w, hi);
+    lo = Half<XT>::dot2((w & MK) | mg, xp.x, lo);
+    hi = Half<XT>::dot2(((w >> 4) & MK) | mg, xp.y, hi);
+    lo = Half<XT>::dot2(((w >> 8) & MK) | mg, xp.z, lo);
+    hi = Half<XT>::dot2(((w >> 12) & MK) | mg, xp.w, hi);
   }
 }
+
+// the decode magic of activation dtype XT in a VGPR (see vgpr_const)
+template <int XT> __device__ inline u32 magic_v() { return vgpr_const(Half<XT>::MAGIC2); }
 
 // hi-pair weight of the fp16 decode (its pairs carry 16q)
 template <int XT> constexpr float hi_scale() { return XT == I4_F16 ? 1.0f / 16.0f : 1.0f; }
@@ -169,12 +184,12 @@ template <int XT> constexpr float hi_scale() { return XT == I4_F16 ? 1.0f / 16.0
 // (xw0..xw3, pair order) and its sums (Sb, S)
 template <int XT, int ST>
 __device__ inline float chunk_dot(const Chunk& k, u32x4 xw0, u32x4 xw1, u32x4 xw2, u32x4 xw3,
-                                  float2 sums, int c, int gshift) {
+                                  float2 sums, int c, int gshift, u32 mg) {
   float lo = 0.f, hi = 0.f;
-  dot8<XT>(k.w.x, xw0, lo, hi);
-  dot8<XT>(k.w.y, xw1, lo, hi);
-  dot8<XT>(k.w.z, xw2, lo, hi);
-  dot8<XT>(k.w.w, xw3, lo, hi);
+  dot8<XT>(k.w.x, xw0, lo, hi, mg);
+  dot8<XT>(k.w.y, xw1, lo, hi, mg);
+  dot8<XT>(k.w.z, xw2, lo, hi, mg);
+  dot8<XT>(k.w.w, xw3, lo, hi, mg);
   const int g = c >> gshift;
   const float z = (float)((k.z >> (4 * (g & 7))) & 15u);
   const float a = fmaf(hi, hi_scale<XT>(), lo);
@@ -200,6 +215,18 @@ template <int XT> __device__ inline float2 sum8(u32x4 d) {
   const float x4 = Half<XT>::to_f32((uint16_t)(d.z & 0xFFFF)), x5 = Half<XT>::to_f32((uint16_t)(d.z >> 16));
   const float x6 = Half<XT>::to_f32((uint16_t)(d.w & 0xFFFF)), x7 = Half<XT>::to_f32((uint16_t)(d.w >> 16));
   const float slo = ((x0 + x4) + (x2 + x6)), shi = ((x1 + x5) + (x3 + x7));
+  return make_float2(fmaf(shi, hi_scale<XT>(), slo), slo + shi);
+}
+
+// (Sb, S) of 8 consecutive half values in their natural order, for words whose
+// nibbles are interleaved (I4_LAYOUT_TILE): decode pair p then covers x
+// dword p, so the "lo" pairs are dwords 0 and 2, the "hi" pairs dwords 1 and 3
+template <int XT> __device__ inline float2 sum8n(u32x4 d) {
+  const float x0 = Half<XT>::to_f32((uint16_t)(d.x & 0xFFFF)), x1 = Half<XT>::to_f32((uint16_t)(d.x >> 16));
+  const float x2 = Half<XT>::to_f32((uint16_t)(d.y & 0xFFFF)), x3 = Half<XT>::to_f32((uint16_t)(d.y >> 16));
+  const float x4 = Half<XT>::to_f32((uint16_t)(d.z & 0xFFFF)), x5 = Half<XT>::to_f32((uint16_t)(d.z >> 16));
+  const float x6 = Half<XT>::to_f32((uint16_t)(d.w & 0xFFFF)), x7 = Half<XT>::to_f32((uint16_t)(d.w >> 16));
+  const float slo = ((x0 + x1) + (x4 + x5)), shi = ((x2 + x3) + (x6 + x7));
   return make_float2(fmaf(shi, hi_scale<XT>(), slo), slo + shi);
 }
 

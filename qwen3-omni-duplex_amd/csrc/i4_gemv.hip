@@ -56,6 +56,7 @@ __global__ __launch_bounds__(WG) void k_gemv_ct(
   rp.s = scale_at<ST>(scale, e * s_es + (int64_t)nn * NG);
   rp.z = zeros ? (const u32*)zeros + e * z_es + (int64_t)nn * NZW : kSymZeros;
   const uint16_t* xrow = x + (int64_t)j * x_stride;
+  const u32 mg = magic_v<XT>();
   Stager<XT> st(1, K);  // activation loads first, weight loads behind them
   auto row_of = [&](int) { return xrow; };
   st.issue(row_of, 0);
@@ -75,7 +76,7 @@ __global__ __launch_bounds__(WG) void k_gemv_ct(
       const int c = cl + (r0 + i) * L;
       if (c < C)
         row += chunk_dot<XT, ST>(ch[i], xs[c], xs[C + c], xs[2 * C + c], xs[3 * C + c], sums[c], c,
-                                 gshift);
+                                 gshift, mg);
     }
   }
   row = group_sum<L>(row);
@@ -138,7 +139,8 @@ __global__ __launch_bounds__(WG) void k_gemv_awq(
   float acc_tot[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc_tot[i] = 0.f;
-  constexpr u32 MK = 0x000F000Fu, MG = Half<XT>::MAGIC2;
+  constexpr u32 MK = 0x000F000Fu;
+  const u32 mg = magic_v<XT>();
   const u32 ONE2 = XT == I4_F16 ? 0x3C003C00u : 0x3F803F80u;  // (1.0, 1.0)
   for (int gk = k0; gk < kend; gk += group) {  // one quantisation group
     const int g = gk / group;
@@ -158,8 +160,8 @@ __global__ __launch_bounds__(WG) void k_gemv_awq(
           // byte b of w0 -> bits 0..7, byte b of w1 -> bits 16..23
           const u32 sel_b = 0x0C000C00u | (u32)(b) | ((u32)(4 + b) << 16);
           const u32 tb = __builtin_amdgcn_perm(w1, w0, sel_b);
-          acc[2 * b] = Half<XT>::dot2((tb & MK) | MG, xp, acc[2 * b]);
-          acc[2 * b + 1] = Half<XT>::dot2(((tb >> 4) & MK) | MG, xp, acc[2 * b + 1]);
+          acc[2 * b] = Half<XT>::dot2((tb & MK) | mg, xp, acc[2 * b]);
+          acc[2 * b + 1] = Half<XT>::dot2(((tb >> 4) & MK) | mg, xp, acc[2 * b + 1]);
         }
       }
     }
@@ -234,7 +236,7 @@ __device__ inline void nib_and_zero(const WView& w, int e, int n, int k, int& q,
     const int SC = w.K >> 7, NZW = (NG + 7) >> 3, b = n >> 4, r = n & 15, c = k >> 5;
     const u32 word = (u32)w.packed[e * w.pes + (((int64_t)b * SC + (c >> 2)) * 16 + r) * 16 +
                                    ((k >> 3) & 3) * 4 + (c & 3)];
-    q = (word >> (4 * (k & 7))) & 15;
+    q = (word >> (4 * awq_slot_of_col(k & 7))) & 15;  // interleaved nibbles
     z = w.zeros ? ((u32)w.zeros[e * w.zes + ((int64_t)b * NZW + (g >> 3)) * 16 + r] >>
                    (4 * (g & 7))) & 15
                 : 8;
@@ -348,7 +350,8 @@ __global__ __launch_bounds__(WG) void k_repack_awq(WView w, int32_t* __restrict_
 }
 
 // CT or AWQ -> TILE, one thread per destination-ordered source item: the
-// CT word m of (e, n), then the scales and the zero words of (e, n).
+// word m of (e, n) with its nibbles interleaved, then the scales and the zero
+// words of (e, n).
 __global__ __launch_bounds__(WG) void k_repack_tile(WView w, int32_t* __restrict__ dp,
                                                     void* __restrict__ ds,
                                                     int32_t* __restrict__ dz, int dst_rows,
@@ -364,12 +367,12 @@ __global__ __launch_bounds__(WG) void k_repack_tile(WView w, int32_t* __restrict
     const int m = (int)(i % KW);
     const int64_t en = i / KW;
     const int n = (int)(en % w.N), e = (int)(en / w.N);
-    u32 word = 0;
+    u32 word = 0;  // column 8m + b in the AWQ nibble slot of b (interleaved)
     for (int b = 0; b < 8; ++b) {
       int q, z;
       float s;
       nib_and_zero(w, e, n, 8 * m + b, q, z, s);
-      word |= (u32)q << (4 * b);
+      word |= (u32)q << (4 * awq_slot_of_col(b));
     }
     const int dn = row_off + n, c = m >> 2, j = m & 3;
     dp[((((int64_t)e * DB + (dn >> 4)) * SC + (c >> 2)) * 16 + (dn & 15)) * 16 + j * 4 + (c & 3)] =

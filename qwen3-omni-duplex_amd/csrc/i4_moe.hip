@@ -17,7 +17,9 @@
 // order): experts with <= 16 tokens become one small entry, larger ones
 // entries of <= 64 tokens, so each weight tile is streamed once per entry
 // instead of once per token (the reference loops over tokens,
-// fused_packed_moe.py:231).  The MFMA kernels are in i4_moe_mfma.hip.
+// fused_packed_moe.py:231).  With T <= 64 every expert is cut into small
+// entries and the large-entry launches are skipped.  The MFMA kernels are in
+// i4_moe_mfma.hip.
 #include "i4_common.h"
 #include "i4_launch.h"
 #include "i4_moe_launch.h"
@@ -221,10 +223,10 @@ struct MoeOps {
   int (*gate_up_ct)(const GateUpArgs&, const TW&, int, hipStream_t);
   int (*down_m1_ct)(const void*, int, const int32_t*, const float*, const TW&, const void*, void*,
                     hipStream_t);
-  int (*mfma_gate_up)(bool, int, const void*, int, const int4*, const int*, const int32_t*,
+  int (*mfma_gate_up)(bool, int, const void*, int, int, const int4*, const int*, const int32_t*,
                       const TW&, int, void*, hipStream_t);
-  int (*mfma_down)(bool, int, const void*, const int4*, const int*, const int32_t*, const TW&,
-                   float*, hipStream_t);
+  int (*mfma_down)(bool, int, const void*, int, const int4*, const int*, const int32_t*,
+                   const TW&, float*, hipStream_t);
 };
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
@@ -338,20 +340,32 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   const int Tk = T * topk;
   const int TW_ = (T + 31) / 32;
   const size_t glds = (size_t)2 * E * TW_ * 4 + (size_t)E * 4;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E, MF_SMALL, MF_SMALL,
-                     ws.perm, ws.entries, ws.n_entries, ws.mf_entries, ws.n_mf_entries);
+  // T <= MF_TOK: no expert has more tokens than one large entry holds, and
+  // small entries of <= MF_SMALL tokens cover every expert in one launch per
+  // projection; above, experts with > MF_SMALL tokens take large entries
+  const bool one_list = T <= MF_TOK;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E,
+                     one_list ? T : MF_SMALL, MF_SMALL, ws.perm, ws.entries, ws.n_entries,
+                     ws.mf_entries, ws.n_mf_entries);
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
-  const int max_s = E < Tk ? E : Tk;  // one small entry per expert at most
+  // entry counts: sum over experts of ceil(n_e / 16) <= min(E, Tk) + Tk / 16
+  const int max_s = (E < Tk ? E : Tk) + (one_list ? Tk / MF_SMALL : 0);
   const int max_b = (E < Tk / (MF_SMALL + 1) ? E : Tk / (MF_SMALL + 1)) + Tk / MF_TOK + 1;
-  rc = ops.mfma_gate_up(true, max_s, x, topk, ws.entries, ws.n_entries, ws.perm, tgu, I, ws.act, s);
-  if (rc) return rc;
-  rc = ops.mfma_gate_up(false, max_b, x, topk, ws.mf_entries, ws.n_mf_entries, ws.perm, tgu, I,
+  rc = ops.mfma_gate_up(true, max_s, x, T, topk, ws.entries, ws.n_entries, ws.perm, tgu, I,
                         ws.act, s);
   if (rc) return rc;
-  rc = ops.mfma_down(true, max_s, ws.act, ws.entries, ws.n_entries, ws.perm, tdn, ws.ys, s);
+  if (!one_list) {
+    rc = ops.mfma_gate_up(false, max_b, x, T, topk, ws.mf_entries, ws.n_mf_entries, ws.perm, tgu,
+                          I, ws.act, s);
+    if (rc) return rc;
+  }
+  rc = ops.mfma_down(true, max_s, ws.act, Tk, ws.entries, ws.n_entries, ws.perm, tdn, ws.ys, s);
   if (rc) return rc;
-  rc = ops.mfma_down(false, max_b, ws.act, ws.mf_entries, ws.n_mf_entries, ws.perm, tdn, ws.ys, s);
-  if (rc) return rc;
+  if (!one_list) {
+    rc = ops.mfma_down(false, max_b, ws.act, Tk, ws.mf_entries, ws.n_mf_entries, ws.perm, tdn,
+                       ws.ys, s);
+    if (rc) return rc;
+  }
   const int64_t tot = (int64_t)T * H;
   dim3 cg((unsigned)((tot + WG - 1) / WG));
 #define I4_COMB_CASE(XT_, KM_)                                                                 \

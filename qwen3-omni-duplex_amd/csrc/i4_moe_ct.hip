@@ -67,6 +67,7 @@ __global__ __launch_bounds__(WG) void k_ct_gate_up(
   float2* sums = (float2*)(lds + (size_t)MT * H * 2);
 
   const int pos0 = blockIdx.y, cnt = 1;
+  const u32 mg = magic_v<XT>();
   Stager<XT> st(MT, H);
   auto row_of = [&](int) -> const uint16_t* { return x; };
   int e;
@@ -121,8 +122,8 @@ __global__ __launch_bounds__(WG) void k_ct_gate_up(
             const u32x4* xt = xs + (size_t)t * 4 * C;
             const u32x4 x0 = xt[c], x1 = xt[C + c], x2 = xt[2 * C + c], x3 = xt[3 * C + c];
             const float2 sm = sums[t * C + c];
-            ag[t] += chunk_dot<XT, ST>(cg[i], x0, x1, x2, x3, sm, c, w.gshift);
-            au[t] += chunk_dot<XT, ST>(cu[i], x0, x1, x2, x3, sm, c, w.gshift);
+            ag[t] += chunk_dot<XT, ST>(cg[i], x0, x1, x2, x3, sm, c, w.gshift, mg);
+            au[t] += chunk_dot<XT, ST>(cu[i], x0, x1, x2, x3, sm, c, w.gshift, mg);
           }
         }
       }
@@ -184,6 +185,7 @@ __global__ __launch_bounds__(WG) void k_ct_down_m1(
   const bool comb = (int)threadIdx.x < RW && on < H;
   const uint16_t res_raw = *(residual ? residual + min(on, H - 1) : act);
   // activations next (all selected rows, contiguous act[j][I])
+  const u32 mg = magic_v<XT>();
   Stager<XT> st(topk, I);
   auto row_of = [&](int j) { return act + (int64_t)j * I; };
   st.issue(row_of, 0);
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(WG) void k_ct_down_m1(
           const int c = cl + (r0 + i) * L;
           if (c < C)
             row[jj] += chunk_dot<XT, ST>(ch[jj][i], xj[c], xj[C + c], xj[2 * C + c], xj[3 * C + c],
-                                         sums[j * C + c], c, w.gshift);
+                                         sums[j * C + c], c, w.gshift, mg);
         }
       }
     }

@@ -37,6 +37,7 @@ __global__ __launch_bounds__(256) void k_tile_gate_up(
   float2* sums = (float2*)(lds + (size_t)H * 2);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 15, kb = lane >> 4;
 
+  const u32 mg = magic_v<XT>();
   TStager<XT> st(1, H);
   auto row_of = [&](int) -> const uint16_t* { return x; };
   int e;
@@ -82,8 +83,8 @@ __global__ __launch_bounds__(256) void k_tile_gate_up(
   for (int i = 0; i < SPW; ++i) {
     const int s = wave + 4 * i;
     if (s < SC) {
-      ag += tile_dot<XT, ST, GB>(sg[i], xj, sj, s, w.gshift);
-      au += tile_dot<XT, ST, GB>(su[i], xj, sj, s, w.gshift);
+      ag += tile_dot<XT, ST, GB>(sg[i], xj, sj, s, w.gshift, mg);
+      au += tile_dot<XT, ST, GB>(su[i], xj, sj, s, w.gshift, mg);
     }
   }
   ag = kgroup_sum(ag);
@@ -121,6 +122,7 @@ __global__ __launch_bounds__(256) void k_tile_down_m1(
   const float wv = wts[min((int)threadIdx.x, topk - 1)];
   const int on = 16 * blockIdx.x + (int)threadIdx.x;  // output row of the combine threads
   const uint16_t res_raw = *(residual ? residual + min(on, w.N - 1) : act);
+  const u32 mg = magic_v<XT>();
   TStager<XT> st(topk, I);
   auto row_of = [&](int j) { return act + (int64_t)j * I; };
   st.issue(row_of, 0);
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(256) void k_tile_down_m1(
         const float2* sj = sums + (4 * j + kb) * C;
 #pragma unroll
         for (int b = 0; b < SCB; ++b)
-          if (s0 + b < SC) acc[jj] += tile_dot<XT, ST, GB>(sl[jj][b], xj, sj, s0 + b, w.gshift);
+          if (s0 + b < SC) acc[jj] += tile_dot<XT, ST, GB>(sl[jj][b], xj, sj, s0 + b, w.gshift, mg);
       }
     }
   }

@@ -44,14 +44,14 @@ int launch_down_m1_ct(const void* act, int topk, const int32_t* sel, const float
 // Grouped (T > 1) expert projections on MFMA.  entries[i] = {expert, first
 // position, tokens, 0} of the expert-sorted (token, slot) list perm; small
 // entries have <= MF_SMALL tokens, large ones <= MF_TOK.
-//   gate_up: act[pos] = silu(gate(x[perm[pos] / topk])) * up(...)
-//   down:    ys[perm[pos]] = down(act[pos]) (fp32)
+//   gate_up: act[pos] = silu(gate(x[perm[pos] / topk])) * up(...), x [T][H]
+//   down:    ys[perm[pos]] = down(act[pos]) (fp32), act [rows][I]
 template <int XT, int ST>
-int launch_mfma_gate_up(bool small, int max_entries, const void* x, int topk, const int4* ent,
-                        const int* nent, const int32_t* perm, const TW& w, int I, void* act,
-                        hipStream_t s);
+int launch_mfma_gate_up(bool small, int max_entries, const void* x, int T, int topk,
+                        const int4* ent, const int* nent, const int32_t* perm, const TW& w, int I,
+                        void* act, hipStream_t s);
 template <int XT, int ST>
-int launch_mfma_down(bool small, int max_entries, const void* act, const int4* ent,
+int launch_mfma_down(bool small, int max_entries, const void* act, int rows, const int4* ent,
                      const int* nent, const int32_t* perm, const TW& w, float* ys, hipStream_t s);
 
 }  // namespace i4

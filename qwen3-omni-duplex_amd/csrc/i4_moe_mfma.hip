@@ -6,8 +6,9 @@
 // (l % 16, l / 16) supplies A[m = r][8 columns] and B[8 columns][n = r] and
 // receives D[4 j + i][r], i < 4.  MFMA step t of superchunk s contracts chunk
 // 4s + t: B is word j of that chunk (component t of the lane's 16-byte tile
-// word) decoded to 8 halves in the (c, c+4) pair order, A the same 8 columns
-// of the token (k = 128 s + 32 t + 8 j) permuted to match.
+// word) decoded to 8 halves, A the same 8 columns of the token (k = 128 s +
+// 32 t + 8 j) as they lie in memory: the tile word's interleaved nibbles put
+// the decoded halves in column order.
 //   fp16: B holds q - z exactly ((M + q) - (M + z), one packed half add per
 //         pair) and a group ends with res += s D.
 //   bf16: B holds M + q exactly (gfx950 has no packed bf16 add) and a group
@@ -15,12 +16,19 @@
 //         activations over the group.
 // Every product is exact and accumulation is fp32, as in the decode kernels.
 //
+// All global reads are raw buffer loads: one descriptor per operand (an
+// expert's weights, scales and zero words; the activation rows), per-lane
+// offsets computed once, and the superchunk / group offsets in scalar
+// registers, so the loop spends no vector instructions on addresses.  A
+// weight without zero points reads its zero words through an empty
+// descriptor (every load returns 0) and ORs in the symmetric 0x88888888.
+//
 // k_tile_mfma_s (entries of <= 16 tokens, one m-block): every lane loads its
-// own A words straight from global memory (the four waves of a workgroup hit
-// the same L1 lines), no LDS and no barrier; the weights and activations of
-// the next two superchunks are in flight while one is multiplied (three-slot
-// register ring, unrolled so every slot index is static, loads issued
-// unconditionally so that the waits before each use stay partial).
+// own A words (the four waves of a workgroup hit the same L1 lines), no LDS
+// and no barrier; the weights and activations of the next two superchunks
+// are in flight while one is multiplied (three-slot register ring, unrolled
+// so every slot index is static, loads issued unconditionally so that the
+// waits before each use stay partial).
 // k_tile_mfma (entries of <= 64 tokens): the activation tile of a superchunk
 // is staged once per workgroup in LDS (double buffered, token stride 272 B so
 // the 16 tokens of an MFMA fall on distinct banks), weights in the same
@@ -38,6 +46,25 @@ static constexpr int MF_TSTRIDE = 17;  // uint4 per staged token row (16 + 1 pad
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// word 3 of a gfx9 buffer descriptor for raw (untyped) dword loads
+static constexpr int kRawBuffer = 0x00020000;
+
+__device__ inline rsrc_t rsrc(const void* base, u32 bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRawBuffer);
+}
+__device__ inline u32x4 bload16(rsrc_t r, u32 voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ inline u32 bload4(rsrc_t r, u32 voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+template <int ST> __device__ inline u32 bload_scale(rsrc_t r, u32 voff, int soff) {
+  if constexpr (ST == I4_F32) return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  else return (u32)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
 
 template <int XT> __device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
   if constexpr (XT == I4_F16)
@@ -48,10 +75,11 @@ template <int XT> __device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// 8 exact halves M + q of one CT word, in the (c, c+4) pair order
-template <int XT> __device__ inline u32x4 decode8(u32 w) {
-  constexpr u32 MK = 0x000F000Fu, MG = Half<XT>::MAGIC2;
-  return u32x4{(w & MK) | MG, ((w >> 4) & MK) | MG, ((w >> 8) & MK) | MG, ((w >> 12) & MK) | MG};
+// 8 exact halves M + q of one tile word (nibble slots (p, p + 4) -> half pair p),
+// columns 8m .. 8m + 7 in order
+template <int XT> __device__ inline u32x4 decode8(u32 w, u32 mg) {
+  constexpr u32 MK = 0x000F000Fu;
+  return u32x4{(w & MK) | mg, ((w >> 4) & MK) | mg, ((w >> 8) & MK) | mg, ((w >> 12) & MK) | mg};
 }
 
 // fp16 pair (M + q0, M + q1) + nz, nz = (-(M + z), -(M + z)): exactly (q0 - z, q1 - z)
@@ -59,11 +87,16 @@ __device__ inline u32 sub_zero(u32 p, u32 nz) {
   return __builtin_bit_cast(u32, __builtin_bit_cast(f16x2, p) + __builtin_bit_cast(f16x2, nz));
 }
 
-// B operand of step t for one n-block
-template <int XT> __device__ inline u32x4 b_operand(u32 word, u32 zw, int g) {
-  u32x4 b = decode8<XT>(word);
+// -(M + z) twice, fp16, for the zero point of group g held in zero word zw
+__device__ inline u32 neg_zero2(u32 zw, int g) {
+  return (0xE400u | ((zw >> (4 * (g & 7))) & 15u)) * 0x00010001u;
+}
+
+// B operand of one MFMA step (nz: neg_zero2 of the step's group, fp16 only;
+// mg: magic_v<XT>())
+template <int XT> __device__ inline u32x4 b_operand(u32 word, u32 nz, u32 mg) {
+  u32x4 b = decode8<XT>(word, mg);
   if constexpr (XT == I4_F16) {
-    const u32 nz = (0xE400u | ((zw >> (4 * (g & 7))) & 15u)) * 0x00010001u;
     b.x = sub_zero(b.x, nz);
     b.y = sub_zero(b.y, nz);
     b.z = sub_zero(b.z, nz);
@@ -81,7 +114,62 @@ __device__ inline int nblock(int tile, int wave, int nb, int I) {
     return tile * (4 * NB) + NB * wave + nb;
 }
 
-template <int XT, int ST, bool GB, int NB> struct MSlot {
+// the weight operands of one wave: NB n-blocks of expert e, lane (r, j)
+template <int ST, int NB> struct WBuf {
+  rsrc_t p, s, z;
+  u32 vw[NB], vs[NB], vz[NB];  // per-lane byte offsets of the n-blocks
+  u32 zor;                     // 0x88888888 when the weight has no zero points
+  int gshift;
+};
+
+template <int ST, int NB>
+__device__ inline WBuf<ST, NB> wbuf(const TW& w, int e, const int (&blk)[NB], int r, int j) {
+  constexpr u32 SB = ST == I4_F32 ? 4 : 2;
+  const u32 SC = (u32)w.K >> 7;
+  const u32 NG = (u32)((w.K + (32 << w.gshift) - 1) >> (w.gshift + 5)), NZW = (NG + 7) >> 3;
+  WBuf<ST, NB> b;
+  b.p = rsrc(w.packed + e * w.pes, (u32)w.N * (u32)(w.K >> 1));
+  b.s = rsrc((const char*)w.scale + e * w.ses * SB, (u32)w.N * NG * SB);
+  if (w.zeros) {
+    b.z = rsrc(w.zeros + e * w.zes, (u32)w.N * NZW * 4u);
+    b.zor = 0u;
+  } else {
+    b.z = rsrc(w.packed, 0u);
+    b.zor = 0x88888888u;
+  }
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const u32 bk = (u32)blk[nb];
+    b.vw[nb] = bk * SC * 1024u + (u32)r * 64u + (u32)j * 16u;
+    b.vs[nb] = (bk * NG * 16u + (u32)r) * SB;
+    b.vz[nb] = (bk * NZW * 16u + (u32)r) * 4u;
+  }
+  b.gshift = w.gshift;
+  return b;
+}
+
+// superchunk sc of every n-block: the 16-byte tile word, the raw scale(s) and
+// the zero word (one zero word covers the superchunk's groups).  Nothing here
+// touches the loaded values, so issuing never waits for a load.
+template <int ST, bool GB, int NB>
+__device__ inline void wissue(const WBuf<ST, NB>& b, int sc, TSlot<GB> (&o)[NB]) {
+  constexpr int SB = ST == I4_F32 ? 4 : 2;
+  const int g0 = (4 * sc) >> b.gshift;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    o[nb].w = bload16(b.p, b.vw[nb], sc * 1024);
+    if constexpr (GB) {
+      o[nb].s[0] = bload_scale<ST>(b.s, b.vs[nb], g0 * 16 * SB);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        o[nb].s[t] = bload_scale<ST>(b.s, b.vs[nb], ((4 * sc + t) >> b.gshift) * 16 * SB);
+    }
+    o[nb].z = bload4(b.z, b.vz[nb], (g0 >> 3) * 64);  // | zor where it is used
+  }
+}
+
+template <bool GB, int NB> struct MSlot {
   TSlot<GB> w[NB];
   u32x4 a[4];
 };
@@ -103,36 +191,35 @@ __device__ inline void correct(f32x4& res, const f32x4& d, u32 sraw, u32 zw, int
 
 template <int XT, int ST, bool GB, bool GATEUP, int NB>
 __global__ __launch_bounds__(256) void k_tile_mfma_s(
-    const uint16_t* __restrict__ src, int topk, const int4* __restrict__ entries,
+    const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ entries,
     const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
     uint16_t* __restrict__ act, float* __restrict__ ys) {
   constexpr bool EXACT = XT == I4_F16;
   constexpr int COLS = GATEUP ? 32 * NB : 64 * NB;
   static_assert(!GATEUP || NB % 2 == 0, "gate_up pairs gate and up blocks");
   if ((int)blockIdx.y >= *n_entries) return;
+  const u32 mg = magic_v<XT>();
   const int4 en = entries[blockIdx.y];
   const int e = en.x, pos0 = en.y, cnt = en.z;
   const int K = w.K, SC = K >> 7;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 15, kb = lane >> 4;
   const bool ev = (unsigned)e < (unsigned)w.E;
-  const int ee = ev ? e : 0;
-  TileRow tr[NB];
+  int blk[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-    tr[nb] = tile_row<ST>(w, ee, nblock<GATEUP, NB>(blockIdx.x, wave, nb, I), ln, kb);
+  for (int nb = 0; nb < NB; ++nb) blk[nb] = nblock<GATEUP, NB>(blockIdx.x, wave, nb, I);
+  const WBuf<ST, NB> wb = wbuf<ST, NB>(w, ev ? e : 0, blk, ln, kb);
   // A row of this lane: token ln of the entry (clamped; rows >= cnt are not stored)
-  const uint16_t* xrow;
-  if constexpr (GATEUP) xrow = src + (int64_t)(perm[pos0 + min(ln, cnt - 1)] / topk) * K;
-  else xrow = src + (int64_t)(pos0 + min(ln, cnt - 1)) * K;
-  xrow += 8 * kb;
+  const int row = GATEUP ? perm[pos0 + min(ln, cnt - 1)] / topk : pos0 + min(ln, cnt - 1);
+  const rsrc_t xr = rsrc(src, src_bytes);
+  const u32 vx = ((u32)row * (u32)K + 8u * (u32)kb) * 2u;
 
-  using Slot = MSlot<XT, ST, GB, NB>;
+  using Slot = MSlot<GB, NB>;
+  Slot s0_, s1_, s2_;
   auto issue = [&](int sc, Slot& sl) {
     sc = min(sc, SC - 1);  // past the end: the last superchunk again, an L2 hit
+    wissue<ST, GB, NB>(wb, sc, sl.w);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) sl.w[nb] = tile_load<ST, GB>(tr[nb], sc, w.gshift);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) sl.a[t] = ldg16(xrow + 128 * sc + 32 * t);
+    for (int t = 0; t < 4; ++t) sl.a[t] = bload16(xr, vx + 64u * t, sc * 256);
   };
   f32x4 res[NB];
 #pragma unroll
@@ -149,20 +236,28 @@ __global__ __launch_bounds__(256) void k_tile_mfma_s(
     f32x4 d[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) d[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int g0 = (4 * sc) >> w.gshift;
+    u32 zw[NB], nz[NB];  // zero words; GB: one zero point for the superchunk
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      zw[nb] = sl.w[nb].z | wb.zor;
+      nz[nb] = EXACT && GB ? neg_zero2(zw[nb], g0) : 0u;
+    }
     float pg = 0.f;  // bf16, GB: partial activation sum over the superchunk
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int g = (4 * sc + t) >> w.gshift;
-      const u32x4 a = pair_order(sl.a[t]);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        d[nb] = mfma16<XT>(a, b_operand<XT>(word_t(sl.w[nb].w, t), sl.w[nb].z, g), d[nb]);
+      for (int nb = 0; nb < NB; ++nb) {
+        const u32 z2 = EXACT && !GB ? neg_zero2(zw[nb], g) : nz[nb];
+        d[nb] = mfma16<XT>(sl.a[t], b_operand<XT>(word_t(sl.w[nb].w, t), z2, mg), d[nb]);
+      }
       if constexpr (!GB) {
         float sm[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (!EXACT) rows_sum(sum8<XT>(sl.a[t]).y, sm);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          correct<XT, ST>(res[nb], d[nb], sl.w[nb].s[t], sl.w[nb].z, g, sm);
+          correct<XT, ST>(res[nb], d[nb], sl.w[nb].s[t], zw[nb], g, sm);
           d[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
       } else if constexpr (!EXACT) {
@@ -170,25 +265,33 @@ __global__ __launch_bounds__(256) void k_tile_mfma_s(
       }
     }
     if constexpr (GB) {
-      const int g = (4 * sc) >> w.gshift;
       float sm[4] = {0.f, 0.f, 0.f, 0.f};
       if constexpr (!EXACT) rows_sum(pg, sm);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) correct<XT, ST>(res[nb], d[nb], sl.w[nb].s[0], sl.w[nb].z, g, sm);
+      for (int nb = 0; nb < NB; ++nb)
+        correct<XT, ST>(res[nb], d[nb], sl.w[nb].s[0], zw[nb], g0, sm);
     }
   };
-  Slot s0, s1, s2;
-  issue(0, s0);
-  issue(1, s1);
-  issue(2, s2);
-  for (int sc = 0; sc < SC; sc += 3) {
-    compute(sc, s0);
-    issue(sc + 3, s0);
-    if (sc + 1 < SC) compute(sc + 1, s1);
-    issue(sc + 4, s1);
-    if (sc + 2 < SC) compute(sc + 2, s2);
-    issue(sc + 5, s2);
-  }
+  // One turn of the ring: each slot computed, then refilled three superchunks
+  // ahead.  The first turn is peeled: the prologue issues the activation loads
+  // after every weight load (their addresses wait for perm), and a loop header
+  // reached from there as well would wait for nearly every load in flight.
+  auto turn = [&](int sc) {
+    compute(sc, s0_);
+    issue(sc + 3, s0_);
+    if (sc + 1 < SC) compute(sc + 1, s1_);
+    issue(sc + 4, s1_);
+    if (sc + 2 < SC) compute(sc + 2, s2_);
+    issue(sc + 5, s2_);
+  };
+  issue(0, s0_);
+  __builtin_amdgcn_sched_barrier(0);
+  issue(1, s1_);
+  __builtin_amdgcn_sched_barrier(0);
+  issue(2, s2_);
+  __builtin_amdgcn_sched_barrier(0);
+  turn(0);
+  for (int sc = 3; sc < SC; sc += 3) turn(sc);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * kb + i;
@@ -211,7 +314,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma_s(
 
 template <int XT, int ST, bool GB, bool GATEUP, int NB>
 __global__ __launch_bounds__(256) void k_tile_mfma(
-    const uint16_t* __restrict__ src, int topk, const int4* __restrict__ entries,
+    const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ entries,
     const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
     uint16_t* __restrict__ act, float* __restrict__ ys) {
   constexpr bool EXACT = XT == I4_F16;
@@ -220,44 +323,39 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
   __shared__ u32x4 xs[2][MF_TOK * MF_TSTRIDE];
   __shared__ float xsum[2][MF_TOK * 4];  // bf16: per token and chunk
   if ((int)blockIdx.y >= *n_entries) return;
+  const u32 mg = magic_v<XT>();
   const int4 en = entries[blockIdx.y];
   const int e = en.x, pos0 = en.y, cnt = en.z;
   const int K = w.K, SC = K >> 7;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 15, kb = lane >> 4;
   const bool ev = (unsigned)e < (unsigned)w.E;
-  const int ee = ev ? e : 0;
   const int nmb = (cnt + 15) >> 4;
-  TileRow tr[NB];
+  int blk[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-    tr[nb] = tile_row<ST>(w, ee, nblock<GATEUP, NB>(blockIdx.x, wave, nb, I), ln, kb);
+  for (int nb = 0; nb < NB; ++nb) blk[nb] = nblock<GATEUP, NB>(blockIdx.x, wave, nb, I);
+  const WBuf<ST, NB> wb = wbuf<ST, NB>(w, ev ? e : 0, blk, ln, kb);
   // staging role: token tk, chunk kc (words 4 kc .. 4 kc + 3) of the superchunk
   const int tk = threadIdx.x >> 2, kc = threadIdx.x & 3;
-  const uint16_t* xrow;
-  if constexpr (GATEUP) xrow = src + (int64_t)(perm[pos0 + min(tk, cnt - 1)] / topk) * K;
-  else xrow = src + (int64_t)(pos0 + min(tk, cnt - 1)) * K;
-  xrow += 32 * kc;
+  const int row = GATEUP ? perm[pos0 + min(tk, cnt - 1)] / topk : pos0 + min(tk, cnt - 1);
+  const rsrc_t xr = rsrc(src, src_bytes);
+  const u32 vx = ((u32)row * (u32)K + 32u * (u32)kc) * 2u;
   u32x4 xd[4];
   auto issue_x = [&](int sc) {
     sc = min(sc, SC - 1);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xd[q] = ldg16(xrow + 128 * sc + 8 * q);
+    for (int q = 0; q < 4; ++q) xd[q] = bload16(xr, vx + 16u * q, sc * 256);
   };
   auto commit_x = [&](int buf) {
     float sm = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      xs[buf][tk * MF_TSTRIDE + 4 * kc + q] = pair_order(xd[q]);
+      xs[buf][tk * MF_TSTRIDE + 4 * kc + q] = xd[q];
       if constexpr (!EXACT) sm += sum8<XT>(xd[q]).y;
     }
     if constexpr (!EXACT) xsum[buf][4 * tk + kc] = sm;
   };
   using WSlot = TSlot<GB>[NB];
-  auto issue_w = [&](int sc, WSlot& sl) {
-    sc = min(sc, SC - 1);
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) sl[nb] = tile_load<ST, GB>(tr[nb], sc, w.gshift);
-  };
+  auto issue_w = [&](int sc, WSlot& sl) { wissue<ST, GB, NB>(wb, min(sc, SC - 1), sl); };
   f32x4 res[4][NB];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
@@ -279,12 +377,21 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) d[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int g0 = (4 * sc) >> w.gshift;
+    u32 zw[NB], nz[NB];  // zero words; GB: one zero point for the superchunk
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      zw[nb] = sl[nb].z | wb.zor;
+      nz[nb] = EXACT && GB ? neg_zero2(zw[nb], g0) : 0u;
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int g = (4 * sc + t) >> w.gshift;
       u32x4 b[NB];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) b[nb] = b_operand<XT>(word_t(sl[nb].w, t), sl[nb].z, g);
+      for (int nb = 0; nb < NB; ++nb)
+        b[nb] = b_operand<XT>(word_t(sl[nb].w, t), EXACT && !GB ? neg_zero2(zw[nb], g) : nz[nb],
+                              mg);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         if (mb < nmb) {
@@ -301,7 +408,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
             if constexpr (!EXACT) rows_sum(buf, mb, t, 1, sm);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-              correct<XT, ST>(res[mb][nb], d[mb][nb], sl[nb].s[t], sl[nb].z, g, sm);
+              correct<XT, ST>(res[mb][nb], d[mb][nb], sl[nb].s[t], zw[nb], g, sm);
               d[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
           }
@@ -309,7 +416,6 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
       }
     }
     if constexpr (GB) {
-      const int g = (4 * sc) >> w.gshift;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         if (mb < nmb) {
@@ -317,7 +423,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
           if constexpr (!EXACT) rows_sum(buf, mb, 0, 4, sm);
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb)
-            correct<XT, ST>(res[mb][nb], d[mb][nb], sl[nb].s[0], sl[nb].z, g, sm);
+            correct<XT, ST>(res[mb][nb], d[mb][nb], sl[nb].s[0], zw[nb], g0, sm);
         }
       }
     }
@@ -334,12 +440,20 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     if (sc < SC) compute(sc, sl, buf);
     issue_w(sc + 3, sl);
   };
+  // prologue loads in ring order, first turn peeled (see k_tile_mfma_s)
   WSlot s0, s1, s2;
   issue_w(0, s0);
+  __builtin_amdgcn_sched_barrier(0);
   issue_w(1, s1);
+  __builtin_amdgcn_sched_barrier(0);
   issue_w(2, s2);
+  __builtin_amdgcn_sched_barrier(0);
   issue_x(0);
-  for (int sc = 0; sc < SC; sc += 3) {
+  __builtin_amdgcn_sched_barrier(0);
+  step(0, s0);
+  step(1, s1);
+  step(2, s2);
+  for (int sc = 3; sc < SC; sc += 3) {
     step(sc, s0);
     step(sc + 1, s1);
     step(sc + 2, s2);
@@ -371,47 +485,54 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
 
 // ---------------------------------------------------------------------------
 template <int XT, int ST, bool GB, bool GATEUP>
-static int mfma_t(bool small, int max_entries, const void* src, int topk, const int4* ent,
-                  const int* nent, const int32_t* perm, const TW& w, int I, void* act, float* ys,
-                  hipStream_t s) {
+static int mfma_t(bool small, int max_entries, const void* src, int src_rows, int topk,
+                  const int4* ent, const int* nent, const int32_t* perm, const TW& w, int I,
+                  void* act, float* ys, hipStream_t s) {
   const int cols = GATEUP ? 32 * MF_NB : 64 * MF_NB;
+  const int64_t src_bytes = (int64_t)src_rows * w.K * 2;
+  // buffer offsets are 32-bit: the activation rows and one expert's weights must fit
+  if (src_bytes >= ((int64_t)1 << 31) || (int64_t)w.N * w.K / 2 >= ((int64_t)1 << 31))
+    return I4_ERR_SHAPE;
   const dim3 grid((GATEUP ? I : w.N) / cols, max_entries);
   if (small)
     hipLaunchKernelGGL((k_tile_mfma_s<XT, ST, GB, GATEUP, MF_NB>), grid, dim3(256), 0, s,
-                       (const uint16_t*)src, topk, ent, nent, perm, w, I, (uint16_t*)act, ys);
+                       (const uint16_t*)src, (u32)src_bytes, topk, ent, nent, perm, w, I,
+                       (uint16_t*)act, ys);
   else
     hipLaunchKernelGGL((k_tile_mfma<XT, ST, GB, GATEUP, MF_NB>), grid, dim3(256), 0, s,
-                       (const uint16_t*)src, topk, ent, nent, perm, w, I, (uint16_t*)act, ys);
+                       (const uint16_t*)src, (u32)src_bytes, topk, ent, nent, perm, w, I,
+                       (uint16_t*)act, ys);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
 template <int XT, int ST>
-int launch_mfma_gate_up(bool small, int max_entries, const void* x, int topk, const int4* ent,
-                        const int* nent, const int32_t* perm, const TW& w, int I, void* act,
-                        hipStream_t s) {
+int launch_mfma_gate_up(bool small, int max_entries, const void* x, int T, int topk,
+                        const int4* ent, const int* nent, const int32_t* perm, const TW& w, int I,
+                        void* act, hipStream_t s) {
   if (w.gshift >= 2)
-    return mfma_t<XT, ST, true, true>(small, max_entries, x, topk, ent, nent, perm, w, I, act,
+    return mfma_t<XT, ST, true, true>(small, max_entries, x, T, topk, ent, nent, perm, w, I, act,
                                       nullptr, s);
-  return mfma_t<XT, ST, false, true>(small, max_entries, x, topk, ent, nent, perm, w, I, act,
+  return mfma_t<XT, ST, false, true>(small, max_entries, x, T, topk, ent, nent, perm, w, I, act,
                                      nullptr, s);
 }
 
 template <int XT, int ST>
-int launch_mfma_down(bool small, int max_entries, const void* act, const int4* ent,
+int launch_mfma_down(bool small, int max_entries, const void* act, int rows, const int4* ent,
                      const int* nent, const int32_t* perm, const TW& w, float* ys, hipStream_t s) {
   if (w.gshift >= 2)
-    return mfma_t<XT, ST, true, false>(small, max_entries, act, 0, ent, nent, perm, w, 0, nullptr,
-                                       ys, s);
-  return mfma_t<XT, ST, false, false>(small, max_entries, act, 0, ent, nent, perm, w, 0, nullptr,
-                                      ys, s);
+    return mfma_t<XT, ST, true, false>(small, max_entries, act, rows, 0, ent, nent, perm, w, 0,
+                                       nullptr, ys, s);
+  return mfma_t<XT, ST, false, false>(small, max_entries, act, rows, 0, ent, nent, perm, w, 0,
+                                      nullptr, ys, s);
 }
 
-#define I4_INST(XT_, ST_)                                                                       \
-  template int launch_mfma_gate_up<XT_, ST_>(bool, int, const void*, int, const int4*,          \
+#define I4_INST(XT_, ST_)                                                                      \
+  template int launch_mfma_gate_up<XT_, ST_>(bool, int, const void*, int, int, const int4*,    \
                                              const int*, const int32_t*, const TW&, int, void*, \
-                                             hipStream_t);                                      \
-  template int launch_mfma_down<XT_, ST_>(bool, int, const void*, const int4*, const int*,      \
-                                          const int32_t*, const TW&, float*, hipStream_t);
+                                             hipStream_t);                                     \
+  template int launch_mfma_down<XT_, ST_>(bool, int, const void*, int, const int4*,            \
+                                          const int*, const int32_t*, const TW&, float*,       \
+                                          hipStream_t);
 I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
 I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)
 #undef I4_INST

@@ -5,6 +5,9 @@
 // lane / 16 the k-group -- loads one 16-byte word holding word j (columns
 // 8j..8j+7) of each of the four chunks, so the 64 lanes read the tile's 1 KB
 // as one contiguous block.  Component t of that word belongs to chunk 4s + t.
+// Nibble slots (i, i + 4) of a word hold the adjacent columns (2i, 2i + 1), so
+// the half pairs the decode builds line up with the activations in their
+// natural order and no operand needs permuting.
 // Scales and zero words are stored per 16-row block and group with the 16
 // rows adjacent, so lane r's side loads are coalesced as well.
 //
@@ -81,7 +84,7 @@ __device__ inline u32 word_t(const u32x4& w, int t) {
 __device__ inline float zero_of(u32 zw, int g) { return (float)((zw >> (4 * (g & 7))) & 15u); }
 
 // Activation staging for the decode kernels: nr rows of K halves in LDS, word
-// jw of chunk c of row r at xs[(4 r + jw) C + c] in decode pair order, and
+// jw of chunk c of row r at xs[(4 r + jw) C + c] in natural order, and
 // its (Sb, S) at sums[(4 r + jw) C + c] (one entry per 16-byte word: a lane
 // of a tile covers one word of each chunk).  issue() puts up to 4 loads per
 // thread in flight and returns; commit() writes them once the caller has
@@ -105,8 +108,8 @@ template <int XT> struct TStager {
       if (idx < total) {
         const int r = idx / words, m = idx - r * words;
         const int o = (4 * r + (m & 3)) * C + (m >> 2);
-        xs[o] = pair_order(d[u]);
-        sums[o] = sum8<XT>(d[u]);
+        xs[o] = d[u];
+        sums[o] = sum8n<XT>(d[u]);
       }
     }
   }
@@ -122,13 +125,13 @@ template <int XT> struct TStager {
 // each chunk): sum over its 32 columns of (q - z) s x, corrected per group.
 template <int XT, int ST, bool GB>
 __device__ inline float tile_dot(const TSlot<GB>& sl, const u32x4* xs, const float2* sums,
-                                 int s, int gshift) {
+                                 int s, int gshift, u32 mg) {
   float acc = 0.f, lo = 0.f, hi = 0.f, sb = 0.f, sp = 0.f;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const u32x4 xw = xs[4 * s + t];
     const float2 sm = sums[4 * s + t];
-    dot8<XT>(word_t(sl.w, t), xw, lo, hi);
+    dot8<XT>(word_t(sl.w, t), xw, lo, hi, mg);
     if constexpr (GB) {
       sb += sm.x;
       sp += sm.y;

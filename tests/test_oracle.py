@@ -142,20 +142,42 @@ def test_ct_awq_layout_equivalence():
 
 
 def test_tile_index_closed_form():
-    """Tile element [e, b, s, r, 4j + t] is CT word 4 (4s + t) + j of row 16b + r."""
+    """Nibble i of tile element [e, b, s, r, 4j + t] is column 128s + 32t + 8j +
+    (0, 2, 4, 6, 1, 3, 5, 7)[i] of row 16b + r, checked against CT nibbles taken
+    with a direct bit expression (nibble c of CT word m is column 8m + c)."""
+    rng = np.random.default_rng(17)
     E, N, K = 2, 32, 256
-    idx = np.arange(E * N * K // 8, dtype=np.int64).reshape(E, N, K // 8).astype(np.int32)
+    p = _gen.words(rng, (E, N, K // 8))
+    Q = np.stack([(p.astype(np.int64) >> (4 * c)) & 15 for c in range(8)], axis=-1).reshape(E, N, K)
     sc = np.arange(E * N * 2, dtype=np.float32).reshape(E, N, 2)
-    t, ts, tz = i4ref.tile_pack(idx, sc, sc.astype(np.int32))
+    t, ts, tz = i4ref.tile_pack(p, sc, sc.astype(np.int32))
     assert t.shape == (E, N // 16, K // 128, 16, 16) and ts.shape == (E, N // 16, 2, 16)
+    order = (0, 2, 4, 6, 1, 3, 5, 7)
     for e, b, s_, r, j, tt in [(0, 0, 0, 0, 0, 0), (1, 1, 1, 15, 3, 3), (0, 1, 0, 7, 2, 1),
                                (1, 0, 1, 3, 1, 2)]:
-        assert t[e, b, s_, r, 4 * j + tt] == idx[e, 16 * b + r, 4 * (4 * s_ + tt) + j]
+        word = int(t[e, b, s_, r, 4 * j + tt]) & 0xFFFFFFFF
+        for i in range(8):
+            col = 128 * s_ + 32 * tt + 8 * j + order[i]
+            assert (word >> (4 * i)) & 15 == Q[e, 16 * b + r, col]
+    # nibbles i and i + 4 are adjacent columns: one (lo, hi) half pair of the decode
+    assert all(order[i + 4] == order[i] + 1 for i in range(4))
     for e, b, g, r in [(0, 0, 0, 0), (1, 1, 1, 15), (0, 1, 0, 9)]:
         assert ts[e, b, g, r] == sc[e, 16 * b + r, g] and tz[e, b, g, r] == int(sc[e, 16 * b + r, g])
     # a lane (r, j) of one 16-byte load holds word j of the four chunks of a superchunk
     lane = t[0, 0, 1, 5, 8:12]
-    assert list(lane) == [idx[0, 5, 4 * (4 + c) + 2] for c in range(4)]
+    assert list(i4ref.deinterleave_words(lane)) == [p[0, 5, 4 * (4 + c) + 2] for c in range(4)]
+    # the CT nibble order itself would put column 8m + 1 in slot 1, not slot 4
+    assert not np.array_equal(t.reshape(-1)[:64], i4ref.deinterleave_words(t.reshape(-1)[:64]))
+
+
+def test_interleave_round_trip_brute_force():
+    """Every value at every nibble slot moves to the slot the AWQ order names."""
+    for c in range(8):
+        for v in range(16):
+            w = np.array([v << (4 * c)], dtype=np.int64).astype(np.uint32).view(np.int32)
+            out = int(i4ref.interleave_words(w)[0]) & 0xFFFFFFFF
+            assert out == v << (4 * (0, 2, 4, 6, 1, 3, 5, 7).index(c))
+            assert i4ref.deinterleave_words(i4ref.interleave_words(w))[0] == w[0]
 
 
 def test_tile_round_trip_and_dequant():
