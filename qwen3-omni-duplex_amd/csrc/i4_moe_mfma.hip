@@ -23,16 +23,16 @@
 // weight without zero points reads its zero words through an empty
 // descriptor (every load returns 0) and ORs in the symmetric 0x88888888.
 //
-// k_tile_mfma_s (entries of <= 16 tokens, one m-block): every lane loads its
-// own A words (the four waves of a workgroup hit the same L1 lines), no LDS
-// and no barrier; the weights and activations of the next two superchunks
-// are in flight while one is multiplied (three-slot register ring, unrolled
-// so every slot index is static, loads issued unconditionally so that the
-// waits before each use stay partial).
-// k_tile_mfma (entries of <= 64 tokens): the activation tile of a superchunk
-// is staged once per workgroup in LDS (double buffered, token stride 272 B so
-// the 16 tokens of an MFMA fall on distinct banks), weights in the same
-// three-slot ring.
+// k_tile_mfma<..., NB, MB>: one entry (<= 16 MB tokens of one expert) times
+// one column tile per workgroup.  The activation tile of a superchunk (16 MB
+// tokens x 128 columns) is loaded once per workgroup and staged in LDS
+// (double buffered, token stride 272 B so the 16 tokens of an MFMA fall on
+// distinct banks); every wave streams its own NB n-blocks through a
+// three-slot register ring (unrolled so every slot index is static, loads
+// issued unconditionally so that the waits before each use stay partial).
+// Small entries (<= 16 tokens) run MB = 1 with NB = 4 where the rows allow,
+// so a wave keeps 12 KB of weights in flight; large entries (<= 64 tokens)
+// run MB = 4, NB = 2, each decoded weight feeding up to four MFMAs.
 //   GATEUP: NB/2 blocks of gate rows and the same up rows per wave, SiLU in
 //           the epilogue, act[pos] in the activation dtype; 32 NB row pairs
 //           per workgroup.
@@ -114,19 +114,22 @@ __device__ inline int nblock(int tile, int wave, int nb, int I) {
     return tile * (4 * NB) + NB * wave + nb;
 }
 
-// the weight operands of one wave: NB n-blocks of expert e, lane (r, j)
+// the weight operands of one wave: NB n-blocks of expert e, lane (r, j).
+// Lane offsets live in VGPRs; the n-block offsets are wave-uniform and go in
+// the scalar offset of each load, with the superchunk / group offset.
 template <int ST, int NB> struct WBuf {
   rsrc_t p, s, z;
-  u32 vw[NB], vs[NB], vz[NB];  // per-lane byte offsets of the n-blocks
+  u32 lw, ls, lz;              // per-lane byte offsets
+  int bw[NB], bs[NB], bz[NB];  // per-n-block byte offsets (wave-uniform)
   u32 zor;                     // 0x88888888 when the weight has no zero points
   int gshift;
 };
 
 template <int ST, int NB>
 __device__ inline WBuf<ST, NB> wbuf(const TW& w, int e, const int (&blk)[NB], int r, int j) {
-  constexpr u32 SB = ST == I4_F32 ? 4 : 2;
-  const u32 SC = (u32)w.K >> 7;
-  const u32 NG = (u32)((w.K + (32 << w.gshift) - 1) >> (w.gshift + 5)), NZW = (NG + 7) >> 3;
+  constexpr int SB = ST == I4_F32 ? 4 : 2;
+  const int SC = w.K >> 7;
+  const int NG = (w.K + (32 << w.gshift) - 1) >> (w.gshift + 5), NZW = (NG + 7) >> 3;
   WBuf<ST, NB> b;
   b.p = rsrc(w.packed + e * w.pes, (u32)w.N * (u32)(w.K >> 1));
   b.s = rsrc((const char*)w.scale + e * w.ses * SB, (u32)w.N * NG * SB);
@@ -137,12 +140,14 @@ __device__ inline WBuf<ST, NB> wbuf(const TW& w, int e, const int (&blk)[NB], in
     b.z = rsrc(w.packed, 0u);
     b.zor = 0x88888888u;
   }
+  b.lw = (u32)r * 64u + (u32)j * 16u;
+  b.ls = (u32)r * SB;
+  b.lz = (u32)r * 4u;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const u32 bk = (u32)blk[nb];
-    b.vw[nb] = bk * SC * 1024u + (u32)r * 64u + (u32)j * 16u;
-    b.vs[nb] = (bk * NG * 16u + (u32)r) * SB;
-    b.vz[nb] = (bk * NZW * 16u + (u32)r) * 4u;
+    b.bw[nb] = blk[nb] * SC * 1024;
+    b.bs[nb] = blk[nb] * NG * 16 * SB;
+    b.bz[nb] = blk[nb] * NZW * 64;
   }
   b.gshift = w.gshift;
   return b;
@@ -157,22 +162,17 @@ __device__ inline void wissue(const WBuf<ST, NB>& b, int sc, TSlot<GB> (&o)[NB])
   const int g0 = (4 * sc) >> b.gshift;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    o[nb].w = bload16(b.p, b.vw[nb], sc * 1024);
+    o[nb].w = bload16(b.p, b.lw, b.bw[nb] + sc * 1024);
     if constexpr (GB) {
-      o[nb].s[0] = bload_scale<ST>(b.s, b.vs[nb], g0 * 16 * SB);
+      o[nb].s[0] = bload_scale<ST>(b.s, b.ls, b.bs[nb] + g0 * 16 * SB);
     } else {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        o[nb].s[t] = bload_scale<ST>(b.s, b.vs[nb], ((4 * sc + t) >> b.gshift) * 16 * SB);
+        o[nb].s[t] = bload_scale<ST>(b.s, b.ls, b.bs[nb] + ((4 * sc + t) >> b.gshift) * 16 * SB);
     }
-    o[nb].z = bload4(b.z, b.vz[nb], (g0 >> 3) * 64);  // | zor where it is used
+    o[nb].z = bload4(b.z, b.lz, b.bz[nb] + (g0 >> 3) * 64);  // | zor where it is used
   }
 }
-
-template <bool GB, int NB> struct MSlot {
-  TSlot<GB> w[NB];
-  u32x4 a[4];
-};
 
 // group correction of one n-block's accumulator (rows m = 4 j + i of column r)
 template <int XT, int ST>
@@ -189,176 +189,79 @@ __device__ inline void correct(f32x4& res, const f32x4& d, u32 sraw, u32 zw, int
   }
 }
 
-template <int XT, int ST, bool GB, bool GATEUP, int NB>
-__global__ __launch_bounds__(256) void k_tile_mfma_s(
-    const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ entries,
-    const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
-    uint16_t* __restrict__ act, float* __restrict__ ys) {
-  constexpr bool EXACT = XT == I4_F16;
-  constexpr int COLS = GATEUP ? 32 * NB : 64 * NB;
-  static_assert(!GATEUP || NB % 2 == 0, "gate_up pairs gate and up blocks");
-  if ((int)blockIdx.y >= *n_entries) return;
-  const u32 mg = magic_v<XT>();
-  const int4 en = entries[blockIdx.y];
-  const int e = en.x, pos0 = en.y, cnt = en.z;
-  const int K = w.K, SC = K >> 7;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 15, kb = lane >> 4;
-  const bool ev = (unsigned)e < (unsigned)w.E;
-  int blk[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) blk[nb] = nblock<GATEUP, NB>(blockIdx.x, wave, nb, I);
-  const WBuf<ST, NB> wb = wbuf<ST, NB>(w, ev ? e : 0, blk, ln, kb);
-  // A row of this lane: token ln of the entry (clamped; rows >= cnt are not stored)
-  const int row = GATEUP ? perm[pos0 + min(ln, cnt - 1)] / topk : pos0 + min(ln, cnt - 1);
-  const rsrc_t xr = rsrc(src, src_bytes);
-  const u32 vx = ((u32)row * (u32)K + 8u * (u32)kb) * 2u;
-
-  using Slot = MSlot<GB, NB>;
-  Slot s0_, s1_, s2_;
-  auto issue = [&](int sc, Slot& sl) {
-    sc = min(sc, SC - 1);  // past the end: the last superchunk again, an L2 hit
-    wissue<ST, GB, NB>(wb, sc, sl.w);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) sl.a[t] = bload16(xr, vx + 64u * t, sc * 256);
-  };
-  f32x4 res[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) res[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // bf16: S of rows m = 4 j + i from this lane's partial sums p (token ln)
-  auto rows_sum = [&](float p, float (&sm)[4]) {
-    const float tot = kgroup_sum(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      sm[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((4 * kb + i) << 2,
-                                                                     __builtin_bit_cast(int, tot)));
-  };
-  auto compute = [&](int sc, const Slot& sl) {
-    f32x4 d[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) d[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int g0 = (4 * sc) >> w.gshift;
-    u32 zw[NB], nz[NB];  // zero words; GB: one zero point for the superchunk
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      zw[nb] = sl.w[nb].z | wb.zor;
-      nz[nb] = EXACT && GB ? neg_zero2(zw[nb], g0) : 0u;
-    }
-    float pg = 0.f;  // bf16, GB: partial activation sum over the superchunk
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int g = (4 * sc + t) >> w.gshift;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const u32 z2 = EXACT && !GB ? neg_zero2(zw[nb], g) : nz[nb];
-        d[nb] = mfma16<XT>(sl.a[t], b_operand<XT>(word_t(sl.w[nb].w, t), z2, mg), d[nb]);
-      }
-      if constexpr (!GB) {
-        float sm[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (!EXACT) rows_sum(sum8<XT>(sl.a[t]).y, sm);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          correct<XT, ST>(res[nb], d[nb], sl.w[nb].s[t], zw[nb], g, sm);
-          d[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-      } else if constexpr (!EXACT) {
-        pg += sum8<XT>(sl.a[t]).y;
-      }
-    }
-    if constexpr (GB) {
-      float sm[4] = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (!EXACT) rows_sum(pg, sm);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        correct<XT, ST>(res[nb], d[nb], sl.w[nb].s[0], zw[nb], g0, sm);
-    }
-  };
-  // One turn of the ring: each slot computed, then refilled three superchunks
-  // ahead.  The first turn is peeled: the prologue issues the activation loads
-  // after every weight load (their addresses wait for perm), and a loop header
-  // reached from there as well would wait for nearly every load in flight.
-  auto turn = [&](int sc) {
-    compute(sc, s0_);
-    issue(sc + 3, s0_);
-    if (sc + 1 < SC) compute(sc + 1, s1_);
-    issue(sc + 4, s1_);
-    if (sc + 2 < SC) compute(sc + 2, s2_);
-    issue(sc + 5, s2_);
-  };
-  issue(0, s0_);
-  __builtin_amdgcn_sched_barrier(0);
-  issue(1, s1_);
-  __builtin_amdgcn_sched_barrier(0);
-  issue(2, s2_);
-  __builtin_amdgcn_sched_barrier(0);
-  turn(0);
-  for (int sc = 3; sc < SC; sc += 3) turn(sc);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = 4 * kb + i;
-    if (m < cnt) {
-      if constexpr (GATEUP) {
-#pragma unroll
-        for (int nb = 0; nb < NB / 2; ++nb) {
-          const int n = blockIdx.x * COLS + 16 * (NB / 2) * wave + 16 * nb + ln;
-          const float v = ev ? silu(res[nb][i]) * res[nb + NB / 2][i] : __builtin_nanf("");
-          act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
-        }
-      } else {
-        const int64_t o = (int64_t)perm[pos0 + m] * w.N + blockIdx.x * COLS + 16 * NB * wave + ln;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) ys[o + 16 * nb] = ev ? res[nb][i] : __builtin_nanf("");
-      }
-    }
-  }
-}
-
-template <int XT, int ST, bool GB, bool GATEUP, int NB>
+// One entry (<= 16 MB tokens of one expert) x one column tile.  MB m-blocks
+// of 16 tokens (1 for the small entries, 4 for the large ones), NB n-blocks
+// of 16 weight rows per wave.
+template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB>
 __global__ __launch_bounds__(256) void k_tile_mfma(
     const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ entries,
     const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
     uint16_t* __restrict__ act, float* __restrict__ ys) {
   constexpr bool EXACT = XT == I4_F16;
   constexpr int COLS = GATEUP ? 32 * NB : 64 * NB;
+  constexpr int TOK = 16 * MB;
   static_assert(!GATEUP || NB % 2 == 0, "gate_up pairs gate and up blocks");
-  __shared__ u32x4 xs[2][MF_TOK * MF_TSTRIDE];
-  __shared__ float xsum[2][MF_TOK * 4];  // bf16: per token and chunk
+  static_assert(MB == 1 || MB == 4, "staging maps 256 threads onto 16 or 64 tokens");
+  __shared__ u32x4 xs[2][TOK * MF_TSTRIDE];
+  __shared__ float xsum[2][TOK * 4];  // bf16: per token and chunk
   if ((int)blockIdx.y >= *n_entries) return;
   const u32 mg = magic_v<XT>();
   const int4 en = entries[blockIdx.y];
   const int e = en.x, pos0 = en.y, cnt = en.z;
   const int K = w.K, SC = K >> 7;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 15, kb = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, ln = lane & 15, kb = lane >> 4;
   const bool ev = (unsigned)e < (unsigned)w.E;
-  const int nmb = (cnt + 15) >> 4;
+  const int nmb = MB == 1 ? 1 : (cnt + 15) >> 4;
   int blk[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) blk[nb] = nblock<GATEUP, NB>(blockIdx.x, wave, nb, I);
   const WBuf<ST, NB> wb = wbuf<ST, NB>(w, ev ? e : 0, blk, ln, kb);
-  // staging role: token tk, chunk kc (words 4 kc .. 4 kc + 3) of the superchunk
-  const int tk = threadIdx.x >> 2, kc = threadIdx.x & 3;
+  // staging role: MB = 4: token tid / 4, chunk tid % 4 (its 4 words);
+  //               MB = 1: token tid / 16, word tid % 16
+  constexpr int WPT = MB;  // 16-byte words per thread and superchunk
+  const int tk = MB == 4 ? (int)threadIdx.x >> 2 : (int)threadIdx.x >> 4;
+  const int kw = MB == 4 ? 4 * ((int)threadIdx.x & 3) : (int)threadIdx.x & 15;  // first word
   const int row = GATEUP ? perm[pos0 + min(tk, cnt - 1)] / topk : pos0 + min(tk, cnt - 1);
   const rsrc_t xr = rsrc(src, src_bytes);
-  const u32 vx = ((u32)row * (u32)K + 32u * (u32)kc) * 2u;
-  u32x4 xd[4];
-  auto issue_x = [&](int sc) {
+  const u32 vx = ((u32)row * (u32)K + 8u * (u32)kw) * 2u;
+  // Ring slot: the weights of one superchunk and, for MB = 1, its activation
+  // word too, issued right after the weights: the in-order wait for that word
+  // at staging time then only covers loads the step needs anyway.  With MB = 4
+  // (four words per thread) the activations are loaded one step ahead instead.
+  struct Slot {
+    TSlot<GB> w[NB];
+    u32x4 x;
+  };
+  u32x4 xd[WPT];
+  auto load_x = [&](int sc, u32x4* dst) {
     sc = min(sc, SC - 1);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xd[q] = bload16(xr, vx + 16u * q, sc * 256);
+    for (int q = 0; q < WPT; ++q) dst[q] = bload16(xr, vx + 16u * q, sc * 256);
   };
-  auto commit_x = [&](int buf) {
+  auto commit_x = [&](int buf, const u32x4* src_x) {
     float sm = 0.f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      xs[buf][tk * MF_TSTRIDE + 4 * kc + q] = xd[q];
-      if constexpr (!EXACT) sm += sum8<XT>(xd[q]).y;
+    for (int q = 0; q < WPT; ++q) {
+      xs[buf][tk * MF_TSTRIDE + kw + q] = src_x[q];
+      if constexpr (!EXACT) sm += sum8<XT>(src_x[q]).y;
     }
-    if constexpr (!EXACT) xsum[buf][4 * tk + kc] = sm;
+    if constexpr (!EXACT) {
+      if constexpr (MB == 1) {
+        sm = group_sum<4>(sm);  // the chunk's 4 words sit in 4 adjacent lanes
+        if ((kw & 3) == 0) xsum[buf][4 * tk + (kw >> 2)] = sm;
+      } else {
+        xsum[buf][4 * tk + (kw >> 2)] = sm;
+      }
+    }
   };
-  using WSlot = TSlot<GB>[NB];
-  auto issue_w = [&](int sc, WSlot& sl) { wissue<ST, GB, NB>(wb, min(sc, SC - 1), sl); };
-  f32x4 res[4][NB];
+  auto issue = [&](int sc, Slot& sl) {
+    wissue<ST, GB, NB>(wb, min(sc, SC - 1), sl.w);
+    if constexpr (MB == 1) load_x(sc, &sl.x);
+  };
+  f32x4 res[MB][NB];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) res[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   // S of rows 16 mb + 4 j + i over chunks [t0, t0 + nt) of the staged superchunk
@@ -371,10 +274,10 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
       sm[i] = v;
     }
   };
-  auto compute = [&](int sc, const WSlot& sl, int buf) {
-    f32x4 d[4][NB];
+  auto compute = [&](int sc, const TSlot<GB> (&sl)[NB], int buf) {
+    f32x4 d[MB][NB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) d[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int g0 = (4 * sc) >> w.gshift;
@@ -387,22 +290,31 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int g = (4 * sc + t) >> w.gshift;
-      u32x4 b[NB];
+      if constexpr (MB == 1) {  // one m-block: each B operand feeds one MFMA
+        const u32x4 a = xs[buf][ln * MF_TSTRIDE + 4 * t + kb];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        b[nb] = b_operand<XT>(word_t(sl[nb].w, t), EXACT && !GB ? neg_zero2(zw[nb], g) : nz[nb],
-                              mg);
+        for (int nb = 0; nb < NB; ++nb)
+          d[0][nb] = mfma16<XT>(
+              a, b_operand<XT>(word_t(sl[nb].w, t), EXACT && !GB ? neg_zero2(zw[nb], g) : nz[nb], mg),
+              d[0][nb]);
+      } else {
+        u32x4 b[NB];
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        if (mb < nmb) {
-          const u32x4 a = xs[buf][(16 * mb + ln) * MF_TSTRIDE + 4 * t + kb];
+        for (int nb = 0; nb < NB; ++nb)
+          b[nb] = b_operand<XT>(word_t(sl[nb].w, t), EXACT && !GB ? neg_zero2(zw[nb], g) : nz[nb],
+                                mg);
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) d[mb][nb] = mfma16<XT>(a, b[nb], d[mb][nb]);
+        for (int mb = 0; mb < MB; ++mb) {
+          if (mb < nmb) {
+            const u32x4 a = xs[buf][(16 * mb + ln) * MF_TSTRIDE + 4 * t + kb];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) d[mb][nb] = mfma16<XT>(a, b[nb], d[mb][nb]);
+          }
         }
       }
       if constexpr (!GB) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
+        for (int mb = 0; mb < MB; ++mb) {
           if (mb < nmb) {
             float sm[4] = {0.f, 0.f, 0.f, 0.f};
             if constexpr (!EXACT) rows_sum(buf, mb, t, 1, sm);
@@ -417,7 +329,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     }
     if constexpr (GB) {
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         if (mb < nmb) {
           float sm[4] = {0.f, 0.f, 0.f, 0.f};
           if constexpr (!EXACT) rows_sum(buf, mb, 0, 4, sm);
@@ -429,26 +341,33 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     }
   };
   // one superchunk: stage its activations (loaded one step earlier), load the
-  // next step's, multiply, refill this weight slot three superchunks ahead
-  auto step = [&](int sc, WSlot& sl) {
+  // next step's, multiply, refill this weight slot three superchunks ahead.
+  // Staging and barrier run past the last superchunk too (clamped data that
+  // nothing reads): a staging store inside the guard would let the compiler
+  // sink the activation load down to it and lose the prefetch.
+  auto step = [&](int sc, Slot& sl) {
     const int buf = sc & 1;
-    if (sc < SC) {
-      commit_x(buf);
-      __syncthreads();
+    if constexpr (MB == 1) {
+      commit_x(buf, &sl.x);
+    } else {
+      commit_x(buf, xd);
     }
-    issue_x(sc + 1);  // unconditional (clamped), like every load of the ring
-    if (sc < SC) compute(sc, sl, buf);
-    issue_w(sc + 3, sl);
+    __syncthreads();
+    if constexpr (MB != 1) load_x(sc + 1, xd);  // unconditional (clamped), like every load
+    if (sc < SC) compute(sc, sl.w, buf);
+    issue(sc + 3, sl);
   };
-  // prologue loads in ring order, first turn peeled (see k_tile_mfma_s)
-  WSlot s0, s1, s2;
-  issue_w(0, s0);
+  // Prologue loads in ring order, first turn peeled: the activation loads wait
+  // for perm and land after the weights, and a loop header reached from the
+  // prologue as well would wait for nearly every load in flight.
+  Slot s0, s1, s2;
+  issue(0, s0);
   __builtin_amdgcn_sched_barrier(0);
-  issue_w(1, s1);
+  issue(1, s1);
   __builtin_amdgcn_sched_barrier(0);
-  issue_w(2, s2);
+  issue(2, s2);
   __builtin_amdgcn_sched_barrier(0);
-  issue_x(0);
+  if constexpr (MB != 1) load_x(0, xd);
   __builtin_amdgcn_sched_barrier(0);
   step(0, s0);
   step(1, s1);
@@ -460,7 +379,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
   }
   // epilogue: lane holds rows m = 16 mb + 4 j + i of column r
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 16 * mb + 4 * kb + i;
@@ -488,20 +407,22 @@ template <int XT, int ST, bool GB, bool GATEUP>
 static int mfma_t(bool small, int max_entries, const void* src, int src_rows, int topk,
                   const int4* ent, const int* nent, const int32_t* perm, const TW& w, int I,
                   void* act, float* ys, hipStream_t s) {
-  const int cols = GATEUP ? 32 * MF_NB : 64 * MF_NB;
   const int64_t src_bytes = (int64_t)src_rows * w.K * 2;
   // buffer offsets are 32-bit: the activation rows and one expert's weights must fit
   if (src_bytes >= ((int64_t)1 << 31) || (int64_t)w.N * w.K / 2 >= ((int64_t)1 << 31))
     return I4_ERR_SHAPE;
-  const dim3 grid((GATEUP ? I : w.N) / cols, max_entries);
-  if (small)
-    hipLaunchKernelGGL((k_tile_mfma_s<XT, ST, GB, GATEUP, MF_NB>), grid, dim3(256), 0, s,
-                       (const uint16_t*)src, (u32)src_bytes, topk, ent, nent, perm, w, I,
-                       (uint16_t*)act, ys);
-  else
-    hipLaunchKernelGGL((k_tile_mfma<XT, ST, GB, GATEUP, MF_NB>), grid, dim3(256), 0, s,
-                       (const uint16_t*)src, (u32)src_bytes, topk, ent, nent, perm, w, I,
-                       (uint16_t*)act, ys);
+  const int n_out = GATEUP ? I : w.N;
+  const int cols = GATEUP ? 32 * MF_NB : 64 * MF_NB;
+#define I4_MF_LAUNCH(NB_, MB_)                                                                  \
+  hipLaunchKernelGGL((k_tile_mfma<XT, ST, GB, GATEUP, NB_, MB_>),                              \
+                     dim3(n_out / (cols * NB_ / MF_NB), max_entries), dim3(256), 0, s,          \
+                     (const uint16_t*)src, (u32)src_bytes, topk, ent, nent, perm, w, I,         \
+                     (uint16_t*)act, ys)
+  // small entries: one m-block and twice the n-blocks per wave when the rows allow
+  if (small && n_out % (2 * cols) == 0) I4_MF_LAUNCH(2 * MF_NB, 1);
+  else if (small) I4_MF_LAUNCH(MF_NB, 1);
+  else I4_MF_LAUNCH(MF_NB, MF_TOK / 16);
+#undef I4_MF_LAUNCH
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
