@@ -10,11 +10,16 @@
 // 32 t + 8 j) as they lie in memory: the tile word's interleaved nibbles put
 // the decoded halves in column order.
 //   fp16: B holds q - z exactly ((M + q) - (M + z), one packed half add per
-//         pair) and a group ends with res += s D.
-//   bf16: B holds M + q exactly (gfx950 has no packed bf16 add) and a group
-//         ends with res += s D - s (M + z) S_m, S_m the sum of token m's
-//         activations over the group.
-// Every product is exact and accumulation is fp32, as in the decode kernels.
+//         pair) and a group ends with res += s D.  Large entries (four
+//         m-blocks) instead fold the scale into B with one packed multiply,
+//         so each dequantised weight is rounded once to fp16 (relative error
+//         <= 2^-11, the numerics of dequantise-then-multiply) and the MFMA
+//         accumulates straight into the result: no second accumulator, which
+//         keeps a 64-token entry within 128 VGPRs.
+//   bf16: B holds M + q exactly (gfx950 has no packed bf16 add or multiply)
+//         and a group ends with res += s D - s (M + z) S_m, S_m the sum of
+//         token m's activations over the group.
+// Accumulation is fp32; apart from the fold every product is exact.
 //
 // All global reads are raw buffer loads: one descriptor per operand (an
 // expert's weights, scales and zero words; the activation rows), per-lane
@@ -103,6 +108,29 @@ template <int XT> __device__ inline u32x4 b_operand(u32 word, u32 nz, u32 mg) {
     b.w = sub_zero(b.w, nz);
   }
   return b;
+}
+
+// the group scale as two fp16 copies (rounded to fp16 when stored wider)
+template <int ST> __device__ inline u32 scale_h2(u32 raw) {
+  if constexpr (ST == I4_F16) {
+    return (raw & 0xFFFFu) * 0x00010001u;
+  } else {
+    const u32 h = __builtin_bit_cast(uint16_t, (_Float16)scale_from_raw<ST>(raw));
+    return h * 0x00010001u;
+  }
+}
+
+// fp16 pairs a * s (one v_pk_mul_f16)
+__device__ inline u32 mul_h2(u32 a, u32 s) {
+  return __builtin_bit_cast(u32, __builtin_bit_cast(f16x2, a) * __builtin_bit_cast(f16x2, s));
+}
+
+// fp16 B operand times the group scale: (q - z) s, one rounding per element.
+// The components go through scalars: a bit cast applied directly to a vector
+// component expression (b.y) reads component 0 with this compiler.
+__device__ inline u32x4 scale_b(u32x4 b, u32 s2) {
+  const u32 b0 = b.x, b1 = b.y, b2 = b.z, b3 = b.w;
+  return u32x4{mul_h2(b0, s2), mul_h2(b1, s2), mul_h2(b2, s2), mul_h2(b3, s2)};
 }
 
 // first row block of n-block nb of wave `wave` in column tile `tile`
@@ -198,6 +226,9 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
     uint16_t* __restrict__ act, float* __restrict__ ys) {
   constexpr bool EXACT = XT == I4_F16;
+  // fp16 with several m-blocks folds the scale into B (see the top); one
+  // m-block keeps the exact form, whose extra registers fit its occupancy
+  constexpr bool FOLD = EXACT && MB > 1;
   constexpr int COLS = GATEUP ? 32 * NB : 64 * NB;
   constexpr int TOK = 16 * MB;
   static_assert(!GATEUP || NB % 2 == 0, "gate_up pairs gate and up blocks");
@@ -275,11 +306,6 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     }
   };
   auto compute = [&](int sc, const TSlot<GB> (&sl)[NB], int buf) {
-    f32x4 d[MB][NB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) d[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int g0 = (4 * sc) >> w.gshift;
     u32 zw[NB], nz[NB];  // zero words; GB: one zero point for the superchunk
 #pragma unroll
@@ -287,6 +313,47 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
       zw[nb] = sl[nb].z | wb.zor;
       nz[nb] = EXACT && GB ? neg_zero2(zw[nb], g0) : 0u;
     }
+    if constexpr (FOLD) {
+      // fp16, several m-blocks: B = (q - z) s, one rounding, accumulated
+      // straight into res
+      u32 s2[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) s2[nb] = GB ? scale_h2<ST>(sl[nb].s[0]) : 0u;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int g = (4 * sc + t) >> w.gshift;
+        auto bop = [&](int nb) {
+          const u32 z2 = GB ? nz[nb] : neg_zero2(zw[nb], g);
+          const u32 sc2 = GB ? s2[nb] : scale_h2<ST>(sl[nb].s[t]);
+          return scale_b(b_operand<XT>(word_t(sl[nb].w, t), z2, mg), sc2);
+        };
+        if constexpr (MB == 1) {  // one m-block: each B operand feeds one MFMA
+          const u32x4 a = xs[buf][ln * MF_TSTRIDE + 4 * t + kb];
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) res[0][nb] = mfma16<XT>(a, bop(nb), res[0][nb]);
+        } else {
+          u32x4 b[NB];
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) b[nb] = bop(nb);
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+            if (mb < nmb) {
+              const u32x4 a = xs[buf][(16 * mb + ln) * MF_TSTRIDE + 4 * t + kb];
+#pragma unroll
+              for (int nb = 0; nb < NB; ++nb) res[mb][nb] = mfma16<XT>(a, b[nb], res[mb][nb]);
+            }
+          }
+        }
+      }
+      return;
+    } else {
+    // exact: B = q - z (fp16) or M + q (bf16), per-group correction (bf16 with
+    // the activation sums)
+    f32x4 d[MB][NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) d[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int g = (4 * sc + t) >> w.gshift;
@@ -295,14 +362,13 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
           d[0][nb] = mfma16<XT>(
-              a, b_operand<XT>(word_t(sl[nb].w, t), EXACT && !GB ? neg_zero2(zw[nb], g) : nz[nb], mg),
+              a, b_operand<XT>(word_t(sl[nb].w, t), GB ? nz[nb] : neg_zero2(zw[nb], g), mg),
               d[0][nb]);
       } else {
         u32x4 b[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
-          b[nb] = b_operand<XT>(word_t(sl[nb].w, t), EXACT && !GB ? neg_zero2(zw[nb], g) : nz[nb],
-                                mg);
+          b[nb] = b_operand<XT>(word_t(sl[nb].w, t), GB ? nz[nb] : neg_zero2(zw[nb], g), mg);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
           if (mb < nmb) {
@@ -338,6 +404,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
             correct<XT, ST>(res[mb][nb], d[mb][nb], sl[nb].s[0], zw[nb], g0, sm);
         }
       }
+    }
     }
   };
   // one superchunk: stage its activations (loaded one step earlier), load the
