@@ -218,8 +218,8 @@ def time_gemvs(pkg, torch, dev, replays=20):
       single:    K=2048 -> N=768, 640 distinct weight copies (526 MB, twice the Infinity
                  Cache) launched back to back;
       attention: q 2048->4096, k/v 2048->512, o 4096->2048, 64 distinct layer sets (628 MB),
-                 each projection timed on its own (all 64 copies back to back) and the four
-                 of a layer back to back.
+                 each projection timed on its own (all 64 copies back to back), the four
+                 of a layer back to back, and (CT) q/k/v as one launch followed by o.
     Each workload runs on the AWQ tensors as the checkpoint holds them (split-K kernel +
     reduction) and on their CT+zeros repack (one launch, what PackedLinear installs).
     Times are per GEMV (or per layer of four), mean / median / p99 over graph replays."""
@@ -288,6 +288,17 @@ def time_gemvs(pkg, torch, dev, replays=20):
     n2 = 64
     projs = {"q": Proj(2048, 4096, n2), "k": Proj(2048, 512, n2), "v": Proj(2048, 512, n2),
              "o": Proj(4096, 2048, n2)}
+    # the q, k, v rows of each layer set in one CT weight (what PackedQKV installs)
+    cts = [projs[n].keep[1] for n in ("q", "k", "v")]
+    qkv = Proj.__new__(Proj)
+    qkv.K, qkv.N = 2048, sum(c.N for c in cts)
+    wq = pkg.QWeight(torch.cat([c.packed for c in cts], 1), torch.cat([c.scale for c in cts], 1),
+                     torch.cat([c.zeros for c in cts], 1), "ct", G, qkv.N, qkv.K)
+    qkv.desc = {"ct": per_copy(wq)}
+    qkv.keep = (wq,)
+    qkv.x = projs["q"].x
+    qkv.y = torch.empty(1, qkv.N, dtype=torch.float16, device=dev)
+    qkv.ws = projs["q"].ws
     for layout in ("ct", "awq"):
         att = {}
         for name, p in projs.items():
@@ -302,6 +313,15 @@ def time_gemvs(pkg, torch, dev, replays=20):
         ts = graph_times(torch, layer_seq, replays)
         att["qkvo_back_to_back"] = stats(ts, n2, sum(awq_gemv_bytes(p.K, p.N)
                                                     for p in projs.values()))
+        if layout == "ct":  # q/k/v rows concatenated into one launch (PackedQKV), then o
+            def fused_seq():
+                for i in range(n2):
+                    qkv.launch("ct", i)
+                    projs["o"].launch("ct", i)
+
+            ts = graph_times(torch, fused_seq, replays)
+            att["qkv_fused_then_o"] = stats(ts, n2, sum(awq_gemv_bytes(p.K, p.N)
+                                                        for p in projs.values()))
         out[f"attention_{layout}"] = att
         log(f"attention q/k/v/o ({layout}): " + ", ".join(
             f"{k} {v['us']:.2f}" for k, v in att.items()) + " us")

@@ -10,7 +10,7 @@ include/i4moe.h).  There is no fallback: without the built library every op
 raises.
 """
 from . import _lib
-from .linear import PackedLinear, patch_attention
+from .linear import PackedLinear, PackedQKV, QKVSlice, concat_rows, patch_attention
 from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_forward, moe_gate_up,
                   moe_route_gate_up, moe_stack, route, router_logits, unpack4, unpack_nibbles,
@@ -24,5 +24,6 @@ __all__ = [
     "dequant", "router_logits", "route", "moe_forward", "moe_gate_up", "moe_route_gate_up",
     "moe_down_combine",
     "moe_stack", "Workspace",
-    "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "patch_attention", "lib",
+    "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "PackedQKV", "QKVSlice",
+    "concat_rows", "patch_attention", "lib",
 ]

@@ -142,40 +142,57 @@ __global__ __launch_bounds__(WG) void k_gemv_awq(
   constexpr u32 MK = 0x000F000Fu;
   const u32 mg = magic_v<XT>();
   const u32 ONE2 = XT == I4_F16 ? 0x3C003C00u : 0x3F803F80u;  // (1.0, 1.0)
-  for (int gk = k0; gk < kend; gk += group) {  // one quantisation group
+  // One quantisation group at a time, its rows in batches of RB row pairs per
+  // k-slot (128 rows): every weight word, the zero word and the 8 scales of a
+  // batch are loaded before any is used (indices clamped, so the loads are
+  // unconditional), then consumed -- one memory round trip per batch.
+  constexpr int RB = 8;
+  const int cwc = cv ? cw : NW - 1;
+  for (int gk = k0; gk < kend; gk += group) {
     const int g = gk / group;
+    const int gend = min(kend, gk + group);
+    const u32 zw = ze ? (u32)ze[(int64_t)g * NW + cwc] : 0x88888888u;
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t si = se + (int64_t)g * N + 8 * cwc + kAwqOrder[i];
+      sv[i] = st == I4_F32 ? load_scale<I4_F32>(scales, si)
+            : st == I4_F16 ? load_scale<I4_F16>(scales, si)
+                           : load_scale<I4_BF16>(scales, si);
+    }
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
     float S = 0.f;
-    const int gend = min(kend, gk + group);
-    for (int k = gk + 2 * slot; k < gend; k += 2 * AWQ_SLOTS) {
-      const u32 xp = xs2[(k - k0) >> 1];
-      S = Half<XT>::dot2(xp, ONE2, S);
-      if (cv) {
-        const u32 w0 = (u32)qe[(int64_t)k * NW + cw];
-        const u32 w1 = (u32)qe[(int64_t)(k + 1) * NW + cw];
+    for (int kb0 = gk + 2 * slot; kb0 < gend; kb0 += 2 * AWQ_SLOTS * RB) {
+      u32 w0[RB], w1[RB];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          // byte b of w0 -> bits 0..7, byte b of w1 -> bits 16..23
-          const u32 sel_b = 0x0C000C00u | (u32)(b) | ((u32)(4 + b) << 16);
-          const u32 tb = __builtin_amdgcn_perm(w1, w0, sel_b);
-          acc[2 * b] = Half<XT>::dot2((tb & MK) | mg, xp, acc[2 * b]);
-          acc[2 * b + 1] = Half<XT>::dot2(((tb >> 4) & MK) | mg, xp, acc[2 * b + 1]);
+      for (int r = 0; r < RB; ++r) {
+        const int k = min(kb0 + 2 * AWQ_SLOTS * r, gend - 2);
+        w0[r] = (u32)qe[(int64_t)k * NW + cwc];
+        w1[r] = (u32)qe[(int64_t)(k + 1) * NW + cwc];
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int k = kb0 + 2 * AWQ_SLOTS * r;
+        if (k < gend) {
+          const u32 xp = xs2[(k - k0) >> 1];
+          S = Half<XT>::dot2(xp, ONE2, S);
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            // byte b of w0 -> bits 0..7, byte b of w1 -> bits 16..23
+            const u32 sel_b = 0x0C000C00u | (u32)(b) | ((u32)(4 + b) << 16);
+            const u32 tb = __builtin_amdgcn_perm(w1[r], w0[r], sel_b);
+            acc[2 * b] = Half<XT>::dot2((tb & MK) | mg, xp, acc[2 * b]);
+            acc[2 * b + 1] = Half<XT>::dot2(((tb >> 4) & MK) | mg, xp, acc[2 * b + 1]);
+          }
         }
       }
     }
-    if (cv) {
-      const u32 zw = ze ? (u32)ze[(int64_t)g * NW + cw] : 0x88888888u;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float z = (float)((zw >> (4 * i)) & 15u);
-        const int64_t si = se + (int64_t)g * N + 8 * cw + kAwqOrder[i];
-        const float s = st == I4_F32 ? load_scale<I4_F32>(scales, si)
-                      : st == I4_F16 ? load_scale<I4_F16>(scales, si)
-                                     : load_scale<I4_BF16>(scales, si);
-        acc_tot[i] += s * (acc[i] - (Half<XT>::MAGIC + z) * S);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float z = (float)((zw >> (4 * i)) & 15u);
+      acc_tot[i] += sv[i] * (acc[i] - (Half<XT>::MAGIC + z) * S);
     }
   }
 #pragma unroll

@@ -251,6 +251,76 @@ def test_linear(pkg, dev, M, layout):
         assert i4ref.rel_err(got2, ref) <= TOL
 
 
+def test_packed_qkv_matches_three_linears(pkg, dev):
+    """q, k, v in one launch equal the three separate launches bit for bit (each row's dot
+    product does not depend on its neighbours): AWQ parts, and CT parts with and without
+    zero points side by side."""
+    rng = np.random.default_rng(41)
+    K, G = 2048, 128
+    x = t_(make_x(rng, (3, K), "f16"), dev)
+    for kind in ("awq", "ct-mixed"):
+        parts = []
+        for i, N in enumerate((512, 128, 128)):
+            if kind == "awq":
+                qw, qz, sc = _gen.awq_weight(rng, 1, K, N, G)
+                parts.append(pkg.QWeight(t_(qw, dev), t_(sc, dev), t_(qz, dev), "awq", G, N, K))
+            else:
+                p, sc, z = _gen.ct_weight(rng, 1, N, K, G, zeros=(i != 1))
+                parts.append(pkg.QWeight(t_(p, dev), t_(sc, dev), None if z is None else t_(z, dev),
+                                         "ct", G, N, K))
+        biases = [t_(rng.standard_normal(p.N).astype(np.float16), dev) for p in parts]
+        biases[2] = None
+        fused = pkg.PackedQKV.from_qweights(*parts, biases=biases)
+        got = fused(x)
+        for y, w, b in zip(got, parts, biases):
+            want = pkg.PackedLinear.from_qweight(w, b)(x)
+            assert torch.equal(y, want)
+
+
+class _FakePacked(torch.nn.Module):
+    """A compressed-tensors pack-quantized Linear as the reference's loader leaves it."""
+
+    def __init__(self, rng, N, K, G=32):
+        super().__init__()
+        p, sc, _ = _gen.ct_weight(rng, 1, N, K, G, sdt=np.float16)
+        self.weight_packed = torch.from_numpy(p[0].copy())
+        self.weight_scale = torch.from_numpy(sc[0].copy())
+        self.weight_shape = torch.tensor([N, K])
+        self.bias = None
+
+
+def test_patch_attention_fuses_qkv(pkg, dev):
+    """patch_attention(fuse_qkv=True) installs one launch for q/k/v; the block's q, k, v and
+    o outputs equal the unfused patch's."""
+    rng = np.random.default_rng(42)
+    K = 512
+
+    def block():
+        m = torch.nn.Module()
+        m.q_proj, m.k_proj, m.v_proj = _FakePacked(rng, 256, K), _FakePacked(rng, 64, K), \
+            _FakePacked(rng, 64, K)
+        m.o_proj = _FakePacked(rng, K, 256)
+        return m
+
+    a = block()
+    b = torch.nn.Module()
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+        src = getattr(a, name)
+        c = _FakePacked(rng, 1, 32)
+        c.weight_packed, c.weight_scale, c.weight_shape = (src.weight_packed.clone(),
+                                                           src.weight_scale.clone(),
+                                                           src.weight_shape.clone())
+        setattr(b, name, c)
+    assert pkg.patch_attention(a, device=dev, verbose=False, fuse_qkv=True) == 4
+    assert pkg.patch_attention(b, device=dev, verbose=False) == 4
+    assert isinstance(a.q_proj, pkg.QKVSlice) and isinstance(b.q_proj, pkg.PackedLinear)
+    x = t_(make_x(rng, (2, K), "f16"), dev)
+    for name in ("q_proj", "k_proj", "v_proj"):
+        assert torch.equal(getattr(a, name)(x), getattr(b, name)(x))
+    h = t_(make_x(rng, (2, 256), "f16"), dev)
+    assert torch.equal(a.o_proj(h), b.o_proj(h))
+
+
 def test_bad_expert_id_gives_nan_not_a_fault(pkg, dev):
     rng = np.random.default_rng(15)
     E, N, K, G = 4, 64, 256, 32

@@ -52,3 +52,31 @@ def test_library_path_is_in_tree(pkg):
 
     assert _lib.LIB_PATH.parent.name == "qwen3-omni-duplex_amd"
     assert _lib.LIB_PATH.exists()
+
+
+def test_shared_qkv_serves_each_slice_once_per_input(pkg):
+    """The fused q/k/v launch runs once for the three projections of one input and again for
+    a new input, even one that reuses the same memory (its cache is dropped after the third
+    slice), an in-place change, or a repeated slice."""
+    from qwen3_omni_duplex_amd.linear import _SharedQKV
+
+    calls = []
+
+    def fused(x):
+        calls.append(x.clone())
+        return (x + 1, x + 2, x + 3)
+
+    sh = _SharedQKV(fused)
+    x = torch.zeros(2, 4)
+    q, k, v = sh.take(x, 0), sh.take(x, 1), sh.take(x, 2)
+    assert len(calls) == 1 and torch.equal(q, x + 1) and torch.equal(v, x + 3)
+    # same storage, same version, after all three slices were served: a fresh launch
+    sh.take(x, 0)
+    assert len(calls) == 2
+    # an in-place change between the slices: recomputed from the new values
+    x.add_(5)
+    k2 = sh.take(x, 1)
+    assert len(calls) == 3 and torch.equal(k2, x + 2)
+    # the same slice twice without the others: the second call launches again
+    sh.take(x, 1)
+    assert len(calls) == 4
