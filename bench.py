@@ -51,7 +51,7 @@ B_LAYER = TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + B_ROUTER + 2 * H * 2      
 B_GATE_UP_LAUNCH = TOPK * B_GATE_UP_EXPERT + H * 2 + TOPK * I * 2
 # HBM bytes per decode gate_up launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (calibrated against a device copy; summary under profiles/)
-GATE_UP_TRAFFIC_BYTES = 13_424_000
+GATE_UP_TRAFFIC_BYTES = 13_435_000
 
 
 def log(msg: str) -> None:
