@@ -34,6 +34,39 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // 16-byte global load (global_load_dwordx4) of a packed-weight stream
 __device__ inline u32x4 ldg16(const void* p) { return *(const u32x4*)p; }
 
+// Raw buffer descriptors: base, size in bytes (loads past it return 0) and
+// word 3 of a gfx9 descriptor for raw (untyped) dword access.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+static constexpr int kRawBuffer = 0x00020000;
+__device__ inline rsrc_t rsrc(const void* base, u32 bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRawBuffer);
+}
+
+// Device-coherent accesses, for data that one workgroup of a launch hands to
+// another: the two may run on different XCDs, each with its own L2, so the
+// store writes through (sc1) and the load is served from memory, not from a
+// line its own L2 may still hold (sc1).  No fence is involved: a consumer
+// recognises finished data by its value (see the sentinel below).
+static constexpr int kCoherent = 16;  // cache-policy bit sc1 of a buffer access
+__device__ inline u32x4 ld16_coherent(rsrc_t r, u32 voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, kCoherent);
+}
+__device__ inline void st_coherent(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 0xFFFF is a NaN in fp16 and bf16 alike; producers that hand over halves
+// this way write every NaN in its canonical form, so the pattern never
+// occurs in finished data and marks a value not yet written.
+static constexpr u32 kPending16 = 0xFFFFu;
+__device__ inline bool has_pending(u32x4 d) {
+  const u32 w[4] = {d.x, d.y, d.z, d.w};
+  bool p = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p |= (w[i] & 0xFFFFu) == kPending16 || (w[i] >> 16) == kPending16;
+  return p;
+}
+
 // The nibble decode computes (w & mask) | magic.  A gfx9 VOP3 instruction
 // reads at most one SGPR and takes no literal, so with both operands constant
 // the compiler emits v_and_b32 + v_or_b32; with the magic in a VGPR it is one
@@ -52,6 +85,7 @@ template <int DT> struct Half;
 
 template <> struct Half<I4_F16> {
   static constexpr u32 MAGIC2 = 0x64006400u;  // two fp16 1024.0
+  static constexpr uint16_t QNAN = 0x7E00u;   // canonical quiet NaN
   static constexpr float MAGIC = 1024.0f;
   __device__ static inline float to_f32(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
@@ -67,6 +101,7 @@ template <> struct Half<I4_F16> {
 
 template <> struct Half<I4_BF16> {
   static constexpr u32 MAGIC2 = 0x43004300u;  // two bf16 128.0
+  static constexpr uint16_t QNAN = 0x7FC0u;   // canonical quiet NaN
   static constexpr float MAGIC = 128.0f;
   __device__ static inline float to_f32(uint16_t b) {
     return __builtin_bit_cast(float, (u32)b << 16);

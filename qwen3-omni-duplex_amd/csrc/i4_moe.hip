@@ -227,12 +227,14 @@ struct MoeOps {
                       const TW&, int, void*, hipStream_t);
   int (*mfma_down)(bool, int, const void*, int, const int4*, const int*, const int32_t*,
                    const TW&, float*, hipStream_t);
+  int (*moe_m1_ct)(const GateUpArgs&, const TW&, const TW&, const void*, void*, hipStream_t);
 };
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
   return MoeOps{&launch_gate_up<XT, ST>,     &launch_down_m1<XT, ST>,
                 &launch_gate_up_ct<XT, ST>,  &launch_down_m1_ct<XT, ST>,
-                &launch_mfma_gate_up<XT, ST>, &launch_mfma_down<XT, ST>};
+                &launch_mfma_gate_up<XT, ST>, &launch_mfma_down<XT, ST>,
+                &launch_moe_m1_ct<XT, ST>};
 }
 
 bool pick_ops(int xt, int gst, int dst, MoeOps* ops) {
@@ -312,16 +314,23 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   int32_t* sel = sel_out ? sel_out : ws.sel;
   float* wts = w_out ? w_out : ws.w;
   const bool ct = gu.layout == I4_LAYOUT_CT;
-  if (T == 1) {  // decode: router -> gate_up (ranks the logits itself) -> down + combine
+  if (T == 1) {
+    // decode: router -> gate_up (ranks the logits itself) -> down + combine;
+    // on CT rows with the router in the block, both expert projections run
+    // as one launch whose down workgroups wait for act in the kernel (the
+    // router launch marks act pending first)
+    const bool one = ct && mw->router_w && moe_m1_ct_fits(topk, H, I);
     const void* lg = logits;
     if (mw->router_w) {
       rc = i4_launch_router_logits(x, xt, 1, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
-                                   mw->norm_w ? ws.xn : nullptr, ws.logits, s);
+                                   mw->norm_w ? ws.xn : nullptr, ws.logits, s,
+                                   one ? ws.act : nullptr, one ? topk * I / 8 : 0);
       if (rc) return rc;
       lg = ws.logits;
       if (mw->norm_w) x = ws.xn;  // the experts run on RMSNorm(x); residual is untouched
     }
     const GateUpArgs a{true, topk, topk, E, renorm, x, sel, lg, wts, ws.act};
+    if (one) return ops.moe_m1_ct(a, to_tw(gu), to_tw(dn), residual, out, s);
     rc = (ct ? ops.gate_up_ct : ops.gate_up)(a, to_tw(gu), I, s);
     if (rc) return rc;
     return (ct ? ops.down_m1_ct : ops.down_m1)(ws.act, topk, sel, wts, to_tw(dn), residual, out, s);

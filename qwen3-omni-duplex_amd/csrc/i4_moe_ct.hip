@@ -15,6 +15,10 @@
 //   k_ct_down_m1: a workgroup owns a slice of output rows across ALL selected
 //     experts, so the routing-weighted combine and the residual add happen in
 //     LDS in a fixed slot order: no atomics, bit-reproducible run to run.
+//   k_ct_moe_m1: both in one launch (the decode path when the block carries
+//     its router): the down workgroups issue their weight loads while gate_up
+//     streams and take act over from the gate_up workgroups inside the launch.
+//     Same arithmetic as the two kernels above, bit for bit.
 #include "i4_launch.h"
 #include "i4_moe_launch.h"
 #include "i4_topk.h"
@@ -52,13 +56,13 @@ template <int ST> __device__ inline RowPtr row_ptr(const QW& w, int e, int n) {
 //             bit-identical in every wave) and takes its slot; workgroup
 //             (0, 0) writes sel[] / wts[] for the down projection
 
-template <int XT, int ST, int L, int MODE>
-__global__ __launch_bounds__(WG) void k_ct_gate_up(
-    const uint16_t* __restrict__ x, int topk, int32_t* __restrict__ sel,
-    const uint16_t* __restrict__ logits, int E_r, int renorm, float* __restrict__ wts, QW w,
-    int I, uint16_t* __restrict__ act) {
+template <int XT, int ST, int L, int MODE, bool HANDOFF>
+__device__ inline void gate_up_body(int bx, int by, const uint16_t* __restrict__ x, int topk,
+                                    int32_t* __restrict__ sel,
+                                    const uint16_t* __restrict__ logits, int E_r, int renorm,
+                                    float* __restrict__ wts, const QW& w, int I,
+                                    uint16_t* __restrict__ act, unsigned char* lds) {
   constexpr int MT = 1;
-  extern __shared__ __align__(16) unsigned char lds[];
   constexpr int RPW = WG / L;
   constexpr int ROUND = 2;
   const int H = w.K, C = H >> 5;
@@ -66,7 +70,7 @@ __global__ __launch_bounds__(WG) void k_ct_gate_up(
   u32x4* xs = (u32x4*)lds;
   float2* sums = (float2*)(lds + (size_t)MT * H * 2);
 
-  const int pos0 = blockIdx.y, cnt = 1;
+  const int pos0 = by, cnt = 1;
   const u32 mg = magic_v<XT>();
   Stager<XT> st(MT, H);
   auto row_of = [&](int) -> const uint16_t* { return x; };
@@ -78,22 +82,22 @@ __global__ __launch_bounds__(WG) void k_ct_gate_up(
       u32 raw[VPL];
       load_row<XT, VPL>(logits, 0, E_r, raw);
       st.issue(row_of, 0);
-      if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
+      if (bx == 0 && by == 0 && threadIdx.x < 64) {
         int my_sel = 0;
         float my_w = 0.f;
         topk_row<XT, VPL>(raw, 0, E_r, topk, renorm, sel, wts, nullptr, 0, &my_sel, &my_w);
         return __builtin_amdgcn_readlane(my_sel, 0);
       }
-      return topk_slot<XT, VPL>(raw, E_r, blockIdx.y);
+      return topk_slot<XT, VPL>(raw, E_r, by);
     };
     e = E_r <= 128 ? route(std::integral_constant<int, 2>{})
                    : route(std::integral_constant<int, 8>{});
   } else {
     st.issue(row_of, 0);
-    e = sel[blockIdx.y];
+    e = sel[by];
   }
   const int rl = threadIdx.x / L, cl = threadIdx.x % L;
-  const int n = blockIdx.x * RPW + rl;
+  const int n = bx * RPW + rl;
   const bool rv = n < I;
   const bool ev = (unsigned)e < (unsigned)w.E;
   const int nn = rv ? n : 0, ee = ev ? e : 0;
@@ -144,10 +148,23 @@ __global__ __launch_bounds__(WG) void k_ct_gate_up(
   for (int t = 0; t < MT; ++t) {
     const float g = group_sum<L>(ag[t]);
     const float u = group_sum<L>(au[t]);
-    if (rv && cl == 0 && t < cnt)
-      act[(int64_t)(pos0 + t) * I + n] =
-          Half<XT>::from_f32(ev ? silu(g) * u : __builtin_nanf(""));
+    if (rv && cl == 0 && t < cnt) {
+      const float v = ev ? silu(g) * u : __builtin_nanf("");
+      uint16_t* dst = act + (int64_t)(pos0 + t) * I + n;
+      if constexpr (HANDOFF) st_coherent(dst, v != v ? Half<XT>::QNAN : Half<XT>::from_f32(v));
+      else *dst = Half<XT>::from_f32(v);
+    }
   }
+}
+
+template <int XT, int ST, int L, int MODE>
+__global__ __launch_bounds__(WG) void k_ct_gate_up(
+    const uint16_t* __restrict__ x, int topk, int32_t* __restrict__ sel,
+    const uint16_t* __restrict__ logits, int E_r, int renorm, float* __restrict__ wts, QW w,
+    int I, uint16_t* __restrict__ act) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  gate_up_body<XT, ST, L, MODE, false>(blockIdx.x, blockIdx.y, x, topk, sel, logits, E_r, renorm,
+                                       wts, w, I, act, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -162,12 +179,40 @@ template <int L> struct DownShape {
   static constexpr int RW = NGR / GPR;
 };
 
-template <int XT, int ST, int L, int JMAX>
-__global__ __launch_bounds__(WG) void k_ct_down_m1(
-    const uint16_t* __restrict__ act, int topk, const int32_t* __restrict__ sel,
-    const float* __restrict__ wts, QW w, const uint16_t* __restrict__ residual,
-    uint16_t* __restrict__ out) {
-  extern __shared__ __align__(16) unsigned char lds[];
+// Polls for the activations of a handoff launch: the rows are loaded
+// device-coherently until no value still holds the pending pattern (the
+// router's launch fills them with it; gate_up workgroups of the same launch
+// overwrite every value).  Returns true if kHandoffSpins polls went by
+// without that, which a launch whose workgroups are dispatched in block order
+// never sees: the bound only guarantees that every wave exits.
+static constexpr int kHandoffSpins = 1 << 20;
+template <int XT> __device__ inline bool poll_rows(Stager<XT>& st, const uint16_t* src) {
+  const int nt = blockDim.x;
+  const rsrc_t r = rsrc(src, (u32)st.total * 16u);
+  for (int it = 0;; ++it) {
+    bool pend = false;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = min(u * nt + (int)threadIdx.x, st.total - 1);
+      st.d[u] = ld16_coherent(r, (u32)idx * 16u);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pend |= has_pending(st.d[u]);
+    if (!__syncthreads_or(pend)) return false;
+    if (it == kHandoffSpins) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// HANDOFF: the experts and routing weights come from the logits (every wave
+// ranks them itself, bit-identical to the gate_up workgroups), and act is
+// polled as it is written by the gate_up workgroups of the same launch.
+template <int XT, int ST, int L, int JMAX, bool HANDOFF>
+__device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int topk,
+                                 const int32_t* __restrict__ sel, const float* __restrict__ wts,
+                                 const uint16_t* __restrict__ logits, int E_r, int renorm,
+                                 const QW& w, const uint16_t* __restrict__ residual,
+                                 uint16_t* __restrict__ out, unsigned char* lds) {
   constexpr int GPR = DownShape<L>::GPR, RW = DownShape<L>::RW;
   constexpr int CR = 4;  // chunks per round
   const int I = w.K, H = w.N, C = I >> 5;
@@ -178,21 +223,34 @@ __global__ __launch_bounds__(WG) void k_ct_down_m1(
 
   static_assert(L * RW >= 64, "the expert group must be uniform across a wave");
   __shared__ float s_w[16];  // routing weights, loaded with the first wave of loads
-  // unconditional loads (clamped indices): a guarded load would be waited for
-  // where its branch joins, before anything else is issued
-  const float wv = wts[min((int)threadIdx.x, topk - 1)];
-  const int on = blockIdx.x * RW + (int)threadIdx.x;  // output row of the combine threads
+  const int gi = threadIdx.x / L, cl = threadIdx.x % L;
+  const int r = gi % RW;
+  const int jg = __builtin_amdgcn_readfirstlane(gi / RW);  // wave-uniform: sel[] via s_load
+  int my_sel = 0;
+  float wv = 0.f;  // lane j < topk of wave 0: slot j's routing weight
+  if constexpr (HANDOFF) {
+    auto route = [&](auto vpl) {
+      constexpr int VPL = decltype(vpl)::value;
+      u32 raw[VPL];
+      load_row<XT, VPL>(logits, 0, E_r, raw);
+      topk_row<XT, VPL>(raw, 0, E_r, topk, renorm, nullptr, nullptr, nullptr, 0, &my_sel, &wv);
+    };
+    if (E_r <= 128) route(std::integral_constant<int, 2>{});
+    else route(std::integral_constant<int, 8>{});
+  } else {
+    // unconditional loads (clamped indices): a guarded load would be waited
+    // for where its branch joins, before anything else is issued
+    wv = wts[min((int)threadIdx.x, topk - 1)];
+  }
+  const int on = bx * RW + (int)threadIdx.x;  // output row of the combine threads
   const bool comb = (int)threadIdx.x < RW && on < H;
   const uint16_t res_raw = *(residual ? residual + min(on, H - 1) : act);
   // activations next (all selected rows, contiguous act[j][I])
   const u32 mg = magic_v<XT>();
   Stager<XT> st(topk, I);
   auto row_of = [&](int j) { return act + (int64_t)j * I; };
-  st.issue(row_of, 0);
-  const int gi = threadIdx.x / L, cl = threadIdx.x % L;
-  const int r = gi % RW;
-  const int jg = __builtin_amdgcn_readfirstlane(gi / RW);  // wave-uniform: sel[] via s_load
-  const int n = blockIdx.x * RW + r;
+  if constexpr (!HANDOFF) st.issue(row_of, 0);
+  const int n = bx * RW + r;
   const bool rv = n < H;
   const int nn = rv ? n : 0;
 
@@ -201,7 +259,8 @@ __global__ __launch_bounds__(WG) void k_ct_down_m1(
 #pragma unroll
   for (int jj = 0; jj < JMAX; ++jj) {
     const int j = jg + jj * GPR;
-    ej[jj] = j < topk ? sel[j] : -1;
+    if constexpr (HANDOFF) ej[jj] = j < topk ? __builtin_amdgcn_readlane(my_sel, j) : -1;
+    else ej[jj] = j < topk ? sel[j] : -1;
     const int ee = (unsigned)ej[jj] < (unsigned)w.E ? ej[jj] : 0;
     rp[jj] = row_ptr<ST>(w, ee, nn);
   }
@@ -236,8 +295,10 @@ __global__ __launch_bounds__(WG) void k_ct_down_m1(
   // round 0 is peeled: a loop-header wait would hold its weight loads behind
   // the activation loads
   load_round(0);
+  bool late = false;
+  if constexpr (HANDOFF) late = poll_rows<XT>(st, act);  // the rows fit one staging round
   st.commit(0, xs, sums);
-  st.rest(row_of, xs, sums);
+  if constexpr (!HANDOFF) st.rest(row_of, xs, sums);
   if ((int)threadIdx.x < topk) s_w[threadIdx.x] = wv;
   __syncthreads();
   dot_round(0);
@@ -256,10 +317,54 @@ __global__ __launch_bounds__(WG) void k_ct_down_m1(
   if (comb) {
     float y = 0.f;
     for (int j = 0; j < topk; ++j) y += s_w[j] * red[j * RW + (int)threadIdx.x];
+    if (late) y = __builtin_nanf("");
     out[on] = Half<XT>::from_f32((residual ? Half<XT>::to_f32(res_raw) : 0.f) + y);
   }
 }
 
+template <int XT, int ST, int L, int JMAX>
+__global__ __launch_bounds__(WG) void k_ct_down_m1(
+    const uint16_t* __restrict__ act, int topk, const int32_t* __restrict__ sel,
+    const float* __restrict__ wts, QW w, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ out) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  down_body<XT, ST, L, JMAX, false>(blockIdx.x, act, topk, sel, wts, nullptr, 0, 0, w, residual,
+                                    out, lds);
+}
+
+// ---------------------------------------------------------------------------
+// One launch for the experts of a decode layer: gate_up workgroups first
+// (block b < n_gate: slot b / gx, row block b % gx), then the down
+// workgroups, which rank the logits, issue their weight loads and then wait
+// for the activations by polling them (poll_rows).  Only later blocks wait,
+// and only for earlier ones, so a launch whose workgroups are dispatched in
+// block order always completes; the down weights stream while gate_up runs,
+// and the kernel boundary between the two projections is gone.
+struct MoeM1Args {
+  const uint16_t* x;
+  int topk;
+  int32_t* sel;
+  const uint16_t* logits;
+  int E_r, renorm;
+  float* wts;
+  QW gu, dn;
+  uint16_t* act;
+  const uint16_t* residual;
+  uint16_t* out;
+  int gx, n_gate;
+};
+
+template <int XT, int ST, int LG, int LD, int JMAX>
+__global__ __launch_bounds__(WG) void k_ct_moe_m1(MoeM1Args a) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int b = blockIdx.x;
+  if (b < a.n_gate)
+    gate_up_body<XT, ST, LG, GU_ROUTE, true>(b % a.gx, b / a.gx, a.x, a.topk, a.sel, a.logits,
+                                             a.E_r, a.renorm, a.wts, a.gu, a.dn.K, a.act, lds);
+  else
+    down_body<XT, ST, LD, JMAX, true>(b - a.n_gate, a.act, a.topk, nullptr, nullptr, a.logits,
+                                      a.E_r, a.renorm, a.dn, a.residual, a.out, lds);
+}
 
 // ---------------------------------------------------------------------------
 // launchers
@@ -335,10 +440,63 @@ int launch_down_m1_ct(const void* act, int topk, const int32_t* sel, const float
   return I4_ERR_SHAPE;
 }
 
+// The single-launch layer covers the lane shapes of the usual widths (gate_up
+// lanes 8..64; down lanes 8 or 16, i.e. I < 1536) with topk <= 8 and the
+// activation rows in one staging round of the down workgroups.
+bool moe_m1_ct_fits(int topk, int H, int I) {
+  const int LD = lanes_per_row(I / 32);
+  if (topk > 8 || (LD != 8 && LD != 16)) return false;
+  if ((int64_t)topk * (I / 8) > 4 * WG) return false;
+  const size_t lds_d = (size_t)topk * (I * 2 + (I / 32) * 8) + (size_t)topk * 8 * 4;
+  const size_t lds_g = (size_t)H * 2 + (H / 32) * 8;
+  return lds_d <= kMaxLds && lds_g <= kMaxLds;
+}
+
+template <int XT, int ST>
+int launch_moe_m1_ct(const GateUpArgs& ga, const TW& tgu, const TW& tdn, const void* res,
+                     void* out, hipStream_t s) {
+  MoeM1Args a;
+  a.gu = to_qw(tgu);
+  a.dn = to_qw(tdn);
+  const int H = a.gu.K, I = a.dn.K;
+  if (!moe_m1_ct_fits(ga.topk, H, I)) return I4_ERR_SHAPE;
+  const int LG = gate_up_lanes(H / 32), LD = lanes_per_row(I / 32);
+  a.x = (const uint16_t*)ga.x;
+  a.topk = ga.topk;
+  a.sel = ga.sel;
+  a.logits = (const uint16_t*)ga.logits;
+  a.E_r = ga.E_r;
+  a.renorm = ga.renorm;
+  a.wts = ga.wts;
+  a.act = (uint16_t*)ga.act;
+  a.residual = (const uint16_t*)res;
+  a.out = (uint16_t*)out;
+  const int rpw = WG / LG;
+  a.gx = (I + rpw - 1) / rpw;
+  a.n_gate = a.gx * ga.topk;
+  constexpr int RW = 8;  // DownShape<8>::RW == DownShape<16>::RW
+  static_assert(DownShape<8>::RW == RW && DownShape<16>::RW == RW, "down rows per workgroup");
+  const size_t lds_d = (size_t)ga.topk * (I * 2 + (I / 32) * 8) + (size_t)ga.topk * RW * 4;
+  const size_t lds_g = (size_t)H * 2 + (H / 32) * 8;
+  const size_t lds = lds_d > lds_g ? lds_d : lds_g;
+  const dim3 grid(a.n_gate + (H + RW - 1) / RW);
+#define I4_M1_CASE(LG_, LD_, J_)                                                              \
+  if (LG == LG_ && LD == LD_) {                                                               \
+    hipLaunchKernelGGL((k_ct_moe_m1<XT, ST, LG_, LD_, J_>), grid, dim3(WG), lds, s, a);      \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                           \
+  }
+  I4_M1_CASE(8, 8, 2) I4_M1_CASE(16, 8, 2) I4_M1_CASE(32, 8, 2) I4_M1_CASE(64, 8, 2)
+  I4_M1_CASE(8, 16, 4) I4_M1_CASE(16, 16, 4) I4_M1_CASE(32, 16, 4) I4_M1_CASE(64, 16, 4)
+#undef I4_M1_CASE
+  return I4_ERR_SHAPE;
+}
+
 #define I4_INST(XT_, ST_)                                                                      \
   template int launch_gate_up_ct<XT_, ST_>(const GateUpArgs&, const TW&, int, hipStream_t);    \
   template int launch_down_m1_ct<XT_, ST_>(const void*, int, const int32_t*, const float*,     \
-                                           const TW&, const void*, void*, hipStream_t);
+                                           const TW&, const void*, void*, hipStream_t);        \
+  template int launch_moe_m1_ct<XT_, ST_>(const GateUpArgs&, const TW&, const TW&, const void*, \
+                                          void*, hipStream_t);
 I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
 I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)
 #undef I4_INST

@@ -40,6 +40,13 @@ int launch_gate_up_ct(const GateUpArgs& a, const TW& w, int I, hipStream_t s);
 template <int XT, int ST>
 int launch_down_m1_ct(const void* act, int topk, const int32_t* sel, const float* wts,
                       const TW& w, const void* residual, void* out, hipStream_t s);
+// both expert projections of a decode layer in one launch (route mode only);
+// act must hold the pending pattern (kPending16) in its topk * I values, which
+// the T = 1 router launch writes.  moe_m1_ct_fits says which shapes it covers.
+bool moe_m1_ct_fits(int topk, int H, int I);
+template <int XT, int ST>
+int launch_moe_m1_ct(const GateUpArgs& a, const TW& gate_up, const TW& down,
+                     const void* residual, void* out, hipStream_t s);
 
 // Grouped (T > 1) expert projections on MFMA.  entries[i] = {expert, first
 // position, tokens, 0} of the expert-sorted (token, slot) list perm; small

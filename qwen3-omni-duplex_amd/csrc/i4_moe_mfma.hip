@@ -51,15 +51,6 @@ static constexpr int MF_TSTRIDE = 17;  // uint4 per staged token row (16 + 1 pad
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-// word 3 of a gfx9 buffer descriptor for raw (untyped) dword loads
-static constexpr int kRawBuffer = 0x00020000;
-
-__device__ inline rsrc_t rsrc(const void* base, u32 bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           kRawBuffer);
-}
 __device__ inline u32x4 bload16(rsrc_t r, u32 voff, int soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
