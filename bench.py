@@ -18,8 +18,8 @@ three layers):
 
 Printed: one JSON line with value = us per layer (stack time / 24, median and
 p99 of the per-token times beside it), plus the roofline of the dominant
-kernel (the decode gate_up + SiLU launch) timed with HIP events on the stream
-it runs on, and a CPU baseline (the reference's CPU expert path restated in
+kernel (the decode experts launch: routing, gate/up, SiLU, down and combine of
+the 8 experts) timed with HIP events on the stream it runs on, and a CPU baseline (the reference's CPU expert path restated in
 torch, oracle/cpu_baseline.py) timed on this host.  Extra fields time the same
 layer at M = 32 (router from weights) and M = 512 (Zipf-skewed logits) with
 their realised expert histograms, HBM and MFMA fractions, and the dequant-GEMV
@@ -48,10 +48,12 @@ B_GATE_UP_EXPERT = 2 * (H * I // 2 + (H // G) * I * 2 + (H // G) * (I // 8) * 4)
 B_DOWN_EXPERT = I * H // 2 + (I // G) * H * 2 + (I // G) * (H // 8) * 4            # 817,152
 B_ROUTER = E * H * 2
 B_LAYER = TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + B_ROUTER + 2 * H * 2        # 20,144,128
-B_GATE_UP_LAUNCH = TOPK * B_GATE_UP_EXPERT + H * 2 + TOPK * I * 2
-# HBM bytes per decode gate_up launch measured with rocprofv3 --pmc FETCH_SIZE and
+# the decode experts launch: 8 experts' gate/up and down weights, the normalised input
+# and the residual in, the activations out and back in, the layer output out
+B_EXPERTS_LAUNCH = TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + 3 * H * 2 + 2 * TOPK * I * 2
+# HBM bytes per decode experts launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (calibrated against a device copy; summary under profiles/)
-GATE_UP_TRAFFIC_BYTES = 13_435_000
+EXPERTS_TRAFFIC_BYTES = None
 
 
 def log(msg: str) -> None:
@@ -125,54 +127,58 @@ def gpu_backlog(torch, dev, ms=20.0):
     return c
 
 
-def time_gate_up(pkg, torch, dev, mods, xns, logits, rounds):
-    """HIP-event timing of the dominant kernel, the decode route + gate_up + SiLU launch, on
-    each layer's own normalised input and logits: back-to-back launches over the layers
-    between one pair of events (average per launch), and each launch bracketed by its own
-    events behind a queued backlog (includes the event overhead)."""
+def time_experts(pkg, torch, dev, mods, hs, rounds):
+    """HIP-event timing of the dominant kernel, k_ct_moe_m1 (top-8 routing, gate/up, SiLU,
+    down, routing-weighted combine and residual of the 8 experts in one launch).  It runs
+    behind its router launch inside one i4_moe_forward call, so it is timed as the
+    difference of two back-to-back loops over the 24 layers on the same stream, each
+    between one pair of events behind a queued backlog: whole decode layers
+    (i4_moe_forward on each layer's own input) and the router launches alone
+    (i4_router_logits, same inputs).  Returns (experts us, layer us, router us) per launch."""
     lb = pkg.lib()
-    from qwen3_omni_duplex_amd import _lib
+    from qwen3_omni_duplex_amd import _lib, ops
 
     stream = torch.cuda.current_stream(dev)
     s_ptr = stream.cuda_stream
-    acts = [torch.empty(TOPK, I, dtype=torch.float16, device=dev) for _ in mods]
-    sel = torch.empty(TOPK, dtype=torch.int32, device=dev)
-    wts = torch.empty(TOPK, dtype=torch.float32, device=dev)
-    cws = [m.gate_up.c() for m in mods]
-    args = [(xns[li].data_ptr(), _lib.F16, ctypes.byref(cws[li]), logits[li].data_ptr(), E, TOPK, 1,
-             sel.data_ptr(), wts.data_ptr(), acts[li].data_ptr(), s_ptr) for li in range(len(mods))]
+    n = len(mods)
+    mws = [ops.moe_weights_c(*m.stack_entry()[:5]) for m in mods]
+    nbytes = lb.i4_moe_workspace_bytes(1, H, I, E, TOPK)
+    wbuf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    outs = [torch.empty(1, H, dtype=torch.float16, device=dev) for _ in mods]
+    xn = torch.empty(1, H, dtype=torch.float16, device=dev)
+    lg = torch.empty(1, E, dtype=torch.float16, device=dev)
 
-    def launch(li):
-        rc = lb.i4_moe_route_gate_up(*args[li])
+    def layer(li):
+        rc = lb.i4_moe_forward(hs[li].data_ptr(), _lib.F16, 1, ctypes.byref(mws[li]), TOPK, 1,
+                               None, hs[li].data_ptr(), outs[li].data_ptr(), None, None,
+                               wbuf.data_ptr(), nbytes, s_ptr)
         if rc:
             raise RuntimeError(lb.i4_strerror(rc).decode())
 
-    n = len(mods)
-    for li in range(n):  # warm
-        launch(li)
-    torch.cuda.synchronize()
-    gpu_backlog(torch, dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(rounds):
-        for li in range(n):
-            launch(li)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    batched = e0.elapsed_time(e1) * 1e3 / (n * rounds)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(n * rounds)]
-    gpu_backlog(torch, dev)
-    k = 0
-    for _ in range(rounds):
-        for li in range(n):
-            evs[k][0].record(stream)
-            launch(li)
-            evs[k][1].record(stream)
-            k += 1
-    torch.cuda.synchronize()
-    per = [a.elapsed_time(b) * 1e3 for a, b in evs]
-    return batched, sum(per) / len(per)
+    def router(li):
+        m = mods[li]
+        rc = lb.i4_router_logits(hs[li].data_ptr(), _lib.F16, 1, H, m.router_w.data_ptr(), E,
+                                 m.norm_weight.data_ptr(), float(m.norm_eps), xn.data_ptr(),
+                                 lg.data_ptr(), s_ptr)
+        if rc:
+            raise RuntimeError(lb.i4_strerror(rc).decode())
+
+    def loop(fn):
+        for li in range(n):  # warm
+            fn(li)
+        torch.cuda.synchronize()
+        gpu_backlog(torch, dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(rounds):
+            for li in range(n):
+                fn(li)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (n * rounds)
+
+    us_layer, us_router = loop(layer), loop(router)
+    return us_layer - us_router, us_layer, us_router
 
 
 def awq_gemv_bytes(K, N):
@@ -475,19 +481,17 @@ def main() -> int:
     ms = ms_graph if ms_graph is not None else ms_eager
     us_layer = ms * 1e3 / args.layers
 
-    # ---- dominant kernel: decode route + gate_up + SiLU, HIP events on its stream
-    xns, lgs = [], []
+    # ---- dominant kernel: the decode experts launch, HIP events on its stream
+    hs = []
     h = xs[1]
     for m in mods:
-        lg, xn = ops.router_logits(h, m.router_w, m.norm_weight, m.norm_eps, return_xn=True)
-        xns.append(xn.reshape(-1).contiguous())
-        lgs.append(lg.reshape(-1).contiguous())
+        hs.append(h)
         h = m(h, residual=h)
     torch.cuda.synchronize()
-    k_us, k_evt = time_gate_up(pkg, torch, dev, mods, xns, lgs, args.kernel_rounds)
-    achieved = B_GATE_UP_LAUNCH / (k_us * 1e-6) / 1e9
-    log(f"route+gate_up kernel: {k_us:.2f} us/launch back-to-back ({k_evt:.2f} with per-launch "
-        f"events) -> {achieved:.0f} GB/s")
+    k_us, k_layer, k_router = time_experts(pkg, torch, dev, mods, hs, args.kernel_rounds)
+    achieved = B_EXPERTS_LAUNCH / (k_us * 1e-6) / 1e9
+    log(f"experts kernel: {k_us:.2f} us/launch (layer {k_layer:.2f} - router {k_router:.2f}, "
+        f"back-to-back) -> {achieved:.0f} GB/s")
 
     # ---- other workloads of the same layer: M=32 (router from weights) and M=512 prefill
     # with Zipf(1.1)-skewed logits (MFMA tiles for hot experts), rotating over the layers
@@ -583,11 +587,13 @@ def main() -> int:
         "layer_GBps": round(B_LAYER / (us_layer * 1e-6) / 1e9, 1),
         "layer_hbm_frac": round(B_LAYER / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": "k_ct_gate_up<route> (decode top-8 routing + gate/up + SiLU, 8 experts)",
+            "kernel": "k_ct_moe_m1 (decode top-8 routing + gate/up + SiLU + down + combine, "
+                      "8 experts, one launch)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
-            "bytes_per_launch": B_GATE_UP_LAUNCH, "us_per_launch": round(k_us, 3),
-            "us_per_launch_own_events": round(k_evt, 3),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": EXPERTS_TRAFFIC_BYTES,
+            "bytes_per_launch": B_EXPERTS_LAUNCH, "us_per_launch": round(k_us, 3),
+            "timing": "layer launches minus router launches, back to back over the 24 layers",
+            "us_per_layer_launches": round(k_layer, 3), "us_per_router_launch": round(k_router, 3),
         },
         "cpu_baseline": cpu,
         "other_workloads": prefill,

@@ -23,6 +23,7 @@
 #include "i4_common.h"
 #include "i4_launch.h"
 #include "i4_moe_launch.h"
+#include "i4_topk.h"
 
 namespace i4 {
 
@@ -80,14 +81,12 @@ __device__ inline int wave_incl_scan(int v) {
   return v;
 }
 
-__global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel, int T, int topk,
-                                                int E, int lo_max, int lo_chunk,
-                                                int32_t* __restrict__ perm,
-                                                int4* __restrict__ entries,
-                                                int* __restrict__ n_entries,
-                                                int4* __restrict__ mf_entries,
-                                                int* __restrict__ n_mf_entries) {
-  extern __shared__ __align__(16) unsigned char lds[];
+// sel may point to LDS (k_route_group) or to global memory (k_group).
+__device__ inline void group_body(const int32_t* sel, int T, int topk, int E, int lo_max,
+                                  int lo_chunk, int32_t* __restrict__ perm,
+                                  int4* __restrict__ entries, int* __restrict__ n_entries,
+                                  int4* __restrict__ mf_entries, int* __restrict__ n_mf_entries,
+                                  unsigned char* lds) {
   __shared__ int s_wsum[16][3];
   const int TW = (T + 31) >> 5;
   u32* bits = (u32*)lds;
@@ -148,6 +147,43 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
         entries[eoff + q] = int4{tid, off + q * lo_chunk, min(lo_chunk, c - q * lo_chunk), 0};
     }
   }
+}
+
+__global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel, int T, int topk,
+                                                int E, int lo_max, int lo_chunk,
+                                                int32_t* __restrict__ perm,
+                                                int4* __restrict__ entries,
+                                                int* __restrict__ n_entries,
+                                                int4* __restrict__ mf_entries,
+                                                int* __restrict__ n_mf_entries) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  group_body(sel, T, topk, E, lo_max, lo_chunk, perm, entries, n_entries, mf_entries,
+             n_mf_entries, lds);
+}
+
+// Few tokens (T <= 64): the 16 waves rank the tokens' logits first (one
+// token per wave at a time, the arithmetic of k_topk), keep the experts in
+// LDS and group them there; one launch instead of two.
+template <int LT, int VPL>
+__global__ __launch_bounds__(1024) void k_route_group(
+    const void* __restrict__ logits, int T, int E, int topk, int renorm,
+    int32_t* __restrict__ sel, float* __restrict__ wts, int lo_max, int lo_chunk,
+    int32_t* __restrict__ perm, int4* __restrict__ entries, int* __restrict__ n_entries,
+    int4* __restrict__ mf_entries, int* __restrict__ n_mf_entries) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  int32_t* sel_l = (int32_t*)lds;  // [T][topk]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int t = wave; t < T; t += blockDim.x >> 6) {
+    u32 raw[VPL];
+    load_row<LT, VPL>(logits, t, E, raw);
+    int my_sel = 0;
+    float my_w = 0.f;
+    topk_row<LT, VPL>(raw, t, E, topk, renorm, sel, wts, nullptr, 0, &my_sel, &my_w);
+    if (lane < topk) sel_l[t * topk + lane] = my_sel;
+  }
+  __syncthreads();
+  group_body(sel_l, T, topk, E, lo_max, lo_chunk, perm, entries, n_entries, mf_entries,
+             n_mf_entries, lds + (((size_t)T * topk * 4 + 15) & ~(size_t)15));
 }
 
 
@@ -344,8 +380,6 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
     lg = ws.logits;
     if (mw->norm_w) x = ws.xn;
   }
-  rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
-  if (rc) return rc;
   const int Tk = T * topk;
   const int TW_ = (T + 31) / 32;
   const size_t glds = (size_t)2 * E * TW_ * 4 + (size_t)E * 4;
@@ -353,9 +387,24 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   // small entries of <= MF_SMALL tokens cover every expert in one launch per
   // projection; above, experts with > MF_SMALL tokens take large entries
   const bool one_list = T <= MF_TOK;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E,
-                     one_list ? T : MF_SMALL, MF_SMALL, ws.perm, ws.entries, ws.n_entries,
-                     ws.mf_entries, ws.n_mf_entries);
+  if (one_list) {  // top-k and grouping in one launch
+    const size_t lds = (((size_t)Tk * 4 + 15) & ~(size_t)15) + glds;
+#define I4_RG_CASE(LT_, VPL_)                                                                  \
+  if (xt == LT_ && E <= 64 * VPL_) {                                                           \
+    hipLaunchKernelGGL((k_route_group<LT_, VPL_>), dim3(1), dim3(1024), lds, s, lg, T, E, topk,  \
+                       renorm, sel, wts, T, MF_SMALL, ws.perm, ws.entries, ws.n_entries,       \
+                       ws.mf_entries, ws.n_mf_entries);                                        \
+  } else
+    I4_RG_CASE(I4_F16, 2) I4_RG_CASE(I4_F16, 8) I4_RG_CASE(I4_BF16, 2) I4_RG_CASE(I4_BF16, 8)
+    return I4_ERR_SHAPE;
+#undef I4_RG_CASE
+  } else {
+    rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E, MF_SMALL,
+                       MF_SMALL, ws.perm, ws.entries, ws.n_entries, ws.mf_entries,
+                       ws.n_mf_entries);
+  }
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
   // entry counts: sum over experts of ceil(n_e / 16) <= min(E, Tk) + Tk / 16
   const int max_s = (E < Tk ? E : Tk) + (one_list ? Tk / MF_SMALL : 0);

@@ -261,14 +261,21 @@ int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr,
                            (const uint16_t*)norm_w, eps, (uint16_t*)xn);
       xin = (const uint16_t*)xn;
     }
-    constexpr int TT = 8, EPW = 2;
-    const dim3 g2((E + 4 * EPW - 1) / (4 * EPW), (T + TT - 1) / TT);
-    const size_t lds = (size_t)TT * (H / 8) * 16;  // <= 64 KB for H <= 4096
-#define I4_RT_CASE(XT_)                                                                       \
-  if (xt == XT_)                                                                              \
-    hipLaunchKernelGGL((k_router_t<XT_, TT, EPW>), g2, dim3(256), lds, s, xin, T, H,           \
-                       (const uint16_t*)wr, E, (uint16_t*)logits);
-    I4_RT_CASE(I4_F16) else I4_RT_CASE(I4_BF16)
+    // tiles of TT tokens x 4 EPW experts: small batches take small tiles so that
+    // the launch still covers the CUs (T = 32: 256 workgroups), larger ones
+    // reuse each staged token and router row more
+#define I4_RT_CASE(XT_, TT_, EPW_)                                                            \
+  if (xt == XT_) {                                                                            \
+    const dim3 g2((E + 4 * EPW_ - 1) / (4 * EPW_), (T + TT_ - 1) / TT_);                      \
+    const size_t lds = (size_t)TT_ * (H / 8) * 16; /* <= 64 KB for H <= 4096 */               \
+    hipLaunchKernelGGL((k_router_t<XT_, TT_, EPW_>), g2, dim3(256), lds, s, xin, T, H,        \
+                       (const uint16_t*)wr, E, (uint16_t*)logits);                            \
+  }
+    if (T <= 64) {
+      I4_RT_CASE(I4_F16, 4, 1) else I4_RT_CASE(I4_BF16, 4, 1)
+    } else {
+      I4_RT_CASE(I4_F16, 8, 2) else I4_RT_CASE(I4_BF16, 8, 2)
+    }
 #undef I4_RT_CASE
   }
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
