@@ -331,6 +331,41 @@ def time_gemvs(pkg, torch, dev, replays=20):
         out[f"attention_{layout}"] = att
         log(f"attention q/k/v/o ({layout}): " + ", ".join(
             f"{k} {v['us']:.2f}" for k, v in att.items()) + " us")
+    # M > 1 (prefill): the same projections on their tile copies (MFMA over 64-row tiles,
+    # what PackedLinear runs from TILE_ROWS rows on) and, at M = 32, the per-row GEMV
+    pre = {}
+    pp = dict(projs, qkv=qkv)  # qkv: the q/k/v rows in one weight (PackedQKV)
+    for M in (32, 512):
+        xm = torch.randn(M, 4096, device=dev, generator=gen).half()
+        ym = torch.empty(M, qkv.N, dtype=torch.float16, device=dev)
+        res = {}
+        for layout in (("tile", "ct") if M == 32 else ("tile",)):
+            for name, p in pp.items():
+                if layout == "tile" and "tile" not in p.desc:
+                    t = p.keep[-1 if name == "qkv" else 1].to_tile()
+                    p.desc["tile"] = per_copy(t)
+                    p.keep = p.keep + (t,)
+                nb = max(lb.i4_linear_workspace_bytes(ctypes.byref(p.desc[layout][0]), M), 16)
+                wsm = torch.empty(nb, dtype=torch.uint8, device=dev)
+
+                def seq(p=p, layout=layout, wsm=wsm):
+                    for i in range(n2):
+                        rc = lb.i4_linear(xm.data_ptr(), _lib.F16, M,
+                                          ctypes.byref(p.desc[layout][i]), None, ym.data_ptr(),
+                                          _lib.F16, wsm.data_ptr(), wsm.numel(),
+                                          torch.cuda.current_stream().cuda_stream)
+                        if rc:
+                            raise RuntimeError(lb.i4_strerror(rc).decode())
+
+                ts = graph_times(torch, seq, max(3, replays // 4))
+                st = stats(ts, n2, awq_gemv_bytes(p.K, p.N) + (M - 1) * 2 * (p.K + p.N))
+                tf = 2.0 * M * p.N * p.K / (st["us"] * 1e-6) / 1e12
+                st.update({"TFLOPs": round(tf, 2), "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4)})
+                res[f"{name}_{layout}"] = st
+        pre[f"M{M}"] = res
+        log(f"attention q/k/v/o at M={M}: " + ", ".join(
+            f"{k} {v['us']:.2f} us ({v['TFLOPs']:.0f} TF/s)" for k, v in res.items()))
+    out["attention_prefill"] = pre
     out["timing"] = ("hipGraph of all copies back to back, HIP events per replay; per-GEMV "
                      "time = replay / copies; bytes = AWQ g128 weights + scales + zeros + x + y")
     return out

@@ -152,7 +152,12 @@ size_t i4_dq_gemv_workspace_bytes(const i4_qweight* w, int k_sel);
 /* TritonPackedLinear.forward (src/duplex/streaming/triton_dequant_gemv.py:151-159):
  *   y[m][n] = sum_k W[n][k] * x[m][k] (+ bias[n]),  m < M, expert 0 of w.
  * One launch for all M rows (the reference launches once per row).  bias is
- * nullable and in y_dtype. */
+ * nullable and in y_dtype.  A CT or AWQ weight runs the dequant-GEMV for
+ * every row; a weight in I4_LAYOUT_TILE (E = 1, N % 128 == 0) runs the MFMA
+ * tile kernel over 64-row tiles, each weight tile streamed once per 64 rows
+ * (the path for prefill and other M > 1 batches); when that grid is small it
+ * is split along K into fp32 partials in the workspace and summed in a fixed
+ * order.  i4_linear_workspace_bytes gives the workspace (0: none needed). */
 int    i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w,
                  const void* bias, void* y, int y_dtype,
                  void* workspace, size_t workspace_bytes, hipStream_t stream);

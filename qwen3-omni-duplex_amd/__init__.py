@@ -10,7 +10,7 @@ include/i4moe.h).  There is no fallback: without the built library every op
 raises.
 """
 from . import _lib
-from .linear import PackedLinear, PackedQKV, QKVSlice, concat_rows, patch_attention
+from .linear import TILE_ROWS, PackedLinear, PackedQKV, QKVSlice, concat_rows, patch_attention
 from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_forward, moe_gate_up,
                   moe_route_gate_up, moe_stack, route, router_logits, unpack4, unpack_nibbles,
@@ -25,5 +25,5 @@ __all__ = [
     "moe_down_combine",
     "moe_stack", "Workspace",
     "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "PackedQKV", "QKVSlice",
-    "concat_rows", "patch_attention", "lib",
+    "concat_rows", "patch_attention", "TILE_ROWS", "lib",
 ]

@@ -17,6 +17,7 @@
 // activation row is staged, so the staging latency hides under the stream.
 #include "i4_common.h"
 #include "i4_launch.h"
+#include "i4_moe_launch.h"
 
 namespace i4 {
 
@@ -575,6 +576,7 @@ int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w
 }
 
 size_t i4_linear_workspace_bytes(const i4_qweight* w, int M) {
+  if (w && w->layout == I4_LAYOUT_TILE && M >= 1) return linear_tile_workspace_bytes(M, w->N, w->K);
   return i4_dq_gemv_workspace_bytes(w, M);
 }
 
@@ -587,7 +589,19 @@ int i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w, const void
   if (!half_dt(x_dtype) || !any_dt(y_dtype)) return I4_ERR_DTYPE;
   if (M < 1 || M > 65535) return I4_ERR_SHAPE;
   if (!al16(x)) return I4_ERR_ALIGN;
-  if (nw.layout == I4_LAYOUT_TILE) return I4_ERR_LAYOUT;
+  if (nw.layout == I4_LAYOUT_TILE) {  // several rows: MFMA over 64-row tiles
+    if (nw.E != 1) return I4_ERR_SHAPE;
+    TW tw{nw.packed, nw.scale, nw.zeros, nw.packed_estride, nw.scale_estride,
+          nw.zeros_estride, i4_group_shift(nw.group), 1, nw.N, nw.K};
+#define I4_LIN_DT(XT_, ST_)                                                                 \
+  if (x_dtype == XT_ && nw.scale_dtype == ST_)                                              \
+    return launch_mfma_linear<XT_, ST_>(x, M, tw, bias, y, y_dtype, workspace, workspace_bytes, \
+                                        stream);
+    I4_LIN_DT(I4_F16, I4_F32) I4_LIN_DT(I4_F16, I4_F16) I4_LIN_DT(I4_F16, I4_BF16)
+    I4_LIN_DT(I4_BF16, I4_F32) I4_LIN_DT(I4_BF16, I4_F16) I4_LIN_DT(I4_BF16, I4_BF16)
+#undef I4_LIN_DT
+    return I4_ERR_DTYPE;
+  }
   nw.E = 1;
   if (nw.layout == I4_LAYOUT_CT)
     return i4_launch_gemv_ct(x, x_dtype, nw.K, &nw, nullptr, M, y, y_dtype, bias, stream);

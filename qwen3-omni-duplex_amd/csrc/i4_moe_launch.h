@@ -61,4 +61,12 @@ template <int XT, int ST>
 int launch_mfma_down(bool small, int max_entries, const void* act, int rows, const int4* ent,
                      const int* nent, const int32_t* perm, const TW& w, float* ys, hipStream_t s);
 
+// Dense linear layer on MFMA: y[M][N] = x[M][K] W^T (+ bias, dtype ot), W one
+// tile-layout weight (E = 1, N % 128 == 0).  Small grids are split along K
+// into fp32 partials in ws (linear_tile_workspace_bytes; 0 when not split).
+template <int XT, int ST>
+int launch_mfma_linear(const void* x, int M, const TW& w, const void* bias, void* y, int ot,
+                       void* ws, size_t ws_bytes, hipStream_t s);
+size_t linear_tile_workspace_bytes(int M, int N, int K);
+
 }  // namespace i4

@@ -211,11 +211,19 @@ __device__ inline void correct(f32x4& res, const f32x4& d, u32 sraw, u32 zw, int
 // One entry (<= 16 MB tokens of one expert) x one column tile.  MB m-blocks
 // of 16 tokens (1 for the small entries, 4 for the large ones), NB n-blocks
 // of 16 weight rows per wave.
-template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB>
+// LIN: a dense linear layer (E = 1) over M rows of src: entry blockIdx.y is
+// rows [16 MB y, 16 MB (y + 1)) in order (no entry list, no permutation), and
+// the epilogue writes y[row][n] + bias[n] in dtype ot to `ys`.  With ksplit >
+// 1, blockIdx.z takes the z-th of ksplit contiguous ranges of superchunks and
+// writes its fp32 partial sums to part[z][row][n] instead (k_linear_finish
+// adds them up).
+template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN = false>
 __global__ __launch_bounds__(256) void k_tile_mfma(
     const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ entries,
     const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
-    uint16_t* __restrict__ act, float* __restrict__ ys) {
+    uint16_t* __restrict__ act, float* __restrict__ ys, int M = 0,
+    const void* __restrict__ bias = nullptr, int ot = 0, int ksplit = 1,
+    float* __restrict__ part = nullptr) {
   constexpr bool EXACT = XT == I4_F16;
   // fp16 with several m-blocks folds the scale into B (see the top); one
   // m-block keeps the exact form, whose extra registers fit its occupancy
@@ -226,11 +234,16 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
   static_assert(MB == 1 || MB == 4, "staging maps 256 threads onto 16 or 64 tokens");
   __shared__ u32x4 xs[2][TOK * MF_TSTRIDE];
   __shared__ float xsum[2][TOK * 4];  // bf16: per token and chunk
-  if ((int)blockIdx.y >= *n_entries) return;
+  static_assert(!(LIN && GATEUP), "a linear layer is a plain projection");
+  if (!LIN && (int)blockIdx.y >= *n_entries) return;
   const u32 mg = magic_v<XT>();
-  const int4 en = entries[blockIdx.y];
+  const int4 en = LIN ? int4{0, (int)blockIdx.y * TOK, min(TOK, M - (int)blockIdx.y * TOK), 0}
+                      : entries[blockIdx.y];
   const int e = en.x, pos0 = en.y, cnt = en.z;
-  const int K = w.K, SC = K >> 7;
+  const int K = w.K, SC_ALL = K >> 7;
+  // superchunks [scb, scb + SC) of this workgroup (all of them unless split)
+  const int scb = LIN ? ((int)blockIdx.z * SC_ALL) / ksplit : 0;
+  const int SC = LIN ? (((int)blockIdx.z + 1) * SC_ALL) / ksplit - scb : SC_ALL;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, ln = lane & 15, kb = lane >> 4;
   const bool ev = (unsigned)e < (unsigned)w.E;
@@ -257,7 +270,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
   };
   u32x4 xd[WPT];
   auto load_x = [&](int sc, u32x4* dst) {
-    sc = min(sc, SC - 1);
+    sc = scb + min(sc, SC - 1);
 #pragma unroll
     for (int q = 0; q < WPT; ++q) dst[q] = bload16(xr, vx + 16u * q, sc * 256);
   };
@@ -278,7 +291,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     }
   };
   auto issue = [&](int sc, Slot& sl) {
-    wissue<ST, GB, NB>(wb, min(sc, SC - 1), sl.w);
+    wissue<ST, GB, NB>(wb, scb + min(sc, SC - 1), sl.w);
     if constexpr (MB == 1) load_x(sc, &sl.x);
   };
   f32x4 res[MB][NB];
@@ -412,7 +425,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     }
     __syncthreads();
     if constexpr (MB != 1) load_x(sc + 1, xd);  // unconditional (clamped), like every load
-    if (sc < SC) compute(sc, sl.w, buf);
+    if (sc < SC) compute(scb + sc, sl.w, buf);
     issue(sc + 3, sl);
   };
   // Prologue loads in ring order, first turn peeled: the activation loads wait
@@ -449,6 +462,30 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
             const float v =
                 ev ? silu(res[mb][nb][i]) * res[mb][nb + NB / 2][i] : __builtin_nanf("");
             act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
+          }
+        } else if constexpr (LIN) {
+          const int n0 = blockIdx.x * COLS + 16 * NB * wave + ln;
+          const int64_t o = (int64_t)(pos0 + m) * w.N + n0;
+          if (ksplit > 1) {
+            float* pz = part + (int64_t)blockIdx.z * M * w.N;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) pz[o + 16 * nb] = res[mb][nb][i];
+            continue;
+          }
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const int n = n0 + 16 * nb;
+            float v = res[mb][nb][i];
+            if (ot == I4_F32) {
+              if (bias) v += ((const float*)bias)[n];
+              store_out<I4_F32>(ys, o + 16 * nb, v);
+            } else if (ot == I4_F16) {
+              if (bias) v += Half<I4_F16>::to_f32(((const uint16_t*)bias)[n]);
+              store_out<I4_F16>(ys, o + 16 * nb, v);
+            } else {
+              if (bias) v += Half<I4_BF16>::to_f32(((const uint16_t*)bias)[n]);
+              store_out<I4_BF16>(ys, o + 16 * nb, v);
+            }
           }
         } else {
           const int64_t o = (int64_t)perm[pos0 + m] * w.N + blockIdx.x * COLS + 16 * NB * wave + ln;
@@ -505,7 +542,79 @@ int launch_mfma_down(bool small, int max_entries, const void* act, int rows, con
                                       nullptr, ys, s);
 }
 
+// y[r][n] = sum_z part[z][r][n] + bias[n] in dtype ot, the K ranges in order
+__global__ __launch_bounds__(256) void k_linear_finish(const float* __restrict__ part, int ksplit,
+                                                       int64_t total, int N,
+                                                       const void* __restrict__ bias,
+                                                       void* __restrict__ y, int ot) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float v = 0.f;
+  for (int z = 0; z < ksplit; ++z) v += part[z * total + i];
+  const int n = (int)(i % N);
+  if (ot == I4_F32) {
+    if (bias) v += ((const float*)bias)[n];
+    store_out<I4_F32>(y, i, v);
+  } else if (ot == I4_F16) {
+    if (bias) v += Half<I4_F16>::to_f32(((const uint16_t*)bias)[n]);
+    store_out<I4_F16>(y, i, v);
+  } else {
+    if (bias) v += Half<I4_BF16>::to_f32(((const uint16_t*)bias)[n]);
+    store_out<I4_BF16>(y, i, v);
+  }
+}
+
+// K ranges of a dense linear launch: a grid of fewer than 256 output tiles
+// (few rows or few columns) is split along K until it has about 512
+// workgroups, each range keeping at least 4 superchunks
+int linear_ksplit(int M, int N, int K) {
+  const int tiles = (N / (64 * MF_NB)) * ((M + MF_TOK - 1) / MF_TOK);
+  const int sc = K / 128;
+  if (tiles >= 256 || sc < 8) return 1;
+  int ks = (512 + tiles - 1) / tiles;
+  if (ks > sc / 4) ks = sc / 4;
+  return ks < 1 ? 1 : ks;
+}
+
+size_t linear_tile_workspace_bytes(int M, int N, int K) {
+  const int ks = linear_ksplit(M, N, K);
+  return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
+}
+
+// dense linear layer y = x W^T (+ bias), W one tile-layout weight (E = 1),
+// x [M][K]: entries of 16 MB rows in order, split along K when the grid is small
+template <int XT, int ST>
+int launch_mfma_linear(const void* x, int M, const TW& w, const void* bias, void* y, int ot,
+                       void* ws, size_t ws_bytes, hipStream_t s) {
+  const int64_t src_bytes = (int64_t)M * w.K * 2;
+  if (src_bytes >= ((int64_t)1 << 31) || (int64_t)w.N * w.K / 2 >= ((int64_t)1 << 31))
+    return I4_ERR_SHAPE;
+  constexpr int COLS = 64 * MF_NB, TOK = MF_TOK;
+  if (w.N % COLS != 0 || w.K % 128 != 0 || w.E != 1) return I4_ERR_SHAPE;
+  const int ks = linear_ksplit(M, w.N, w.K);
+  if (ks > 1 && (!ws || ws_bytes < linear_tile_workspace_bytes(M, w.N, w.K)))
+    return I4_ERR_WORKSPACE;
+  const dim3 grid(w.N / COLS, (M + TOK - 1) / TOK, ks);
+#define I4_LIN(GB_)                                                                            \
+  hipLaunchKernelGGL((k_tile_mfma<XT, ST, GB_, false, MF_NB, TOK / 16, true>), grid, dim3(256), \
+                     0, s, (const uint16_t*)x, (u32)src_bytes, 0, nullptr, nullptr, nullptr, w, \
+                     0, nullptr, (float*)y, M, bias, ot, ks, (float*)ws)
+  if (w.gshift >= 2) I4_LIN(true);
+  else I4_LIN(false);
+#undef I4_LIN
+  if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
+  if (ks > 1) {
+    const int64_t total = (int64_t)M * w.N;
+    hipLaunchKernelGGL(k_linear_finish, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       (const float*)ws, ks, total, w.N, bias, y, ot);
+    if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
+  }
+  return I4_OK;
+}
+
 #define I4_INST(XT_, ST_)                                                                      \
+  template int launch_mfma_linear<XT_, ST_>(const void*, int, const TW&, const void*, void*,   \
+                                            int, void*, size_t, hipStream_t);                  \
   template int launch_mfma_gate_up<XT_, ST_>(bool, int, const void*, int, int, const int4*,    \
                                              const int*, const int32_t*, const TW&, int, void*, \
                                              hipStream_t);                                     \

@@ -251,6 +251,37 @@ def test_linear(pkg, dev, M, layout):
         assert i4ref.rel_err(got2, ref) <= TOL
 
 
+@pytest.mark.parametrize("M,N", [(16, 512), (64, 512), (100, 512), (512, 512), (512, 4096)])
+@pytest.mark.parametrize("fmt", ["awq-g128-f16", "ct-g32-bf16"])
+def test_linear_tile_rows(pkg, dev, M, N, fmt):
+    """Batches of >= TILE_ROWS rows run on MFMA from the tile copy (64-row tiles, ragged last
+    tile; split along K into fp32 partials unless the grid has 256 tiles, as at 512 x 4096):
+    the same product as the per-row dequant-GEMV, against the oracle's fp32 matmul."""
+    rng = np.random.default_rng(60 + M + N)
+    K = 2048
+    if fmt == "awq-g128-f16":
+        G, xdt = 128, "f16"
+        qw, qz, sc = _gen.awq_weight(rng, 1, K, N, G)
+        w = pkg.QWeight(t_(qw, dev), t_(sc, dev), t_(qz, dev), "awq", G, N, K)
+        W = i4ref.awq_dequant(qw, qz, sc, G)[0]
+        bias = rng.standard_normal(N).astype(np.float16)
+    else:  # the reference checkpoint's format: CT g32 symmetric, bf16 scales and activations
+        G, xdt = 32, "bf16"
+        p, sc, _ = _gen.ct_weight(rng, 1, N, K, G, sdt="bf16")
+        w = pkg.QWeight(t_(p, dev), t_(sc, dev), None, "ct", G, N, K)
+        W = i4ref.ct_dequant(p, f_(sc), K, G)[0]
+        bias = i4ref.f32_to_bf16_bits(rng.standard_normal(N).astype(np.float32))
+    lin = pkg.PackedLinear.from_qweight(w, t_(bias, dev))
+    assert lin.w_tile is not None and lin.w_tile.layout == "tile"
+    x = make_x(rng, (M, K), xdt)
+    got = host(pkg.ops.linear(t_(x, dev), lin.w_tile, lin.bias))  # the MFMA path at any M
+    ref = f_(x) @ W.T + f_(bias)
+    assert np.all(np.isfinite(got))
+    assert i4ref.rel_err(got, ref) <= TOL
+    rows = host(pkg.ops.linear(t_(x, dev), lin.w, lin.bias))  # the per-row GEMV
+    assert i4ref.rel_err(got, rows) <= TOL
+
+
 def test_packed_qkv_matches_three_linears(pkg, dev):
     """q, k, v in one launch equal the three separate launches bit for bit (each row's dot
     product does not depend on its neighbours): AWQ parts, and CT parts with and without
@@ -275,6 +306,13 @@ def test_packed_qkv_matches_three_linears(pkg, dev):
         for y, w, b in zip(got, parts, biases):
             want = pkg.PackedLinear.from_qweight(w, b)(x)
             assert torch.equal(y, want)
+        # the tile path (40 rows): the parts keep their 128-row tiles, but how far K is
+        # split depends on the launch's whole grid, so the sums may round differently
+        xl = t_(make_x(rng, (40, K), "f16"), dev)
+        got = fused(xl)
+        for y, w, b in zip(got, parts, biases):
+            want = pkg.PackedLinear.from_qweight(w, b)(xl)
+            assert i4ref.rel_err(host(y), host(want)) <= 1e-3
 
 
 class _FakePacked(torch.nn.Module):
