@@ -638,6 +638,69 @@ def test_stack_matches_layer_loop_and_oracle(pkg, dev):
     assert torch.equal(stack, h)
 
 
+def _stack_modules(pkg, dev, rng, xdt, norm, n_distinct=3):
+    """n_distinct small blocks (32 experts, H 2048, I 768) in the activation dtype xdt."""
+    sdt = "bf16" if xdt == "bf16" else np.float16
+    mods = []
+    for _ in range(n_distinct):
+        m, _, _, _ = _awq_moe(pkg, dev, rng, E=32, sdt=sdt)
+        tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+        m.register_buffer("router_w", m.router_w.to(tdt), persistent=False)
+        if norm:
+            nw = torch.from_numpy(rng.uniform(0.5, 1.5, 2048).astype(np.float32)).to(dev, tdt)
+            m.register_buffer("norm_weight", nw, persistent=False)
+            m.norm_eps = 1e-6
+        mods.append(m)
+    return mods
+
+
+@pytest.mark.parametrize("xdt,norm,n_layers", [("f16", True, 26), ("bf16", True, 5),
+                                               ("f16", False, 3), ("bf16", False, 1)])
+def test_stack_matches_layer_loop_variants(pkg, dev, xdt, norm, n_layers):
+    """The one-call decode stack equals the module-by-module loop bit for bit: an even and an
+    odd number of layers (the call alternates its outputs between the workspace and out), bf16,
+    and without the RMSNorm."""
+    rng = np.random.default_rng(61 + n_layers)
+    mods = _stack_modules(pkg, dev, rng, xdt, norm)
+    layers = [mods[i % len(mods)] for i in range(n_layers)]
+    x = make_x(rng, (1, 2048), "f16") * (1.0 if norm else 0.1)  # un-normalised layers grow
+    xt = t_(i4ref.f32_to_bf16_bits(x.astype(np.float32)) if xdt == "bf16" else x, dev)
+    stack = pkg.moe_stack(xt, [m.stack_entry() for m in layers], 8)
+    h = xt
+    for m in layers:
+        h = m(h, residual=h)
+    assert torch.isfinite(stack).all()
+    assert torch.equal(stack, h)
+    again = pkg.moe_stack(xt, [m.stack_entry() for m in layers], 8)
+    assert torch.equal(again, stack)
+
+
+def test_stack_graph_replays_match_eager(pkg, dev):
+    """The decode stack (two launches per layer) captured in a hipGraph gives the eager result
+    on every replay, with other work and new inputs between replays."""
+    rng = np.random.default_rng(71)
+    mods = _stack_modules(pkg, dev, rng, "f16", True)
+    entries = [m.stack_entry() for m in mods * 2]
+    ws = pkg.Workspace()
+    xs = [t_(make_x(rng, (1, 2048), "f16"), dev) for _ in range(3)]
+    eager = [pkg.moe_stack(x, entries, 8, workspace=ws).clone() for x in xs]
+    static_x = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        pkg.moe_stack(static_x, entries, 8, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = pkg.moe_stack(static_x, entries, 8, workspace=ws)
+    for r in range(6):
+        static_x.copy_(xs[r % 3])
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[r % 3])
+        _ = (torch.randn(256, 256, device=dev) @ torch.randn(256, 256, device=dev)).sum().item()
+
+
 @pytest.mark.parametrize("T", [1, 9])
 def test_router_logits_with_norm(pkg, dev, T):
     rng = np.random.default_rng(29 + T)
