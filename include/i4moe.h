@@ -257,6 +257,35 @@ int    i4_moe_stack_forward(const void* x, int x_dtype, int T,
                             size_t workspace_bytes, hipStream_t stream);
 size_t i4_moe_stack_workspace_bytes(int T, int H, int I, int E, int topk);
 
+/* Qwen3OmniMoeThinkerTextRMSNorm.forward (transformers modeling_qwen3_omni_moe.py:
+ * 1388-1393, 5.15; the Thinker decoder layer's input_layernorm, which the clock
+ * path runs in front of every attention block, clock.py:164-172):
+ *   out[t] = w * (x[t] * rsqrt(mean(x[t]^2) + eps)), the normalised row rounded to
+ *   x_dtype before the weight multiply, as the reference casts.  H % 8 == 0, H <= 4096. */
+int    i4_rmsnorm(const void* x, int x_dtype, int T, int H, const void* norm_w, float eps,
+                  void* out, hipStream_t stream);
+
+/* The attention core of one decode token of a Thinker layer,
+ * Qwen3OmniMoeThinkerTextAttention.forward (modeling_qwen3_omni_moe.py:1473-1514)
+ * between its q/k/v and o projections, with the DynamicCache of clock.py:164-172:
+ *   qkv      [n_heads + 2 n_kv_heads][head_dim], the fused q|k|v projection output;
+ *   q/k      RMSNorm over head_dim with q_norm_w / k_norm_w, then the rotary
+ *            embedding at position pos with inv_freq[head_dim / 2] (host array;
+ *            text positions make the interleaved mRoPE the 1-D one);
+ *   cache    k_cache / v_cache [n_kv_heads][max_len][head_dim]; row pos receives this
+ *            token's k and v, rows [0, pos] are attended (GQA: query head h reads kv
+ *            head h / (n_heads / n_kv_heads));
+ *   out      [n_heads][head_dim] = softmax(q k^T / sqrt(head_dim)) v, fp32 inside,
+ *            rounded once to x_dtype.
+ * head_dim == 128, n_heads / n_kv_heads <= 8, 0 <= pos < max_len.  The workspace
+ * (i4_attn_decode_workspace_bytes) needs no initial contents. */
+int    i4_attn_decode(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
+                      const void* q_norm_w, const void* k_norm_w, float eps,
+                      const float* inv_freq, int pos, void* k_cache, void* v_cache,
+                      int max_len, void* out, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+size_t i4_attn_decode_workspace_bytes(int n_heads, int head_dim, int max_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,18 +7,21 @@ Drop-in replacements for thecodacus/qwen3-omni-duplex's quantized compute:
   fuse_packed_moe_blocks <- fused_packed_moe.py:278
   loader                 <- src/duplex/streaming/clock.py:45 (load_thinker_prefix),
                             src/duplex/loader.py:31 (packed triplets from safetensors)
+  ThinkerDecoder         <- the Thinker[0:24] decode step the clock path runs
+                            (clock.py:164-172): attention with KV cache + MoE per layer
 all executed by the hand-written HIP kernels of libi4moe.so (C ABI in
 include/i4moe.h).  There is no fallback: without the built library every op
 raises.
 """
 from . import _lib
 from .linear import TILE_ROWS, PackedLinear, PackedQKV, QKVSlice, concat_rows, patch_attention
-from .loader import (Checkpoint, load_attention, load_moe_layer, load_thinker_moe_stack,
-                     read_moe_layer)
+from .attention import ThinkerAttention, ThinkerDecoder, ThinkerDecoderLayer, rope_inv_freq
+from .loader import (Checkpoint, load_attention, load_moe_layer, load_thinker_decoder,
+                     load_thinker_layer, load_thinker_moe_stack, read_moe_layer)
 from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_forward, moe_gate_up,
                   moe_route_gate_up, moe_stack, route, router_logits, unpack4, unpack_nibbles,
-                  Workspace)
+                  Workspace, rmsnorm, attn_decode)
 from .weights import QWeight, repack_awq_to_ct, repack_tile
 
 lib = _lib.lib
@@ -31,4 +34,6 @@ __all__ = [
     "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "PackedQKV", "QKVSlice",
     "concat_rows", "patch_attention", "TILE_ROWS", "lib",
     "Checkpoint", "read_moe_layer", "load_moe_layer", "load_thinker_moe_stack", "load_attention",
+    "load_thinker_layer", "load_thinker_decoder", "rmsnorm", "attn_decode",
+    "ThinkerAttention", "ThinkerDecoderLayer", "ThinkerDecoder", "rope_inv_freq",
 ]

@@ -1,0 +1,100 @@
+"""Thinker decode step around the int4 path: attention block, decoder layer, stack.
+
+The clock path runs Thinker[0:24] one token per frame (src/duplex/streaming/
+clock.py:164-172: `th(inputs_embeds=emb, past_key_values=th_kv, use_cache=True)`),
+i.e. transformers' Qwen3OmniMoeThinkerTextDecoderLayer.forward
+(modeling_qwen3_omni_moe.py:1539-1565 in transformers 5.15) per layer:
+
+    h = h + o_proj(attention(input_layernorm(h)))            ThinkerAttention
+    h = h + moe(post_attention_layernorm(h))                  FusedPackedMoE (norm fused)
+
+with the projections on the library's int4 GEMVs (q|k|v as one launch, o with the
+residual added in the same launch), and q/k norm, rotary embedding, KV-cache append
+and GQA attention in i4_attn_decode.  The KV cache is preallocated
+([n_kv_heads, max_len, head_dim] per layer, the activation dtype) instead of
+transformers' growing DynamicCache.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .linear import PackedLinear, PackedQKV
+from .moe import FusedPackedMoE
+
+
+def rope_inv_freq(head_dim: int, theta: float) -> torch.Tensor:
+    """inv_freq of the default rotary embedding, computed as transformers does
+    (compute_default_rope_parameters: 1 / theta ** (arange(0, d, 2) / d) in fp32)."""
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+
+
+class ThinkerAttention(nn.Module):
+    """One decode token of the attention half of a Thinker layer, residual included."""
+
+    def __init__(self, qkv: PackedQKV, o_proj: PackedLinear, q_norm_w: torch.Tensor,
+                 k_norm_w: torch.Tensor, input_norm_w: torch.Tensor, n_heads: int,
+                 n_kv_heads: int, head_dim: int = 128, eps: float = 1e-6,
+                 rope_theta: float = 1_000_000.0, max_len: int = 4096):
+        super().__init__()
+        self.qkv, self.o_proj = qkv, o_proj
+        self.n_heads, self.n_kv_heads, self.head_dim = int(n_heads), int(n_kv_heads), int(head_dim)
+        self.eps = float(eps)
+        if qkv.sizes != (n_heads * head_dim, n_kv_heads * head_dim, n_kv_heads * head_dim):
+            raise ValueError(f"q|k|v rows {qkv.sizes} do not match {n_heads}/{n_kv_heads} heads")
+        dt = input_norm_w.dtype
+        self.register_buffer("q_norm_w", q_norm_w.to(dt).contiguous(), persistent=False)
+        self.register_buffer("k_norm_w", k_norm_w.to(dt).contiguous(), persistent=False)
+        self.register_buffer("input_norm_w", input_norm_w.contiguous(), persistent=False)
+        self.inv_freq = rope_inv_freq(head_dim, rope_theta)  # host table
+        shape = (n_kv_heads, max_len, head_dim)
+        dev = input_norm_w.device
+        self.register_buffer("k_cache", torch.zeros(shape, dtype=dt, device=dev), persistent=False)
+        self.register_buffer("v_cache", torch.zeros(shape, dtype=dt, device=dev), persistent=False)
+        self.max_len = int(max_len)
+        self.workspace = ops.Workspace()
+
+    def forward(self, h: torch.Tensor, pos: int) -> torch.Tensor:
+        """h [1, H] (one token at cache position pos) -> h + o_proj(attn(norm(h)))."""
+        if h.numel() != h.shape[-1]:
+            raise ValueError("ThinkerAttention decodes one token")
+        if not 0 <= pos < self.max_len:
+            raise ValueError(f"position {pos} outside the cache (max_len {self.max_len})")
+        xn = ops.rmsnorm(h, self.input_norm_w, self.eps)
+        qkv = self.qkv.lin(xn)
+        a = ops.attn_decode(qkv, self.n_heads, self.n_kv_heads, self.q_norm_w, self.k_norm_w,
+                            self.eps, self.inv_freq, pos, self.k_cache, self.v_cache,
+                            self.workspace)
+        # one token: the residual enters the o_proj launch as its bias
+        return ops.linear(a.view(1, -1), self.o_proj.w, bias=h.reshape(-1)).view(h.shape)
+
+
+class ThinkerDecoderLayer(nn.Module):
+    """Qwen3OmniMoeThinkerTextDecoderLayer.forward for one decode token."""
+
+    def __init__(self, attn: ThinkerAttention, moe: FusedPackedMoE):
+        super().__init__()
+        if moe.norm_weight is None:
+            raise ValueError("the MoE block must carry its post_attention_layernorm")
+        self.attn, self.moe = attn, moe
+
+    def forward(self, h: torch.Tensor, pos: int) -> torch.Tensor:
+        h = self.attn(h, pos)
+        return self.moe(h, residual=h)
+
+
+class ThinkerDecoder(nn.Module):
+    """Thinker[0:n] decode: step(h, pos) runs every layer on one token and returns the
+    hidden state after the last layer (the clock path's layer-24 tap, clock.py:168)."""
+
+    def __init__(self, layers: list[ThinkerDecoderLayer]):
+        super().__init__()
+        self.layers = nn.ModuleList(layers)
+
+    def step(self, h: torch.Tensor, pos: int) -> torch.Tensor:
+        for layer in self.layers:
+            h = layer(h, pos)
+        return h
+
+    forward = step

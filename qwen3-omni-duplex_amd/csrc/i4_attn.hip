@@ -1,0 +1,282 @@
+// Decode attention of the Thinker's text layers (one token), the caller of the
+// int4 path: transformers Qwen3OmniMoeThinkerTextAttention.forward
+// (modeling_qwen3_omni_moe.py:1473-1514 in transformers 5.15) with the
+// DynamicCache of src/duplex/streaming/clock.py:164-172.  The q/k/v and o
+// projections are the library's int4 GEMVs; this file holds what lies between
+// them:
+//   k_qk_norm_rope  one wave per head of the fused q|k|v output: RMSNorm over
+//                   head_dim (q_norm / k_norm), the rotary embedding at `pos`
+//                   (cos / sin rounded to the activation dtype and every product
+//                   rounded, as transformers computes in bf16), q to q_out, k and
+//                   v appended to the cache at row `pos`;
+//   k_attn_chunk    one workgroup per (kv head, 64 cached positions): scores of
+//                   the kv head's query heads (GQA: each K and V row is loaded
+//                   once for all of them), the chunk's softmax statistics and the
+//                   probability-weighted sum of V, all in fp32;
+//   k_attn_combine  merges the chunks of each query head (flash-decoding) and
+//                   rounds the output once to the activation dtype.
+// Text positions are equal along mRoPE's three axes, where the interleaved
+// multimodal rotary embedding (apply_interleaved_mrope) reduces to the 1-D one
+// with inv_freq[i] = theta^(-2i / head_dim).
+#include "i4_common.h"
+#include "i4_launch.h"
+
+namespace i4 {
+
+static constexpr int HD = 128;    // head_dim
+static constexpr int ACH = 64;    // cached positions per attention workgroup
+static constexpr int GQMAX = 8;   // query heads per kv head
+
+struct RopeTab {
+  float inv_freq[HD / 2];
+};
+
+template <int XT> __device__ inline float rnd(float v) {
+  return Half<XT>::to_f32(Half<XT>::from_f32(v));
+}
+
+__device__ inline float xor32(float v) {
+  const int src = ((int)__lane_id() ^ 32) << 2;
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, v)));
+}
+
+template <int L> __device__ inline float group_max(float v) {
+  if constexpr (L >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));
+  if constexpr (L >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));
+  if constexpr (L >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+  if constexpr (L >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+  if constexpr (L >= 32)
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v),
+                                                                        0x401F)));  // xor 16
+  return v;
+}
+
+// Blocks [0, nq): query heads, [nq, nq + nkv): key heads, then value heads, in
+// the row order of the fused projection output.  Lane l holds dims 2l, 2l + 1;
+// rotate_half pairs dim d with d +- 64, i.e. lane l with lane l ^ 32.
+template <int XT>
+__global__ __launch_bounds__(64) void k_qk_norm_rope(
+    const uint16_t* __restrict__ qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, float eps, int pos, RopeTab rt,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    int64_t head_stride) {
+  const int h = blockIdx.x, lane = threadIdx.x;
+  const bool isq = h < nq, isk = !isq && h < nq + nkv;
+  const u32 raw = *(const u32*)(qkv + (int64_t)h * HD + 2 * lane);
+  uint16_t* dst = isq ? q_out + (int64_t)h * HD
+                      : (isk ? k_cache + (int64_t)(h - nq) * head_stride
+                             : v_cache + (int64_t)(h - nq - nkv) * head_stride) +
+                            (int64_t)pos * HD;
+  if (!isq && !isk) {  // values enter the cache as they are
+    *(u32*)(dst + 2 * lane) = raw;
+    return;
+  }
+  const float x0 = Half<XT>::to_f32((uint16_t)raw), x1 = Half<XT>::to_f32((uint16_t)(raw >> 16));
+  const float ss = group_sum<64>(x0 * x0 + x1 * x1);
+  const float r = 1.0f / sqrtf(ss / (float)HD + eps);
+  const u32 n = norm_pair<XT>(raw, *(const u32*)((isq ? qn_w : kn_w) + 2 * lane), r);
+  const float a0 = Half<XT>::to_f32((uint16_t)n), a1 = Half<XT>::to_f32((uint16_t)(n >> 16));
+  const float b0 = xor32(a0), b1 = xor32(a1);  // dims 2l +- 64, 2l + 1 +- 64
+  const int i0 = (2 * lane) & (HD / 2 - 1);
+  const float g0 = (float)pos * rt.inv_freq[i0], g1 = (float)pos * rt.inv_freq[i0 + 1];
+  const float c0 = rnd<XT>(cosf(g0)), s0 = rnd<XT>(sinf(g0));
+  const float c1 = rnd<XT>(cosf(g1)), s1 = rnd<XT>(sinf(g1));
+  // rotate_half(x)[d] = -x[d + 64] (d < 64), x[d - 64] (d >= 64)
+  const float sg = lane < 32 ? -1.f : 1.f;
+  const float o0 = rnd<XT>(rnd<XT>(a0 * c0) + rnd<XT>(sg * b0 * s0));
+  const float o1 = rnd<XT>(rnd<XT>(a1 * c1) + rnd<XT>(sg * b1 * s1));
+  *(u32*)(dst + 2 * lane) =
+      (u32)Half<XT>::from_f32(o0) | ((u32)Half<XT>::from_f32(o1) << 16);
+}
+
+// Workgroup (chunk c, kv head g): positions [64c, 64c + 64) of [0, S).
+// part[(c * nq + head) * (2 + HD)] = {chunk max m, sum l, acc[HD]} with
+// acc = sum_j exp(s_j - m) v_j and s_j = scale * q . k_j.
+template <int XT, int GQ>
+__global__ __launch_bounds__(256) void k_attn_chunk(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
+    const uint16_t* __restrict__ v_cache, int64_t head_stride, int S, float scale, int nq,
+    float* __restrict__ part) {
+  __shared__ float s_q[GQ][HD];
+  __shared__ float s_p[GQ][ACH];
+  __shared__ float s_red[4][GQ][HD];
+  __shared__ float s_stat[GQ][2];
+  const int c = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
+  const int c0 = c * ACH;
+  const int64_t kv0 = (int64_t)g * head_stride;
+  // K rows of the chunk first: thread t reads dims [32 (t & 3), +32) of key t >> 2
+  const int j = t >> 2, qp = t & 3;
+  const bool kvalid = c0 + j < S;
+  const uint16_t* krow = k_cache + kv0 + (int64_t)min(c0 + j, S - 1) * HD + 32 * qp;
+  u32x4 kw[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) kw[u] = ldg16(krow + 8 * u);
+  for (int i = t; i < GQ * HD; i += 256)
+    s_q[i / HD][i % HD] = Half<XT>::to_f32(q[(int64_t)g * GQ * HD + i]);
+  __syncthreads();
+  float sc[GQ];
+#pragma unroll
+  for (int h = 0; h < GQ; ++h) sc[h] = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const u32 w[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = 32 * qp + 8 * u + 2 * e;
+      const float k0 = Half<XT>::to_f32((uint16_t)w[e]);
+      const float k1 = Half<XT>::to_f32((uint16_t)(w[e] >> 16));
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) sc[h] += k0 * s_q[h][d] + k1 * s_q[h][d + 1];
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < GQ; ++h) {
+    const float v = group_sum<4>(sc[h]);
+    if (qp == 0) s_p[h][j] = kvalid ? v * scale : -__builtin_inff();
+  }
+  __syncthreads();
+  // chunk softmax: 32 threads per query head, two positions each
+  {
+    const int hh = t >> 5, jj = t & 31;
+    if (hh < GQ) {
+      const float v0 = s_p[hh][jj], v1 = s_p[hh][jj + 32];
+      const float m = group_max<32>(fmaxf(v0, v1));  // position c0 < S is always valid
+      const float p0 = expf(v0 - m), p1 = expf(v1 - m);
+      s_p[hh][jj] = p0;
+      s_p[hh][jj + 32] = p1;
+      const float l = group_sum<32>(p0 + p1);
+      if (jj == 0) {
+        s_stat[hh][0] = m;
+        s_stat[hh][1] = l;
+      }
+    }
+  }
+  __syncthreads();
+  // P V: thread t sums dims 2 (t & 63), 2 (t & 63) + 1 over positions [16 (t >> 6), +16)
+  const int d2 = t & 63, ks = t >> 6;
+  u32 vv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    vv[i] = *(const u32*)(v_cache + kv0 + (int64_t)min(c0 + 16 * ks + i, S - 1) * HD + 2 * d2);
+  float acc[GQ][2];
+#pragma unroll
+  for (int h = 0; h < GQ; ++h) acc[h][0] = acc[h][1] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float v0 = Half<XT>::to_f32((uint16_t)vv[i]);
+    const float v1 = Half<XT>::to_f32((uint16_t)(vv[i] >> 16));
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+      const float p = s_p[h][16 * ks + i];  // 0 past S
+      acc[h][0] += p * v0;
+      acc[h][1] += p * v1;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < GQ; ++h) {
+    s_red[ks][h][2 * d2] = acc[h][0];
+    s_red[ks][h][2 * d2 + 1] = acc[h][1];
+  }
+  __syncthreads();
+  for (int i = t; i < GQ * HD; i += 256) {
+    const int h = i / HD, d = i % HD;
+    const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
+    float* dst = part + ((int64_t)c * nq + g * GQ + h) * (2 + HD);
+    dst[2 + d] = o;
+    if (d == 0) {
+      dst[0] = s_stat[h][0];
+      dst[1] = s_stat[h][1];
+    }
+  }
+}
+
+// One workgroup of HD threads per query head: out = sum_c w_c acc_c / sum_c w_c l_c
+// with w_c = exp(m_c - max_c m_c), in chunk order.
+template <int XT>
+__global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ part, int nq,
+                                                     int nch, uint16_t* __restrict__ out) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  float M = -__builtin_inff();
+  for (int c = 0; c < nch; ++c) M = fmaxf(M, part[((int64_t)c * nq + h) * (2 + HD)]);
+  float L = 0.f, O = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    const float* p = part + ((int64_t)c * nq + h) * (2 + HD);
+    const float w = expf(p[0] - M);
+    L += p[1] * w;
+    O += p[2 + d] * w;
+  }
+  out[(int64_t)h * HD + d] = Half<XT>::from_f32(O / L);
+}
+
+namespace {
+
+size_t attn_ws(int nq, int max_len) {
+  const size_t q = ((size_t)nq * HD * 2 + 255) & ~(size_t)255;
+  const size_t nch = ((size_t)max_len + ACH - 1) / ACH;
+  return q + nch * nq * (2 + HD) * sizeof(float);
+}
+
+template <int XT>
+int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* kn_w, float eps,
+                const RopeTab& rt, int pos, void* k_cache, void* v_cache, int max_len, void* out,
+                void* ws, hipStream_t s) {
+  const int64_t hs = (int64_t)max_len * HD;
+  uint16_t* qo = (uint16_t*)ws;
+  float* part = (float*)((char*)ws + (((size_t)nq * HD * 2 + 255) & ~(size_t)255));
+  hipLaunchKernelGGL(k_qk_norm_rope<XT>, dim3(nq + 2 * nkv), dim3(64), 0, s,
+                     (const uint16_t*)qkv, nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w,
+                     eps, pos, rt, qo, (uint16_t*)k_cache, (uint16_t*)v_cache, hs);
+  const int S = pos + 1;
+  const int nch = (S + ACH - 1) / ACH;
+  const int gq = nq / nkv;
+  const float scale = 1.0f / sqrtf((float)HD);
+  const dim3 grid(nch, nkv);
+#define I4_AC_CASE(G_)                                                                        \
+  if (gq == G_)                                                                               \
+    hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, qo,                    \
+                       (const uint16_t*)k_cache, (const uint16_t*)v_cache, hs, S, scale, nq,  \
+                       part);                                                                 \
+  else
+  I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) I4_AC_CASE(8) return I4_ERR_SHAPE;
+#undef I4_AC_CASE
+  hipLaunchKernelGGL(k_attn_combine<XT>, dim3(nq), dim3(HD), 0, s, part, nq, nch,
+                     (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+}  // namespace
+}  // namespace i4
+
+extern "C" {
+
+size_t i4_attn_decode_workspace_bytes(int n_heads, int head_dim, int max_len) {
+  if (n_heads < 1 || head_dim != i4::HD || max_len < 1) return 0;
+  return i4::attn_ws(n_heads, max_len);
+}
+
+int i4_attn_decode(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
+                   const void* q_norm_w, const void* k_norm_w, float eps, const float* inv_freq,
+                   int pos, void* k_cache, void* v_cache, int max_len, void* out,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !inv_freq || !k_cache || !v_cache || !out)
+    return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  if (head_dim != i4::HD || n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads ||
+      n_heads / n_kv_heads > i4::GQMAX || n_heads > 1024 || max_len < 1 || pos < 0 ||
+      pos >= max_len)
+    return I4_ERR_SHAPE;
+  if (((uintptr_t)qkv & 3) || ((uintptr_t)q_norm_w & 3) || ((uintptr_t)k_norm_w & 3) ||
+      ((uintptr_t)k_cache & 15) || ((uintptr_t)v_cache & 15) || ((uintptr_t)out & 3))
+    return I4_ERR_ALIGN;
+  if (!workspace || workspace_bytes < i4::attn_ws(n_heads, max_len)) return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  i4::RopeTab rt;
+  for (int i = 0; i < i4::HD / 2; ++i) rt.inv_freq[i] = inv_freq[i];
+  return x_dtype == I4_F16
+             ? i4::attn_launch<I4_F16>(qkv, n_heads, n_kv_heads, q_norm_w, k_norm_w, eps, rt, pos,
+                                       k_cache, v_cache, max_len, out, workspace, stream)
+             : i4::attn_launch<I4_BF16>(qkv, n_heads, n_kv_heads, q_norm_w, k_norm_w, eps, rt,
+                                        pos, k_cache, v_cache, max_len, out, workspace, stream);
+}
+
+}  // extern "C"

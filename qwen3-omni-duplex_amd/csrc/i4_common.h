@@ -333,6 +333,29 @@ template <int XT> struct Stager {
   }
 };
 
+// RMSNorm of 8 values (one 16-byte load): round(round(x * r) * w), the order
+// of transformers' Qwen3OmniMoeThinkerTextRMSNorm.forward
+// (modeling_qwen3_omni_moe.py:1388-1393 in transformers 5.15).
+template <int XT> __device__ inline u32 norm_pair(u32 xp, u32 wp, float r) {
+  const float a = Half<XT>::to_f32(Half<XT>::from_f32(Half<XT>::to_f32((uint16_t)xp) * r));
+  const float b = Half<XT>::to_f32(Half<XT>::from_f32(Half<XT>::to_f32((uint16_t)(xp >> 16)) * r));
+  const u32 lo = Half<XT>::from_f32(a * Half<XT>::to_f32((uint16_t)wp));
+  const u32 hi = Half<XT>::from_f32(b * Half<XT>::to_f32((uint16_t)(wp >> 16)));
+  return lo | (hi << 16);
+}
+
+template <int XT> __device__ inline float sumsq8(u32x4 d) {
+  float s = 0.f;
+  const u32 w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = Half<XT>::to_f32((uint16_t)w[i]), b = Half<XT>::to_f32((uint16_t)(w[i] >> 16));
+    s += a * a;
+    s += b * b;
+  }
+  return s;
+}
+
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 
 

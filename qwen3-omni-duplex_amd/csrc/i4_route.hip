@@ -13,29 +13,6 @@
 
 namespace i4 {
 
-// RMSNorm of 8 values (one 16-byte load): round(round(x * r) * w), the order
-// of transformers' Qwen3OmniMoeThinkerTextRMSNorm.forward
-// (modeling_qwen3_omni_moe.py:1388-1393 in transformers 5.15).
-template <int XT> __device__ inline u32 norm_pair(u32 xp, u32 wp, float r) {
-  const float a = Half<XT>::to_f32(Half<XT>::from_f32(Half<XT>::to_f32((uint16_t)xp) * r));
-  const float b = Half<XT>::to_f32(Half<XT>::from_f32(Half<XT>::to_f32((uint16_t)(xp >> 16)) * r));
-  const u32 lo = Half<XT>::from_f32(a * Half<XT>::to_f32((uint16_t)wp));
-  const u32 hi = Half<XT>::from_f32(b * Half<XT>::to_f32((uint16_t)(wp >> 16)));
-  return lo | (hi << 16);
-}
-
-template <int XT> __device__ inline float sumsq8(u32x4 d) {
-  float s = 0.f;
-  const u32 w[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float a = Half<XT>::to_f32((uint16_t)w[i]), b = Half<XT>::to_f32((uint16_t)(w[i] >> 16));
-    s += a * a;
-    s += b * b;
-  }
-  return s;
-}
-
 // T = 1: the workgroup normalises x once (8 values per thread, x and the norm
 // weights loaded ahead of the router rows), shares xn through LDS, and each
 // wave dots one expert row.  The sum of squares is reduced in the same fixed
@@ -312,6 +289,21 @@ int i4_router_logits(const void* x, int x_dtype, int T, int H, const void* route
   if (((uintptr_t)x & 15) || ((uintptr_t)router_w & 15)) return I4_ERR_ALIGN;
   return i4_launch_router_logits(x, x_dtype, T, H, router_w, E, norm_w, norm_eps, xn_out, logits,
                                  stream);
+}
+
+int i4_rmsnorm(const void* x, int x_dtype, int T, int H, const void* norm_w, float eps, void* out,
+               hipStream_t stream) {
+  if (!x || !norm_w || !out) return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  if (T < 1 || T > 65535 * 4 || H < 8 || H % 8 != 0 || H > 4096) return I4_ERR_SHAPE;
+  if (((uintptr_t)x & 15) || ((uintptr_t)norm_w & 15) || ((uintptr_t)out & 15)) return I4_ERR_ALIGN;
+  if (x_dtype == I4_F16)
+    hipLaunchKernelGGL(i4::k_rmsnorm_t<I4_F16>, dim3(T), dim3(256), 0, stream,
+                       (const uint16_t*)x, H, (const uint16_t*)norm_w, eps, (uint16_t*)out);
+  else
+    hipLaunchKernelGGL(i4::k_rmsnorm_t<I4_BF16>, dim3(T), dim3(256), 0, stream,
+                       (const uint16_t*)x, H, (const uint16_t*)norm_w, eps, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
 int i4_route_topk(const void* logits, int logits_dtype, int T, int E, int topk, int renorm,

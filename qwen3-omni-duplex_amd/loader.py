@@ -32,6 +32,7 @@ from pathlib import Path
 
 import torch
 
+from .attention import ThinkerAttention, ThinkerDecoder, ThinkerDecoderLayer
 from .linear import PackedLinear, PackedQKV
 from .moe import FusedPackedMoE
 from .weights import QWeight
@@ -212,3 +213,38 @@ def load_attention(ckpt: Checkpoint, layer: int, device="cuda", fuse_qkv: bool =
         return {"qkv": PackedQKV.from_qweights(ws["q_proj"], ws["k_proj"], ws["v_proj"]),
                 "o": PackedLinear.from_qweight(ws["o_proj"], tile=tile)}
     return {k: PackedLinear.from_qweight(w, tile=tile) for k, w in ws.items()}
+
+
+def rope_theta(tc: dict) -> float:
+    """rope_theta of a text config (top level, or inside rope_parameters / rope_scaling)."""
+    for src in (tc, tc.get("rope_parameters") or {}, tc.get("rope_scaling") or {}):
+        if "rope_theta" in src:
+            return float(src["rope_theta"])
+    return 10000.0
+
+
+def load_thinker_layer(ckpt: Checkpoint, layer: int, device="cuda", dtype=torch.bfloat16,
+                       max_len: int = 4096, layouts: str = "both") -> ThinkerDecoderLayer:
+    """One Thinker decoder layer for decode: attention (input_layernorm, q|k|v in one
+    launch, q_norm / k_norm, rotary, KV cache of max_len positions, o_proj) and the MoE
+    block with its post_attention_layernorm (clock.py:45-103 loads the same tensors)."""
+    tc = ckpt.text_config()
+    base = f"{PREFIX}.{layer}"
+    nh, nkv = int(tc["num_attention_heads"]), int(tc["num_key_value_heads"])
+    hd = int(tc.get("head_dim") or tc["hidden_size"] // nh)
+    proj = load_attention(ckpt, layer, device, fuse_qkv=True)
+    attn = ThinkerAttention(
+        proj["qkv"], proj["o"],
+        ckpt.tensor(f"{base}.self_attn.q_norm.weight").to(device, dtype),
+        ckpt.tensor(f"{base}.self_attn.k_norm.weight").to(device, dtype),
+        ckpt.tensor(f"{base}.input_layernorm.weight").to(device, dtype),
+        nh, nkv, hd, float(tc.get("rms_norm_eps", 1e-6)), rope_theta(tc), max_len)
+    return ThinkerDecoderLayer(attn, load_moe_layer(ckpt, layer, device, dtype, layouts))
+
+
+def load_thinker_decoder(root: str | Path, n_layers: int = 24, device="cuda",
+                         dtype=torch.bfloat16, max_len: int = 4096) -> ThinkerDecoder:
+    """Thinker[0:n_layers] for one-token decode steps (the clock path's prefix)."""
+    ckpt = Checkpoint(root)
+    return ThinkerDecoder([load_thinker_layer(ckpt, layer, device, dtype, max_len)
+                           for layer in range(n_layers)])

@@ -7,6 +7,9 @@
     route          fused_packed_moe.py:195-199
     moe_forward    FusedPackedMoE.forward, fused_packed_moe.py:191-263
     moe_stack      Thinker[0:24] MoE stack with residual adds (clock.py:168-171)
+    rmsnorm        Qwen3OmniMoeThinkerTextRMSNorm (the decoder's input_layernorm)
+    attn_decode    Qwen3OmniMoeThinkerTextAttention.forward between its projections,
+                   one decode token with a KV cache (clock.py:164-172)
 
 Every op enqueues on torch's current stream of the tensors' device and never
 synchronises.
@@ -319,3 +322,48 @@ def moe_stack(x: torch.Tensor, layers: list[tuple], top_k: int,
                                        int(norm_topk_prob), out.data_ptr(), ws.data_ptr(),
                                        ws.numel(), _lib.stream(dev)))
     return out.view(shape)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Qwen3OmniMoeThinkerTextRMSNorm over the last dim (i4_rmsnorm), in x.dtype."""
+    dev = _lib.require_device(x, weight)
+    if weight.dtype != x.dtype:
+        raise RuntimeError("the norm weight must have the activation dtype")
+    xf = x.reshape(-1, x.shape[-1]).contiguous()
+    out = torch.empty_like(xf)
+    _lib.check(_lib.lib().i4_rmsnorm(xf.data_ptr(), _lib.half_code(x.dtype), xf.shape[0],
+                                     xf.shape[1], weight.contiguous().data_ptr(), float(eps),
+                                     out.data_ptr(), _lib.stream(dev)))
+    return out.view(x.shape)
+
+
+def attn_decode(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: torch.Tensor,
+                k_norm_w: torch.Tensor, eps: float, inv_freq: torch.Tensor, pos: int,
+                k_cache: torch.Tensor, v_cache: torch.Tensor,
+                workspace: Workspace | None = None) -> torch.Tensor:
+    """Decode attention of one token (i4_attn_decode) between the q/k/v and o projections:
+    qkv [n_heads + 2 n_kv_heads, head_dim] in, [n_heads * head_dim] out; appends k / v at
+    row `pos` of the caches [n_kv_heads, max_len, head_dim] and attends rows [0, pos].
+    inv_freq is the host fp32 table of the rotary embedding ([head_dim / 2])."""
+    dev = _lib.require_device(qkv, q_norm_w, k_norm_w, k_cache, v_cache)
+    xt = _lib.half_code(qkv.dtype)
+    nkv, max_len, hd = k_cache.shape
+    if k_cache.dtype != qkv.dtype or v_cache.shape != k_cache.shape or v_cache.dtype != qkv.dtype:
+        raise RuntimeError("the caches must be [n_kv_heads, max_len, head_dim] in the activation dtype")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise RuntimeError("the caches must be contiguous")
+    if qkv.numel() != (n_heads + 2 * n_kv_heads) * hd or nkv != n_kv_heads:
+        raise RuntimeError("qkv / cache shapes do not match the head counts")
+    tab = inv_freq.detach().to("cpu", torch.float32).contiguous()
+    if tab.numel() != hd // 2:
+        raise RuntimeError("inv_freq must hold head_dim / 2 values")
+    lb = _lib.lib()
+    nbytes = lb.i4_attn_decode_workspace_bytes(n_heads, hd, max_len)
+    ws = (workspace or Workspace()).get(nbytes, dev)
+    out = torch.empty(n_heads * hd, dtype=qkv.dtype, device=dev)
+    _lib.check(lb.i4_attn_decode(
+        qkv.contiguous().data_ptr(), xt, n_heads, n_kv_heads, hd,
+        q_norm_w.contiguous().data_ptr(), k_norm_w.contiguous().data_ptr(), float(eps),
+        tab.data_ptr(), int(pos), k_cache.data_ptr(), v_cache.data_ptr(), max_len,
+        out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(dev)))
+    return out

@@ -35,8 +35,10 @@ def _linear(rng, out_f, in_f, G):
 
 
 def write_checkpoint(root: Path, rng, n_layers=2, E=4, H=256, I=128, G=32, top_k=2,
-                     shards=2, attention=None, single_file=False, group_in_config=True):
-    """attention = (q_out, kv_out) adds self_attn.{q,k,v,o}_proj to every layer."""
+                     shards=2, attention=None, single_file=False, group_in_config=True,
+                     head_dim=128):
+    """attention = (q_out, kv_out) adds self_attn.{q,k,v,o}_proj and q_norm / k_norm
+    ([head_dim]) to every layer."""
     root = Path(root)
     root.mkdir(parents=True, exist_ok=True)
     truth, blobs = [], [dict() for _ in range(shards)]
@@ -58,8 +60,10 @@ def write_checkpoint(root: Path, rng, n_layers=2, E=4, H=256, I=128, G=32, top_k
             rng.uniform(0.5, 1.5, H).astype(np.float32)))
         blob[f"{base}.mlp.gate.weight"] = _bf16(router)
         blob[f"{base}.post_attention_layernorm.weight"] = _bf16(norm)
-        blob[f"{base}.input_layernorm.weight"] = _bf16(np.ones(H, np.float32))
-        t["router"], t["norm"] = router, norm
+        in_norm = i4ref.bf16_bits_to_f32(i4ref.f32_to_bf16_bits(
+            rng.uniform(0.5, 1.5, H).astype(np.float32)))
+        blob[f"{base}.input_layernorm.weight"] = _bf16(in_norm)
+        t["router"], t["norm"], t["in_norm"] = router, norm, in_norm
         if attention is not None:
             q_out, kv_out = attention
             for proj, (o, i) in (("q_proj", (q_out, H)), ("k_proj", (kv_out, H)),
@@ -68,6 +72,11 @@ def write_checkpoint(root: Path, rng, n_layers=2, E=4, H=256, I=128, G=32, top_k
                 t["attn"][proj] = (q, s)
                 for k, v in tens.items():
                     blob[f"{base}.self_attn.{proj}.{k}"] = v
+            for nm in ("q_norm", "k_norm"):
+                w = i4ref.bf16_bits_to_f32(i4ref.f32_to_bf16_bits(
+                    rng.uniform(0.5, 1.5, head_dim).astype(np.float32)))
+                blob[f"{base}.self_attn.{nm}.weight"] = _bf16(w)
+                t["attn"][nm] = w
         truth.append(t)
     from safetensors.torch import save_file
 
@@ -85,7 +94,10 @@ def write_checkpoint(root: Path, rng, n_layers=2, E=4, H=256, I=128, G=32, top_k
     cfg = {"thinker_config": {"text_config": {
         "num_experts": E, "num_experts_per_tok": top_k, "hidden_size": H,
         "moe_intermediate_size": I, "norm_topk_prob": True, "rms_norm_eps": 1e-6,
-        "decoder_sparse_step": 1, "mlp_only_layers": [], "num_hidden_layers": n_layers}}}
+        "decoder_sparse_step": 1, "mlp_only_layers": [], "num_hidden_layers": n_layers,
+        "head_dim": head_dim, "rope_theta": 1000000.0,
+        "num_attention_heads": (attention[0] // head_dim) if attention else 1,
+        "num_key_value_heads": (attention[1] // head_dim) if attention else 1}}}
     if group_in_config:
         cfg["quantization_config"] = {"format": "pack-quantized", "config_groups": {"group_0": {
             "weights": {"num_bits": 4, "group_size": G, "symmetric": True,

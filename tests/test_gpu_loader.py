@@ -89,3 +89,96 @@ def test_loaded_attention_projections(pkg, dev, ckpt, rows):
     ref = i4ref.bf16_bits_to_f32(xo).astype(np.float64) @ W.T
     assert i4ref.rel_err(host(lin["o_proj"](t_(xo, dev))), ref) <= TOL
     assert i4ref.rel_err(host(fused["o"](t_(xo, dev))), ref) <= TOL
+
+
+def _attn_weights(t):
+    return {n[0]: torch.from_numpy(_ckpt.dense(t["attn"][f"{n}_proj"])).float()
+            for n in ("q", "k", "v", "o")}
+
+
+def _bf16_to_torch(a):
+    return torch.from_numpy(i4ref.bf16_bits_to_f32(a)).float()
+
+
+@pytest.mark.parametrize("start", [0, 60])
+def test_thinker_attention_decode_matches_reference(pkg, dev, ckpt, start):
+    """Decode steps through ThinkerAttention (input RMSNorm, q|k|v GEMV, q/k norm + rotary +
+    cache append, GQA attention over the cache, o_proj + residual) against the fp32
+    reference on the same inputs; start = 60 crosses the 64-position chunk boundary and
+    reads cache rows written by earlier calls."""
+    from tests import _thinker_ref
+
+    root, truth = ckpt
+    ld = _ld(pkg)
+    layer = ld.load_thinker_layer(ld.Checkpoint(root), 1, dev, torch.bfloat16, max_len=256)
+    attn = layer.attn
+    t = truth[1]
+    W = _attn_weights(t)
+    rng = np.random.default_rng(90 + start)
+    # rows [0, start) of the cache: arbitrary earlier keys / values, shared by both sides
+    kv = [i4ref.f32_to_bf16_bits(rng.standard_normal((4, start, 128)).astype(np.float32))
+          for _ in range(2)]
+    attn.k_cache[:, :start] = t_(kv[0], dev)
+    attn.v_cache[:, :start] = t_(kv[1], dev)
+    cache = {"k": _bf16_to_torch(kv[0]), "v": _bf16_to_torch(kv[1])}
+    for pos in range(start, start + 6):
+        h = make_x(rng, (1, H), "bf16")
+        got = host(attn(t_(h, dev), pos))[0]
+        ref = _thinker_ref.attention_decode(
+            _bf16_to_torch(h[0]), W, torch.from_numpy(t["attn"]["q_norm"]),
+            torch.from_numpy(t["attn"]["k_norm"]), torch.from_numpy(t["in_norm"]), 1e-6,
+            pkg.rope_inv_freq(128, 1e6), pos, cache, 32, 4).numpy()
+        assert np.all(np.isfinite(got))
+        # the attention's own contribution, checked apart from the residual
+        res = i4ref.bf16_bits_to_f32(h[0]).astype(np.float64)
+        assert i4ref.rel_err(got - res, ref - res) <= TOL
+        # the cache rows the kernel wrote match the reference's (k normed + rotated, v as is)
+        kg = attn.k_cache[:, pos].float().cpu().numpy()
+        assert i4ref.rel_err(kg, cache["k"][:, pos].numpy()) <= TOL
+        vg = attn.v_cache[:, pos].float().cpu().numpy()
+        assert i4ref.rel_err(vg, cache["v"][:, pos].numpy()) <= TOL
+
+
+def test_thinker_attention_long_context(pkg, dev, ckpt):
+    """One decode step at position 3000 (47 chunks merged by the combine kernel)."""
+    from tests import _thinker_ref
+
+    root, truth = ckpt
+    ld = _ld(pkg)
+    layer = ld.load_thinker_layer(ld.Checkpoint(root), 0, dev, torch.bfloat16, max_len=4096)
+    attn = layer.attn
+    t = truth[0]
+    rng = np.random.default_rng(95)
+    P = 3000
+    kv = [i4ref.f32_to_bf16_bits(rng.standard_normal((4, P, 128)).astype(np.float32))
+          for _ in range(2)]
+    attn.k_cache[:, :P] = t_(kv[0], dev)
+    attn.v_cache[:, :P] = t_(kv[1], dev)
+    cache = {"k": _bf16_to_torch(kv[0]), "v": _bf16_to_torch(kv[1])}
+    h = make_x(rng, (1, H), "bf16")
+    got = host(attn(t_(h, dev), P))[0]
+    ref = _thinker_ref.attention_decode(
+        _bf16_to_torch(h[0]), _attn_weights(t), torch.from_numpy(t["attn"]["q_norm"]),
+        torch.from_numpy(t["attn"]["k_norm"]), torch.from_numpy(t["in_norm"]), 1e-6,
+        pkg.rope_inv_freq(128, 1e6), P, cache, 32, 4).numpy()
+    res = i4ref.bf16_bits_to_f32(h[0]).astype(np.float64)
+    assert i4ref.rel_err(got - res, ref - res) <= TOL
+
+
+def test_thinker_decoder_step_composes(pkg, dev, ckpt):
+    """ThinkerDecoder.step = attention then MoE block per layer, bit for bit, and finite over
+    several positions (the per-block parity is checked above and in the MoE tests)."""
+    root, _ = ckpt
+    ld = _ld(pkg)
+    dec = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=64)
+    twin = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=64)
+    rng = np.random.default_rng(96)
+    for pos in range(4):
+        x = t_(make_x(rng, (1, H), "bf16"), dev)
+        out = dec.step(x, pos)
+        h = x
+        for layer in twin.layers:
+            h = layer.attn(h, pos)
+            h = layer.moe(h, residual=h)
+        assert torch.isfinite(out.float()).all()
+        assert torch.equal(out, h)
