@@ -213,6 +213,58 @@ def graph_times(torch, launches, replays):
     return [a.elapsed_time(b) * 1e3 for a, b in evs]
 
 
+def time_decode_step(pkg, torch, dev, mods, ctx, replays):
+    """The Thinker[0:24] decode step around the MoE stack (clock.py:164-172): per layer the
+    attention half (input RMSNorm, q|k|v int4 GEMV, q/k norm + rotary + KV-cache append,
+    GQA attention over ctx cached positions, o_proj + residual) and the MoE block.  Attention
+    weights are CT g32 symmetric int4 with fp16 scales (the reference checkpoint's packing),
+    32 query / 4 kv heads of 128, generated on the device; cache rows [0, ctx) random.
+    Each timed region is one hipGraph of all layers at position ctx."""
+    nh, nkv, hd, gs = 32, 4, 128, 32
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4321)
+
+    def ct(N, K):
+        p = torch.randint(-2**31, 2**31, (1, N, K // 8), dtype=torch.int32, device=dev,
+                          generator=gen)
+        sc = (torch.rand(1, N, K // gs, device=dev, generator=gen) * 0.018 + 0.002).half()
+        return pkg.QWeight(p, sc, None, "ct", gs, N, K)
+
+    def vec(n, lo=0.8, hi=1.2):
+        return (torch.rand(n, device=dev, generator=gen) * (hi - lo) + lo).half()
+
+    layers = []
+    for m in mods:
+        qkv = pkg.PackedQKV.from_qweights(ct(nh * hd, H), ct(nkv * hd, H), ct(nkv * hd, H))
+        o = pkg.PackedLinear.from_qweight(ct(H, nh * hd))
+        attn = pkg.ThinkerAttention(qkv, o, vec(hd), vec(hd), vec(H), nh, nkv, hd,
+                                    max_len=ctx + 64)
+        attn.k_cache[:, :ctx] = torch.randn(nkv, ctx, hd, device=dev, generator=gen).half()
+        attn.v_cache[:, :ctx] = torch.randn(nkv, ctx, hd, device=dev, generator=gen).half()
+        layers.append(pkg.ThinkerDecoderLayer(attn, m))
+    dec = pkg.ThinkerDecoder(layers)
+    x = torch.randn(1, H, device=dev, generator=gen).half()
+    out = {}
+    for name, fn in (("step", lambda: dec.step(x, ctx)),
+                     ("attention", lambda: [l.attn(x, ctx) for l in layers])):
+        ts = graph_times(torch, fn, replays)
+        us = sum(ts) / len(ts)
+        out[name] = {"us_per_token": round(us, 2), "us_per_layer": round(us / len(layers), 3),
+                     "us_median": round(pct(ts, 50), 2), "us_p99": round(pct(ts, 99), 2)}
+    h = dec.step(x, ctx)
+    torch.cuda.synchronize()
+    if not torch.isfinite(h.float()).all():
+        raise RuntimeError("the decode step produced non-finite values")
+    # K and V bytes read by the attention of one layer at this context (fp16 cache)
+    kv_bytes = 2 * nkv * (ctx + 1) * hd * 2
+    w_bytes = (nh * hd + 2 * nkv * hd) * H // 2 + H * nh * hd // 2
+    return {"context": ctx, "layers": len(layers), **out,
+            "attention_weight_bytes_per_layer": w_bytes + (nh * hd + 2 * nkv * hd) * (H // gs) * 2
+            + H * (nh * hd // gs) * 2, "kv_bytes_per_layer": kv_bytes,
+            "timing": "hipGraph of all layers at position ctx (cache rows [0, ctx) filled), "
+                      f"mean over {replays} replays"}
+
+
 def pct(vals, q):
     v = sorted(vals)
     return v[min(len(v) - 1, int(round(q / 100 * (len(v) - 1))))]
@@ -419,6 +471,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--kernel-rounds", type=int, default=8)
+    ap.add_argument("--decode-step", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the whole Thinker decode step (attention + MoE per layer)")
+    ap.add_argument("--context", type=int, default=1024,
+                    help="cached positions the decode step attends")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill", action=argparse.BooleanOptionalAction, default=True,
@@ -585,6 +641,12 @@ def main() -> int:
 
     gemv = time_gemvs(pkg, torch, dev, args.replays) if args.gemv else None
 
+    decode = None
+    if args.decode_step:
+        decode = time_decode_step(pkg, torch, dev, mods, args.context, args.replays)
+        log(f"decode step (context {args.context}): {decode['step']['us_per_token']:.1f} us/token, "
+            f"attention {decode['attention']['us_per_layer']:.2f} us/layer")
+
     # ---- CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -633,6 +695,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "other_workloads": prefill,
         "gemv": gemv,
+        "thinker_decode_step": decode,
     }
     print(json.dumps(res), flush=True)
     return 0

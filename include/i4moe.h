@@ -163,6 +163,16 @@ int    i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w,
                  void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t i4_linear_workspace_bytes(const i4_qweight* w, int M);
 
+/* y = W RMSNorm(x) (+ bias) for every row of x in one launch: the decoder's
+ * input_layernorm in front of the fused q|k|v projection (transformers
+ * Qwen3OmniMoeThinkerTextDecoderLayer.forward, modeling_qwen3_omni_moe.py:1547-1549;
+ * the reference runs the norm, then TritonPackedLinear, triton_dequant_gemv.py:151-159).
+ * Each workgroup normalises its staged row with the arithmetic of i4_rmsnorm, so the
+ * result equals i4_rmsnorm followed by i4_linear bit for bit.  CT weights, K <= 4096. */
+int    i4_rmsnorm_linear(const void* x, int x_dtype, int M, const void* norm_w, float eps,
+                         const i4_qweight* w, const void* bias, void* y, int y_dtype,
+                         hipStream_t stream);
+
 /* unpack4 (src/duplex/streaming/fused_packed_moe.py:54-65): raw nibbles of
  * every expert in logical [E][N][K] order as uint8 0..15 (the reference's
  * signed value is nibble - 8).  Same device decode as the GEMV kernels. */
@@ -277,8 +287,9 @@ int    i4_rmsnorm(const void* x, int x_dtype, int T, int H, const void* norm_w, 
  *            head h / (n_heads / n_kv_heads));
  *   out      [n_heads][head_dim] = softmax(q k^T / sqrt(head_dim)) v, fp32 inside,
  *            rounded once to x_dtype.
- * head_dim == 128, n_heads / n_kv_heads <= 8, 0 <= pos < max_len.  The workspace
- * (i4_attn_decode_workspace_bytes) needs no initial contents. */
+ * head_dim == 128, n_heads / n_kv_heads <= 8, 0 <= pos < max_len <= 65536.  The workspace
+ * (i4_attn_decode_workspace_bytes) needs no initial contents; calls sharing one must not
+ * overlap. */
 int    i4_attn_decode(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
                       const void* q_norm_w, const void* k_norm_w, float eps,
                       const float* inv_freq, int pos, void* k_cache, void* v_cache,

@@ -21,7 +21,7 @@ from .loader import (Checkpoint, load_attention, load_moe_layer, load_thinker_de
 from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_forward, moe_gate_up,
                   moe_route_gate_up, moe_stack, route, router_logits, unpack4, unpack_nibbles,
-                  Workspace, rmsnorm, attn_decode)
+                  Workspace, rmsnorm, rmsnorm_linear, attn_decode)
 from .weights import QWeight, repack_awq_to_ct, repack_tile
 
 lib = _lib.lib
@@ -34,6 +34,6 @@ __all__ = [
     "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "PackedQKV", "QKVSlice",
     "concat_rows", "patch_attention", "TILE_ROWS", "lib",
     "Checkpoint", "read_moe_layer", "load_moe_layer", "load_thinker_moe_stack", "load_attention",
-    "load_thinker_layer", "load_thinker_decoder", "rmsnorm", "attn_decode",
+    "load_thinker_layer", "load_thinker_decoder", "rmsnorm", "rmsnorm_linear", "attn_decode",
     "ThinkerAttention", "ThinkerDecoderLayer", "ThinkerDecoder", "rope_inv_freq",
 ]

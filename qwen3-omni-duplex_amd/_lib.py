@@ -84,6 +84,8 @@ SIGNATURES = {
     "i4_moe_stack_forward": (c_int, [c_void_p, c_int, c_int, POINTER(MoeWeightsC), c_int, c_int,
                                      c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "i4_moe_stack_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "i4_rmsnorm_linear": (c_int, [c_void_p, c_int, c_int, c_void_p, ctypes.c_float,
+                                  POINTER(QWeightC), c_void_p, c_void_p, c_int, c_void_p]),
     "i4_rmsnorm": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, ctypes.c_float, c_void_p,
                            c_void_p]),
     "i4_attn_decode": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,

@@ -61,8 +61,8 @@ class ThinkerAttention(nn.Module):
             raise ValueError("ThinkerAttention decodes one token")
         if not 0 <= pos < self.max_len:
             raise ValueError(f"position {pos} outside the cache (max_len {self.max_len})")
-        xn = ops.rmsnorm(h, self.input_norm_w, self.eps)
-        qkv = self.qkv.lin(xn)
+        # input_layernorm folded into the q|k|v launch
+        qkv = ops.rmsnorm_linear(h, self.input_norm_w, self.eps, self.qkv.lin.w)
         a = ops.attn_decode(qkv, self.n_heads, self.n_kv_heads, self.q_norm_w, self.k_norm_w,
                             self.eps, self.inv_freq, pos, self.k_cache, self.v_cache,
                             self.workspace)

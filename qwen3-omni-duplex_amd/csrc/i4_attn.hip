@@ -4,15 +4,15 @@
 // DynamicCache of src/duplex/streaming/clock.py:164-172.  The q/k/v and o
 // projections are the library's int4 GEMVs; this file holds what lies between
 // them:
-//   k_qk_norm_rope  one wave per head of the fused q|k|v output: RMSNorm over
-//                   head_dim (q_norm / k_norm), the rotary embedding at `pos`
-//                   (cos / sin rounded to the activation dtype and every product
-//                   rounded, as transformers computes in bf16), q to q_out, k and
-//                   v appended to the cache at row `pos`;
-//   k_attn_chunk    one workgroup per (kv head, 64 cached positions): scores of
-//                   the kv head's query heads (GQA: each K and V row is loaded
-//                   once for all of them), the chunk's softmax statistics and the
-//                   probability-weighted sum of V, all in fp32;
+//   k_attn_chunk    one workgroup per (kv head, 64 cached positions): RMSNorm
+//                   over head_dim (q_norm / k_norm) and the rotary embedding at
+//                   `pos` for the kv head's query heads and (in the workgroup
+//                   holding `pos`) this token's key, which it appends to the
+//                   cache with its value (cos / sin rounded to the activation
+//                   dtype and every product rounded, as transformers computes in
+//                   bf16); then the scores of the query heads (GQA: each K and V
+//                   row is loaded once for all of them), the chunk's softmax
+//                   statistics and the probability-weighted sum of V in fp32;
 //   k_attn_combine  merges the chunks of each query head (flash-decoding) and
 //                   rounds the output once to the activation dtype.
 // Text positions are equal along mRoPE's three axes, where the interleaved
@@ -26,6 +26,7 @@ namespace i4 {
 static constexpr int HD = 128;    // head_dim
 static constexpr int ACH = 64;    // cached positions per attention workgroup
 static constexpr int GQMAX = 8;   // query heads per kv head
+static constexpr int PSTR = HD + 4;  // floats per chunk partial: m, l, pad, acc[HD] at 4
 
 struct RopeTab {
   float inv_freq[HD / 2];
@@ -51,30 +52,16 @@ template <int L> __device__ inline float group_max(float v) {
   return v;
 }
 
-// Blocks [0, nq): query heads, [nq, nq + nkv): key heads, then value heads, in
-// the row order of the fused projection output.  Lane l holds dims 2l, 2l + 1;
+// RMSNorm over one head (lane l holds dims 2l, 2l + 1 of the 128) and the
+// rotary embedding at `pos`; returns the two rounded outputs packed.
 // rotate_half pairs dim d with d +- 64, i.e. lane l with lane l ^ 32.
 template <int XT>
-__global__ __launch_bounds__(64) void k_qk_norm_rope(
-    const uint16_t* __restrict__ qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
-    const uint16_t* __restrict__ kn_w, float eps, int pos, RopeTab rt,
-    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
-    int64_t head_stride) {
-  const int h = blockIdx.x, lane = threadIdx.x;
-  const bool isq = h < nq, isk = !isq && h < nq + nkv;
-  const u32 raw = *(const u32*)(qkv + (int64_t)h * HD + 2 * lane);
-  uint16_t* dst = isq ? q_out + (int64_t)h * HD
-                      : (isk ? k_cache + (int64_t)(h - nq) * head_stride
-                             : v_cache + (int64_t)(h - nq - nkv) * head_stride) +
-                            (int64_t)pos * HD;
-  if (!isq && !isk) {  // values enter the cache as they are
-    *(u32*)(dst + 2 * lane) = raw;
-    return;
-  }
+__device__ inline u32 head_norm_rope(u32 raw, u32 wraw, float eps, int pos, const RopeTab& rt) {
+  const int lane = __lane_id();
   const float x0 = Half<XT>::to_f32((uint16_t)raw), x1 = Half<XT>::to_f32((uint16_t)(raw >> 16));
   const float ss = group_sum<64>(x0 * x0 + x1 * x1);
   const float r = 1.0f / sqrtf(ss / (float)HD + eps);
-  const u32 n = norm_pair<XT>(raw, *(const u32*)((isq ? qn_w : kn_w) + 2 * lane), r);
+  const u32 n = norm_pair<XT>(raw, wraw, r);
   const float a0 = Half<XT>::to_f32((uint16_t)n), a1 = Half<XT>::to_f32((uint16_t)(n >> 16));
   const float b0 = xor32(a0), b1 = xor32(a1);  // dims 2l +- 64, 2l + 1 +- 64
   const int i0 = (2 * lane) & (HD / 2 - 1);
@@ -85,50 +72,92 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(
   const float sg = lane < 32 ? -1.f : 1.f;
   const float o0 = rnd<XT>(rnd<XT>(a0 * c0) + rnd<XT>(sg * b0 * s0));
   const float o1 = rnd<XT>(rnd<XT>(a1 * c1) + rnd<XT>(sg * b1 * s1));
-  *(u32*)(dst + 2 * lane) =
-      (u32)Half<XT>::from_f32(o0) | ((u32)Half<XT>::from_f32(o1) << 16);
+  return (u32)Half<XT>::from_f32(o0) | ((u32)Half<XT>::from_f32(o1) << 16);
 }
 
-// Workgroup (chunk c, kv head g): positions [64c, 64c + 64) of [0, S).
-// part[(c * nq + head) * (2 + HD)] = {chunk max m, sum l, acc[HD]} with
-// acc = sum_j exp(s_j - m) v_j and s_j = scale * q . k_j.
+// Workgroup (chunk c, kv head g) attends positions [64c, 64c + 64) of [0, S),
+// S = pos + 1.  It issues its K and V rows first, then normalises and rotates
+// the group's query heads itself from the projection output (each chunk of a
+// group repeats that: 8 heads of 128 values), and the workgroup whose chunk
+// holds `pos` also makes this token's key (normalised, rotated) and value,
+// stores them in the cache and uses them in place of the rows it could not
+// have loaded.  Scores are v_dot2 products of the rounded half-precision q and
+// k pairs with fp32 accumulation; softmax statistics and P V in fp32.
+// part[(c * nq + head) * PSTR] = {chunk max m, sum l, -, -, acc[HD]}.
 template <int XT, int GQ>
 __global__ __launch_bounds__(256) void k_attn_chunk(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
-    const uint16_t* __restrict__ v_cache, int64_t head_stride, int S, float scale, int nq,
-    float* __restrict__ part) {
-  __shared__ float s_q[GQ][HD];
-  __shared__ float s_p[GQ][ACH];
+    const uint16_t* __restrict__ qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, float eps, int pos, RopeTab rt,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t head_stride,
+    float scale, float* __restrict__ part) {
+  __shared__ __align__(16) u32 s_q[GQ][HD / 2];  // rotated q pairs
+  __shared__ u32 s_knew[HD / 2], s_vnew[HD / 2];
+  __shared__ __align__(16) float s_p[GQ][ACH];
   __shared__ float s_red[4][GQ][HD];
   __shared__ float s_stat[GQ][2];
   const int c = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
-  const int c0 = c * ACH;
+  const int wave = t >> 6, lane = t & 63;
+  const int S = pos + 1, c0 = c * ACH;
+  const bool last = c0 + ACH >= S;  // the chunk that holds pos
   const int64_t kv0 = (int64_t)g * head_stride;
-  // K rows of the chunk first: thread t reads dims [32 (t & 3), +32) of key t >> 2
+  // the projection rows this workgroup rotates come first: wave w takes query
+  // heads w and w + 4, and wave 0 of the last chunk this token's key and value
+  constexpr int QPW = (GQ + 3) / 4;
+  u32 qraw[QPW], qw = *(const u32*)(qn_w + 2 * lane), kraw = 0, kwn = 0, vraw = 0;
+#pragma unroll
+  for (int i = 0; i < QPW; ++i)
+    qraw[i] = *(const u32*)(qkv + (int64_t)(g * GQ + min(wave + 4 * i, GQ - 1)) * HD + 2 * lane);
+  if (last && wave == 0) {
+    kraw = *(const u32*)(qkv + (int64_t)(nq + g) * HD + 2 * lane);
+    vraw = *(const u32*)(qkv + (int64_t)(nq + nkv + g) * HD + 2 * lane);
+    kwn = *(const u32*)(kn_w + 2 * lane);
+  }
+  // K: thread t reads dims [32 (t & 3), +32) of position c0 + (t >> 2), rows < pos
   const int j = t >> 2, qp = t & 3;
-  const bool kvalid = c0 + j < S;
-  const uint16_t* krow = k_cache + kv0 + (int64_t)min(c0 + j, S - 1) * HD + 32 * qp;
+  const int kr = min(c0 + j, max(pos - 1, 0));
+  const uint16_t* krow = k_cache + kv0 + (int64_t)kr * HD + 32 * qp;
   u32x4 kw[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) kw[u] = ldg16(krow + 8 * u);
-  for (int i = t; i < GQ * HD; i += 256)
-    s_q[i / HD][i % HD] = Half<XT>::to_f32(q[(int64_t)g * GQ * HD + i]);
+  // V: thread t reads dims 2 (t & 63), +1 of positions c0 + 16 (t >> 6) + i
+  const int d2 = t & 63, ks = t >> 6;
+  u32 vv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    vv[i] = *(const u32*)(v_cache + kv0 + (int64_t)min(c0 + 16 * ks + i, max(pos - 1, 0)) * HD +
+                          2 * d2);
+#pragma unroll
+  for (int i = 0; i < QPW; ++i)
+    if (wave + 4 * i < GQ) s_q[wave + 4 * i][lane] = head_norm_rope<XT>(qraw[i], qw, eps, pos, rt);
+  if (last && wave == 0) {
+    const u32 kn = head_norm_rope<XT>(kraw, kwn, eps, pos, rt);
+    s_knew[lane] = kn;
+    s_vnew[lane] = vraw;
+    *(u32*)(k_cache + kv0 + (int64_t)pos * HD + 2 * lane) = kn;
+    *(u32*)(v_cache + kv0 + (int64_t)pos * HD + 2 * lane) = vraw;
+  }
   __syncthreads();
+  if (last && c0 + j >= pos) {  // this token's key replaces the row that was loaded
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      kw[u] = u32x4{s_knew[16 * qp + 4 * u], s_knew[16 * qp + 4 * u + 1],
+                    s_knew[16 * qp + 4 * u + 2], s_knew[16 * qp + 4 * u + 3]};
+  }
   float sc[GQ];
 #pragma unroll
-  for (int h = 0; h < GQ; ++h) sc[h] = 0.f;
+  for (int h = 0; h < GQ; ++h) {
+    float a = 0.f;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const u32 w[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int d = 32 * qp + 8 * u + 2 * e;
-      const float k0 = Half<XT>::to_f32((uint16_t)w[e]);
-      const float k1 = Half<XT>::to_f32((uint16_t)(w[e] >> 16));
-#pragma unroll
-      for (int h = 0; h < GQ; ++h) sc[h] += k0 * s_q[h][d] + k1 * s_q[h][d + 1];
+    for (int u = 0; u < 4; ++u) {
+      const u32x4 qv = *(const u32x4*)&s_q[h][16 * qp + 4 * u];
+      a = Half<XT>::dot2(kw[u].x, qv.x, a);
+      a = Half<XT>::dot2(kw[u].y, qv.y, a);
+      a = Half<XT>::dot2(kw[u].z, qv.z, a);
+      a = Half<XT>::dot2(kw[u].w, qv.w, a);
     }
+    sc[h] = a;
   }
+  const bool kvalid = c0 + j < S;
 #pragma unroll
   for (int h = 0; h < GQ; ++h) {
     const float v = group_sum<4>(sc[h]);
@@ -152,24 +181,27 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
     }
   }
   __syncthreads();
-  // P V: thread t sums dims 2 (t & 63), 2 (t & 63) + 1 over positions [16 (t >> 6), +16)
-  const int d2 = t & 63, ks = t >> 6;
-  u32 vv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    vv[i] = *(const u32*)(v_cache + kv0 + (int64_t)min(c0 + 16 * ks + i, S - 1) * HD + 2 * d2);
   float acc[GQ][2];
 #pragma unroll
   for (int h = 0; h < GQ; ++h) acc[h][0] = acc[h][1] = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float v0 = Half<XT>::to_f32((uint16_t)vv[i]);
-    const float v1 = Half<XT>::to_f32((uint16_t)(vv[i] >> 16));
+  for (int i4 = 0; i4 < 16; i4 += 4) {
+    float4 p4[GQ];
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) {
-      const float p = s_p[h][16 * ks + i];  // 0 past S
-      acc[h][0] += p * v0;
-      acc[h][1] += p * v1;
+    for (int h = 0; h < GQ; ++h) p4[h] = *(const float4*)&s_p[h][16 * ks + i4];  // 0 past S
+#pragma unroll
+    for (int i = i4; i < i4 + 4; ++i) {
+      // this token's value at pos, and in place of the rows past it (weight 0, but a
+      // cache row never written may hold a NaN)
+      const u32 vw = (last && c0 + 16 * ks + i >= pos) ? s_vnew[d2] : vv[i];
+      const float v0 = Half<XT>::to_f32((uint16_t)vw);
+      const float v1 = Half<XT>::to_f32((uint16_t)(vw >> 16));
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) {
+        const float p = i == i4 ? p4[h].x : i == i4 + 1 ? p4[h].y : i == i4 + 2 ? p4[h].z : p4[h].w;
+        acc[h][0] += p * v0;
+        acc[h][1] += p * v1;
+      }
     }
   }
 #pragma unroll
@@ -181,8 +213,8 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   for (int i = t; i < GQ * HD; i += 256) {
     const int h = i / HD, d = i % HD;
     const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
-    float* dst = part + ((int64_t)c * nq + g * GQ + h) * (2 + HD);
-    dst[2 + d] = o;
+    float* dst = part + ((int64_t)c * nq + g * GQ + h) * PSTR;
+    dst[4 + d] = o;
     if (d == 0) {
       dst[0] = s_stat[h][0];
       dst[1] = s_stat[h][1];
@@ -190,30 +222,50 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   }
 }
 
-// One workgroup of HD threads per query head: out = sum_c w_c acc_c / sum_c w_c l_c
-// with w_c = exp(m_c - max_c m_c), in chunk order.
+// One workgroup of HD threads per query head merges its chunks:
+// out = sum_c w_c acc_c / sum_c w_c l_c with w_c = exp(m_c - max_c m_c), in chunk
+// order.  The chunk statistics are read by all threads at once and the weights kept
+// in LDS, so the accumulator loads of the final pass are independent.
+static constexpr int CMB = 1024;  // chunks per head at most (max_len <= 65536)
 template <int XT>
 __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ part, int nq,
                                                      int nch, uint16_t* __restrict__ out) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  float M = -__builtin_inff();
-  for (int c = 0; c < nch; ++c) M = fmaxf(M, part[((int64_t)c * nq + h) * (2 + HD)]);
-  float L = 0.f, O = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    const float* p = part + ((int64_t)c * nq + h) * (2 + HD);
-    const float w = expf(p[0] - M);
-    L += p[1] * w;
-    O += p[2 + d] * w;
+  __shared__ float s_w[CMB];
+  __shared__ float s_r[2][HD / 64];
+  const int h = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  auto at = [&](int c) { return part + ((int64_t)c * nq + h) * PSTR; };
+  float m = -__builtin_inff();
+  for (int c = t; c < nch; c += HD) {
+    s_w[c] = at(c)[0];
+    m = fmaxf(m, s_w[c]);
   }
-  out[(int64_t)h * HD + d] = Half<XT>::from_f32(O / L);
+  m = group_max<32>(m);
+  m = fmaxf(m, xor32(m));
+  if (lane == 0) s_r[0][wave] = m;
+  __syncthreads();
+  const float M = fmaxf(s_r[0][0], s_r[0][1]);
+  float l = 0.f;
+  for (int c = t; c < nch; c += HD) {
+    const float w = expf(s_w[c] - M);
+    s_w[c] = w;
+    l += at(c)[1] * w;
+  }
+  l = group_sum<64>(l);
+  if (lane == 0) s_r[1][wave] = l;
+  __syncthreads();
+  const float L = s_r[1][0] + s_r[1][1];
+  float o = 0.f;
+#pragma unroll 8
+  for (int c = 0; c < nch; ++c) o += at(c)[4 + t] * s_w[c];
+  out[(int64_t)h * HD + t] = Half<XT>::from_f32(o / L);
 }
 
 namespace {
 
+// workspace: the chunk partials [nch][nq][PSTR] fp32
 size_t attn_ws(int nq, int max_len) {
-  const size_t q = ((size_t)nq * HD * 2 + 255) & ~(size_t)255;
   const size_t nch = ((size_t)max_len + ACH - 1) / ACH;
-  return q + nch * nq * (2 + HD) * sizeof(float);
+  return nch * nq * PSTR * sizeof(float);
 }
 
 template <int XT>
@@ -221,11 +273,7 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
                 const RopeTab& rt, int pos, void* k_cache, void* v_cache, int max_len, void* out,
                 void* ws, hipStream_t s) {
   const int64_t hs = (int64_t)max_len * HD;
-  uint16_t* qo = (uint16_t*)ws;
-  float* part = (float*)((char*)ws + (((size_t)nq * HD * 2 + 255) & ~(size_t)255));
-  hipLaunchKernelGGL(k_qk_norm_rope<XT>, dim3(nq + 2 * nkv), dim3(64), 0, s,
-                     (const uint16_t*)qkv, nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w,
-                     eps, pos, rt, qo, (uint16_t*)k_cache, (uint16_t*)v_cache, hs);
+  float* part = (float*)ws;
   const int S = pos + 1;
   const int nch = (S + ACH - 1) / ACH;
   const int gq = nq / nkv;
@@ -233,9 +281,9 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   const dim3 grid(nch, nkv);
 #define I4_AC_CASE(G_)                                                                        \
   if (gq == G_)                                                                               \
-    hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, qo,                    \
-                       (const uint16_t*)k_cache, (const uint16_t*)v_cache, hs, S, scale, nq,  \
-                       part);                                                                 \
+    hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, (const uint16_t*)qkv,  \
+                       nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w, eps, pos, rt,   \
+                       (uint16_t*)k_cache, (uint16_t*)v_cache, hs, scale, part);            \
   else
   I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) I4_AC_CASE(8) return I4_ERR_SHAPE;
 #undef I4_AC_CASE
@@ -262,8 +310,8 @@ int i4_attn_decode(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, in
     return I4_ERR_NULL;
   if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
   if (head_dim != i4::HD || n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads ||
-      n_heads / n_kv_heads > i4::GQMAX || n_heads > 1024 || max_len < 1 || pos < 0 ||
-      pos >= max_len)
+      n_heads / n_kv_heads > i4::GQMAX || n_heads > 1024 || max_len < 1 ||
+      max_len > i4::ACH * i4::CMB || pos < 0 || pos >= max_len)
     return I4_ERR_SHAPE;
   if (((uintptr_t)qkv & 3) || ((uintptr_t)q_norm_w & 3) || ((uintptr_t)k_norm_w & 3) ||
       ((uintptr_t)k_cache & 15) || ((uintptr_t)v_cache & 15) || ((uintptr_t)out & 3))

@@ -24,12 +24,16 @@ namespace i4 {
 static constexpr int WG = 256;
 static constexpr int ROUND = 4;  // chunks per lane whose loads are in flight together
 
-template <int XT, int ST, int L>
+// NORM: each workgroup first applies the RMSNorm with weight nw to its staged x
+// row (K <= 4096), with the arithmetic of k_rmsnorm_t (same thread -> word map
+// and reduction order), so the result equals i4_rmsnorm followed by the GEMV.
+template <int XT, int ST, int L, bool NORM>
 __global__ __launch_bounds__(WG) void k_gemv_ct(
     const uint16_t* __restrict__ x, int64_t x_stride, const int32_t* __restrict__ packed,
     int64_t p_es, const void* __restrict__ scale, int64_t s_es,
     const int32_t* __restrict__ zeros, int64_t z_es, const int32_t* __restrict__ sel, int E,
-    int N, int K, int gshift, void* __restrict__ out, int ot, const void* __restrict__ bias) {
+    int N, int K, int gshift, void* __restrict__ out, int ot, const void* __restrict__ bias,
+    const uint16_t* __restrict__ nw, float eps) {
   extern __shared__ __align__(16) unsigned char lds[];
   constexpr int RPW = WG / L;
   const int C = K >> 5, KW = K >> 3;
@@ -61,6 +65,11 @@ __global__ __launch_bounds__(WG) void k_gemv_ct(
   Stager<XT> st(1, K);  // activation loads first, weight loads behind them
   auto row_of = [&](int) { return xrow; };
   st.issue(row_of, 0);
+  u32x4 gv[2];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) gv[u] = ldg16(nw + 8 * min(u * WG + (int)threadIdx.x, st.total - 1));
+  }
 
   float row = 0.f;
   for (int r0 = 0; r0 < cpl; r0 += ROUND) {
@@ -68,6 +77,25 @@ __global__ __launch_bounds__(WG) void k_gemv_ct(
 #pragma unroll
     for (int i = 0; i < ROUND; ++i) ch[i] = load_chunk<ST>(rp, min(cl + (r0 + i) * L, C - 1), gshift);
     if (r0 == 0) {
+      if constexpr (NORM) {
+        __shared__ float s_ss[WG / 64];
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          if (u * WG + (int)threadIdx.x < st.total) ss += sumsq8<XT>(st.d[u]);
+        ss = group_sum<64>(ss);
+        if ((threadIdx.x & 63) == 0) s_ss[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float r =
+            1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)K + eps);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          st.d[u].x = norm_pair<XT>(st.d[u].x, gv[u].x, r);
+          st.d[u].y = norm_pair<XT>(st.d[u].y, gv[u].y, r);
+          st.d[u].z = norm_pair<XT>(st.d[u].z, gv[u].z, r);
+          st.d[u].w = norm_pair<XT>(st.d[u].w, gv[u].w, r);
+        }
+      }
       st.commit(0, xs, sums);
       st.rest(row_of, xs, sums);
       __syncthreads();
@@ -490,22 +518,27 @@ int i4_check_weight(const i4_qweight* w, i4_qweight* norm) {
 template <int XT, int ST>
 static int launch_gemv_ct_t(const void* x, int64_t x_stride, const i4_qweight* w,
                             const int32_t* sel, int k_sel, void* out, int ot, const void* bias,
-                            hipStream_t s) {
+                            hipStream_t s, const void* nw = nullptr, float eps = 0.f) {
   const int C = w->K / 32;
   const int L = lanes_per_row(C);
   const int rpw = WG / L;
   dim3 grid((w->N + rpw - 1) / rpw, k_sel);
   const size_t lds = (size_t)w->K * 2 + (size_t)C * 8;
   const int gshift = i4_group_shift(w->group);
-#define I4_GEMV_CASE(L_)                                                                        \
+#define I4_GEMV_CASE(L_, NORM_)                                                                 \
   if (L == L_) {                                                                                \
-    hipLaunchKernelGGL((k_gemv_ct<XT, ST, L_>), grid, dim3(WG), lds, s, (const uint16_t*)x,     \
-                       x_stride, w->packed, w->packed_estride, w->scale, w->scale_estride,      \
-                       w->zeros, w->zeros_estride, sel, w->E, w->N, w->K, gshift, out, ot,      \
-                       bias);                                                                   \
+    hipLaunchKernelGGL((k_gemv_ct<XT, ST, L_, NORM_>), grid, dim3(WG), lds, s,                  \
+                       (const uint16_t*)x, x_stride, w->packed, w->packed_estride, w->scale,    \
+                       w->scale_estride, w->zeros, w->zeros_estride, sel, w->E, w->N, w->K,     \
+                       gshift, out, ot, bias, (const uint16_t*)nw, eps);                        \
     return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
   }
-  I4_GEMV_CASE(4) I4_GEMV_CASE(8) I4_GEMV_CASE(16) I4_GEMV_CASE(32) I4_GEMV_CASE(64)
+  if (nw) {  // K <= 4096: C <= 128 lanes' worth, L in 8..32
+    I4_GEMV_CASE(8, true) I4_GEMV_CASE(16, true) I4_GEMV_CASE(32, true)
+    return I4_ERR_SHAPE;
+  }
+  I4_GEMV_CASE(4, false) I4_GEMV_CASE(8, false) I4_GEMV_CASE(16, false) I4_GEMV_CASE(32, false)
+  I4_GEMV_CASE(64, false)
 #undef I4_GEMV_CASE
   return I4_ERR_SHAPE;
 }
@@ -573,6 +606,28 @@ int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w
                              stream);
   return launch_gemv_awq(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr,
                          workspace, workspace_bytes, stream);
+}
+
+int i4_rmsnorm_linear(const void* x, int x_dtype, int M, const void* norm_w, float eps,
+                      const i4_qweight* w, const void* bias, void* y, int y_dtype,
+                      hipStream_t stream) {
+  i4_qweight nw;
+  int rc = i4_check_weight(w, &nw);
+  if (rc) return rc;
+  if (!x || !y || !norm_w) return I4_ERR_NULL;
+  if (!half_dt(x_dtype) || !any_dt(y_dtype)) return I4_ERR_DTYPE;
+  if (nw.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (M < 1 || M > 65535 || nw.K > 4096 || nw.K % 8) return I4_ERR_SHAPE;
+  if (!al16(x) || !al16(norm_w)) return I4_ERR_ALIGN;
+  nw.E = 1;
+#define I4_NL_DT(XT_, ST_)                                                                   \
+  if (x_dtype == XT_ && nw.scale_dtype == ST_)                                               \
+    return launch_gemv_ct_t<XT_, ST_>(x, nw.K, &nw, nullptr, M, y, y_dtype, bias, stream,     \
+                                      norm_w, eps);
+  I4_NL_DT(I4_F16, I4_F32) I4_NL_DT(I4_F16, I4_F16) I4_NL_DT(I4_F16, I4_BF16)
+  I4_NL_DT(I4_BF16, I4_F32) I4_NL_DT(I4_BF16, I4_F16) I4_NL_DT(I4_BF16, I4_BF16)
+#undef I4_NL_DT
+  return I4_ERR_DTYPE;
 }
 
 size_t i4_linear_workspace_bytes(const i4_qweight* w, int M) {

@@ -8,6 +8,7 @@
     moe_forward    FusedPackedMoE.forward, fused_packed_moe.py:191-263
     moe_stack      Thinker[0:24] MoE stack with residual adds (clock.py:168-171)
     rmsnorm        Qwen3OmniMoeThinkerTextRMSNorm (the decoder's input_layernorm)
+    rmsnorm_linear the same norm folded into an int4 Linear (one launch)
     attn_decode    Qwen3OmniMoeThinkerTextAttention.forward between its projections,
                    one decode token with a KV cache (clock.py:164-172)
 
@@ -367,3 +368,23 @@ def attn_decode(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: torc
         tab.data_ptr(), int(pos), k_cache.data_ptr(), v_cache.data_ptr(), max_len,
         out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(dev)))
     return out
+
+
+def rmsnorm_linear(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: QWeight,
+                   bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None):
+    """y = RMSNorm(x) W^T (+ bias) in one launch (i4_rmsnorm_linear; CT weight, K <= 4096),
+    equal bit for bit to linear(rmsnorm(x, norm_w, eps), w, bias)."""
+    dev = _lib.require_device(x, norm_w, w.packed, bias)
+    if norm_w.dtype != x.dtype:
+        raise RuntimeError("the norm weight must have the activation dtype")
+    flat = x.reshape(-1, w.K).contiguous()
+    M = flat.shape[0]
+    od = out_dtype or x.dtype
+    y = torch.empty(M, w.N, dtype=od, device=dev)
+    b = None if bias is None else bias.to(od).contiguous()
+    cw = w.c()
+    _lib.check(_lib.lib().i4_rmsnorm_linear(flat.data_ptr(), _lib.half_code(x.dtype), M,
+                                            norm_w.contiguous().data_ptr(), float(eps),
+                                            ctypes.byref(cw), _lib.ptr(b), y.data_ptr(),
+                                            _lib.dtype_code(od), _lib.stream(dev)))
+    return y.view(*x.shape[:-1], w.N)

@@ -182,3 +182,30 @@ def test_thinker_decoder_step_composes(pkg, dev, ckpt):
             h = layer.moe(h, residual=h)
         assert torch.isfinite(out.float()).all()
         assert torch.equal(out, h)
+
+
+@pytest.mark.parametrize("xdt,K,M", [("bf16", 2048, 1), ("f16", 4096, 3), ("bf16", 4096, 1)])
+def test_rmsnorm_linear_equals_norm_then_linear(pkg, dev, xdt, K, M):
+    """The norm folded into the GEMV gives exactly rmsnorm() then linear(), and the norm
+    itself matches the oracle's RMSNorm."""
+    rng = np.random.default_rng(97 + K + M)
+    tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    p, s, _ = _ckpt_ct(rng, 640, K)
+    w = pkg.QWeight(t_(p, dev), t_(s, dev).to(tdt), None, "ct", 32, 640, K)
+    x = t_(make_x(rng, (M, K), xdt), dev)
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float32)).to(dev, tdt)
+    xn = pkg.rmsnorm(x, nw, 1e-6)
+    ref_xn = i4ref.rmsnorm(np.asarray(host(x), np.float64), np.asarray(host(nw), np.float64),
+                           1e-6, "bf16" if xdt == "bf16" else "f16")
+    ulp = np.abs(ref_xn) * (2.0 ** (-7 if xdt == "bf16" else -10)) + 1e-7
+    assert np.all(np.abs(np.asarray(host(xn), np.float64) - ref_xn) <= 2 * ulp)
+    want = pkg.linear(xn, w)
+    got = pkg.rmsnorm_linear(x, nw, 1e-6, w)
+    assert torch.equal(got, want)
+
+
+def _ckpt_ct(rng, N, K, G=32):
+    from tests import _gen
+
+    p, s, _ = _gen.ct_weight(rng, 1, N, K, G, sdt=np.float32)
+    return p, s, None
