@@ -22,9 +22,11 @@ kernel (the decode experts launch: routing, gate/up, SiLU, down and combine of
 the 8 experts) timed with HIP events on the stream it runs on, and a CPU baseline (the reference's CPU expert path restated in
 torch, oracle/cpu_baseline.py) timed on this host.  Extra fields time the same
 layer at M = 32 (router from weights) and M = 512 (Zipf-skewed logits) with
-their realised expert histograms, HBM and MFMA fractions, and the dequant-GEMV
+their realised expert histograms, HBM and MFMA fractions, the dequant-GEMV
 workloads (a 2048 -> 768 GEMV and the four attention projections, individually
-and back to back).
+and back to back), and the whole Thinker[0:24] decode step around the MoE stack
+(attention with a KV cache at --context positions + MoE per layer,
+thinker_decode_step).
 """
 from __future__ import annotations
 

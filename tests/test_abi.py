@@ -167,3 +167,43 @@ def test_moe_validation_codes(pkg):
     assert lib.i4_moe_forward(0x30000, 1, 1, ctypes.byref(nrm), 8, 1, 0x90000, None, 0x70000,
                               None, None, 0x100000, ws, None) == -1
     assert lib.i4_moe_stack_workspace_bytes(1, 2048, 768, 128, 8) > ws
+
+
+def test_decode_attention_validation_codes(pkg):
+    """i4_attn_decode / i4_rmsnorm / i4_rmsnorm_linear reject bad calls before any launch."""
+    from qwen3_omni_duplex_amd import _lib
+
+    lib = pkg.lib()
+    tab = (ctypes.c_float * 64)(*([1.0] * 64))
+    ws = lib.i4_attn_decode_workspace_bytes(32, 128, 4096)
+    assert ws > 0 and lib.i4_attn_decode_workspace_bytes(32, 64, 4096) == 0
+    call = lambda **kw: lib.i4_attn_decode(
+        kw.get("qkv", 0x30000), kw.get("xt", 2), kw.get("nh", 32), kw.get("nkv", 4),
+        kw.get("hd", 128), 0x40000, 0x50000, 1e-6, kw.get("tab", tab), kw.get("pos", 5),
+        kw.get("kc", 0x100000), 0x200000, kw.get("ml", 4096), 0x60000, kw.get("ws", 0x300000),
+        kw.get("wsb", ws), None)
+    assert call(qkv=None) == -1
+    assert call(tab=None) == -1
+    assert call(xt=0) == -3
+    assert call(hd=64) == -2            # head_dim is 128
+    assert call(nkv=5) == -2            # heads per kv head must divide
+    assert call(nh=64, nkv=4) == -2     # at most 8 query heads per kv head
+    assert call(pos=4096) == -2         # the row for this token must exist
+    assert call(pos=-1) == -2
+    assert call(ml=70000) == -2         # merge bound: 1024 chunks of 64
+    assert call(kc=0x100008) == -4      # caches 16-byte aligned
+    assert call(wsb=ws - 1) == -7
+    assert call(ws=0x300010) == -4
+    assert lib.i4_rmsnorm(0x30000, 1, 1, 4100, 0x40000, 1e-6, 0x50000, None) == -2
+    assert lib.i4_rmsnorm(0x30000, 0, 1, 2048, 0x40000, 1e-6, 0x50000, None) == -3
+    assert lib.i4_rmsnorm(0x30008, 1, 1, 2048, 0x40000, 1e-6, 0x50000, None) == -4
+    assert lib.i4_rmsnorm(0x30000, 1, 1, 2048, None, 1e-6, 0x50000, None) == -1
+    w = _qw(_lib, E=1, N=5120, K=2048)
+    assert lib.i4_rmsnorm_linear(0x30000, 1, 1, None, 1e-6, ctypes.byref(w), None, 0x50000, 1,
+                                 None) == -1
+    wk = _qw(_lib, E=1, N=2048, K=8192)
+    assert lib.i4_rmsnorm_linear(0x30000, 1, 1, 0x40000, 1e-6, ctypes.byref(wk), None, 0x50000, 1,
+                                 None) == -2
+    wt = _qw(_lib, E=1, N=5120, K=2048, group=128, layout=2)
+    assert lib.i4_rmsnorm_linear(0x30000, 1, 1, 0x40000, 1e-6, ctypes.byref(wt), None, 0x50000, 1,
+                                 None) == -5
