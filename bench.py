@@ -221,7 +221,7 @@ def time_decode_step(pkg, torch, dev, mods, ctx, replays):
     GQA attention over ctx cached positions, o_proj + residual) and the MoE block.  Attention
     weights are CT g32 symmetric int4 with fp16 scales (the reference checkpoint's packing),
     32 query / 4 kv heads of 128, generated on the device; cache rows [0, ctx) random.
-    Each timed region is one hipGraph of all layers at position ctx."""
+    Each timed region is one hipGraph of all layers, the position read from device memory."""
     nh, nkv, hd, gs = 32, 4, 128, 32
     gen = torch.Generator(device=dev)
     gen.manual_seed(4321)
@@ -246,15 +246,25 @@ def time_decode_step(pkg, torch, dev, mods, ctx, replays):
         layers.append(pkg.ThinkerDecoderLayer(attn, m))
     dec = pkg.ThinkerDecoder(layers)
     x = torch.randn(1, H, device=dev, generator=gen).half()
+    pos = torch.full((1,), ctx, dtype=torch.int32, device=dev)  # read by the kernels
     out = {}
-    for name, fn in (("step", lambda: dec.step(x, ctx)),
-                     ("attention", lambda: [l.attn(x, ctx) for l in layers])):
+    for name, fn in (("step", lambda: dec.step(x, pos)),
+                     ("attention", lambda: [l.attn(x, pos) for l in layers])):
         ts = graph_times(torch, fn, replays)
         us = sum(ts) / len(ts)
         out[name] = {"us_per_token": round(us, 2), "us_per_layer": round(us / len(layers), 3),
                      "us_median": round(pct(ts, 50), 2), "us_p99": round(pct(ts, 99), 2)}
-    h = dec.step(x, ctx)
+    # eager: one Python call per op (the caller's loop without a graph)
+    for _ in range(3):
+        dec.step(x, ctx)
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n_eager = 20
+    for _ in range(n_eager):
+        h = dec.step(x, ctx)
+    torch.cuda.synchronize()
+    out["step_eager"] = {"us_per_token": round((time.perf_counter() - t0) / n_eager * 1e6, 1),
+                         "timing": f"wall clock over {n_eager} eager steps"}
     if not torch.isfinite(h.float()).all():
         raise RuntimeError("the decode step produced non-finite values")
     # K and V bytes read by the attention of one layer at this context (fp16 cache)
@@ -263,7 +273,8 @@ def time_decode_step(pkg, torch, dev, mods, ctx, replays):
     return {"context": ctx, "layers": len(layers), **out,
             "attention_weight_bytes_per_layer": w_bytes + (nh * hd + 2 * nkv * hd) * (H // gs) * 2
             + H * (nh * hd // gs) * 2, "kv_bytes_per_layer": kv_bytes,
-            "timing": "hipGraph of all layers at position ctx (cache rows [0, ctx) filled), "
+            "timing": "hipGraph of all layers with the position in device memory (one graph "
+                      "serves every token), at position ctx with cache rows [0, ctx) filled, "
                       f"mean over {replays} replays"}
 
 

@@ -295,6 +295,15 @@ int    i4_attn_decode(const void* qkv, int x_dtype, int n_heads, int n_kv_heads,
                       const float* inv_freq, int pos, void* k_cache, void* v_cache,
                       int max_len, void* out, void* workspace, size_t workspace_bytes,
                       hipStream_t stream);
+/* i4_attn_decode with the position in device memory (int32, read by the kernels), so one
+ * captured hipGraph of a decode step serves every token: the launch covers all of max_len's
+ * 64-position chunks and those past *pos exit at once.  A *pos outside [0, max_len) writes
+ * nothing to the caches and NaN to out. */
+int    i4_attn_decode_at(const void* qkv, int x_dtype, int n_heads, int n_kv_heads,
+                         int head_dim, const void* q_norm_w, const void* k_norm_w, float eps,
+                         const float* inv_freq, const int32_t* pos, void* k_cache,
+                         void* v_cache, int max_len, void* out, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
 size_t i4_attn_decode_workspace_bytes(int n_heads, int head_dim, int max_len);
 
 #ifdef __cplusplus

@@ -91,6 +91,9 @@ SIGNATURES = {
     "i4_attn_decode": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                                ctypes.c_float, c_void_p, c_int, c_void_p, c_void_p, c_int,
                                c_void_p, c_void_p, c_size_t, c_void_p]),
+    "i4_attn_decode_at": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                  ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                  c_void_p, c_void_p, c_size_t, c_void_p]),
     "i4_attn_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
 }
 

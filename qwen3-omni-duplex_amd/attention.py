@@ -55,11 +55,15 @@ class ThinkerAttention(nn.Module):
         self.max_len = int(max_len)
         self.workspace = ops.Workspace()
 
-    def forward(self, h: torch.Tensor, pos: int) -> torch.Tensor:
-        """h [1, H] (one token at cache position pos) -> h + o_proj(attn(norm(h)))."""
+    def forward(self, h: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
+        """h [1, H] (one token at cache position pos) -> h + o_proj(attn(norm(h))).
+
+        pos is an int, or an int32 device tensor of one element that the kernels read (a
+        decode step captured in a hipGraph then serves every token; a position outside the
+        cache gives NaN and leaves the cache untouched)."""
         if h.numel() != h.shape[-1]:
             raise ValueError("ThinkerAttention decodes one token")
-        if not 0 <= pos < self.max_len:
+        if not isinstance(pos, torch.Tensor) and not 0 <= pos < self.max_len:
             raise ValueError(f"position {pos} outside the cache (max_len {self.max_len})")
         # input_layernorm folded into the q|k|v launch
         qkv = ops.rmsnorm_linear(h, self.input_norm_w, self.eps, self.qkv.lin.w)
@@ -79,7 +83,7 @@ class ThinkerDecoderLayer(nn.Module):
             raise ValueError("the MoE block must carry its post_attention_layernorm")
         self.attn, self.moe = attn, moe
 
-    def forward(self, h: torch.Tensor, pos: int) -> torch.Tensor:
+    def forward(self, h: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
         h = self.attn(h, pos)
         return self.moe(h, residual=h)
 
@@ -92,7 +96,7 @@ class ThinkerDecoder(nn.Module):
         super().__init__()
         self.layers = nn.ModuleList(layers)
 
-    def step(self, h: torch.Tensor, pos: int) -> torch.Tensor:
+    def step(self, h: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
         for layer in self.layers:
             h = layer(h, pos)
         return h

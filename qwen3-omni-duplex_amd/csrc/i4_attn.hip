@@ -87,9 +87,10 @@ __device__ inline u32 head_norm_rope(u32 raw, u32 wraw, float eps, int pos, cons
 template <int XT, int GQ>
 __global__ __launch_bounds__(256) void k_attn_chunk(
     const uint16_t* __restrict__ qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
-    const uint16_t* __restrict__ kn_w, float eps, int pos, RopeTab rt,
-    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t head_stride,
-    float scale, float* __restrict__ part) {
+    const uint16_t* __restrict__ kn_w, float eps, const int32_t* __restrict__ pos_dev,
+    int pos_host, int max_len, RopeTab rt, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
+    float* __restrict__ part) {
   __shared__ __align__(16) u32 s_q[GQ][HD / 2];  // rotated q pairs
   __shared__ u32 s_knew[HD / 2], s_vnew[HD / 2];
   __shared__ __align__(16) float s_p[GQ][ACH];
@@ -97,7 +98,11 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   __shared__ float s_stat[GQ][2];
   const int c = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
   const int wave = t >> 6, lane = t & 63;
+  // the position from device memory (a captured graph serves every token) or the
+  // host; a grid sized for max_len leaves the chunks past it idle
+  const int pos = pos_dev ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_host;
   const int S = pos + 1, c0 = c * ACH;
+  if (pos < 0 || pos >= max_len || c0 >= S) return;
   const bool last = c0 + ACH >= S;  // the chunk that holds pos
   const int64_t kv0 = (int64_t)g * head_stride;
   // the projection rows this workgroup rotates come first: wave w takes query
@@ -229,10 +234,18 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
 static constexpr int CMB = 1024;  // chunks per head at most (max_len <= 65536)
 template <int XT>
 __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ part, int nq,
-                                                     int nch, uint16_t* __restrict__ out) {
+                                                     const int32_t* __restrict__ pos_dev,
+                                                     int pos_host, int max_len,
+                                                     uint16_t* __restrict__ out) {
   __shared__ float s_w[CMB];
   __shared__ float s_r[2][HD / 64];
   const int h = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int pos = pos_dev ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_host;
+  if (pos < 0 || pos >= max_len) {  // no row to attend: the chunk kernel wrote nothing
+    out[(int64_t)h * HD + t] = Half<XT>::QNAN;
+    return;
+  }
+  const int nch = (pos + ACH) / ACH;
   auto at = [&](int c) { return part + ((int64_t)c * nq + h) * PSTR; };
   float m = -__builtin_inff();
   for (int c = t; c < nch; c += HD) {
@@ -270,25 +283,26 @@ size_t attn_ws(int nq, int max_len) {
 
 template <int XT>
 int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* kn_w, float eps,
-                const RopeTab& rt, int pos, void* k_cache, void* v_cache, int max_len, void* out,
-                void* ws, hipStream_t s) {
+                const RopeTab& rt, const int32_t* pos_dev, int pos, void* k_cache,
+                void* v_cache, int max_len, void* out, void* ws, hipStream_t s) {
   const int64_t hs = (int64_t)max_len * HD;
   float* part = (float*)ws;
-  const int S = pos + 1;
-  const int nch = (S + ACH - 1) / ACH;
+  // device position: every chunk of max_len is launched, those past pos exit at once
+  const int nch = ((pos_dev ? max_len : pos + 1) + ACH - 1) / ACH;
   const int gq = nq / nkv;
   const float scale = 1.0f / sqrtf((float)HD);
   const dim3 grid(nch, nkv);
 #define I4_AC_CASE(G_)                                                                        \
   if (gq == G_)                                                                               \
     hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, (const uint16_t*)qkv,  \
-                       nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w, eps, pos, rt,   \
+                       nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w, eps, pos_dev,   \
+                       pos, max_len, rt,                                                      \
                        (uint16_t*)k_cache, (uint16_t*)v_cache, hs, scale, part);            \
   else
   I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) I4_AC_CASE(8) return I4_ERR_SHAPE;
 #undef I4_AC_CASE
-  hipLaunchKernelGGL(k_attn_combine<XT>, dim3(nq), dim3(HD), 0, s, part, nq, nch,
-                     (uint16_t*)out);
+  hipLaunchKernelGGL(k_attn_combine<XT>, dim3(nq), dim3(HD), 0, s, part, nq, pos_dev, pos,
+                     max_len, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
@@ -302,29 +316,53 @@ size_t i4_attn_decode_workspace_bytes(int n_heads, int head_dim, int max_len) {
   return i4::attn_ws(n_heads, max_len);
 }
 
-int i4_attn_decode(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
-                   const void* q_norm_w, const void* k_norm_w, float eps, const float* inv_freq,
-                   int pos, void* k_cache, void* v_cache, int max_len, void* out,
-                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
+static int attn_entry(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
+                      const void* q_norm_w, const void* k_norm_w, float eps,
+                      const float* inv_freq, const int32_t* pos_dev, int pos, void* k_cache,
+                      void* v_cache, int max_len, void* out, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
   if (!qkv || !q_norm_w || !k_norm_w || !inv_freq || !k_cache || !v_cache || !out)
     return I4_ERR_NULL;
   if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
   if (head_dim != i4::HD || n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads ||
       n_heads / n_kv_heads > i4::GQMAX || n_heads > 1024 || max_len < 1 ||
-      max_len > i4::ACH * i4::CMB || pos < 0 || pos >= max_len)
+      max_len > i4::ACH * i4::CMB || (!pos_dev && (pos < 0 || pos >= max_len)))
     return I4_ERR_SHAPE;
   if (((uintptr_t)qkv & 3) || ((uintptr_t)q_norm_w & 3) || ((uintptr_t)k_norm_w & 3) ||
-      ((uintptr_t)k_cache & 15) || ((uintptr_t)v_cache & 15) || ((uintptr_t)out & 3))
+      ((uintptr_t)k_cache & 15) || ((uintptr_t)v_cache & 15) || ((uintptr_t)out & 3) ||
+      ((uintptr_t)pos_dev & 3))
     return I4_ERR_ALIGN;
   if (!workspace || workspace_bytes < i4::attn_ws(n_heads, max_len)) return I4_ERR_WORKSPACE;
   if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
   i4::RopeTab rt;
   for (int i = 0; i < i4::HD / 2; ++i) rt.inv_freq[i] = inv_freq[i];
   return x_dtype == I4_F16
-             ? i4::attn_launch<I4_F16>(qkv, n_heads, n_kv_heads, q_norm_w, k_norm_w, eps, rt, pos,
-                                       k_cache, v_cache, max_len, out, workspace, stream)
+             ? i4::attn_launch<I4_F16>(qkv, n_heads, n_kv_heads, q_norm_w, k_norm_w, eps, rt,
+                                       pos_dev, pos, k_cache, v_cache, max_len, out, workspace,
+                                       stream)
              : i4::attn_launch<I4_BF16>(qkv, n_heads, n_kv_heads, q_norm_w, k_norm_w, eps, rt,
-                                        pos, k_cache, v_cache, max_len, out, workspace, stream);
+                                        pos_dev, pos, k_cache, v_cache, max_len, out, workspace,
+                                        stream);
+}
+
+int i4_attn_decode(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
+                   const void* q_norm_w, const void* k_norm_w, float eps, const float* inv_freq,
+                   int pos, void* k_cache, void* v_cache, int max_len, void* out,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
+                    inv_freq, nullptr, pos, k_cache, v_cache, max_len, out, workspace,
+                    workspace_bytes, stream);
+}
+
+int i4_attn_decode_at(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
+                      const void* q_norm_w, const void* k_norm_w, float eps,
+                      const float* inv_freq, const int32_t* pos, void* k_cache, void* v_cache,
+                      int max_len, void* out, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream) {
+  if (!pos) return I4_ERR_NULL;
+  return attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
+                    inv_freq, pos, 0, k_cache, v_cache, max_len, out, workspace,
+                    workspace_bytes, stream);
 }
 
 }  // extern "C"

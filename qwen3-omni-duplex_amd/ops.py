@@ -339,14 +339,21 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.T
 
 
 def attn_decode(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: torch.Tensor,
-                k_norm_w: torch.Tensor, eps: float, inv_freq: torch.Tensor, pos: int,
-                k_cache: torch.Tensor, v_cache: torch.Tensor,
+                k_norm_w: torch.Tensor, eps: float, inv_freq: torch.Tensor,
+                pos: int | torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 workspace: Workspace | None = None) -> torch.Tensor:
     """Decode attention of one token (i4_attn_decode) between the q/k/v and o projections:
     qkv [n_heads + 2 n_kv_heads, head_dim] in, [n_heads * head_dim] out; appends k / v at
     row `pos` of the caches [n_kv_heads, max_len, head_dim] and attends rows [0, pos].
-    inv_freq is the host fp32 table of the rotary embedding ([head_dim / 2])."""
+    inv_freq is the host fp32 table of the rotary embedding ([head_dim / 2]).  pos may be an
+    int32 device tensor of one element (i4_attn_decode_at): the kernels read it, so a
+    captured graph serves every position."""
     dev = _lib.require_device(qkv, q_norm_w, k_norm_w, k_cache, v_cache)
+    pos_dev = None
+    if isinstance(pos, torch.Tensor):
+        if pos.device != dev or pos.dtype != torch.int32 or pos.numel() != 1:
+            raise RuntimeError("a device position is one int32 on the tensors' device")
+        pos_dev = pos
     xt = _lib.half_code(qkv.dtype)
     nkv, max_len, hd = k_cache.shape
     if k_cache.dtype != qkv.dtype or v_cache.shape != k_cache.shape or v_cache.dtype != qkv.dtype:
@@ -362,11 +369,15 @@ def attn_decode(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: torc
     nbytes = lb.i4_attn_decode_workspace_bytes(n_heads, hd, max_len)
     ws = (workspace or Workspace()).get(nbytes, dev)
     out = torch.empty(n_heads * hd, dtype=qkv.dtype, device=dev)
-    _lib.check(lb.i4_attn_decode(
-        qkv.contiguous().data_ptr(), xt, n_heads, n_kv_heads, hd,
-        q_norm_w.contiguous().data_ptr(), k_norm_w.contiguous().data_ptr(), float(eps),
-        tab.data_ptr(), int(pos), k_cache.data_ptr(), v_cache.data_ptr(), max_len,
-        out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(dev)))
+    args = (qkv.contiguous().data_ptr(), xt, n_heads, n_kv_heads, hd,
+            q_norm_w.contiguous().data_ptr(), k_norm_w.contiguous().data_ptr(), float(eps),
+            tab.data_ptr())
+    tail = (k_cache.data_ptr(), v_cache.data_ptr(), max_len, out.data_ptr(), ws.data_ptr(),
+            ws.numel(), _lib.stream(dev))
+    if pos_dev is None:
+        _lib.check(lb.i4_attn_decode(*args, int(pos), *tail))
+    else:
+        _lib.check(lb.i4_attn_decode_at(*args, pos_dev.data_ptr(), *tail))
     return out
 
 

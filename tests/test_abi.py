@@ -207,3 +207,8 @@ def test_decode_attention_validation_codes(pkg):
     wt = _qw(_lib, E=1, N=5120, K=2048, group=128, layout=2)
     assert lib.i4_rmsnorm_linear(0x30000, 1, 1, 0x40000, 1e-6, ctypes.byref(wt), None, 0x50000, 1,
                                  None) == -5
+
+    assert lib.i4_attn_decode_at(0x30000, 2, 32, 4, 128, 0x40000, 0x50000, 1e-6, tab, None,
+                                 0x100000, 0x200000, 4096, 0x60000, 0x300000, ws, None) == -1
+    assert lib.i4_attn_decode_at(0x30000, 2, 32, 4, 128, 0x40000, 0x50000, 1e-6, tab, 0x70002,
+                                 0x100000, 0x200000, 4096, 0x60000, 0x300000, ws, None) == -4

@@ -209,3 +209,85 @@ def _ckpt_ct(rng, N, K, G=32):
 
     p, s, _ = _gen.ct_weight(rng, 1, N, K, G, sdt=np.float32)
     return p, s, None
+
+
+@pytest.mark.parametrize("xdt,nh,nkv,pos", [("f16", 8, 8, 0), ("f16", 16, 4, 70), ("bf16", 8, 4, 129),
+                                            ("bf16", 4, 2, 5)])
+def test_attn_decode_head_layouts(pkg, dev, xdt, nh, nkv, pos):
+    """i4_attn_decode alone for 1, 2, 4 query heads per kv head, fp16 and bf16, against the
+    fp32 reference; cache rows [0, pos) preset, rows past pos NaN (never written rows must not
+    reach the output)."""
+    from tests import _thinker_ref
+
+    rng = np.random.default_rng(200 + nh + pos)
+    tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    hd, max_len = 128, 256
+    qkv = torch.from_numpy(rng.standard_normal((nh + 2 * nkv) * hd).astype(np.float32)).to(dev, tdt)
+    qn = torch.from_numpy(rng.uniform(0.5, 1.5, hd).astype(np.float32)).to(dev, tdt)
+    kn = torch.from_numpy(rng.uniform(0.5, 1.5, hd).astype(np.float32)).to(dev, tdt)
+    kc = torch.full((nkv, max_len, hd), float("nan"), dtype=tdt, device=dev)
+    vc = torch.full((nkv, max_len, hd), float("nan"), dtype=tdt, device=dev)
+    kc[:, :pos] = torch.randn(nkv, pos, hd, device=dev).to(tdt)
+    vc[:, :pos] = torch.randn(nkv, pos, hd, device=dev).to(tdt)
+    inv = pkg.rope_inv_freq(hd, 1e6)
+    out = pkg.attn_decode(qkv, nh, nkv, qn, kn, 1e-6, inv, pos, kc, vc)
+    # reference: the projections are the identity here, so feed q/k/v through W = I
+    x = qkv.float().cpu()
+    q, k, v = x[:nh * hd].view(nh, hd), x[nh * hd:(nh + nkv) * hd].view(nkv, hd), x[(nh + nkv) * hd:].view(nkv, hd)
+    q = _thinker_ref.rmsnorm(q, qn.float().cpu(), 1e-6)
+    k = _thinker_ref.rmsnorm(k, kn.float().cpu(), 1e-6)
+    f = pos * inv
+    emb = torch.cat((f, f))
+    q = q * emb.cos() + _thinker_ref.rotate_half(q) * emb.sin()
+    k = k * emb.cos() + _thinker_ref.rotate_half(k) * emb.sin()
+    K = torch.cat((kc[:, :pos].float().cpu(), k[:, None]), 1).repeat_interleave(nh // nkv, 0)
+    V = torch.cat((vc[:, :pos].float().cpu(), v[:, None]), 1).repeat_interleave(nh // nkv, 0)
+    p = torch.softmax(torch.einsum("hd,hsd->hs", q, K) / hd ** 0.5, -1)
+    ref = torch.einsum("hs,hsd->hd", p, V).reshape(-1).numpy()
+    got = out.float().cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert i4ref.rel_err(got, ref) <= TOL
+    # this token's k and v landed in row pos
+    assert i4ref.rel_err(kc[:, pos].float().cpu().numpy(), k.numpy()) <= TOL
+    assert torch.equal(vc[:, pos], v.to(tdt).to(dev))
+
+
+def test_decode_step_graph_with_device_position(pkg, dev, ckpt):
+    """One hipGraph of the 2-layer decode step, captured with the position in device memory,
+    replayed for positions 0..5 with new inputs (and other work between replays): every
+    replay equals an eager step at the host position, bit for bit; a position past the cache
+    gives NaN and leaves the cache as it was."""
+    root, _ = ckpt
+    ld = _ld(pkg)
+    dec = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=128)
+    twin = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=128)
+    rng = np.random.default_rng(98)
+    xs = [t_(make_x(rng, (1, H), "bf16"), dev) for _ in range(6)]
+    h_buf = xs[0].clone()
+    pos_buf = torch.zeros(1, dtype=torch.int32, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        dec.step(h_buf, pos_buf)  # warm the workspaces outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for layer in dec.layers:  # the warm-up wrote row 0: start both decoders clean
+        layer.attn.k_cache.zero_()
+        layer.attn.v_cache.zero_()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = dec.step(h_buf, pos_buf)
+    for p in range(6):
+        h_buf.copy_(xs[p])
+        pos_buf.fill_(p)
+        g.replay()
+        want = twin.step(xs[p], p)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), p
+        _ = (torch.randn(256, 256, device=dev) @ torch.randn(256, 256, device=dev)).sum().item()
+    kc = dec.layers[0].attn.k_cache.clone()
+    pos_buf.fill_(128)
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
+    assert torch.equal(dec.layers[0].attn.k_cache, kc)
