@@ -24,9 +24,9 @@ torch, oracle/cpu_baseline.py) timed on this host.  Extra fields time the same
 layer at M = 32 (router from weights) and M = 512 (Zipf-skewed logits) with
 their realised expert histograms, HBM and MFMA fractions, the dequant-GEMV
 workloads (a 2048 -> 768 GEMV and the four attention projections, individually
-and back to back), and the whole Thinker[0:24] decode step around the MoE stack
+and back to back), the whole Thinker[0:24] decode step around the MoE stack
 (attention with a KV cache at --context positions + MoE per layer,
-thinker_decode_step).
+thinker_decode_step), and the Talker's 16-bit / int8 MoE blocks (talker_moe).
 """
 from __future__ import annotations
 
@@ -278,6 +278,66 @@ def time_decode_step(pkg, torch, dev, mods, ctx, replays):
                       f"mean over {replays} replays"}
 
 
+def time_talker_moe(pkg, torch, dev, replays, n_layers=20):
+    """The Talker's MoE blocks (FusedMoE, src/duplex/streaming/fused_moe.py:40-141) at one
+    decode token: hidden 1024, 128 experts, top-6 (renormalised), expert FFN 384, shared
+    expert FFN 768 with its sigmoid gate, 20 layers chained with residual adds; experts in
+    bf16 and in the reference's int8 mode (per-output-row scales; the shared expert stays
+    bf16).  Weights ~ N(0, 0.01), router ~ N(0, 0.05), x ~ N(0, 1), bf16, generated on the
+    device.  Each timed region is one hipGraph of the 20 layers (3 launches per layer)."""
+    Ht, Et, Kt, It, Ist = 1024, 128, 6, 384, 768
+    dt = torch.bfloat16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2468)
+
+    def rnd(*shape, sd=0.01):
+        return (torch.randn(*shape, device=dev, generator=gen) * sd).to(dt)
+
+    x = rnd(1, Ht, sd=1.0)
+    base = [dict(gu=rnd(Et, 2 * It, Ht), dn=rnd(Et, Ht, It), rw=rnd(Et, Ht, sd=0.05),
+                 sgu=rnd(2 * Ist, Ht), sdn=rnd(Ht, Ist), sgw=rnd(Ht, sd=0.05))
+            for _ in range(n_layers)]
+    out = {}
+    for mode in ("bf16", "int8"):
+        layers = []
+        for b in base:
+            p = dict(b, gus=None, dns=None)
+            if mode == "int8":
+                p["gu"], p["gus"] = pkg.quantize_q8(b["gu"])
+                p["dn"], p["dns"] = pkg.quantize_q8(b["dn"])
+            layers.append(p)
+        ws = pkg.Workspace()
+        res = {}
+
+        def step():
+            h = x
+            for p in layers:
+                h = pkg.dmoe_forward(h, p["gu"], p["dn"], Kt, router_w=p["rw"],
+                                     gate_up_scale=p["gus"], down_scale=p["dns"],
+                                     shared_gate_up=p["sgu"], shared_down=p["sdn"],
+                                     shared_gate_w=p["sgw"], residual=h, workspace=ws)
+            res["h"] = h
+
+        ts = graph_times(torch, step, replays)
+        if not torch.isfinite(res["h"].float()).all():
+            raise RuntimeError("the Talker MoE chain produced non-finite values")
+        us = sum(ts) / len(ts) / n_layers
+        wb = 1 if mode == "int8" else 2
+        routed = Kt * 3 * It * Ht * wb + (Kt * (2 * It + Ht) * 2 if mode == "int8" else 0)
+        nbytes = (routed + 3 * Ist * Ht * 2 + Et * Ht * 2 + Ht * 2 + 3 * Ht * 2
+                  + 2 * (Kt * It + Ist) * 2)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[mode] = {"us_per_layer": round(us, 3), "us_per_token": round(us * n_layers, 2),
+                     "us_median_per_token": round(pct(ts, 50), 2),
+                     "bytes_per_layer": nbytes, "GBps": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return {"layers": n_layers, **out,
+            "workload": "Talker MoE block at M=1: hidden 1024, 128 experts, top-6, FFN 384, "
+                        "shared expert 768 + sigmoid gate, residual chain",
+            "timing": f"hipGraph of {n_layers} layers (router, gate|up, down launches each), "
+                      f"mean over {replays} replays"}
+
+
 def pct(vals, q):
     v = sorted(vals)
     return v[min(len(v) - 1, int(round(q / 100 * (len(v) - 1))))]
@@ -486,6 +546,8 @@ def main() -> int:
     ap.add_argument("--kernel-rounds", type=int, default=8)
     ap.add_argument("--decode-step", action=argparse.BooleanOptionalAction, default=True,
                     help="also time the whole Thinker decode step (attention + MoE per layer)")
+    ap.add_argument("--talker", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the Talker's 16-bit / int8 MoE blocks (20 layers, M=1)")
     ap.add_argument("--context", type=int, default=1024,
                     help="cached positions the decode step attends")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -660,6 +722,12 @@ def main() -> int:
         log(f"decode step (context {args.context}): {decode['step']['us_per_token']:.1f} us/token, "
             f"attention {decode['attention']['us_per_layer']:.2f} us/layer")
 
+    talker = None
+    if args.talker:
+        talker = time_talker_moe(pkg, torch, dev, args.replays)
+        log(f"Talker MoE: bf16 {talker['bf16']['us_per_layer']:.2f} us/layer, "
+            f"int8 {talker['int8']['us_per_layer']:.2f} us/layer")
+
     # ---- CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -709,6 +777,7 @@ def main() -> int:
         "other_workloads": prefill,
         "gemv": gemv,
         "thinker_decode_step": decode,
+        "talker_moe": talker,
     }
     print(json.dumps(res), flush=True)
     return 0

@@ -306,6 +306,54 @@ int    i4_attn_decode_at(const void* qkv, int x_dtype, int n_heads, int n_kv_hea
                          size_t workspace_bytes, hipStream_t stream);
 size_t i4_attn_decode_workspace_bytes(int n_heads, int head_dim, int max_len);
 
+/* ------------------------------------------------------------------------
+ * MoE block on 16-bit or int8 experts with a sigmoid-gated shared expert: the
+ * Talker's block.  Replaces FusedMoE.forward (src/duplex/streaming/fused_moe.py:
+ * 99-141), which itself stands in for transformers'
+ * Qwen3OmniMoeTalkerTextSparseMoeBlock.forward (modeling_qwen3_omni_moe.py:
+ * 2722-2733, transformers 5.15). */
+
+/* One stacked weight [E][N][K], row-major and densely stacked.  scale == NULL:
+ * data holds values in the activation dtype; else data holds int8 q and scale
+ * [E][N] (activation dtype) one scale per output row, value = q * scale -- the
+ * per-output-channel symmetric int8 of FusedMoE's q8 mode (fused_moe.py:84-94). */
+typedef struct i4_dweight {
+  const void* data;
+  const void* scale;
+  int32_t     E, N, K;
+} i4_dweight;
+
+/* One MoE block as FusedMoE stores it (fused_moe.py:59-97). */
+typedef struct i4_dmoe_weights {
+  i4_dweight  gate_up;          /* [E][2I][H]: rows [0,I) gate_proj, [I,2I) up_proj */
+  i4_dweight  down;             /* [E][H][I]; same format as gate_up               */
+  const void* router_w;         /* [E][H] in the activation dtype; may be NULL when
+                                   logits are passed                                */
+  i4_dweight  shared_gate_up;   /* [1][2Is][H]; data NULL: no shared expert         */
+  i4_dweight  shared_down;      /* [1][H][Is]                                       */
+  const void* shared_gate_w;    /* [H] (shared_expert_gate, Linear(H, 1)); NULL: 1 */
+} i4_dmoe_weights;
+
+/* out[t] = residual[t] + sum_j w[t][j] * down_e(act_e), e = sel[t][j],
+ *          act_e = silu(gate_e(x[t])) * up_e(x[t]) rounded to x_dtype
+ *          + sigmoid(shared_gate_w . x[t]) * down_s(silu(gate_s x[t]) * up_s x[t])
+ * Routing (fused_moe.py:103-108): logits = router_w x (rounded to x_dtype; or the
+ * given [T][E] logits when router_w is NULL), softmax in fp32, top-k (ties to the
+ * lower id), renormalised over the k when renorm != 0.  The shared gate's logit and
+ * sigmoid are rounded to x_dtype as the 16-bit Linear and sigmoid round them; the
+ * rest is fp32 and the output is rounded once.  residual, sel_out and w_out
+ * ([T][topk], fp32) are optional.  H % 16 == 0, 16 <= H <= 2048; I, Is multiples
+ * of 16, at most 1024 (16-bit) or 2048 (int8); E <= 512; topk <= 8, <= 7 with a
+ * shared expert; T <= 65535.  Each token streams its own experts' rows (a
+ * decode-shaped kernel; the reference gathers per token as well, fused_moe.py:121). */
+int    i4_dmoe_forward(const void* x, int x_dtype, int T, const i4_dmoe_weights* weights,
+                       int topk, int renorm, const void* logits, const void* residual,
+                       void* out, int32_t* sel_out, float* w_out, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+/* Workspace of i4_dmoe_forward (logits, routing, activations; 16-byte aligned, no
+ * initial contents).  Calls sharing one workspace must not overlap. */
+size_t i4_dmoe_workspace_bytes(int T, int E, int topk, int I, int Is);
+
 #ifdef __cplusplus
 }
 #endif

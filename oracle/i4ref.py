@@ -324,6 +324,71 @@ def moe_layer_grouped(x, sel, w, dense_gu, dense_dn, act_dtype, residual=None):
     return out
 
 
+# ---------------------------------------------------------------------------
+# Talker MoE block: FusedMoE (src/duplex/streaming/fused_moe.py:40-141), the
+# stand-in for transformers' Qwen3OmniMoeTalkerTextSparseMoeBlock
+# (modeling_qwen3_omni_moe.py:2712-2733, transformers 5.15).
+def q8_quantize(W, dtype: str):
+    """Per-output-channel symmetric int8 of fused_moe.py:84-94, with the 16-bit
+    arithmetic of the reference's tensors: every op computes in fp32 and rounds
+    to `dtype` (the weights' dtype).
+        s = (amax_k |W| clamped at 1e-8) / 127;  q = clamp(round(W / s), -127, 127)
+    W [..., N, K] holds values exactly representable in `dtype`.
+    Returns (q int8 [..., N, K], s float64 [..., N, 1])."""
+    W32 = np.asarray(W, np.float32)
+    floor = np.float32(round_half(np.array([1e-8], np.float32), dtype)[0])
+    amax = np.maximum(np.abs(W32).max(axis=-1, keepdims=True), floor)
+    s = round_half(amax / np.float32(127.0), dtype).astype(np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        r = round_half(W32 / s, dtype)                  # the 16-bit quotient
+    # an all-zero fp16 row has s = 0 (1e-8 underflows in fp16): its 0 / 0 quotients
+    # convert to q = 0, as torch's NaN -> int8 conversion gives
+    r = np.where(np.isnan(r), 0.0, r)
+    q = np.clip(np.round(r), -127, 127).astype(np.int8)  # round half to even
+    return q, s.astype(np.float64)
+
+
+def sigmoid(v):
+    return 1.0 / (1.0 + np.exp(-np.asarray(v, np.float64)))
+
+
+def dense_moe(x, sel, w, Wgu, Wdn, act_dtype: str | None, shared=None, residual=None,
+              out_dtype: str | None = None) -> np.ndarray:
+    """FusedMoE.forward after routing (fused_moe.py:110-141), fp64.
+
+    x [T, H]; sel / w [T, k]; Wgu [E, 2I, H] (gate rows first); Wdn [E, H, I].
+    shared = (Wsgu [2Is, H], Wsdn [H, Is], gate_w [H] or None) adds
+    sigmoid(gate_w . x) * down_s(silu(gate_s x) * up_s x) (fused_moe.py:136-140).
+    act_dtype rounds each activation (routed and shared), the shared gate's logit
+    and its sigmoid to the activation dtype, where the reference's 16-bit
+    tensors round them (:127, :139)."""
+    x = np.asarray(x, np.float64)
+    out = moe_layer(x, sel, w, Wgu, Wdn, act_dtype)
+    if shared is not None:
+        Wsgu, Wsdn, gate_w = shared
+        Is = Wsgu.shape[0] // 2
+        gu = x @ np.asarray(Wsgu, np.float64).T                 # [T, 2Is]
+        a = silu(gu[:, :Is]) * gu[:, Is:]
+        if act_dtype is not None:
+            a = round_half(a, act_dtype)
+        y = a @ np.asarray(Wsdn, np.float64).T                  # [T, H]
+        if gate_w is None:
+            g = np.ones((x.shape[0], 1))
+        else:
+            z = x @ np.asarray(gate_w, np.float64).reshape(-1, 1)
+            if act_dtype is not None:
+                z = round_half(z, act_dtype)
+            g = sigmoid(z)
+            if act_dtype is not None:
+                g = round_half(g, act_dtype)
+        out = out + g * y
+    if residual is not None:
+        out = out + np.asarray(residual, np.float64)
+    if out_dtype is not None:
+        out = round_half(out, out_dtype)
+    return out
+
+
 def rel_err(got, ref) -> float:
     """max |got - ref| / max |ref| -- the tolerance measure of the parity bar."""
     got = np.asarray(got, np.float64)

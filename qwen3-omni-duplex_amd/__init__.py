@@ -9,6 +9,9 @@ Drop-in replacements for thecodacus/qwen3-omni-duplex's quantized compute:
                             src/duplex/loader.py:31 (packed triplets from safetensors)
   ThinkerDecoder         <- the Thinker[0:24] decode step the clock path runs
                             (clock.py:164-172): attention with KV cache + MoE per layer
+  FusedMoE               <- src/duplex/streaming/fused_moe.py:40 (16-bit / int8
+                            experts + gated shared expert: the Talker's block)
+  fuse_moe_blocks        <- fused_moe.py:144
 all executed by the hand-written HIP kernels of libi4moe.so (C ABI in
 include/i4moe.h).  There is no fallback: without the built library every op
 raises.
@@ -18,10 +21,11 @@ from .linear import TILE_ROWS, PackedLinear, PackedQKV, QKVSlice, concat_rows, p
 from .attention import ThinkerAttention, ThinkerDecoder, ThinkerDecoderLayer, rope_inv_freq
 from .loader import (Checkpoint, load_attention, load_moe_layer, load_thinker_decoder,
                      load_thinker_layer, load_thinker_moe_stack, read_moe_layer)
+from .fused_moe import FusedMoE, fuse_moe_blocks, quantize_q8
 from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_forward, moe_gate_up,
                   moe_route_gate_up, moe_stack, route, router_logits, unpack4, unpack_nibbles,
-                  Workspace, rmsnorm, rmsnorm_linear, attn_decode)
+                  Workspace, rmsnorm, rmsnorm_linear, attn_decode, dmoe_forward)
 from .weights import QWeight, repack_awq_to_ct, repack_tile
 
 lib = _lib.lib
@@ -36,4 +40,5 @@ __all__ = [
     "Checkpoint", "read_moe_layer", "load_moe_layer", "load_thinker_moe_stack", "load_attention",
     "load_thinker_layer", "load_thinker_decoder", "rmsnorm", "rmsnorm_linear", "attn_decode",
     "ThinkerAttention", "ThinkerDecoderLayer", "ThinkerDecoder", "rope_inv_freq",
+    "FusedMoE", "fuse_moe_blocks", "quantize_q8", "dmoe_forward",
 ]

@@ -51,6 +51,21 @@ class MoeWeightsC(ctypes.Structure):
                 ("gate_up_tile", QWeightC), ("down_tile", QWeightC)]
 
 
+class DWeightC(ctypes.Structure):
+    """struct i4_dweight"""
+
+    _fields_ = [("data", c_void_p), ("scale", c_void_p), ("E", c_int32), ("N", c_int32),
+                ("K", c_int32)]
+
+
+class DmoeWeightsC(ctypes.Structure):
+    """struct i4_dmoe_weights"""
+
+    _fields_ = [("gate_up", DWeightC), ("down", DWeightC), ("router_w", c_void_p),
+                ("shared_gate_up", DWeightC), ("shared_down", DWeightC),
+                ("shared_gate_w", c_void_p)]
+
+
 # name -> (restype, argtypes); every function declared in include/i4moe.h
 SIGNATURES = {
     "i4_abi_version": (c_int, []),
@@ -95,6 +110,10 @@ SIGNATURES = {
                                   ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                   c_void_p, c_void_p, c_size_t, c_void_p]),
     "i4_attn_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "i4_dmoe_forward": (c_int, [c_void_p, c_int, c_int, POINTER(DmoeWeightsC), c_int, c_int,
+                                c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_size_t, c_void_p]),
+    "i4_dmoe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
 }
 
 _lib = None

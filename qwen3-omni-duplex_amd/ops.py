@@ -11,6 +11,8 @@
     rmsnorm_linear the same norm folded into an int4 Linear (one launch)
     attn_decode    Qwen3OmniMoeThinkerTextAttention.forward between its projections,
                    one decode token with a KV cache (clock.py:164-172)
+    dmoe_forward   FusedMoE.forward, src/duplex/streaming/fused_moe.py:99-141 (16-bit or
+                   int8 experts, sigmoid-gated shared expert: the Talker's block)
 
 Every op enqueues on torch's current stream of the tensors' device and never
 synchronises.
@@ -399,3 +401,87 @@ def rmsnorm_linear(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: QWeight
                                             ctypes.byref(cw), _lib.ptr(b), y.data_ptr(),
                                             _lib.dtype_code(od), _lib.stream(dev)))
     return y.view(*x.shape[:-1], w.N)
+
+
+def dweight_c(data: torch.Tensor, scale: torch.Tensor | None = None) -> _lib.DWeightC:
+    """struct i4_dweight of a stacked weight [E, N, K] (or one matrix [N, K]):
+    16-bit values, or int8 with one scale per output row ([E, N] or [E, N, 1])."""
+    if data.dim() == 2:
+        data = data.unsqueeze(0)
+    if data.dim() != 3 or not data.is_contiguous():
+        raise ValueError("a stacked weight is a contiguous [E, N, K] tensor")
+    E, N, K = data.shape
+    if scale is None:
+        if data.dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError(f"16-bit weights expected, got {data.dtype} (int8 needs a scale)")
+    else:
+        if data.dtype != torch.int8:
+            raise ValueError(f"scaled weights are int8, got {data.dtype}")
+        if scale.numel() != E * N or not scale.is_contiguous():
+            raise ValueError("one contiguous scale per output row ([E, N]) expected")
+    return _lib.DWeightC(data=data.data_ptr(), scale=_lib.ptr(scale), E=E, N=N, K=K)
+
+
+def dmoe_workspace_bytes(T: int, E: int, top_k: int, I: int, Is: int) -> int:
+    return _lib.lib().i4_dmoe_workspace_bytes(T, E, top_k, I, Is)
+
+
+def dmoe_forward(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, top_k: int,
+                 router_w: torch.Tensor | None = None, logits: torch.Tensor | None = None,
+                 norm_topk_prob: bool = True, gate_up_scale: torch.Tensor | None = None,
+                 down_scale: torch.Tensor | None = None,
+                 shared_gate_up: torch.Tensor | None = None,
+                 shared_down: torch.Tensor | None = None,
+                 shared_gate_w: torch.Tensor | None = None,
+                 shared_gate_up_scale: torch.Tensor | None = None,
+                 shared_down_scale: torch.Tensor | None = None,
+                 residual: torch.Tensor | None = None, return_routing: bool = False,
+                 workspace: Workspace | None = None):
+    """MoE block on 16-bit / int8 experts with an optional gated shared expert
+    (FusedMoE.forward, src/duplex/streaming/fused_moe.py:99-141):
+      out = residual + sum_j w_j down_e(silu(gate_e x) * up_e x)
+            + sigmoid(shared_gate_w . x) * down_s(silu(gate_s x) * up_s x)
+    gate_up [E, 2I, H] (gate rows first), down [E, H, I]; int8 weights come with
+    per-output-row scales in the activation dtype.  Three launches (router
+    logits, gate_up + SiLU + routing, down + combine) for any number of tokens."""
+    dev = _lib.require_device(x, gate_up, down, router_w, logits, shared_gate_up, shared_down,
+                              shared_gate_w, residual)
+    xt = _lib.half_code(x.dtype)
+    for s in (gate_up_scale, down_scale, shared_gate_up_scale, shared_down_scale):
+        if s is not None and s.dtype != x.dtype:
+            raise ValueError(f"int8 scales must be in the activation dtype {x.dtype}, got {s.dtype}")
+    for w in (gate_up, down, shared_gate_up, shared_down):
+        if w is not None and w.dtype != torch.int8 and w.dtype != x.dtype:
+            raise ValueError(f"16-bit weights must be in the activation dtype {x.dtype}")
+    if router_w is None and logits is None:
+        raise RuntimeError("need router_w or logits")
+    if (shared_gate_up is None) != (shared_down is None):
+        raise ValueError("give the shared expert's gate|up and down together")
+    shape = x.shape
+    xf = x.reshape(-1, shape[-1]).contiguous()
+    T, H = xf.shape
+    E, I = gate_up.shape[0], gate_up.shape[1] // 2
+    Is = 0 if shared_gate_up is None else shared_gate_up.shape[-2] // 2
+    rw = None if router_w is None else router_w.to(x.dtype).contiguous()
+    lg = None if router_w is not None else logits.reshape(T, E).to(x.dtype).contiguous()
+    sgw = None if shared_gate_w is None else shared_gate_w.reshape(-1).to(x.dtype).contiguous()
+    rs = None if residual is None else residual.reshape(T, H).to(x.dtype).contiguous()
+    out = torch.empty(T, H, dtype=x.dtype, device=dev)
+    sel = torch.empty(T, top_k, dtype=torch.int32, device=dev) if return_routing else None
+    wts = torch.empty(T, top_k, dtype=torch.float32, device=dev) if return_routing else None
+    dw = _lib.DmoeWeightsC(gate_up=dweight_c(gate_up, gate_up_scale),
+                           down=dweight_c(down, down_scale), router_w=_lib.ptr(rw),
+                           shared_gate_w=_lib.ptr(sgw))
+    if shared_gate_up is not None:
+        dw.shared_gate_up = dweight_c(shared_gate_up, shared_gate_up_scale)
+        dw.shared_down = dweight_c(shared_down, shared_down_scale)
+    lb = _lib.lib()
+    ws = (workspace or Workspace()).get(lb.i4_dmoe_workspace_bytes(T, E, top_k, I, Is), dev)
+    _lib.check(lb.i4_dmoe_forward(xf.data_ptr(), xt, T, ctypes.byref(dw), top_k,
+                                  int(norm_topk_prob), _lib.ptr(lg), _lib.ptr(rs),
+                                  out.data_ptr(), _lib.ptr(sel), _lib.ptr(wts), ws.data_ptr(),
+                                  ws.numel(), _lib.stream(dev)))
+    out = out.view(shape)
+    if return_routing:
+        return out, sel, wts
+    return out

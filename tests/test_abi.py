@@ -212,3 +212,49 @@ def test_decode_attention_validation_codes(pkg):
                                  0x100000, 0x200000, 4096, 0x60000, 0x300000, ws, None) == -1
     assert lib.i4_attn_decode_at(0x30000, 2, 32, 4, 128, 0x40000, 0x50000, 1e-6, tab, 0x70002,
                                  0x100000, 0x200000, 4096, 0x60000, 0x300000, ws, None) == -4
+
+
+def test_dense_moe_validation_codes(pkg):
+    """i4_dmoe_forward rejects bad calls before any launch (Talker shapes: H 1024,
+    E 128, I 384, shared I 768, top-6)."""
+    from qwen3_omni_duplex_amd import _lib
+
+    lib = pkg.lib()
+    ws = lib.i4_dmoe_workspace_bytes(1, 128, 6, 384, 768)
+    assert ws > 0 and lib.i4_dmoe_workspace_bytes(0, 128, 6, 384, 768) == 0
+
+    def dw(data, E, N, K, scale=None):
+        return _lib.DWeightC(data=data, scale=scale, E=E, N=N, K=K)
+
+    def weights(**kw):
+        w = _lib.DmoeWeightsC(
+            gate_up=kw.get("gu", dw(0x100000, 128, 768, 1024)),
+            down=kw.get("dn", dw(0x200000, 128, 1024, 384)),
+            router_w=kw.get("rw", 0x300000),
+            shared_gate_up=kw.get("sgu", dw(0x400000, 1, 1536, 1024)),
+            shared_down=kw.get("sdn", dw(0x500000, 1, 1024, 768)),
+            shared_gate_w=kw.get("sgw", 0x600000))
+        return w
+
+    def call(w=None, xt=2, T=1, k=6, x=0x30000, wsb=ws, wsp=0x700000, logits=None):
+        w = weights() if w is None else w
+        return lib.i4_dmoe_forward(x, xt, T, ctypes.byref(w), k, 1, logits, None, 0x40000, None,
+                                   None, wsp, wsb, None)
+
+    assert call(x=None) == -1
+    assert call(w=weights(rw=None)) == -1                       # no router and no logits
+    assert call(xt=0) == -3
+    assert call(T=0) == -2 and call(T=65536) == -2
+    assert call(k=8) == -2                                      # 7 slots + the shared expert
+    assert call(w=weights(gu=dw(0x100000, 128, 768, 1000))) == -2   # H % 16
+    assert call(w=weights(gu=dw(0x100000, 128, 768, 4096))) == -2   # H <= 2048
+    assert call(w=weights(dn=dw(0x200000, 128, 1024, 380))) == -2   # down K = I
+    assert call(w=weights(dn=dw(0x200000, 64, 1024, 384))) == -2    # same E
+    assert call(w=weights(gu=dw(0x100008, 128, 768, 1024))) == -4   # 16-byte rows
+    assert call(w=weights(gu=dw(0x100000, 128, 768, 1024, scale=0x800000))) == -3  # mixed
+    assert call(w=weights(sgu=dw(0x400000, 2, 1536, 1024))) == -2   # one shared expert
+    assert call(w=weights(sgu=dw(0, 1, 1536, 1024))) == -1          # shared down, no gate|up
+    assert call(w=weights(sgu=dw(0x400000, 1, 4096, 1024),
+                          sdn=dw(0x500000, 1, 1024, 2048))) == -2   # 16-bit shared I <= 1024
+    assert call(wsb=ws - 1) == -7
+    assert call(wsp=0x700008) == -4
