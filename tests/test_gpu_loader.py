@@ -291,3 +291,67 @@ def test_decode_step_graph_with_device_position(pkg, dev, ckpt):
     torch.cuda.synchronize()
     assert torch.isnan(out.float()).all()
     assert torch.equal(dec.layers[0].attn.k_cache, kc)
+
+
+def test_thinker_decoder_matches_transformers_layers(pkg, dev, ckpt):
+    """Two Thinker decoder layers read from the checkpoint run five decode steps on the
+    GPU (bf16 activations, int4 weights) against transformers' own
+    Qwen3OmniMoeThinkerTextDecoderLayer x 2 (5.15, eager, fp32 on the CPU, DynamicCache,
+    interleaved mRoPE at text positions) holding the same dequantised weights: the layer-2
+    hidden state of every step within TOL.  This pins the composition (input norm,
+    attention, residual, post-attention norm, MoE, residual) against the module the clock
+    path runs (clock.py:164-172).  The router weights are scaled by 8 on both sides (exact
+    in bf16) so that the 8th / 9th expert of a token stay far apart compared with the bf16
+    rounding of the logits, and both sides pick the same experts."""
+    M = pytest.importorskip("transformers.models.qwen3_omni_moe.modeling_qwen3_omni_moe")
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3_omni_moe.configuration_qwen3_omni_moe import (
+        Qwen3OmniMoeTextConfig,
+    )
+
+    root, truth = ckpt
+    ld = _ld(pkg)
+    dec = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=64)
+    cfg = Qwen3OmniMoeTextConfig(
+        hidden_size=H, num_attention_heads=32, num_key_value_heads=4, head_dim=128,
+        rope_scaling={"interleaved": True, "mrope_interleaved": True,
+                      "mrope_section": [24, 20, 20], "rope_type": "default", "type": "default"},
+        rope_theta=1e6, num_hidden_layers=2, num_experts=E, num_experts_per_tok=8,
+        moe_intermediate_size=I, intermediate_size=I, rms_norm_eps=1e-6, norm_topk_prob=True,
+        decoder_sparse_step=1, mlp_only_layers=[])
+    cfg._attn_implementation = "eager"
+    cfg._experts_implementation = "eager"
+    f32 = lambda a: torch.from_numpy(np.asarray(a, np.float32))
+    layers = []
+    with torch.no_grad():
+        for li, t in enumerate(truth):
+            lay = M.Qwen3OmniMoeThinkerTextDecoderLayer(cfg, li).float().eval()
+            lay.input_layernorm.weight.copy_(f32(t["in_norm"]))
+            lay.post_attention_layernorm.weight.copy_(f32(t["norm"]))
+            for n in "qkvo":
+                getattr(lay.self_attn, f"{n}_proj").weight.copy_(
+                    f32(_ckpt.dense(t["attn"][f"{n}_proj"])))
+            lay.self_attn.q_norm.weight.copy_(f32(t["attn"]["q_norm"]))
+            lay.self_attn.k_norm.weight.copy_(f32(t["attn"]["k_norm"]))
+            lay.mlp.gate.weight.copy_(f32(t["router"]) * 8)
+            dgu, ddn = _dense_fns(t)
+            for e in range(E):
+                lay.mlp.experts.gate_up_proj[e].copy_(f32(dgu(e)))
+                lay.mlp.experts.down_proj[e].copy_(f32(ddn(e)))
+            layers.append(lay)
+        for layer in dec.layers:
+            layer.moe.router_w.mul_(8)
+    rot = M.Qwen3OmniMoeThinkerTextRotaryEmbedding(cfg)
+    cache = DynamicCache()
+    rng = np.random.default_rng(97)
+    for pos in range(5):
+        x = make_x(rng, (1, H), "bf16")
+        got = host(dec.step(t_(x, dev), pos))[0]
+        h = torch.from_numpy(i4ref.bf16_bits_to_f32(x)).float().view(1, 1, H)
+        with torch.no_grad():
+            cos, sin = rot(h, torch.tensor([[pos]]))
+            for lay in layers:
+                h = lay(h, position_embeddings=(cos, sin), past_key_values=cache, use_cache=True)
+        ref = h.view(-1).double().numpy()
+        assert np.all(np.isfinite(got))
+        assert i4ref.rel_err(got, ref) <= TOL, f"pos {pos}"
