@@ -188,10 +188,10 @@ def awq_gemv_bytes(K, N):
     return K * N // 2 + (K // G) * N * 2 + (K // G) * (N // 8) * 4 + 2 * K + 2 * N
 
 
-def graph_times(torch, launches, replays):
+def graph_times(torch, launches, replays, warm=3):
     """Capture launches() (which enqueues on the current stream) in one hipGraph and replay
-    it; returns the per-replay times in microseconds, each from a pair of HIP events on the
-    replay stream."""
+    it (`warm` untimed replays first); returns the per-replay times in microseconds, each
+    from a pair of HIP events on the replay stream."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -201,7 +201,7 @@ def graph_times(torch, launches, replays):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         launches()
-    for _ in range(3):
+    for _ in range(warm):
         graph.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
@@ -318,7 +318,7 @@ def time_talker_moe(pkg, torch, dev, replays, n_layers=20):
                                      shared_gate_w=p["sgw"], residual=h, workspace=ws)
             res["h"] = h
 
-        ts = graph_times(torch, step, replays)
+        ts = graph_times(torch, step, replays, warm=50)
         if not torch.isfinite(res["h"].float()).all():
             raise RuntimeError("the Talker MoE chain produced non-finite values")
         us = sum(ts) / len(ts) / n_layers

@@ -19,8 +19,8 @@
 //                makes sigmoid(g_s . x).  SiLU gating happens in registers and
 //                only the activation, rounded to the activation dtype as
 //                fused_moe.py:127 rounds it, is written.
-//   k_d_down     two output rows per workgroup across every slot of one token
-//                (16 lanes per (row, slot)); the routing-weighted combine, the
+//   k_d_down     one output row per workgroup across every slot of one token
+//                (32 lanes per slot); the routing-weighted combine, the
 //                gated shared expert and an optional residual are summed in
 //                fixed slot order: no atomics, bit-reproducible.
 // 16-bit rows are dotted with v_dot2_f32_{f16,bf16} (exact products, fp32
@@ -146,7 +146,7 @@ __device__ inline int route_slot_v(const DGateUpArgs& a, int t, int slot) {
 template <int XT, bool I8>
 __device__ inline void gate_up_rows(const DGateUpArgs& a, const DW w, int e, uint16_t* dst,
                                     int t) {
-  constexpr int L = I8 ? 16 : 32, RPW = DWG / L, BPE = I8 ? 1 : 2;
+  constexpr int L = I8 ? 32 : 64, RPW = DWG / L, BPE = I8 ? 1 : 2;
   const int I = w.N >> 1, H = w.K;
   if ((int)blockIdx.x * RPW >= I) return;
   extern __shared__ __align__(16) unsigned char lds[];
@@ -245,11 +245,14 @@ struct DDownArgs {
   uint16_t* out;             // [T][H]
 };
 
-// grid (ceil(H / 2), T).  Lane group g (16 lanes) computes row 2 bx + g / 8 of
-// slot g % 8 (slot topk: the shared expert; higher slots idle).
+// grid (H, T).  Lane group g (32 lanes) computes row bx of slot g (slot topk:
+// the shared expert; higher slots idle).  Lane counts here and in k_d_gate_up
+// (one wave per 16-bit row pair, half a wave per int8 pair) were picked by a
+// sweep at the Talker's shapes: within 0.5 us of each other per block for bf16,
+// 1 us faster than half as many lanes for int8.
 template <int XT, bool RI8, bool SI8>
 __global__ __launch_bounds__(DWG) void k_d_down(DDownArgs a) {
-  constexpr int L = 16, RW = 2, NSG = 8;
+  constexpr int L = 32, RW = 1, NSG = 8;
   constexpr bool F32 = RI8 || SI8;
   const int t = blockIdx.y, topk = a.topk;
   const int I = a.dn.K, H = a.dn.N;
@@ -367,12 +370,12 @@ DW to_dw(const i4_dweight& w) {
 template <int XT, bool RI8, bool SI8>
 int dmoe_launch(const DGateUpArgs& ga, const DDownArgs& da, int T, int H, hipStream_t s) {
   const int I = ga.gu.N >> 1, Is = ga.sgu.data ? ga.sgu.N >> 1 : 0;
-  const int rpw_r = RI8 ? DWG / 16 : DWG / 32, rpw_s = SI8 ? DWG / 16 : DWG / 32;
+  const int rpw_r = RI8 ? DWG / 32 : DWG / 64, rpw_s = SI8 ? DWG / 32 : DWG / 64;
   const int bx = max((I + rpw_r - 1) / rpw_r, Is ? (Is + rpw_s - 1) / rpw_s : 0);
   hipLaunchKernelGGL((k_d_gate_up<XT, RI8, SI8>), dim3(bx, ga.topk + 1, T), dim3(DWG),
                      stage_bytes(H, RI8 || SI8), s, ga);
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
-  hipLaunchKernelGGL((k_d_down<XT, RI8, SI8>), dim3((H + 1) / 2, T), dim3(DWG),
+  hipLaunchKernelGGL((k_d_down<XT, RI8, SI8>), dim3(H, T), dim3(DWG),
                      stage_bytes(da.topk * I + Is, RI8 || SI8), s, da);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
