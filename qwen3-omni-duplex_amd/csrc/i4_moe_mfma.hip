@@ -513,9 +513,9 @@ static int mfma_t(bool small, int max_entries, const void* src, int src_rows, in
                      dim3(n_out / (cols * NB_ / MF_NB), max_entries), dim3(256), 0, s,          \
                      (const uint16_t*)src, (u32)src_bytes, topk, ent, nent, perm, w, I,         \
                      (uint16_t*)act, ys)
-  // small entries: one m-block and twice the n-blocks per wave when the rows allow
-  if (small && n_out % (2 * cols) == 0) I4_MF_LAUNCH(2 * MF_NB, 1);
-  else if (small) I4_MF_LAUNCH(MF_NB, 1);
+  // small entries: one m-block; MF_NB n-blocks per wave (twice the n-blocks, half the
+  // workgroups, was 5 % slower per M = 32 layer and 2 % per M = 512 layer)
+  if (small) I4_MF_LAUNCH(MF_NB, 1);
   else I4_MF_LAUNCH(MF_NB, MF_TOK / 16);
 #undef I4_MF_LAUNCH
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
