@@ -90,13 +90,17 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
     const uint16_t* __restrict__ kn_w, float eps, const int32_t* __restrict__ pos_dev,
     int pos_host, int max_len, RopeTab rt, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
-    float* __restrict__ part) {
+    float* __restrict__ part, int gsplit) {
   __shared__ __align__(16) u32 s_q[GQ][HD / 2];  // rotated q pairs
   __shared__ u32 s_knew[HD / 2], s_vnew[HD / 2];
   __shared__ __align__(16) float s_p[GQ][ACH];
   __shared__ float s_red[4][GQ][HD];
   __shared__ float s_stat[GQ][2];
-  const int c = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
+  // kv head g; this workgroup's GQ query heads start at q0 (gsplit workgroups share a
+  // kv head, each with GQ of its GQ * gsplit query heads)
+  const int c = blockIdx.x, g = blockIdx.y / gsplit, t = threadIdx.x;
+  const int q0 = g * GQ * gsplit + (blockIdx.y % gsplit) * GQ;
+  const bool writer = blockIdx.y % gsplit == 0;  // appends this token's k / v
   const int wave = t >> 6, lane = t & 63;
   // the position from device memory (a captured graph serves every token) or the
   // host; a grid sized for max_len leaves the chunks past it idle
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   u32 qraw[QPW], qw = *(const u32*)(qn_w + 2 * lane), kraw = 0, kwn = 0, vraw = 0;
 #pragma unroll
   for (int i = 0; i < QPW; ++i)
-    qraw[i] = *(const u32*)(qkv + (int64_t)(g * GQ + min(wave + 4 * i, GQ - 1)) * HD + 2 * lane);
+    qraw[i] = *(const u32*)(qkv + (int64_t)(q0 + min(wave + 4 * i, GQ - 1)) * HD + 2 * lane);
   if (last && wave == 0) {
     kraw = *(const u32*)(qkv + (int64_t)(nq + g) * HD + 2 * lane);
     vraw = *(const u32*)(qkv + (int64_t)(nq + nkv + g) * HD + 2 * lane);
@@ -138,8 +142,10 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
     const u32 kn = head_norm_rope<XT>(kraw, kwn, eps, pos, rt);
     s_knew[lane] = kn;
     s_vnew[lane] = vraw;
-    *(u32*)(k_cache + kv0 + (int64_t)pos * HD + 2 * lane) = kn;
-    *(u32*)(v_cache + kv0 + (int64_t)pos * HD + 2 * lane) = vraw;
+    if (writer) {
+      *(u32*)(k_cache + kv0 + (int64_t)pos * HD + 2 * lane) = kn;
+      *(u32*)(v_cache + kv0 + (int64_t)pos * HD + 2 * lane) = vraw;
+    }
   }
   __syncthreads();
   if (last && c0 + j >= pos) {  // this token's key replaces the row that was loaded
@@ -218,7 +224,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   for (int i = t; i < GQ * HD; i += 256) {
     const int h = i / HD, d = i % HD;
     const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
-    float* dst = part + ((int64_t)c * nq + g * GQ + h) * PSTR;
+    float* dst = part + ((int64_t)c * nq + q0 + h) * PSTR;
     dst[4 + d] = o;
     if (d == 0) {
       dst[0] = s_stat[h][0];
@@ -291,15 +297,19 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   const int nch = ((pos_dev ? max_len : pos + 1) + ACH - 1) / ACH;
   const int gq = nq / nkv;
   const float scale = 1.0f / sqrtf((float)HD);
-  const dim3 grid(nch, nkv);
+  // 8 query heads per kv head run as two workgroups of 4 (shorter score and P V
+  // chains per workgroup; both load the chunk's K / V): the Thinker's decode step
+  // took 829 instead of 874 us per token at context 1024, four workgroups of 2 849
+  const int gsplit = gq == 8 ? 2 : 1;
+  const dim3 grid(nch, nkv * gsplit);
 #define I4_AC_CASE(G_)                                                                        \
-  if (gq == G_)                                                                               \
+  if (gq / gsplit == G_)                                                                      \
     hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, (const uint16_t*)qkv,  \
                        nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w, eps, pos_dev,   \
                        pos, max_len, rt,                                                      \
-                       (uint16_t*)k_cache, (uint16_t*)v_cache, hs, scale, part);            \
+                       (uint16_t*)k_cache, (uint16_t*)v_cache, hs, scale, part, gsplit);    \
   else
-  I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) I4_AC_CASE(8) return I4_ERR_SHAPE;
+  I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) return I4_ERR_SHAPE;
 #undef I4_AC_CASE
   hipLaunchKernelGGL(k_attn_combine<XT>, dim3(nq), dim3(HD), 0, s, part, nq, pos_dev, pos,
                      max_len, (uint16_t*)out);
