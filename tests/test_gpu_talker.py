@@ -253,3 +253,25 @@ def test_dmoe_rejects_cpu_tensors(pkg):
         pkg.dmoe_forward(x, torch.zeros(E, 2 * I, H, dtype=torch.bfloat16),
                          torch.zeros(E, H, I, dtype=torch.bfloat16), K,
                          router_w=torch.zeros(E, H, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("T,q8", [(64, False), (300, True)])
+def test_dmoe_tokens_are_independent(pkg, dev, T, q8):
+    """Size-independent property at batch sizes the oracle would take long on: every token
+    of a T-token call equals the same token run alone, bit for bit (per-token routing
+    through the batched router -- one-token tiles up to 64 tokens, 8-token tiles above --
+    gives the single-token router's logits, and each token streams its own experts)."""
+    S = _stacks(dev, torch.bfloat16, seed=21)
+    gu, dn, gus, dns = S["gu"], S["dn"], None, None
+    if q8:
+        gu, gus = pkg.quantize_q8(gu)
+        dn, dns = pkg.quantize_q8(dn)
+    g = torch.Generator(device=dev).manual_seed(22)
+    x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+    kw = dict(router_w=S["rw"], gate_up_scale=gus, down_scale=dns, shared_gate_up=S["sgu"],
+              shared_down=S["sdn"], shared_gate_w=S["sgw"])
+    out = pkg.dmoe_forward(x, gu, dn, K, **kw)
+    for t in (0, 1, T // 2, T - 2, T - 1):
+        one = pkg.dmoe_forward(x[t:t + 1].contiguous(), gu, dn, K, **kw)
+        assert torch.equal(out[t:t + 1], one), f"token {t} of {T}"
+    assert torch.isfinite(out.float()).all()
