@@ -30,11 +30,13 @@ namespace i4 {
 static constexpr int WG = 256;
 static constexpr int TCHUNK = 1024;  // tokens handled by one pass of the pipeline
 
-// out[t] = residual[t] + sum_j w[t][j] ys[t][j] in slot order.  KMAX >= topk
-// slots are loaded unconditionally (indices clamped) so that all loads of a
-// thread are in flight together.
+// out[t] = residual[t] + sum_j w[t][j] ys[t][j] in slot order, ys [T * topk][H]
+// in the activation dtype (each expert's output rounded as the reference rounds
+// it, fused_packed_moe.py:262; half the bytes of fp32 through HBM), the sum in
+// fp32.  KMAX >= topk slots are loaded unconditionally (indices clamped) so that
+// all loads of a thread are in flight together.
 template <int XT, int KMAX>
-__global__ __launch_bounds__(WG) void k_moe_combine(const float* __restrict__ ys,
+__global__ __launch_bounds__(WG) void k_moe_combine(const uint16_t* __restrict__ ys,
                                                     const float* __restrict__ wts,
                                                     const int32_t* __restrict__ sel, int T,
                                                     int topk, int E, int H,
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(WG) void k_moe_combine(const float* __restrict__ ys
     const int s = t * topk + min(j, topk - 1);
     sl[j] = sel[s];
     wv[j] = wts[s];
-    yv[j] = ys[(int64_t)s * H + n];
+    yv[j] = Half<XT>::to_f32(ys[(int64_t)s * H + n]);
   }
   float y = 0.f;
 #pragma unroll
@@ -227,7 +229,7 @@ MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
   m.sel = (int32_t*)take(Tk * 4);
   m.w = (float*)take(Tk * 4);
   m.act = (uint16_t*)take(Tk * I * 2);
-  m.ys = Tc > 1 ? (float*)take(Tk * H * 4) : nullptr;
+  m.ys = Tc > 1 ? (float*)take(Tk * H * 2) : nullptr;  // [Tk][H] in the activation dtype
   m.perm = (int32_t*)take(Tk * 4);
   m.entries = (int4*)take((E + Tk) * sizeof(int4));
   m.n_entries = (int*)take(4);
@@ -427,8 +429,8 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   const int64_t tot = (int64_t)T * H;
   dim3 cg((unsigned)((tot + WG - 1) / WG));
 #define I4_COMB_CASE(XT_, KM_)                                                                 \
-  hipLaunchKernelGGL((k_moe_combine<XT_, KM_>), cg, dim3(WG), 0, s, ws.ys, wts, sel, T, topk, E, \
-                     H, (const uint16_t*)residual, (uint16_t*)out)
+  hipLaunchKernelGGL((k_moe_combine<XT_, KM_>), cg, dim3(WG), 0, s, (const uint16_t*)ws.ys, wts, \
+                     sel, T, topk, E, H, (const uint16_t*)residual, (uint16_t*)out)
   if (xt == I4_F16) {
     if (topk <= 8) I4_COMB_CASE(I4_F16, 8);
     else I4_COMB_CASE(I4_F16, 16);

@@ -490,7 +490,9 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
         } else {
           const int64_t o = (int64_t)perm[pos0 + m] * w.N + blockIdx.x * COLS + 16 * NB * wave + ln;
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) ys[o + 16 * nb] = ev ? res[mb][nb][i] : __builtin_nanf("");
+          // the expert's output in the activation dtype (k_moe_combine sums the slots)
+          for (int nb = 0; nb < NB; ++nb)
+            ((uint16_t*)ys)[o + 16 * nb] = Half<XT>::from_f32(ev ? res[mb][nb][i] : __builtin_nanf(""));
         }
       }
     }
