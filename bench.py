@@ -520,7 +520,22 @@ def routing_stats(sels, per_expert_bytes, extra_bytes):
             "bytes": int(d * per_expert_bytes + extra_bytes)}
 
 
+def cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
 def cpu_baseline(torch, first, xs, seconds):
+    """The reference's CPU paths restated in torch (oracle/cpu_baseline.py), timed on this host
+    over bounded samples: the M = 1 MoE layer on all threads (the reported value) and on one
+    thread, the M = 32 layer, and reference_gemv for the single 2048 -> 768 GEMV and the four
+    attention projections back to back.  The weights are layer 0's (MoE) and fresh seeded AWQ
+    tensors of the workload's shapes (GEMVs); `seconds` bounds the whole leg."""
     from oracle import cpu_baseline as cb
 
     g, u, d, wr = first
@@ -528,16 +543,56 @@ def cpu_baseline(torch, first, xs, seconds):
     gate, up, down = host(g), host(u), host(d)
     router = wr.detach().float().cpu()
     x = torch.stack([t.detach().float().cpu().reshape(-1) for t in xs[:64]])
-    med, reps = cb.time_layer(x, router, gate, up, down, seconds=seconds, top_k=TOPK, group=G)
-    model = ""
+    threads = torch.get_num_threads()
+    med, reps = cb.time_layer(x, router, gate, up, down, seconds=0.35 * seconds, top_k=TOPK,
+                              group=G)
+    torch.set_num_threads(1)
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return med * 1e6, reps, torch.get_num_threads(), model or platform.processor()
+        med1, reps1 = cb.time_layer(x, router, gate, up, down, seconds=0.15 * seconds, top_k=TOPK,
+                                    group=G)
+    finally:
+        torch.set_num_threads(threads)
+    x32 = [x[i:i + 32] for i in (0, 32)]
+    med32, reps32 = cb.time_calls(
+        lambda i: cb.moe_layer(x32[i % 2], router, gate, up, down, TOPK, G), 0.25 * seconds, 2)
+
+    gen = torch.Generator().manual_seed(5)
+
+    def awq(K, N):
+        return (torch.randint(-2**31, 2**31, (K, N // 8), dtype=torch.int32, generator=gen),
+                torch.randint(-2**31, 2**31, (K // G, N // 8), dtype=torch.int32, generator=gen),
+                (torch.rand(K // G, N, generator=gen) * 0.018 + 0.002).half())
+
+    c1 = awq(H, I)
+    xk = torch.randn(4, 4096, generator=gen).half()
+    med_c1, reps_c1 = cb.time_calls(lambda i: cb.gemv(xk[i % 4, :H], *c1, group=G),
+                                    0.1 * seconds)
+    proj = {"q": awq(2048, 4096), "k": awq(2048, 512), "v": awq(2048, 512), "o": awq(4096, 2048)}
+
+    def attn(i):
+        xi = xk[i % 4]
+        for name in ("q", "k", "v"):
+            cb.gemv(xi[:2048], *proj[name], group=G)
+        cb.gemv(xi, *proj["o"], group=G)
+
+    med_c2, reps_c2 = cb.time_calls(attn, 0.15 * seconds)
+    model = cpu_model_name()
+    return {
+        "value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+        "sample": f"{reps} M=1 MoE layers (layer 0 weights, distinct inputs), median; torch fp32 "
+                  f"on {threads} threads of {model}",
+        "cpu_model": model, "host_threads": os.cpu_count(),
+        "one_thread": {"us_per_layer": round(med1 * 1e6, 1), "reps": reps1},
+        "configs": {
+            "single_gemv_2048x768": {"us": round(med_c1 * 1e6, 1), "reps": reps_c1,
+                                     "path": "reference_gemv: fp32 dequant + matmul"},
+            "attention_qkvo_back_to_back": {"us": round(med_c2 * 1e6, 1), "reps": reps_c2,
+                                            "path": "reference_gemv x 4 (q, k, v, o)"},
+            "moe_layer_M32": {"us_per_layer": round(med32 * 1e6, 1), "reps": reps32,
+                              "tokens_per_s": round(32 / med32, 1),
+                              "path": "CPU expert path, per token (fused_packed_moe.py:202-220)"},
+        },
+    }
 
 
 def main() -> int:
@@ -553,7 +608,8 @@ def main() -> int:
                     help="also time the Talker's 16-bit / int8 MoE blocks (20 layers, M=1)")
     ap.add_argument("--context", type=int, default=1024,
                     help="cached positions the decode step attends")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="bound on the CPU baseline leg (all of its samples together)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill", action=argparse.BooleanOptionalAction, default=True,
                     help="also time the M=32 and M=512 workloads (reported as extra fields)")
@@ -742,11 +798,9 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log(f"CPU baseline: ~{args.cpu_seconds:.0f} s sample")
-        us_cpu, reps, cores, model = cpu_baseline(torch, first, xs, args.cpu_seconds)
-        cpu = {"value": round(us_cpu, 1), "unit": "us/layer", "cores": cores, "kind": "port",
-               "sample": f"{reps} M=1 MoE layers (layer 0 weights, distinct inputs), median; "
-                         f"torch fp32 on {cores} threads of {model}"}
-        log(f"CPU: {us_cpu:.0f} us/layer")
+        cpu = cpu_baseline(torch, first, xs, args.cpu_seconds)
+        log(f"CPU: {cpu['value']:.0f} us/layer ({cpu['cores']} threads), "
+            f"{cpu['one_thread']['us_per_layer']:.0f} us/layer on one thread")
 
     res = {
         "metric": "µs per int4 Thinker MoE layer at M=1; achieved HBM GB/s as % of MI355X peak",

@@ -67,7 +67,7 @@
 extern "C" {
 #endif
 
-#define I4_ABI_VERSION 3
+#define I4_ABI_VERSION 4
 
 /* status codes */
 #define I4_OK               0
@@ -79,7 +79,9 @@ extern "C" {
 #define I4_ERR_GROUP       -6  /* group size not a multiple of 32                */
 #define I4_ERR_WORKSPACE   -7  /* workspace missing or too small                 */
 #define I4_ERR_LAUNCH      -8  /* the HIP runtime rejected a kernel launch       */
-#define I4_ERR_STRIDE      -9  /* expert stride smaller than one expert          */
+#define I4_ERR_STRIDE      -9  /* expert or row stride smaller than its data     */
+#define I4_ERR_HANDOFF    -10  /* a decode wait for activations gave up (NaN out) */
+#define I4_ERR_SCRATCH    -11  /* call needs more than the static scratch holds   */
 
 /* element types */
 #define I4_F32  0
@@ -141,8 +143,13 @@ const char* i4_strerror(int code);
  * x_stride = 0 shares one activation row across the selected experts (the
  * gate_up call, fused_packed_moe.py:255); x_stride = K gives each expert its
  * own row (the down call, fused_packed_moe.py:261).  Accumulation is fp32.
- * out is [k_sel][N] in out_dtype (I4_F32 matches the reference).  The AWQ
- * layout needs a workspace of i4_dq_gemv_workspace_bytes(); CT needs none. */
+ * out is [k_sel][N] in out_dtype (I4_F32 matches the reference).  Either
+ * layout runs in one launch; i4_dq_gemv_workspace_bytes() returns 0 and the
+ * workspace arguments are kept for callers written against it (they may be
+ * NULL / 0).  AWQ scales must be 16-byte aligned (also between experts).
+ * A group at least as long as K is one scale per output row (the per-channel
+ * branch of quant/dequant.py:75-76); a K that is not a multiple of the group
+ * leaves a short last group (NG = ceil(K / group) scales per row). */
 int    i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride,
                   const i4_qweight* w, const int32_t* sel, int k_sel,
                   void* out, int out_dtype,
@@ -236,6 +243,33 @@ int    i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* w
  * intermediate activations; no state is kept between calls).  Calls that
  * share one workspace must not overlap. */
 size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
+
+/* Byte offset, inside the workspace of i4_moe_forward / i4_moe_stack_forward
+ * with these sizes, of an int32 status word that every call rewrites on the
+ * device: I4_OK, or I4_ERR_HANDOFF when a workgroup of the single-launch decode
+ * layer gave up waiting for the activations of its own launch (its output rows
+ * are then NaN).  The host reads it after the stream has finished the call; a
+ * stack call reports a give-up in any of its layers.  The wait only ends that
+ * way if the launch's workgroups are not dispatched in block order, which the
+ * wait assumes (no reference counterpart: the reference faults instead,
+ * src/duplex/streaming/fused_packed_moe.py:227-229). */
+size_t i4_moe_status_offset(int T, int H, int I, int E, int topk);
+
+/* The consumer half of the single-launch decode layer on its own: the down
+ * workgroups of i4_moe_forward's T = 1 experts launch rank the [E_r] logits
+ * (as fused_packed_moe.py:195-199 does), wait for act [topk][I] (x_dtype,
+ * slot order of the ranking) by polling it until no value still holds the
+ * pending pattern 0xFFFF, then compute out = residual + sum_j w_j
+ * down_{sel_j}(act_j) (fused_packed_moe.py:261-262).  Each workgroup polls at
+ * most max_polls times; one that gives up writes NaN to its output rows and
+ * I4_ERR_HANDOFF to *status (int32, device; I4_OK is written first by the
+ * caller or left from before: the kernel only ever stores the failure).  For
+ * activations produced by another launch running concurrently, and for
+ * testing the bounded wait from the host.  CT down weights, topk <= 8. */
+int    i4_moe_down_wait(const void* act, int x_dtype, const i4_qweight* down,
+                        const void* logits, int E_r, int topk, int renorm,
+                        const void* residual, void* out, int32_t* status, int max_polls,
+                        hipStream_t stream);
 
 /* The two expert stages of one decode token with routing already known --
  * the body of the reference's per-token loop (fused_packed_moe.py:231-263):

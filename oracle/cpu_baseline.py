@@ -1,11 +1,14 @@
-"""Timed CPU baseline of one int4 MoE layer -- TEST/BENCH INFRASTRUCTURE ONLY.
+"""Timed CPU baselines -- TEST/BENCH INFRASTRUCTURE ONLY.
 
 Only bench.py's cpu_baseline leg (and tests) may use this; the product never
-does.  It restates the reference's CPU expert path,
-src/duplex/streaming/fused_packed_moe.py:202-220, in torch on the host:
-  route in fp32 (:195-199), then per token and selected expert dequantise the
-  packed gate/up/down weights to fp32 (:213,217 via _dequant :183-189),
-  matmul -> silu(g) * u -> matmul, and sum w_j * y_j (:214-219).
+does.  Two reference paths are restated in torch on the host:
+  - moe_layer: the reference's CPU expert path,
+    src/duplex/streaming/fused_packed_moe.py:202-220: route in fp32 (:195-199),
+    then per token and selected expert dequantise the packed gate/up/down
+    weights to fp32 (:213,217 via _dequant :183-189), matmul -> silu(g) * u ->
+    matmul, and sum w_j * y_j (:214-219);
+  - gemv: reference_gemv, src/duplex/streaming/triton_dequant_gemv.py:116-122:
+    dequantise the selected weight to fp32, then one matmul with x.
 The weights are in the workload's AutoAWQ g128 format (qweight [K, N/8] with
 nibble order 0,2,4,6,1,3,5,7, qzeros, fp16 scales) instead of the
 checkpoint's symmetric group-32 format; only the unpack differs.
@@ -55,6 +58,25 @@ def moe_layer(x, router_w, gate, up, down, top_k=8, group=128):
             y += w[t, j] * (act @ awq_dequant(down[0][e], down[1][e], down[2][e], group))
         outs.append(y)
     return torch.stack(outs)
+
+
+def gemv(x, qweight, qzeros, scales, group=128):
+    """reference_gemv on one AWQ weight: y [N] = dequant(W)^T-form product with x [K], fp32."""
+    return x.float() @ awq_dequant(qweight, qzeros, scales, group)
+
+
+def time_calls(fn, seconds=2.0, min_reps=3):
+    """Median seconds of fn(i) over a bounded sample (at least min_reps calls)."""
+    times = []
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end or len(times) < min_reps:
+        t0 = time.perf_counter()
+        fn(i)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    times.sort()
+    return times[len(times) // 2], len(times)
 
 
 def time_layer(x, router_w, gate, up, down, seconds=10.0, top_k=8, group=128, min_reps=3):

@@ -35,10 +35,8 @@ def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
     """Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet)."""
     u = np.asarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
     rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
-    out = rounded.astype(np.uint16)
     nan = np.isnan(np.asarray(a, dtype=np.float32))
-    out[nan] = 0x7FC0
-    return out
+    return np.where(nan, np.uint16(0x7FC0), rounded.astype(np.uint16)).astype(np.uint16)
 
 
 def round_half(a: np.ndarray, dtype: str) -> np.ndarray:
@@ -277,8 +275,12 @@ def silu(v: np.ndarray) -> np.ndarray:
 
 
 def moe_layer(x, sel, w, Wgu, Wdn, act_dtype: str | None, residual=None,
-              out_dtype: str | None = None) -> np.ndarray:
-    """x [T, H]; sel/w [T, k]; Wgu dense [E, 2I, H] (gate rows first); Wdn dense [E, H, I]."""
+              out_dtype: str | None = None, y_dtype: str | None = None) -> np.ndarray:
+    """x [T, H]; sel/w [T, k]; Wgu dense [E, 2I, H] (gate rows first); Wdn dense [E, H, I].
+
+    y_dtype rounds each expert's output before the routing-weighted sum, the
+    reference's y.to(x.dtype) (fused_packed_moe.py:262); the sum itself stays
+    float64 here (the reference's bf16 product and sum are not modelled)."""
     x = np.asarray(x, np.float64)
     T = x.shape[0]
     I = Wgu.shape[1] // 2
@@ -291,7 +293,10 @@ def moe_layer(x, sel, w, Wgu, Wdn, act_dtype: str | None, residual=None,
             a = silu(gu[:I]) * gu[I:]
             if act_dtype is not None:
                 a = round_half(a, act_dtype)
-            out[t] += w[t, j] * (Wdn[e] @ a)
+            y = Wdn[e] @ a
+            if y_dtype is not None:
+                y = round_half(y, y_dtype)
+            out[t] += w[t, j] * y
     if residual is not None:
         out = out + np.asarray(residual, np.float64)
     if out_dtype is not None:
@@ -299,7 +304,8 @@ def moe_layer(x, sel, w, Wgu, Wdn, act_dtype: str | None, residual=None,
     return out
 
 
-def moe_layer_grouped(x, sel, w, dense_gu, dense_dn, act_dtype, residual=None):
+def moe_layer_grouped(x, sel, w, dense_gu, dense_dn, act_dtype, residual=None,
+                      y_dtype: str | None = None):
     """Same as moe_layer, computed per expert over all its tokens (for large T).
 
     dense_gu(e) / dense_dn(e) return expert e's dense matrices on demand so only
@@ -318,6 +324,8 @@ def moe_layer_grouped(x, sel, w, dense_gu, dense_dn, act_dtype, residual=None):
         if act_dtype is not None:
             a = round_half(a, act_dtype)
         y = a @ dense_dn(int(e)).T             # [n, H]
+        if y_dtype is not None:
+            y = round_half(y, y_dtype)
         np.add.at(out, tt, w[tt, jj][:, None] * y)
     if residual is not None:
         out = out + np.asarray(residual, np.float64)

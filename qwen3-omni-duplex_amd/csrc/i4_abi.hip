@@ -17,6 +17,10 @@ const char* i4_strerror(int code) {
     case I4_ERR_WORKSPACE: return "i4: workspace missing or too small";
     case I4_ERR_LAUNCH: return "i4: the HIP runtime rejected a kernel launch";
     case I4_ERR_STRIDE: return "i4: expert or row stride smaller than the data it spans";
+    case I4_ERR_HANDOFF:
+      return "i4: a decode workgroup gave up waiting for its launch's activations (NaN rows)";
+    case I4_ERR_SCRATCH:
+      return "i4: the call needs more scratch than the library's static buffer holds";
     default: return "i4: unknown error code";
   }
 }

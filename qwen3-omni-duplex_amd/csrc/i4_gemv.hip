@@ -2,7 +2,8 @@
 //
 //   k_gemv_ct      gathered GEMV on the compressed-tensors layout
 //                  (replaces _dq_gemv_kernel, triton_dequant_gemv.py:32-82)
-//   k_gemv_awq     split-K GEMV straight on AutoAWQ packing + k_reduce_split
+//   k_gemv_awq     GEMV straight on AutoAWQ packing, one launch (K reduced
+//                  inside each workgroup)
 //   k_unpack       raw nibbles in logical [E][N][K] order (unpack4,
 //                  fused_packed_moe.py:54-65)
 //   k_dequant      dense (q - z) * s (FusedPackedMoE._dequant, :183-189)
@@ -125,138 +126,118 @@ __global__ __launch_bounds__(WG) void k_gemv_ct(
 }
 
 // ---------------------------------------------------------------------------
-// AWQ split-K GEMV.  Thread t of a workgroup owns column word cw = tile*32 +
-// (t & 31) (8 output columns) and k-slot t >> 5; the workgroup covers rows
-// [k0, k0 + KS) of the weight.  A k-slot processes row pairs (k, k+1); the
-// two words are merged byte-wise with v_perm_b32 so that every column gets a
-// (row k, row k+1) pair for v_dot2.  Partial sums go to part[split][j][N].
-static constexpr int AWQ_TILE = 32;  // column words per workgroup
-static constexpr int AWQ_SLOTS = WG / AWQ_TILE;
-__constant__ int kAwqOrder[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+// AWQ GEMV in one launch.  A workgroup owns one column word (8 output columns)
+// of one selected expert over all of K, so the K reduction stays inside it and
+// the launch has N / 8 workgroups per expert: thread t takes the row blocks t,
+// t + 256, ... of RB rows (RB divides the group, so a block lies in one
+// quantisation group).  Row pairs (k, k+1) of a column are merged byte-wise
+// with v_perm_b32 into (M + q_k, M + q_k+1) halves for v_dot2 against (x_k,
+// x_k+1); per block and column the bias M and the zero point are removed with
+// the block's activation sum and the block's scale applied:
+//     s (sum (M + q) x - (M + z) sum x).
+// The 256 partials of a column are then summed in a fixed order (wave sums,
+// then the four waves), so the result does not depend on timing.  Measured
+// on the 2048 -> 768 GEMV: one word per workgroup beats two or four (which
+// halve / quarter the workgroups: 12.5 / 13.6 us against 6.2), and the
+// XCD-aware tile order below beats plain block order (6.6 -> 6.2 us; q_proj
+// 2048 -> 4096 11.3 -> 8.8 us).
+__device__ inline constexpr int awq_col(int slot) {  // column of nibble slot, 0,2,4,6,1,3,5,7
+  return (slot & 3) * 2 + (slot >> 2);
+}
 
-template <int XT>
+template <int XT, int ST, int RB>
 __global__ __launch_bounds__(WG) void k_gemv_awq(
     const uint16_t* __restrict__ x, int64_t x_stride, const int32_t* __restrict__ qw, int64_t q_es,
-    const void* __restrict__ scales, int64_t s_es, int st, const int32_t* __restrict__ qz,
-    int64_t z_es, const int32_t* __restrict__ sel, int E, int N, int K, int group, int KS,
-    float* __restrict__ part) {
-  __shared__ u32 xs2[2048];          // (x[k], x[k+1]) pairs of this split, KS <= 4096
-  __shared__ float red[AWQ_SLOTS][AWQ_TILE][8];
+    const void* __restrict__ scales, int64_t s_es, const int32_t* __restrict__ qz, int64_t z_es,
+    const int32_t* __restrict__ sel, int E, int N, int K, int gshift, void* __restrict__ out,
+    int ot, const void* __restrict__ bias) {
+  __shared__ float red[WG / 64][8];
   const int NW = N >> 3;
-  const int j = blockIdx.z, split = blockIdx.y, nsplit = gridDim.y;
-  const int t = threadIdx.x, lc = t & (AWQ_TILE - 1), slot = t / AWQ_TILE;
-  const int cw = blockIdx.x * AWQ_TILE + lc;
-  const bool cv = cw < NW;
-  const int k0 = split * KS;
-  const int kend = min(K, k0 + KS);
+  // XCD-aware word order: workgroups are dispatched round-robin over the 8 XCDs
+  // (block b on XCD b % 8), so each XCD gets a contiguous run of words and the
+  // words that share a cache line are mostly read through one XCD's L2
+  int cw = blockIdx.x;
+  const int per = (int)gridDim.x >> 3;
+  if ((int)blockIdx.x < per * 8) cw = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  const int j = blockIdx.y;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const int e = sel ? sel[j] : 0;
   const bool ev = (unsigned)e < (unsigned)E;
-  float* dst = part + ((int64_t)split * gridDim.z + j) * N;
-  if (!ev) {
-    if (cv && slot == 0)
-      for (int i = 0; i < 8; ++i) dst[8 * cw + i] = __builtin_nanf("");
-    return;
-  }
-  // stage x pairs of this split
+  const int ee = ev ? e : 0;
+  const int32_t* qe = qw + ee * q_es + cw;
+  const int32_t* ze = qz ? qz + ee * z_es + cw : nullptr;
   const uint16_t* xrow = x + (int64_t)j * x_stride;
-  for (int p = t; p < (kend - k0) / 2; p += WG) xs2[p] = *(const u32*)(xrow + k0 + 2 * p);
-  __syncthreads();
-
-  const int32_t* qe = qw + e * q_es;
-  const int32_t* ze = qz ? qz + e * z_es : nullptr;
-  const int64_t se = e * s_es;
-  float acc_tot[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc_tot[i] = 0.f;
   constexpr u32 MK = 0x000F000Fu;
   const u32 mg = magic_v<XT>();
   const u32 ONE2 = XT == I4_F16 ? 0x3C003C00u : 0x3F803F80u;  // (1.0, 1.0)
-  // One quantisation group at a time, its rows in batches of RB row pairs per
-  // k-slot (128 rows): every weight word, the zero word and the 8 scales of a
-  // batch are loaded before any is used (indices clamped, so the loads are
-  // unconditional), then consumed -- one memory round trip per batch.
-  constexpr int RB = 8;
-  const int cwc = cv ? cw : NW - 1;
-  for (int gk = k0; gk < kend; gk += group) {
-    const int g = gk / group;
-    const int gend = min(kend, gk + group);
-    const u32 zw = ze ? (u32)ze[(int64_t)g * NW + cwc] : 0x88888888u;
-    float sv[8];
+  constexpr int SPL = ST == I4_F32 ? 4 : 8;  // scales per 16-byte load
+  float tot[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t si = se + (int64_t)g * N + 8 * cwc + kAwqOrder[i];
-      sv[i] = st == I4_F32 ? load_scale<I4_F32>(scales, si)
-            : st == I4_F16 ? load_scale<I4_F16>(scales, si)
-                           : load_scale<I4_BF16>(scales, si);
-    }
+  for (int c = 0; c < 8; ++c) tot[c] = 0.f;
+  for (int k0 = t * RB; k0 < K; k0 += WG * RB) {
+    // every load of the block first: weights, activations, scales, zero word
+    u32 wv[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) wv[r] = (u32)qe[(int64_t)(k0 + r) * NW];
+    u32 xp[RB / 2];
+#pragma unroll
+    for (int p = 0; p < RB / 2; ++p) xp[p] = *(const u32*)(xrow + k0 + 2 * p);
+    const int g = k0 >> gshift;
+    const char* sp = (const char*)scales + (ee * s_es + (int64_t)g * N + 8 * cw) *
+                                               (ST == I4_F32 ? 4 : 2);
+    u32x4 sv[8 / SPL];
+#pragma unroll
+    for (int v = 0; v < 8 / SPL; ++v) sv[v] = ldg16(sp + 16 * v);
+    const u32 zw = ze ? (u32)ze[(int64_t)g * NW] : 0x88888888u;
     float acc[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    for (int c = 0; c < 8; ++c) acc[c] = 0.f;
     float S = 0.f;
-    for (int kb0 = gk + 2 * slot; kb0 < gend; kb0 += 2 * AWQ_SLOTS * RB) {
-      u32 w0[RB], w1[RB];
 #pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        const int k = min(kb0 + 2 * AWQ_SLOTS * r, gend - 2);
-        w0[r] = (u32)qe[(int64_t)k * NW + cwc];
-        w1[r] = (u32)qe[(int64_t)(k + 1) * NW + cwc];
-      }
+    for (int p = 0; p < RB / 2; ++p) {
+      S = Half<XT>::dot2(xp[p], ONE2, S);
 #pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        const int k = kb0 + 2 * AWQ_SLOTS * r;
-        if (k < gend) {
-          const u32 xp = xs2[(k - k0) >> 1];
-          S = Half<XT>::dot2(xp, ONE2, S);
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            // byte b of w0 -> bits 0..7, byte b of w1 -> bits 16..23
-            const u32 sel_b = 0x0C000C00u | (u32)(b) | ((u32)(4 + b) << 16);
-            const u32 tb = __builtin_amdgcn_perm(w1[r], w0[r], sel_b);
-            acc[2 * b] = Half<XT>::dot2((tb & MK) | mg, xp, acc[2 * b]);
-            acc[2 * b + 1] = Half<XT>::dot2(((tb >> 4) & MK) | mg, xp, acc[2 * b + 1]);
-          }
-        }
+      for (int b = 0; b < 4; ++b) {
+        // byte b of row 2p -> bits 0..7, byte b of row 2p + 1 -> bits 16..23
+        const u32 sel_b = 0x0C000C00u | (u32)(b) | ((u32)(4 + b) << 16);
+        const u32 tb = __builtin_amdgcn_perm(wv[2 * p + 1], wv[2 * p], sel_b);
+        acc[2 * b] = Half<XT>::dot2((tb & MK) | mg, xp[p], acc[2 * b]);
+        acc[2 * b + 1] = Half<XT>::dot2(((tb >> 4) & MK) | mg, xp[p], acc[2 * b + 1]);
       }
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float z = (float)((zw >> (4 * i)) & 15u);
-      acc_tot[i] += sv[i] * (acc[i] - (Half<XT>::MAGIC + z) * S);
+    for (int sl = 0; sl < 8; ++sl) {
+      const float z = (float)((zw >> (4 * sl)) & 15u);
+      const int c = awq_col(sl);
+      const u32x4 q = sv[c / SPL];
+      const int ci = c % SPL;
+      const int wsel = ST == I4_F32 ? ci : ci >> 1;
+      const u32 word = wsel == 0 ? q.x : wsel == 1 ? q.y : wsel == 2 ? q.z : q.w;
+      const u32 raw = ST == I4_F32 ? word : (ci & 1 ? word >> 16 : word & 0xFFFFu);
+      tot[sl] += scale_from_raw<ST>(raw) * (acc[sl] - (Half<XT>::MAGIC + z) * S);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) red[slot][lc][i] = acc_tot[i];
+  for (int c = 0; c < 8; ++c) {
+    const float v = group_sum<64>(tot[c]);
+    if (lane == 0) red[wave][c] = v;
+  }
   __syncthreads();
-  {
-    const int ol = t >> 3, oi = t & 7;  // 32 words x 8 slots = 256 outputs
-    const int ocw = blockIdx.x * AWQ_TILE + ol;
-    if (ocw < NW) {
-      float s = 0.f;
-      for (int sl = 0; sl < AWQ_SLOTS; ++sl) s += red[sl][ol][oi];
-      dst[8 * ocw + kAwqOrder[oi]] = s;
+  if (t < 8) {
+    float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+    if (!ev) v = __builtin_nanf("");
+    const int n = 8 * cw + awq_col(t);
+    const int64_t o = (int64_t)j * N + n;
+    if (ot == I4_F32) {
+      if (bias) v += ((const float*)bias)[n];
+      store_out<I4_F32>(out, o, v);
+    } else if (ot == I4_F16) {
+      if (bias) v += Half<I4_F16>::to_f32(((const uint16_t*)bias)[n]);
+      store_out<I4_F16>(out, o, v);
+    } else {
+      if (bias) v += Half<I4_BF16>::to_f32(((const uint16_t*)bias)[n]);
+      store_out<I4_BF16>(out, o, v);
     }
-  }
-  (void)nsplit;
-}
-
-// out[j][n] = sum_s part[s][j][n] (+ bias[n]), fixed split order
-__global__ __launch_bounds__(WG) void k_reduce_split(const float* __restrict__ part, int nsplit,
-                                                     int64_t total, int N, void* __restrict__ out,
-                                                     int ot, const void* __restrict__ bias) {
-  const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
-  if (i >= total) return;
-  float s = 0.f;
-  for (int p = 0; p < nsplit; ++p) s += part[(int64_t)p * total + i];
-  const int n = (int)(i % N);
-  if (ot == I4_F32) {
-    if (bias) s += ((const float*)bias)[n];
-    store_out<I4_F32>(out, i, s);
-  } else if (ot == I4_F16) {
-    if (bias) s += Half<I4_F16>::to_f32(((const uint16_t*)bias)[n]);
-    store_out<I4_F16>(out, i, s);
-  } else {
-    if (bias) s += Half<I4_BF16>::to_f32(((const uint16_t*)bias)[n]);
-    store_out<I4_BF16>(out, i, s);
   }
 }
 
@@ -481,13 +462,6 @@ inline int64_t dense_zes(const i4_qweight* w) {  // CT and TILE hold the same wo
                                     : (int64_t)w->N * ((scale_ng(w) + 7) / 8);
 }
 
-inline int awq_split_rows(const i4_qweight* w) {
-  int gps = 1;
-  while ((int64_t)w->K > (int64_t)w->group * gps * 32) gps *= 2;
-  int ks = w->group * gps;
-  if (ks > 4096) ks = 4096 / w->group * w->group;
-  return ks;
-}
 
 }  // namespace
 
@@ -501,9 +475,17 @@ int i4_check_weight(const i4_qweight* w, i4_qweight* norm) {
   if (w->K % 32 != 0 || w->K > 16384) return I4_ERR_SHAPE;
   if (w->layout == I4_LAYOUT_AWQ && w->N % 8 != 0) return I4_ERR_SHAPE;
   if (w->layout == I4_LAYOUT_TILE && (w->N % 16 != 0 || w->K % 128 != 0)) return I4_ERR_SHAPE;
-  if (w->group < 32 || (w->group & (w->group - 1)) != 0) return I4_ERR_GROUP;
+  // a group spanning the whole row is one scale per output row (the per-channel
+  // branch of quant/dequant.py:75-76); kernels index groups by powers of two
+  int group = w->group;
+  if (group >= w->K) {
+    group = 32;
+    while (group < w->K) group <<= 1;
+  }
+  if (group < 32 || (group & (group - 1)) != 0) return I4_ERR_GROUP;
   if (!al16(w->packed)) return I4_ERR_ALIGN;
   *norm = *w;
+  norm->group = group;
   if (!norm->packed_estride) norm->packed_estride = dense_pes(w);
   if (!norm->scale_estride) norm->scale_estride = dense_ses(w);
   if (!norm->zeros_estride) norm->zeros_estride = dense_zes(w);
@@ -555,38 +537,57 @@ int i4_launch_gemv_ct(const void* x, int xt, int64_t x_stride, const i4_qweight*
   return I4_ERR_DTYPE;
 }
 
+// the AWQ GEMV reads scales 16 bytes at a time
+inline bool awq_scales_aligned(const i4_qweight& w) {
+  const int sb = w.scale_dtype == I4_F32 ? 4 : 2;
+  return ((uintptr_t)w.scale & 15) == 0 && (w.E == 1 || (w.scale_estride * sb) % 16 == 0);
+}
+
+// rows per block of the AWQ GEMV: one block per thread up to K = 256 RB, RB | group
+inline int awq_rows_per_block(int K, int group) {
+  int rb = 2;
+  while (rb < 16 && rb * WG < K) rb *= 2;
+  return rb < group ? rb : group;
+}
+
+template <int XT, int ST>
+static int launch_gemv_awq_t(const void* x, int64_t x_stride, const i4_qweight* w,
+                             const int32_t* sel, int k_sel, void* out, int ot, const void* bias,
+                             hipStream_t s) {
+  const int RB = awq_rows_per_block(w->K, w->group);
+  int gshift = 0;
+  while ((1 << gshift) < w->group) ++gshift;
+  const dim3 grid(w->N / 8, k_sel);
+#define I4_AWQ_CASE(RB_)                                                                        \
+  if (RB == RB_) {                                                                              \
+    hipLaunchKernelGGL((k_gemv_awq<XT, ST, RB_>), grid, dim3(WG), 0, s, (const uint16_t*)x,     \
+                       x_stride, w->packed, w->packed_estride, w->scale, w->scale_estride,      \
+                       w->zeros, w->zeros_estride, sel, w->E, w->N, w->K, gshift, out, ot, bias); \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
+  }
+  I4_AWQ_CASE(2) I4_AWQ_CASE(4) I4_AWQ_CASE(8) I4_AWQ_CASE(16)
+#undef I4_AWQ_CASE
+  return I4_ERR_SHAPE;
+}
+
 static int launch_gemv_awq(const void* x, int xt, int64_t x_stride, const i4_qweight* w,
                            const int32_t* sel, int k_sel, void* out, int ot, const void* bias,
-                           void* ws, size_t ws_bytes, hipStream_t s) {
-  const int KS = awq_split_rows(w);
-  const int nsplit = (w->K + KS - 1) / KS;
-  const size_t need = (size_t)nsplit * k_sel * w->N * sizeof(float);
-  if (!ws || ws_bytes < need) return I4_ERR_WORKSPACE;
-  dim3 grid((w->N / 8 + AWQ_TILE - 1) / AWQ_TILE, nsplit, k_sel);
-  if (xt == I4_F16)
-    hipLaunchKernelGGL((k_gemv_awq<I4_F16>), grid, dim3(WG), 0, s, (const uint16_t*)x, x_stride,
-                       w->packed, w->packed_estride, w->scale, w->scale_estride, w->scale_dtype,
-                       w->zeros, w->zeros_estride, sel, w->E, w->N, w->K, w->group, KS,
-                       (float*)ws);
-  else
-    hipLaunchKernelGGL((k_gemv_awq<I4_BF16>), grid, dim3(WG), 0, s, (const uint16_t*)x, x_stride,
-                       w->packed, w->packed_estride, w->scale, w->scale_estride, w->scale_dtype,
-                       w->zeros, w->zeros_estride, sel, w->E, w->N, w->K, w->group, KS,
-                       (float*)ws);
-  if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
-  const int64_t total = (int64_t)k_sel * w->N;
-  hipLaunchKernelGGL(k_reduce_split, dim3((unsigned)((total + WG - 1) / WG)), dim3(WG), 0, s,
-                     (const float*)ws, nsplit, total, w->N, out, ot, bias);
-  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+                           hipStream_t s) {
+#define I4_AWQ_DT(XT_, ST_)                                                              \
+  if (xt == XT_ && w->scale_dtype == ST_)                                                \
+    return launch_gemv_awq_t<XT_, ST_>(x, x_stride, w, sel, k_sel, out, ot, bias, s);
+  I4_AWQ_DT(I4_F16, I4_F32) I4_AWQ_DT(I4_F16, I4_F16) I4_AWQ_DT(I4_F16, I4_BF16)
+  I4_AWQ_DT(I4_BF16, I4_F32) I4_AWQ_DT(I4_BF16, I4_F16) I4_AWQ_DT(I4_BF16, I4_BF16)
+#undef I4_AWQ_DT
+  return I4_ERR_DTYPE;
 }
 
 extern "C" {
 
 size_t i4_dq_gemv_workspace_bytes(const i4_qweight* w, int k_sel) {
-  if (!w || w->layout != I4_LAYOUT_AWQ || k_sel < 1 || w->group < 32) return 0;
-  const int KS = awq_split_rows(w);
-  const int nsplit = (w->K + KS - 1) / KS;
-  return (size_t)nsplit * k_sel * w->N * sizeof(float);
+  (void)w;
+  (void)k_sel;
+  return 0;  // every layout runs in one launch without scratch
 }
 
 int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w,
@@ -601,11 +602,13 @@ int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w
   if (x_stride != 0 && x_stride < nw.K) return I4_ERR_STRIDE;
   if (!al16(x) || (x_stride * 2) % 16 != 0) return I4_ERR_ALIGN;
   if (nw.layout == I4_LAYOUT_TILE) return I4_ERR_LAYOUT;  // the MoE kernels' layout
+  if (nw.layout == I4_LAYOUT_AWQ && !awq_scales_aligned(nw)) return I4_ERR_ALIGN;
   if (nw.layout == I4_LAYOUT_CT)
     return i4_launch_gemv_ct(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr,
                              stream);
-  return launch_gemv_awq(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr,
-                         workspace, workspace_bytes, stream);
+  (void)workspace;
+  (void)workspace_bytes;
+  return launch_gemv_awq(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr, stream);
 }
 
 int i4_rmsnorm_linear(const void* x, int x_dtype, int M, const void* norm_w, float eps,
@@ -660,8 +663,8 @@ int i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w, const void
   nw.E = 1;
   if (nw.layout == I4_LAYOUT_CT)
     return i4_launch_gemv_ct(x, x_dtype, nw.K, &nw, nullptr, M, y, y_dtype, bias, stream);
-  return launch_gemv_awq(x, x_dtype, nw.K, &nw, nullptr, M, y, y_dtype, bias, workspace,
-                         workspace_bytes, stream);
+  if (!awq_scales_aligned(nw)) return I4_ERR_ALIGN;
+  return launch_gemv_awq(x, x_dtype, nw.K, &nw, nullptr, M, y, y_dtype, bias, stream);
 }
 
 static WView make_view(const i4_qweight& w) {

@@ -24,9 +24,10 @@ int i4_launch_gemv_ct(const void* x, int xt, int64_t x_stride, const i4_qweight*
 
 // Launch router logits / top-k without re-validating (callers validated).
 // T = 1 only: pend (16-byte aligned, n_pend 16-byte units) is filled with
-// 0xFFFF halves, the pending pattern of the single-launch expert stage.
+// 0xFFFF halves, the pending pattern of the single-launch expert stage, and
+// *status (nullable) is set to I4_OK for the failure that stage may report.
 int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr, int E,
                             const void* norm_w, float eps, void* xn, void* logits, hipStream_t s,
-                            void* pend = nullptr, int n_pend = 0);
+                            void* pend = nullptr, int n_pend = 0, int32_t* status = nullptr);
 int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
                    float* wf, void* wh, int wht, hipStream_t s);

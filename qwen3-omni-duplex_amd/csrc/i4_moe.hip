@@ -157,8 +157,10 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
                                                 int4* __restrict__ entries,
                                                 int* __restrict__ n_entries,
                                                 int4* __restrict__ mf_entries,
-                                                int* __restrict__ n_mf_entries) {
+                                                int* __restrict__ n_mf_entries,
+                                                int32_t* __restrict__ status) {
   extern __shared__ __align__(16) unsigned char lds[];
+  if (status && threadIdx.x == 0) *status = I4_OK;  // nothing on this path waits
   group_body(sel, T, topk, E, lo_max, lo_chunk, perm, entries, n_entries, mf_entries,
              n_mf_entries, lds);
 }
@@ -171,8 +173,9 @@ __global__ __launch_bounds__(1024) void k_route_group(
     const void* __restrict__ logits, int T, int E, int topk, int renorm,
     int32_t* __restrict__ sel, float* __restrict__ wts, int lo_max, int lo_chunk,
     int32_t* __restrict__ perm, int4* __restrict__ entries, int* __restrict__ n_entries,
-    int4* __restrict__ mf_entries, int* __restrict__ n_mf_entries) {
+    int4* __restrict__ mf_entries, int* __restrict__ n_mf_entries, int32_t* __restrict__ status) {
   extern __shared__ __align__(16) unsigned char lds[];
+  if (status && threadIdx.x == 0) *status = I4_OK;  // nothing on this path waits
   int32_t* sel_l = (int32_t*)lds;  // [T][topk]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int t = wave; t < T; t += blockDim.x >> 6) {
@@ -211,6 +214,7 @@ struct MoeWs {
   int* n_entries;
   int4* mf_entries;  // large MFMA entries (<= MF_TOK tokens)
   int* n_mf_entries;
+  int32_t* status;  // I4_OK or I4_ERR_HANDOFF (i4_moe_status_offset)
   size_t bytes;
 };
 
@@ -235,6 +239,7 @@ MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
   m.n_entries = (int*)take(4);
   m.mf_entries = (int4*)take((E + Tk / MF_TOK + 1) * sizeof(int4));
   m.n_mf_entries = (int*)take(4);
+  m.status = (int32_t*)take(4);
   m.bytes = o;
   return m;
 }
@@ -264,8 +269,9 @@ struct MoeOps {
   int (*mfma_gate_up)(bool, int, const void*, int, int, const int4*, const int*, const int32_t*,
                       const TW&, int, void*, hipStream_t);
   int (*mfma_down)(bool, int, const void*, int, const int4*, const int*, const int32_t*,
-                   const TW&, float*, hipStream_t);
-  int (*moe_m1_ct)(const GateUpArgs&, const TW&, const TW&, const void*, void*, hipStream_t);
+                   const TW&, void*, hipStream_t);
+  int (*moe_m1_ct)(const GateUpArgs&, const TW*, const TW&, const void*, void*, int32_t*, int,
+                   hipStream_t);
 };
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
@@ -341,10 +347,13 @@ int check_moe(const i4_moe_weights* mw, int x_dtype, int T, int topk, i4_qweight
   return I4_OK;
 }
 
+// reset: this chunk's first kernel clears the status word (the first chunk of
+// a call, the first layer of a stack), so a later give-up is not overwritten
 int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_qweight& gu,
               const i4_qweight& dn, const i4_qweight& tg, const i4_qweight& td, int topk,
               int renorm, const void* logits, const void* residual, void* out, int32_t* sel_out,
-              float* w_out, const MoeWs& ws, hipStream_t s) {
+              float* w_out, const MoeWs& ws, bool reset, hipStream_t s) {
+  int32_t* st_reset = reset ? ws.status : nullptr;
   const int H = gu.K, I = dn.K, E = gu.E;
   MoeOps ops;
   if (!pick_ops(xt, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
@@ -362,13 +371,17 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
     if (mw->router_w) {
       rc = i4_launch_router_logits(x, xt, 1, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
                                    mw->norm_w ? ws.xn : nullptr, ws.logits, s,
-                                   one ? ws.act : nullptr, one ? topk * I / 8 : 0);
+                                   one ? ws.act : nullptr, one ? topk * I / 8 : 0, st_reset);
       if (rc) return rc;
       lg = ws.logits;
       if (mw->norm_w) x = ws.xn;  // the experts run on RMSNorm(x); residual is untouched
+      st_reset = nullptr;
     }
-    const GateUpArgs a{true, topk, topk, E, renorm, x, sel, lg, wts, ws.act};
-    if (one) return ops.moe_m1_ct(a, to_tw(gu), to_tw(dn), residual, out, s);
+    const GateUpArgs a{true, topk, topk, E, renorm, x, sel, lg, wts, ws.act, st_reset};
+    if (one) {
+      const TW tg_ = to_tw(gu);
+      return ops.moe_m1_ct(a, &tg_, to_tw(dn), residual, out, ws.status, kHandoffPolls, s);
+    }
     rc = (ct ? ops.gate_up_ct : ops.gate_up)(a, to_tw(gu), I, s);
     if (rc) return rc;
     return (ct ? ops.down_m1_ct : ops.down_m1)(ws.act, topk, sel, wts, to_tw(dn), residual, out, s);
@@ -395,7 +408,7 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   if (xt == LT_ && E <= 64 * VPL_) {                                                           \
     hipLaunchKernelGGL((k_route_group<LT_, VPL_>), dim3(1), dim3(1024), lds, s, lg, T, E, topk,  \
                        renorm, sel, wts, T, MF_SMALL, ws.perm, ws.entries, ws.n_entries,       \
-                       ws.mf_entries, ws.n_mf_entries);                                        \
+                       ws.mf_entries, ws.n_mf_entries, st_reset);                              \
   } else
     I4_RG_CASE(I4_F16, 2) I4_RG_CASE(I4_F16, 8) I4_RG_CASE(I4_BF16, 2) I4_RG_CASE(I4_BF16, 8)
     return I4_ERR_SHAPE;
@@ -405,7 +418,7 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
     if (rc) return rc;
     hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E, MF_SMALL,
                        MF_SMALL, ws.perm, ws.entries, ws.n_entries, ws.mf_entries,
-                       ws.n_mf_entries);
+                       ws.n_mf_entries, st_reset);
   }
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
   // entry counts: sum over experts of ceil(n_e / 16) <= min(E, Tk) + Tk / 16
@@ -442,19 +455,12 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
-}  // namespace
-
-extern "C" {
-
-size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk) {
-  if (T < 1 || H < 1 || I < 1 || E < 1 || topk < 1) return 0;
-  return carve(nullptr, T, H, I, E, topk).bytes;
-}
-
-int i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weights, int topk,
-                   int renorm, const void* logits, const void* residual, void* out,
-                   int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
-                   hipStream_t stream) {
+// i4_moe_forward with the status reset under the caller's control (the stack
+// clears it in its first layer only, so a give-up in any layer stays visible)
+int moe_forward_impl(const void* x, int x_dtype, int T, const i4_moe_weights* weights, int topk,
+                     int renorm, const void* logits, const void* residual, void* out,
+                     int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
+                     bool reset, hipStream_t stream) {
   i4_qweight gu, dn, tg, td;
   int rc = check_moe(weights, x_dtype, T, topk, &gu, &dn, &tg, &td);
   if (rc) return rc;
@@ -477,10 +483,55 @@ int i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weig
     void* os = (char*)out + (size_t)t0 * H * 2;
     rc = moe_chunk(xs, x_dtype, Tc, weights, gu, dn, tg, td, topk, renorm, lg, rs, os,
                    sel_out ? sel_out + (size_t)t0 * topk : nullptr,
-                   w_out ? w_out + (size_t)t0 * topk : nullptr, ws, stream);
+                   w_out ? w_out + (size_t)t0 * topk : nullptr, ws, reset && t0 == 0, stream);
     if (rc) return rc;
   }
   return I4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk) {
+  if (T < 1 || H < 1 || I < 1 || E < 1 || topk < 1) return 0;
+  return carve(nullptr, T, H, I, E, topk).bytes;
+}
+
+size_t i4_moe_status_offset(int T, int H, int I, int E, int topk) {
+  if (T < 1 || H < 1 || I < 1 || E < 1 || topk < 1) return 0;
+  char* const base = (char*)(uintptr_t)4096;  // carve() lays out from any aligned base
+  return (size_t)((char*)carve(base, T, H, I, E, topk).status - base);
+}
+
+int i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weights, int topk,
+                   int renorm, const void* logits, const void* residual, void* out,
+                   int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
+  return moe_forward_impl(x, x_dtype, T, weights, topk, renorm, logits, residual, out, sel_out,
+                          w_out, workspace, workspace_bytes, true, stream);
+}
+
+int i4_moe_down_wait(const void* act, int x_dtype, const i4_qweight* down, const void* logits,
+                     int E_r, int topk, int renorm, const void* residual, void* out,
+                     int32_t* status, int max_polls, hipStream_t stream) {
+  i4_qweight dn;
+  int rc = check_decode(down, &dn);
+  if (rc) return rc;
+  if (!act || !logits || !out || !status) return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  if (dn.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (E_r < 1 || E_r > 512 || E_r > dn.E || topk < 1 || topk > E_r || max_polls < 0)
+    return I4_ERR_SHAPE;
+  if (!moe_m1_ct_fits(topk, dn.N, dn.K)) return I4_ERR_SHAPE;
+  if (((uintptr_t)act & 15) || ((uintptr_t)out & 15) || ((uintptr_t)residual & 15) ||
+      ((uintptr_t)status & 3))
+    return I4_ERR_ALIGN;
+  MoeOps ops;
+  if (!pick_ops(x_dtype, dn.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
+  const GateUpArgs a{true, topk, topk, E_r, renorm, nullptr, nullptr, logits, nullptr,
+                     const_cast<void*>(act), nullptr};
+  return ops.moe_m1_ct(a, nullptr, to_tw(dn), residual, out, status, max_polls, stream);
 }
 
 int i4_moe_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up, const int32_t* sel,
@@ -496,7 +547,7 @@ int i4_moe_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up, const 
   MoeOps ops;
   if (!pick_ops(x_dtype, gu.scale_dtype, gu.scale_dtype, &ops)) return I4_ERR_DTYPE;
   const GateUpArgs a{false, topk, topk, 0, 0, x, const_cast<int32_t*>(sel), nullptr, nullptr,
-                     act};
+                     act, nullptr};
   return (gu.layout == I4_LAYOUT_CT ? ops.gate_up_ct : ops.gate_up)(a, to_tw(gu), gu.N / 2, stream);
 }
 
@@ -514,7 +565,7 @@ int i4_moe_route_gate_up(const void* x, int x_dtype, const i4_qweight* gate_up,
   if (((uintptr_t)x & 15) || ((uintptr_t)act & 15)) return I4_ERR_ALIGN;
   MoeOps ops;
   if (!pick_ops(x_dtype, gu.scale_dtype, gu.scale_dtype, &ops)) return I4_ERR_DTYPE;
-  const GateUpArgs a{true, topk, topk, E_r, renorm, x, sel_out, logits, w_out, act};
+  const GateUpArgs a{true, topk, topk, E_r, renorm, x, sel_out, logits, w_out, act, nullptr};
   return (gu.layout == I4_LAYOUT_CT ? ops.gate_up_ct : ops.gate_up)(a, to_tw(gu), gu.N / 2, stream);
 }
 
@@ -564,8 +615,8 @@ int i4_moe_stack_forward(const void* x, int x_dtype, int T, const i4_moe_weights
   const void* h = x;
   for (int l = 0; l < n_layers; ++l) {
     void* dst = ((n_layers - 1 - l) % 2 == 0) ? out : buf;
-    rc = i4_moe_forward(h, x_dtype, T, &layers[l], topk, renorm, nullptr, h, dst, nullptr,
-                        nullptr, workspace, mbytes, stream);
+    rc = moe_forward_impl(h, x_dtype, T, &layers[l], topk, renorm, nullptr, h, dst, nullptr,
+                          nullptr, workspace, mbytes, l == 0, stream);
     if (rc) return rc;
     h = dst;
   }

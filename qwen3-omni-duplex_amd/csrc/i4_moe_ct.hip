@@ -161,8 +161,9 @@ template <int XT, int ST, int L, int MODE>
 __global__ __launch_bounds__(WG) void k_ct_gate_up(
     const uint16_t* __restrict__ x, int topk, int32_t* __restrict__ sel,
     const uint16_t* __restrict__ logits, int E_r, int renorm, float* __restrict__ wts, QW w,
-    int I, uint16_t* __restrict__ act) {
+    int I, uint16_t* __restrict__ act, int32_t* __restrict__ status) {
   extern __shared__ __align__(16) unsigned char lds[];
+  if (status && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *status = I4_OK;
   gate_up_body<XT, ST, L, MODE, false>(blockIdx.x, blockIdx.y, x, topk, sel, logits, E_r, renorm,
                                        wts, w, I, act, lds);
 }
@@ -182,11 +183,11 @@ template <int L> struct DownShape {
 // Polls for the activations of a handoff launch: the rows are loaded
 // device-coherently until no value still holds the pending pattern (the
 // router's launch fills them with it; gate_up workgroups of the same launch
-// overwrite every value).  Returns true if kHandoffSpins polls went by
-// without that, which a launch whose workgroups are dispatched in block order
-// never sees: the bound only guarantees that every wave exits.
-static constexpr int kHandoffSpins = 1 << 20;
-template <int XT> __device__ inline bool poll_rows(Stager<XT>& st, const uint16_t* src) {
+// overwrite every value).  Returns true if max_polls polls went by without
+// that, which a launch whose workgroups are dispatched in block order never
+// sees: the bound guarantees that every wave exits.
+template <int XT>
+__device__ inline bool poll_rows(Stager<XT>& st, const uint16_t* src, int max_polls) {
   const int nt = blockDim.x;
   const rsrc_t r = rsrc(src, (u32)st.total * 16u);
   for (int it = 0;; ++it) {
@@ -199,7 +200,7 @@ template <int XT> __device__ inline bool poll_rows(Stager<XT>& st, const uint16_
 #pragma unroll
     for (int u = 0; u < 4; ++u) pend |= has_pending(st.d[u]);
     if (!__syncthreads_or(pend)) return false;
-    if (it == kHandoffSpins) return true;
+    if (it >= max_polls) return true;
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -212,7 +213,8 @@ __device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int t
                                  const int32_t* __restrict__ sel, const float* __restrict__ wts,
                                  const uint16_t* __restrict__ logits, int E_r, int renorm,
                                  const QW& w, const uint16_t* __restrict__ residual,
-                                 uint16_t* __restrict__ out, unsigned char* lds) {
+                                 uint16_t* __restrict__ out, unsigned char* lds,
+                                 int32_t* __restrict__ status = nullptr, int max_polls = 0) {
   constexpr int GPR = DownShape<L>::GPR, RW = DownShape<L>::RW;
   constexpr int CR = 4;  // chunks per round
   const int I = w.K, H = w.N, C = I >> 5;
@@ -296,7 +298,7 @@ __device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int t
   // the activation loads
   load_round(0);
   bool late = false;
-  if constexpr (HANDOFF) late = poll_rows<XT>(st, act);  // the rows fit one staging round
+  if constexpr (HANDOFF) late = poll_rows<XT>(st, act, max_polls);  // one staging round
   st.commit(0, xs, sums);
   if constexpr (!HANDOFF) st.rest(row_of, xs, sums);
   if ((int)threadIdx.x < topk) s_w[threadIdx.x] = wv;
@@ -309,7 +311,9 @@ __device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int t
 #pragma unroll
   for (int jj = 0; jj < JMAX; ++jj) {
     const int j = jg + jj * GPR;
-    const float v = group_sum<L>(row[jj]);
+    // each expert's output rounded to the activation dtype before the weighted
+    // sum, as the reference's y.to(x.dtype) does (fused_packed_moe.py:262)
+    const float v = Half<XT>::to_f32(Half<XT>::from_f32(group_sum<L>(row[jj])));
     if (j < topk && cl == 0)
       red[j * RW + r] = (unsigned)ej[jj] < (unsigned)w.E ? v : __builtin_nanf("");
   }
@@ -319,6 +323,9 @@ __device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int t
     for (int j = 0; j < topk; ++j) y += s_w[j] * red[j * RW + (int)threadIdx.x];
     if (late) y = __builtin_nanf("");
     out[on] = Half<XT>::from_f32((residual ? Half<XT>::to_f32(res_raw) : 0.f) + y);
+  }
+  if constexpr (HANDOFF) {
+    if (late && threadIdx.x == 0) *status = I4_ERR_HANDOFF;
   }
 }
 
@@ -351,7 +358,8 @@ struct MoeM1Args {
   uint16_t* act;
   const uint16_t* residual;
   uint16_t* out;
-  int gx, n_gate;
+  int32_t* status;  // I4_ERR_HANDOFF is stored here by a workgroup whose wait gave up
+  int gx, n_gate, max_polls;
 };
 
 template <int XT, int ST, int LG, int LD, int JMAX>
@@ -363,7 +371,8 @@ __global__ __launch_bounds__(WG) void k_ct_moe_m1(MoeM1Args a) {
                                              a.E_r, a.renorm, a.wts, a.gu, a.dn.K, a.act, lds);
   else
     down_body<XT, ST, LD, JMAX, true>(b - a.n_gate, a.act, a.topk, nullptr, nullptr, a.logits,
-                                      a.E_r, a.renorm, a.dn, a.residual, a.out, lds);
+                                      a.E_r, a.renorm, a.dn, a.residual, a.out, lds, a.status,
+                                      a.max_polls);
 }
 
 // ---------------------------------------------------------------------------
@@ -396,7 +405,7 @@ static int ct_gate_up_t(int L, dim3 grid, size_t lds, hipStream_t s, const GateU
   if (L == L_) {                                                                                \
     hipLaunchKernelGGL((k_ct_gate_up<XT, ST, L_, MODE>), grid, dim3(WG), lds, s,                \
                        (const uint16_t*)a.x, a.topk, a.sel, (const uint16_t*)a.logits, a.E_r,   \
-                       a.renorm, a.wts, w, I, (uint16_t*)a.act);                                \
+                       a.renorm, a.wts, w, I, (uint16_t*)a.act, a.status);                      \
     return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
   }
   I4_GU_CASE(8) I4_GU_CASE(16) I4_GU_CASE(32) I4_GU_CASE(64)
@@ -453,12 +462,13 @@ bool moe_m1_ct_fits(int topk, int H, int I) {
 }
 
 template <int XT, int ST>
-int launch_moe_m1_ct(const GateUpArgs& ga, const TW& tgu, const TW& tdn, const void* res,
-                     void* out, hipStream_t s) {
+int launch_moe_m1_ct(const GateUpArgs& ga, const TW* tgu, const TW& tdn, const void* res,
+                     void* out, int32_t* status, int max_polls, hipStream_t s) {
   MoeM1Args a;
-  a.gu = to_qw(tgu);
   a.dn = to_qw(tdn);
-  const int H = a.gu.K, I = a.dn.K;
+  a.gu = tgu ? to_qw(*tgu) : a.dn;  // without gate_up workgroups only its shape is unused
+  const int H = a.dn.N, I = a.dn.K;
+  if (!status || max_polls < 0) return I4_ERR_NULL;
   if (!moe_m1_ct_fits(ga.topk, H, I)) return I4_ERR_SHAPE;
   const int LG = gate_up_lanes(H / 32), LD = lanes_per_row(I / 32);
   a.x = (const uint16_t*)ga.x;
@@ -471,9 +481,11 @@ int launch_moe_m1_ct(const GateUpArgs& ga, const TW& tgu, const TW& tdn, const v
   a.act = (uint16_t*)ga.act;
   a.residual = (const uint16_t*)res;
   a.out = (uint16_t*)out;
+  a.status = status;
+  a.max_polls = max_polls;
   const int rpw = WG / LG;
   a.gx = (I + rpw - 1) / rpw;
-  a.n_gate = a.gx * ga.topk;
+  a.n_gate = tgu ? a.gx * ga.topk : 0;
   constexpr int RW = 8;  // DownShape<8>::RW == DownShape<16>::RW
   static_assert(DownShape<8>::RW == RW && DownShape<16>::RW == RW, "down rows per workgroup");
   const size_t lds_d = (size_t)ga.topk * (I * 2 + (I / 32) * 8) + (size_t)ga.topk * RW * 4;
@@ -495,8 +507,8 @@ int launch_moe_m1_ct(const GateUpArgs& ga, const TW& tgu, const TW& tdn, const v
   template int launch_gate_up_ct<XT_, ST_>(const GateUpArgs&, const TW&, int, hipStream_t);    \
   template int launch_down_m1_ct<XT_, ST_>(const void*, int, const int32_t*, const float*,     \
                                            const TW&, const void*, void*, hipStream_t);        \
-  template int launch_moe_m1_ct<XT_, ST_>(const GateUpArgs&, const TW&, const TW&, const void*, \
-                                          void*, hipStream_t);
+  template int launch_moe_m1_ct<XT_, ST_>(const GateUpArgs&, const TW*, const TW&, const void*, \
+                                          void*, int32_t*, int, hipStream_t);
 I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
 I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)
 #undef I4_INST

@@ -29,9 +29,10 @@ template <int XT, int ST, bool GB, int SPW, int MODE>
 __global__ __launch_bounds__(256) void k_tile_gate_up(
     const uint16_t* __restrict__ x, int topk, int32_t* __restrict__ sel,
     const uint16_t* __restrict__ logits, int E_r, int renorm, float* __restrict__ wts, TW w,
-    int I, uint16_t* __restrict__ act) {
+    int I, uint16_t* __restrict__ act, int32_t* __restrict__ status) {
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ float red[4][32];
+  if (status && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *status = I4_OK;
   const int H = w.K, C = H >> 5, SC = H >> 7;
   u32x4* xs = (u32x4*)lds;
   float2* sums = (float2*)(lds + (size_t)H * 2);
@@ -164,7 +165,9 @@ __global__ __launch_bounds__(256) void k_tile_down_m1(
 #pragma unroll
   for (int jj = 0; jj < JMAX; ++jj) {
     const int j = wave + 4 * jj;
-    const float v = kgroup_sum(acc[jj]);
+    // each expert's output rounded to the activation dtype before the weighted
+    // sum, as the reference's y.to(x.dtype) does (fused_packed_moe.py:262)
+    const float v = Half<XT>::to_f32(Half<XT>::from_f32(kgroup_sum(acc[jj])));
     if (j < topk && kb == 0) red[j][ln] = (unsigned)ej[jj] < (unsigned)w.E ? v : __builtin_nanf("");
   }
   __syncthreads();
@@ -187,7 +190,7 @@ static int gate_up_t(const GateUpArgs& a, const TW& w, int I, hipStream_t s) {
   if (spw <= SPW_) {                                                                         \
     hipLaunchKernelGGL((k_tile_gate_up<XT, ST, GB, SPW_, MODE>), grid, dim3(256), lds, s,    \
                        (const uint16_t*)a.x, a.topk, a.sel, (const uint16_t*)a.logits, a.E_r, \
-                       a.renorm, a.wts, w, I, (uint16_t*)a.act);                             \
+                       a.renorm, a.wts, w, I, (uint16_t*)a.act, a.status);                   \
     return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                          \
   }
   I4_GU_CASE(1) I4_GU_CASE(2) I4_GU_CASE(4) I4_GU_CASE(8)

@@ -26,6 +26,7 @@ struct GateUpArgs {
   const void* logits;
   float* wts;
   void* act;
+  int32_t* status;  // nullable: workgroup (0, 0) sets it to I4_OK (no wait in these kernels)
 };
 
 // tile weights (i4_moe_decode.hip)
@@ -42,24 +43,30 @@ int launch_down_m1_ct(const void* act, int topk, const int32_t* sel, const float
                       const TW& w, const void* residual, void* out, hipStream_t s);
 // both expert projections of a decode layer in one launch (route mode only);
 // act must hold the pending pattern (kPending16) in its topk * I values, which
-// the T = 1 router launch writes.  moe_m1_ct_fits says which shapes it covers.
+// the T = 1 router launch writes.  A down workgroup polls act at most
+// max_polls times; one that gives up writes NaN rows and I4_ERR_HANDOFF to
+// *status.  gate_up == nullptr launches the down workgroups alone (act is then
+// produced elsewhere).  moe_m1_ct_fits says which shapes it covers.
+static constexpr int kHandoffPolls = 1 << 20;
 bool moe_m1_ct_fits(int topk, int H, int I);
 template <int XT, int ST>
-int launch_moe_m1_ct(const GateUpArgs& a, const TW& gate_up, const TW& down,
-                     const void* residual, void* out, hipStream_t s);
+int launch_moe_m1_ct(const GateUpArgs& a, const TW* gate_up, const TW& down,
+                     const void* residual, void* out, int32_t* status, int max_polls,
+                     hipStream_t s);
 
 // Grouped (T > 1) expert projections on MFMA.  entries[i] = {expert, first
 // position, tokens, 0} of the expert-sorted (token, slot) list perm; small
 // entries have <= MF_SMALL tokens, large ones <= MF_TOK.
 //   gate_up: act[pos] = silu(gate(x[perm[pos] / topk])) * up(...), x [T][H]
-//   down:    ys[perm[pos]] = down(act[pos]) (fp32), act [rows][I]
+//   down:    ys[perm[pos]] = down(act[pos]) rounded to the activation dtype
+//            (the reference's y.to(x.dtype), fused_packed_moe.py:262), act [rows][I]
 template <int XT, int ST>
 int launch_mfma_gate_up(bool small, int max_entries, const void* x, int T, int topk,
                         const int4* ent, const int* nent, const int32_t* perm, const TW& w, int I,
                         void* act, hipStream_t s);
 template <int XT, int ST>
 int launch_mfma_down(bool small, int max_entries, const void* act, int rows, const int4* ent,
-                     const int* nent, const int32_t* perm, const TW& w, float* ys, hipStream_t s);
+                     const int* nent, const int32_t* perm, const TW& w, void* ys, hipStream_t s);
 
 // Dense linear layer on MFMA: y[M][N] = x[M][K] W^T (+ bias, dtype ot), W one
 // tile-layout weight (E = 1, N % 128 == 0).  Small grids are split along K

@@ -41,7 +41,8 @@
 //   GATEUP: NB/2 blocks of gate rows and the same up rows per wave, SiLU in
 //           the epilogue, act[pos] in the activation dtype; 32 NB row pairs
 //           per workgroup.
-//   DOWN:   NB blocks of output rows per wave, ys[slot] in fp32; 64 NB rows
+//   DOWN:   NB blocks of output rows per wave, ys[slot] rounded to the
+//           activation dtype (the reference's y.to(x.dtype), fused_packed_moe.py:262); 64 NB rows
 //           per workgroup.
 #include "i4_moe_launch.h"
 
@@ -536,12 +537,14 @@ int launch_mfma_gate_up(bool small, int max_entries, const void* x, int T, int t
 
 template <int XT, int ST>
 int launch_mfma_down(bool small, int max_entries, const void* act, int rows, const int4* ent,
-                     const int* nent, const int32_t* perm, const TW& w, float* ys, hipStream_t s) {
+                     const int* nent, const int32_t* perm, const TW& w, void* ys, hipStream_t s) {
+  // the kernel's output pointer is typed for the dense linear's fp32 path; the
+  // MoE down projection stores activation-dtype halves through it
   if (w.gshift >= 2)
     return mfma_t<XT, ST, true, false>(small, max_entries, act, rows, 0, ent, nent, perm, w, 0,
-                                       nullptr, ys, s);
+                                       nullptr, (float*)ys, s);
   return mfma_t<XT, ST, false, false>(small, max_entries, act, rows, 0, ent, nent, perm, w, 0,
-                                      nullptr, ys, s);
+                                      nullptr, (float*)ys, s);
 }
 
 // y[r][n] = sum_z part[z][r][n] + bias[n] in dtype ot, the K ranges in order
@@ -621,7 +624,7 @@ int launch_mfma_linear(const void* x, int M, const TW& w, const void* bias, void
                                              const int*, const int32_t*, const TW&, int, void*, \
                                              hipStream_t);                                     \
   template int launch_mfma_down<XT_, ST_>(bool, int, const void*, int, const int4*,            \
-                                          const int*, const int32_t*, const TW&, float*,       \
+                                          const int*, const int32_t*, const TW&, void*,        \
                                           hipStream_t);
 I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
 I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)

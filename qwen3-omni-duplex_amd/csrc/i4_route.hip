@@ -18,17 +18,20 @@ namespace i4 {
 // wave dots one expert row.  The sum of squares is reduced in the same fixed
 // order in every workgroup, so all of them use the same r bit for bit.
 // pend[0..n_pend) (16-byte units) is filled with the pending pattern for a
-// following single-launch expert stage, which polls it (n_pend = 0: none).
+// following single-launch expert stage, which polls it (n_pend = 0: none), and
+// *status (when given) is cleared for the failure that stage may report.
 template <int XT, bool NORM>
 __global__ __launch_bounds__(256) void k_router_m1(
     const uint16_t* __restrict__ x, int H, const uint16_t* __restrict__ wr, int E,
     const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
-    uint16_t* __restrict__ logits, u32x4* __restrict__ pend, int n_pend) {
+    uint16_t* __restrict__ logits, u32x4* __restrict__ pend, int n_pend,
+    int32_t* __restrict__ status) {
   constexpr int RL = 8;  // 512-element rounds of a router row (H <= 4096)
   __shared__ u32x4 s_xn[512];
   __shared__ float s_ss[4];
   for (int i = blockIdx.x * 256 + (int)threadIdx.x; i < n_pend; i += gridDim.x * 256)
     pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
+  if (status && blockIdx.x == 0 && threadIdx.x == 0) *status = I4_OK;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int words = H >> 3, rounds = (H + 511) / 512;
   u32x4 xv[2], gv[2];
@@ -216,14 +219,14 @@ using namespace i4;
 
 int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr, int E,
                             const void* norm_w, float eps, void* xn, void* logits, hipStream_t s,
-                            void* pend, int n_pend) {
+                            void* pend, int n_pend, int32_t* status) {
   dim3 grid((E + 3) / 4, 1);
   if (T == 1) {
 #define I4_RM1_CASE(XT_, N_)                                                                  \
   if (xt == XT_ && (norm_w != nullptr) == N_)                                                 \
     hipLaunchKernelGGL((k_router_m1<XT_, N_>), grid, dim3(256), 0, s, (const uint16_t*)x, H,  \
                        (const uint16_t*)wr, E, (const uint16_t*)norm_w, eps, (uint16_t*)xn,   \
-                       (uint16_t*)logits, (u32x4*)pend, n_pend);
+                       (uint16_t*)logits, (u32x4*)pend, n_pend, status);
     I4_RM1_CASE(I4_F16, true) else I4_RM1_CASE(I4_F16, false) else I4_RM1_CASE(I4_BF16, true)
     else I4_RM1_CASE(I4_BF16, false)
 #undef I4_RM1_CASE

@@ -184,6 +184,24 @@ def _decode_layout(*ws: QWeight) -> None:
                              "convert once with QWeight.to_ct() / to_tile()")
 
 
+def _check_block_dtypes(x_dtype: torch.dtype, H: int, E: int, router_w: torch.Tensor | None,
+                        norm_w: torch.Tensor | None) -> None:
+    """The kernels read the router and norm weights in the activation dtype, as the
+    reference's half-precision gate Linear does (F.linear raises on a mismatch)."""
+    if router_w is not None:
+        if router_w.dtype != x_dtype:
+            raise RuntimeError(f"router weight is {router_w.dtype}, activations are {x_dtype}: "
+                               "build the block in the activation dtype")
+        if tuple(router_w.shape) != (E, H) or not router_w.is_contiguous():
+            raise RuntimeError(f"router weight must be a contiguous [{E}, {H}] tensor, "
+                               f"got {tuple(router_w.shape)}")
+    if norm_w is not None:
+        if norm_w.dtype != x_dtype:
+            raise RuntimeError(f"norm weight is {norm_w.dtype}, activations are {x_dtype}")
+        if norm_w.numel() != H or not norm_w.is_contiguous():
+            raise RuntimeError(f"norm weight must hold {H} contiguous values")
+
+
 def moe_weights_c(gate_up: QWeight, down: QWeight, router_w: torch.Tensor | None,
                   norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
                   gate_up_tile: QWeight | None = None,
@@ -235,6 +253,7 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
     E, I = gate_up.E, down.K
     if router_w is None and logits is None:
         raise RuntimeError("need router_w or logits")
+    _check_block_dtypes(x.dtype, H, E, router_w, norm_w)
     lg = None
     if router_w is None:
         lg = logits.reshape(T, E).to(x.dtype).contiguous()
@@ -254,6 +273,43 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
     if return_routing:
         return out, sel, wts
     return out
+
+
+def moe_status(workspace: Workspace, T: int, H: int, I: int, E: int, top_k: int) -> int:
+    """The status word the last i4_moe_forward / stack call with this workspace left
+    (0, or the I4_ERR_HANDOFF code when a decode wait gave up); synchronises the device."""
+    off = _lib.lib().i4_moe_status_offset(T, H, I, E, top_k)
+    if workspace.buf is None or workspace.buf.numel() < off + 4:
+        raise RuntimeError("the workspace has not served a call of these sizes")
+    torch.cuda.synchronize(workspace.buf.device)
+    return int(workspace.buf[off:off + 4].view(torch.int32).item())
+
+
+def moe_down_wait(act: torch.Tensor, down: QWeight, logits: torch.Tensor, top_k: int,
+                  norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
+                  status: torch.Tensor | None = None, max_polls: int = 1 << 20):
+    """The down workgroups of the single-launch decode layer on their own (i4_moe_down_wait):
+    rank `logits`, wait (at most max_polls polls) until no value of act [k, I] holds the
+    pending pattern 0xFFFF, then out = residual + sum_j w_j down_{sel_j}(act_j) -> [H].
+    Returns (out, status); status (int32 [1], device) receives the I4_ERR_HANDOFF code when
+    a workgroup gave up (its rows are NaN) and is otherwise left as given (zeroed here
+    when not given)."""
+    _decode_layout(down)
+    dev = _lib.require_device(act, down.packed, logits, residual, status)
+    xt = _lib.half_code(act.dtype)
+    lg = logits.reshape(-1).to(act.dtype).contiguous()
+    rs = None if residual is None else residual.reshape(-1).to(act.dtype).contiguous()
+    if status is None:
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+    elif status.dtype != torch.int32 or status.numel() < 1:
+        raise RuntimeError("status is an int32 device tensor")
+    out = torch.empty(down.N, dtype=act.dtype, device=dev)
+    cw = down.c()
+    _lib.check(_lib.lib().i4_moe_down_wait(act.contiguous().data_ptr(), xt, ctypes.byref(cw),
+                                           lg.data_ptr(), lg.numel(), top_k,
+                                           int(norm_topk_prob), _lib.ptr(rs), out.data_ptr(),
+                                           status.data_ptr(), int(max_polls), _lib.stream(dev)))
+    return out, status
 
 
 def moe_gate_up(x: torch.Tensor, gate_up: QWeight, sel: torch.Tensor) -> torch.Tensor:
@@ -316,6 +372,10 @@ def moe_stack(x: torch.Tensor, layers: list[tuple], top_k: int,
     xf = x.reshape(-1, shape[-1]).contiguous()
     T, H = xf.shape
     gu0, dn0 = layers[0][0], layers[0][1]
+    for layer in layers:
+        if len(layer) < 3 or layer[2] is None:
+            raise RuntimeError("every layer of the stack routes with its own router weight")
+        _check_block_dtypes(x.dtype, H, layer[0].E, layer[2], layer[3] if len(layer) > 3 else None)
     arr = (_lib.MoeWeightsC * len(layers))(*[moe_weights_c(*layer) for layer in layers])
     lb = _lib.lib()
     nbytes = lb.i4_moe_stack_workspace_bytes(T, H, dn0.K, gu0.E, top_k)

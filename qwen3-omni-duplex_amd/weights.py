@@ -53,7 +53,15 @@ class QWeight:
                 continue
             if t.dim() == 2:
                 t = t.unsqueeze(0)
-            setattr(self, name, t.contiguous())
+            # Views are used in place, never copied: the descriptor carries the stride
+            # between experts (the reference's kernel takes strides too,
+            # triton_dequant_gemv.py:105-110), while each expert's rows must be dense.
+            if not _dense_per_expert(t):
+                raise ValueError(
+                    f"{name} {tuple(t.shape)} with strides {t.stride()}: each expert's "
+                    "elements must be densely laid out (only the stride between experts may "
+                    "differ); pass .contiguous() explicitly to copy")
+            setattr(self, name, t)
         if self.packed.dtype != torch.int32:
             raise ValueError("packed weights must be int32")
         if self.zeros is not None and self.zeros.dtype != torch.int32:
@@ -90,11 +98,12 @@ class QWeight:
         return self.packed.device
 
     def c(self) -> _lib.QWeightC:
-        """The i4_qweight descriptor (dense expert strides)."""
+        """The i4_qweight descriptor, with the tensors' strides between experts."""
         return _lib.QWeightC(
             packed=self.packed.data_ptr(), scale=self.scale.data_ptr(),
             zeros=None if self.zeros is None else self.zeros.data_ptr(),
-            packed_estride=0, scale_estride=0, zeros_estride=0,
+            packed_estride=_estride(self.packed), scale_estride=_estride(self.scale),
+            zeros_estride=0 if self.zeros is None else _estride(self.zeros),
             layout=_lib.LAYOUTS[self.layout], group=self.group,
             scale_dtype=_lib.dtype_code(self.scale.dtype), E=self.E, N=self.N, K=self.K)
 
@@ -121,6 +130,23 @@ class QWeight:
     def awq(qweight, scales, qzeros=None, group=128) -> "QWeight":
         q = qweight if qweight.dim() == 3 else qweight.unsqueeze(0)
         return QWeight(qweight, scales, qzeros, "awq", group, q.shape[2] * 8, q.shape[1])
+
+
+def _dense_per_expert(t: torch.Tensor) -> bool:
+    """True when every expert t[e] is row-major dense and experts do not overlap."""
+    want = 1
+    for size, stride in zip(reversed(t.shape[1:]), reversed(t.stride()[1:])):
+        if size != 1 and stride != want:
+            return False
+        want *= size
+    return t.shape[0] == 1 or t.stride(0) >= want
+
+
+def _estride(t: torch.Tensor) -> int:
+    """Element stride between experts (0: densely stacked, the descriptor's default)."""
+    if t.shape[0] == 1:
+        return 0
+    return int(t.stride(0))
 
 
 def repack_awq_to_ct(parts: list[QWeight]) -> QWeight:

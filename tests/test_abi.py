@@ -36,9 +36,10 @@ def test_every_declared_symbol_is_exported_and_bound(pkg):
 
 def test_version_and_errors(pkg):
     lib = pkg.lib()
-    assert lib.i4_abi_version() == 3
+    assert lib.i4_abi_version() == 4
     codes = {0: b"ok", -1: b"NULL", -2: b"dimension", -3: b"element type", -4: b"aligned",
-             -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride"}
+             -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride",
+             -10: b"gave up waiting", -11: b"static buffer"}
     for c, frag in codes.items():
         assert frag in lib.i4_strerror(c)
     assert b"unknown" in lib.i4_strerror(-99)
@@ -84,11 +85,13 @@ def test_call_validation_codes(pkg):
     assert lib.i4_dq_gemv(0x30000, 1, 100, ctypes.byref(w), 0x40000, 8, 0x50000, 0, None, 0, None) == -9
     assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(w), None, 8, 0x50000, 0, None, 0, None) == -1
     assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(w), 0x40000, 0, 0x50000, 0, None, 0, None) == -2
-    # AWQ needs its split-K workspace
+    # AWQ runs in one launch without a workspace, reading its scales 16 bytes at a time
     wa = _qw(_lib, layout=1)
-    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wa), 8) > 0
-    assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(wa), 0x40000, 8, 0x50000, 0, None, 0, None) == -7
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wa), 8) == 0
     assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(w), 8) == 0
+    wa_odd = _qw(_lib, layout=1, scale=0x20008)
+    assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(wa_odd), 0x40000, 8, 0x50000, 0, None, 0,
+                          None) == -4
     # routing limits
     assert lib.i4_route_topk(0x30000, 1, 1, 128, 0, 1, 0x40000, None, None, 0, None) == -2
     assert lib.i4_route_topk(0x30000, 1, 1, 1024, 8, 1, 0x40000, None, None, 0, None) == -2
@@ -258,3 +261,50 @@ def test_dense_moe_validation_codes(pkg):
                           sdn=dw(0x500000, 1, 1024, 2048))) == -2   # 16-bit shared I <= 1024
     assert call(wsb=ws - 1) == -7
     assert call(wsp=0x700008) == -4
+
+
+def test_status_word_lies_inside_the_workspace(pkg):
+    lib = pkg.lib()
+    for T, H, I, E, k in ((1, 2048, 768, 128, 8), (32, 2048, 768, 128, 8), (512, 1024, 384, 64, 6)):
+        off = lib.i4_moe_status_offset(T, H, I, E, k)
+        assert off % 4 == 0 and 0 < off and off + 4 <= lib.i4_moe_workspace_bytes(T, H, I, E, k)
+    assert lib.i4_moe_status_offset(0, 2048, 768, 128, 8) == 0
+
+
+def test_whole_row_group_is_per_channel(pkg):
+    """A group at least as long as the row is one scale per output row (the reference's
+    per-channel branch, quant/dequant.py:75-76): accepted, where other non-powers of two are
+    refused."""
+    from qwen3_omni_duplex_amd import _lib
+
+    lib = pkg.lib()
+    for group, K, code in ((768, 768, -1), (1000, 768, -1), (96, 768, -6), (48, 256, -6)):
+        w = _qw(_lib, group=group, K=K)
+        # sel = NULL: a valid weight gets as far as the pointer check
+        rc = lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(w), None, 8, 0x50000, 0, None, 0, None)
+        assert rc == code, (group, K, rc)
+
+
+def test_down_wait_validation_codes(pkg):
+    from qwen3_omni_duplex_amd import _lib
+
+    lib = pkg.lib()
+    dn = _qw(_lib, E=128, N=2048, K=768, group=128)
+    args = dict(act=0x30000, xt=1, lg=0x40000, E_r=128, k=8, renorm=1, res=None, out=0x50000,
+                status=0x60000, polls=16)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.i4_moe_down_wait(a["act"], a["xt"], ctypes.byref(dn), a["lg"], a["E_r"], a["k"],
+                                    a["renorm"], a["res"], a["out"], a["status"], a["polls"], None)
+
+    assert call(status=None) == -1
+    assert call(act=None) == -1
+    assert call(xt=0) == -3
+    assert call(k=9) == -2            # the single-launch layer covers top-k <= 8
+    assert call(E_r=129) == -2
+    assert call(polls=-1) == -2
+    assert call(out=0x50008) == -4
+    tile = _qw(_lib, E=128, N=2048, K=768, group=128, layout=2)
+    assert lib.i4_moe_down_wait(0x30000, 1, ctypes.byref(tile), 0x40000, 128, 8, 1, None, 0x50000,
+                                0x60000, 16, None) == -5

@@ -80,3 +80,44 @@ def test_shared_qkv_serves_each_slice_once_per_input(pkg):
     # the same slice twice without the others: the second call launches again
     sh.take(x, 1)
     assert len(calls) == 4
+
+
+def test_qweight_uses_expert_strided_views_in_place(pkg):
+    """A view that is strided between experts only (e.g. the up half of a stacked gate|up) is
+    used in place, its stride carried in the descriptor; a view whose rows are not dense is
+    refused instead of being copied behind the caller's back."""
+    gu = torch.arange(4 * 32 * 16, dtype=torch.int32).reshape(4, 32, 16)
+    sc = torch.ones(4, 32, 4, dtype=torch.float16)
+    up = pkg.QWeight(gu[:, 16:], sc[:, 16:], None, "ct", 32, 16, 128)
+    assert up.packed.data_ptr() == gu[:, 16:].data_ptr()   # no copy
+    c = up.c()
+    assert (c.packed_estride, c.scale_estride, c.zeros_estride) == (32 * 16, 32 * 4, 0)
+    dense = pkg.QWeight(gu, sc, None, "ct", 32, 32, 128)
+    assert dense.c().packed_estride == 32 * 16  # any stride is passed explicitly
+    one = pkg.QWeight(gu[1], sc[1], None, "ct", 32, 32, 128)
+    assert one.E == 1 and one.c().packed_estride == 0
+    with pytest.raises(ValueError, match="densely"):
+        pkg.QWeight(gu[:, :, :8], sc[:, :, :2], None, "ct", 32, 32, 64)   # rows cut short
+    with pytest.raises(ValueError, match="densely"):
+        pkg.QWeight(gu.transpose(1, 2).contiguous().transpose(1, 2), sc, None, "ct", 32, 32, 128)
+    with pytest.raises(ValueError, match="densely"):  # experts that overlap in memory
+        pkg.QWeight(gu[:1].expand(4, 32, 16), sc, None, "ct", 32, 32, 128)
+
+
+def test_block_weights_must_match_the_activation_dtype(pkg):
+    """The kernels read the router and norm weights in the activation dtype (as the
+    reference's half-precision gate Linear does, where F.linear raises on a mismatch)."""
+    from qwen3_omni_duplex_amd import ops
+
+    rw = torch.zeros(8, 64, dtype=torch.bfloat16)
+    nw = torch.ones(64, dtype=torch.float16)
+    ops._check_block_dtypes(torch.bfloat16, 64, 8, rw, None)
+    with pytest.raises(RuntimeError, match="router weight is torch.bfloat16"):
+        ops._check_block_dtypes(torch.float16, 64, 8, rw, None)
+    with pytest.raises(RuntimeError, match="norm weight"):
+        ops._check_block_dtypes(torch.bfloat16, 64, 8, rw, nw)
+    with pytest.raises(RuntimeError, match=r"\[8, 64\]"):
+        ops._check_block_dtypes(torch.bfloat16, 64, 8, rw.t().contiguous().t()[:, :32], None)
+    with pytest.raises(RuntimeError, match=r"\[8, 64\]"):
+        ops._check_block_dtypes(torch.bfloat16, 64, 8, torch.zeros(16, 64, dtype=torch.bfloat16),
+                                None)

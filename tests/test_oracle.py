@@ -309,6 +309,82 @@ def test_moe_grouped_equals_per_token():
     np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("dt,eps", [("f16", 2.0 ** -12), ("bf16", 2.0 ** -9)])
+def test_moe_expert_output_rounds_before_the_weighted_sum(dt, eps):
+    """y_dtype rounds each expert's output y_e to the activation dtype and only then weights
+    it (fused_packed_moe.py:262, (y.to(x.dtype) * w).sum(0)).  Two experts whose output is
+    1 + eps (below half an ulp above 1 in dt) give exactly sum(w) = 1 with the rounding and
+    1 + eps without it; rounding the weighted products instead would not sum to 1."""
+    H, I, E = 1, 1, 2
+    x = np.array([[1.0]])
+    g, u = 3.0, 0.5
+    a = float(i4ref.silu(np.array(g))) * u
+    Wgu = np.array([[[g], [u]]] * E)                      # gate row, up row
+    Wdn = np.array([[[(1.0 + eps) / a]]] * E)
+    sel = np.array([[0, 1]])
+    w = np.array([[0.3, 0.7]])
+    plain = i4ref.moe_layer(x, sel, w, Wgu, Wdn, None)
+    np.testing.assert_allclose(plain[0, 0], 1.0 + eps, rtol=1e-14)
+    got = i4ref.moe_layer(x, sel, w, Wgu, Wdn, None, y_dtype=dt)
+    assert got[0, 0] == pytest.approx(1.0, abs=1e-15)
+    wrong = i4ref.round_half(0.3 * (1.0 + eps), dt) + i4ref.round_half(0.7 * (1.0 + eps), dt)
+    assert abs(wrong - 1.0) > 1e-6  # the other placement is distinguishable
+    grouped = i4ref.moe_layer_grouped(x, sel, w, lambda e: Wgu[e], lambda e: Wdn[e], None,
+                                      y_dtype=dt)
+    assert grouped[0, 0] == pytest.approx(1.0, abs=1e-15)
+
+
+def test_moe_grouped_equals_per_token_with_output_rounding():
+    rng = np.random.default_rng(18)
+    E, H, I, T, k = 6, 32, 16, 9, 3
+    Wgu = rng.standard_normal((E, 2 * I, H)) * 0.1
+    Wdn = rng.standard_normal((E, H, I)) * 0.1
+    x = rng.standard_normal((T, H))
+    sel, w = i4ref.route(rng.standard_normal((T, E)), k)
+    a = i4ref.moe_layer(x, sel, w, Wgu, Wdn, "bf16", residual=x, y_dtype="bf16")
+    b = i4ref.moe_layer_grouped(x, sel, w, lambda e: Wgu[e], lambda e: Wdn[e], "bf16",
+                                residual=x, y_dtype="bf16")
+    np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-12)
+    c = i4ref.moe_layer(x, sel, w, Wgu, Wdn, "bf16", residual=x)
+    assert 0 < np.max(np.abs(a - c)) <= 2.0 ** -8 * np.max(np.abs(c))
+
+
+def test_cpu_baseline_matches_the_oracle():
+    """The timed CPU baseline (oracle/cpu_baseline.py, the reference's CPU expert path in torch
+    fp32) computes the oracle's MoE layer on seeded AWQ inputs, and its reference_gemv
+    restatement the oracle's GEMV: the figure it times is a figure of the right computation."""
+    import torch
+
+    from oracle import cpu_baseline as cb
+
+    rng = np.random.default_rng(19)
+    E, H, I, G, T, k = 12, 256, 128, 128, 5, 4
+
+    def awq(K, N):
+        return (rng.integers(-2**31, 2**31, (E, K, N // 8), dtype=np.int64).astype(np.int32),
+                rng.integers(-2**31, 2**31, (E, K // G, N // 8), dtype=np.int64).astype(np.int32),
+                rng.uniform(0.002, 0.02, (E, K // G, N)).astype(np.float16))
+
+    g, u, d = awq(H, I), awq(H, I), awq(I, H)
+    wr = (rng.standard_normal((E, H)) * 0.3).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = x.astype(np.float64) @ wr.astype(np.float64).T
+    srt = np.sort(logits, axis=1)[:, ::-1]
+    assert np.min(srt[:, k - 1] - srt[:, k]) > 1e-3  # no near-tie at the top-k cut
+    sel, w = i4ref.route(logits, k)
+    Wgu = np.concatenate([i4ref.awq_dequant(*g, G), i4ref.awq_dequant(*u, G)], axis=1)
+    Wdn = i4ref.awq_dequant(*d, G)
+    ref = i4ref.moe_layer(x, sel, w, Wgu, Wdn, None)
+    tt = lambda p: tuple(torch.from_numpy(a) for a in p)
+    got = cb.moe_layer(torch.from_numpy(x), torch.from_numpy(wr), tt(g), tt(u), tt(d), top_k=k,
+                       group=G).numpy()
+    assert i4ref.rel_err(got, ref) <= 1e-5
+    np.testing.assert_array_equal(cb.awq_unpack(torch.from_numpy(g[0])).numpy(),
+                                  i4ref.awq_nibbles(g[0]))
+    y = cb.gemv(torch.from_numpy(x[0]), *(torch.from_numpy(a[3]) for a in g), group=G).numpy()
+    assert i4ref.rel_err(y, i4ref.dq_gemv(x[0], i4ref.awq_dequant(*g, G), [3])[0]) <= 1e-5
+
+
 def test_moe_identical_experts_ignore_routing():
     """With every expert equal and renormalised weights, routing cannot matter."""
     rng = np.random.default_rng(9)
