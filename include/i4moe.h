@@ -388,6 +388,22 @@ int    i4_dmoe_forward(const void* x, int x_dtype, int T, const i4_dmoe_weights*
  * initial contents).  Calls sharing one workspace must not overlap. */
 size_t i4_dmoe_workspace_bytes(int T, int E, int topk, int I, int Is);
 
+/* ------------------------------------------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): i4_moe_forward with its workspace taken from a static
+ * device array of I4_NOALLOC_SCRATCH_BYTES inside the library, one per GPU,
+ * held until the process ends.  It allocates nothing and calls no allocating
+ * routine.  A call whose i4_moe_workspace_bytes() exceeds the array returns
+ * I4_ERR_SCRATCH without launching (8 MiB covers a decode token and batches of
+ * up to ~160 tokens at hidden 2048, FFN 768, 128 experts, top-8).  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU race. */
+#define I4_NOALLOC_SCRATCH_BYTES (8u << 20)
+int    i4_moe_forward_noalloc(const void* x, int x_dtype, int T,
+                              const i4_moe_weights* weights, int topk, int renorm,
+                              const void* logits, const void* residual, void* out,
+                              int32_t* sel_out, float* w_out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

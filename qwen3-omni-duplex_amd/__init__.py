@@ -24,7 +24,7 @@ from .loader import (Checkpoint, load_attention, load_moe_layer, load_thinker_de
 from .fused_moe import FusedMoE, fuse_moe_blocks, quantize_q8
 from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_down_wait, moe_forward,
-                  moe_gate_up, moe_route_gate_up, moe_stack, moe_status,
+                  moe_forward_noalloc, moe_gate_up, moe_route_gate_up, moe_stack, moe_status,
                   route, router_logits, unpack4, unpack_nibbles, Workspace, rmsnorm,
                   rmsnorm_linear, attn_decode, dmoe_forward)
 from .weights import QWeight, repack_awq_to_ct, repack_tile
@@ -34,7 +34,7 @@ lib = _lib.lib
 __all__ = [
     "QWeight", "repack_awq_to_ct", "repack_tile", "dequant_gemv", "linear", "unpack4", "unpack_nibbles",
     "dequant", "router_logits", "route", "moe_forward", "moe_gate_up", "moe_route_gate_up",
-    "moe_down_combine", "moe_down_wait", "moe_status",
+    "moe_down_combine", "moe_down_wait", "moe_status", "moe_forward_noalloc",
     "moe_stack", "Workspace",
     "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "PackedQKV", "QKVSlice",
     "concat_rows", "patch_attention", "TILE_ROWS", "lib",

@@ -312,6 +312,42 @@ def moe_down_wait(act: torch.Tensor, down: QWeight, logits: torch.Tensor, top_k:
     return out, status
 
 
+def moe_forward_noalloc(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
+                        router_w: torch.Tensor | None = None, logits: torch.Tensor | None = None,
+                        norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
+                        norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
+                        gate_up_tile: QWeight | None = None, down_tile: QWeight | None = None,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """moe_forward through i4_moe_forward_noalloc: the library's static per-GPU scratch
+    replaces the workspace (no device allocation by the library; `out` may be given so that
+    nothing is allocated here either).  Calls that overlap on one GPU race."""
+    dev = _lib.require_device(x, gate_up.packed, down.packed, router_w, logits, residual, norm_w,
+                              out)
+    xt = _lib.half_code(x.dtype)
+    xf = x.reshape(-1, x.shape[-1])
+    if not xf.is_contiguous():
+        raise RuntimeError("x must be contiguous")
+    T, H = xf.shape
+    E = gate_up.E
+    if router_w is None and logits is None:
+        raise RuntimeError("need router_w or logits")
+    _check_block_dtypes(x.dtype, H, E, router_w, norm_w)
+    for t, name in ((logits, "logits"), (residual, "residual")):
+        if t is not None and (t.dtype != x.dtype or not t.is_contiguous()):
+            raise RuntimeError(f"{name} must be contiguous in the activation dtype")
+    if out is None:
+        out = torch.empty(T, H, dtype=x.dtype, device=dev)
+    elif out.dtype != x.dtype or out.numel() != T * H or not out.is_contiguous():
+        raise RuntimeError("out must be a contiguous [T, H] tensor in the activation dtype")
+    mw = moe_weights_c(gate_up, down, router_w if logits is None else None, norm_w, norm_eps,
+                       gate_up_tile, down_tile)
+    _lib.check(_lib.lib().i4_moe_forward_noalloc(xf.data_ptr(), xt, T, ctypes.byref(mw), top_k,
+                                                 int(norm_topk_prob), _lib.ptr(logits),
+                                                 _lib.ptr(residual), out.data_ptr(), None, None,
+                                                 _lib.stream(dev)))
+    return out.view(x.shape)
+
+
 def moe_gate_up(x: torch.Tensor, gate_up: QWeight, sel: torch.Tensor) -> torch.Tensor:
     """Decode gate_up stage: act [k, I] = silu(gate_e x) * up_e x for e = sel (x is [H])."""
     _decode_layout(gate_up)
