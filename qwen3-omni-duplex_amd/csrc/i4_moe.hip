@@ -272,13 +272,15 @@ struct MoeOps {
                    const TW&, void*, hipStream_t);
   int (*moe_m1_ct)(const GateUpArgs&, const TW*, const TW&, const void*, void*, int32_t*, int,
                    hipStream_t);
+  int (*mfma_mixed)(bool, int, int, const void*, int, int, const int4*, const int*, const int4*,
+                    const int*, const int32_t*, const TW&, int, void*, hipStream_t);
 };
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
   return MoeOps{&launch_gate_up<XT, ST>,     &launch_down_m1<XT, ST>,
                 &launch_gate_up_ct<XT, ST>,  &launch_down_m1_ct<XT, ST>,
                 &launch_mfma_gate_up<XT, ST>, &launch_mfma_down<XT, ST>,
-                &launch_moe_m1_ct<XT, ST>};
+                &launch_moe_m1_ct<XT, ST>,   &launch_mfma_mixed<XT, ST>};
 }
 
 bool pick_ops(int xt, int gst, int dst, MoeOps* ops) {
@@ -401,7 +403,7 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   // T <= MF_TOK: no expert has more tokens than one large entry holds, and
   // small entries of <= MF_SMALL tokens cover every expert in one launch per
   // projection; above, experts with > MF_SMALL tokens take large entries
-  const bool one_list = T <= MF_TOK;
+  const bool one_list = T <= ONE_LIST_T;
   if (one_list) {  // top-k and grouping in one launch
     const size_t lds = (((size_t)Tk * 4 + 15) & ~(size_t)15) + glds;
 #define I4_RG_CASE(LT_, VPL_)                                                                  \
@@ -424,19 +426,18 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   // entry counts: sum over experts of ceil(n_e / 16) <= min(E, Tk) + Tk / 16
   const int max_s = (E < Tk ? E : Tk) + (one_list ? Tk / MF_SMALL : 0);
   const int max_b = (E < Tk / (MF_SMALL + 1) ? E : Tk / (MF_SMALL + 1)) + Tk / MF_TOK + 1;
-  rc = ops.mfma_gate_up(true, max_s, x, T, topk, ws.entries, ws.n_entries, ws.perm, tgu, I,
-                        ws.act, s);
-  if (rc) return rc;
-  if (!one_list) {
-    rc = ops.mfma_gate_up(false, max_b, x, T, topk, ws.mf_entries, ws.n_mf_entries, ws.perm, tgu,
-                          I, ws.act, s);
+  if (one_list) {
+    rc = ops.mfma_gate_up(true, max_s, x, T, topk, ws.entries, ws.n_entries, ws.perm, tgu, I,
+                          ws.act, s);
     if (rc) return rc;
-  }
-  rc = ops.mfma_down(true, max_s, ws.act, Tk, ws.entries, ws.n_entries, ws.perm, tdn, ws.ys, s);
-  if (rc) return rc;
-  if (!one_list) {
-    rc = ops.mfma_down(false, max_b, ws.act, Tk, ws.mf_entries, ws.n_mf_entries, ws.perm, tdn,
-                       ws.ys, s);
+    rc = ops.mfma_down(true, max_s, ws.act, Tk, ws.entries, ws.n_entries, ws.perm, tdn, ws.ys, s);
+    if (rc) return rc;
+  } else {  // large and small entries of a projection share one launch
+    rc = ops.mfma_mixed(true, max_b, max_s, x, T, topk, ws.mf_entries, ws.n_mf_entries,
+                        ws.entries, ws.n_entries, ws.perm, tgu, I, ws.act, s);
+    if (rc) return rc;
+    rc = ops.mfma_mixed(false, max_b, max_s, ws.act, Tk, topk, ws.mf_entries, ws.n_mf_entries,
+                        ws.entries, ws.n_entries, ws.perm, tdn, I, ws.ys, s);
     if (rc) return rc;
   }
   const int64_t tot = (int64_t)T * H;

@@ -10,6 +10,8 @@
 namespace i4 {
 
 static constexpr int MF_TOK = 64;    // tokens per entry of the large-entry MFMA kernel
+static constexpr int LIN_TOK = 64;   // rows per tile of the dense linear MFMA launch
+static constexpr int ONE_LIST_T = 64;  // up to this many tokens: small entries only
 static constexpr int MF_SMALL = 16;  // experts with at most this many tokens: one m-block
 static constexpr int MF_NB = 2;      // n-blocks of 16 weight rows per wave
 
@@ -67,6 +69,15 @@ int launch_mfma_gate_up(bool small, int max_entries, const void* x, int T, int t
 template <int XT, int ST>
 int launch_mfma_down(bool small, int max_entries, const void* act, int rows, const int4* ent,
                      const int* nent, const int32_t* perm, const TW& w, void* ys, hipStream_t s);
+
+// Both lists of one projection in one launch: large entries in grid rows
+// [0, max_large), small ones after them.  gate_up: src = x, out = act;
+// down: src = act, out = ys.
+template <int XT, int ST>
+int launch_mfma_mixed(bool gate_up, int max_large, int max_small, const void* src, int src_rows,
+                      int topk, const int4* large, const int* n_large, const int4* small,
+                      const int* n_small, const int32_t* perm, const TW& w, int I, void* out,
+                      hipStream_t s);
 
 // Dense linear layer on MFMA: y[M][N] = x[M][K] W^T (+ bias, dtype ot), W one
 // tile-layout weight (E = 1, N % 128 == 0).  Small grids are split along K

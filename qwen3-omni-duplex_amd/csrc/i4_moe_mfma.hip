@@ -218,13 +218,18 @@ __device__ inline void correct(f32x4& res, const f32x4& d, u32 sraw, u32 zw, int
 // 1, blockIdx.z takes the z-th of ksplit contiguous ranges of superchunks and
 // writes its fp32 partial sums to part[z][row][n] instead (k_linear_finish
 // adds them up).
-template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN = false>
-__global__ __launch_bounds__(256) void k_tile_mfma(
-    const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ entries,
-    const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
-    uint16_t* __restrict__ act, float* __restrict__ ys, int M = 0,
-    const void* __restrict__ bias = nullptr, int ot = 0, int ksplit = 1,
-    float* __restrict__ part = nullptr) {
+// The body takes its block coordinates (bx: column tile, by: entry, bz: K range)
+// and its LDS (two staging buffers of 16 MB tokens, XSB uint4 apart, and two
+// activation-sum buffers, XSUMB floats apart) from the kernel that runs it, so one
+// launch can serve entries of both sizes (k_tile_mfma_mixed).
+template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN>
+__device__ inline void tile_mfma_body(
+    int bx, int by, int bz, u32x4* __restrict__ xs0, int XSB, float* __restrict__ xsum0,
+    int XSUMB, const uint16_t* __restrict__ src, u32 src_bytes, int topk,
+    const int4* __restrict__ entries, const int* __restrict__ n_entries,
+    const int32_t* __restrict__ perm, const TW& w, int I, uint16_t* __restrict__ act,
+    float* __restrict__ ys, int M, const void* __restrict__ bias, int ot, int ksplit,
+    float* __restrict__ part) {
   constexpr bool EXACT = XT == I4_F16;
   // fp16 with several m-blocks folds the scale into B (see the top); one
   // m-block keeps the exact form, whose extra registers fit its occupancy
@@ -232,32 +237,34 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
   constexpr int COLS = GATEUP ? 32 * NB : 64 * NB;
   constexpr int TOK = 16 * MB;
   static_assert(!GATEUP || NB % 2 == 0, "gate_up pairs gate and up blocks");
-  static_assert(MB == 1 || MB == 4, "staging maps 256 threads onto 16 or 64 tokens");
-  __shared__ u32x4 xs[2][TOK * MF_TSTRIDE];
-  __shared__ float xsum[2][TOK * 4];  // bf16: per token and chunk
+  static_assert(MB == 1 || MB == 4 || MB == 8, "staging maps 256 threads onto 16, 64 or 128 tokens");
+  // 128-token tiles stage one superchunk at a time (the LDS of two would halve occupancy)
+  constexpr bool DBUF = MB <= 4;
   static_assert(!(LIN && GATEUP), "a linear layer is a plain projection");
-  if (!LIN && (int)blockIdx.y >= *n_entries) return;
+  auto XS = [&](int buf, int i) -> u32x4& { return xs0[buf * XSB + i]; };
+  auto XSUM = [&](int buf, int i) -> float& { return xsum0[buf * XSUMB + i]; };
+  if (!LIN && by >= *n_entries) return;
   const u32 mg = magic_v<XT>();
-  const int4 en = LIN ? int4{0, (int)blockIdx.y * TOK, min(TOK, M - (int)blockIdx.y * TOK), 0}
-                      : entries[blockIdx.y];
+  const int4 en = LIN ? int4{0, by * TOK, min(TOK, M - by * TOK), 0} : entries[by];
   const int e = en.x, pos0 = en.y, cnt = en.z;
   const int K = w.K, SC_ALL = K >> 7;
   // superchunks [scb, scb + SC) of this workgroup (all of them unless split)
-  const int scb = LIN ? ((int)blockIdx.z * SC_ALL) / ksplit : 0;
-  const int SC = LIN ? (((int)blockIdx.z + 1) * SC_ALL) / ksplit - scb : SC_ALL;
+  const int scb = LIN ? (bz * SC_ALL) / ksplit : 0;
+  const int SC = LIN ? ((bz + 1) * SC_ALL) / ksplit - scb : SC_ALL;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, ln = lane & 15, kb = lane >> 4;
   const bool ev = (unsigned)e < (unsigned)w.E;
   const int nmb = MB == 1 ? 1 : (cnt + 15) >> 4;
   int blk[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) blk[nb] = nblock<GATEUP, NB>(blockIdx.x, wave, nb, I);
+  for (int nb = 0; nb < NB; ++nb) blk[nb] = nblock<GATEUP, NB>(bx, wave, nb, I);
   const WBuf<ST, NB> wb = wbuf<ST, NB>(w, ev ? e : 0, blk, ln, kb);
-  // staging role: MB = 4: token tid / 4, chunk tid % 4 (its 4 words);
-  //               MB = 1: token tid / 16, word tid % 16
+  // staging role: token tid / (16 / MB), words MB (tid % (16 / MB)) .. + MB - 1 of its
+  // 16 (MB = 1: one word; 4: one chunk; 8: two chunks)
   constexpr int WPT = MB;  // 16-byte words per thread and superchunk
-  const int tk = MB == 4 ? (int)threadIdx.x >> 2 : (int)threadIdx.x >> 4;
-  const int kw = MB == 4 ? 4 * ((int)threadIdx.x & 3) : (int)threadIdx.x & 15;  // first word
+  constexpr int TPT = 16 / MB;  // threads per staged token
+  const int tk = (int)threadIdx.x / TPT;
+  const int kw = MB * ((int)threadIdx.x % TPT);  // first word
   const int row = GATEUP ? perm[pos0 + min(tk, cnt - 1)] / topk : pos0 + min(tk, cnt - 1);
   const rsrc_t xr = rsrc(src, src_bytes);
   const u32 vx = ((u32)row * (u32)K + 8u * (u32)kw) * 2u;
@@ -276,18 +283,24 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     for (int q = 0; q < WPT; ++q) dst[q] = bload16(xr, vx + 16u * q, sc * 256);
   };
   auto commit_x = [&](int buf, const u32x4* src_x) {
-    float sm = 0.f;
+    float sm = 0.f, sm1 = 0.f;  // sm1: the second chunk of a two-chunk thread (MB = 8)
 #pragma unroll
     for (int q = 0; q < WPT; ++q) {
-      xs[buf][tk * MF_TSTRIDE + kw + q] = src_x[q];
-      if constexpr (!EXACT) sm += sum8<XT>(src_x[q]).y;
+      XS(buf, tk * MF_TSTRIDE + kw + q) = src_x[q];
+      if constexpr (!EXACT) {
+        if (q < 4) sm += sum8<XT>(src_x[q]).y;
+        else sm1 += sum8<XT>(src_x[q]).y;
+      }
     }
     if constexpr (!EXACT) {
       if constexpr (MB == 1) {
         sm = group_sum<4>(sm);  // the chunk's 4 words sit in 4 adjacent lanes
-        if ((kw & 3) == 0) xsum[buf][4 * tk + (kw >> 2)] = sm;
-      } else {
-        xsum[buf][4 * tk + (kw >> 2)] = sm;
+        if ((kw & 3) == 0) XSUM(buf, 4 * tk + (kw >> 2)) = sm;
+      } else if constexpr (MB == 4) {
+        XSUM(buf, 4 * tk + (kw >> 2)) = sm;
+      } else {  // two chunks per thread
+        XSUM(buf, 4 * tk + (kw >> 2)) = sm;
+        XSUM(buf, 4 * tk + (kw >> 2) + 1) = sm1;
       }
     }
   };
@@ -304,7 +317,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
   auto rows_sum = [&](int buf, int mb, int t0, int nt, float (&sm)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float* p = &xsum[buf][4 * (16 * mb + 4 * kb + i)];
+      const float* p = &XSUM(buf, 4 * (16 * mb + 4 * kb + i));
       float v = 0.f;
       for (int t = t0; t < t0 + nt; ++t) v += p[t];
       sm[i] = v;
@@ -333,7 +346,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
           return scale_b(b_operand<XT>(word_t(sl[nb].w, t), z2, mg), sc2);
         };
         if constexpr (MB == 1) {  // one m-block: each B operand feeds one MFMA
-          const u32x4 a = xs[buf][ln * MF_TSTRIDE + 4 * t + kb];
+          const u32x4 a = XS(buf, ln * MF_TSTRIDE + 4 * t + kb);
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) res[0][nb] = mfma16<XT>(a, bop(nb), res[0][nb]);
         } else {
@@ -343,7 +356,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
             if (mb < nmb) {
-              const u32x4 a = xs[buf][(16 * mb + ln) * MF_TSTRIDE + 4 * t + kb];
+              const u32x4 a = XS(buf, (16 * mb + ln) * MF_TSTRIDE + 4 * t + kb);
 #pragma unroll
               for (int nb = 0; nb < NB; ++nb) res[mb][nb] = mfma16<XT>(a, b[nb], res[mb][nb]);
             }
@@ -363,7 +376,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
     for (int t = 0; t < 4; ++t) {
       const int g = (4 * sc + t) >> w.gshift;
       if constexpr (MB == 1) {  // one m-block: each B operand feeds one MFMA
-        const u32x4 a = xs[buf][ln * MF_TSTRIDE + 4 * t + kb];
+        const u32x4 a = XS(buf, ln * MF_TSTRIDE + 4 * t + kb);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
           d[0][nb] = mfma16<XT>(
@@ -377,7 +390,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
           if (mb < nmb) {
-            const u32x4 a = xs[buf][(16 * mb + ln) * MF_TSTRIDE + 4 * t + kb];
+            const u32x4 a = XS(buf, (16 * mb + ln) * MF_TSTRIDE + 4 * t + kb);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) d[mb][nb] = mfma16<XT>(a, b[nb], d[mb][nb]);
           }
@@ -418,7 +431,8 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
   // nothing reads): a staging store inside the guard would let the compiler
   // sink the activation load down to it and lose the prefetch.
   auto step = [&](int sc, Slot& sl) {
-    const int buf = sc & 1;
+    const int buf = DBUF ? sc & 1 : 0;
+    if constexpr (!DBUF) __syncthreads();  // the previous superchunk's reads are done
     if constexpr (MB == 1) {
       commit_x(buf, &sl.x);
     } else {
@@ -459,16 +473,16 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
         if constexpr (GATEUP) {
 #pragma unroll
           for (int nb = 0; nb < NB / 2; ++nb) {
-            const int n = blockIdx.x * COLS + 16 * (NB / 2) * wave + 16 * nb + ln;
+            const int n = bx * COLS + 16 * (NB / 2) * wave + 16 * nb + ln;
             const float v =
                 ev ? silu(res[mb][nb][i]) * res[mb][nb + NB / 2][i] : __builtin_nanf("");
             act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
           }
         } else if constexpr (LIN) {
-          const int n0 = blockIdx.x * COLS + 16 * NB * wave + ln;
+          const int n0 = bx * COLS + 16 * NB * wave + ln;
           const int64_t o = (int64_t)(pos0 + m) * w.N + n0;
           if (ksplit > 1) {
-            float* pz = part + (int64_t)blockIdx.z * M * w.N;
+            float* pz = part + (int64_t)bz * M * w.N;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) pz[o + 16 * nb] = res[mb][nb][i];
             continue;
@@ -489,7 +503,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
             }
           }
         } else {
-          const int64_t o = (int64_t)perm[pos0 + m] * w.N + blockIdx.x * COLS + 16 * NB * wave + ln;
+          const int64_t o = (int64_t)perm[pos0 + m] * w.N + bx * COLS + 16 * NB * wave + ln;
 #pragma unroll
           // the expert's output in the activation dtype (k_moe_combine sums the slots)
           for (int nb = 0; nb < NB; ++nb)
@@ -498,6 +512,47 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
       }
     }
   }
+}
+
+template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN = false>
+__global__ __launch_bounds__(256) void k_tile_mfma(
+    const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ entries,
+    const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
+    uint16_t* __restrict__ act, float* __restrict__ ys, int M = 0,
+    const void* __restrict__ bias = nullptr, int ot = 0, int ksplit = 1,
+    float* __restrict__ part = nullptr) {
+  constexpr int TOK = 16 * MB;
+  constexpr int NBUF = MB <= 4 ? 2 : 1;  // 128-token tiles are staged single-buffered
+  __shared__ u32x4 xs[NBUF][TOK * MF_TSTRIDE];
+  __shared__ float xsum[NBUF][TOK * 4];  // bf16: per token and chunk
+  tile_mfma_body<XT, ST, GB, GATEUP, NB, MB, LIN>(
+      blockIdx.x, blockIdx.y, blockIdx.z, &xs[0][0], TOK * MF_TSTRIDE, &xsum[0][0], TOK * 4, src,
+      src_bytes, topk, entries, n_entries, perm, w, I, act, ys, M, bias, ot, ksplit, part);
+}
+
+// Both entry lists of a projection in one launch: rows [0, max_large) of the grid
+// take the large entries (four m-blocks), the rest the small ones (one m-block).
+// The large ones come first, so the longest workgroups are dispatched first and
+// the small entries' weight streaming fills the machine behind them.
+template <int XT, int ST, bool GB, bool GATEUP, int NB>
+__global__ __launch_bounds__(256) void k_tile_mfma_mixed(
+    const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ large,
+    const int* __restrict__ n_large, int max_large, const int4* __restrict__ small,
+    const int* __restrict__ n_small, const int32_t* __restrict__ perm, TW w, int I,
+    uint16_t* __restrict__ act, float* __restrict__ ys) {
+  constexpr int TOKL = MF_TOK;
+  constexpr int NBUF = MF_TOK <= 64 ? 2 : 1;  // 128-token tiles are staged single-buffered
+  __shared__ u32x4 xs[NBUF * TOKL * MF_TSTRIDE];
+  __shared__ float xsum[NBUF * TOKL * 4];
+  const int y = blockIdx.y;
+  if (y < max_large)
+    tile_mfma_body<XT, ST, GB, GATEUP, NB, MF_TOK / 16, false>(
+        blockIdx.x, y, 0, xs, TOKL * MF_TSTRIDE, xsum, TOKL * 4, src, src_bytes,
+        topk, large, n_large, perm, w, I, act, ys, 0, nullptr, 0, 1, nullptr);
+  else
+    tile_mfma_body<XT, ST, GB, GATEUP, NB, 1, false>(
+        blockIdx.x, y - max_large, 0, xs, 16 * MF_TSTRIDE, xsum, 16 * 4, src,
+        src_bytes, topk, small, n_small, perm, w, I, act, ys, 0, nullptr, 0, 1, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -547,6 +602,41 @@ int launch_mfma_down(bool small, int max_entries, const void* act, int rows, con
                                       nullptr, (float*)ys, s);
 }
 
+// both entry lists of one projection in one launch (k_tile_mfma_mixed)
+template <int XT, int ST, bool GB, bool GATEUP>
+static int mixed_t(int max_large, int max_small, const void* src, int src_rows, int topk,
+                   const int4* large, const int* n_large, const int4* small, const int* n_small,
+                   const int32_t* perm, const TW& w, int I, void* act, void* ys, hipStream_t s) {
+  const int64_t src_bytes = (int64_t)src_rows * w.K * 2;
+  if (src_bytes >= ((int64_t)1 << 31) || (int64_t)w.N * w.K / 2 >= ((int64_t)1 << 31))
+    return I4_ERR_SHAPE;
+  const int n_out = GATEUP ? I : w.N;
+  const int cols = GATEUP ? 32 * MF_NB : 64 * MF_NB;
+  hipLaunchKernelGGL((k_tile_mfma_mixed<XT, ST, GB, GATEUP, MF_NB>),
+                     dim3(n_out / cols, max_large + max_small), dim3(256), 0, s,
+                     (const uint16_t*)src, (u32)src_bytes, topk, large, n_large, max_large, small,
+                     n_small, perm, w, I, (uint16_t*)act, (float*)ys);
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+template <int XT, int ST>
+int launch_mfma_mixed(bool gate_up, int max_large, int max_small, const void* src, int src_rows,
+                      int topk, const int4* large, const int* n_large, const int4* small,
+                      const int* n_small, const int32_t* perm, const TW& w, int I, void* out,
+                      hipStream_t s) {
+  // gate_up: src = x [T][H], out = act; down: src = act [rows][I], out = ys
+  const bool gb = w.gshift >= 2;
+  if (gate_up)
+    return gb ? mixed_t<XT, ST, true, true>(max_large, max_small, src, src_rows, topk, large,
+                                            n_large, small, n_small, perm, w, I, out, nullptr, s)
+              : mixed_t<XT, ST, false, true>(max_large, max_small, src, src_rows, topk, large,
+                                             n_large, small, n_small, perm, w, I, out, nullptr, s);
+  return gb ? mixed_t<XT, ST, true, false>(max_large, max_small, src, src_rows, 0, large, n_large,
+                                           small, n_small, perm, w, 0, nullptr, out, s)
+            : mixed_t<XT, ST, false, false>(max_large, max_small, src, src_rows, 0, large,
+                                            n_large, small, n_small, perm, w, 0, nullptr, out, s);
+}
+
 // y[r][n] = sum_z part[z][r][n] + bias[n] in dtype ot, the K ranges in order
 __global__ __launch_bounds__(256) void k_linear_finish(const float* __restrict__ part, int ksplit,
                                                        int64_t total, int N,
@@ -573,7 +663,7 @@ __global__ __launch_bounds__(256) void k_linear_finish(const float* __restrict__
 // (few rows or few columns) is split along K until it has about 512
 // workgroups, each range keeping at least 4 superchunks
 int linear_ksplit(int M, int N, int K) {
-  const int tiles = (N / (64 * MF_NB)) * ((M + MF_TOK - 1) / MF_TOK);
+  const int tiles = (N / (64 * MF_NB)) * ((M + LIN_TOK - 1) / LIN_TOK);
   const int sc = K / 128;
   if (tiles >= 256 || sc < 8) return 1;
   int ks = (512 + tiles - 1) / tiles;
@@ -594,7 +684,7 @@ int launch_mfma_linear(const void* x, int M, const TW& w, const void* bias, void
   const int64_t src_bytes = (int64_t)M * w.K * 2;
   if (src_bytes >= ((int64_t)1 << 31) || (int64_t)w.N * w.K / 2 >= ((int64_t)1 << 31))
     return I4_ERR_SHAPE;
-  constexpr int COLS = 64 * MF_NB, TOK = MF_TOK;
+  constexpr int COLS = 64 * MF_NB, TOK = LIN_TOK;
   if (w.N % COLS != 0 || w.K % 128 != 0 || w.E != 1) return I4_ERR_SHAPE;
   const int ks = linear_ksplit(M, w.N, w.K);
   if (ks > 1 && (!ws || ws_bytes < linear_tile_workspace_bytes(M, w.N, w.K)))
@@ -625,7 +715,10 @@ int launch_mfma_linear(const void* x, int M, const TW& w, const void* bias, void
                                              hipStream_t);                                     \
   template int launch_mfma_down<XT_, ST_>(bool, int, const void*, int, const int4*,            \
                                           const int*, const int32_t*, const TW&, void*,        \
-                                          hipStream_t);
+                                          hipStream_t);                                        \
+  template int launch_mfma_mixed<XT_, ST_>(bool, int, int, const void*, int, int, const int4*, \
+                                           const int*, const int4*, const int*, const int32_t*, \
+                                           const TW&, int, void*, hipStream_t);
 I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
 I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)
 #undef I4_INST
