@@ -70,9 +70,9 @@ template <int XT, int ST>
 int launch_mfma_down(bool small, int max_entries, const void* act, int rows, const int4* ent,
                      const int* nent, const int32_t* perm, const TW& w, void* ys, hipStream_t s);
 
-// Both lists of one projection in one launch: large entries in grid rows
-// [0, max_large), small ones after them.  gate_up: src = x, out = act;
-// down: src = act, out = ys.
+// Both lists of one projection in one launch over max_large + max_small grid
+// rows: the large entries first, the small ones right after them, idle rows
+// last.  gate_up: src = x, out = act; down: src = act, out = ys.
 template <int XT, int ST>
 int launch_mfma_mixed(bool gate_up, int max_large, int max_small, const void* src, int src_rows,
                       int topk, const int4* large, const int* n_large, const int4* small,

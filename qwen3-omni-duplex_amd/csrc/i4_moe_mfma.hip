@@ -530,28 +530,30 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
       src_bytes, topk, entries, n_entries, perm, w, I, act, ys, M, bias, ot, ksplit, part);
 }
 
-// Both entry lists of a projection in one launch: rows [0, max_large) of the grid
-// take the large entries (four m-blocks), the rest the small ones (one m-block).
-// The large ones come first, so the longest workgroups are dispatched first and
-// the small entries' weight streaming fills the machine behind them.
+// Both entry lists of a projection in one launch: rows [0, n_large) of the grid
+// take the large entries (four m-blocks), the next n_small rows the small ones
+// (one m-block) and the rest of the grid (sized for the worst case) exits.  The
+// large ones come first, so the longest workgroups are dispatched first and the
+// small entries' weight streaming fills the machine behind them; the idle rows
+// come last, so no small entry waits behind their dispatch.
 template <int XT, int ST, bool GB, bool GATEUP, int NB>
 __global__ __launch_bounds__(256) void k_tile_mfma_mixed(
     const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ large,
-    const int* __restrict__ n_large, int max_large, const int4* __restrict__ small,
+    const int* __restrict__ n_large, const int4* __restrict__ small,
     const int* __restrict__ n_small, const int32_t* __restrict__ perm, TW w, int I,
     uint16_t* __restrict__ act, float* __restrict__ ys) {
   constexpr int TOKL = MF_TOK;
   constexpr int NBUF = MF_TOK <= 64 ? 2 : 1;  // 128-token tiles are staged single-buffered
   __shared__ u32x4 xs[NBUF * TOKL * MF_TSTRIDE];
   __shared__ float xsum[NBUF * TOKL * 4];
-  const int y = blockIdx.y;
-  if (y < max_large)
+  const int y = blockIdx.y, nl = *n_large;
+  if (y < nl)
     tile_mfma_body<XT, ST, GB, GATEUP, NB, MF_TOK / 16, false>(
         blockIdx.x, y, 0, xs, TOKL * MF_TSTRIDE, xsum, TOKL * 4, src, src_bytes,
         topk, large, n_large, perm, w, I, act, ys, 0, nullptr, 0, 1, nullptr);
   else
     tile_mfma_body<XT, ST, GB, GATEUP, NB, 1, false>(
-        blockIdx.x, y - max_large, 0, xs, 16 * MF_TSTRIDE, xsum, 16 * 4, src,
+        blockIdx.x, y - nl, 0, xs, 16 * MF_TSTRIDE, xsum, 16 * 4, src,
         src_bytes, topk, small, n_small, perm, w, I, act, ys, 0, nullptr, 0, 1, nullptr);
 }
 
@@ -614,8 +616,8 @@ static int mixed_t(int max_large, int max_small, const void* src, int src_rows, 
   const int cols = GATEUP ? 32 * MF_NB : 64 * MF_NB;
   hipLaunchKernelGGL((k_tile_mfma_mixed<XT, ST, GB, GATEUP, MF_NB>),
                      dim3(n_out / cols, max_large + max_small), dim3(256), 0, s,
-                     (const uint16_t*)src, (u32)src_bytes, topk, large, n_large, max_large, small,
-                     n_small, perm, w, I, (uint16_t*)act, (float*)ys);
+                     (const uint16_t*)src, (u32)src_bytes, topk, large, n_large, small, n_small,
+                     perm, w, I, (uint16_t*)act, (float*)ys);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
