@@ -67,7 +67,7 @@
 extern "C" {
 #endif
 
-#define I4_ABI_VERSION 4
+#define I4_ABI_VERSION 5
 
 /* status codes */
 #define I4_OK               0
@@ -387,6 +387,29 @@ int    i4_dmoe_forward(const void* x, int x_dtype, int T, const i4_dmoe_weights*
 /* Workspace of i4_dmoe_forward (logits, routing, activations; 16-byte aligned, no
  * initial contents).  Calls sharing one workspace must not overlap. */
 size_t i4_dmoe_workspace_bytes(int T, int E, int topk, int I, int Is);
+
+/* One decode token (T = 1) with router_w in the block and 16-bit routed experts
+ * runs in two launches:
+ * the router's, which also marks the activations pending, and one launch
+ * whose gate|up workgroups write them while its down workgroups rank the
+ * logits themselves and poll the activations until no value still holds the
+ * pending pattern 0xFFFF (topk * I + Is <= 4096).  Byte offset, in the
+ * workspace of i4_dmoe_forward with these sizes, of the int32 status word
+ * every call rewrites: I4_OK, or I4_ERR_HANDOFF when a down workgroup gave up
+ * waiting (its output row is then NaN).  As for i4_moe_status_offset, the
+ * wait assumes block-order dispatch (no reference counterpart). */
+size_t i4_dmoe_status_offset(int T, int E, int topk, int I, int Is);
+
+/* The down workgroups of that launch on their own, for one token (T = 1) with
+ * the given [E] logits: they poll the workspace's activations as they are,
+ * at most max_polls times, and a workgroup that gives up writes NaN to its
+ * row and I4_ERR_HANDOFF to the status word (only the failure is stored).
+ * 16-bit routed experts.  For testing the bounded wait from the host (the
+ * reference's block, fused_moe.py:99-141, has no such wait). */
+int    i4_dmoe_down_wait(const void* x, int x_dtype, const i4_dmoe_weights* weights,
+                         int topk, int renorm, const void* logits, const void* residual,
+                         void* out, void* workspace, size_t workspace_bytes, int max_polls,
+                         hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * No counterpart in the reference.  For callers that cannot allocate device

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libi4moe.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # element types and layouts (include/i4moe.h)
 F32, F16, BF16 = 0, 1, 2
@@ -120,6 +120,10 @@ SIGNATURES = {
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_size_t, c_void_p]),
     "i4_dmoe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "i4_dmoe_status_offset": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "i4_dmoe_down_wait": (c_int, [c_void_p, c_int, POINTER(DmoeWeightsC), c_int, c_int,
+                                  c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_int,
+                                  c_void_p]),
 }
 
 _lib = None

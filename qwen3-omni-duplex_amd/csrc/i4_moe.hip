@@ -178,13 +178,21 @@ __global__ __launch_bounds__(1024) void k_route_group(
   if (status && threadIdx.x == 0) *status = I4_OK;  // nothing on this path waits
   int32_t* sel_l = (int32_t*)lds;  // [T][topk]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int t = wave; t < T; t += blockDim.x >> 6) {
-    u32 raw[VPL];
-    load_row<LT, VPL>(logits, t, E, raw);
-    int my_sel = 0;
-    float my_w = 0.f;
-    topk_row<LT, VPL>(raw, t, E, topk, renorm, sel, wts, nullptr, 0, &my_sel, &my_w);
-    if (lane < topk) sel_l[t * topk + lane] = my_sel;
+  // every row of the wave's tokens in flight before the first ranking
+  constexpr int RPW = ONE_LIST_T / 16;  // tokens per wave at most (16 waves)
+  u32 raw[RPW][VPL];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+    if (wave + 16 * r < T) load_row<LT, VPL>(logits, wave + 16 * r, E, raw[r]);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int t = wave + 16 * r;
+    if (t < T) {
+      int my_sel = 0;
+      float my_w = 0.f;
+      topk_row<LT, VPL>(raw[r], t, E, topk, renorm, sel, wts, nullptr, 0, &my_sel, &my_w);
+      if (lane < topk) sel_l[t * topk + lane] = my_sel;
+    }
   }
   __syncthreads();
   group_body(sel_l, T, topk, E, lo_max, lo_chunk, perm, entries, n_entries, mf_entries,

@@ -97,31 +97,35 @@ __global__ __launch_bounds__(256) void k_router_m1(
 // product needs (8 l + 512 i) -- forms their partial sums in the same order and
 // reduces each group of 64 with the same wave sum, so r, the normalised words
 // and the logit are those of k_router_m1.  No LDS, no barrier.
-template <int XT, bool NORM>
+// H = 1024 (the Talker's hidden size) works the same way with lanes standing in
+// for threads l and l + 64 only: k_router_m1's waves 2 and 3 hold no words and
+// add zeros.
+template <int XT, bool NORM, int H>
 __global__ __launch_bounds__(64) void k_router_m1w(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, int E,
     const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
     uint16_t* __restrict__ logits, u32x4* __restrict__ pend, int n_pend,
     int32_t* __restrict__ status) {
-  constexpr int H = 2048, W = H / 8;  // words of x; lane l owns words l + 64 i
+  static_assert(H == 1024 || H == 2048, "one 512-value round per 64 lanes, 2 or 4 rounds");
+  constexpr int NR = H / 512;  // lane l owns words l + 64 i, i < NR
   for (int i = blockIdx.x * 64 + (int)threadIdx.x; i < n_pend; i += gridDim.x * 64)
     pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
   if (status && blockIdx.x == 0 && threadIdx.x == 0) *status = I4_OK;
   const int lane = threadIdx.x, e = blockIdx.x;
-  u32x4 xv[4], gv[4], wv[4];
+  u32x4 xv[NR], gv[NR], wv[NR];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NR; ++i) {
     xv[i] = ldg16(x + 8 * (lane + 64 * i));
     if constexpr (NORM) gv[i] = ldg16(nw + 8 * (lane + 64 * i));
     wv[i] = ldg16(wr + (int64_t)e * H + 8 * lane + 512 * i);
   }
   if constexpr (NORM) {
-    float ws[4];
+    float ws[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ws[i] = group_sum<64>(sumsq8<XT>(xv[i]));  // wave i's sum
+    for (int i = 0; i < NR; ++i) ws[i] = group_sum<64>(sumsq8<XT>(xv[i]));  // wave i's sum
     const float r = 1.0f / sqrtf(((ws[0] + ws[1]) + (ws[2] + ws[3])) / (float)H + eps);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NR; ++i) {
       xv[i].x = norm_pair<XT>(xv[i].x, gv[i].x, r);
       xv[i].y = norm_pair<XT>(xv[i].y, gv[i].y, r);
       xv[i].z = norm_pair<XT>(xv[i].z, gv[i].z, r);
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(64) void k_router_m1w(
   }
   float a = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NR; ++i) {
     a = Half<XT>::dot2(wv[i].x, xv[i].x, a);
     a = Half<XT>::dot2(wv[i].y, xv[i].y, a);
     a = Half<XT>::dot2(wv[i].z, xv[i].z, a);
@@ -139,7 +143,6 @@ __global__ __launch_bounds__(64) void k_router_m1w(
   }
   a = group_sum<64>(a);
   if (lane == 0) logits[e] = Half<XT>::from_f32(a);
-  (void)W;
 }
 
 // T > 1, pass 1: RMSNorm of one token per workgroup with exactly the
@@ -273,14 +276,16 @@ int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr,
                             const void* norm_w, float eps, void* xn, void* logits, hipStream_t s,
                             void* pend, int n_pend, int32_t* status) {
   dim3 grid((E + 3) / 4, 1);
-  if (T == 1 && H == 2048) {  // one wavefront per expert
-#define I4_RM1W_CASE(XT_, N_)                                                                  \
-  if (xt == XT_ && (norm_w != nullptr) == N_)                                                  \
-    hipLaunchKernelGGL((k_router_m1w<XT_, N_>), dim3(E), dim3(64), 0, s, (const uint16_t*)x,   \
-                       (const uint16_t*)wr, E, (const uint16_t*)norm_w, eps, (uint16_t*)xn,    \
-                       (uint16_t*)logits, (u32x4*)pend, n_pend, status);
-    I4_RM1W_CASE(I4_F16, true) else I4_RM1W_CASE(I4_F16, false) else I4_RM1W_CASE(I4_BF16, true)
-    else I4_RM1W_CASE(I4_BF16, false)
+  if (T == 1 && (H == 2048 || H == 1024)) {  // one wavefront per expert
+#define I4_RM1W_CASE(XT_, N_, H_)                                                              \
+  if (xt == XT_ && (norm_w != nullptr) == N_ && H == H_)                                       \
+    hipLaunchKernelGGL((k_router_m1w<XT_, N_, H_>), dim3(E), dim3(64), 0, s,                   \
+                       (const uint16_t*)x, (const uint16_t*)wr, E, (const uint16_t*)norm_w,    \
+                       eps, (uint16_t*)xn, (uint16_t*)logits, (u32x4*)pend, n_pend, status);
+    I4_RM1W_CASE(I4_F16, true, 2048) else I4_RM1W_CASE(I4_F16, false, 2048)
+    else I4_RM1W_CASE(I4_BF16, true, 2048) else I4_RM1W_CASE(I4_BF16, false, 2048)
+    else I4_RM1W_CASE(I4_F16, true, 1024) else I4_RM1W_CASE(I4_F16, false, 1024)
+    else I4_RM1W_CASE(I4_BF16, true, 1024) else I4_RM1W_CASE(I4_BF16, false, 1024)
 #undef I4_RM1W_CASE
   } else if (T == 1) {
 #define I4_RM1_CASE(XT_, N_)                                                                  \

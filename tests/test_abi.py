@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported_and_bound(pkg):
 
 def test_version_and_errors(pkg):
     lib = pkg.lib()
-    assert lib.i4_abi_version() == 4
+    assert lib.i4_abi_version() == 5
     codes = {0: b"ok", -1: b"NULL", -2: b"dimension", -3: b"element type", -4: b"aligned",
              -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride",
              -10: b"gave up waiting", -11: b"static buffer"}
@@ -261,6 +261,31 @@ def test_dense_moe_validation_codes(pkg):
                           sdn=dw(0x500000, 1, 1024, 2048))) == -2   # 16-bit shared I <= 1024
     assert call(wsb=ws - 1) == -7
     assert call(wsp=0x700008) == -4
+
+    # the single-launch block's down stage on its own: one token, given logits
+    def wait(w=None, xt=2, k=6, logits=0x50000, polls=16, wsb=ws):
+        w = weights() if w is None else w
+        return lib.i4_dmoe_down_wait(0x30000, xt, ctypes.byref(w), k, 1, logits, None, 0x40000,
+                                     0x700000, wsb, polls, None)
+
+    assert wait(xt=0) == -3
+    assert wait(logits=None) == -2                              # ranks the given logits
+    assert wait(polls=-1) == -2
+    assert wait(k=8) == -2
+    assert wait(wsb=ws - 1) == -7
+    big = weights(dn=dw(0x200000, 128, 1024, 1024), gu=dw(0x100000, 128, 2048, 1024))
+    assert wait(w=big, wsb=1 << 30) == -2                       # 6 x 1024 + 768 > 4096 staged
+    q8 = weights(gu=dw(0x100000, 128, 768, 1024, scale=0x800000),
+                 dn=dw(0x200000, 128, 1024, 384, scale=0x900000))
+    assert wait(w=q8) == -3                                     # int8 experts: three launches
+
+
+def test_dense_moe_status_word_lies_inside_the_workspace(pkg):
+    lib = pkg.lib()
+    for T, E, k, I, Is in ((1, 128, 6, 384, 768), (5, 128, 6, 384, 0), (1, 16, 4, 48, 32)):
+        off = lib.i4_dmoe_status_offset(T, E, k, I, Is)
+        assert off % 4 == 0 and 0 < off and off + 4 <= lib.i4_dmoe_workspace_bytes(T, E, k, I, Is)
+    assert lib.i4_dmoe_status_offset(0, 128, 6, 384, 768) == 0
 
 
 def test_status_word_lies_inside_the_workspace(pkg):

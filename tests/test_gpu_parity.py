@@ -787,11 +787,14 @@ def test_router_logits_with_norm(pkg, dev, T):
 
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("norm", [False, True])
-def test_router_tokens_match_single_token_bits(pkg, dev, xdt, norm):
+@pytest.mark.parametrize("H", [2048, 1024, 768])
+def test_router_tokens_match_single_token_bits(pkg, dev, xdt, norm, H):
     """The multi-token router gives every token the logits and RMSNorm output it gets alone,
-    bit for bit (so routing never depends on the batch), including a ragged last tile."""
+    bit for bit (so routing never depends on the batch), including a ragged last tile; the
+    single-token router is the one-wavefront-per-expert kernel at H = 2048 (the Thinker) and
+    1024 (the Talker), the four-wavefront one otherwise."""
     rng = np.random.default_rng(41)
-    E, H, T = 128, 2048, 19
+    E, T = 128, 19
     wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
     wr = i4ref.f32_to_bf16_bits(wr) if xdt == "bf16" else wr.astype(np.float16)
     x = t_(make_x(rng, (T, H), xdt), dev)

@@ -102,12 +102,79 @@ def test_dmoe_variants(pkg, dev, case):
     _check(pkg, _stacks(dev, torch.bfloat16, seed=3), torch.bfloat16, 3, **case)
 
 
+@pytest.mark.parametrize("case", [
+    dict(shared=False), dict(gate=False), dict(residual=True), dict(renorm=False),
+    dict(top_k=7), dict(shared=False, top_k=8), dict(q8=True, residual=True),
+    dict(dt=torch.float16, q8=True, gate=False),
+])
+def test_dmoe_single_launch_variants(pkg, dev, case):
+    """One token with the router in the block: with 16-bit experts gate|up and down run in
+    one launch (the down workgroups rank the logits, make the shared gate and wait for the
+    activations), int8 experts in two."""
+    print(f"dmoe single launch {case}", flush=True)
+    case = dict(case)
+    dt = case.pop("dt", torch.bfloat16)
+    _check(pkg, _stacks(dev, dt, seed=6), dt, 1, **case)
+
+
+def test_dmoe_single_launch_equals_two_launches(pkg, dev):
+    """The single-launch decode block and the two-launch path over the same logits give the
+    same output, routing and weights bit for bit, in bf16 and int8 modes."""
+    for dt, q8 in ((torch.bfloat16, False), (torch.bfloat16, True), (torch.float16, False)):
+        S = _stacks(dev, dt, seed=7)
+        x = S["x"][:1].contiguous()
+        gu, dn, gus, dns = S["gu"], S["dn"], None, None
+        if q8:
+            gu, gus = pkg.quantize_q8(S["gu"])
+            dn, dns = pkg.quantize_q8(S["dn"])
+        kw = dict(gate_up_scale=gus, down_scale=dns, shared_gate_up=S["sgu"],
+                  shared_down=S["sdn"], shared_gate_w=S["sgw"], residual=S["res"][:1],
+                  return_routing=True)
+        a = pkg.dmoe_forward(x, gu, dn, K, router_w=S["rw"], **kw)
+        b = pkg.dmoe_forward(x, gu, dn, K, logits=pkg.router_logits(x, S["rw"]), **kw)
+        torch.cuda.synchronize()
+        for u, v in zip(a, b):
+            assert torch.equal(u, v), f"single launch differs (dt={dt}, q8={q8})"
+
+
+def test_dmoe_wait_gives_up_visibly(pkg, dev):
+    """The down workgroups of the single-launch block run alone with their bound on the wait
+    lowered from the host: with the activations left pending they give up, write NaN and
+    report I4_ERR_HANDOFF, and every kernel exits; with the activations in place (left by a
+    full call on the same workspace) they reproduce that call's output bit for bit; the
+    status word reads I4_OK after ordinary calls whatever the workspace held."""
+    S = _stacks(dev, torch.bfloat16, seed=8)
+    x = S["x"][:1].contiguous()
+    kw = dict(shared_gate_up=S["sgu"], shared_down=S["sdn"], shared_gate_w=S["sgw"],
+              residual=S["res"][:1])
+    ws = pkg.Workspace()
+    nb = pkg.ops.dmoe_workspace_bytes(1, E, K, I, IS)
+    for T in (1, 3, 1):
+        ws.get(pkg.ops.dmoe_workspace_bytes(T, E, K, I, IS), dev).fill_(0xA5)
+        pkg.dmoe_forward(S["x"][:T].contiguous(), S["gu"], S["dn"], K, router_w=S["rw"],
+                         workspace=ws, shared_gate_up=S["sgu"], shared_down=S["sdn"],
+                         shared_gate_w=S["sgw"])
+        assert pkg.dmoe_status(ws, T, E, K, I, IS) == 0
+    want = pkg.dmoe_forward(x, S["gu"], S["dn"], K, router_w=S["rw"], workspace=ws, **kw)
+    lg = pkg.router_logits(x, S["rw"])
+    got = pkg.dmoe_down_wait(x, S["gu"], S["dn"], K, lg, ws, max_polls=4, **kw)
+    assert pkg.dmoe_status(ws, 1, E, K, I, IS) == 0
+    assert torch.equal(got, want.reshape(-1))
+    for polls in (0, 3):
+        ws.get(nb, dev).fill_(0xFF)  # every activation pending, status word included
+        ws.buf[pkg.lib().i4_dmoe_status_offset(1, E, K, I, IS):][:4].zero_()
+        out = pkg.dmoe_down_wait(x, S["gu"], S["dn"], K, lg, ws, max_polls=polls, **kw)
+        assert pkg.dmoe_status(ws, 1, E, K, I, IS) == -10
+        assert torch.isnan(out.float()).all()
+
+
 def test_dmoe_small_shapes(pkg, dev):
     """H 256, 16 experts (one logit per lane pair), I 48, shared 32: the clamped
     chunk and row paths (fewer chunks than lanes)."""
     S = _stacks(dev, torch.bfloat16, seed=4, E=16, I=48, Is=32, H=256)
-    _check(pkg, S, torch.bfloat16, 4, top_k=4)
-    _check(pkg, S, torch.bfloat16, 4, top_k=4, q8=True)
+    for T in (4, 1):
+        _check(pkg, S, torch.bfloat16, T, top_k=4)
+        _check(pkg, S, torch.bfloat16, T, top_k=4, q8=True)
 
 
 def test_dmoe_is_deterministic(pkg, dev):
