@@ -295,12 +295,14 @@ template <int L> __device__ inline float group_sum(float v) {
 // issue() puts up to 4 loads per thread in flight and returns; the caller
 // issues its weight loads next and only then commit()s, so the LDS writes
 // wait for the activations alone (loads retire in issue order).
-template <int XT> struct Stager {
+// NT: the workgroup size, a compile-time constant in the index arithmetic
+// (every user launches 256 threads)
+template <int XT, int NT = 256> struct Stager {
   u32x4 d[4];
   int total, words, C;
   __device__ inline Stager(int nr, int K) : total(nr * (K >> 3)), words(K >> 3), C(K >> 5) {}
   template <class RowOf> __device__ inline void issue(RowOf row_of, int i0) {
-    const int nt = blockDim.x;
+    constexpr int nt = NT;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int idx = min(i0 + u * nt + (int)threadIdx.x, total - 1);
@@ -309,7 +311,7 @@ template <int XT> struct Stager {
     }
   }
   __device__ inline void commit(int i0, u32x4* xs, float2* sums) {
-    const int nt = blockDim.x;
+    constexpr int nt = NT;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int idx = i0 + u * nt + (int)threadIdx.x;
@@ -324,9 +326,9 @@ template <int XT> struct Stager {
       }
     }
   }
-  // everything beyond the first round (rows longer than 4 * blockDim words)
+  // everything beyond the first round (rows longer than 4 * NT words)
   template <class RowOf> __device__ inline void rest(RowOf row_of, u32x4* xs, float2* sums) {
-    for (int i0 = 4 * (int)blockDim.x; i0 < total; i0 += 4 * (int)blockDim.x) {
+    for (int i0 = 4 * NT; i0 < total; i0 += 4 * NT) {
       issue(row_of, i0);
       commit(i0, xs, sums);
     }

@@ -188,7 +188,7 @@ template <int L> struct DownShape {
 // sees: the bound guarantees that every wave exits.
 template <int XT>
 __device__ inline bool poll_rows(Stager<XT>& st, const uint16_t* src, int max_polls) {
-  const int nt = blockDim.x;
+  constexpr int nt = WG;
   const rsrc_t r = rsrc(src, (u32)st.total * 16u);
   for (int it = 0;; ++it) {
     bool pend = false;
