@@ -643,376 +643,3 @@ def dmoe_forward(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, top
     if return_routing:
         return out, sel, wts
     return out
-
-
-def moe_status(workspace: Workspace, T: int, H: int, I: int, E: int, top_k: int) -> int:
-    """The status word the last i4_moe_forward / stack call with this workspace left
-    (0, or the I4_ERR_HANDOFF code when a decode wait gave up); synchronises the device."""
-    off = _lib.lib().i4_moe_status_offset(T, H, I, E, top_k)
-    if workspace.buf is None or workspace.buf.numel() < off + 4:
-        raise RuntimeError("the workspace has not served a call of these sizes")
-    torch.cuda.synchronize(workspace.buf.device)
-    return int(workspace.buf[off:off + 4].view(torch.int32).item())
-
-
-def moe_down_wait(act: torch.Tensor, down: QWeight, logits: torch.Tensor, top_k: int,
-                  norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
-                  status: torch.Tensor | None = None, max_polls: int = 1 << 20):
-    """The down workgroups of the single-launch decode layer on their own (i4_moe_down_wait):
-    rank `logits`, wait (at most max_polls polls) until no value of act [k, I] holds the
-    pending pattern 0xFFFF, then out = residual + sum_j w_j down_{sel_j}(act_j) -> [H].
-    Returns (out, status); status (int32 [1], device) receives the I4_ERR_HANDOFF code when
-    a workgroup gave up (its rows are NaN) and is otherwise left as given (zeroed here
-    when not given)."""
-    _decode_layout(down)
-    dev = _lib.require_device(act, down.packed, logits, residual, status)
-    xt = _lib.half_code(act.dtype)
-    lg = logits.reshape(-1).to(act.dtype).contiguous()
-    rs = None if residual is None else residual.reshape(-1).to(act.dtype).contiguous()
-    if status is None:
-        status = torch.zeros(1, dtype=torch.int32, device=dev)
-    elif status.dtype != torch.int32 or status.numel() < 1:
-        raise RuntimeError("status is an int32 device tensor")
-    out = torch.empty(down.N, dtype=act.dtype, device=dev)
-    cw = down.c()
-    _lib.check(_lib.lib().i4_moe_down_wait(act.contiguous().data_ptr(), xt, ctypes.byref(cw),
-                                           lg.data_ptr(), lg.numel(), top_k,
-                                           int(norm_topk_prob), _lib.ptr(rs), out.data_ptr(),
-                                           status.data_ptr(), int(max_polls), _lib.stream(dev)))
-    return out, status
-
-
-def moe_forward_noalloc(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
-                        router_w: torch.Tensor | None = None, logits: torch.Tensor | None = None,
-                        norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
-                        norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
-                        gate_up_tile: QWeight | None = None, down_tile: QWeight | None = None,
-                        out: torch.Tensor | None = None) -> torch.Tensor:
-    """moe_forward through i4_moe_forward_noalloc: the library's static per-GPU scratch
-    replaces the workspace (no device allocation by the library; `out` may be given so that
-    nothing is allocated here either).  Calls that overlap on one GPU race."""
-    dev = _lib.require_device(x, gate_up.packed, down.packed, router_w, logits, residual, norm_w,
-                              out)
-    xt = _lib.half_code(x.dtype)
-    xf = x.reshape(-1, x.shape[-1])
-    if not xf.is_contiguous():
-        raise RuntimeError("x must be contiguous")
-    T, H = xf.shape
-    E = gate_up.E
-    if router_w is None and logits is None:
-        raise RuntimeError("need router_w or logits")
-    _check_block_dtypes(x.dtype, H, E, router_w, norm_w)
-    for t, name in ((logits, "logits"), (residual, "residual")):
-        if t is not None and (t.dtype != x.dtype or not t.is_contiguous()):
-            raise RuntimeError(f"{name} must be contiguous in the activation dtype")
-    if out is None:
-        out = torch.empty(T, H, dtype=x.dtype, device=dev)
-    elif out.dtype != x.dtype or out.numel() != T * H or not out.is_contiguous():
-        raise RuntimeError("out must be a contiguous [T, H] tensor in the activation dtype")
-    mw = moe_weights_c(gate_up, down, router_w if logits is None else None, norm_w, norm_eps,
-                       gate_up_tile, down_tile)
-    _lib.check(_lib.lib().i4_moe_forward_noalloc(xf.data_ptr(), xt, T, ctypes.byref(mw), top_k,
-                                                 int(norm_topk_prob), _lib.ptr(logits),
-                                                 _lib.ptr(residual), out.data_ptr(), None, None,
-                                                 _lib.stream(dev)))
-    return out.view(x.shape)
-
-
-def moe_gate_up(x: torch.Tensor, gate_up: QWeight, sel: torch.Tensor) -> torch.Tensor:
-    """Decode gate_up stage: act [k, I] = silu(gate_e x) * up_e x for e = sel (x is [H])."""
-    _decode_layout(gate_up)
-    dev = _lib.require_device(x, gate_up.packed, sel)
-    xt = _lib.half_code(x.dtype)
-    xc = x.reshape(-1).contiguous()
-    s32 = sel.reshape(-1).to(torch.int32).contiguous()
-    act = torch.empty(s32.numel(), gate_up.N // 2, dtype=x.dtype, device=dev)
-    cw = gate_up.c()
-    _lib.check(_lib.lib().i4_moe_gate_up(xc.data_ptr(), xt, ctypes.byref(cw), s32.data_ptr(),
-                                         s32.numel(), act.data_ptr(), _lib.stream(dev)))
-    return act
-
-
-def moe_route_gate_up(x: torch.Tensor, gate_up: QWeight, logits: torch.Tensor, top_k: int,
-                      norm_topk_prob: bool = True):
-    """Decode routing + gate_up stage in one launch: (act [k, I], sel [k] int32, w [k] fp32)."""
-    _decode_layout(gate_up)
-    dev = _lib.require_device(x, gate_up.packed, logits)
-    xt = _lib.half_code(x.dtype)
-    xc = x.reshape(-1).contiguous()
-    lg = logits.reshape(-1).to(x.dtype).contiguous()
-    act = torch.empty(top_k, gate_up.N // 2, dtype=x.dtype, device=dev)
-    sel = torch.empty(top_k, dtype=torch.int32, device=dev)
-    w = torch.empty(top_k, dtype=torch.float32, device=dev)
-    cw = gate_up.c()
-    _lib.check(_lib.lib().i4_moe_route_gate_up(xc.data_ptr(), xt, ctypes.byref(cw), lg.data_ptr(),
-                                               lg.numel(), top_k, int(norm_topk_prob),
-                                               sel.data_ptr(), w.data_ptr(), act.data_ptr(),
-                                               _lib.stream(dev)))
-    return act, sel, w
-
-
-def moe_down_combine(act: torch.Tensor, down: QWeight, sel: torch.Tensor, w: torch.Tensor,
-                     residual: torch.Tensor | None = None) -> torch.Tensor:
-    """Decode down stage: residual + sum_j w[j] down_{sel[j]}(act[j]) -> [H]."""
-    _decode_layout(down)
-    dev = _lib.require_device(act, down.packed, sel, w, residual)
-    xt = _lib.half_code(act.dtype)
-    s32 = sel.reshape(-1).to(torch.int32).contiguous()
-    wf = w.reshape(-1).to(torch.float32).contiguous()
-    rs = None if residual is None else residual.reshape(-1).to(act.dtype).contiguous()
-    out = torch.empty(down.N, dtype=act.dtype, device=dev)
-    cw = down.c()
-    _lib.check(_lib.lib().i4_moe_down_combine(act.contiguous().data_ptr(), xt, ctypes.byref(cw),
-                                              s32.data_ptr(), wf.data_ptr(), s32.numel(),
-                                              _lib.ptr(rs), out.data_ptr(), _lib.stream(dev)))
-    return out
-
-
-def moe_stack(x: torch.Tensor, layers: list[tuple], top_k: int,
-              norm_topk_prob: bool = True, workspace: Workspace | None = None) -> torch.Tensor:
-    """h <- h + moe_l(norm_l(h)) over layers
-    [(gate_up, down, router_w[, norm_w[, eps[, gate_up_tile, down_tile]]]), ...]."""
-    dev = _lib.require_device(x)
-    xt = _lib.half_code(x.dtype)
-    shape = x.shape
-    xf = x.reshape(-1, shape[-1]).contiguous()
-    T, H = xf.shape
-    gu0, dn0 = layers[0][0], layers[0][1]
-    for layer in layers:
-        if len(layer) < 3 or layer[2] is None:
-            raise RuntimeError("every layer of the stack routes with its own router weight")
-        _check_block_dtypes(x.dtype, H, layer[0].E, layer[2], layer[3] if len(layer) > 3 else None)
-    arr = (_lib.MoeWeightsC * len(layers))(*[moe_weights_c(*layer) for layer in layers])
-    lb = _lib.lib()
-    nbytes = lb.i4_moe_stack_workspace_bytes(T, H, dn0.K, gu0.E, top_k)
-    ws = (workspace or Workspace()).get(nbytes, dev)
-    out = torch.empty_like(xf)
-    _lib.check(lb.i4_moe_stack_forward(xf.data_ptr(), xt, T, arr, len(layers), top_k,
-                                       int(norm_topk_prob), out.data_ptr(), ws.data_ptr(),
-                                       ws.numel(), _lib.stream(dev)))
-    return out.view(shape)
-
-
-def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """Qwen3OmniMoeThinkerTextRMSNorm over the last dim (i4_rmsnorm), in x.dtype."""
-    dev = _lib.require_device(x, weight)
-    if weight.dtype != x.dtype:
-        raise RuntimeError("the norm weight must have the activation dtype")
-    xf = x.reshape(-1, x.shape[-1]).contiguous()
-    out = torch.empty_like(xf)
-    _lib.check(_lib.lib().i4_rmsnorm(xf.data_ptr(), _lib.half_code(x.dtype), xf.shape[0],
-                                     xf.shape[1], weight.contiguous().data_ptr(), float(eps),
-                                     out.data_ptr(), _lib.stream(dev)))
-    return out.view(x.shape)
-
-
-def attn_decode(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: torch.Tensor,
-                k_norm_w: torch.Tensor, eps: float, inv_freq: torch.Tensor,
-                pos: int | torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                workspace: Workspace | None = None) -> torch.Tensor:
-    """Decode attention of one token (i4_attn_decode) between the q/k/v and o projections:
-    qkv [n_heads + 2 n_kv_heads, head_dim] in, [n_heads * head_dim] out; appends k / v at
-    row `pos` of the caches [n_kv_heads, max_len, head_dim] and attends rows [0, pos].
-    inv_freq is the host fp32 table of the rotary embedding ([head_dim / 2]).  pos may be an
-    int32 device tensor of one element (i4_attn_decode_at): the kernels read it, so a
-    captured graph serves every position."""
-    dev = _lib.require_device(qkv, q_norm_w, k_norm_w, k_cache, v_cache)
-    pos_dev = None
-    if isinstance(pos, torch.Tensor):
-        if pos.device != dev or pos.dtype != torch.int32 or pos.numel() != 1:
-            raise RuntimeError("a device position is one int32 on the tensors' device")
-        pos_dev = pos
-    xt = _lib.half_code(qkv.dtype)
-    nkv, max_len, hd = k_cache.shape
-    if k_cache.dtype != qkv.dtype or v_cache.shape != k_cache.shape or v_cache.dtype != qkv.dtype:
-        raise RuntimeError("the caches must be [n_kv_heads, max_len, head_dim] in the activation dtype")
-    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
-        raise RuntimeError("the caches must be contiguous")
-    if qkv.numel() != (n_heads + 2 * n_kv_heads) * hd or nkv != n_kv_heads:
-        raise RuntimeError("qkv / cache shapes do not match the head counts")
-    tab = inv_freq.detach().to("cpu", torch.float32).contiguous()
-    if tab.numel() != hd // 2:
-        raise RuntimeError("inv_freq must hold head_dim / 2 values")
-    lb = _lib.lib()
-    nbytes = lb.i4_attn_decode_workspace_bytes(n_heads, hd, max_len)
-    ws = (workspace or Workspace()).get(nbytes, dev)
-    out = torch.empty(n_heads * hd, dtype=qkv.dtype, device=dev)
-    args = (qkv.contiguous().data_ptr(), xt, n_heads, n_kv_heads, hd,
-            q_norm_w.contiguous().data_ptr(), k_norm_w.contiguous().data_ptr(), float(eps),
-            tab.data_ptr())
-    tail = (k_cache.data_ptr(), v_cache.data_ptr(), max_len, out.data_ptr(), ws.data_ptr(),
-            ws.numel(), _lib.stream(dev))
-    if pos_dev is None:
-        _lib.check(lb.i4_attn_decode(*args, int(pos), *tail))
-    else:
-        _lib.check(lb.i4_attn_decode_at(*args, pos_dev.data_ptr(), *tail))
-    return out
-
-
-def rmsnorm_linear(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: QWeight,
-                   bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None):
-    """y = RMSNorm(x) W^T (+ bias) in one launch (i4_rmsnorm_linear; CT weight, K <= 4096),
-    equal bit for bit to linear(rmsnorm(x, norm_w, eps), w, bias)."""
-    dev = _lib.require_device(x, norm_w, w.packed, bias)
-    if norm_w.dtype != x.dtype:
-        raise RuntimeError("the norm weight must have the activation dtype")
-    flat = x.reshape(-1, w.K).contiguous()
-    M = flat.shape[0]
-    od = out_dtype or x.dtype
-    y = torch.empty(M, w.N, dtype=od, device=dev)
-    b = None if bias is None else bias.to(od).contiguous()
-    cw = w.c()
-    _lib.check(_lib.lib().i4_rmsnorm_linear(flat.data_ptr(), _lib.half_code(x.dtype), M,
-                                            norm_w.contiguous().data_ptr(), float(eps),
-                                            ctypes.byref(cw), _lib.ptr(b), y.data_ptr(),
-                                            _lib.dtype_code(od), _lib.stream(dev)))
-    return y.view(*x.shape[:-1], w.N)
-
-
-def dweight_c(data: torch.Tensor, scale: torch.Tensor | None = None) -> _lib.DWeightC:
-    """struct i4_dweight of a stacked weight [E, N, K] (or one matrix [N, K]):
-    16-bit values, or int8 with one scale per output row ([E, N] or [E, N, 1])."""
-    if data.dim() == 2:
-        data = data.unsqueeze(0)
-    if data.dim() != 3 or not data.is_contiguous():
-        raise ValueError("a stacked weight is a contiguous [E, N, K] tensor")
-    E, N, K = data.shape
-    if scale is None:
-        if data.dtype not in (torch.float16, torch.bfloat16):
-            raise ValueError(f"16-bit weights expected, got {data.dtype} (int8 needs a scale)")
-    else:
-        if data.dtype != torch.int8:
-            raise ValueError(f"scaled weights are int8, got {data.dtype}")
-        if scale.numel() != E * N or not scale.is_contiguous():
-            raise ValueError("one contiguous scale per output row ([E, N]) expected")
-    return _lib.DWeightC(data=data.data_ptr(), scale=_lib.ptr(scale), E=E, N=N, K=K)
-
-
-def dmoe_workspace_bytes(T: int, E: int, top_k: int, I: int, Is: int) -> int:
-    return _lib.lib().i4_dmoe_workspace_bytes(T, E, top_k, I, Is)
-
-
-def _dmoe_weights(dtype, gate_up, down, rw, gate_up_scale, down_scale, shared_gate_up,
-                  shared_down, shared_gate_w, shared_gate_up_scale, shared_down_scale):
-    """struct i4_dmoe_weights, and the converted tensors it points into (kept alive by
-    the caller until the call is queued)."""
-    sgw = None if shared_gate_w is None else shared_gate_w.reshape(-1).to(dtype).contiguous()
-    dw = _lib.DmoeWeightsC(gate_up=dweight_c(gate_up, gate_up_scale),
-                           down=dweight_c(down, down_scale), router_w=_lib.ptr(rw),
-                           shared_gate_w=_lib.ptr(sgw))
-    if shared_gate_up is not None:
-        dw.shared_gate_up = dweight_c(shared_gate_up, shared_gate_up_scale)
-        dw.shared_down = dweight_c(shared_down, shared_down_scale)
-    return dw, (rw, sgw)
-
-
-def dmoe_status(workspace: Workspace, T: int, E: int, top_k: int, I: int, Is: int) -> int:
-    """The status word the last dmoe_forward call with this workspace left (0, or the
-    I4_ERR_HANDOFF code when a down workgroup of the single-launch decode block gave up
-    waiting for its activations); synchronises the device."""
-    off = _lib.lib().i4_dmoe_status_offset(T, E, top_k, I, Is)
-    if workspace.buf is None or workspace.buf.numel() < off + 4:
-        raise RuntimeError("the workspace has not served a call of these sizes")
-    torch.cuda.synchronize(workspace.buf.device)
-    return int(workspace.buf[off:off + 4].view(torch.int32).item())
-
-
-def dmoe_down_wait(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, top_k: int,
-                   logits: torch.Tensor, workspace: Workspace, norm_topk_prob: bool = True,
-                   gate_up_scale: torch.Tensor | None = None,
-                   down_scale: torch.Tensor | None = None,
-                   shared_gate_up: torch.Tensor | None = None,
-                   shared_down: torch.Tensor | None = None,
-                   shared_gate_w: torch.Tensor | None = None,
-                   shared_gate_up_scale: torch.Tensor | None = None,
-                   shared_down_scale: torch.Tensor | None = None,
-                   residual: torch.Tensor | None = None, max_polls: int = 1 << 20):
-    """The down workgroups of dmoe_forward's single-launch decode block on their own
-    (i4_dmoe_down_wait), for one token: they rank `logits`, poll the workspace's
-    activations as they are (at most max_polls times) and compute the block's output [H];
-    a workgroup that gives up writes NaN and leaves I4_ERR_HANDOFF in the status word
-    (dmoe_status)."""
-    dev = _lib.require_device(x, gate_up, down, logits, shared_gate_up, shared_down,
-                              shared_gate_w, residual)
-    xt = _lib.half_code(x.dtype)
-    xf = x.reshape(-1).contiguous()
-    H = xf.numel()
-    E, I = gate_up.shape[0], gate_up.shape[1] // 2
-    Is = 0 if shared_gate_up is None else shared_gate_up.shape[-2] // 2
-    lg = logits.reshape(E).to(x.dtype).contiguous()
-    rs = None if residual is None else residual.reshape(H).to(x.dtype).contiguous()
-    out = torch.empty(H, dtype=x.dtype, device=dev)
-    dw, keep = _dmoe_weights(x.dtype, gate_up, down, None, gate_up_scale, down_scale,
-                             shared_gate_up, shared_down, shared_gate_w, shared_gate_up_scale,
-                             shared_down_scale)
-    lb = _lib.lib()
-    ws = workspace.get(lb.i4_dmoe_workspace_bytes(1, E, top_k, I, Is), dev)
-    _lib.check(lb.i4_dmoe_down_wait(xf.data_ptr(), xt, ctypes.byref(dw), top_k,
-                                    int(norm_topk_prob), lg.data_ptr(), _lib.ptr(rs),
-                                    out.data_ptr(), ws.data_ptr(), ws.numel(), int(max_polls),
-                                    _lib.stream(dev)))
-    del keep
-    return out
-
-
-def dmoe_forward(x: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, top_k: int,
-                 router_w: torch.Tensor | None = None, logits: torch.Tensor | None = None,
-                 norm_topk_prob: bool = True, gate_up_scale: torch.Tensor | None = None,
-                 down_scale: torch.Tensor | None = None,
-                 shared_gate_up: torch.Tensor | None = None,
-                 shared_down: torch.Tensor | None = None,
-                 shared_gate_w: torch.Tensor | None = None,
-                 shared_gate_up_scale: torch.Tensor | None = None,
-                 shared_down_scale: torch.Tensor | None = None,
-                 residual: torch.Tensor | None = None, return_routing: bool = False,
-                 workspace: Workspace | None = None):
-    """MoE block on 16-bit / int8 experts with an optional gated shared expert
-    (FusedMoE.forward, src/duplex/streaming/fused_moe.py:99-141):
-      out = residual + sum_j w_j down_e(silu(gate_e x) * up_e x)
-            + sigmoid(shared_gate_w . x) * down_s(silu(gate_s x) * up_s x)
-    gate_up [E, 2I, H] (gate rows first), down [E, H, I]; int8 weights come with
-    per-output-row scales in the activation dtype.  Three launches (router
-    logits, gate_up + SiLU + routing, down + combine); one token with router_w and 16-bit
-    experts runs in two (router logits; gate_up and down in one launch, the down
-    workgroups waiting for the activations: dmoe_status reports a wait that gave up)."""
-    dev = _lib.require_device(x, gate_up, down, router_w, logits, shared_gate_up, shared_down,
-                              shared_gate_w, residual)
-    xt = _lib.half_code(x.dtype)
-    for s in (gate_up_scale, down_scale, shared_gate_up_scale, shared_down_scale):
-        if s is not None and s.dtype != x.dtype:
-            raise ValueError(f"int8 scales must be in the activation dtype {x.dtype}, got {s.dtype}")
-    for w in (gate_up, down, shared_gate_up, shared_down):
-        if w is not None and w.dtype != torch.int8 and w.dtype != x.dtype:
-            raise ValueError(f"16-bit weights must be in the activation dtype {x.dtype}")
-    if router_w is None and logits is None:
-        raise RuntimeError("need router_w or logits")
-    if (shared_gate_up is None) != (shared_down is None):
-        raise ValueError("give the shared expert's gate|up and down together")
-    shape = x.shape
-    xf = x.reshape(-1, shape[-1]).contiguous()
-    T, H = xf.shape
-    E, I = gate_up.shape[0], gate_up.shape[1] // 2
-    Is = 0 if shared_gate_up is None else shared_gate_up.shape[-2] // 2
-    rw = None if router_w is None else router_w.to(x.dtype).contiguous()
-    lg = None if router_w is not None else logits.reshape(T, E).to(x.dtype).contiguous()
-    sgw = None if shared_gate_w is None else shared_gate_w.reshape(-1).to(x.dtype).contiguous()
-    rs = None if residual is None else residual.reshape(T, H).to(x.dtype).contiguous()
-    out = torch.empty(T, H, dtype=x.dtype, device=dev)
-    sel = torch.empty(T, top_k, dtype=torch.int32, device=dev) if return_routing else None
-    wts = torch.empty(T, top_k, dtype=torch.float32, device=dev) if return_routing else None
-    dw = _lib.DmoeWeightsC(gate_up=dweight_c(gate_up, gate_up_scale),
-                           down=dweight_c(down, down_scale), router_w=_lib.ptr(rw),
-                           shared_gate_w=_lib.ptr(sgw))
-    if shared_gate_up is not None:
-        dw.shared_gate_up = dweight_c(shared_gate_up, shared_gate_up_scale)
-        dw.shared_down = dweight_c(shared_down, shared_down_scale)
-    lb = _lib.lib()
-    ws = (workspace or Workspace()).get(lb.i4_dmoe_workspace_bytes(T, E, top_k, I, Is), dev)
-    _lib.check(lb.i4_dmoe_forward(xf.data_ptr(), xt, T, ctypes.byref(dw), top_k,
-                                  int(norm_topk_prob), _lib.ptr(lg), _lib.ptr(rs),
-                                  out.data_ptr(), _lib.ptr(sel), _lib.ptr(wts), ws.data_ptr(),
-                                  ws.numel(), _lib.stream(dev)))
-    out = out.view(shape)
-    if return_routing:
-        return out, sel, wts
-    return out
