@@ -233,49 +233,59 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   }
 }
 
-// One workgroup of HD threads per query head merges its chunks:
-// out = sum_c w_c acc_c / sum_c w_c l_c with w_c = exp(m_c - max_c m_c), in chunk
-// order.  The chunk statistics are read by all threads at once and the weights kept
-// in LDS, so the accumulator loads of the final pass are independent.
+// One workgroup of HD threads per query head merges its chunks (flash-decoding):
+// out = o / L with a running maximum M over the chunks in chunk order,
+// L = sum_c l_c e^(m_c - M), o = sum_c acc_c e^(m_c - M).  Every load of a batch of
+// CMB_B chunks (their statistics, read alike by all threads, and thread t's
+// accumulator value) is issued before any is used, so a context of up to
+// 64 CMB_B positions costs one memory round trip.
 static constexpr int CMB = 1024;  // chunks per head at most (max_len <= 65536)
+static constexpr int CMB_B = 16;  // chunks per batch of loads
 template <int XT>
 __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ part, int nq,
                                                      const int32_t* __restrict__ pos_dev,
                                                      int pos_host, int max_len,
                                                      uint16_t* __restrict__ out) {
-  __shared__ float s_w[CMB];
-  __shared__ float s_r[2][HD / 64];
-  const int h = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int h = blockIdx.x, t = threadIdx.x;
   const int pos = pos_dev ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_host;
   if (pos < 0 || pos >= max_len) {  // no row to attend: the chunk kernel wrote nothing
     out[(int64_t)h * HD + t] = Half<XT>::QNAN;
     return;
   }
   const int nch = (pos + ACH) / ACH;
-  auto at = [&](int c) { return part + ((int64_t)c * nq + h) * PSTR; };
-  float m = -__builtin_inff();
-  for (int c = t; c < nch; c += HD) {
-    s_w[c] = at(c)[0];
-    m = fmaxf(m, s_w[c]);
+  // raw buffer loads, all issued unconditionally (clamped chunk index): a guarded
+  // load would be waited for where its branch joins
+  const rsrc_t pr = rsrc(part, (u32)nch * (u32)nq * (u32)PSTR * 4u);
+  const u32 vml = (u32)h * PSTR * 4u, vac = vml + (4u + (u32)t) * 4u;
+  const u32 cs = (u32)nq * PSTR * 4u;  // bytes between chunks
+  float M = -__builtin_inff(), L = 0.f, o = 0.f;
+  for (int cb = 0; cb < nch; cb += CMB_B) {
+    float m[CMB_B], l[CMB_B], a[CMB_B];
+#pragma unroll
+    for (int i = 0; i < CMB_B; ++i) {
+      const int so = (int)((u32)min(cb + i, nch - 1) * cs);
+      const u32 m_b = __builtin_amdgcn_raw_buffer_load_b32(pr, vml, so, 0);
+      const u32 l_b = __builtin_amdgcn_raw_buffer_load_b32(pr, vml + 4u, so, 0);
+      const u32 a_b = __builtin_amdgcn_raw_buffer_load_b32(pr, vac, so, 0);
+      m[i] = cb + i < nch ? __builtin_bit_cast(float, m_b) : -__builtin_inff();
+      l[i] = __builtin_bit_cast(float, l_b);
+      a[i] = __builtin_bit_cast(float, a_b);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch in flight before any use
+    float mb = M;
+#pragma unroll
+    for (int i = 0; i < CMB_B; ++i) mb = fmaxf(mb, m[i]);
+    const float sc = expf(M - mb);  // M = -inf at first: sc = 0
+    L *= sc;
+    o *= sc;
+#pragma unroll
+    for (int i = 0; i < CMB_B; ++i) {
+      const float w = expf(m[i] - mb);  // 0 for the chunks past nch
+      L = fmaf(l[i], w, L);
+      o = fmaf(a[i], w, o);
+    }
+    M = mb;
   }
-  m = group_max<32>(m);
-  m = fmaxf(m, xor32(m));
-  if (lane == 0) s_r[0][wave] = m;
-  __syncthreads();
-  const float M = fmaxf(s_r[0][0], s_r[0][1]);
-  float l = 0.f;
-  for (int c = t; c < nch; c += HD) {
-    const float w = expf(s_w[c] - M);
-    s_w[c] = w;
-    l += at(c)[1] * w;
-  }
-  l = group_sum<64>(l);
-  if (lane == 0) s_r[1][wave] = l;
-  __syncthreads();
-  const float L = s_r[1][0] + s_r[1][1];
-  float o = 0.f;
-#pragma unroll 8
-  for (int c = 0; c < nch; ++c) o += at(c)[4 + t] * s_w[c];
   out[(int64_t)h * HD + t] = Half<XT>::from_f32(o / L);
 }
 
