@@ -71,16 +71,45 @@ __global__ __launch_bounds__(WG) void k_moe_combine(const uint16_t* __restrict__
 //   bits[e][w]: bit b set <=> token 32w + b selected expert e
 //   pre [e][w]: popcount of bits[e][0..w)
 // and thread e owns expert e for the three exclusive prefix sums (tokens,
-// first-list entries, second-list entries), done as wave scans plus a scan of
-// the wave totals.
+// first-list entries, second-list entries), done as wave scans plus a sum of
+// the totals of the waves before its own.
+//
+// Inclusive prefix sum over the 64 lanes of a wave in DPP: shifts by 1, 2, 4
+// and 8 lanes within each row of 16 (a lane with no source adds 0), then lane
+// 15's total broadcast to rows 1 and 3 and lane 31's to rows 2 and 3 (the GCN
+// wave scan of AMD's cross-lane operations guide).
 __device__ inline int wave_incl_scan(int v) {
-  const int lane = __lane_id();
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int u = __shfl_up(v, d, 64);
-    if (lane >= d) v += u;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return v;
+}
+
+// One pass over a thread's (token, slot) pairs, SPT of them loaded before any
+// is used (a loop that loads and uses one pair per turn waits a whole memory
+// round trip per pair).  f(s, e) runs for every pair s < ns with its expert e.
+template <int SPT, class F>
+__device__ inline void for_pairs(const int32_t* sel, int ns, F f) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  for (int s0 = 0; s0 < ns; s0 += SPT * nt) {
+    int ev[SPT];
+#pragma unroll
+    for (int u = 0; u < SPT; ++u) ev[u] = sel[min(s0 + u * nt + tid, ns - 1)];
+#pragma unroll
+    for (int u = 0; u < SPT; ++u) {
+      const int s = s0 + u * nt + tid;
+      if (s < ns) f(s, ev[u]);
+    }
+  }
+}
+template <class F> __device__ inline void pairs(const int32_t* sel, int ns, F f) {
+  const int nt = blockDim.x;
+  if (ns <= nt) for_pairs<1>(sel, ns, f);
+  else if (ns <= 4 * nt) for_pairs<4>(sel, ns, f);
+  else for_pairs<8>(sel, ns, f);
 }
 
 // sel may point to LDS (k_route_group) or to global memory (k_group).
@@ -89,23 +118,35 @@ __device__ inline void group_body(const int32_t* sel, int T, int topk, int E, in
                                   int4* __restrict__ entries, int* __restrict__ n_entries,
                                   int4* __restrict__ mf_entries, int* __restrict__ n_mf_entries,
                                   unsigned char* lds) {
-  __shared__ int s_wsum[16][3];
+  __shared__ int s_wsum[3][16];
   const int TW = (T + 31) >> 5;
   u32* bits = (u32*)lds;
   u32* pre = bits + E * TW;
   const int tid = threadIdx.x, nt = blockDim.x, wave = tid >> 6, lane = tid & 63;
+  const int ns = T * topk;
+  // capacities of the lists (the workspace holds E + T topk and E + T topk / MF_TOK + 1);
+  // every index is checked against them, so no store can leave its buffer
+  const int cap_s = E + ns, cap_m = E + ns / MF_TOK + 1;
   for (int i = tid; i < E * TW; i += nt) bits[i] = 0u;
   __syncthreads();
-  for (int s = tid; s < T * topk; s += nt) {
-    const int e = sel[s], t = s / topk;
+  pairs(sel, ns, [&](int s, int e) {
+    const int t = s / topk;
     if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * TW + (t >> 5)], 1u << (t & 31));
-  }
+  });
   __syncthreads();
   int c = 0;
   if (tid < E) {
-    for (int wd = 0; wd < TW; ++wd) {
-      pre[tid * TW + wd] = (u32)c;
-      c += __popc(bits[tid * TW + wd]);
+    for (int w0 = 0; w0 < TW; w0 += 4) {  // four words read before any is counted
+      u32 b[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] = bits[tid * TW + min(w0 + u, TW - 1)];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (w0 + u < TW) {
+          pre[tid * TW + w0 + u] = (u32)c;
+          c += __popc(b[u]);
+        }
+      }
     }
   }
   const bool big = c > lo_max;
@@ -113,40 +154,44 @@ __device__ inline void group_body(const int32_t* sel, int T, int topk, int E, in
   const int nm = big ? (c + MF_TOK - 1) / MF_TOK : 0;
   const int ic = wave_incl_scan(c), ie = wave_incl_scan(ne), im = wave_incl_scan(nm);
   if (lane == 63) {
-    s_wsum[wave][0] = ic;
-    s_wsum[wave][1] = ie;
-    s_wsum[wave][2] = im;
+    s_wsum[0][wave] = ic;
+    s_wsum[1][wave] = ie;
+    s_wsum[2][wave] = im;
   }
   __syncthreads();
-  int bc = 0, be = 0, bm = 0;  // totals of the waves before this one
-  for (int v = 0; v < wave; ++v) {
-    bc += s_wsum[v][0];
-    be += s_wsum[v][1];
-    bm += s_wsum[v][2];
-  }
+  // totals of the waves before this one: lane v < wave reads wave v's, then a sum
+  const int nw = nt >> 6;
+  const bool before = lane < wave && lane < nw;
+  const int wl = min(lane, 15);
+  const int bc = (int)group_sum<64>((float)(before ? s_wsum[0][wl] : 0));
+  const int be = (int)group_sum<64>((float)(before ? s_wsum[1][wl] : 0));
+  const int bm = (int)group_sum<64>((float)(before ? s_wsum[2][wl] : 0));
   const int off = bc + ic - c, eoff = be + ie - ne, moff = bm + im - nm;
   if (tid == nt - 1) {  // the last thread's inclusive sums are the totals
-    *n_entries = be + ie;
-    *n_mf_entries = bm + im;
+    *n_entries = min(be + ie, cap_s);
+    *n_mf_entries = min(bm + im, cap_m);
   }
   int* s_off = (int*)(pre + E * TW);  // [E]
   if (tid < E) s_off[tid] = off;
   __syncthreads();
-  for (int s = tid; s < T * topk; s += nt) {
-    const int e = sel[s], t = s / topk;
+  pairs(sel, ns, [&](int s, int e) {
+    const int t = s / topk;
     if ((unsigned)e < (unsigned)E) {
       const u32 word = bits[e * TW + (t >> 5)];
       const int below = __popc(word & ((1u << (t & 31)) - 1u));
-      perm[s_off[e] + (int)pre[e * TW + (t >> 5)] + below] = s;
+      const int at = s_off[e] + (int)pre[e * TW + (t >> 5)] + below;
+      if ((unsigned)at < (unsigned)ns) perm[at] = s;
     }
-  }
+  });
   if (tid < E) {
     if (big) {
       for (int q = 0; q < nm; ++q)
-        mf_entries[moff + q] = int4{tid, off + q * MF_TOK, min(MF_TOK, c - q * MF_TOK), 0};
+        if (moff + q < cap_m)
+          mf_entries[moff + q] = int4{tid, off + q * MF_TOK, min(MF_TOK, c - q * MF_TOK), 0};
     } else {
       for (int q = 0; q < ne; ++q)
-        entries[eoff + q] = int4{tid, off + q * lo_chunk, min(lo_chunk, c - q * lo_chunk), 0};
+        if (eoff + q < cap_s)
+          entries[eoff + q] = int4{tid, off + q * lo_chunk, min(lo_chunk, c - q * lo_chunk), 0};
     }
   }
 }
