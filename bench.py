@@ -58,7 +58,7 @@ B_LAYER = TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + B_ROUTER + 2 * H * 2      
 B_EXPERTS_LAUNCH = TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + 3 * H * 2 + 2 * TOPK * I * 2
 # HBM bytes per decode experts launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (calibrated against a device copy; summary under profiles/)
-EXPERTS_TRAFFIC_BYTES = 21_066_349
+EXPERTS_TRAFFIC_BYTES = 21_166_930
 
 
 def log(msg: str) -> None:
