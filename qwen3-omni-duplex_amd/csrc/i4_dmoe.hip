@@ -195,14 +195,36 @@ __device__ inline void gate_up_rows(const DGateUpArgs& a, const DW w, int e, uin
   }
   g = group_sum<L>(g);
   u = group_sum<L>(u);
+  // COH: the workgroup's RPW values are gathered in LDS and written through as one
+  // 8- or 16-byte store (one store per value reached the pollers later, measured on
+  // the Thinker's decode layer)
+  __shared__ __align__(16) uint16_t s_act[RPW];
   if (cl == 0 && n < I) {
     if constexpr (I8) {
       g *= Half<XT>::to_f32(w.scale[(int64_t)e * w.N + n]);
       u *= Half<XT>::to_f32(w.scale[(int64_t)e * w.N + I + n]);
     }
     const float v = silu(g) * u;
-    if constexpr (COH) st_coherent(dst + n, v != v ? Half<XT>::QNAN : Half<XT>::from_f32(v));
+    if constexpr (COH) s_act[rl] = v != v ? Half<XT>::QNAN : Half<XT>::from_f32(v);
     else dst[n] = Half<XT>::from_f32(v);
+  }
+  if constexpr (COH) {
+    static_assert(RPW == 4 || RPW == 8, "8 or 16 bytes of values per workgroup");
+    __syncthreads();
+    const int n0 = bx * RPW, nv = min(RPW, I - n0);
+    if (nv == RPW && (I & 7) == 0) {  // aligned whole store
+      if (threadIdx.x == 0) {
+        if constexpr (RPW == 8) {
+          const rsrc_t r = rsrc(dst + n0, 16u);
+          __builtin_amdgcn_raw_buffer_store_b128(*(const u32x4*)s_act, r, 0u, 0, kCoherent);
+        } else {
+          __hip_atomic_store((uint64_t*)(dst + n0), *(const uint64_t*)s_act, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    } else if ((int)threadIdx.x < nv) {
+      st_coherent(dst + n0 + threadIdx.x, s_act[threadIdx.x]);
+    }
   }
 }
 
