@@ -229,7 +229,8 @@ __device__ inline void correct(f32x4& res, const f32x4& d, u32 sraw, u32 zw, int
 // and its LDS (two staging buffers of 16 MB tokens, XSB uint4 apart, and two
 // activation-sum buffers, XSUMB floats apart) from the kernel that runs it, so one
 // launch can serve entries of both sizes (k_tile_mfma_mixed).
-template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN>
+// RING: weight superchunks in flight per wave (2 or 3 register slots).
+template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN, int RING = 3>
 __device__ inline void tile_mfma_body(
     int bx, int by, int bz, u32x4* __restrict__ xs0, int XSB, float* __restrict__ xsum0,
     int XSUMB, const uint16_t* __restrict__ src, u32 src_bytes, int topk,
@@ -448,27 +449,44 @@ __device__ inline void tile_mfma_body(
     __syncthreads();
     if constexpr (MB != 1) load_x(sc + 1, xd);  // unconditional (clamped), like every load
     if (sc < SC) compute(scb + sc, sl.w, buf);
-    issue(sc + 3, sl);
+    issue(sc + RING, sl);
   };
   // Prologue loads in ring order, first turn peeled: the activation loads wait
   // for perm and land after the weights, and a loop header reached from the
   // prologue as well would wait for nearly every load in flight.
-  Slot s0, s1, s2;
-  issue(0, s0);
-  __builtin_amdgcn_sched_barrier(0);
-  issue(1, s1);
-  __builtin_amdgcn_sched_barrier(0);
-  issue(2, s2);
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (MB != 1) load_x(0, xd);
-  __builtin_amdgcn_sched_barrier(0);
-  step(0, s0);
-  step(1, s1);
-  step(2, s2);
-  for (int sc = 3; sc < SC; sc += 3) {
-    step(sc, s0);
-    step(sc + 1, s1);
-    step(sc + 2, s2);
+  static_assert(RING == 2 || RING == 3, "two or three ring slots");
+  if constexpr (RING == 3) {
+    Slot s0, s1, s2;
+    issue(0, s0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(1, s1);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(2, s2);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (MB != 1) load_x(0, xd);
+    __builtin_amdgcn_sched_barrier(0);
+    step(0, s0);
+    step(1, s1);
+    step(2, s2);
+    for (int sc = 3; sc < SC; sc += 3) {
+      step(sc, s0);
+      step(sc + 1, s1);
+      step(sc + 2, s2);
+    }
+  } else {
+    Slot s0, s1;
+    issue(0, s0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(1, s1);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (MB != 1) load_x(0, xd);
+    __builtin_amdgcn_sched_barrier(0);
+    step(0, s0);
+    step(1, s1);
+    for (int sc = 2; sc < SC; sc += 2) {
+      step(sc, s0);
+      step(sc + 1, s1);
+    }
   }
   // epilogue: lane holds rows m = 16 mb + 4 j + i of column r
 #pragma unroll
@@ -532,7 +550,9 @@ __global__ __launch_bounds__(256) void k_tile_mfma(
   constexpr int NBUF = MB <= 4 ? 2 : 1;  // 128-token tiles are staged single-buffered
   __shared__ u32x4 xs[NBUF][TOK * MF_TSTRIDE];
   __shared__ float xsum[NBUF][TOK * 4];  // bf16: per token and chunk
-  tile_mfma_body<XT, ST, GB, GATEUP, NB, MB, LIN>(
+  // one-m-block entries alone: two ring slots keep the wave at <= 80 VGPRs, so six
+  // workgroups fit a CU and the T <= 64 launches run in one round
+  tile_mfma_body<XT, ST, GB, GATEUP, NB, MB, LIN, (MB == 1 && !LIN) ? 2 : 3>(
       blockIdx.x, blockIdx.y, blockIdx.z, &xs[0][0], TOK * MF_TSTRIDE, &xsum[0][0], TOK * 4, src,
       src_bytes, topk, entries, n_entries, perm, w, I, act, ys, M, bias, ot, ksplit, part);
 }
