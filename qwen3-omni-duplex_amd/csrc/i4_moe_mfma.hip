@@ -539,8 +539,12 @@ __device__ inline void tile_mfma_body(
   }
 }
 
-template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN = false>
-__global__ __launch_bounds__(256) void k_tile_mfma(
+// WPE: minimum waves per SIMD the register allocation must allow (1: no bound).  The
+// one-m-block down projection on fp16 activations with one group per superchunk fits
+// eight (64 VGPRs, no spill; the other forms would spill), so all of a T <= 64 down
+// launch's workgroups are resident at once.
+template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN = false, int WPE = 1>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void k_tile_mfma(
     const uint16_t* __restrict__ src, u32 src_bytes, int topk, const int4* __restrict__ entries,
     const int* __restrict__ n_entries, const int32_t* __restrict__ perm, TW w, int I,
     uint16_t* __restrict__ act, float* __restrict__ ys, int M = 0,
@@ -596,7 +600,8 @@ static int mfma_t(bool small, int max_entries, const void* src, int src_rows, in
   const int n_out = GATEUP ? I : w.N;
   const int cols = GATEUP ? 32 * MF_NB : 64 * MF_NB;
 #define I4_MF_LAUNCH(NB_, MB_)                                                                  \
-  hipLaunchKernelGGL((k_tile_mfma<XT, ST, GB, GATEUP, NB_, MB_>),                              \
+  hipLaunchKernelGGL((k_tile_mfma<XT, ST, GB, GATEUP, NB_, MB_, false,                         \
+                                  (!GATEUP && MB_ == 1 && XT == I4_F16 && GB) ? 8 : 1>),       \
                      dim3(n_out / (cols * NB_ / MF_NB), max_entries), dim3(256), 0, s,          \
                      (const uint16_t*)src, (u32)src_bytes, topk, ent, nent, perm, w, I,         \
                      (uint16_t*)act, ys)
