@@ -68,8 +68,9 @@ __global__ __launch_bounds__(WG) void k_moe_combine(const uint16_t* __restrict__
 // into two lists: experts with <= lo_max tokens get entries of <= lo_chunk
 // tokens in `entries`, the others entries of <= MF_TOK tokens in
 // `mf_entries`.  One workgroup of 1024 threads (E <= 1024):
-//   bits[e][w]: bit b set <=> token 32w + b selected expert e
-//   pre [e][w]: popcount of bits[e][0..w)
+//   bits[w][e]: bit b set <=> token 32w + b selected expert e
+//   pre [w][e]: popcount of bits[0..w)[e]
+// (word-major, so the thread of expert e and its neighbours read adjacent words)
 // and thread e owns expert e for the three exclusive prefix sums (tokens,
 // first-list entries, second-list entries), done as wave scans plus a sum of
 // the totals of the waves before its own.
@@ -112,7 +113,6 @@ template <class F> __device__ inline void pairs(const int32_t* sel, int ns, F f)
   else for_pairs<8>(sel, ns, f);
 }
 
-// sel may point to LDS (k_route_group) or to global memory (k_group).
 __device__ inline void group_body(const int32_t* sel, int T, int topk, int E, int lo_max,
                                   int lo_chunk, int32_t* __restrict__ perm,
                                   int4* __restrict__ entries, int* __restrict__ n_entries,
@@ -131,7 +131,7 @@ __device__ inline void group_body(const int32_t* sel, int T, int topk, int E, in
   __syncthreads();
   pairs(sel, ns, [&](int s, int e) {
     const int t = s / topk;
-    if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * TW + (t >> 5)], 1u << (t & 31));
+    if ((unsigned)e < (unsigned)E) atomicOr(&bits[(t >> 5) * E + e], 1u << (t & 31));
   });
   __syncthreads();
   int c = 0;
@@ -139,11 +139,11 @@ __device__ inline void group_body(const int32_t* sel, int T, int topk, int E, in
     for (int w0 = 0; w0 < TW; w0 += 4) {  // four words read before any is counted
       u32 b[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) b[u] = bits[tid * TW + min(w0 + u, TW - 1)];
+      for (int u = 0; u < 4; ++u) b[u] = bits[min(w0 + u, TW - 1) * E + tid];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         if (w0 + u < TW) {
-          pre[tid * TW + w0 + u] = (u32)c;
+          pre[(w0 + u) * E + tid] = (u32)c;
           c += __popc(b[u]);
         }
       }
@@ -177,9 +177,9 @@ __device__ inline void group_body(const int32_t* sel, int T, int topk, int E, in
   pairs(sel, ns, [&](int s, int e) {
     const int t = s / topk;
     if ((unsigned)e < (unsigned)E) {
-      const u32 word = bits[e * TW + (t >> 5)];
+      const u32 word = bits[(t >> 5) * E + e];
       const int below = __popc(word & ((1u << (t & 31)) - 1u));
-      const int at = s_off[e] + (int)pre[e * TW + (t >> 5)] + below;
+      const int at = s_off[e] + (int)pre[(t >> 5) * E + e] + below;
       if ((unsigned)at < (unsigned)ns) perm[at] = s;
     }
   });
@@ -210,39 +210,6 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
              n_mf_entries, lds);
 }
 
-// Few tokens (T <= 64): the 16 waves rank the tokens' logits first (one
-// token per wave at a time, the arithmetic of k_topk), keep the experts in
-// LDS and group them there; one launch instead of two.
-template <int LT, int VPL>
-__global__ __launch_bounds__(1024) void k_route_group(
-    const void* __restrict__ logits, int T, int E, int topk, int renorm,
-    int32_t* __restrict__ sel, float* __restrict__ wts, int lo_max, int lo_chunk,
-    int32_t* __restrict__ perm, int4* __restrict__ entries, int* __restrict__ n_entries,
-    int4* __restrict__ mf_entries, int* __restrict__ n_mf_entries, int32_t* __restrict__ status) {
-  extern __shared__ __align__(16) unsigned char lds[];
-  if (status && threadIdx.x == 0) *status = I4_OK;  // nothing on this path waits
-  int32_t* sel_l = (int32_t*)lds;  // [T][topk]
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // every row of the wave's tokens in flight before the first ranking
-  constexpr int RPW = ONE_LIST_T / 16;  // tokens per wave at most (16 waves)
-  u32 raw[RPW][VPL];
-#pragma unroll
-  for (int r = 0; r < RPW; ++r)
-    if (wave + 16 * r < T) load_row<LT, VPL>(logits, wave + 16 * r, E, raw[r]);
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const int t = wave + 16 * r;
-    if (t < T) {
-      int my_sel = 0;
-      float my_w = 0.f;
-      topk_row<LT, VPL>(raw[r], t, E, topk, renorm, sel, wts, nullptr, 0, &my_sel, &my_w);
-      if (lane < topk) sel_l[t * topk + lane] = my_sel;
-    }
-  }
-  __syncthreads();
-  group_body(sel_l, T, topk, E, lo_max, lo_chunk, perm, entries, n_entries, mf_entries,
-             n_mf_entries, lds + (((size_t)T * topk * 4 + 15) & ~(size_t)15));
-}
 
 
 }  // namespace i4
@@ -457,24 +424,14 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   // small entries of <= MF_SMALL tokens cover every expert in one launch per
   // projection; above, experts with > MF_SMALL tokens take large entries
   const bool one_list = T <= ONE_LIST_T;
-  if (one_list) {  // top-k and grouping in one launch
-    const size_t lds = (((size_t)Tk * 4 + 15) & ~(size_t)15) + glds;
-#define I4_RG_CASE(LT_, VPL_)                                                                  \
-  if (xt == LT_ && E <= 64 * VPL_) {                                                           \
-    hipLaunchKernelGGL((k_route_group<LT_, VPL_>), dim3(1), dim3(1024), lds, s, lg, T, E, topk,  \
-                       renorm, sel, wts, T, MF_SMALL, ws.perm, ws.entries, ws.n_entries,       \
-                       ws.mf_entries, ws.n_mf_entries, st_reset);                              \
-  } else
-    I4_RG_CASE(I4_F16, 2) I4_RG_CASE(I4_F16, 8) I4_RG_CASE(I4_BF16, 2) I4_RG_CASE(I4_BF16, 8)
-    return I4_ERR_SHAPE;
-#undef I4_RG_CASE
-  } else {
-    rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E, MF_SMALL,
-                       MF_SMALL, ws.perm, ws.entries, ws.n_entries, ws.mf_entries,
-                       ws.n_mf_entries, st_reset);
-  }
+  // top-k on T / 4 workgroups (one token per wave), then the grouping: ranking every
+  // token inside the one grouping workgroup queued the waves' scalar bisection steps on
+  // one CU's scalar unit (5 us of the launch at T = 32; separate launches 1.5 us faster)
+  rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E,
+                     one_list ? T : MF_SMALL, MF_SMALL, ws.perm, ws.entries, ws.n_entries,
+                     ws.mf_entries, ws.n_mf_entries, st_reset);
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
   // entry counts: sum over experts of ceil(n_e / 16) <= min(E, Tk) + Tk / 16
   const int max_s = (E < Tk ? E : Tk) + (one_list ? Tk / MF_SMALL : 0);
