@@ -354,8 +354,9 @@ def time_gemvs(pkg, torch, dev, replays=20):
       attention: q 2048->4096, k/v 2048->512, o 4096->2048, 64 distinct layer sets (628 MB),
                  each projection timed on its own (all 64 copies back to back), the four
                  of a layer back to back, and (CT) q/k/v as one launch followed by o.
-    Each workload runs on the AWQ tensors as the checkpoint holds them (split-K kernel +
-    reduction) and on their CT+zeros repack (one launch, what PackedLinear installs).
+    Each workload runs on the AWQ tensors as the checkpoint holds them (one launch, split
+    along K, the last slice of each column strip summing the strip's partials) and on their
+    CT+zeros repack (one launch, what PackedLinear installs).
     Times are per GEMV (or per layer of four), mean / median / p99 over graph replays."""
     from qwen3_omni_duplex_amd import _lib
 
@@ -392,7 +393,8 @@ def time_gemvs(pkg, torch, dev, replays=20):
             self.x = torch.randn(1, K, device=dev, generator=gen).half()
             self.y = torch.empty(1, N, dtype=torch.float16, device=dev)
             nb = lb.i4_linear_workspace_bytes(ctypes.byref(self.desc["awq"][0]), 1)
-            self.ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
+            # AWQ split-K partials start (and stay) pending: every byte 0xFF
+            self.ws = torch.full((max(nb, 256),), 255, dtype=torch.uint8, device=dev)
 
         def launch(self, layout, i):
             d = self.desc[layout][i]

@@ -67,7 +67,7 @@
 extern "C" {
 #endif
 
-#define I4_ABI_VERSION 5
+#define I4_ABI_VERSION 6
 
 /* status codes */
 #define I4_OK               0
@@ -144,9 +144,15 @@ const char* i4_strerror(int code);
  * gate_up call, fused_packed_moe.py:255); x_stride = K gives each expert its
  * own row (the down call, fused_packed_moe.py:261).  Accumulation is fp32.
  * out is [k_sel][N] in out_dtype (I4_F32 matches the reference).  Either
- * layout runs in one launch; i4_dq_gemv_workspace_bytes() returns 0 and the
- * workspace arguments are kept for callers written against it (they may be
- * NULL / 0).  AWQ scales must be 16-byte aligned (also between experts).
+ * layout runs in one launch.  CT and most AWQ shapes need no workspace
+ * (i4_dq_gemv_workspace_bytes() returns 0; NULL / 0 is accepted).  An AWQ
+ * weight with N % 32 == 0 whose K-complete launch would stream more than 2048
+ * rows per CU (K x ceil(N / 8 * k_sel / 256) > 2048, e.g. 2048 -> 4096 and
+ * 4096 -> 2048) is split along K when the caller passes the workspace that
+ * i4_dq_gemv_workspace_bytes() names: 256-byte aligned, every byte 0xFF before
+ * its first call (each call leaves it so), one workspace per stream; with a
+ * NULL workspace it runs K-complete, a smaller one is I4_ERR_WORKSPACE.  AWQ
+ * scales must be 16-byte aligned (also between experts).
  * A group at least as long as K is one scale per output row (the per-channel
  * branch of quant/dequant.py:75-76); a K that is not a multiple of the group
  * leaves a short last group (NG = ceil(K / group) scales per row). */
@@ -164,7 +170,9 @@ size_t i4_dq_gemv_workspace_bytes(const i4_qweight* w, int k_sel);
  * tile kernel over 64-row tiles, each weight tile streamed once per 64 rows
  * (the path for prefill and other M > 1 batches); when that grid is small it
  * is split along K into fp32 partials in the workspace and summed in a fixed
- * order.  i4_linear_workspace_bytes gives the workspace (0: none needed). */
+ * order.  i4_linear_workspace_bytes gives the workspace (0: none needed); for
+ * an AWQ weight it is i4_dq_gemv's split-K workspace, with the same 0xFF
+ * contract. */
 int    i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w,
                  const void* bias, void* y, int y_dtype,
                  void* workspace, size_t workspace_bytes, hipStream_t stream);

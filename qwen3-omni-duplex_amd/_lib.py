@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libi4moe.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # element types and layouts (include/i4moe.h)
 F32, F16, BF16 = 0, 1, 2

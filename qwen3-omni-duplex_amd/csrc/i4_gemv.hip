@@ -242,6 +242,248 @@ __global__ __launch_bounds__(WG) void k_gemv_awq(
 }
 
 // ---------------------------------------------------------------------------
+// AWQ GEMV split along K, one launch.  A K-complete workgroup reads a column
+// word as 4 bytes out of every 128-byte line of its K rows, so each CU fills
+// K lines for 4 K bytes of weights (2048-4096 fills per CU at the attention
+// shapes).  Here a workgroup owns a strip of 256 columns (32 words: one whole
+// line per row) over a slice of KS rows, so every line it fills is used in
+// full and the launch has (N / 256) x (K / KS) workgroups per row of x:
+//   thread t: quad q = t & 7 (words 4q..4q+3 of the strip, 32 columns) and
+//   row pair rp = t >> 3 of each 16 * NWAVE-row pass (rows k, k+1 merged
+//   byte-wise into (M + q_k, M + q_k+1) halves for v_dot2, as in k_gemv_awq);
+//   the zero point is removed per thread with its pair sums of x, the
+//   per-thread column sums are reduced over the row pairs with a halving lane
+//   butterfly (xor 8, 16, 32: each step keeps half the columns) and then
+//   across the waves in LDS, and the slice's scale (loaded with the weights)
+//   is applied once per column: a slice lies inside one quantisation group.
+// Hand-over without atomics or fences: slices 0..P-2 of a strip store their
+// fp32 partials (1 KB) write-through and exit; slice P-1, dispatched after
+// them, reads the other partials from memory until none holds the pending
+// pattern (0xFFFFFFFF, a NaN no slice writes: NaNs are stored canonical),
+// sums them in a fixed order (slice classes s mod NWAVE, then its own slice),
+// writes y, and puts the pattern back.  The partials must hold the pattern
+// before the first launch; every launch leaves it there.  A reducer that
+// polls max_polls times without seeing every partial writes NaN.
+static constexpr int SK_COLS = 256;  // columns per strip
+static constexpr u32 kPending32 = 0xFFFFFFFFu;
+static constexpr int kAwqPolls = 1 << 20;
+
+template <int XT, int ST, int NWAVE, int PPT>
+__global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
+    const uint16_t* __restrict__ x, int64_t x_stride, const int32_t* __restrict__ qw, int64_t q_es,
+    const void* __restrict__ scales, int64_t s_es, const int32_t* __restrict__ qz, int64_t z_es,
+    const int32_t* __restrict__ sel, int E, int N, int gshift, int S, int P,
+    float* part, void* __restrict__ out, int ot, const void* __restrict__ bias, int max_polls) {
+  constexpr int NT = 64 * NWAVE, PASS = 16 * NWAVE, KS = PASS * PPT, CPT = SK_COLS / NT;
+  __shared__ f32x4 red[NWAVE][64];
+  const int strip = (int)blockIdx.x / P, slice = (int)blockIdx.x % P;
+  const int j = blockIdx.y;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int q = t & 7, rp = t >> 3;
+  const int NW = N >> 3;
+  const int e = sel ? sel[j] : 0;
+  const bool ev = (unsigned)e < (unsigned)E;
+  const int ee = ev ? e : 0;
+  const int w0 = strip * 32 + 4 * q;  // N % 32 == 0: a quad is wholly inside or outside
+  const int wc = w0 < NW ? w0 : 0;
+  const int k0 = slice * KS, g = k0 >> gshift;
+  const int32_t* qe = qw + ee * q_es + wc;
+  const uint16_t* xrow = x + (int64_t)j * x_stride;
+
+  // every load first: weight row pairs, x pairs, the zero words, the output
+  // columns' scales (thread t finishes strip columns ct = t + NT c, mapped as
+  // quad ct >> 5, word (ct >> 3) & 3 of the quad, nibble slot ct & 7)
+  u32x4 wa[PPT], wb[PPT];
+  u32 xp[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int k = k0 + 2 * (rp + (PASS / 2) * i);
+    wa[i] = ldg16(qe + (int64_t)k * NW);
+    wb[i] = ldg16(qe + (int64_t)(k + 1) * NW);
+  }
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) xp[i] = *(const u32*)(xrow + k0 + 2 * (rp + (PASS / 2) * i));
+  u32x4 zv = {0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+  if (qz) zv = ldg16(qz + ee * z_es + (int64_t)g * NW + wc);
+  int ncol[CPT];
+  u32 sraw[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int ct = t + NT * c;
+    const int word = strip * 32 + (ct >> 3);
+    ncol[c] = word < NW ? 8 * word + awq_col(ct & 7) : -1;
+    sraw[c] = load_scale_raw<ST>(scales, ee * s_es + (int64_t)g * N + (word < NW ? ncol[c] : 0));
+  }
+
+  constexpr u32 MK = 0x000F000Fu;
+  const u32 mg = magic_v<XT>();
+  const u32 ONE2 = XT == I4_F16 ? 0x3C003C00u : 0x3F803F80u;  // (1.0, 1.0)
+  float acc[32];  // column slot sl of word jw at 8 jw + sl
+#pragma unroll
+  for (int c = 0; c < 32; ++c) acc[c] = 0.f;
+  float Sx = 0.f;
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    Sx = Half<XT>::dot2(xp[i], ONE2, Sx);
+    const u32 av[4] = {wa[i].x, wa[i].y, wa[i].z, wa[i].w};
+    const u32 bv[4] = {wb[i].x, wb[i].y, wb[i].z, wb[i].w};
+#pragma unroll
+    for (int jw = 0; jw < 4; ++jw) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        // byte b of row k -> bits 0..7, byte b of row k + 1 -> bits 16..23
+        const u32 sel_b = 0x0C000C00u | (u32)(b) | ((u32)(4 + b) << 16);
+        const u32 tb = __builtin_amdgcn_perm(bv[jw], av[jw], sel_b);
+        acc[8 * jw + 2 * b] = Half<XT>::dot2((tb & MK) | mg, xp[i], acc[8 * jw + 2 * b]);
+        acc[8 * jw + 2 * b + 1] =
+            Half<XT>::dot2(((tb >> 4) & MK) | mg, xp[i], acc[8 * jw + 2 * b + 1]);
+      }
+    }
+  }
+  {
+    const u32 zw[4] = {zv.x, zv.y, zv.z, zv.w};
+#pragma unroll
+    for (int jw = 0; jw < 4; ++jw)
+#pragma unroll
+      for (int sl = 0; sl < 8; ++sl)
+        acc[8 * jw + sl] =
+            fmaf(-(Half<XT>::MAGIC + (float)((zw[jw] >> (4 * sl)) & 15u)), Sx, acc[8 * jw + sl]);
+  }
+
+  // halving butterfly over the 8 row pairs of the wave that share q
+  const bool h1 = (lane >> 3) & 1, h2 = (lane >> 4) & 1, h3 = (lane >> 5) & 1;
+  float u1[16], u2[8];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float keep = h1 ? acc[16 + i] : acc[i], send = h1 ? acc[i] : acc[16 + i];
+    u1[i] = keep + dpp_mov<0x128>(send);  // row_ror:8, lane ^ 8
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float keep = h2 ? u1[8 + i] : u1[i], send = h2 ? u1[i] : u1[8 + i];
+    u2[i] = keep + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(
+                                                  __builtin_bit_cast(int, send), 0x401F));  // ^16
+  }
+  {
+    const int src = (lane ^ 32) << 2;
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float keep = h3 ? u2[4 + i] : u2[i], send = h3 ? u2[i] : u2[4 + i];
+      r[i] = keep + __builtin_bit_cast(
+                        float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, send)));
+    }
+    // lane (q, h1 h2 h3) now holds columns 16 h1 + 8 h2 + 4 h3 + 0..3 of quad q
+    red[wave][lane] = f32x4{r[0], r[1], r[2], r[3]};
+  }
+  __syncthreads();
+
+  // cross-wave sum and scale: this slice's partial of columns ct = t + NT c
+  float mine[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int ct = t + NT * c, qq = ct >> 5, cc = ct & 31;
+    const int src = qq + 8 * (((cc >> 4) & 1) | (((cc >> 3) & 1) << 1) | (((cc >> 2) & 1) << 2));
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+      const f32x4 r = red[w][src];
+      const int i = cc & 3;
+      v += i == 0 ? r.x : i == 1 ? r.y : i == 2 ? r.z : r.w;
+    }
+    v *= scale_from_raw<ST>(sraw[c]);
+    mine[c] = ev ? (v != v ? __builtin_nanf("") : v) : __builtin_nanf("");  // canonical NaN
+  }
+  float* strip_part = part + (int64_t)(j * S + strip) * P * SK_COLS;
+  if (slice != P - 1) {  // a producer: hand the partial over and leave
+#pragma unroll
+    for (int c = 0; c < CPT; ++c)
+      if (ncol[c] >= 0)
+        __hip_atomic_store(strip_part + (int64_t)slice * SK_COLS + (ncol[c] & 255), mine[c],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  // the reducer: thread t reads columns 4 (t % 64) .. +3 of the slices
+  // s = t / 64 (mod NWAVE), up to 16 * NWAVE slices per round trip, until none
+  // is pending; the slice classes are then added in class order in LDS
+  __shared__ f32x4 red2[NWAVE][64];
+  __shared__ int s_gave_up;
+  if (t == 0) s_gave_up = 0;
+  {
+    constexpr int MAXB = 16;
+    const rsrc_t pr = rsrc(strip_part, (u32)P * SK_COLS * 4u);
+    const int cg = lane, so = wave;
+    const bool cv = strip * SK_COLS + 4 * cg < N;  // whole column quads (N % 32 == 0)
+    f32x4 a4 = {0.f, 0.f, 0.f, 0.f};
+    bool gave_up = false;
+    for (int s0 = 0; s0 < P - 1; s0 += NWAVE * MAXB) {
+      u32x4 pv[MAXB];
+      for (int poll = 0;; ++poll) {
+        bool pending = false;
+#pragma unroll
+        for (int i = 0; i < MAXB; ++i) {  // past the last producer: re-read it, unused
+          const int sl = min(s0 + so + NWAVE * i, P - 2);
+          pv[i] = ld16_coherent(pr, (u32)(sl * SK_COLS + 4 * cg) * 4u);
+        }
+#pragma unroll
+        for (int i = 0; i < MAXB; ++i)  // only the slices this thread owns: an owner puts
+          pending |= cv && s0 + so + NWAVE * i < P - 1 &&  // the pattern back once it read one
+                     (pv[i].x == kPending32 || pv[i].y == kPending32 ||
+                      pv[i].z == kPending32 || pv[i].w == kPending32);
+        if (!pending) break;
+        if (poll >= max_polls) {
+          gave_up = true;
+          break;
+        }
+        // another pass issues the loads again: part is not __restrict__, so the
+        // clobber below may have written it and the loads cannot be hoisted
+        __builtin_amdgcn_s_sleep(1);
+        asm volatile("" ::: "memory");
+      }
+#pragma unroll
+      for (int i = 0; i < MAXB; ++i) {
+        const int sl = s0 + so + NWAVE * i;
+        if (sl < P - 1 && cv) {
+          a4 += __builtin_bit_cast(f32x4, pv[i]);  // whole vector
+          const u32x4 pend = {kPending32, kPending32, kPending32, kPending32};
+          __builtin_amdgcn_raw_buffer_store_b128(pend, pr, (u32)(sl * SK_COLS + 4 * cg) * 4u, 0,
+                                                 kCoherent);  // pending again for the next launch
+        }
+      }
+    }
+    red2[so][cg] = a4;
+    if (gave_up) s_gave_up = 1;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    if (ncol[c] < 0) continue;
+    const int n = ncol[c], nl = n & 255;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+      const f32x4 r = red2[w][nl >> 2];
+      const int i = nl & 3;
+      v += i == 0 ? r.x : i == 1 ? r.y : i == 2 ? r.z : r.w;
+    }
+    v += mine[c];  // the last slice's own partial
+    if (s_gave_up) v = __builtin_nanf("");
+    const int64_t o = (int64_t)j * N + n;
+    if (ot == I4_F32) {
+      if (bias) v += ((const float*)bias)[n];
+      store_out<I4_F32>(out, o, v);
+    } else if (ot == I4_F16) {
+      if (bias) v += Half<I4_F16>::to_f32(((const uint16_t*)bias)[n]);
+      store_out<I4_F16>(out, o, v);
+    } else {
+      if (bias) v += Half<I4_BF16>::to_f32(((const uint16_t*)bias)[n]);
+      store_out<I4_BF16>(out, o, v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // logical nibble / dequantised value of W[e][n][k] for both layouts
 struct WView {
   const int32_t* packed;
@@ -570,9 +812,80 @@ static int launch_gemv_awq_t(const void* x, int64_t x_stride, const i4_qweight* 
   return I4_ERR_SHAPE;
 }
 
+// Split-K plan of the AWQ GEMV: waves per workgroup, row pairs per thread
+// (slice = 16 * waves * pairs rows), strips, slices; waves == 0: the shape
+// keeps the K-complete kernel.  The hand-over costs about 2 us (measured: the
+// split launch takes 5.5-6.0 us at 2048 -> 512 / 768 against 4.9 / 5.8
+// K-complete, 6.5 / 6.8 at 2048 -> 4096 and 4096 -> 2048 against 8.5-9.6), so
+// the split is taken only where the K-complete launch fills more than 2048 rows
+// of lines per CU (K rows per workgroup, N / 8 workgroups per row of x over 256
+// CUs).  Its slice is the largest of 128 / 64 / 32 rows that divides K and the
+// group: a slice's loads are one round trip at any of these sizes, and fewer
+// slices make fewer partials to hand over.
+struct AwqSplit {
+  int nwave, ppt, S, P;
+};
+static AwqSplit awq_split_plan(const i4_qweight& w, int k_sel) {
+  AwqSplit p{0, 0, 0, 0};
+  if (w.layout != I4_LAYOUT_AWQ || w.N % 32 != 0 || k_sel < 1) return p;
+  if (w.zeros && (((uintptr_t)w.zeros & 15) || (w.E > 1 && w.zeros_estride % 4))) return p;
+  const int64_t rounds = ((int64_t)(w.N / 8) * k_sel + 255) / 256;
+  if ((int64_t)w.K * rounds <= 2048) return p;
+  const int S = (w.N / 8 + 31) / 32;
+  static const int opts[3][2] = {{4, 2}, {4, 1}, {2, 1}};
+  for (const auto& o : opts) {
+    const int ks = 16 * o[0] * o[1];
+    if (w.K % ks != 0 || w.group % ks != 0) continue;
+    p = AwqSplit{o[0], o[1], S, w.K / ks};
+    break;
+  }
+  return p;
+}
+// workspace of a split-K plan: the fp32 slice partials, [row][strip][slice][256],
+// every byte 0xFF (the pending pattern) before the first launch
+static size_t awq_split_bytes(const AwqSplit& p, int k_sel) {
+  if (!p.nwave) return 0;
+  return (size_t)k_sel * p.S * p.P * SK_COLS * sizeof(float);
+}
+
+template <int XT, int ST>
+static int launch_gemv_awq_sk_t(const void* x, int64_t x_stride, const i4_qweight* w,
+                                const int32_t* sel, int k_sel, void* out, int ot,
+                                const void* bias, const AwqSplit& p, void* ws, hipStream_t s) {
+  int gshift = 0;
+  while ((1 << gshift) < w->group) ++gshift;
+  const dim3 grid(p.S * p.P, k_sel);
+  float* part = (float*)ws;
+#define I4_SK_CASE(NW_, PPT_)                                                                     \
+  if (p.nwave == NW_ && p.ppt == PPT_) {                                                          \
+    hipLaunchKernelGGL((k_gemv_awq_sk<XT, ST, NW_, PPT_>), grid, dim3(64 * NW_), 0, s,            \
+                       (const uint16_t*)x, x_stride, w->packed, w->packed_estride, w->scale,      \
+                       w->scale_estride, w->zeros, w->zeros_estride, sel, w->E, w->N, gshift,     \
+                       p.S, p.P, part, out, ot, bias, kAwqPolls);                                 \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                               \
+  }
+  I4_SK_CASE(4, 2) I4_SK_CASE(4, 1) I4_SK_CASE(2, 1)
+#undef I4_SK_CASE
+  return I4_ERR_SHAPE;
+}
+
+// AWQ GEMV: split along K when the caller passes the plan's workspace, else
+// the K-complete kernel (no workspace)
 static int launch_gemv_awq(const void* x, int xt, int64_t x_stride, const i4_qweight* w,
                            const int32_t* sel, int k_sel, void* out, int ot, const void* bias,
-                           hipStream_t s) {
+                           void* ws, size_t ws_bytes, hipStream_t s) {
+  const AwqSplit p = awq_split_plan(*w, k_sel);
+  if (p.nwave && ws) {
+    if (ws_bytes < awq_split_bytes(p, k_sel)) return I4_ERR_WORKSPACE;
+    if ((uintptr_t)ws & 255) return I4_ERR_ALIGN;
+#define I4_AWQ_DT(XT_, ST_)                                                                   \
+  if (xt == XT_ && w->scale_dtype == ST_)                                                     \
+    return launch_gemv_awq_sk_t<XT_, ST_>(x, x_stride, w, sel, k_sel, out, ot, bias, p, ws, s);
+    I4_AWQ_DT(I4_F16, I4_F32) I4_AWQ_DT(I4_F16, I4_F16) I4_AWQ_DT(I4_F16, I4_BF16)
+    I4_AWQ_DT(I4_BF16, I4_F32) I4_AWQ_DT(I4_BF16, I4_F16) I4_AWQ_DT(I4_BF16, I4_BF16)
+#undef I4_AWQ_DT
+    return I4_ERR_DTYPE;
+  }
 #define I4_AWQ_DT(XT_, ST_)                                                              \
   if (xt == XT_ && w->scale_dtype == ST_)                                                \
     return launch_gemv_awq_t<XT_, ST_>(x, x_stride, w, sel, k_sel, out, ot, bias, s);
@@ -585,9 +898,9 @@ static int launch_gemv_awq(const void* x, int xt, int64_t x_stride, const i4_qwe
 extern "C" {
 
 size_t i4_dq_gemv_workspace_bytes(const i4_qweight* w, int k_sel) {
-  (void)w;
-  (void)k_sel;
-  return 0;  // every layout runs in one launch without scratch
+  i4_qweight nw;
+  if (!w || i4_check_weight(w, &nw) != I4_OK) return 0;
+  return awq_split_bytes(awq_split_plan(nw, k_sel), k_sel);
 }
 
 int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w,
@@ -606,9 +919,8 @@ int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w
   if (nw.layout == I4_LAYOUT_CT)
     return i4_launch_gemv_ct(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr,
                              stream);
-  (void)workspace;
-  (void)workspace_bytes;
-  return launch_gemv_awq(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr, stream);
+  return launch_gemv_awq(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr,
+                         workspace, workspace_bytes, stream);
 }
 
 int i4_rmsnorm_linear(const void* x, int x_dtype, int M, const void* norm_w, float eps,
@@ -664,7 +976,8 @@ int i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w, const void
   if (nw.layout == I4_LAYOUT_CT)
     return i4_launch_gemv_ct(x, x_dtype, nw.K, &nw, nullptr, M, y, y_dtype, bias, stream);
   if (!awq_scales_aligned(nw)) return I4_ERR_ALIGN;
-  return launch_gemv_awq(x, x_dtype, nw.K, &nw, nullptr, M, y, y_dtype, bias, stream);
+  return launch_gemv_awq(x, x_dtype, nw.K, &nw, nullptr, M, y, y_dtype, bias, workspace,
+                         workspace_bytes, stream);
 }
 
 static WView make_view(const i4_qweight& w) {

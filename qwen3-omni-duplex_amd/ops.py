@@ -27,9 +27,13 @@ from . import _lib
 from .weights import QWeight
 
 
-def _ws(nbytes: int, device: torch.device) -> torch.Tensor | None:
+def _ws(nbytes: int, device: torch.device, pending: bool = False) -> torch.Tensor | None:
+    """Per-call workspace; pending=True for the AWQ GEMV, whose split-K partials start as
+    the pending pattern (every byte 0xFF)."""
     if nbytes == 0:
         return None
+    if pending:
+        return torch.full((nbytes,), 255, dtype=torch.uint8, device=device)
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
@@ -65,7 +69,7 @@ def dequant_gemv(x, packed, scale, sel, group=32, block_r=64, nw_blk=8, *, zeros
     out = torch.empty(k, w.N, dtype=out_dtype, device=dev)
     lb = _lib.lib()
     cw = w.c()
-    ws = _ws(lb.i4_dq_gemv_workspace_bytes(ctypes.byref(cw), k), dev)
+    ws = _ws(lb.i4_dq_gemv_workspace_bytes(ctypes.byref(cw), k), dev, pending=True)
     _lib.check(lb.i4_dq_gemv(xc.data_ptr(), xt, s_x, ctypes.byref(cw), sel32.data_ptr(), k,
                              out.data_ptr(), _lib.dtype_code(out_dtype),
                              None if ws is None else ws.data_ptr(),
@@ -92,7 +96,7 @@ def linear(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
             raise RuntimeError("bias length != out_features")
     lb = _lib.lib()
     cw = w.c()
-    ws = _ws(lb.i4_linear_workspace_bytes(ctypes.byref(cw), M), dev)
+    ws = _ws(lb.i4_linear_workspace_bytes(ctypes.byref(cw), M), dev, pending=w.layout == "awq")
     _lib.check(lb.i4_linear(flat.data_ptr(), xt, M, ctypes.byref(cw), _lib.ptr(b), y.data_ptr(),
                             _lib.dtype_code(od), None if ws is None else ws.data_ptr(),
                             0 if ws is None else ws.numel(), _lib.stream(dev)))

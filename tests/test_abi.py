@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported_and_bound(pkg):
 
 def test_version_and_errors(pkg):
     lib = pkg.lib()
-    assert lib.i4_abi_version() == 5
+    assert lib.i4_abi_version() == 6
     codes = {0: b"ok", -1: b"NULL", -2: b"dimension", -3: b"element type", -4: b"aligned",
              -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride",
              -10: b"gave up waiting", -11: b"static buffer"}
@@ -85,10 +85,23 @@ def test_call_validation_codes(pkg):
     assert lib.i4_dq_gemv(0x30000, 1, 100, ctypes.byref(w), 0x40000, 8, 0x50000, 0, None, 0, None) == -9
     assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(w), None, 8, 0x50000, 0, None, 0, None) == -1
     assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(w), 0x40000, 0, 0x50000, 0, None, 0, None) == -2
-    # AWQ runs in one launch without a workspace, reading its scales 16 bytes at a time
-    wa = _qw(_lib, layout=1)
-    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wa), 8) == 0
+    # AWQ with N % 32 == 0 and more than 2048 rows of lines per CU in a K-complete launch
+    # splits K over a workspace of fp32 partials per row of x, 256-column strip and K slice
+    # (K = 4096, group 128: 128-row slices, 32 of them); without a workspace, or at smaller
+    # shapes, it runs K-complete workgroups; CT needs none; AWQ scales are read 16 bytes
+    # at a time
+    wa = _qw(_lib, layout=1, N=256, K=4096, group=128)
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wa), 8) == 8 * 1 * 32 * 256 * 4
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(_qw(_lib, layout=1)), 8) == 0
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(_qw(_lib, layout=1, N=40, K=4096)),
+                                          8) == 0
     assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(w), 8) == 0
+    assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(wa), 0x40000, 8, 0x50000, 0, 0x60000, 16,
+                          None) == -7
+    assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(wa), 0x40000, 8, 0x50000, 0, 0x60010,
+                          1 << 20, None) == -4
+    assert lib.i4_linear_workspace_bytes(
+        ctypes.byref(_qw(_lib, layout=1, E=1, N=256, K=4096, group=128)), 1) == 32 * 256 * 4
     wa_odd = _qw(_lib, layout=1, scale=0x20008)
     assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(wa_odd), 0x40000, 8, 0x50000, 0, None, 0,
                           None) == -4

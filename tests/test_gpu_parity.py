@@ -15,6 +15,7 @@ in seconds.
 """
 from __future__ import annotations
 
+import ctypes
 import zlib
 
 import numpy as np
@@ -271,9 +272,10 @@ def test_dq_gemv_strided_views_run_in_place(pkg, dev):
                                        (768, 768, "bf16", 32), (96, 8192, "f16", 64),
                                        (256, 768, "f16", 768)])
 def test_dq_gemv_awq(pkg, dev, N, K, xdt, G):
-    """The AWQ GEMV in place (one launch, K reduced inside each workgroup): the workload's
-    shapes, column counts that are not a multiple of 32 (one word per load), short and long
-    rows, group 32 / 64, and one scale per output row (group = K)."""
+    """The AWQ GEMV in place, one launch (split along K into 256-column strips at 2048 ->
+    4096, 4096 -> 2048 and 8192 -> 96, K-complete workgroups elsewhere): the workload's
+    shapes, column counts that are not a multiple of 32 or of 256 (a partial strip), short
+    and long rows, group 32 / 64, and one scale per output row (group = K)."""
     rng = np.random.default_rng(N + K)
     E, k = 2, 2
     qw, qz, sc = _gen.awq_weight(rng, E, K, N, G)
@@ -286,6 +288,53 @@ def test_dq_gemv_awq(pkg, dev, N, K, xdt, G):
     err = i4ref.rel_err(got, ref)
     assert err <= 1e-4, err
     assert got.shape == (k, N)
+
+
+@pytest.mark.parametrize("N,K,G", [(768, 2048, 128), (4096, 2048, 128), (96, 8192, 64)])
+def test_dq_gemv_awq_split_k_handover(pkg, dev, N, K, G):
+    """Both AWQ kernels through the C ABI: split along K (workspace given) and K-complete
+    (no workspace) each match the oracle.  The split launch's partials start as the pending
+    pattern and every call leaves them so, so five calls in a row on one workspace give
+    identical outputs (the last slice of a strip adds the partials in a fixed order)."""
+    from qwen3_omni_duplex_amd import _lib
+
+    lb = pkg.lib()
+    rng = np.random.default_rng(7 + N + K)
+    E, k = 3, 3
+    qw, qz, sc = _gen.awq_weight(rng, E, K, N, G)
+    w = pkg.QWeight(t_(qw, dev), t_(sc, dev), t_(qz, dev), "awq", G, N, K)
+    sel = np.array([2, 0, 1], np.int32)
+    x = make_x(rng, (k, K), "f16")
+    ref = i4ref.dq_gemv(f_(x), i4ref.awq_dequant(qw, qz, sc, G), sel)
+    xd, seld = t_(x, dev), t_(sel, dev)
+    cw = w.c()
+    nb = lb.i4_dq_gemv_workspace_bytes(ctypes.byref(cw), k)
+    assert nb > 0
+    ws = torch.full((nb,), 255, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(wsp):
+        y = torch.empty(k, N, dtype=torch.float32, device=dev)
+        rc = lb.i4_dq_gemv(xd.data_ptr(), _lib.F16, K, ctypes.byref(cw), seld.data_ptr(), k,
+                           y.data_ptr(), _lib.F32, None if wsp is None else wsp.data_ptr(),
+                           0 if wsp is None else wsp.numel(), stream)
+        assert rc == 0, lb.i4_strerror(rc)
+        return y
+
+    whole = host(run(None))
+    assert i4ref.rel_err(whole, ref) <= 1e-4
+    outs = []
+    for _ in range(5):
+        outs.append(run(ws))
+        torch.cuda.synchronize()
+        assert bool((ws == 255).all())
+    for y in outs[1:]:
+        assert torch.equal(y, outs[0])
+    assert i4ref.rel_err(host(outs[0]), ref) <= 1e-4
+    # a workspace one byte short is refused before anything runs
+    y = torch.empty(k, N, dtype=torch.float16, device=dev)
+    assert lb.i4_dq_gemv(xd.data_ptr(), _lib.F16, K, ctypes.byref(cw), seld.data_ptr(), k,
+                         y.data_ptr(), _lib.F16, ws.data_ptr(), nb - 1, stream) == -7
 
 
 @pytest.mark.parametrize("M", [1, 5])
