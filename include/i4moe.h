@@ -347,6 +347,25 @@ int    i4_attn_decode_at(const void* qkv, int x_dtype, int n_heads, int n_kv_hea
                          void* v_cache, int max_len, void* out, void* workspace,
                          size_t workspace_bytes, hipStream_t stream);
 size_t i4_attn_decode_workspace_bytes(int n_heads, int head_dim, int max_len);
+/* The attention core above followed by the o_proj projection with the residual added,
+ *   y = residual + o_w attn,   y / residual [o_w->N] in x_dtype (residual nullable),
+ * which the reference runs as the attention then TritonPackedLinear(o_proj)
+ * (triton_dequant_gemv.py:151-159) and the decoder layer's residual add
+ * (modeling_qwen3_omni_moe.py:1547-1552 in transformers 5.15).  o_w: one CT weight
+ * (E = 1) with K = n_heads * head_dim <= 8192.  The chunk merge and o_proj run as one
+ * launch whose o_proj workgroups stream their weights while the heads are merged and
+ * then take the merged heads over inside the launch; the result equals
+ * i4_attn_decode(_at) followed by i4_linear(o_w, bias = residual) bit for bit.
+ * pos_dev (int32 on the device, nullable) overrides pos as in i4_attn_decode_at.
+ * Workspace: i4_attn_decode_o_workspace_bytes(), no initial contents; calls sharing one
+ * must not overlap. */
+int    i4_attn_decode_o(const void* qkv, int x_dtype, int n_heads, int n_kv_heads,
+                        int head_dim, const void* q_norm_w, const void* k_norm_w, float eps,
+                        const float* inv_freq, const int32_t* pos_dev, int pos, void* k_cache,
+                        void* v_cache, int max_len, const i4_qweight* o_w,
+                        const void* residual, void* y, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+size_t i4_attn_decode_o_workspace_bytes(int n_heads, int head_dim, int max_len);
 
 /* ------------------------------------------------------------------------
  * MoE block on 16-bit or int8 experts with a sigmoid-gated shared expert: the

@@ -116,6 +116,11 @@ SIGNATURES = {
                                   ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                   c_void_p, c_void_p, c_size_t, c_void_p]),
     "i4_attn_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "i4_attn_decode_o": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                 ctypes.c_float, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                                 c_int, POINTER(QWeightC), c_void_p, c_void_p, c_void_p,
+                                 c_size_t, c_void_p]),
+    "i4_attn_decode_o_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "i4_dmoe_forward": (c_int, [c_void_p, c_int, c_int, POINTER(DmoeWeightsC), c_int, c_int,
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_size_t, c_void_p]),

@@ -19,7 +19,9 @@
 // multimodal rotary embedding (apply_interleaved_mrope) reduces to the 1-D one
 // with inv_freq[i] = theta^(-2i / head_dim).
 #include "i4_common.h"
+#include "i4_gemv_body.h"
 #include "i4_launch.h"
+#include "i4_moe_launch.h"
 
 namespace i4 {
 
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
     const uint16_t* __restrict__ kn_w, float eps, const int32_t* __restrict__ pos_dev,
     int pos_host, int max_len, RopeTab rt, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
-    float* __restrict__ part, int gsplit) {
+    float* __restrict__ part, int gsplit, u32x4* __restrict__ pend, int n_pend) {
   __shared__ __align__(16) u32 s_q[GQ][HD / 2];  // rotated q pairs
   __shared__ u32 s_knew[HD / 2], s_vnew[HD / 2];
   __shared__ __align__(16) float s_p[GQ][ACH];
@@ -105,6 +107,10 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   // the position from device memory (a captured graph serves every token) or the
   // host; a grid sized for max_len leaves the chunks past it idle
   const int pos = pos_dev ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_host;
+  // pend (n_pend 16-byte units, nullable): the attention output of a launch that hands
+  // it to o_proj inside the launch (k_attn_o) starts as the pending pattern
+  if (c == 0 && blockIdx.y == 0)
+    for (int i = t; i < n_pend; i += 256) pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
   const int S = pos + 1, c0 = c * ACH;
   if (pos < 0 || pos >= max_len || c0 >= S) return;
   const bool last = c0 + ACH >= S;  // the chunk that holds pos
@@ -241,17 +247,12 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
 // 64 CMB_B positions costs one memory round trip.
 static constexpr int CMB = 1024;  // chunks per head at most (max_len <= 65536)
 static constexpr int CMB_B = 16;  // chunks per batch of loads
+// Head h's output dimension t (bits in the activation dtype): the merge of the
+// chunks' (m, l, acc) partials.
 template <int XT>
-__global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ part, int nq,
-                                                     const int32_t* __restrict__ pos_dev,
-                                                     int pos_host, int max_len,
-                                                     uint16_t* __restrict__ out) {
-  const int h = blockIdx.x, t = threadIdx.x;
-  const int pos = pos_dev ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_host;
-  if (pos < 0 || pos >= max_len) {  // no row to attend: the chunk kernel wrote nothing
-    out[(int64_t)h * HD + t] = Half<XT>::QNAN;
-    return;
-  }
+__device__ inline uint16_t combine_head(const float* __restrict__ part, int nq, int h, int t,
+                                        int pos, int max_len) {
+  if (pos < 0 || pos >= max_len) return Half<XT>::QNAN;  // no row to attend: no partials
   const int nch = (pos + ACH) / ACH;
   // raw buffer loads, all issued unconditionally (clamped chunk index): a guarded
   // load would be waited for where its branch joins
@@ -286,21 +287,106 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ p
     }
     M = mb;
   }
-  out[(int64_t)h * HD + t] = Half<XT>::from_f32(o / L);
+  return Half<XT>::from_f32(o / L);
+}
+
+template <int XT>
+__global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ part, int nq,
+                                                     const int32_t* __restrict__ pos_dev,
+                                                     int pos_host, int max_len,
+                                                     uint16_t* __restrict__ out) {
+  const int h = blockIdx.x, t = threadIdx.x;
+  const int pos = pos_dev ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_host;
+  out[(int64_t)h * HD + t] = combine_head<XT>(part, nq, h, t, pos, max_len);
+}
+
+// The combine and o_proj in one launch: blocks [0, nq) merge one head each and
+// write its 128 outputs to att as 16-byte stores written through to memory
+// (NaN in canonical form; att holds the pending pattern from the chunk launch);
+// the later blocks are the o_proj GEMV rows (gemv_ct_body with POLL: their
+// first weight loads go out at once, then they poll att), y = W att + residual.
+// Only later blocks wait, and only for earlier ones, so a launch whose
+// workgroups are dispatched in block order always completes; a wait that gives
+// up after max_polls polls leaves its rows NaN.
+struct OProj {
+  const int32_t* packed;
+  const void* scale;
+  const int32_t* zeros;
+  int N, K, gshift;
+};
+
+template <int XT, int ST, int L>
+__global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, int nq,
+                                                const int32_t* __restrict__ pos_dev, int pos_host,
+                                                int max_len, uint16_t* __restrict__ att, OProj o,
+                                                const uint16_t* __restrict__ residual,
+                                                uint16_t* __restrict__ y, int max_polls) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int b = blockIdx.x, t = threadIdx.x;
+  if (b < nq) {
+    __shared__ __align__(16) uint16_t s_o[HD];
+    if (t < HD) {
+      const int pos = pos_dev ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_host;
+      const uint16_t v = combine_head<XT>(part, nq, b, t, pos, max_len);
+      const float f = Half<XT>::to_f32(v);
+      s_o[t] = f != f ? Half<XT>::QNAN : v;
+    }
+    __syncthreads();
+    if (t < HD / 8) {
+      const rsrc_t r = rsrc(att + (int64_t)b * HD, HD * 2u);
+      __builtin_amdgcn_raw_buffer_store_b128(((const u32x4*)s_o)[t], r, (u32)t * 16u, 0,
+                                             kCoherent);
+    }
+    return;
+  }
+  gemv_ct_body<XT, ST, L, false, true>(b - nq, 0, att, 0, o.packed, 0, o.scale, 0, o.zeros, 0,
+                                       nullptr, 1, o.N, o.K, o.gshift, y, XT, residual, nullptr,
+                                       0.f, lds, max_polls);
 }
 
 namespace {
 
-// workspace: the chunk partials [nch][nq][PSTR] fp32
+// workspace: the chunk partials [nch][nq][PSTR] fp32 (then, for the launch with
+// o_proj, the attention output [nq][HD] at the next 256-byte boundary)
 size_t attn_ws(int nq, int max_len) {
   const size_t nch = ((size_t)max_len + ACH - 1) / ACH;
   return nch * nq * PSTR * sizeof(float);
+}
+size_t attn_o_ws(int nq, int max_len) {
+  return ((attn_ws(nq, max_len) + 255) & ~(size_t)255) + (size_t)nq * HD * 2;
+}
+
+// o_proj behind the attention (k_attn_o), or none (o == nullptr: k_attn_combine)
+struct OLaunch {
+  OProj w;
+  int st;  // scale dtype
+  const void* residual;
+  void* y;
+};
+
+template <int XT, int ST>
+int launch_attn_o(const float* part, int nq, const int32_t* pos_dev, int pos, int max_len,
+                  uint16_t* att, const OLaunch& o, hipStream_t s) {
+  const int C = o.w.K / 32, L = gemv_lanes_per_row(C), rpw = 256 / L;
+  const dim3 grid(nq + (o.w.N + rpw - 1) / rpw);
+  const size_t lds = (size_t)o.w.K * 2 + (size_t)C * 8;
+#define I4_AO_CASE(L_)                                                                          \
+  if (L == L_) {                                                                                \
+    hipLaunchKernelGGL((k_attn_o<XT, ST, L_>), grid, dim3(256), lds, s, part, nq, pos_dev, pos, \
+                       max_len, att, o.w, (const uint16_t*)o.residual, (uint16_t*)o.y,          \
+                       kHandoffPolls);                                                          \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
+  }
+  I4_AO_CASE(8) I4_AO_CASE(16) I4_AO_CASE(32) I4_AO_CASE(64)
+#undef I4_AO_CASE
+  return I4_ERR_SHAPE;
 }
 
 template <int XT>
 int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* kn_w, float eps,
                 const RopeTab& rt, const int32_t* pos_dev, int pos, void* k_cache,
-                void* v_cache, int max_len, void* out, void* ws, hipStream_t s) {
+                void* v_cache, int max_len, void* out, void* ws, hipStream_t s,
+                const OLaunch* o = nullptr) {
   const int64_t hs = (int64_t)max_len * HD;
   float* part = (float*)ws;
   // device position: every chunk of max_len is launched, those past pos exit at once
@@ -317,10 +403,19 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
     hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, (const uint16_t*)qkv,  \
                        nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w, eps, pos_dev,   \
                        pos, max_len, rt,                                                      \
-                       (uint16_t*)k_cache, (uint16_t*)v_cache, hs, scale, part, gsplit);    \
+                       (uint16_t*)k_cache, (uint16_t*)v_cache, hs, scale, part, gsplit,     \
+                       (u32x4*)(o ? out : nullptr), o ? nq * HD / 8 : 0);                   \
   else
   I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) return I4_ERR_SHAPE;
 #undef I4_AC_CASE
+  if (o) {  // out is the attention output buffer in the workspace
+    if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
+    if (o->st == I4_F32)
+      return launch_attn_o<XT, I4_F32>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, s);
+    if (o->st == I4_F16)
+      return launch_attn_o<XT, I4_F16>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, s);
+    return launch_attn_o<XT, I4_BF16>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, s);
+  }
   hipLaunchKernelGGL(k_attn_combine<XT>, dim3(nq), dim3(HD), 0, s, part, nq, pos_dev, pos,
                      max_len, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
@@ -336,11 +431,17 @@ size_t i4_attn_decode_workspace_bytes(int n_heads, int head_dim, int max_len) {
   return i4::attn_ws(n_heads, max_len);
 }
 
+size_t i4_attn_decode_o_workspace_bytes(int n_heads, int head_dim, int max_len) {
+  if (n_heads < 1 || head_dim != i4::HD || max_len < 1) return 0;
+  return i4::attn_o_ws(n_heads, max_len);
+}
+
 static int attn_entry(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
                       const void* q_norm_w, const void* k_norm_w, float eps,
                       const float* inv_freq, const int32_t* pos_dev, int pos, void* k_cache,
                       void* v_cache, int max_len, void* out, void* workspace,
-                      size_t workspace_bytes, hipStream_t stream) {
+                      size_t workspace_bytes, hipStream_t stream,
+                      const i4::OLaunch* o = nullptr) {
   if (!qkv || !q_norm_w || !k_norm_w || !inv_freq || !k_cache || !v_cache || !out)
     return I4_ERR_NULL;
   if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
@@ -352,17 +453,20 @@ static int attn_entry(const void* qkv, int x_dtype, int n_heads, int n_kv_heads,
       ((uintptr_t)k_cache & 15) || ((uintptr_t)v_cache & 15) || ((uintptr_t)out & 3) ||
       ((uintptr_t)pos_dev & 3))
     return I4_ERR_ALIGN;
-  if (!workspace || workspace_bytes < i4::attn_ws(n_heads, max_len)) return I4_ERR_WORKSPACE;
+  const size_t need = o ? i4::attn_o_ws(n_heads, max_len) : i4::attn_ws(n_heads, max_len);
+  if (!workspace || workspace_bytes < need) return I4_ERR_WORKSPACE;
   if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
   i4::RopeTab rt;
   for (int i = 0; i < i4::HD / 2; ++i) rt.inv_freq[i] = inv_freq[i];
+  // with o_proj the attention output lives in the workspace, after the partials
+  void* att = o ? (char*)workspace + ((i4::attn_ws(n_heads, max_len) + 255) & ~(size_t)255) : out;
   return x_dtype == I4_F16
              ? i4::attn_launch<I4_F16>(qkv, n_heads, n_kv_heads, q_norm_w, k_norm_w, eps, rt,
-                                       pos_dev, pos, k_cache, v_cache, max_len, out, workspace,
-                                       stream)
+                                       pos_dev, pos, k_cache, v_cache, max_len, att, workspace,
+                                       stream, o)
              : i4::attn_launch<I4_BF16>(qkv, n_heads, n_kv_heads, q_norm_w, k_norm_w, eps, rt,
-                                        pos_dev, pos, k_cache, v_cache, max_len, out, workspace,
-                                        stream);
+                                        pos_dev, pos, k_cache, v_cache, max_len, att, workspace,
+                                        stream, o);
 }
 
 int i4_attn_decode(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
@@ -383,6 +487,30 @@ int i4_attn_decode_at(const void* qkv, int x_dtype, int n_heads, int n_kv_heads,
   return attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
                     inv_freq, pos, 0, k_cache, v_cache, max_len, out, workspace,
                     workspace_bytes, stream);
+}
+
+int i4_attn_decode_o(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
+                     const void* q_norm_w, const void* k_norm_w, float eps,
+                     const float* inv_freq, const int32_t* pos_dev, int pos, void* k_cache,
+                     void* v_cache, int max_len, const i4_qweight* o_w, const void* residual,
+                     void* y, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!o_w || !y) return I4_ERR_NULL;
+  i4_qweight nw;
+  const int rc = i4_check_weight(o_w, &nw);
+  if (rc) return rc;
+  if (nw.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  // o_proj: one weight, K = the attention output (one staging round of the poll)
+  if (nw.E != 1 || nw.K != n_heads * head_dim || nw.K < 256 || nw.K > 8192)
+    return I4_ERR_SHAPE;
+  if (((uintptr_t)y & 1) || ((uintptr_t)residual & 1)) return I4_ERR_ALIGN;
+  i4::OLaunch o;
+  o.w = i4::OProj{nw.packed, nw.scale, nw.zeros, nw.N, nw.K, i4_group_shift(nw.group)};
+  o.st = nw.scale_dtype;
+  o.residual = residual;
+  o.y = y;
+  return attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
+                    inv_freq, pos_dev, pos, k_cache, v_cache, max_len, y, workspace,
+                    workspace_bytes, stream, &o);
 }
 
 }  // extern "C"

@@ -335,6 +335,32 @@ template <int XT, int NT = 256> struct Stager {
   }
 };
 
+// Polls for the activations of a handoff launch (one staging round: at most
+// 4 x 256 16-byte words): the rows are loaded device-coherently until no value
+// still holds the pending pattern (an earlier launch fills them with it;
+// producer workgroups of the same launch overwrite every value).  Returns true
+// if max_polls polls went by without that, which a launch whose workgroups are
+// dispatched in block order never sees: the bound guarantees that every wave
+// exits.  The barrier in each pass also keeps the loads inside the loop.
+template <int XT>
+__device__ inline bool poll_rows(Stager<XT, 256>& st, const uint16_t* src, int max_polls) {
+  constexpr int nt = 256;
+  const rsrc_t r = rsrc(src, (u32)st.total * 16u);
+  for (int it = 0;; ++it) {
+    bool pend = false;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = min(u * nt + (int)threadIdx.x, st.total - 1);
+      st.d[u] = ld16_coherent(r, (u32)idx * 16u);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pend |= has_pending(st.d[u]);
+    if (!__syncthreads_or(pend)) return false;
+    if (it >= max_polls) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 // RMSNorm of 8 values (one 16-byte load): round(round(x * r) * w), the order
 // of transformers' Qwen3OmniMoeThinkerTextRMSNorm.forward
 // (modeling_qwen3_omni_moe.py:1388-1393 in transformers 5.15).

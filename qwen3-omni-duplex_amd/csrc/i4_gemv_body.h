@@ -1,0 +1,136 @@
+// Body of the CT dequant-GEMV (k_gemv_ct), shared by the GEMV launches and by
+// launches that run it behind a producer of their activation row.
+//
+// L lanes cooperate on one output row; lane l of the row owns the 32-column
+// chunks c = l, l + L, l + 2L, ... and streams each chunk with one 16-byte
+// load, so the L lanes of a row read L*16 contiguous bytes (L >= 8 keeps every
+// load a whole 128-byte line).  A 256-thread workgroup therefore owns 256/L
+// consecutive rows of one selected expert.  All weight loads of a round are
+// issued before the activation row is staged, so the staging latency hides
+// under the stream.
+#pragma once
+
+#include "i4_common.h"
+
+namespace i4 {
+
+static constexpr int GEMV_WG = 256;
+static constexpr int GEMV_ROUND = 4;  // chunks per lane whose loads are in flight together
+
+// NORM: each workgroup first applies the RMSNorm with weight nw to its staged x
+// row (K <= 4096), with the arithmetic of k_rmsnorm_t (same thread -> word map
+// and reduction order), so the result equals i4_rmsnorm followed by the GEMV.
+// POLL: x (one row, K <= 8192) is written by earlier workgroups of the same
+// launch and holds the pending pattern until then; the workgroup issues its
+// first round of weight loads, then polls x (poll_rows) instead of loading it.
+// Rows of a workgroup whose wait gives up come out NaN.
+template <int XT, int ST, int L, bool NORM, bool POLL>
+__device__ inline void gemv_ct_body(
+    int bx, int j, const uint16_t* __restrict__ x, int64_t x_stride,
+    const int32_t* __restrict__ packed, int64_t p_es, const void* __restrict__ scale,
+    int64_t s_es, const int32_t* __restrict__ zeros, int64_t z_es,
+    const int32_t* __restrict__ sel, int E, int N, int K, int gshift, void* __restrict__ out,
+    int ot, const void* __restrict__ bias, const uint16_t* __restrict__ nw, float eps,
+    unsigned char* lds, int max_polls) {
+  constexpr int WG = GEMV_WG, ROUND = GEMV_ROUND;
+  static_assert(!(NORM && POLL), "a polled row is used as it arrives");
+  constexpr int RPW = WG / L;
+  const int C = K >> 5, KW = K >> 3;
+  const int NG = (C + (1 << gshift) - 1) >> gshift, NZW = (NG + 7) >> 3;
+  const int cpl = (C + L - 1) / L;
+  u32x4* xs = (u32x4*)lds;
+  float2* sums = (float2*)(lds + (size_t)K * 2);
+
+  const int rl = threadIdx.x / L, cl = threadIdx.x % L;
+  const int n = bx * RPW + rl;
+  const bool rv = n < N;
+  const int e = sel ? sel[j] : 0;
+  if ((unsigned)e >= (unsigned)E) {  // bad expert id: never dereference it
+    if (rv && cl == 0) {
+      if (ot == I4_F32) store_out<I4_F32>(out, (int64_t)j * N + n, __builtin_nanf(""));
+      else if (ot == I4_F16) store_out<I4_F16>(out, (int64_t)j * N + n, __builtin_nanf(""));
+      else store_out<I4_BF16>(out, (int64_t)j * N + n, __builtin_nanf(""));
+    }
+    return;
+  }
+  const int nn = rv ? n : 0;
+  RowPtr rp;
+  rp.p = packed + e * p_es + (int64_t)nn * KW;
+  rp.s = scale_at<ST>(scale, e * s_es + (int64_t)nn * NG);
+  rp.z = zeros ? (const u32*)zeros + e * z_es + (int64_t)nn * NZW : kSymZeros;
+  const uint16_t* xrow = x + (int64_t)j * x_stride;
+  const u32 mg = magic_v<XT>();
+  Stager<XT> st(1, K);  // activation loads first, weight loads behind them
+  auto row_of = [&](int) { return xrow; };
+  if constexpr (!POLL) st.issue(row_of, 0);
+  u32x4 gv[2];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) gv[u] = ldg16(nw + 8 * min(u * WG + (int)threadIdx.x, st.total - 1));
+  }
+
+  bool late = false;
+  float row = 0.f;
+  for (int r0 = 0; r0 < cpl; r0 += ROUND) {
+    Chunk ch[ROUND];
+#pragma unroll
+    for (int i = 0; i < ROUND; ++i) ch[i] = load_chunk<ST>(rp, min(cl + (r0 + i) * L, C - 1), gshift);
+    if (r0 == 0) {
+      if constexpr (POLL) late = poll_rows<XT>(st, xrow, max_polls);
+      if constexpr (NORM) {
+        __shared__ float s_ss[WG / 64];
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          if (u * WG + (int)threadIdx.x < st.total) ss += sumsq8<XT>(st.d[u]);
+        ss = group_sum<64>(ss);
+        if ((threadIdx.x & 63) == 0) s_ss[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float r =
+            1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)K + eps);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          st.d[u].x = norm_pair<XT>(st.d[u].x, gv[u].x, r);
+          st.d[u].y = norm_pair<XT>(st.d[u].y, gv[u].y, r);
+          st.d[u].z = norm_pair<XT>(st.d[u].z, gv[u].z, r);
+          st.d[u].w = norm_pair<XT>(st.d[u].w, gv[u].w, r);
+        }
+      }
+      st.commit(0, xs, sums);
+      if constexpr (!POLL) st.rest(row_of, xs, sums);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < ROUND; ++i) {
+      const int c = cl + (r0 + i) * L;
+      if (c < C)
+        row += chunk_dot<XT, ST>(ch[i], xs[c], xs[C + c], xs[2 * C + c], xs[3 * C + c], sums[c], c,
+                                 gshift, mg);
+    }
+  }
+  row = group_sum<L>(row);
+  if (rv && cl == 0) {
+    if (late) row = __builtin_nanf("");
+    const int64_t o = (int64_t)j * N + n;
+    if (ot == I4_F32) {
+      if (bias) row += ((const float*)bias)[n];
+      store_out<I4_F32>(out, o, row);
+    } else if (ot == I4_F16) {
+      if (bias) row += Half<I4_F16>::to_f32(((const uint16_t*)bias)[n]);
+      store_out<I4_F16>(out, o, row);
+    } else {
+      if (bias) row += Half<I4_BF16>::to_f32(((const uint16_t*)bias)[n]);
+      store_out<I4_BF16>(out, o, row);
+    }
+  }
+}
+
+// lanes per output row (4..64, 3+ chunks per lane when the row is long enough)
+inline int gemv_lanes_per_row(int C) {
+  int L = 4;
+  while (L * 2 <= C && L < 64) L *= 2;
+  while (L > 8 && C < 3 * L) L /= 2;
+  return L;
+}
+
+}  // namespace i4

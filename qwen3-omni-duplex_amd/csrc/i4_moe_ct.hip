@@ -199,31 +199,6 @@ template <int L> struct DownShape {
   static constexpr int RW = NGR / GPR;
 };
 
-// Polls for the activations of a handoff launch: the rows are loaded
-// device-coherently until no value still holds the pending pattern (the
-// router's launch fills them with it; gate_up workgroups of the same launch
-// overwrite every value).  Returns true if max_polls polls went by without
-// that, which a launch whose workgroups are dispatched in block order never
-// sees: the bound guarantees that every wave exits.
-template <int XT>
-__device__ inline bool poll_rows(Stager<XT>& st, const uint16_t* src, int max_polls) {
-  constexpr int nt = WG;
-  const rsrc_t r = rsrc(src, (u32)st.total * 16u);
-  for (int it = 0;; ++it) {
-    bool pend = false;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int idx = min(u * nt + (int)threadIdx.x, st.total - 1);
-      st.d[u] = ld16_coherent(r, (u32)idx * 16u);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) pend |= has_pending(st.d[u]);
-    if (!__syncthreads_or(pend)) return false;
-    if (it >= max_polls) return true;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
 // HANDOFF: the experts and routing weights come from the logits (every wave
 // ranks them itself, bit-identical to the gate_up workgroups), and act is
 // polled as it is written by the gate_up workgroups of the same launch.
@@ -406,7 +381,7 @@ inline int gate_up_lanes(int C) {
 
 // lanes per output row of the down projection (8..64, 3+ chunks per lane
 // when the row is long enough)
-inline int lanes_per_row(int C) {
+inline int down_lanes_per_row(int C) {
   int L = 8;
   while (L * 2 <= C && L < 64) L *= 2;
   while (L > 8 && C < 3 * L) L /= 2;
@@ -450,7 +425,7 @@ int launch_down_m1_ct(const void* act, int topk, const int32_t* sel, const float
                       const TW& tw, const void* res, void* out, hipStream_t s) {
   const QW w = to_qw(tw);
   const int I = w.K, C = I / 32;
-  const int L = lanes_per_row(C);
+  const int L = down_lanes_per_row(C);
   const size_t lds_base = (size_t)topk * (I * 2 + C * 8);
 #define I4_DN_CASE(L_, J_)                                                                     \
   if (L == L_ && (topk + DownShape<L_>::GPR - 1) / DownShape<L_>::GPR <= J_) {                 \
@@ -472,7 +447,7 @@ int launch_down_m1_ct(const void* act, int topk, const int32_t* sel, const float
 // lanes 8..64; down lanes 8 or 16, i.e. I < 1536) with topk <= 8 and the
 // activation rows in one staging round of the down workgroups.
 bool moe_m1_ct_fits(int topk, int H, int I) {
-  const int LD = lanes_per_row(I / 32);
+  const int LD = down_lanes_per_row(I / 32);
   if (topk > 8 || (LD != 8 && LD != 16)) return false;
   if ((int64_t)topk * (I / 8) > 4 * WG) return false;
   const size_t lds_d = (size_t)topk * (I * 2 + (I / 32) * 8) + (size_t)topk * 8 * 4;
@@ -489,7 +464,7 @@ int launch_moe_m1_ct(const GateUpArgs& ga, const TW* tgu, const TW& tdn, const v
   const int H = a.dn.N, I = a.dn.K;
   if (!status || max_polls < 0) return I4_ERR_NULL;
   if (!moe_m1_ct_fits(ga.topk, H, I)) return I4_ERR_SHAPE;
-  const int LG = gate_up_lanes(H / 32), LD = lanes_per_row(I / 32);
+  const int LG = gate_up_lanes(H / 32), LD = down_lanes_per_row(I / 32);
   a.x = (const uint16_t*)ga.x;
   a.topk = ga.topk;
   a.sel = ga.sel;

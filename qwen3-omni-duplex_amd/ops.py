@@ -483,6 +483,52 @@ def attn_decode(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: torc
     return out
 
 
+def attn_decode_o(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: torch.Tensor,
+                  k_norm_w: torch.Tensor, eps: float, inv_freq: torch.Tensor,
+                  pos: int | torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  o_w: QWeight, residual: torch.Tensor | None = None,
+                  workspace: Workspace | None = None) -> torch.Tensor:
+    """attn_decode followed by the o projection and the residual add (i4_attn_decode_o):
+    returns residual + o_w attn as [o_w.N] in the activation dtype, equal bit for bit to
+    linear(attn_decode(...), o_w, bias=residual), in one launch fewer (the o_proj
+    workgroups take the merged heads over inside the merge launch).  o_w is a CT weight."""
+    dev = _lib.require_device(qkv, q_norm_w, k_norm_w, k_cache, v_cache, o_w.packed, residual)
+    pos_dev = None
+    if isinstance(pos, torch.Tensor):
+        if pos.device != dev or pos.dtype != torch.int32 or pos.numel() != 1:
+            raise RuntimeError("a device position is one int32 on the tensors' device")
+        pos_dev = pos
+    xt = _lib.half_code(qkv.dtype)
+    nkv, max_len, hd = k_cache.shape
+    if k_cache.dtype != qkv.dtype or v_cache.shape != k_cache.shape or v_cache.dtype != qkv.dtype:
+        raise RuntimeError("the caches must be [n_kv_heads, max_len, head_dim] in the activation dtype")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise RuntimeError("the caches must be contiguous")
+    if qkv.numel() != (n_heads + 2 * n_kv_heads) * hd or nkv != n_kv_heads:
+        raise RuntimeError("qkv / cache shapes do not match the head counts")
+    res = None
+    if residual is not None:
+        if residual.dtype != qkv.dtype or residual.numel() != o_w.N:
+            raise RuntimeError("the residual must be [o_w.N] in the activation dtype")
+        res = residual.contiguous()
+    tab = inv_freq.detach().to("cpu", torch.float32).contiguous()
+    if tab.numel() != hd // 2:
+        raise RuntimeError("inv_freq must hold head_dim / 2 values")
+    lb = _lib.lib()
+    ws = (workspace or Workspace()).get(lb.i4_attn_decode_o_workspace_bytes(n_heads, hd, max_len),
+                                        dev)
+    y = torch.empty(o_w.N, dtype=qkv.dtype, device=dev)
+    cw = o_w.c()
+    _lib.check(lb.i4_attn_decode_o(
+        qkv.contiguous().data_ptr(), xt, n_heads, n_kv_heads, hd,
+        q_norm_w.contiguous().data_ptr(), k_norm_w.contiguous().data_ptr(), float(eps),
+        tab.data_ptr(), None if pos_dev is None else pos_dev.data_ptr(),
+        0 if pos_dev is not None else int(pos), k_cache.data_ptr(), v_cache.data_ptr(), max_len,
+        ctypes.byref(cw), _lib.ptr(res), y.data_ptr(), ws.data_ptr(), ws.numel(),
+        _lib.stream(dev)))
+    return y
+
+
 def rmsnorm_linear(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: QWeight,
                    bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None):
     """y = RMSNorm(x) W^T (+ bias) in one launch (i4_rmsnorm_linear; CT weight, K <= 4096),

@@ -229,6 +229,24 @@ def test_decode_attention_validation_codes(pkg):
     assert lib.i4_attn_decode_at(0x30000, 2, 32, 4, 128, 0x40000, 0x50000, 1e-6, tab, 0x70002,
                                  0x100000, 0x200000, 4096, 0x60000, 0x300000, ws, None) == -4
 
+    # with o_proj: a CT weight of K = n_heads * head_dim, and a larger workspace (the
+    # merged heads live in it after the partials, at a 256-byte boundary)
+    wso = lib.i4_attn_decode_o_workspace_bytes(32, 128, 4096)
+    assert wso == ((ws + 255) & ~255) + 32 * 128 * 2
+    ow = _qw(_lib, E=1, N=2048, K=4096, group=32)
+    callo = lambda **kw: lib.i4_attn_decode_o(
+        0x30000, 2, kw.get("nh", 32), 4, 128, 0x40000, 0x50000, 1e-6, tab, kw.get("pd", None),
+        5, 0x100000, 0x200000, 4096, kw.get("ow", ctypes.byref(ow)), kw.get("res", 0x80000),
+        kw.get("y", 0x90000), 0x300000, kw.get("wsb", wso), None)
+    assert callo(ow=None) == -1
+    assert callo(y=None) == -1
+    assert callo(ow=ctypes.byref(_qw(_lib, E=1, N=2048, K=4096, group=128, layout=1))) == -5
+    assert callo(ow=ctypes.byref(_qw(_lib, E=1, N=2048, K=2048, group=32))) == -2  # K != 32*128
+    assert callo(ow=ctypes.byref(_qw(_lib, E=2, N=2048, K=4096, group=32))) == -2  # one weight
+    assert callo(res=0x80001) == -4
+    assert callo(wsb=ws) == -7          # the partials alone do not hold the merged heads
+    assert callo(pd=0x70002) == -4
+
 
 def test_dense_moe_validation_codes(pkg):
     """i4_dmoe_forward rejects bad calls before any launch (Talker shapes: H 1024,

@@ -252,6 +252,54 @@ def test_attn_decode_head_layouts(pkg, dev, xdt, nh, nkv, pos):
     assert torch.equal(vc[:, pos], v.to(tdt).to(dev))
 
 
+@pytest.mark.parametrize("xdt,nh,nkv,pos,N,G", [("bf16", 32, 4, 1000, 2048, 32),
+                                                 ("f16", 32, 4, 63, 2048, 128),
+                                                 ("f16", 16, 4, 70, 1024, 32),
+                                                 ("bf16", 8, 8, 0, 2048, 64)])
+def test_attn_decode_o_equals_attention_then_o_proj(pkg, dev, xdt, nh, nkv, pos, N, G):
+    """i4_attn_decode_o (head merge and o_proj in one launch, the o_proj workgroups taking
+    the merged heads over inside it) equals i4_attn_decode followed by i4_linear with the
+    residual as bias, bit for bit: the Thinker's 32 / 4 heads at context 1000 and at the
+    last row of a chunk, other head layouts and groups, host and device positions; a device
+    position past the cache gives NaN."""
+    rng = np.random.default_rng(300 + nh + pos)
+    tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    hd, max_len = 128, 1024
+    K = nh * hd
+    from tests import _gen
+
+    p, sc, z = _gen.ct_weight(rng, 1, N, K, G, zeros=G != 32)
+    w = pkg.QWeight(t_(p, dev), t_(sc, dev).to(tdt), None if z is None else t_(z, dev), "ct",
+                    G, N, K)
+    qkv = torch.from_numpy(rng.standard_normal((nh + 2 * nkv) * hd).astype(np.float32)).to(dev, tdt)
+    qn = torch.from_numpy(rng.uniform(0.5, 1.5, hd).astype(np.float32)).to(dev, tdt)
+    kn = torch.from_numpy(rng.uniform(0.5, 1.5, hd).astype(np.float32)).to(dev, tdt)
+    cache = [torch.randn(nkv, max_len, hd, device=dev).to(tdt) for _ in range(2)]
+    res = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(dev, tdt)
+    inv = pkg.rope_inv_freq(hd, 1e6)
+    kc, vc = cache[0].clone(), cache[1].clone()
+    a = pkg.attn_decode(qkv, nh, nkv, qn, kn, 1e-6, inv, pos, kc, vc)
+    want = pkg.linear(a.view(1, -1), w, bias=res).view(-1)
+    for dev_pos in (False, True):
+        kc2, vc2 = cache[0].clone(), cache[1].clone()
+        pp = torch.full((1,), pos, dtype=torch.int32, device=dev) if dev_pos else pos
+        got = pkg.attn_decode_o(qkv, nh, nkv, qn, kn, 1e-6, inv, pp, kc2, vc2, w, res)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(got, want), dev_pos
+        assert torch.equal(kc2, kc) and torch.equal(vc2, vc)
+    # the o_proj GEMV itself against the oracle's fp32 product on the same attention output
+    W = i4ref.ct_dequant(p, w.scale.float().cpu().numpy(), K, G, zeros=z)[0]
+    ref = np.asarray(host(a), np.float64) @ W.T.astype(np.float64) + np.asarray(host(res), np.float64)
+    assert i4ref.rel_err(np.asarray(host(want), np.float64), ref) <= TOL
+    bad = torch.full((1,), max_len, dtype=torch.int32, device=dev)
+    kc3 = cache[0].clone()
+    got = pkg.attn_decode_o(qkv, nh, nkv, qn, kn, 1e-6, inv, bad, kc3, cache[1].clone(), w, res)
+    torch.cuda.synchronize()
+    assert torch.isnan(got.float()).all()
+    assert torch.equal(kc3, cache[0])
+
+
 def test_decode_step_graph_with_device_position(pkg, dev, ckpt):
     """One hipGraph of the 2-layer decode step, captured with the position in device memory,
     replayed for positions 0..5 with new inputs (and other work between replays): every
