@@ -287,7 +287,9 @@ def time_talker_moe(pkg, torch, dev, replays, n_layers=20):
     expert FFN 768 with its sigmoid gate, 20 layers chained with residual adds; experts in
     bf16 and in the reference's int8 mode (per-output-row scales; the shared expert stays
     bf16).  Weights ~ N(0, 0.01), router ~ N(0, 0.05), x ~ N(0, 1), bf16, generated on the
-    device.  Each timed region is one hipGraph of the 20 layers (3 launches per layer)."""
+    device.  Each timed region is one hipGraph of the 20 layers (per layer the router launch
+    and, for 16-bit experts, one launch of gate|up and down; int8 experts: gate|up and down
+    launches)."""
     Ht, Et, Kt, It, Ist = 1024, 128, 6, 384, 768
     dt = torch.bfloat16
     gen = torch.Generator(device=dev)
@@ -337,7 +339,8 @@ def time_talker_moe(pkg, torch, dev, replays, n_layers=20):
     return {"layers": n_layers, **out,
             "workload": "Talker MoE block at M=1: hidden 1024, 128 experts, top-6, FFN 384, "
                         "shared expert 768 + sigmoid gate, residual chain",
-            "timing": f"hipGraph of {n_layers} layers (router, gate|up, down launches each), "
+            "timing": f"hipGraph of {n_layers} layers (router + one expert launch each for "
+                      "bf16; router, gate|up, down for int8), "
                       f"mean over {replays} replays"}
 
 
