@@ -184,6 +184,7 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
     float* part, void* __restrict__ out, int ot, const void* __restrict__ bias, int max_polls) {
   constexpr int NT = 64 * NWAVE, PASS = 16 * NWAVE, KS = PASS * PPT, CPT = SK_COLS / NT;
   __shared__ f32x4 red[NWAVE][64];
+  __shared__ int s_gave_up;  // the reducer's wait gave up (set before the first barrier)
   const int strip = (int)blockIdx.x / P, slice = (int)blockIdx.x % P;
   const int j = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -284,6 +285,7 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
     // lane (q, h1 h2 h3) now holds columns 16 h1 + 8 h2 + 4 h3 + 0..3 of quad q
     red[wave][lane] = f32x4{r[0], r[1], r[2], r[3]};
   }
+  if (t == 0) s_gave_up = 0;
   __syncthreads();
 
   // cross-wave sum and scale: this slice's partial of columns ct = t + NT c
@@ -316,8 +318,6 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
   // s = t / 64 (mod NWAVE), up to 16 * NWAVE slices per round trip, until none
   // is pending; the slice classes are then added in class order in LDS
   __shared__ f32x4 red2[NWAVE][64];
-  __shared__ int s_gave_up;
-  if (t == 0) s_gave_up = 0;
   {
     constexpr int MAXB = 16;
     const rsrc_t pr = rsrc(strip_part, (u32)P * SK_COLS * 4u);
