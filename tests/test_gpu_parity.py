@@ -503,6 +503,24 @@ def test_route_topk_bit_exact(pkg, dev, ldt):
     np.testing.assert_allclose(host(wh).astype(np.float64), w_ref, rtol=1e-3, atol=1e-5)
 
 
+@pytest.mark.parametrize("E,k", [(60, 8), (96, 6), (200, 8), (512, 1), (512, 8)])
+def test_route_topk_expert_counts(pkg, dev, E, k):
+    """Top-k at expert counts that leave lanes of the wave empty (60, 96: two logits per lane
+    with the tail masked) or take eight logits per lane (200, 512), top-1 / 6 / 8, fp16 and
+    bf16 logits with exact ties, also across the top-k cut: indices bit-exact with the
+    oracle's ranking (value, then lower id), weights to fp32 rounding."""
+    rng = np.random.default_rng(300 + E + k)
+    T = 96
+    v = rng.standard_normal((T, E)).astype(np.float32)
+    v[:24] = np.round(v[:24] * 2) / 2  # many exact ties
+    v[24] = 0.0                        # every logit tied
+    for lg in (v.astype(np.float16), i4ref.f32_to_bf16_bits(v)):
+        w, sel = pkg.route(t_(lg, dev), k, w_dtype=torch.float32)
+        sel_ref, w_ref = i4ref.route(f_(lg), k)
+        np.testing.assert_array_equal(sel.cpu().numpy(), sel_ref)
+        np.testing.assert_allclose(host(w), w_ref, rtol=1e-5, atol=1e-7)
+
+
 def test_route_without_renorm(pkg, dev):
     rng = np.random.default_rng(17)
     lg = rng.standard_normal((8, 128)).astype(np.float16)
@@ -529,7 +547,8 @@ def test_router_logits(pkg, dev, xdt, T):
 
 
 # ---------------------------------------------------------------- MoE block
-def _awq_moe(pkg, dev, rng, E=128, H=2048, I=768, G=128, sdt=np.float16, layouts="both"):
+def _awq_moe(pkg, dev, rng, E=128, H=2048, I=768, G=128, sdt=np.float16, layouts="both",
+             top_k=8):
     g = _gen.awq_weight(rng, E, H, I, G, sdt)
     u = _gen.awq_weight(rng, E, H, I, G, sdt)
     d = _gen.awq_weight(rng, E, I, H, G, sdt)
@@ -539,7 +558,8 @@ def _awq_moe(pkg, dev, rng, E=128, H=2048, I=768, G=128, sdt=np.float16, layouts
         return pkg.QWeight(t_(part[0], dev), t_(part[2], dev), t_(part[1], dev), "awq", G,
                            part[0].shape[2] * 8, part[0].shape[1])
 
-    moe = pkg.FusedPackedMoE.from_awq(q(g), q(u), q(d), t_(wr, dev), top_k=8, layouts=layouts)
+    moe = pkg.FusedPackedMoE.from_awq(q(g), q(u), q(d), t_(wr, dev), top_k=top_k,
+                                      layouts=layouts)
     dgu = lambda e: np.concatenate([i4ref.awq_dequant(g[0][e], g[1][e], f_(g[2][e]), G),
                                     i4ref.awq_dequant(u[0][e], u[1][e], f_(u[2][e]), G)], axis=0)
     ddn = lambda e: i4ref.awq_dequant(d[0][e], d[1][e], f_(d[2][e]), G)
@@ -642,6 +662,19 @@ def test_moe_decode_reference_format(pkg, dev, layouts):
     ddn = lambda e: i4ref.ct_dequant(dp[e], f_(ds[e]), I, G)
     for _ in range(2):
         _check_moe(pkg, moe, dgu, ddn, make_x(rng, (1, H), "bf16"), "bf16", dev)
+
+
+@pytest.mark.parametrize("k", [4, 6])
+def test_moe_other_top_k(pkg, dev, k):
+    """Top-4 and top-6 of 128 experts: the single-launch decode layer (its down workgroups'
+    expert groups past top-k stay idle) and the grouped MFMA path at 32 tokens, routing
+    bit-exact, outputs against the oracle."""
+    rng = np.random.default_rng(40 + k)
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, top_k=k)
+    x1 = make_x(rng, (1, 2048), "f16")
+    _check_moe(pkg, moe, dgu, ddn, x1, "f16", dev, residual=x1)
+    x = make_x(rng, (32, 2048), "f16")
+    _check_moe(pkg, moe, dgu, ddn, x, "f16", dev, residual=x)
 
 
 def test_moe_m32(pkg, dev):
