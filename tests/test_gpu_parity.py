@@ -677,6 +677,30 @@ def test_moe_other_top_k(pkg, dev, k):
     _check_moe(pkg, moe, dgu, ddn, x, "f16", dev, residual=x)
 
 
+def test_moe_entry_size_boundaries(pkg, dev):
+    """Experts with exactly 1, 16, 17, 64, 65, 128 and 129 tokens: the edges of the one-m-block
+    small entries (<= 16 tokens) and of the 64-token large entries (several per expert, the
+    last one ragged), in one grouped call of 129 tokens whose logits put each token's top-8
+    on chosen experts (distinct values, no ties)."""
+    rng = np.random.default_rng(46)
+    E, T, H = 128, 129, 2048
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng)
+    sizes = {0: 1, 1: 16, 2: 17, 3: 64, 4: 65, 5: 128, 6: 129}
+    lg = rng.uniform(-4.0, -1.0, (T, E)).astype(np.float32)
+    fill = 7
+    for t in range(T):
+        chosen = [e for e, n in sizes.items() if t < n]
+        while len(chosen) < 8:  # the rest of the top-8 from experts 7..22 in turn
+            chosen.append(fill)
+            fill = 7 + (fill - 7 + 1) % 16
+        lg[t, chosen] = 2.0 + 0.01 * np.arange(8) + rng.uniform(0, 0.001, 8)
+    lg = lg.astype(np.float16)
+    counts = np.bincount(i4ref.route(lg.astype(np.float64), 8)[0].ravel(), minlength=E)
+    assert [counts[e] for e in sizes] == list(sizes.values())
+    x = make_x(rng, (T, H), "f16")
+    _check_moe(pkg, moe, dgu, ddn, x, "f16", dev, logits=lg, residual=x)
+
+
 def test_moe_m32(pkg, dev):
     rng = np.random.default_rng(23)
     moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng)
