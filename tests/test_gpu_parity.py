@@ -623,6 +623,21 @@ def test_moe_decode_m1(pkg, dev, layouts):
 
 
 @pytest.mark.parametrize("layouts", ["both", "tile"])
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+def test_moe_decode_m1_given_logits(pkg, dev, layouts, xdt):
+    """A decode block handed its router logits (no router weight: the routed gate_up launch
+    ranks them, then down + combine), with and without the residual, against the oracle."""
+    rng = np.random.default_rng(26)
+    sdt = "bf16" if xdt == "bf16" else np.float16
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, sdt=sdt, layouts=layouts)
+    for rep in range(2):
+        x = make_x(rng, (1, 2048), xdt)
+        lg = rng.standard_normal((1, 128)).astype(np.float32)
+        lg = i4ref.f32_to_bf16_bits(lg) if xdt == "bf16" else lg.astype(np.float16)
+        _check_moe(pkg, moe, dgu, ddn, x, xdt, dev, logits=lg, residual=x if rep else None)
+
+
+@pytest.mark.parametrize("layouts", ["both", "tile"])
 def test_decode_stages_compose_to_the_block(pkg, dev, layouts):
     """route+gate_up, gate_up(sel) and down+combine reproduce moe_forward at T=1 bit for bit,
     and the stage outputs match the oracle."""
