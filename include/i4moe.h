@@ -67,7 +67,7 @@
 extern "C" {
 #endif
 
-#define I4_ABI_VERSION 6
+#define I4_ABI_VERSION 7
 
 /* status codes */
 #define I4_OK               0
@@ -366,6 +366,38 @@ int    i4_attn_decode_o(const void* qkv, int x_dtype, int n_heads, int n_kv_head
                         const void* residual, void* y, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
 size_t i4_attn_decode_o_workspace_bytes(int n_heads, int head_dim, int max_len);
+
+/* One decode token through a whole Thinker decoder layer:
+ * Qwen3OmniMoeThinkerTextDecoderLayer.forward (modeling_qwen3_omni_moe.py:1539-1565
+ * in transformers 5.15), whose MoE block the reference replaces with
+ * FusedPackedMoE.forward (src/duplex/streaming/fused_packed_moe.py:191-220):
+ *   h2  = h + o_w attention(RMSNorm(h; in_norm_w, eps) qkv_w^T)
+ *   out = h2 + MoE(RMSNorm(h2; moe->norm_w, moe->norm_eps))
+ * with the attention of i4_attn_decode_o (q_norm_w / k_norm_w also use eps) and the
+ * MoE block of i4_moe_forward at T = 1 (router_w and norm_w required, CT experts).
+ * Four launches: the q|k|v GEMV with the input norm, the attention chunks, the head
+ * merge + o_proj + the MoE router (the router waves wait inside that launch for the
+ * o_proj output), the experts.  The result, the cache rows and the MoE status word
+ * equal i4_rmsnorm_linear + i4_attn_decode_o(residual = h) + i4_moe_forward(T = 1,
+ * residual = h2) bit for bit.  qkv_w, o_w: one CT weight each, qkv_w [(n_heads +
+ * 2 n_kv_heads) head_dim][H], o_w [H][n_heads head_dim]; H = 1024 or 2048.  h and
+ * out ([H], x_dtype, 16-byte aligned) may be the same buffer.  pos_dev as in
+ * i4_attn_decode_o.  Workspace: i4_thinker_layer_workspace_bytes(), no initial
+ * contents, 256-byte aligned; it begins with i4_moe_forward's T = 1 workspace, so a
+ * router or expert wait that gave up leaves I4_ERR_HANDOFF at
+ * i4_moe_status_offset(1, H, I, E, topk).  Calls sharing one must not overlap.
+ * i4_thinker_layer_workspace_bytes returns 0 for sizes the entry does not take
+ * (also an expert shape outside its single-launch expert kernel). */
+int    i4_thinker_layer_decode(const void* h, int x_dtype, const void* in_norm_w, float eps,
+                               const i4_qweight* qkv_w, int n_heads, int n_kv_heads,
+                               int head_dim, const void* q_norm_w, const void* k_norm_w,
+                               const float* inv_freq, const int32_t* pos_dev, int pos,
+                               void* k_cache, void* v_cache, int max_len,
+                               const i4_qweight* o_w, const i4_moe_weights* moe, int topk,
+                               int renorm, void* out, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+size_t i4_thinker_layer_workspace_bytes(int n_heads, int n_kv_heads, int head_dim,
+                                        int max_len, int H, int I, int E, int topk);
 
 /* ------------------------------------------------------------------------
  * MoE block on 16-bit or int8 experts with a sigmoid-gated shared expert: the

@@ -88,8 +88,34 @@ class ThinkerDecoderLayer(nn.Module):
         if moe.norm_weight is None:
             raise ValueError("the MoE block must carry its post_attention_layernorm")
         self.attn, self.moe = attn, moe
+        self._fused: bool | None = None
+
+    def fused(self) -> bool:
+        """Whether forward runs as one i4_thinker_layer_decode call: CT projections and
+        experts of the single-launch expert kernel, with the router in the block."""
+        a, m = self.attn, self.moe
+        if self._fused is None:
+            self._fused = bool(
+                a.qkv.lin.w.layout == "ct" and a.o_proj.w.layout == "ct"
+                and m.gate_up.layout == "ct" and m.router_w is not None
+                and ops.thinker_layer_fits(a.n_heads, a.n_kv_heads, a.head_dim, a.max_len,
+                                           m.hidden, m.down.K, m.gate_up.E, m.top_k))
+        return self._fused
 
     def forward(self, h: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
+        if h.numel() == h.shape[-1] and self.fused():
+            a, m = self.attn, self.moe
+            if not isinstance(pos, torch.Tensor) and not 0 <= pos < a.max_len:
+                raise ValueError(f"position {pos} outside the cache (max_len {a.max_len})")
+            return ops.thinker_layer_decode(
+                h, a.input_norm_w, a.eps, a.qkv.lin.w, a.n_heads, a.n_kv_heads, a.q_norm_w,
+                a.k_norm_w, a.inv_freq, pos, a.k_cache, a.v_cache, a.o_proj.w, m.gate_up,
+                m.down, m.top_k, m.router_w, m.norm_weight, m.norm_eps, m.norm_topk_prob,
+                a.workspace)
+        return self.unfused(h, pos)
+
+    def unfused(self, h: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
+        """The attention block, then the MoE block (each its own entry points)."""
         h = self.attn(h, pos)
         return self.moe(h, residual=h)
 

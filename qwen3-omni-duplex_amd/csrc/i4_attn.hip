@@ -22,6 +22,7 @@
 #include "i4_gemv_body.h"
 #include "i4_launch.h"
 #include "i4_moe_launch.h"
+#include "i4_router_body.h"
 
 namespace i4 {
 
@@ -92,7 +93,8 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
     const uint16_t* __restrict__ kn_w, float eps, const int32_t* __restrict__ pos_dev,
     int pos_host, int max_len, RopeTab rt, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
-    float* __restrict__ part, int gsplit, u32x4* __restrict__ pend, int n_pend) {
+    float* __restrict__ part, int gsplit, u32x4* __restrict__ pend, int n_pend,
+    int32_t* __restrict__ status) {
   __shared__ __align__(16) u32 s_q[GQ][HD / 2];  // rotated q pairs
   __shared__ u32 s_knew[HD / 2], s_vnew[HD / 2];
   __shared__ __align__(16) float s_p[GQ][ACH];
@@ -108,9 +110,13 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   // host; a grid sized for max_len leaves the chunks past it idle
   const int pos = pos_dev ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_host;
   // pend (n_pend 16-byte units, nullable): the attention output of a launch that hands
-  // it to o_proj inside the launch (k_attn_o) starts as the pending pattern
-  if (c == 0 && blockIdx.y == 0)
+  // it to o_proj inside the launch (k_attn_o), and the o_proj output when the MoE router
+  // waits for it there, start as the pending pattern; status (nullable) is reset here,
+  // before the launch whose router waves may report a wait that gave up
+  if (c == 0 && blockIdx.y == 0) {
     for (int i = t; i < n_pend; i += 256) pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
+    if (status && t == 0) *status = I4_OK;
+  }
   const int S = pos + 1, c0 = c * ACH;
   if (pos < 0 || pos >= max_len || c0 >= S) return;
   const bool last = c0 + ACH >= S;  // the chunk that holds pos
@@ -308,6 +314,14 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ p
 // Only later blocks wait, and only for earlier ones, so a launch whose
 // workgroups are dispatched in block order always completes; a wait that gives
 // up after max_polls polls leaves its rows NaN.
+// RH (the hidden size, 0 for none): the MoE router of the decoder layer runs
+// behind the o_proj workgroups (i4_thinker_layer_decode).  Those then write y
+// through to memory (it holds the pending pattern from the chunk launch), and
+// the last workgroups, four router waves each (router_wave, one expert row per
+// wave), issue their router weight loads, wait for the whole of y, and write the
+// logits of RMSNorm(y) and (expert 0's wave) that normalised row.  They also arm
+// the experts' activations with the pending pattern for the experts launch; a
+// router wait that gives up writes I4_ERR_HANDOFF to status.
 struct OProj {
   const int32_t* packed;
   const void* scale;
@@ -315,12 +329,27 @@ struct OProj {
   int N, K, gshift;
 };
 
-template <int XT, int ST, int L>
+struct RFold {
+  const uint16_t* wr;  // [E][H] router weight
+  const uint16_t* nw;  // [H] post-attention norm weight
+  float eps;
+  uint16_t* xn;        // [H] normalised row out
+  uint16_t* logits;    // [E] logits out
+  u32x4* act;          // experts' activations to arm, n_act 16-byte words
+  int n_act;
+  int32_t* status;
+  int E;
+  int n_o;  // o_proj workgroups
+};
+
+// y is not __restrict__: the router waves poll it, and a restrict pointer would let
+// the compiler take their loads out of the wait loop
+template <int XT, int ST, int L, int RH>
 __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, int nq,
                                                 const int32_t* __restrict__ pos_dev, int pos_host,
                                                 int max_len, uint16_t* __restrict__ att, OProj o,
                                                 const uint16_t* __restrict__ residual,
-                                                uint16_t* __restrict__ y, int max_polls) {
+                                                uint16_t* y, int max_polls, RFold r) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int b = blockIdx.x, t = threadIdx.x;
   if (b < nq) {
@@ -339,9 +368,25 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     }
     return;
   }
-  gemv_ct_body<XT, ST, L, false, true>(b - nq, 0, att, 0, o.packed, 0, o.scale, 0, o.zeros, 0,
-                                       nullptr, 1, o.N, o.K, o.gshift, y, XT, residual, nullptr,
-                                       0.f, lds, max_polls);
+  if constexpr (RH != 0) {
+    if (b >= nq + r.n_o) {
+      const int rb = b - nq - r.n_o, nrb = (int)gridDim.x - nq - r.n_o;
+      for (int i = rb * 256 + t; i < r.n_act; i += nrb * 256) r.act[i] = u32x4{~0u, ~0u, ~0u, ~0u};
+      const int e = rb * 4 + (t >> 6);  // wave-uniform
+      if (e >= r.E) return;
+      bool late = false;
+      router_wave<XT, true, RH, true>(y, r.wr, e, r.nw, r.eps, r.xn, r.logits, max_polls, &late);
+      if (late && (t & 63) == 0) *r.status = I4_ERR_HANDOFF;
+      return;
+    }
+    gemv_ct_body<XT, ST, L, false, true, true>(b - nq, 0, att, 0, o.packed, 0, o.scale, 0,
+                                               o.zeros, 0, nullptr, 1, o.N, o.K, o.gshift, y, XT,
+                                               residual, nullptr, 0.f, lds, max_polls);
+  } else {
+    gemv_ct_body<XT, ST, L, false, true>(b - nq, 0, att, 0, o.packed, 0, o.scale, 0, o.zeros, 0,
+                                         nullptr, 1, o.N, o.K, o.gshift, y, XT, residual, nullptr,
+                                         0.f, lds, max_polls);
+  }
 }
 
 namespace {
@@ -356,28 +401,42 @@ size_t attn_o_ws(int nq, int max_len) {
   return ((attn_ws(nq, max_len) + 255) & ~(size_t)255) + (size_t)nq * HD * 2;
 }
 
-// o_proj behind the attention (k_attn_o), or none (o == nullptr: k_attn_combine)
+// o_proj behind the attention (k_attn_o), or none (o == nullptr: k_attn_combine);
+// route: the MoE router behind o_proj (y then directly follows the attention output,
+// and w.N is the hidden size, 1024 or 2048)
 struct OLaunch {
   OProj w;
   int st;  // scale dtype
   const void* residual;
   void* y;
+  const RFold* route = nullptr;
 };
 
 template <int XT, int ST>
 int launch_attn_o(const float* part, int nq, const int32_t* pos_dev, int pos, int max_len,
                   uint16_t* att, const OLaunch& o, hipStream_t s) {
   const int C = o.w.K / 32, L = gemv_lanes_per_row(C), rpw = 256 / L;
-  const dim3 grid(nq + (o.w.N + rpw - 1) / rpw);
-  const size_t lds = (size_t)o.w.K * 2 + (size_t)C * 8;
-#define I4_AO_CASE(L_)                                                                          \
-  if (L == L_) {                                                                                \
-    hipLaunchKernelGGL((k_attn_o<XT, ST, L_>), grid, dim3(256), lds, s, part, nq, pos_dev, pos, \
-                       max_len, att, o.w, (const uint16_t*)o.residual, (uint16_t*)o.y,          \
-                       kHandoffPolls);                                                          \
-    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                             \
+  const int n_o = (o.w.N + rpw - 1) / rpw;
+  RFold r{};
+  int rh = 0, n_r = 0;
+  if (o.route) {
+    r = *o.route;
+    r.n_o = n_o;
+    rh = o.w.N;
+    n_r = (r.E + 3) / 4;
   }
-  I4_AO_CASE(8) I4_AO_CASE(16) I4_AO_CASE(32) I4_AO_CASE(64)
+  const dim3 grid(nq + n_o + n_r);
+  const size_t lds = (size_t)o.w.K * 2 + (size_t)C * 8;
+#define I4_AO_CASE(L_, RH_)                                                                   \
+  if (L == L_ && rh == RH_) {                                                                 \
+    hipLaunchKernelGGL((k_attn_o<XT, ST, L_, RH_>), grid, dim3(256), lds, s, part, nq,        \
+                       pos_dev, pos, max_len, att, o.w, (const uint16_t*)o.residual,          \
+                       (uint16_t*)o.y, kHandoffPolls, r);                                     \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                           \
+  }
+  I4_AO_CASE(8, 0) I4_AO_CASE(16, 0) I4_AO_CASE(32, 0) I4_AO_CASE(64, 0)
+  I4_AO_CASE(8, 1024) I4_AO_CASE(16, 1024) I4_AO_CASE(32, 1024) I4_AO_CASE(64, 1024)
+  I4_AO_CASE(8, 2048) I4_AO_CASE(16, 2048) I4_AO_CASE(32, 2048) I4_AO_CASE(64, 2048)
 #undef I4_AO_CASE
   return I4_ERR_SHAPE;
 }
@@ -398,13 +457,17 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   // took 829 instead of 874 us per token at context 1024, four workgroups of 2 849
   const int gsplit = gq == 8 ? 2 : 1;
   const dim3 grid(nch, nkv * gsplit);
+  // with o_proj, the attention output (and, with the router, y right behind it) start
+  // pending
+  const int n_pend = !o ? 0 : (nq * HD + (o->route ? o->w.N : 0)) / 8;
+  int32_t* st_reset = o && o->route ? o->route->status : nullptr;
 #define I4_AC_CASE(G_)                                                                        \
   if (gq / gsplit == G_)                                                                      \
     hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, (const uint16_t*)qkv,  \
                        nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w, eps, pos_dev,   \
                        pos, max_len, rt,                                                      \
                        (uint16_t*)k_cache, (uint16_t*)v_cache, hs, scale, part, gsplit,     \
-                       (u32x4*)(o ? out : nullptr), o ? nq * HD / 8 : 0);                   \
+                       (u32x4*)(o ? out : nullptr), n_pend, st_reset);                      \
   else
   I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) return I4_ERR_SHAPE;
 #undef I4_AC_CASE
@@ -419,6 +482,24 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   hipLaunchKernelGGL(k_attn_combine<XT>, dim3(nq), dim3(HD), 0, s, part, nq, pos_dev, pos,
                      max_len, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// workspace of i4_thinker_layer_decode: i4_moe_forward's T = 1 workspace first (so its
+// status word sits at i4_moe_status_offset(1, H, I, E, topk)), then the attention's
+// (chunk partials, attention output) with the o_proj output h2 right behind it, then
+// the q|k|v projection
+struct LayerWs {
+  size_t part, h2, qkv, bytes;
+};
+LayerWs layer_ws(int nq, int nkv, int max_len, int H, int I, int E, int topk) {
+  LayerWs l;
+  l.part = al256(i4_moe_workspace_bytes(1, H, I, E, topk));
+  l.h2 = l.part + attn_o_ws(nq, max_len);
+  l.qkv = al256(l.h2 + (size_t)H * 2);
+  l.bytes = l.qkv + al256((size_t)(nq + 2 * nkv) * HD * 2);
+  return l;
 }
 
 }  // namespace
@@ -436,12 +517,11 @@ size_t i4_attn_decode_o_workspace_bytes(int n_heads, int head_dim, int max_len) 
   return i4::attn_o_ws(n_heads, max_len);
 }
 
-static int attn_entry(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
-                      const void* q_norm_w, const void* k_norm_w, float eps,
-                      const float* inv_freq, const int32_t* pos_dev, int pos, void* k_cache,
-                      void* v_cache, int max_len, void* out, void* workspace,
-                      size_t workspace_bytes, hipStream_t stream,
-                      const i4::OLaunch* o = nullptr) {
+// the attention entries' checks, made before any launch
+static int attn_check(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
+                      const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                      const int32_t* pos_dev, int pos, void* k_cache, void* v_cache,
+                      int max_len, void* out) {
   if (!qkv || !q_norm_w || !k_norm_w || !inv_freq || !k_cache || !v_cache || !out)
     return I4_ERR_NULL;
   if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
@@ -453,6 +533,18 @@ static int attn_entry(const void* qkv, int x_dtype, int n_heads, int n_kv_heads,
       ((uintptr_t)k_cache & 15) || ((uintptr_t)v_cache & 15) || ((uintptr_t)out & 3) ||
       ((uintptr_t)pos_dev & 3))
     return I4_ERR_ALIGN;
+  return I4_OK;
+}
+
+static int attn_entry(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, int head_dim,
+                      const void* q_norm_w, const void* k_norm_w, float eps,
+                      const float* inv_freq, const int32_t* pos_dev, int pos, void* k_cache,
+                      void* v_cache, int max_len, void* out, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream,
+                      const i4::OLaunch* o = nullptr) {
+  const int rc = attn_check(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w,
+                            inv_freq, pos_dev, pos, k_cache, v_cache, max_len, out);
+  if (rc) return rc;
   const size_t need = o ? i4::attn_o_ws(n_heads, max_len) : i4::attn_ws(n_heads, max_len);
   if (!workspace || workspace_bytes < need) return I4_ERR_WORKSPACE;
   if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
@@ -511,6 +603,71 @@ int i4_attn_decode_o(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, 
   return attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
                     inv_freq, pos_dev, pos, k_cache, v_cache, max_len, y, workspace,
                     workspace_bytes, stream, &o);
+}
+
+size_t i4_thinker_layer_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len,
+                                        int H, int I, int E, int topk) {
+  if (n_heads < 1 || n_kv_heads < 1 || head_dim != i4::HD || max_len < 1) return 0;
+  // 0 also for an MoE shape outside the single-launch expert kernel
+  if ((H != 1024 && H != 2048) || !i4::moe_m1_ct_fits(topk, H, I)) return 0;
+  if (i4_moe_workspace_bytes(1, H, I, E, topk) == 0) return 0;
+  return i4::layer_ws(n_heads, n_kv_heads, max_len, H, I, E, topk).bytes;
+}
+
+int i4_thinker_layer_decode(const void* h, int x_dtype, const void* in_norm_w, float eps,
+                            const i4_qweight* qkv_w, int n_heads, int n_kv_heads, int head_dim,
+                            const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                            const int32_t* pos_dev, int pos, void* k_cache, void* v_cache,
+                            int max_len, const i4_qweight* o_w, const i4_moe_weights* moe,
+                            int topk, int renorm, void* out, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+  if (!h || !in_norm_w || !qkv_w || !o_w || !moe || !out) return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  i4_qweight qw, ow;
+  int rc = i4_check_weight(qkv_w, &qw);
+  if (rc) return rc;
+  rc = i4_check_weight(o_w, &ow);
+  if (rc) return rc;
+  if (qw.layout != I4_LAYOUT_CT || ow.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (!workspace) return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  // the MoE block: CT experts of the single-launch kernel, router and norm present
+  i4::MoeDecodeBufs mb;
+  rc = i4::moe_decode_bufs(moe, x_dtype, topk, workspace, workspace_bytes, &mb);
+  if (rc) return rc;
+  const int H = mb.H;
+  if (n_heads < 1 || n_kv_heads < 1 || head_dim != i4::HD) return I4_ERR_SHAPE;
+  if (qw.E != 1 || qw.K != H || qw.N != (n_heads + 2 * n_kv_heads) * i4::HD) return I4_ERR_SHAPE;
+  // o_proj: one staging round of the poll (K <= 8192), N = H
+  if (ow.E != 1 || ow.N != H || ow.K != n_heads * i4::HD || ow.K < 256 || ow.K > 8192)
+    return I4_ERR_SHAPE;
+  if (((uintptr_t)h & 15) || ((uintptr_t)out & 15)) return I4_ERR_ALIGN;
+  if (!q_norm_w || !k_norm_w || !inv_freq || !k_cache || !v_cache) return I4_ERR_NULL;
+  const i4::LayerWs l = i4::layer_ws(n_heads, n_kv_heads, max_len, H, mb.I, mb.E, topk);
+  if (workspace_bytes < l.bytes) return I4_ERR_WORKSPACE;
+  char* ws = (char*)workspace;
+  void* qkv = ws + l.qkv;
+  void* h2 = ws + l.h2;
+  // every check of the three launches before the first of them
+  rc = attn_check(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, inv_freq,
+                  pos_dev, pos, k_cache, v_cache, max_len, h2);
+  if (rc) return rc;
+  if (((uintptr_t)in_norm_w & 15)) return I4_ERR_ALIGN;
+  rc = i4_rmsnorm_linear(h, x_dtype, 1, in_norm_w, eps, &qw, nullptr, qkv, x_dtype, stream);
+  if (rc) return rc;
+  const i4::RFold r{(const uint16_t*)moe->router_w, (const uint16_t*)moe->norm_w, moe->norm_eps,
+                    mb.xn, mb.logits, mb.act, mb.n_act, mb.status, mb.E, 0};
+  i4::OLaunch o;
+  o.w = i4::OProj{ow.packed, ow.scale, ow.zeros, ow.N, ow.K, i4_group_shift(ow.group)};
+  o.st = ow.scale_dtype;
+  o.residual = h;
+  o.y = h2;
+  o.route = &r;
+  rc = attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps, inv_freq,
+                  pos_dev, pos, k_cache, v_cache, max_len, h2, ws + l.part, l.h2 - l.part, stream,
+                  &o);
+  if (rc) return rc;
+  return i4::moe_decode_experts(mb, x_dtype, topk, renorm, h2, out, workspace, stream);
 }
 
 }  // extern "C"

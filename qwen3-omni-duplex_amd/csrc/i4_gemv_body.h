@@ -24,8 +24,12 @@ static constexpr int GEMV_ROUND = 4;  // chunks per lane whose loads are in flig
 // launch and holds the pending pattern until then; the workgroup issues its
 // first round of weight loads, then polls x (poll_rows) instead of loading it.
 // Rows of a workgroup whose wait gives up come out NaN.
-template <int XT, int ST, int L, bool NORM, bool POLL>
-__device__ inline void gemv_ct_body(
+// HANDOFF: out (ot = XT) is read by later workgroups of the same launch: the
+// workgroup's rows are gathered in LDS and written through to memory as whole
+// 16-byte stores where they are aligned (else value by value), NaN in canonical form (so the pending
+// pattern never appears in finished values).  Same arithmetic as the plain store.
+template <int XT, int ST, int L, bool NORM, bool POLL, bool HANDOFF = false>
+__device__ __forceinline__ void gemv_ct_body(
     int bx, int j, const uint16_t* __restrict__ x, int64_t x_stride,
     const int32_t* __restrict__ packed, int64_t p_es, const void* __restrict__ scale,
     int64_t s_es, const int32_t* __restrict__ zeros, int64_t z_es,
@@ -109,6 +113,28 @@ __device__ inline void gemv_ct_body(
     }
   }
   row = group_sum<L>(row);
+  if constexpr (HANDOFF) {
+    __shared__ __align__(16) uint16_t s_y[RPW];
+    if (rv && cl == 0) {
+      if (late) row = __builtin_nanf("");
+      if (bias) row += Half<XT>::to_f32(((const uint16_t*)bias)[n]);
+      const uint16_t b = Half<XT>::from_f32(row);
+      s_y[rl] = row != row ? Half<XT>::QNAN : b;
+    }
+    __syncthreads();
+    const int n0 = bx * RPW, nv = min(RPW, N - n0);
+    uint16_t* dst = (uint16_t*)out + (int64_t)j * N + n0;
+    if (RPW % 8 == 0 && nv == RPW && ((uintptr_t)dst & 15) == 0) {
+      if ((int)threadIdx.x < RPW / 8) {
+        const rsrc_t r = rsrc(dst, (u32)RPW * 2u);
+        __builtin_amdgcn_raw_buffer_store_b128(((const u32x4*)s_y)[threadIdx.x], r,
+                                               (u32)threadIdx.x * 16u, 0, kCoherent);
+      }
+    } else if ((int)threadIdx.x < nv) {
+      st_coherent(dst + threadIdx.x, s_y[threadIdx.x]);
+    }
+    return;
+  }
   if (rv && cl == 0) {
     if (late) row = __builtin_nanf("");
     const int64_t o = (int64_t)j * N + n;

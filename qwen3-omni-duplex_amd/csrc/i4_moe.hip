@@ -502,6 +502,51 @@ int moe_forward_impl(const void* x, int x_dtype, int T, const i4_moe_weights* we
 
 }  // namespace
 
+namespace i4 {
+
+int moe_decode_bufs(const i4_moe_weights* mw, int x_dtype, int topk, void* ws, size_t ws_bytes,
+                    MoeDecodeBufs* b) {
+  i4_qweight gu, dn, tg, td;
+  int rc = check_moe(mw, x_dtype, 1, topk, &gu, &dn, &tg, &td);
+  if (rc) return rc;
+  if (!mw->router_w || !mw->norm_w) return I4_ERR_NULL;
+  if (gu.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  const int H = gu.K, I = dn.K, E = gu.E;
+  if ((H != 1024 && H != 2048) || !moe_m1_ct_fits(topk, H, I)) return I4_ERR_SHAPE;
+  if (((uintptr_t)mw->router_w & 15) || ((uintptr_t)mw->norm_w & 15)) return I4_ERR_ALIGN;
+  if (!ws || ws_bytes < carve(nullptr, 1, H, I, E, topk).bytes) return I4_ERR_WORKSPACE;
+  if ((uintptr_t)ws & 255) return I4_ERR_ALIGN;
+  MoeOps ops;
+  if (!pick_ops(x_dtype, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
+  const MoeWs w = carve(ws, 1, H, I, E, topk);
+  b->logits = (uint16_t*)w.logits;
+  b->xn = w.xn;
+  b->act = (u32x4*)w.act;
+  b->n_act = topk * I / 8;
+  b->status = w.status;
+  b->H = H;
+  b->I = I;
+  b->E = E;
+  b->gate_up = gu;
+  b->down = dn;
+  return I4_OK;
+}
+
+int moe_decode_experts(const MoeDecodeBufs& b, int x_dtype, int topk, int renorm,
+                       const void* residual, void* out, void* ws, hipStream_t s) {
+  const i4_qweight& gu = b.gate_up;
+  const i4_qweight& dn = b.down;
+  const MoeWs w = carve(ws, 1, gu.K, dn.K, gu.E, topk);
+  MoeOps ops;
+  if (!pick_ops(x_dtype, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
+  // the status word was reset before the router launch, which may have reported in it
+  const GateUpArgs a{true, topk, topk, gu.E, renorm, w.xn, w.sel, w.logits, w.w, w.act, nullptr};
+  const TW tg = to_tw(gu);
+  return ops.moe_m1_ct(a, &tg, to_tw(dn), residual, out, w.status, kHandoffPolls, s);
+}
+
+}  // namespace i4
+
 extern "C" {
 
 size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk) {

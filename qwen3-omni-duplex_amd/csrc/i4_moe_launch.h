@@ -56,6 +56,27 @@ int launch_moe_m1_ct(const GateUpArgs& a, const TW* gate_up, const TW& down,
                      const void* residual, void* out, int32_t* status, int max_polls,
                      hipStream_t s);
 
+// The T = 1 MoE block of a decoder layer whose router runs in an earlier launch
+// (i4_thinker_layer_decode, i4_attn.hip): that launch writes the logits and the
+// normalised row, arms act with the pending pattern and reports a wait that gave
+// up in status; the buffers are those of i4_moe_forward's T = 1 workspace at ws.
+struct MoeDecodeBufs {
+  uint16_t* logits;  // [E] router logits, the activation dtype
+  uint16_t* xn;      // [H] RMSNorm(x) with the block's norm weight
+  u32x4* act;        // [topk * I] activations, n_act 16-byte words
+  int n_act;
+  int32_t* status;
+  int H, I, E;
+  i4_qweight gate_up, down;  // validated (i4_check_weight) CT weights
+};
+// Validates the block for that use (CT rows, router and norm present, a shape of
+// the single-launch expert kernel, H the router wave's 1024 or 2048).
+int moe_decode_bufs(const i4_moe_weights* mw, int x_dtype, int topk, void* ws, size_t ws_bytes,
+                    MoeDecodeBufs* b);
+// The experts launch of that block: out = residual + MoE(xn) from the logits.
+int moe_decode_experts(const MoeDecodeBufs& b, int x_dtype, int topk, int renorm,
+                       const void* residual, void* out, void* ws, hipStream_t s);
+
 // Grouped (T > 1) expert projections on MFMA.  entries[i] = {expert, first
 // position, tokens, 0} of the expert-sorted (token, slot) list perm; small
 // entries have <= MF_SMALL tokens, large ones <= MF_TOK.

@@ -8,6 +8,7 @@
 // ranking the probabilities.  Exact ties are broken by the lower expert id
 // (torch.topk leaves that order unspecified).
 #include "i4_common.h"
+#include "i4_router_body.h"
 #include "i4_launch.h"
 #include "i4_topk.h"
 
@@ -106,43 +107,10 @@ __global__ __launch_bounds__(64) void k_router_m1w(
     const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
     uint16_t* __restrict__ logits, u32x4* __restrict__ pend, int n_pend,
     int32_t* __restrict__ status) {
-  static_assert(H == 1024 || H == 2048, "one 512-value round per 64 lanes, 2 or 4 rounds");
-  constexpr int NR = H / 512;  // lane l owns words l + 64 i, i < NR
   for (int i = blockIdx.x * 64 + (int)threadIdx.x; i < n_pend; i += gridDim.x * 64)
     pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
   if (status && blockIdx.x == 0 && threadIdx.x == 0) *status = I4_OK;
-  const int lane = threadIdx.x, e = blockIdx.x;
-  u32x4 xv[NR], gv[NR], wv[NR];
-#pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    xv[i] = ldg16(x + 8 * (lane + 64 * i));
-    if constexpr (NORM) gv[i] = ldg16(nw + 8 * (lane + 64 * i));
-    wv[i] = ldg16(wr + (int64_t)e * H + 8 * lane + 512 * i);
-  }
-  if constexpr (NORM) {
-    float ws[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < NR; ++i) ws[i] = group_sum<64>(sumsq8<XT>(xv[i]));  // wave i's sum
-    const float r = 1.0f / sqrtf(((ws[0] + ws[1]) + (ws[2] + ws[3])) / (float)H + eps);
-#pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      xv[i].x = norm_pair<XT>(xv[i].x, gv[i].x, r);
-      xv[i].y = norm_pair<XT>(xv[i].y, gv[i].y, r);
-      xv[i].z = norm_pair<XT>(xv[i].z, gv[i].z, r);
-      xv[i].w = norm_pair<XT>(xv[i].w, gv[i].w, r);
-      if (xn_out && e == 0) *(u32x4*)(xn_out + 8 * (lane + 64 * i)) = xv[i];
-    }
-  }
-  float a = 0.f;
-#pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    a = Half<XT>::dot2(wv[i].x, xv[i].x, a);
-    a = Half<XT>::dot2(wv[i].y, xv[i].y, a);
-    a = Half<XT>::dot2(wv[i].z, xv[i].z, a);
-    a = Half<XT>::dot2(wv[i].w, xv[i].w, a);
-  }
-  a = group_sum<64>(a);
-  if (lane == 0) logits[e] = Half<XT>::from_f32(a);
+  router_wave<XT, NORM, H, false>(x, wr, blockIdx.x, nw, eps, xn_out, logits);
 }
 
 // T > 1, pass 1: RMSNorm of one token per workgroup with exactly the

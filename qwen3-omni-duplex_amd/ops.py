@@ -529,6 +529,68 @@ def attn_decode_o(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: to
     return y
 
 
+def thinker_layer_fits(n_heads: int, n_kv_heads: int, head_dim: int, max_len: int, H: int,
+                      I: int, E: int, top_k: int) -> bool:
+    """Whether i4_thinker_layer_decode takes a layer of these sizes."""
+    return _lib.lib().i4_thinker_layer_workspace_bytes(n_heads, n_kv_heads, head_dim, max_len,
+                                                       H, I, E, top_k) > 0
+
+
+def thinker_layer_decode(h: torch.Tensor, in_norm_w: torch.Tensor, eps: float, qkv_w: QWeight,
+                         n_heads: int, n_kv_heads: int, q_norm_w: torch.Tensor,
+                         k_norm_w: torch.Tensor, inv_freq: torch.Tensor, pos: int | torch.Tensor,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor, o_w: QWeight,
+                         gate_up: QWeight, down: QWeight, top_k: int, router_w: torch.Tensor,
+                         norm_w: torch.Tensor, norm_eps: float, norm_topk_prob: bool = True,
+                         workspace: Workspace | None = None) -> torch.Tensor:
+    """One decode token through a Thinker decoder layer (i4_thinker_layer_decode):
+    h2 = h + o_proj(attention(RMSNorm(h))), then h2 + MoE(RMSNorm(h2)), in four launches
+    (the MoE router runs in the o_proj launch, behind the workgroups producing h2).
+    Equal bit for bit to rmsnorm_linear + attn_decode_o + moe_forward(residual=h2).
+    qkv_w, o_w and the experts are CT weights; h is [..., H] holding one token."""
+    dev = _lib.require_device(h, in_norm_w, q_norm_w, k_norm_w, k_cache, v_cache, o_w.packed,
+                              gate_up.packed, down.packed, router_w, norm_w)
+    if h.numel() != h.shape[-1]:
+        raise RuntimeError("thinker_layer_decode takes one token")
+    pos_dev = None
+    if isinstance(pos, torch.Tensor):
+        if pos.device != dev or pos.dtype != torch.int32 or pos.numel() != 1:
+            raise RuntimeError("a device position is one int32 on the tensors' device")
+        pos_dev = pos
+    xt = _lib.half_code(h.dtype)
+    H = h.shape[-1]
+    E, I = gate_up.E, down.K
+    _check_block_dtypes(h.dtype, H, E, router_w, norm_w)
+    for t, name in ((in_norm_w, "input norm"), (q_norm_w, "q norm"), (k_norm_w, "k norm")):
+        if t.dtype != h.dtype:
+            raise RuntimeError(f"the {name} weight must have the activation dtype")
+    nkv, max_len, hd = k_cache.shape
+    if k_cache.dtype != h.dtype or v_cache.shape != k_cache.shape or v_cache.dtype != h.dtype:
+        raise RuntimeError("the caches must be [n_kv_heads, max_len, head_dim] in the activation dtype")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or nkv != n_kv_heads:
+        raise RuntimeError("the caches must be contiguous [n_kv_heads, max_len, head_dim]")
+    tab = inv_freq.detach().to("cpu", torch.float32).contiguous()
+    if tab.numel() != hd // 2:
+        raise RuntimeError("inv_freq must hold head_dim / 2 values")
+    hf = h.reshape(-1).contiguous()
+    out = torch.empty_like(hf)
+    lb = _lib.lib()
+    nbytes = lb.i4_thinker_layer_workspace_bytes(n_heads, n_kv_heads, hd, max_len, H, I, E, top_k)
+    if nbytes == 0:
+        raise RuntimeError("unsupported Thinker layer shape")
+    ws = (workspace or Workspace()).get(nbytes, dev)
+    qw, ow = qkv_w.c(), o_w.c()
+    mw = moe_weights_c(gate_up, down, router_w, norm_w, norm_eps)
+    _lib.check(lb.i4_thinker_layer_decode(
+        hf.data_ptr(), xt, in_norm_w.contiguous().data_ptr(), float(eps), ctypes.byref(qw),
+        n_heads, n_kv_heads, hd, q_norm_w.contiguous().data_ptr(),
+        k_norm_w.contiguous().data_ptr(), tab.data_ptr(),
+        None if pos_dev is None else pos_dev.data_ptr(), 0 if pos_dev is not None else int(pos),
+        k_cache.data_ptr(), v_cache.data_ptr(), max_len, ctypes.byref(ow), ctypes.byref(mw),
+        top_k, int(norm_topk_prob), out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(dev)))
+    return out.view(h.shape)
+
+
 def rmsnorm_linear(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: QWeight,
                    bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None):
     """y = RMSNorm(x) W^T (+ bias) in one launch (i4_rmsnorm_linear; CT weight, K <= 4096),

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported_and_bound(pkg):
 
 def test_version_and_errors(pkg):
     lib = pkg.lib()
-    assert lib.i4_abi_version() == 6
+    assert lib.i4_abi_version() == 7
     codes = {0: b"ok", -1: b"NULL", -2: b"dimension", -3: b"element type", -4: b"aligned",
              -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride",
              -10: b"gave up waiting", -11: b"static buffer"}
@@ -246,6 +246,59 @@ def test_decode_attention_validation_codes(pkg):
     assert callo(res=0x80001) == -4
     assert callo(wsb=ws) == -7          # the partials alone do not hold the merged heads
     assert callo(pd=0x70002) == -4
+
+
+def test_thinker_layer_validation_codes(pkg):
+    """i4_thinker_layer_decode rejects bad calls before its first launch (Thinker sizes:
+    32 / 4 heads, hidden 2048, 128 experts of FFN 768, top-8), and its workspace query
+    returns 0 for sizes the entry does not take."""
+    from qwen3_omni_duplex_amd import _lib
+
+    lib = pkg.lib()
+    tab = (ctypes.c_float * 64)()
+    wsb = lib.i4_thinker_layer_workspace_bytes(32, 4, 128, 4096, 2048, 768, 128, 8)
+    # MoE workspace, attention workspace + h2, q|k|v, each from a 256-byte boundary
+    parts = (lib.i4_moe_workspace_bytes(1, 2048, 768, 128, 8),
+             lib.i4_attn_decode_o_workspace_bytes(32, 128, 4096) + 2048 * 2, 40 * 128 * 2)
+    assert wsb == sum((b + 255) & ~255 for b in parts)
+    fits = lambda **kw: lib.i4_thinker_layer_workspace_bytes(
+        32, 4, kw.get("hd", 128), 4096, kw.get("H", 2048), kw.get("I", 768), 128, kw.get("k", 8))
+    assert fits(H=1024) > 0
+    assert fits(H=3072) == 0            # the router wave covers H 1024 and 2048
+    assert fits(hd=64) == 0
+    assert fits(k=9) == 0               # past the single-launch expert kernel
+    assert fits(I=4096) == 0
+    qw = _qw(_lib, E=1, N=5120, K=2048)
+    ow = _qw(_lib, E=1, N=2048, K=4096)
+    gu = _qw(_lib, E=128, N=1536, K=2048, group=128)
+    dn = _qw(_lib, E=128, N=2048, K=768, group=128)
+    mw = _lib.MoeWeightsC(gate_up=gu, down=dn, router_w=0x60000, norm_w=0x61000, norm_eps=1e-6)
+    call = lambda **kw: lib.i4_thinker_layer_decode(
+        kw.get("h", 0x30000), kw.get("xt", 1), 0x40000, 1e-6, ctypes.byref(kw.get("qw", qw)),
+        kw.get("nh", 32), 4, 128, 0x50000, 0x51000, tab, kw.get("pd", None), kw.get("pos", 5),
+        0x100000, 0x200000, 4096, ctypes.byref(kw.get("ow", ow)), ctypes.byref(kw.get("mw", mw)),
+        kw.get("k", 8), 1, kw.get("out", 0x70000), kw.get("ws", 0x1000000), kw.get("wsb", wsb),
+        None)
+    assert call(h=None) == -1
+    assert call(out=None) == -1
+    assert call(xt=0) == -3
+    assert call(ow=_qw(_lib, E=1, N=2048, K=4096, group=128, layout=1)) == -5
+    assert call(mw=_lib.MoeWeightsC(gate_up=gu, down=dn, router_w=None, norm_w=0x61000)) == -1
+    assert call(mw=_lib.MoeWeightsC(gate_up=gu, down=dn, router_w=0x60000, norm_w=None)) == -1
+    tile = _lib.MoeWeightsC(gate_up=_qw(_lib, E=128, N=1536, K=2048, group=128, layout=2),
+                            down=_qw(_lib, E=128, N=2048, K=768, group=128, layout=2),
+                            router_w=0x60000, norm_w=0x61000)
+    assert call(mw=tile) == -5
+    assert call(k=9) == -2
+    assert call(qw=_qw(_lib, E=1, N=5000, K=2048)) == -2    # rows of 32 + 2 x 4 heads
+    assert call(ow=_qw(_lib, E=1, N=1024, K=4096)) == -2    # o_proj rows = H
+    assert call(nh=16) == -2
+    assert call(out=0x70008) == -4
+    assert call(wsb=wsb - 1) == -7
+    assert call(ws=None) == -7
+    assert call(ws=0x1000010) == -4
+    assert call(pos=4096) == -2         # the attention's checks come before any launch
+    assert call(pd=0x70002) == -4
 
 
 def test_dense_moe_validation_codes(pkg):

@@ -172,6 +172,7 @@ def test_thinker_decoder_step_composes(pkg, dev, ckpt):
     ld = _ld(pkg)
     dec = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=64)
     twin = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=64)
+    assert all(layer.fused() for layer in dec.layers)  # step runs i4_thinker_layer_decode
     rng = np.random.default_rng(96)
     for pos in range(4):
         x = t_(make_x(rng, (1, H), "bf16"), dev)
@@ -298,6 +299,80 @@ def test_attn_decode_o_equals_attention_then_o_proj(pkg, dev, xdt, nh, nkv, pos,
     torch.cuda.synchronize()
     assert torch.isnan(got.float()).all()
     assert torch.equal(kc3, cache[0])
+
+
+def _synthetic_layer(pkg, dev, tdt, H, E, I, top_k, nh, nkv, max_len, renorm, seed):
+    """A Thinker decoder layer of random CT int4 weights (g32, scales in the activation
+    dtype), router ~ N(0, 0.05), norm weights in [0.8, 1.2), cache rows random."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+
+    def ct(e, N, K):
+        p = torch.randint(-2**31, 2**31, (e, N, K // 8), dtype=torch.int32, device=dev,
+                          generator=gen)
+        sc = (torch.rand(e, N, K // 32, device=dev, generator=gen) * 0.018 + 0.002).to(tdt)
+        return pkg.QWeight(p, sc, None, "ct", 32, N, K)
+
+    def vec(n):
+        return (torch.rand(n, device=dev, generator=gen) * 0.4 + 0.8).to(tdt)
+
+    hd = 128
+    qkv = pkg.PackedQKV.from_qweights(ct(1, nh * hd, H), ct(1, nkv * hd, H), ct(1, nkv * hd, H))
+    o = pkg.PackedLinear.from_qweight(ct(1, H, nh * hd))
+    attn = pkg.ThinkerAttention(qkv, o, vec(hd), vec(hd), vec(H), nh, nkv, hd, max_len=max_len)
+    attn.k_cache.copy_(torch.randn(nkv, max_len, hd, device=dev, generator=gen).to(tdt))
+    attn.v_cache.copy_(torch.randn(nkv, max_len, hd, device=dev, generator=gen).to(tdt))
+    wr = (torch.randn(E, H, device=dev, generator=gen) * 0.05).to(tdt)
+    moe = pkg.FusedPackedMoE.from_stacked(ct(E, 2 * I, H), ct(E, H, I), wr, top_k,
+                                          norm_topk_prob=renorm, norm_weight=vec(H))
+    return pkg.ThinkerDecoderLayer(attn, moe)
+
+
+@pytest.mark.parametrize("xdt,H,E,I,top_k,nh,nkv,renorm", [
+    ("f16", 2048, 128, 768, 8, 32, 4, True),     # the Thinker's layer
+    ("bf16", 2048, 128, 768, 8, 32, 4, True),
+    ("bf16", 1024, 64, 768, 4, 16, 8, False),
+    ("f16", 1024, 32, 512, 6, 8, 2, True)])
+def test_thinker_layer_decode_equals_attention_then_moe(pkg, dev, xdt, H, E, I, top_k, nh, nkv,
+                                                        renorm):
+    """i4_thinker_layer_decode (the MoE router inside the head merge + o_proj launch, its
+    waves waiting there for the o_proj output) equals the attention block followed by the
+    MoE block (i4_attn_decode_o, then i4_moe_forward with residual h2) bit for bit: output,
+    both caches and a status word left at 0; host and device positions, the last row of a
+    chunk, position 0; a device position past the cache gives NaN and leaves the cache."""
+    tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    max_len = 1024
+    assert pkg.thinker_layer_fits(nh, nkv, 128, max_len, H, I, E, top_k)
+    layer = _synthetic_layer(pkg, dev, tdt, H, E, I, top_k, nh, nkv, max_len, renorm,
+                             seed=500 + H + E + top_k)
+    assert layer.fused()
+    a = layer.attn
+    cache0 = (a.k_cache.clone(), a.v_cache.clone())
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    for pos in (1000, 63, 0, 517):
+        x = torch.randn(1, H, device=dev, generator=gen).to(tdt)
+        for dev_pos in (False, True):
+            a.k_cache.copy_(cache0[0])
+            a.v_cache.copy_(cache0[1])
+            want = layer.unfused(x, pos)
+            kc, vc = a.k_cache.clone(), a.v_cache.clone()
+            a.k_cache.copy_(cache0[0])
+            a.v_cache.copy_(cache0[1])
+            pp = torch.full((1,), pos, dtype=torch.int32, device=dev) if dev_pos else pos
+            got = layer(x, pp)
+            torch.cuda.synchronize()
+            assert torch.isfinite(got.float()).all()
+            assert torch.equal(got, want), (pos, dev_pos)
+            assert torch.equal(a.k_cache, kc) and torch.equal(a.v_cache, vc)
+            assert pkg.moe_status(a.workspace, 1, H, I, E, top_k) == 0
+    a.k_cache.copy_(cache0[0])
+    bad = torch.full((1,), max_len, dtype=torch.int32, device=dev)
+    got = layer(x, bad)
+    torch.cuda.synchronize()
+    assert torch.isnan(got.float()).all()
+    assert torch.equal(a.k_cache, cache0[0])
+    assert pkg.moe_status(a.workspace, 1, H, I, E, top_k) == 0
 
 
 def test_decode_step_graph_with_device_position(pkg, dev, ckpt):
