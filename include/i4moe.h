@@ -399,6 +399,38 @@ int    i4_thinker_layer_decode(const void* h, int x_dtype, const void* in_norm_w
 size_t i4_thinker_layer_workspace_bytes(int n_heads, int n_kv_heads, int head_dim,
                                         int max_len, int H, int I, int E, int topk);
 
+/* One Thinker decoder layer's weights and KV cache, for i4_thinker_decode_step. */
+typedef struct i4_thinker_layer {
+  const void* in_norm_w;   /* [H] input_layernorm weight, x_dtype */
+  const void* q_norm_w;    /* [head_dim] q_norm / k_norm weights, x_dtype */
+  const void* k_norm_w;
+  void*       k_cache;     /* [n_kv_heads][max_len][head_dim], x_dtype */
+  void*       v_cache;
+  float       eps;         /* input, q and k RMSNorm epsilon */
+  i4_qweight  qkv;         /* CT [(n_heads + 2 n_kv_heads) head_dim][H] */
+  i4_qweight  o;           /* CT [H][n_heads head_dim] */
+  i4_moe_weights moe;      /* CT experts; router_w and norm_w (post-attention norm) */
+} i4_thinker_layer;
+
+/* One decode token through n_layers Thinker decoder layers: the clock path's
+ * `th(inputs_embeds=emb, past_key_values=th_kv)` over Thinker[0:n] (src/duplex/
+ * streaming/clock.py:164-172), i.e. i4_thinker_layer_decode per layer, h -> out,
+ * in one call (the hidden state between layers stays in the workspace).  The
+ * result and the caches equal i4_thinker_layer_decode applied layer by layer bit
+ * for bit.  Every layer has the same head counts, H, I, E; the checks of all
+ * layers come before the first launch.
+ * Workspace: i4_thinker_decode_step_workspace_bytes(), no initial contents,
+ * 256-byte aligned; it begins with i4_moe_forward's T = 1 workspace, whose status
+ * word (i4_moe_status_offset(1, H, I, E, topk)) is cleared by the first layer and
+ * then holds I4_ERR_HANDOFF if any wait of the step gave up. */
+int    i4_thinker_decode_step(const void* h, int x_dtype, const i4_thinker_layer* layers,
+                              int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                              const float* inv_freq, const int32_t* pos_dev, int pos,
+                              int max_len, int topk, int renorm, void* out, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+size_t i4_thinker_decode_step_workspace_bytes(int n_heads, int n_kv_heads, int head_dim,
+                                              int max_len, int H, int I, int E, int topk);
+
 /* ------------------------------------------------------------------------
  * MoE block on 16-bit or int8 experts with a sigmoid-gated shared expert: the
  * Talker's block.  Replaces FusedMoE.forward (src/duplex/streaming/fused_moe.py:

@@ -27,7 +27,8 @@ from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_down_wait
                   moe_forward_noalloc, moe_gate_up, moe_route_gate_up, moe_stack, moe_status,
                   route, router_logits, unpack4, unpack_nibbles, Workspace, rmsnorm,
                   rmsnorm_linear, attn_decode, attn_decode_o, thinker_layer_decode,
-                  thinker_layer_fits, dmoe_forward, dmoe_status, dmoe_down_wait)
+                  thinker_layer_fits, thinker_layer_c, thinker_decode_step, dmoe_forward,
+                  dmoe_status, dmoe_down_wait)
 from .weights import QWeight, repack_awq_to_ct, repack_tile
 
 lib = _lib.lib
@@ -41,7 +42,8 @@ __all__ = [
     "concat_rows", "patch_attention", "TILE_ROWS", "lib",
     "Checkpoint", "read_moe_layer", "load_moe_layer", "load_thinker_moe_stack", "load_attention",
     "load_thinker_layer", "load_thinker_decoder", "rmsnorm", "rmsnorm_linear", "attn_decode",
-    "attn_decode_o", "thinker_layer_decode", "thinker_layer_fits",
+    "attn_decode_o", "thinker_layer_decode", "thinker_layer_fits", "thinker_layer_c",
+    "thinker_decode_step",
     "ThinkerAttention", "ThinkerDecoderLayer", "ThinkerDecoder", "rope_inv_freq",
     "FusedMoE", "fuse_moe_blocks", "quantize_q8", "dmoe_forward", "dmoe_status",
     "dmoe_down_wait",

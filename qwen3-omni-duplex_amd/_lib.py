@@ -66,6 +66,14 @@ class DmoeWeightsC(ctypes.Structure):
                 ("shared_gate_w", c_void_p)]
 
 
+class ThinkerLayerC(ctypes.Structure):
+    """struct i4_thinker_layer"""
+
+    _fields_ = [("in_norm_w", c_void_p), ("q_norm_w", c_void_p), ("k_norm_w", c_void_p),
+                ("k_cache", c_void_p), ("v_cache", c_void_p), ("eps", ctypes.c_float),
+                ("qkv", QWeightC), ("o", QWeightC), ("moe", MoeWeightsC)]
+
+
 # name -> (restype, argtypes); every function declared in include/i4moe.h
 SIGNATURES = {
     "i4_abi_version": (c_int, []),
@@ -128,6 +136,11 @@ SIGNATURES = {
                                         c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "i4_thinker_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int,
                                                     c_int, c_int]),
+    "i4_thinker_decode_step": (c_int, [c_void_p, c_int, POINTER(ThinkerLayerC), c_int, c_int,
+                                       c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_int,
+                                       c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "i4_thinker_decode_step_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int,
+                                                          c_int, c_int, c_int]),
     "i4_dmoe_forward": (c_int, [c_void_p, c_int, c_int, POINTER(DmoeWeightsC), c_int, c_int,
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_size_t, c_void_p]),

@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from . import ops
+from . import _lib, ops
 from .linear import PackedLinear, PackedQKV
 from .moe import FusedPackedMoE
 
@@ -127,8 +127,47 @@ class ThinkerDecoder(nn.Module):
     def __init__(self, layers: list[ThinkerDecoderLayer]):
         super().__init__()
         self.layers = nn.ModuleList(layers)
+        self.workspace = ops.Workspace()
+        self._fused: bool | None = None
+        self._layers_c = None
+
+    def _apply(self, fn, *args, **kwargs):
+        # moved tensors: the layer structs hold their old addresses
+        self._fused, self._layers_c = None, None
+        return super()._apply(fn, *args, **kwargs)
+
+    def fused(self) -> bool:
+        """Whether step runs as one i4_thinker_decode_step call: every layer takes
+        i4_thinker_layer_decode and all share their sizes, dtype and routing."""
+        if self._fused is None:
+            ls = list(self.layers)
+
+            def sizes(l):
+                a, m = l.attn, l.moe
+                return (a.n_heads, a.n_kv_heads, a.head_dim, a.max_len, m.hidden, m.down.K,
+                        m.gate_up.E, m.top_k, m.norm_topk_prob, a.input_norm_w.dtype,
+                        tuple(a.inv_freq.tolist()))
+
+            self._fused = bool(ls) and all(l.fused() for l in ls) and all(
+                sizes(l) == sizes(ls[0]) for l in ls)
+        return self._fused
 
     def step(self, h: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
+        if h.numel() == h.shape[-1] and self.fused():
+            a0, m0 = self.layers[0].attn, self.layers[0].moe
+            if not isinstance(pos, torch.Tensor) and not 0 <= pos < a0.max_len:
+                raise ValueError(f"position {pos} outside the cache (max_len {a0.max_len})")
+            if self._layers_c is None:
+                arr = _lib.ThinkerLayerC * len(self.layers)
+                self._layers_c = arr(*[ops.thinker_layer_c(l.attn, l.moe) for l in self.layers])
+            return ops.thinker_decode_step(
+                h, self._layers_c, len(self.layers), a0.n_heads, a0.n_kv_heads, a0.head_dim,
+                a0.inv_freq, pos, a0.max_len, m0.hidden, m0.down.K, m0.gate_up.E, m0.top_k,
+                m0.norm_topk_prob, self.workspace)
+        return self.unfused(h, pos)
+
+    def unfused(self, h: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
+        """Layer by layer (each its own i4_thinker_layer_decode or module calls)."""
         for layer in self.layers:
             h = layer(h, pos)
         return h

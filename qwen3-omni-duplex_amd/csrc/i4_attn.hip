@@ -410,6 +410,7 @@ struct OLaunch {
   const void* residual;
   void* y;
   const RFold* route = nullptr;
+  bool reset_status = true;  // with route: the chunk launch clears route->status
 };
 
 template <int XT, int ST>
@@ -460,7 +461,7 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   // with o_proj, the attention output (and, with the router, y right behind it) start
   // pending
   const int n_pend = !o ? 0 : (nq * HD + (o->route ? o->w.N : 0)) / 8;
-  int32_t* st_reset = o && o->route ? o->route->status : nullptr;
+  int32_t* st_reset = o && o->route && o->reset_status ? o->route->status : nullptr;
 #define I4_AC_CASE(G_)                                                                        \
   if (gq / gsplit == G_)                                                                      \
     hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, (const uint16_t*)qkv,  \
@@ -484,7 +485,11 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
+}  // namespace
+
 inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+namespace {
 
 // workspace of i4_thinker_layer_decode: i4_moe_forward's T = 1 workspace first (so its
 // status word sits at i4_moe_status_offset(1, H, I, E, topk)), then the attention's
@@ -614,6 +619,82 @@ size_t i4_thinker_layer_workspace_bytes(int n_heads, int n_kv_heads, int head_di
   return i4::layer_ws(n_heads, n_kv_heads, max_len, H, I, E, topk).bytes;
 }
 
+size_t i4_thinker_decode_step_workspace_bytes(int n_heads, int n_kv_heads, int head_dim,
+                                              int max_len, int H, int I, int E, int topk) {
+  const size_t b =
+      i4_thinker_layer_workspace_bytes(n_heads, n_kv_heads, head_dim, max_len, H, I, E, topk);
+  return b ? b + i4::al256((size_t)H * 2) : 0;  // + the hidden state between layers
+}
+
+// One layer's checks (every one made before any launch) and its launches.
+struct LayerOk {
+  i4_qweight qw, ow;
+  i4::MoeDecodeBufs mb;
+  i4::LayerWs l;
+};
+
+static int layer_check(const i4_thinker_layer& L, int x_dtype, int n_heads, int n_kv_heads,
+                       int head_dim, const float* inv_freq, const int32_t* pos_dev, int pos,
+                       int max_len, int topk, void* workspace, size_t workspace_bytes,
+                       size_t extra, LayerOk* c) {
+  if (!L.in_norm_w || !L.q_norm_w || !L.k_norm_w || !L.k_cache || !L.v_cache) return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  int rc = i4_check_weight(&L.qkv, &c->qw);
+  if (rc) return rc;
+  rc = i4_check_weight(&L.o, &c->ow);
+  if (rc) return rc;
+  if (c->qw.layout != I4_LAYOUT_CT || c->ow.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (!workspace) return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  // the MoE block: CT experts of the single-launch kernel, router and norm present
+  rc = i4::moe_decode_bufs(&L.moe, x_dtype, topk, workspace, workspace_bytes, &c->mb);
+  if (rc) return rc;
+  const int H = c->mb.H;
+  if (n_heads < 1 || n_kv_heads < 1 || head_dim != i4::HD) return I4_ERR_SHAPE;
+  const i4_qweight &qw = c->qw, &ow = c->ow;
+  if (qw.E != 1 || qw.K != H || qw.N != (n_heads + 2 * n_kv_heads) * i4::HD) return I4_ERR_SHAPE;
+  // o_proj: one staging round of the poll (K <= 8192), N = H
+  if (ow.E != 1 || ow.N != H || ow.K != n_heads * i4::HD || ow.K < 256 || ow.K > 8192)
+    return I4_ERR_SHAPE;
+  if ((uintptr_t)L.in_norm_w & 15) return I4_ERR_ALIGN;
+  c->l = i4::layer_ws(n_heads, n_kv_heads, max_len, H, c->mb.I, c->mb.E, topk);
+  if (workspace_bytes < c->l.bytes + extra) return I4_ERR_WORKSPACE;
+  char* ws = (char*)workspace;
+  return attn_check(ws + c->l.qkv, x_dtype, n_heads, n_kv_heads, head_dim, L.q_norm_w,
+                    L.k_norm_w, inv_freq, pos_dev, pos, L.k_cache, L.v_cache, max_len,
+                    ws + c->l.h2);
+}
+
+// h -> out through one layer; reset: the chunk launch clears the status word.
+static int layer_launch(const i4_thinker_layer& L, const LayerOk& c, int x_dtype,
+                        int n_heads, int n_kv_heads, const float* inv_freq,
+                        const int32_t* pos_dev, int pos, int max_len, int topk, int renorm,
+                        const void* h, bool reset, void* out, void* workspace,
+                        hipStream_t stream) {
+  char* ws = (char*)workspace;
+  void* qkv = ws + c.l.qkv;
+  void* h2 = ws + c.l.h2;
+  int rc = i4_rmsnorm_linear(h, x_dtype, 1, L.in_norm_w, L.eps, &c.qw, nullptr, qkv, x_dtype,
+                             stream);
+  if (rc) return rc;
+  const i4::RFold r{(const uint16_t*)L.moe.router_w, (const uint16_t*)L.moe.norm_w,
+                    L.moe.norm_eps, c.mb.xn, c.mb.logits, c.mb.act, c.mb.n_act, c.mb.status,
+                    c.mb.E, 0};
+  i4::OLaunch o;
+  const i4_qweight& ow = c.ow;
+  o.w = i4::OProj{ow.packed, ow.scale, ow.zeros, ow.N, ow.K, i4_group_shift(ow.group)};
+  o.st = ow.scale_dtype;
+  o.residual = h;
+  o.y = h2;
+  o.route = &r;
+  o.reset_status = reset;
+  rc = attn_entry(qkv, x_dtype, n_heads, n_kv_heads, i4::HD, L.q_norm_w, L.k_norm_w, L.eps,
+                  inv_freq, pos_dev, pos, L.k_cache, L.v_cache, max_len, h2, ws + c.l.part,
+                  c.l.h2 - c.l.part, stream, &o);
+  if (rc) return rc;
+  return i4::moe_decode_experts(c.mb, x_dtype, topk, renorm, h2, out, workspace, stream);
+}
+
 int i4_thinker_layer_decode(const void* h, int x_dtype, const void* in_norm_w, float eps,
                             const i4_qweight* qkv_w, int n_heads, int n_kv_heads, int head_dim,
                             const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
@@ -622,52 +703,56 @@ int i4_thinker_layer_decode(const void* h, int x_dtype, const void* in_norm_w, f
                             int topk, int renorm, void* out, void* workspace,
                             size_t workspace_bytes, hipStream_t stream) {
   if (!h || !in_norm_w || !qkv_w || !o_w || !moe || !out) return I4_ERR_NULL;
-  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
-  i4_qweight qw, ow;
-  int rc = i4_check_weight(qkv_w, &qw);
-  if (rc) return rc;
-  rc = i4_check_weight(o_w, &ow);
-  if (rc) return rc;
-  if (qw.layout != I4_LAYOUT_CT || ow.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
-  if (!workspace) return I4_ERR_WORKSPACE;
-  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
-  // the MoE block: CT experts of the single-launch kernel, router and norm present
-  i4::MoeDecodeBufs mb;
-  rc = i4::moe_decode_bufs(moe, x_dtype, topk, workspace, workspace_bytes, &mb);
-  if (rc) return rc;
-  const int H = mb.H;
-  if (n_heads < 1 || n_kv_heads < 1 || head_dim != i4::HD) return I4_ERR_SHAPE;
-  if (qw.E != 1 || qw.K != H || qw.N != (n_heads + 2 * n_kv_heads) * i4::HD) return I4_ERR_SHAPE;
-  // o_proj: one staging round of the poll (K <= 8192), N = H
-  if (ow.E != 1 || ow.N != H || ow.K != n_heads * i4::HD || ow.K < 256 || ow.K > 8192)
-    return I4_ERR_SHAPE;
   if (((uintptr_t)h & 15) || ((uintptr_t)out & 15)) return I4_ERR_ALIGN;
-  if (!q_norm_w || !k_norm_w || !inv_freq || !k_cache || !v_cache) return I4_ERR_NULL;
-  const i4::LayerWs l = i4::layer_ws(n_heads, n_kv_heads, max_len, H, mb.I, mb.E, topk);
-  if (workspace_bytes < l.bytes) return I4_ERR_WORKSPACE;
-  char* ws = (char*)workspace;
-  void* qkv = ws + l.qkv;
-  void* h2 = ws + l.h2;
-  // every check of the three launches before the first of them
-  rc = attn_check(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, inv_freq,
-                  pos_dev, pos, k_cache, v_cache, max_len, h2);
+  i4_thinker_layer L;
+  L.in_norm_w = in_norm_w;
+  L.q_norm_w = q_norm_w;
+  L.k_norm_w = k_norm_w;
+  L.k_cache = k_cache;
+  L.v_cache = v_cache;
+  L.eps = eps;
+  L.qkv = *qkv_w;
+  L.o = *o_w;
+  L.moe = *moe;
+  LayerOk c;
+  const int rc = layer_check(L, x_dtype, n_heads, n_kv_heads, head_dim, inv_freq, pos_dev, pos,
+                             max_len, topk, workspace, workspace_bytes, 0, &c);
   if (rc) return rc;
-  if (((uintptr_t)in_norm_w & 15)) return I4_ERR_ALIGN;
-  rc = i4_rmsnorm_linear(h, x_dtype, 1, in_norm_w, eps, &qw, nullptr, qkv, x_dtype, stream);
-  if (rc) return rc;
-  const i4::RFold r{(const uint16_t*)moe->router_w, (const uint16_t*)moe->norm_w, moe->norm_eps,
-                    mb.xn, mb.logits, mb.act, mb.n_act, mb.status, mb.E, 0};
-  i4::OLaunch o;
-  o.w = i4::OProj{ow.packed, ow.scale, ow.zeros, ow.N, ow.K, i4_group_shift(ow.group)};
-  o.st = ow.scale_dtype;
-  o.residual = h;
-  o.y = h2;
-  o.route = &r;
-  rc = attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps, inv_freq,
-                  pos_dev, pos, k_cache, v_cache, max_len, h2, ws + l.part, l.h2 - l.part, stream,
-                  &o);
-  if (rc) return rc;
-  return i4::moe_decode_experts(mb, x_dtype, topk, renorm, h2, out, workspace, stream);
+  return layer_launch(L, c, x_dtype, n_heads, n_kv_heads, inv_freq, pos_dev, pos, max_len, topk,
+                      renorm, h, true, out, workspace, stream);
+}
+
+int i4_thinker_decode_step(const void* h, int x_dtype, const i4_thinker_layer* layers,
+                           int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                           const float* inv_freq, const int32_t* pos_dev, int pos, int max_len,
+                           int topk, int renorm, void* out, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+  if (!h || !layers || !out) return I4_ERR_NULL;
+  if (n_layers < 1 || n_layers > 256) return I4_ERR_SHAPE;
+  if (((uintptr_t)h & 15) || ((uintptr_t)out & 15)) return I4_ERR_ALIGN;
+  LayerOk c[256];
+  for (int l = 0; l < n_layers; ++l) {
+    int rc = layer_check(layers[l], x_dtype, n_heads, n_kv_heads, head_dim, inv_freq, pos_dev,
+                         pos, max_len, topk, workspace, workspace_bytes, 0, &c[l]);
+    if (rc) return rc;
+    // every layer shares one workspace layout
+    if (c[l].mb.H != c[0].mb.H || c[l].mb.I != c[0].mb.I || c[l].mb.E != c[0].mb.E)
+      return I4_ERR_SHAPE;
+  }
+  // the hidden state between layers: one buffer serves them all (a layer reads its input
+  // in its first three launches and writes its output in the fourth)
+  if (workspace_bytes < c[0].l.bytes + i4::al256((size_t)c[0].mb.H * 2)) return I4_ERR_WORKSPACE;
+  void* hbuf = (char*)workspace + c[0].l.bytes;
+  const void* cur = h;
+  for (int l = 0; l < n_layers; ++l) {
+    void* dst = l == n_layers - 1 ? out : hbuf;
+    const int rc = layer_launch(layers[l], c[l], x_dtype, n_heads, n_kv_heads, inv_freq,
+                                pos_dev, pos, max_len, topk, renorm, cur, l == 0, dst,
+                                workspace, stream);
+    if (rc) return rc;
+    cur = dst;
+  }
+  return I4_OK;
 }
 
 }  // extern "C"

@@ -591,6 +591,52 @@ def thinker_layer_decode(h: torch.Tensor, in_norm_w: torch.Tensor, eps: float, q
     return out.view(h.shape)
 
 
+def thinker_layer_c(attn, moe) -> _lib.ThinkerLayerC:
+    """struct i4_thinker_layer of a ThinkerAttention and its FusedPackedMoE (the struct
+    holds raw pointers: the modules' tensors must stay where they are while it is used)."""
+    return _lib.ThinkerLayerC(
+        in_norm_w=attn.input_norm_w.data_ptr(), q_norm_w=attn.q_norm_w.data_ptr(),
+        k_norm_w=attn.k_norm_w.data_ptr(), k_cache=attn.k_cache.data_ptr(),
+        v_cache=attn.v_cache.data_ptr(), eps=float(attn.eps), qkv=attn.qkv.lin.w.c(),
+        o=attn.o_proj.w.c(),
+        moe=moe_weights_c(moe.gate_up, moe.down, moe.router_w, moe.norm_weight, moe.norm_eps))
+
+
+def thinker_decode_step(h: torch.Tensor, layers_c, n_layers: int, n_heads: int, n_kv_heads: int,
+                        head_dim: int, inv_freq: torch.Tensor, pos: int | torch.Tensor,
+                        max_len: int, H: int, I: int, E: int, top_k: int,
+                        norm_topk_prob: bool = True,
+                        workspace: Workspace | None = None) -> torch.Tensor:
+    """One decode token through n_layers Thinker decoder layers (i4_thinker_decode_step,
+    one library call): layers_c is a ctypes array of thinker_layer_c structs.  Equal bit
+    for bit to thinker_layer_decode layer by layer."""
+    dev = _lib.require_device(h)
+    if h.numel() != H:
+        raise RuntimeError(f"thinker_decode_step takes one token of {H} values")
+    pos_dev = None
+    if isinstance(pos, torch.Tensor):
+        if pos.device != dev or pos.dtype != torch.int32 or pos.numel() != 1:
+            raise RuntimeError("a device position is one int32 on the tensors' device")
+        pos_dev = pos
+    tab = inv_freq.detach().to("cpu", torch.float32).contiguous()
+    if tab.numel() != head_dim // 2:
+        raise RuntimeError("inv_freq must hold head_dim / 2 values")
+    hf = h.reshape(-1).contiguous()
+    out = torch.empty_like(hf)
+    lb = _lib.lib()
+    nbytes = lb.i4_thinker_decode_step_workspace_bytes(n_heads, n_kv_heads, head_dim, max_len,
+                                                       H, I, E, top_k)
+    if nbytes == 0:
+        raise RuntimeError("unsupported Thinker layer shape")
+    ws = (workspace or Workspace()).get(nbytes, dev)
+    _lib.check(lb.i4_thinker_decode_step(
+        hf.data_ptr(), _lib.half_code(h.dtype), layers_c, n_layers, n_heads, n_kv_heads,
+        head_dim, tab.data_ptr(), None if pos_dev is None else pos_dev.data_ptr(),
+        0 if pos_dev is not None else int(pos), max_len, top_k, int(norm_topk_prob),
+        out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(dev)))
+    return out.view(h.shape)
+
+
 def rmsnorm_linear(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: QWeight,
                    bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None):
     """y = RMSNorm(x) W^T (+ bias) in one launch (i4_rmsnorm_linear; CT weight, K <= 4096),

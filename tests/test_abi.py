@@ -300,6 +300,37 @@ def test_thinker_layer_validation_codes(pkg):
     assert call(pos=4096) == -2         # the attention's checks come before any launch
     assert call(pd=0x70002) == -4
 
+    # the decode step: the layer's workspace and the hidden state between layers; every
+    # layer is checked before the first launch
+    wss = lib.i4_thinker_decode_step_workspace_bytes(32, 4, 128, 4096, 2048, 768, 128, 8)
+    assert wss == wsb + 4096
+    assert lib.i4_thinker_decode_step_workspace_bytes(32, 4, 128, 4096, 3072, 768, 128, 8) == 0
+
+    def layer(**kw):
+        return _lib.ThinkerLayerC(in_norm_w=kw.get("nw", 0x40000), q_norm_w=0x50000,
+                                  k_norm_w=0x51000, k_cache=kw.get("kc", 0x100000),
+                                  v_cache=0x200000, eps=1e-6, qkv=qw, o=ow,
+                                  moe=kw.get("mw", mw))
+
+    def step(ls, **kw):
+        arr = (_lib.ThinkerLayerC * len(ls))(*ls)
+        return lib.i4_thinker_decode_step(
+            kw.get("h", 0x30000), 1, arr, kw.get("n", len(ls)), 32, 4, 128, tab, None,
+            kw.get("pos", 5), 4096, 8, 1, 0x70000, 0x1000000, kw.get("wsb", wss), None)
+
+    good = layer()
+    assert step([good, good], h=None) == -1
+    assert step([good, good], n=0) == -2
+    assert step([good, good], wsb=wss - 1) == -7
+    assert step([good, good], pos=4096) == -2
+    assert step([good, layer(nw=None)]) == -1           # the last layer's checks too
+    assert step([good, layer(kc=0x100008)]) == -4
+    assert step([good, layer(mw=tile)]) == -5
+    other = _lib.MoeWeightsC(gate_up=_qw(_lib, E=64, N=1536, K=2048, group=128),
+                             down=_qw(_lib, E=64, N=2048, K=768, group=128),
+                             router_w=0x60000, norm_w=0x61000)
+    assert step([good, layer(mw=other)]) == -2           # one workspace layout for all
+
 
 def test_dense_moe_validation_codes(pkg):
     """i4_dmoe_forward rejects bad calls before any launch (Talker shapes: H 1024,

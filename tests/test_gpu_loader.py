@@ -172,7 +172,7 @@ def test_thinker_decoder_step_composes(pkg, dev, ckpt):
     ld = _ld(pkg)
     dec = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=64)
     twin = ld.load_thinker_decoder(root, 2, dev, torch.bfloat16, max_len=64)
-    assert all(layer.fused() for layer in dec.layers)  # step runs i4_thinker_layer_decode
+    assert dec.fused()  # step runs i4_thinker_decode_step
     rng = np.random.default_rng(96)
     for pos in range(4):
         x = t_(make_x(rng, (1, H), "bf16"), dev)
@@ -301,23 +301,27 @@ def test_attn_decode_o_equals_attention_then_o_proj(pkg, dev, xdt, nh, nkv, pos,
     assert torch.equal(kc3, cache[0])
 
 
-def _synthetic_layer(pkg, dev, tdt, H, E, I, top_k, nh, nkv, max_len, renorm, seed):
+def _synthetic_layer(pkg, dev, tdt, H, E, I, top_k, nh, nkv, max_len, renorm, seed,
+                     qkv_scales=None):
     """A Thinker decoder layer of random CT int4 weights (g32, scales in the activation
-    dtype), router ~ N(0, 0.05), norm weights in [0.8, 1.2), cache rows random."""
+    dtype or qkv_scales for q|k|v), router ~ N(0, 0.05), norm weights in [0.8, 1.2), cache
+    rows random."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
 
-    def ct(e, N, K):
+    def ct(e, N, K, sdt=tdt):
         p = torch.randint(-2**31, 2**31, (e, N, K // 8), dtype=torch.int32, device=dev,
                           generator=gen)
-        sc = (torch.rand(e, N, K // 32, device=dev, generator=gen) * 0.018 + 0.002).to(tdt)
+        sc = (torch.rand(e, N, K // 32, device=dev, generator=gen) * 0.018 + 0.002).to(sdt)
         return pkg.QWeight(p, sc, None, "ct", 32, N, K)
 
     def vec(n):
         return (torch.rand(n, device=dev, generator=gen) * 0.4 + 0.8).to(tdt)
 
     hd = 128
-    qkv = pkg.PackedQKV.from_qweights(ct(1, nh * hd, H), ct(1, nkv * hd, H), ct(1, nkv * hd, H))
+    qs = qkv_scales or tdt
+    qkv = pkg.PackedQKV.from_qweights(ct(1, nh * hd, H, qs), ct(1, nkv * hd, H, qs),
+                                      ct(1, nkv * hd, H, qs))
     o = pkg.PackedLinear.from_qweight(ct(1, H, nh * hd))
     attn = pkg.ThinkerAttention(qkv, o, vec(hd), vec(hd), vec(H), nh, nkv, hd, max_len=max_len)
     attn.k_cache.copy_(torch.randn(nkv, max_len, hd, device=dev, generator=gen).to(tdt))
@@ -373,6 +377,47 @@ def test_thinker_layer_decode_equals_attention_then_moe(pkg, dev, xdt, H, E, I, 
     assert torch.isnan(got.float()).all()
     assert torch.equal(a.k_cache, cache0[0])
     assert pkg.moe_status(a.workspace, 1, H, I, E, top_k) == 0
+
+
+@pytest.mark.parametrize("xdt,H,E,I,top_k,nh,nkv,qkv_scales", [
+    ("f16", 2048, 128, 768, 8, 32, 4, None),           # the Thinker's layers
+    ("bf16", 1024, 32, 512, 6, 8, 2, None),
+    ("f16", 2048, 64, 768, 8, 32, 4, torch.float32)])  # fp32 q|k|v scales
+def test_thinker_decode_step_equals_layer_by_layer(pkg, dev, xdt, H, E, I, top_k, nh, nkv,
+                                                   qkv_scales):
+    """i4_thinker_decode_step over three layers (one call, the hidden state between layers
+    kept in its workspace) equals i4_thinker_layer_decode layer by layer, bit for bit:
+    output, every cache and a status word of 0; host and device positions."""
+    tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    max_len = 512
+    layers = [_synthetic_layer(pkg, dev, tdt, H, E, I, top_k, nh, nkv, max_len, True,
+                               seed=900 + 7 * i + H, qkv_scales=qkv_scales) for i in range(3)]
+    dec = pkg.ThinkerDecoder(layers)
+    assert dec.fused()
+    caches = [(l.attn.k_cache.clone(), l.attn.v_cache.clone()) for l in layers]
+
+    def restore():
+        for l, (k, v) in zip(layers, caches):
+            l.attn.k_cache.copy_(k)
+            l.attn.v_cache.copy_(v)
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(31)
+    for pos in (300, 127, 0):
+        x = torch.randn(1, H, device=dev, generator=gen).to(tdt)
+        restore()
+        want = dec.unfused(x, pos)
+        want_kv = [(l.attn.k_cache.clone(), l.attn.v_cache.clone()) for l in layers]
+        for dev_pos in (False, True):
+            restore()
+            pp = torch.full((1,), pos, dtype=torch.int32, device=dev) if dev_pos else pos
+            got = dec.step(x, pp)
+            torch.cuda.synchronize()
+            assert torch.isfinite(got.float()).all()
+            assert torch.equal(got, want), (pos, dev_pos)
+            for l, (k, v) in zip(layers, want_kv):
+                assert torch.equal(l.attn.k_cache, k) and torch.equal(l.attn.v_cache, v)
+            assert pkg.moe_status(dec.workspace, 1, H, I, E, top_k) == 0
 
 
 def test_decode_step_graph_with_device_position(pkg, dev, ckpt):
