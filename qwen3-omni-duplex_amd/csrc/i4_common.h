@@ -364,9 +364,15 @@ __device__ inline bool poll_rows(Stager<XT, 256>& st, const uint16_t* src, int m
 // RMSNorm of 8 values (one 16-byte load): round(round(x * r) * w), the order
 // of transformers' Qwen3OmniMoeThinkerTextRMSNorm.forward
 // (modeling_qwen3_omni_moe.py:1388-1393 in transformers 5.15).
+// x * r is rounded to fp32 before the conversion: the empty asm keeps the compiler
+// from fusing the product into the conversion (v_fma_mixlo, one rounding), which it
+// does in some instantiations and not in others, so that every kernel normalises
+// alike and as torch does (an fp32 product, then .to(dtype)).
 template <int XT> __device__ inline u32 norm_pair(u32 xp, u32 wp, float r) {
-  const float a = Half<XT>::to_f32(Half<XT>::from_f32(Half<XT>::to_f32((uint16_t)xp) * r));
-  const float b = Half<XT>::to_f32(Half<XT>::from_f32(Half<XT>::to_f32((uint16_t)(xp >> 16)) * r));
+  float pa = Half<XT>::to_f32((uint16_t)xp) * r, pb = Half<XT>::to_f32((uint16_t)(xp >> 16)) * r;
+  asm volatile("" : "+v"(pa), "+v"(pb));
+  const float a = Half<XT>::to_f32(Half<XT>::from_f32(pa));
+  const float b = Half<XT>::to_f32(Half<XT>::from_f32(pb));
   const u32 lo = Half<XT>::from_f32(a * Half<XT>::to_f32((uint16_t)wp));
   const u32 hi = Half<XT>::from_f32(b * Half<XT>::to_f32((uint16_t)(wp >> 16)));
   return lo | (hi << 16);

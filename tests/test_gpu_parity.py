@@ -859,8 +859,35 @@ def test_stack_matches_layer_loop_variants(pkg, dev, xdt, norm, n_layers):
         h = m(h, residual=h)
     assert torch.isfinite(stack).all()
     assert torch.equal(stack, h)
-    again = pkg.moe_stack(xt, [m.stack_entry() for m in layers], 8)
+    ws = pkg.Workspace()
+    again = pkg.moe_stack(xt, [m.stack_entry() for m in layers], 8, workspace=ws)
     assert torch.equal(again, stack)
+    assert pkg.moe_status(ws, 1, 2048, 768, 32, 8) == 0
+
+
+@pytest.mark.parametrize("norm,top_k,n_layers", [(True, 8, 4), (False, 4, 3)])
+def test_stack_hidden_1024(pkg, dev, norm, top_k, n_layers):
+    """A decode stack at hidden 1024 (the router wave of 1024 values) equals the module loop
+    bit for bit, with its status word left at 0."""
+    rng = np.random.default_rng(140 + n_layers)
+    mods = []
+    for _ in range(n_layers):
+        m, _, _, _ = _awq_moe(pkg, dev, rng, E=16, H=1024, I=768, top_k=top_k)
+        if norm:
+            nw = rng.uniform(0.5, 1.5, 1024).astype(np.float16)
+            m.register_buffer("norm_weight", t_(nw, dev), persistent=False)
+            m.norm_eps = 1e-6
+        mods.append(m)
+    x = make_x(rng, (1, 1024), "f16") * (1.0 if norm else 0.1)
+    xt = t_(x, dev)
+    ws = pkg.Workspace()
+    stack = pkg.moe_stack(xt, [m.stack_entry() for m in mods], top_k, workspace=ws)
+    h = xt
+    for m in mods:
+        h = m(h, residual=h)
+    assert torch.isfinite(stack).all()
+    assert torch.equal(stack, h)
+    assert pkg.moe_status(ws, 1, 1024, 768, 16, top_k) == 0
 
 
 def test_stack_graph_replays_match_eager(pkg, dev):
