@@ -356,10 +356,11 @@ def time_gemvs(pkg, torch, dev, replays=20):
                  Cache) launched back to back;
       attention: q 2048->4096, k/v 2048->512, o 4096->2048, 64 distinct layer sets (628 MB),
                  each projection timed on its own (all 64 copies back to back), the four
-                 of a layer back to back, and (CT) q/k/v as one launch followed by o.
+                 of a layer back to back, and q/k/v as one launch followed by o.
     Each workload runs on the AWQ tensors as the checkpoint holds them (one launch, split
-    along K, the last slice of each column strip summing the strip's partials) and on their
-    CT+zeros repack (one launch, what PackedLinear installs).
+    along K, the last slice of each column strip summing the strip's partials; q/k/v as one
+    launch over their columns side by side, PackedQKV(repack=False)) and on their CT+zeros
+    repack (one launch, what PackedLinear installs).
     Times are per GEMV (or per layer of four), mean / median / p99 over graph replays."""
     from qwen3_omni_duplex_amd import _lib
 
@@ -433,11 +434,16 @@ def time_gemvs(pkg, torch, dev, replays=20):
     qkv.K, qkv.N = 2048, sum(c.N for c in cts)
     wq = pkg.QWeight(torch.cat([c.packed for c in cts], 1), torch.cat([c.scale for c in cts], 1),
                      torch.cat([c.zeros for c in cts], 1), "ct", G, qkv.N, qkv.K)
-    qkv.desc = {"ct": per_copy(wq)}
-    qkv.keep = (wq,)
+    # and in AWQ packing, the q, k, v columns side by side (PackedQKV(repack=False))
+    awqs = [projs[n].keep[0] for n in ("q", "k", "v")]
+    wqa = pkg.QWeight(torch.cat([a.packed for a in awqs], 2), torch.cat([a.scale for a in awqs], 2),
+                      torch.cat([a.zeros for a in awqs], 2), "awq", G, qkv.N, qkv.K)
+    qkv.desc = {"ct": per_copy(wq), "awq": per_copy(wqa)}
+    qkv.keep = (wq, wqa)
     qkv.x = projs["q"].x
     qkv.y = torch.empty(1, qkv.N, dtype=torch.float16, device=dev)
-    qkv.ws = projs["q"].ws
+    nb = lb.i4_linear_workspace_bytes(ctypes.byref(qkv.desc["awq"][0]), 1)
+    qkv.ws = torch.full((max(nb, 256),), 255, dtype=torch.uint8, device=dev)
     for layout in ("ct", "awq"):
         att = {}
         for name, p in projs.items():
@@ -452,15 +458,15 @@ def time_gemvs(pkg, torch, dev, replays=20):
         ts = graph_times(torch, layer_seq, replays)
         att["qkvo_back_to_back"] = stats(ts, n2, sum(awq_gemv_bytes(p.K, p.N)
                                                     for p in projs.values()))
-        if layout == "ct":  # q/k/v rows concatenated into one launch (PackedQKV), then o
-            def fused_seq():
-                for i in range(n2):
-                    qkv.launch("ct", i)
-                    projs["o"].launch("ct", i)
+        # q/k/v as one launch (PackedQKV: CT rows, or AWQ columns side by side), then o
+        def fused_seq():
+            for i in range(n2):
+                qkv.launch(layout, i)
+                projs["o"].launch(layout, i)
 
-            ts = graph_times(torch, fused_seq, replays)
-            att["qkv_fused_then_o"] = stats(ts, n2, sum(awq_gemv_bytes(p.K, p.N)
-                                                        for p in projs.values()))
+        ts = graph_times(torch, fused_seq, replays)
+        att["qkv_fused_then_o"] = stats(ts, n2, sum(awq_gemv_bytes(p.K, p.N)
+                                                    for p in projs.values()))
         out[f"attention_{layout}"] = att
         log(f"attention q/k/v/o ({layout}): " + ", ".join(
             f"{k} {v['us']:.2f}" for k, v in att.items()) + " us")
@@ -475,7 +481,7 @@ def time_gemvs(pkg, torch, dev, replays=20):
         for layout in (("tile", "ct") if M == 32 else ("tile",)):
             for name, p in pp.items():
                 if layout == "tile" and "tile" not in p.desc:
-                    t = p.keep[-1 if name == "qkv" else 1].to_tile()
+                    t = p.keep[0 if name == "qkv" else 1].to_tile()  # from the CT weight
                     p.desc["tile"] = per_copy(t)
                     p.keep = p.keep + (t,)
                 nb = max(lb.i4_linear_workspace_bytes(ctypes.byref(p.desc[layout][0]), M), 16)

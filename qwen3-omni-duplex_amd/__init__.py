@@ -17,7 +17,8 @@ include/i4moe.h).  There is no fallback: without the built library every op
 raises.
 """
 from . import _lib
-from .linear import TILE_ROWS, PackedLinear, PackedQKV, QKVSlice, concat_rows, patch_attention
+from .linear import (TILE_ROWS, PackedLinear, PackedQKV, QKVSlice, concat_cols_awq, concat_rows,
+                     patch_attention)
 from .attention import ThinkerAttention, ThinkerDecoder, ThinkerDecoderLayer, rope_inv_freq
 from .loader import (Checkpoint, load_attention, load_moe_layer, load_thinker_decoder,
                      load_thinker_layer, load_thinker_moe_stack, read_moe_layer)
@@ -39,7 +40,7 @@ __all__ = [
     "moe_down_combine", "moe_down_wait", "moe_status", "moe_forward_noalloc",
     "moe_stack", "Workspace",
     "FusedPackedMoE", "fuse_packed_moe_blocks", "PackedLinear", "PackedQKV", "QKVSlice",
-    "concat_rows", "patch_attention", "TILE_ROWS", "lib",
+    "concat_rows", "concat_cols_awq", "patch_attention", "TILE_ROWS", "lib",
     "Checkpoint", "read_moe_layer", "load_moe_layer", "load_thinker_moe_stack", "load_attention",
     "load_thinker_layer", "load_thinker_decoder", "rmsnorm", "rmsnorm_linear", "attn_decode",
     "attn_decode_o", "thinker_layer_decode", "thinker_layer_fits", "thinker_layer_c",

@@ -104,6 +104,28 @@ def concat_rows(parts: list[QWeight]) -> QWeight:
     return QWeight(packed, scale, zeros, "ct", c0.group, sum(c.N for c in cts), c0.K)
 
 
+def concat_cols_awq(parts: list[QWeight]) -> QWeight:
+    """One AWQ weight (E = 1) holding the output columns of parts in order, still in
+    AutoAWQ packing ([K][N / 8] words, [groups][N] scales, [groups][N / 8] zero words):
+    the in-place GEMV then serves q, k and v in one launch.  A part without zero
+    points gets explicit 8s when another has them."""
+    p0 = parts[0]
+    for p in parts:
+        if (p.layout != "awq" or p.E != 1 or p.K != p0.K or p.group != p0.group
+                or p.scale.dtype != p0.scale.dtype or p.N % 8):
+            raise ValueError("column-concatenated AWQ parts need E = 1, N % 8 == 0 and equal "
+                             "K, group, scale dtype")
+    packed = torch.cat([p.packed for p in parts], dim=2)
+    scale = torch.cat([p.scale for p in parts], dim=2)
+    zeros = None
+    if any(p.zeros is not None for p in parts):
+        ng = -(-p0.K // p0.group)
+        zeros = torch.cat([p.zeros if p.zeros is not None else
+                           torch.full((1, ng, p.N // 8), _SYM_ZEROS, dtype=torch.int32,
+                                      device=p.device) for p in parts], dim=2)
+    return QWeight(packed, scale, zeros, "awq", p0.group, sum(p.N for p in parts), p0.K)
+
+
 class PackedQKV(nn.Module):
     """q, k and v projections of one attention block as one int4 GEMV launch.
 
@@ -122,15 +144,19 @@ class PackedQKV(nn.Module):
         self.sizes = tuple(int(v) for v in sizes)
 
     @classmethod
-    def from_qweights(cls, q: QWeight, k: QWeight, v: QWeight, biases=None) -> "PackedQKV":
-        w = concat_rows([q, k, v])
+    def from_qweights(cls, q: QWeight, k: QWeight, v: QWeight, biases=None,
+                      repack: bool = True) -> "PackedQKV":
+        """repack=False keeps AWQ parts in AWQ packing (concat_cols_awq, the in-place
+        GEMV, no tile copy); otherwise the rows are concatenated in CT (concat_rows)."""
+        in_place = not repack and all(p.layout == "awq" for p in (q, k, v))
+        w = concat_cols_awq([q, k, v]) if in_place else concat_rows([q, k, v])
         bias = None
         if biases is not None and any(b is not None for b in biases):
             dt = next(b.dtype for b in biases if b is not None)
             bias = torch.cat([b.to(dt) if b is not None else
                               torch.zeros(p.N, dtype=dt, device=p.device)
                               for b, p in zip(biases, (q, k, v))])
-        return cls(w, (q.N, k.N, v.N), bias)
+        return cls(w, (q.N, k.N, v.N), bias, tile=not in_place)
 
     def forward(self, x: torch.Tensor):
         y = self.lin(x)

@@ -425,6 +425,32 @@ def test_packed_qkv_matches_three_linears(pkg, dev):
             assert i4ref.rel_err(host(y), host(want)) <= 1e-3
 
 
+def test_packed_qkv_awq_in_place(pkg, dev):
+    """q|k|v kept in AWQ packing (PackedQKV(repack=False): the columns side by side, one
+    in-place GEMV launch, split along K at these sizes) against the oracle's fp64 product,
+    and against the three separate in-place launches (whose k / v run K-complete: the sums
+    may round differently, so within 1e-3)."""
+    rng = np.random.default_rng(43)
+    K, G = 2048, 128
+    x = t_(make_x(rng, (1, K), "f16"), dev)
+    parts, dense = [], []
+    for i, N in enumerate((4096, 512, 512)):
+        qw, qz, sc = _gen.awq_weight(rng, 1, K, N, G)
+        z = None if i == 2 else qz
+        parts.append(pkg.QWeight(t_(qw, dev), t_(sc, dev), None if z is None else t_(z, dev),
+                                 "awq", G, N, K))
+        dense.append(i4ref.awq_dequant(qw[0], None if z is None else z[0], f_(sc[0]), G))
+    fused = pkg.PackedQKV.from_qweights(*parts, repack=False)
+    assert fused.lin.w.layout == "awq" and fused.lin.w_tile is None
+    got = fused(x)
+    xf = np.asarray(host(x), np.float64)[0]
+    for y, w, d in zip(got, parts, dense):
+        ref = d @ xf
+        assert i4ref.rel_err(np.asarray(host(y), np.float64)[0], ref) <= TOL
+        alone = pkg.PackedLinear.from_qweight(w, repack=False)(x)
+        assert i4ref.rel_err(host(y), host(alone)) <= 1e-3
+
+
 class _FakePacked(torch.nn.Module):
     """A compressed-tensors pack-quantized Linear as the reference's loader leaves it."""
 

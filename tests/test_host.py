@@ -121,3 +121,34 @@ def test_block_weights_must_match_the_activation_dtype(pkg):
     with pytest.raises(RuntimeError, match=r"\[8, 64\]"):
         ops._check_block_dtypes(torch.bfloat16, 64, 8, torch.zeros(16, 64, dtype=torch.bfloat16),
                                 None)
+
+
+def test_concat_cols_awq_keeps_the_awq_format(pkg):
+    """q|k|v side by side in AWQ packing: words, scales and zero words concatenated along
+    N; a part without zero points gets explicit 8s.  Dequantised by the oracle, the result
+    is the parts' rows stacked in order (pins the layout the in-place GEMV reads)."""
+    import numpy as np
+
+    from oracle import i4ref
+    from tests import _gen
+
+    rng = np.random.default_rng(5)
+    K, G = 256, 128
+    parts, dense = [], []
+    for i, N in enumerate((64, 32, 32)):
+        qw, qz, sc = _gen.awq_weight(rng, 1, K, N, G)
+        z = None if i == 1 else torch.from_numpy(qz)
+        parts.append(pkg.QWeight(torch.from_numpy(qw), torch.from_numpy(sc), z, "awq", G, N, K))
+        dense.append(i4ref.awq_dequant(qw[0], None if i == 1 else qz[0], sc[0], G))
+    w = pkg.concat_cols_awq(parts)
+    assert (w.layout, w.N, w.K, w.E) == ("awq", 128, K, 1)
+    assert torch.equal(w.packed[0, :, 8:12], parts[1].packed[0])
+    assert (w.zeros[0, :, 8:12] == -2004318072).all()  # 0x88888888: every zero point 8
+    got = i4ref.awq_dequant(w.packed[0].numpy(), w.zeros[0].numpy(), w.scale[0].numpy(), G)
+    assert np.array_equal(got, np.concatenate(dense, axis=0))
+    qw, qz, sc = _gen.awq_weight(rng, 1, 128, 32, G)  # another K
+    other = pkg.QWeight(torch.from_numpy(qw), torch.from_numpy(sc), torch.from_numpy(qz), "awq",
+                        G, 32, 128)
+    with pytest.raises(ValueError):
+        pkg.concat_cols_awq([parts[0], other])
+
