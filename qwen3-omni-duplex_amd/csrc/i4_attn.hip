@@ -728,27 +728,29 @@ int i4_thinker_decode_step(const void* h, int x_dtype, const i4_thinker_layer* l
                            int topk, int renorm, void* out, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
   if (!h || !layers || !out) return I4_ERR_NULL;
-  if (n_layers < 1 || n_layers > 256) return I4_ERR_SHAPE;
+  if (n_layers < 1) return I4_ERR_SHAPE;
   if (((uintptr_t)h & 15) || ((uintptr_t)out & 15)) return I4_ERR_ALIGN;
-  LayerOk c[256];
+  // every layer's checks first (a host pass per layer, repeated before its launches)
+  LayerOk c0, c;
   for (int l = 0; l < n_layers; ++l) {
     int rc = layer_check(layers[l], x_dtype, n_heads, n_kv_heads, head_dim, inv_freq, pos_dev,
-                         pos, max_len, topk, workspace, workspace_bytes, 0, &c[l]);
+                         pos, max_len, topk, workspace, workspace_bytes, 0, l ? &c : &c0);
     if (rc) return rc;
     // every layer shares one workspace layout
-    if (c[l].mb.H != c[0].mb.H || c[l].mb.I != c[0].mb.I || c[l].mb.E != c[0].mb.E)
-      return I4_ERR_SHAPE;
+    if (l && (c.mb.H != c0.mb.H || c.mb.I != c0.mb.I || c.mb.E != c0.mb.E)) return I4_ERR_SHAPE;
   }
   // the hidden state between layers: one buffer serves them all (a layer reads its input
   // in its first three launches and writes its output in the fourth)
-  if (workspace_bytes < c[0].l.bytes + i4::al256((size_t)c[0].mb.H * 2)) return I4_ERR_WORKSPACE;
-  void* hbuf = (char*)workspace + c[0].l.bytes;
+  if (workspace_bytes < c0.l.bytes + i4::al256((size_t)c0.mb.H * 2)) return I4_ERR_WORKSPACE;
+  void* hbuf = (char*)workspace + c0.l.bytes;
   const void* cur = h;
   for (int l = 0; l < n_layers; ++l) {
     void* dst = l == n_layers - 1 ? out : hbuf;
-    const int rc = layer_launch(layers[l], c[l], x_dtype, n_heads, n_kv_heads, inv_freq,
-                                pos_dev, pos, max_len, topk, renorm, cur, l == 0, dst,
-                                workspace, stream);
+    int rc = layer_check(layers[l], x_dtype, n_heads, n_kv_heads, head_dim, inv_freq, pos_dev,
+                         pos, max_len, topk, workspace, workspace_bytes, 0, &c);
+    if (rc) return rc;
+    rc = layer_launch(layers[l], c, x_dtype, n_heads, n_kv_heads, inv_freq, pos_dev, pos,
+                      max_len, topk, renorm, cur, l == 0, dst, workspace, stream);
     if (rc) return rc;
     cur = dst;
   }
