@@ -416,7 +416,7 @@ struct OLaunch {
 template <int XT, int ST>
 int launch_attn_o(const float* part, int nq, const int32_t* pos_dev, int pos, int max_len,
                   uint16_t* att, const OLaunch& o, hipStream_t s) {
-  const int C = o.w.K / 32, L = gemv_lanes_per_row(C), rpw = 256 / L;
+  const int C = o.w.K / 32, L = gemv_lanes_per_row(C, o.w.N), rpw = 256 / L;
   const int n_o = (o.w.N + rpw - 1) / rpw;
   RFold r{};
   int rh = 0, n_r = 0;

@@ -646,7 +646,7 @@ static int launch_gemv_ct_t(const void* x, int64_t x_stride, const i4_qweight* w
                             const int32_t* sel, int k_sel, void* out, int ot, const void* bias,
                             hipStream_t s, const void* nw = nullptr, float eps = 0.f) {
   const int C = w->K / 32;
-  const int L = gemv_lanes_per_row(C);
+  const int L = gemv_lanes_per_row(C, w->N);
   const int rpw = WG / L;
   dim3 grid((w->N + rpw - 1) / rpw, k_sel);
   const size_t lds = (size_t)w->K * 2 + (size_t)C * 8;
