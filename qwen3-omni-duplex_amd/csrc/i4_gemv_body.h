@@ -155,7 +155,8 @@ __device__ __forceinline__ void gemv_ct_body(
 // long enough, 2+ (twice the lanes, twice the workgroups) for N <= 1024 and N > 4096.
 // Measured at K = 2048 on one MI355X: 2048 -> 768 3.71 -> 3.53 us, 2048 -> 512 3.32 ->
 // 3.17, the decode step's q|k|v with its input norm (N = 5120) 0.3 us faster per layer;
-// q_proj 2048 -> 4096 slower (3.80 -> 4.17), so that band keeps 3+ chunks.
+// q_proj 2048 -> 4096 slower (3.80 -> 4.17), so that band keeps 3+ chunks; and
+// 4096-value rows stay at 32 lanes (64: o_proj 4096 -> 2048 3.88 -> 4.30 us).
 inline int gemv_lanes_per_row(int C, int N) {
   const int per = N <= 1024 || N > 4096 ? 2 : 3;
   int L = 4;
