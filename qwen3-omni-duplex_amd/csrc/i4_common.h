@@ -49,6 +49,9 @@ __device__ inline rsrc_t rsrc(const void* base, u32 bytes) {
 // line its own L2 may still hold (sc1).  No fence is involved: a consumer
 // recognises finished data by its value (see the sentinel below).
 static constexpr int kCoherent = 16;  // cache-policy bit sc1 of a buffer access
+// A store with sc0 instead stays in its XCD's L2 (and reaches memory later), where a
+// sc1 load from a CU of the same XCD finds it sooner than one written through.
+static constexpr int kL2Only = 1;
 __device__ inline u32x4 ld16_coherent(rsrc_t r, u32 voff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, kCoherent);
 }

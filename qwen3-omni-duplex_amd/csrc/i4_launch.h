@@ -31,3 +31,14 @@ int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr,
                             void* pend = nullptr, int n_pend = 0, int32_t* status = nullptr);
 int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
                    float* wf, void* wh, int wht, hipStream_t s);
+
+// T = 1 router launch that first completes the previous layer of an XCD-local experts
+// launch: h = res + sum_k wts[k] ypart[k] (kc == 8 slot rows of H values), written to
+// h_out, then routed as i4_launch_router_logits routes x (H = 1024 or 2048).
+int i4_launch_router_sum(const void* res, const void* ypart, const float* wts, int kc,
+                         void* h_out, int xt, int H, const void* wr, int E, const void* norm_w,
+                         float eps, void* xn, void* logits, hipStream_t s, void* pend,
+                         int n_pend, int32_t* status);
+// The completion alone: out = res + sum_k wts[k] ypart[k].
+int i4_launch_moe_sum(const void* res, const void* ypart, const float* wts, int kc, int xt,
+                      int H, void* out, hipStream_t s);

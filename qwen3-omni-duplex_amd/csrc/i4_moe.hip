@@ -294,13 +294,15 @@ struct MoeOps {
                    hipStream_t);
   int (*mfma_mixed)(bool, int, int, const void*, int, int, const int4*, const int*, const int4*,
                     const int*, const int32_t*, const TW&, int, void*, hipStream_t);
+  int (*moe_m1x_ct)(const GateUpArgs&, const TW&, const TW&, void*, int32_t*, int, hipStream_t);
 };
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
   return MoeOps{&launch_gate_up<XT, ST>,     &launch_down_m1<XT, ST>,
                 &launch_gate_up_ct<XT, ST>,  &launch_down_m1_ct<XT, ST>,
                 &launch_mfma_gate_up<XT, ST>, &launch_mfma_down<XT, ST>,
-                &launch_moe_m1_ct<XT, ST>,   &launch_mfma_mixed<XT, ST>};
+                &launch_moe_m1_ct<XT, ST>,   &launch_mfma_mixed<XT, ST>,
+                &launch_moe_m1x_ct<XT, ST>};
 }
 
 bool pick_ops(int xt, int gst, int dst, MoeOps* ops) {
@@ -547,6 +549,68 @@ int moe_decode_experts(const MoeDecodeBufs& b, int x_dtype, int topk, int renorm
 
 }  // namespace i4
 
+namespace {
+
+// stack workspace beyond the T = 1 MoE workspace: the hidden state between layers;
+// at T = 1 a second one and the slot outputs [topk][H] of the XCD-local path
+size_t stack_extra_bytes(int T, int H, int topk) {
+  const size_t h = al256((size_t)T * H * 2);
+  return T == 1 ? 2 * h + al256((size_t)topk * H * 2) : h;
+}
+
+// every layer of a T = 1 stack can run the XCD-local experts launch (validated blocks)
+bool stack_xcd_local(const i4_moe_weights* layers, int n, int xt, int topk) {
+  for (int l = 0; l < n; ++l) {
+    const i4_moe_weights& w = layers[l];
+    const int H = w.gate_up.K, I = w.down.K;
+    MoeOps ops;
+    if (w.gate_up.layout != I4_LAYOUT_CT || !w.router_w || (H != 1024 && H != 2048) ||
+        !moe_m1x_ct_fits(topk, H, I) || !pick_ops(xt, w.gate_up.scale_dtype,
+                                                  w.down.scale_dtype, &ops))
+      return false;
+  }
+  return true;
+}
+
+// T = 1 stack on the XCD-local experts launch.  Layer l's router launch first
+// completes layer l - 1 (h_l = h_{l-1} + sum_j w_j y_j, written to hb[l % 2]) and
+// routes h_l; the experts launch leaves its slot outputs in ypart and its routing
+// weights in ws.w; one more launch completes the last layer into out.  The router
+// launch of layer 0 clears the status word, so a wait that gives up in any layer
+// stays visible.
+int stack_m1x(const void* x, int xt, const i4_moe_weights* layers, int n, int topk, int renorm,
+              void* out, const MoeWs& ws, uint16_t* hb0, uint16_t* hb1, uint16_t* ypart,
+              hipStream_t s) {
+  const void* h = x;  // h_l, the input of layer l
+  for (int l = 0; l < n; ++l) {
+    const i4_moe_weights* mw = &layers[l];
+    i4_qweight gu, dn, tg, td;
+    int rc = check_moe(mw, xt, 1, topk, &gu, &dn, &tg, &td);
+    if (rc) return rc;
+    const int H = gu.K, I = dn.K, E = gu.E;
+    MoeOps ops;
+    if (!pick_ops(xt, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
+    uint16_t* xn = mw->norm_w ? ws.xn : nullptr;
+    if (l == 0) {
+      rc = i4_launch_router_logits(h, xt, 1, H, mw->router_w, E, mw->norm_w, mw->norm_eps, xn,
+                                   ws.logits, s, ws.act, topk * I / 8, ws.status);
+    } else {
+      uint16_t* hl = (l % 2) ? hb1 : hb0;
+      rc = i4_launch_router_sum(h, ypart, ws.w, topk, hl, xt, H, mw->router_w, E, mw->norm_w,
+                                mw->norm_eps, xn, ws.logits, s, ws.act, topk * I / 8, nullptr);
+      h = hl;
+    }
+    if (rc) return rc;
+    const GateUpArgs a{true, topk, topk, E, renorm, xn ? (const void*)xn : h, ws.sel, ws.logits,
+                       ws.w, ws.act, nullptr};
+    rc = ops.moe_m1x_ct(a, to_tw(gu), to_tw(dn), ypart, ws.status, kHandoffPolls, s);
+    if (rc) return rc;
+  }
+  return i4_launch_moe_sum(h, ypart, ws.w, topk, xt, layers[0].gate_up.K, out, s);
+}
+
+}  // namespace
+
 extern "C" {
 
 size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk) {
@@ -645,7 +709,7 @@ int i4_moe_down_combine(const void* act, int x_dtype, const i4_qweight* down, co
 size_t i4_moe_stack_workspace_bytes(int T, int H, int I, int E, int topk) {
   const size_t m = i4_moe_workspace_bytes(T, H, I, E, topk);
   if (!m) return 0;
-  return m + al256((size_t)T * H * 2);
+  return m + stack_extra_bytes(T, H, topk);
 }
 
 int i4_moe_stack_forward(const void* x, int x_dtype, int T, const i4_moe_weights* layers,
@@ -665,9 +729,15 @@ int i4_moe_stack_forward(const void* x, int x_dtype, int T, const i4_moe_weights
     if (layers[l].gate_up.K != H || layers[l].down.K != I || layers[l].gate_up.E != E)
       return I4_ERR_SHAPE;
   const size_t mbytes = i4_moe_workspace_bytes(T, H, I, E, topk);
-  if (!workspace || workspace_bytes < mbytes + al256((size_t)T * H * 2)) return I4_ERR_WORKSPACE;
+  if (!workspace || workspace_bytes < mbytes + stack_extra_bytes(T, H, topk))
+    return I4_ERR_WORKSPACE;
   if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
   void* buf = (char*)workspace + mbytes;
+  if (T == 1 && stack_xcd_local(layers, n_layers, x_dtype, topk))
+    return stack_m1x(x, x_dtype, layers, n_layers, topk, renorm, out,
+                     carve(workspace, 1, H, I, E, topk), (uint16_t*)buf,
+                     (uint16_t*)((char*)buf + al256((size_t)H * 2)),
+                     (uint16_t*)((char*)buf + 2 * al256((size_t)H * 2)), stream);
   const void* h = x;
   for (int l = 0; l < n_layers; ++l) {
     void* dst = ((n_layers - 1 - l) % 2 == 0) ? out : buf;

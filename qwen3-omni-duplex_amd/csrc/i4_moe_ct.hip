@@ -56,7 +56,7 @@ template <int ST> __device__ inline RowPtr row_ptr(const QW& w, int e, int n) {
 //             bit-identical in every wave) and takes its slot; workgroup
 //             (0, 0) writes sel[] / wts[] for the down projection
 
-template <int XT, int ST, int L, int MODE, bool HANDOFF>
+template <int XT, int ST, int L, int MODE, bool HANDOFF, bool XCD_LOCAL = false>
 __device__ inline void gate_up_body(int bx, int by, const uint16_t* __restrict__ x, int topk,
                                     int32_t* __restrict__ sel,
                                     const uint16_t* __restrict__ logits, int E_r, int renorm,
@@ -167,11 +167,18 @@ __device__ inline void gate_up_body(int bx, int by, const uint16_t* __restrict__
     if (RPW % 8 == 0 && nv == RPW && (I & 7) == 0) {  // 16-byte aligned whole words
       if ((int)threadIdx.x < RPW / 8) {
         const rsrc_t r = rsrc(dst, (u32)RPW * 2u);
-        __builtin_amdgcn_raw_buffer_store_b128(((const u32x4*)s_act)[threadIdx.x], r,
-                                               (u32)threadIdx.x * 16u, 0, kCoherent);
+        const u32x4 v = ((const u32x4*)s_act)[threadIdx.x];
+        // XCD_LOCAL: into this XCD's L2, where the readers on the same XCD find it
+        // before a write-through store would be done (which holds the line meanwhile)
+        __builtin_amdgcn_raw_buffer_store_b128(v, r, (u32)threadIdx.x * 16u, 0,
+                                               XCD_LOCAL ? kL2Only : kCoherent);
       }
     } else if ((int)threadIdx.x < nv) {
-      st_coherent(dst + threadIdx.x, s_act[threadIdx.x]);
+      if constexpr (XCD_LOCAL)
+        __hip_atomic_store(dst + threadIdx.x, s_act[threadIdx.x], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      else
+        st_coherent(dst + threadIdx.x, s_act[threadIdx.x]);
     }
   }
 }
@@ -314,7 +321,7 @@ __device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int t
   __syncthreads();
   if (comb) {
     float y = 0.f;
-    for (int j = 0; j < topk; ++j) y += s_w[j] * red[j * RW + (int)threadIdx.x];
+    for (int j = 0; j < topk; ++j) y = __builtin_fmaf(s_w[j], red[j * RW + (int)threadIdx.x], y);
     if (late) y = __builtin_nanf("");
     out[on] = Half<XT>::from_f32((residual ? Half<XT>::to_f32(res_raw) : 0.f) + y);
   }
@@ -367,6 +374,152 @@ __global__ __launch_bounds__(WG) void k_ct_moe_m1(MoeM1Args a) {
     down_body<XT, ST, LD, JMAX, true>(b - a.n_gate, a.act, a.topk, nullptr, nullptr, a.logits,
                                       a.E_r, a.renorm, a.dn, a.residual, a.out, lds, a.status,
                                       a.max_polls);
+}
+
+// ---------------------------------------------------------------------------
+// XCD-local decode layer (top-8 on 8 XCDs).  Workgroups go round-robin over the
+// XCDs (block b on XCD b % 8, the same residue for every partition size that
+// divides 8), so slot j takes every block b with b % 8 == j: the gate_up rows of
+// expert sel[j] and its whole down projection run on one XCD.  The gate_up
+// workgroups store act[j] written through to memory and then once more into their
+// L2 (sc0), where the down workgroups of slot j, on the same XCD, find it: their
+// polls (loads served past the L1) see a line that L2 holds dirty without the
+// round trip to memory (measured on one MI355X: 0.16-0.24 us from store to a
+// poll that sees it, against 0.4-0.64 us written through), and each writes its
+// rows of the slot's output y[j], rounded to the activation dtype (the
+// reference's y.to(x.dtype), fused_packed_moe.py:262).  The routing-weighted sum
+// over the slots and the residual are left to the next launch (the next layer's
+// router, k_router_m1ws, or k_moe_sum_m1), whose kernel boundary takes the place
+// of the cross-XCD hand-over of the activations.  Per expert, the same dot
+// products in the same order as k_ct_moe_m1's down workgroups: the layer is
+// bit for bit the same.
+static constexpr int XCDS = 8;
+
+// Polls one activation row that producers of the same launch write (kPending16
+// until then) with loads served past the L1 (sc1): on the producers' XCD such a load
+// is served by a line their L2 holds dirty, elsewhere from memory.  Returns true if
+// max_polls passes went by without every value.  Thread t reads words t, t + 256, ...
+// of the row (st.d[u]), and only those; the barrier of each pass keeps the loads
+// inside the loop.
+template <int XT>
+__device__ inline bool poll_row_xcd(Stager<XT, 256>& st, const uint16_t* src, int max_polls) {
+  const rsrc_t r = rsrc(src, (u32)st.total * 16u);
+  for (int it = 0;; ++it) {
+    bool pend = false;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = u * 256 + (int)threadIdx.x;
+      if (idx < st.total) st.d[u] = ld16_coherent(r, (u32)idx * 16u);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (u * 256 + (int)threadIdx.x < st.total) pend |= has_pending(st.d[u]);
+    if (!__syncthreads_or(pend)) return false;
+    if (it >= max_polls) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Down projection of slot j for output rows [m RWD, (m + 1) RWD): L lanes per row
+// (lane l: chunks l, l + L, ... -- the chunk order of down_body), JR rows per lane
+// group.  Expert sel[j] is ranked from the logits by every wave.
+template <int XT, int ST, int L, int JR>
+__device__ inline void down_slot_body(int j, int m, const uint16_t* __restrict__ act,
+                                      const uint16_t* __restrict__ logits, int E_r, const QW& w,
+                                      uint16_t* __restrict__ ypart, unsigned char* lds,
+                                      int32_t* __restrict__ status, int max_polls) {
+  constexpr int RP = WG / L, RWD = RP * JR;
+  constexpr int CR = 4;  // chunks per round
+  const int I = w.K, H = w.N, C = I >> 5;
+  const int cpl = (C + L - 1) / L;
+  u32x4* xs = (u32x4*)lds;
+  float2* sums = (float2*)(lds + (size_t)I * 2);
+  // every wave ranks the logits itself (one ranking wave handing the expert to the
+  // others through LDS was slower: 13.26 against 12.82 us per stack layer)
+  auto route = [&](auto vpl) -> int {
+    constexpr int VPL = decltype(vpl)::value;
+    u32 raw[VPL];
+    load_row<XT, VPL>(logits, 0, E_r, raw);
+    return topk_slot<XT, VPL>(raw, E_r, j);
+  };
+  const int e = E_r <= 128 ? route(std::integral_constant<int, 2>{})
+                           : route(std::integral_constant<int, 8>{});
+  const bool ev = (unsigned)e < (unsigned)w.E;
+  const int ee = ev ? e : 0;
+  const int rl = threadIdx.x / L, cl = threadIdx.x % L;
+  const u32 mg = magic_v<XT>();
+  RowPtr rp[JR];
+#pragma unroll
+  for (int jr = 0; jr < JR; ++jr) rp[jr] = row_ptr<ST>(w, ee, min(m * RWD + rl + RP * jr, H - 1));
+  float row[JR];
+#pragma unroll
+  for (int jr = 0; jr < JR; ++jr) row[jr] = 0.f;
+  Chunk ch[JR][CR];
+  auto load_round = [&](int r0) {
+#pragma unroll
+    for (int jr = 0; jr < JR; ++jr)
+#pragma unroll
+      for (int i = 0; i < CR; ++i)
+        if (i == 0 || (r0 + i) * L < C)  // wave-uniform: skips rounds past the row's end
+          ch[jr][i] = load_chunk<ST>(rp[jr], min(cl + (r0 + i) * L, C - 1), w.gshift);
+  };
+  auto dot_round = [&](int r0) {
+#pragma unroll
+    for (int jr = 0; jr < JR; ++jr)
+#pragma unroll
+      for (int i = 0; i < CR; ++i) {
+        const int c = cl + (r0 + i) * L;
+        if (c < C)
+          row[jr] += chunk_dot<XT, ST>(ch[jr][i], xs[c], xs[C + c], xs[2 * C + c], xs[3 * C + c],
+                                       sums[c], c, w.gshift, mg);
+      }
+  };
+  // the weight loads go out first; the activation row is polled behind them
+  load_round(0);
+  Stager<XT> st(1, I);
+  const bool late = poll_row_xcd<XT>(st, act + (int64_t)j * I, max_polls);
+  st.commit(0, xs, sums);
+  __syncthreads();
+  dot_round(0);
+  for (int r0 = CR; r0 < cpl; r0 += CR) {
+    load_round(r0);
+    dot_round(r0);
+  }
+#pragma unroll
+  for (int jr = 0; jr < JR; ++jr) {
+    const int n = m * RWD + rl + RP * jr;
+    const float v = group_sum<L>(row[jr]);
+    if (cl == 0 && n < H)
+      ypart[(int64_t)j * H + n] = ev && !late ? Half<XT>::from_f32(v) : Half<XT>::QNAN;
+  }
+  if (late && threadIdx.x == 0) *status = I4_ERR_HANDOFF;
+}
+
+struct MoeM1xArgs {
+  const uint16_t* x;  // the experts' input row (RMSNorm(h) when the block has a norm)
+  int32_t* sel;       // written by block 0 with wts: the routing of the layer
+  float* wts;
+  const uint16_t* logits;
+  int E_r, renorm;
+  QW gu, dn;
+  uint16_t* act;    // [8][I], the pending pattern before the launch
+  uint16_t* ypart;  // [8][H] slot outputs
+  int32_t* status;  // I4_ERR_HANDOFF is stored here by a down workgroup whose wait gave up
+  int n_gate, max_polls;
+};
+
+template <int XT, int ST, int LG, int LD>
+__global__ __launch_bounds__(WG) void k_ct_moe_m1x(MoeM1xArgs a) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int b = blockIdx.x;
+  if (b < a.n_gate) {
+    gate_up_body<XT, ST, LG, GU_ROUTE, true, true>(b / XCDS, b % XCDS, a.x, XCDS, a.sel, a.logits,
+                                             a.E_r, a.renorm, a.wts, a.gu, a.dn.K, a.act, lds);
+  } else {
+    const int d = b - a.n_gate;
+    down_slot_body<XT, ST, LD, LD / 4>(d % XCDS, d / XCDS, a.act, a.logits, a.E_r, a.dn, a.ypart,
+                                       lds, a.status, a.max_polls);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -497,12 +650,59 @@ int launch_moe_m1_ct(const GateUpArgs& ga, const TW* tgu, const TW& tdn, const v
   return I4_ERR_SHAPE;
 }
 
+// The XCD-local layer covers top-8 blocks with the single-launch kernel's lane
+// shapes (down lanes 8 or 16: 64 output rows per down workgroup).
+bool moe_m1x_ct_fits(int topk, int H, int I) {
+  return topk == XCDS && moe_m1_ct_fits(topk, H, I) && (H % 8) == 0;
+}
+
+template <int XT, int ST>
+int launch_moe_m1x_ct(const GateUpArgs& ga, const TW& tgu, const TW& tdn, void* ypart,
+                      int32_t* status, int max_polls, hipStream_t s) {
+  MoeM1xArgs a;
+  a.gu = to_qw(tgu);
+  a.dn = to_qw(tdn);
+  const int H = a.dn.N, I = a.dn.K;
+  if (!status || max_polls < 0) return I4_ERR_NULL;
+  if (!moe_m1x_ct_fits(ga.topk, H, I)) return I4_ERR_SHAPE;
+  const int LG = gate_up_lanes(H / 32), LD = down_lanes_per_row(I / 32);
+  a.x = (const uint16_t*)ga.x;
+  a.sel = ga.sel;
+  a.logits = (const uint16_t*)ga.logits;
+  a.E_r = ga.E_r;
+  a.renorm = ga.renorm;
+  a.wts = ga.wts;
+  a.act = (uint16_t*)ga.act;
+  a.ypart = (uint16_t*)ypart;
+  a.status = status;
+  a.max_polls = max_polls;
+  const int rpw = WG / LG;
+  a.n_gate = ((I + rpw - 1) / rpw) * XCDS;
+  constexpr int RWD = 64;  // (WG / LD) * (LD / 4) output rows per down workgroup
+  const int n_down = ((H + RWD - 1) / RWD) * XCDS;
+  const size_t lds_d = (size_t)I * 2 + (size_t)(I / 32) * 8;
+  const size_t lds_g = (size_t)H * 2 + (H / 32) * 8;
+  const size_t lds = lds_d > lds_g ? lds_d : lds_g;
+  const dim3 grid(a.n_gate + n_down);
+#define I4_M1X_CASE(LG_, LD_)                                                                 \
+  if (LG == LG_ && LD == LD_) {                                                               \
+    hipLaunchKernelGGL((k_ct_moe_m1x<XT, ST, LG_, LD_>), grid, dim3(WG), lds, s, a);          \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                           \
+  }
+  I4_M1X_CASE(8, 8) I4_M1X_CASE(16, 8) I4_M1X_CASE(32, 8) I4_M1X_CASE(64, 8)
+  I4_M1X_CASE(8, 16) I4_M1X_CASE(16, 16) I4_M1X_CASE(32, 16) I4_M1X_CASE(64, 16)
+#undef I4_M1X_CASE
+  return I4_ERR_SHAPE;
+}
+
 #define I4_INST(XT_, ST_)                                                                      \
   template int launch_gate_up_ct<XT_, ST_>(const GateUpArgs&, const TW&, int, hipStream_t);    \
   template int launch_down_m1_ct<XT_, ST_>(const void*, int, const int32_t*, const float*,     \
                                            const TW&, const void*, void*, hipStream_t);        \
   template int launch_moe_m1_ct<XT_, ST_>(const GateUpArgs&, const TW*, const TW&, const void*, \
-                                          void*, int32_t*, int, hipStream_t);
+                                          void*, int32_t*, int, hipStream_t);                  \
+  template int launch_moe_m1x_ct<XT_, ST_>(const GateUpArgs&, const TW&, const TW&, void*,      \
+                                           int32_t*, int, hipStream_t);
 I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
 I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)
 #undef I4_INST

@@ -56,6 +56,16 @@ int launch_moe_m1_ct(const GateUpArgs& a, const TW* gate_up, const TW& down,
                      const void* residual, void* out, int32_t* status, int max_polls,
                      hipStream_t s);
 
+// The same layer with slot j's gate_up and down workgroups on XCD j (top-8): the
+// down workgroups take act[j] over through that XCD's L2 and write the slot's
+// output rows ypart[j][H] (activation dtype); the routing-weighted sum and the
+// residual are left to the next launch (i4_launch_router_sum / i4_launch_moe_sum,
+// with the weights block 0 writes to a.wts).  act must hold the pending pattern.
+bool moe_m1x_ct_fits(int topk, int H, int I);
+template <int XT, int ST>
+int launch_moe_m1x_ct(const GateUpArgs& a, const TW& gate_up, const TW& down, void* ypart,
+                      int32_t* status, int max_polls, hipStream_t s);
+
 // The T = 1 MoE block of a decoder layer whose router runs in an earlier launch
 // (i4_thinker_layer_decode, i4_attn.hip): that launch writes the logits and the
 // normalised row, arms act with the pending pattern and reports a wait that gave

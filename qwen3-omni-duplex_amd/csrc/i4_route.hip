@@ -113,6 +113,106 @@ __global__ __launch_bounds__(64) void k_router_m1w(
   router_wave<XT, NORM, H, false>(x, wr, blockIdx.x, nw, eps, xn_out, logits);
 }
 
+// k_router_m1w for the layer after an XCD-local experts launch (k_ct_moe_m1x): the
+// workgroup first completes that layer, h = residual + sum_k wts[k] ypart[k]
+// (slot_sum8; workgroup 0 writes h to h_out, the layer's output and the next
+// residual), then routes h.  Thread t completes word t of h into LDS, wave w forms the
+// sum of squares of words 64 w .. 64 w + 63 -- the partial sum router_wave's lanes
+// form for i = w -- and wave 0 routes expert blockIdx.x from the staged row with the
+// arithmetic of router_finish, so the logits and the normalised row are those of
+// k_router_m1w bit for bit.  Four waves share the completion's 9 H half loads
+// (one wave alone: 13.4 us per stack layer against 12.8; four experts per workgroup,
+// one per wave, 13.2).
+template <int XT, bool NORM, int H, int KC>
+__global__ __launch_bounds__(256) void k_router_m1ws(
+    const uint16_t* __restrict__ res, const uint16_t* __restrict__ ypart,
+    const float* __restrict__ wts, uint16_t* __restrict__ h_out,
+    const uint16_t* __restrict__ wr, int E, const uint16_t* __restrict__ nw, float eps,
+    uint16_t* __restrict__ xn_out, uint16_t* __restrict__ logits, u32x4* __restrict__ pend,
+    int n_pend, int32_t* __restrict__ status) {
+  constexpr int NR = H / 512, W = H / 8;
+  static_assert(W <= 256, "one word of the row per thread");
+  __shared__ u32x4 s_h[W];
+  __shared__ float s_ss[4];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  for (int i = blockIdx.x * 256 + t; i < n_pend; i += gridDim.x * 256)
+    pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
+  if (status && blockIdx.x == 0 && t == 0) *status = I4_OK;
+  const int e = blockIdx.x;
+  const bool router = wave == 0 && e < E;
+  u32x4 wv[NR], gv[NR];
+  if (router) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      wv[i] = ldg16(wr + (int64_t)e * H + 8 * lane + 512 * i);
+      if constexpr (NORM) gv[i] = ldg16(nw + 8 * (lane + 64 * i));
+    }
+  }
+  float ss = 0.f;
+  if (t < W) {
+    u32x4 y[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) y[k] = ldg16(ypart + (int64_t)k * H + 8 * t);
+    const u32x4 rv = ldg16(res + 8 * t);
+    float w[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) w[k] = wts[k];
+    const u32x4 h = slot_sum8<XT, KC>(rv, y, w);
+    s_h[t] = h;
+    if (h_out && blockIdx.x == 0) *(u32x4*)(h_out + 8 * t) = h;
+    if constexpr (NORM) ss = sumsq8<XT>(h);
+  }
+  if constexpr (NORM) {
+    ss = group_sum<64>(ss);
+    if (lane == 0) s_ss[wave] = ss;
+  }
+  __syncthreads();
+  if (!router) return;
+  u32x4 xv[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) xv[i] = s_h[lane + 64 * i];
+  if constexpr (NORM) {
+    const float r = 1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)H + eps);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      xv[i].x = norm_pair<XT>(xv[i].x, gv[i].x, r);
+      xv[i].y = norm_pair<XT>(xv[i].y, gv[i].y, r);
+      xv[i].z = norm_pair<XT>(xv[i].z, gv[i].z, r);
+      xv[i].w = norm_pair<XT>(xv[i].w, gv[i].w, r);
+      if (xn_out && e == 0) *(u32x4*)(xn_out + 8 * (lane + 64 * i)) = xv[i];
+    }
+  }
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    a = Half<XT>::dot2(wv[i].x, xv[i].x, a);
+    a = Half<XT>::dot2(wv[i].y, xv[i].y, a);
+    a = Half<XT>::dot2(wv[i].z, xv[i].z, a);
+    a = Half<XT>::dot2(wv[i].w, xv[i].w, a);
+  }
+  a = group_sum<64>(a);
+  if (lane == 0) logits[e] = Half<XT>::from_f32(a);
+}
+
+// The same completion alone, for the last layer: out = residual + sum_k wts[k] ypart[k],
+// one 16-byte word of each row per thread.
+template <int XT, int KC>
+__global__ __launch_bounds__(64) void k_moe_sum_m1(const uint16_t* __restrict__ res,
+                                                   const uint16_t* __restrict__ ypart,
+                                                   const float* __restrict__ wts, int H,
+                                                   uint16_t* __restrict__ out) {
+  const int m = blockIdx.x * 64 + (int)threadIdx.x;
+  if (m >= H / 8) return;
+  u32x4 y[KC];
+#pragma unroll
+  for (int k = 0; k < KC; ++k) y[k] = ldg16(ypart + (int64_t)k * H + 8 * m);
+  const u32x4 r = ldg16(res + 8 * m);
+  float w[KC];
+#pragma unroll
+  for (int k = 0; k < KC; ++k) w[k] = wts[k];
+  *(u32x4*)(out + 8 * m) = slot_sum8<XT, KC>(r, y, w);
+}
+
 // T > 1, pass 1: RMSNorm of one token per workgroup with exactly the
 // arithmetic of k_router_m1 (same thread -> word map, same reduction order),
 // so each token's xn is bit for bit the one it gets alone.
@@ -293,6 +393,40 @@ int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr,
     }
 #undef I4_RT_CASE
   }
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
+}
+
+int i4_launch_router_sum(const void* res, const void* ypart, const float* wts, int kc,
+                         void* h_out, int xt, int H, const void* wr, int E, const void* norm_w,
+                         float eps, void* xn, void* logits, hipStream_t s, void* pend,
+                         int n_pend, int32_t* status) {
+#define I4_RS_CASE(XT_, N_, H_)                                                                \
+  if (xt == XT_ && (norm_w != nullptr) == N_ && H == H_) {                                     \
+    hipLaunchKernelGGL((k_router_m1ws<XT_, N_, H_, 8>), dim3(E), dim3(256), 0, s,              \
+                       (const uint16_t*)res, (const uint16_t*)ypart, wts, (uint16_t*)h_out,    \
+                       (const uint16_t*)wr, E, (const uint16_t*)norm_w, eps, (uint16_t*)xn,    \
+                       (uint16_t*)logits, (u32x4*)pend, n_pend, status);                       \
+    return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                            \
+  }
+  if (kc != 8) return I4_ERR_SHAPE;
+  I4_RS_CASE(I4_F16, true, 2048) I4_RS_CASE(I4_F16, false, 2048)
+  I4_RS_CASE(I4_BF16, true, 2048) I4_RS_CASE(I4_BF16, false, 2048)
+  I4_RS_CASE(I4_F16, true, 1024) I4_RS_CASE(I4_F16, false, 1024)
+  I4_RS_CASE(I4_BF16, true, 1024) I4_RS_CASE(I4_BF16, false, 1024)
+#undef I4_RS_CASE
+  return I4_ERR_SHAPE;
+}
+
+int i4_launch_moe_sum(const void* res, const void* ypart, const float* wts, int kc, int xt,
+                      int H, void* out, hipStream_t s) {
+  if (kc != 8 || H % 8 != 0) return I4_ERR_SHAPE;
+  const dim3 grid((H / 8 + 63) / 64);
+  if (xt == I4_F16)
+    hipLaunchKernelGGL((k_moe_sum_m1<I4_F16, 8>), grid, dim3(64), 0, s, (const uint16_t*)res,
+                       (const uint16_t*)ypart, wts, H, (uint16_t*)out);
+  else
+    hipLaunchKernelGGL((k_moe_sum_m1<I4_BF16, 8>), grid, dim3(64), 0, s, (const uint16_t*)res,
+                       (const uint16_t*)ypart, wts, H, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 

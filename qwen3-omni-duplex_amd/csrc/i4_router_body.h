@@ -15,6 +15,42 @@ template <int NR> __device__ inline bool wave_pending(const u32x4 (&v)[NR]) {
   return __builtin_amdgcn_ballot_w64(p) != 0;
 }
 
+// The part of the router wave after its row x is in registers: RMSNorm (with NORM),
+// the normalised row to xn_out (expert 0's wave), the dot with router row wv and the
+// logit.  Lane l holds words l + 64 i of x, the norm weight and the router row.
+template <int XT, bool NORM, int H>
+__device__ __forceinline__ void router_finish(u32x4 (&xv)[H / 512], const u32x4 (&gv)[H / 512],
+                                              const u32x4 (&wv)[H / 512], int e, float eps,
+                                              uint16_t* __restrict__ xn_out,
+                                              uint16_t* __restrict__ logits) {
+  constexpr int NR = H / 512;
+  const int lane = threadIdx.x & 63;
+  if constexpr (NORM) {
+    float ws[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NR; ++i) ws[i] = group_sum<64>(sumsq8<XT>(xv[i]));  // wave i's sum
+    const float r = 1.0f / sqrtf(((ws[0] + ws[1]) + (ws[2] + ws[3])) / (float)H + eps);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      xv[i].x = norm_pair<XT>(xv[i].x, gv[i].x, r);
+      xv[i].y = norm_pair<XT>(xv[i].y, gv[i].y, r);
+      xv[i].z = norm_pair<XT>(xv[i].z, gv[i].z, r);
+      xv[i].w = norm_pair<XT>(xv[i].w, gv[i].w, r);
+      if (xn_out && e == 0) *(u32x4*)(xn_out + 8 * (lane + 64 * i)) = xv[i];
+    }
+  }
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    a = Half<XT>::dot2(wv[i].x, xv[i].x, a);
+    a = Half<XT>::dot2(wv[i].y, xv[i].y, a);
+    a = Half<XT>::dot2(wv[i].z, xv[i].z, a);
+    a = Half<XT>::dot2(wv[i].w, xv[i].w, a);
+  }
+  a = group_sum<64>(a);
+  if (lane == 0) logits[e] = Half<XT>::from_f32(a);
+}
+
 // Logit of expert row e from x (H halves): with NORM, x = RMSNorm(x; nw, eps) first
 // (the wave writes the normalised row to xn_out when e == 0).  Lane l owns words
 // l + 64 i, i < H / 512 (k_router_m1's threads l, l + 64, ..., same partial sums in
@@ -53,30 +89,35 @@ __device__ __forceinline__ void router_wave(const uint16_t* x, const uint16_t* _
       asm volatile("" ::: "memory");
     }
   }
-  if constexpr (NORM) {
-    float ws[4] = {0.f, 0.f, 0.f, 0.f};
+  router_finish<XT, NORM, H>(xv, gv, wv, e, eps, xn_out, logits);
+}
+
+// The routing-weighted sum that completes a decode layer whose experts left one
+// output row per slot (k_ct_moe_m1x):
+//   h = residual + sum_k w[k] y[k],  in fp32 in slot order, rounded once,
+// for the 8 values of one 16-byte word of each row: the arithmetic of the single-launch
+// combine (k_ct_moe_m1's down workgroups), so the result is equal bit for bit.
+template <int XT, int KC>
+__device__ __forceinline__ u32x4 slot_sum8(u32x4 res, const u32x4 (&y)[KC], const float (&w)[KC]) {
+  const u32 rw[4] = {res.x, res.y, res.z, res.w};
+  u32 o[4];
 #pragma unroll
-    for (int i = 0; i < NR; ++i) ws[i] = group_sum<64>(sumsq8<XT>(xv[i]));  // wave i's sum
-    const float r = 1.0f / sqrtf(((ws[0] + ws[1]) + (ws[2] + ws[3])) / (float)H + eps);
+  for (int q = 0; q < 4; ++q) {
+    u32 pair = 0;
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      xv[i].x = norm_pair<XT>(xv[i].x, gv[i].x, r);
-      xv[i].y = norm_pair<XT>(xv[i].y, gv[i].y, r);
-      xv[i].z = norm_pair<XT>(xv[i].z, gv[i].z, r);
-      xv[i].w = norm_pair<XT>(xv[i].w, gv[i].w, r);
-      if (xn_out && e == 0) *(u32x4*)(xn_out + 8 * (lane + 64 * i)) = xv[i];
+    for (int h = 0; h < 2; ++h) {
+      float f = 0.f;
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const u32 yw[4] = {y[k].x, y[k].y, y[k].z, y[k].w};
+        f = __builtin_fmaf(w[k], Half<XT>::to_f32((uint16_t)(yw[q] >> (16 * h))), f);
+      }
+      const float v = Half<XT>::to_f32((uint16_t)(rw[q] >> (16 * h))) + f;
+      pair |= (u32)Half<XT>::from_f32(v) << (16 * h);
     }
+    o[q] = pair;
   }
-  float a = 0.f;
-#pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    a = Half<XT>::dot2(wv[i].x, xv[i].x, a);
-    a = Half<XT>::dot2(wv[i].y, xv[i].y, a);
-    a = Half<XT>::dot2(wv[i].z, xv[i].z, a);
-    a = Half<XT>::dot2(wv[i].w, xv[i].w, a);
-  }
-  a = group_sum<64>(a);
-  if (lane == 0) logits[e] = Half<XT>::from_f32(a);
+  return u32x4{o[0], o[1], o[2], o[3]};
 }
 
 }  // namespace i4
