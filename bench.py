@@ -17,7 +17,7 @@ three layers):
   beyond the 256 MB Infinity Cache.
 
 Printed: one JSON line with value = us per layer (stack time / 24 for the faster of
-the two ways to run a token -- one C call enqueueing the stack's 48 launches, or a
+the two ways to run a token -- one C call enqueueing the stack's 49 launches, or a
 hipGraph replay, which also copies the token's input into the captured buffer --
 both reported, median and p99 of that mode's per-token times beside them), plus the
 roofline of the dominant
@@ -53,12 +53,14 @@ B_GATE_UP_EXPERT = 2 * (H * I // 2 + (H // G) * I * 2 + (H // G) * (I // 8) * 4)
 B_DOWN_EXPERT = I * H // 2 + (I // G) * H * 2 + (I // G) * (H // 8) * 4            # 817,152
 B_ROUTER = E * H * 2
 B_LAYER = TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + B_ROUTER + 2 * H * 2        # 20,144,128
-# the decode experts launch: 8 experts' gate/up and down weights, the normalised input
-# and the residual in, the activations out and back in, the layer output out
-B_EXPERTS_LAUNCH = TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + 3 * H * 2 + 2 * TOPK * I * 2
+# the decode experts launch of the stack (k_ct_moe_m1x): 8 experts' gate/up and down
+# weights, the normalised input in, the activations out and back in, the 8 slot output
+# rows out (their routing-weighted sum and the residual are the next launch's)
+B_EXPERTS_LAUNCH = (TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + H * 2 + 2 * TOPK * I * 2
+                    + TOPK * H * 2)                                                  # 19,673,088
 # HBM bytes per decode experts launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (calibrated against a device copy; summary under profiles/)
-EXPERTS_TRAFFIC_BYTES = 21_166_930
+EXPERTS_TRAFFIC_BYTES = 20_083_701
 
 
 def log(msg: str) -> None:
@@ -133,57 +135,55 @@ def gpu_backlog(torch, dev, ms=20.0):
 
 
 def time_experts(pkg, torch, dev, mods, hs, rounds):
-    """HIP-event timing of the dominant kernel, k_ct_moe_m1 (top-8 routing, gate/up, SiLU,
-    down, routing-weighted combine and residual of the 8 experts in one launch).  It runs
-    behind its router launch inside one i4_moe_forward call, so it is timed as the
-    difference of two back-to-back loops over the 24 layers on the same stream, each
-    between one pair of events behind a queued backlog: whole decode layers
-    (i4_moe_forward on each layer's own input) and the router launches alone
-    (i4_router_logits, same inputs).  Returns (experts us, layer us, router us) per launch."""
-    lb = pkg.lib()
-    from qwen3_omni_duplex_amd import _lib, ops
+    """HIP-event timing of the dominant kernel, k_ct_moe_m1x: the experts launch of the
+    stack's decode layer (top-8 routing, gate/up, SiLU and down of the 8 experts, each slot on
+    its own XCD, slot output rows out), on the stream it is launched on.  Every layer's
+    router launch (i4_moe_route_sum on the layer's own input) runs first, untimed; a pair of
+    events brackets each experts launch (i4_moe_experts_x) behind it, over `rounds` passes
+    of the 24 layers queued behind a backlog.  Also returned: the same loop's layer time
+    (router + experts, one pair of events around all of it) and the router launches alone.
+    Returns (experts us, layer us, router us) per launch."""
+    from qwen3_omni_duplex_amd import ops
 
     stream = torch.cuda.current_stream(dev)
-    s_ptr = stream.cuda_stream
     n = len(mods)
-    mws = [ops.moe_weights_c(*m.stack_entry()[:5]) for m in mods]
-    nbytes = lb.i4_moe_workspace_bytes(1, H, I, E, TOPK)
-    wbuf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    outs = [torch.empty(1, H, dtype=torch.float16, device=dev) for _ in mods]
-    xn = torch.empty(1, H, dtype=torch.float16, device=dev)
-    lg = torch.empty(1, E, dtype=torch.float16, device=dev)
+    ws = pkg.Workspace()
+    pieces = [ops.StackLayerX(m.stack_entry(), TOPK, torch.float16, workspace=ws) for m in mods]
+    ypart = torch.empty(TOPK, H, dtype=torch.float16, device=dev)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
 
-    def layer(li):
-        rc = lb.i4_moe_forward(hs[li].data_ptr(), _lib.F16, 1, ctypes.byref(mws[li]), TOPK, 1,
-                               None, hs[li].data_ptr(), outs[li].data_ptr(), None, None,
-                               wbuf.data_ptr(), nbytes, s_ptr)
-        if rc:
-            raise RuntimeError(lb.i4_strerror(rc).decode())
-
-    def router(li):
-        m = mods[li]
-        rc = lb.i4_router_logits(hs[li].data_ptr(), _lib.F16, 1, H, m.router_w.data_ptr(), E,
-                                 m.norm_weight.data_ptr(), float(m.norm_eps), xn.data_ptr(),
-                                 lg.data_ptr(), s_ptr)
-        if rc:
-            raise RuntimeError(lb.i4_strerror(rc).decode())
-
-    def loop(fn):
+    def loop(experts, per_launch=None):
         for li in range(n):  # warm
-            fn(li)
+            pieces[li].route(hs[li], reset_status=li == 0)
+            if experts:
+                pieces[li].experts(hs[li], ypart)
         torch.cuda.synchronize()
         gpu_backlog(torch, dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0, e1 = ev(), ev()
         e0.record(stream)
         for _ in range(rounds):
             for li in range(n):
-                fn(li)
+                pieces[li].route(hs[li])
+                if experts:
+                    if per_launch is not None:
+                        a, b = ev(), ev()
+                        a.record(stream)
+                        pieces[li].experts(hs[li], ypart)
+                        b.record(stream)
+                        per_launch.append((a, b))
+                    else:
+                        pieces[li].experts(hs[li], ypart)
         e1.record(stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (n * rounds)
 
-    us_layer, us_router = loop(layer), loop(router)
-    return us_layer - us_router, us_layer, us_router
+    us_layer, us_router = loop(True), loop(False)
+    pairs = []
+    loop(True, pairs)
+    us_experts = sum(a.elapsed_time(b) for a, b in pairs) * 1e3 / len(pairs)
+    if ops.moe_status(ws, 1, H, I, E, TOPK) != 0:
+        raise RuntimeError("a decode wait of the experts launch gave up")
+    return us_experts, us_layer, us_router
 
 
 def awq_gemv_bytes(K, N):
@@ -665,7 +665,7 @@ def main() -> int:
     layers = [m.stack_entry() for m in mods]
     ws = pkg.Workspace()
 
-    # ---- eager: one C call per token (the stack's 48 launches)
+    # ---- eager: one C call per token (the stack's 2 launches per layer and a last one)
     lb = pkg.lib()
     from qwen3_omni_duplex_amd import _lib, ops
 
@@ -686,7 +686,7 @@ def main() -> int:
     ms_eager, wall_eager = time_stack(torch, eager_step, args.steps, args.warmup, per_eager)
     log(f"eager: {ms_eager:.3f} ms/token ({ms_eager * 1e3 / args.layers:.2f} us/layer)")
 
-    # ---- hipGraph: the 96 launches of one token captured once, replayed per token
+    # ---- hipGraph: the 49 launches of one token captured once, replayed per token
     ms_graph = None
     if not args.eager:
         static_x = xs[0].clone()
@@ -720,7 +720,7 @@ def main() -> int:
         ms, mode = ms_graph, "hipGraph replay of the stack (input copied into its buffer)"
         per_token = per_graph
     else:
-        ms, mode = ms_eager, "one i4_moe_stack_forward call per token (48 launches)"
+        ms, mode = ms_eager, "one i4_moe_stack_forward call per token (49 launches)"
         per_token = per_eager
     us_layer = ms * 1e3 / args.layers
 
@@ -733,8 +733,8 @@ def main() -> int:
     torch.cuda.synchronize()
     k_us, k_layer, k_router = time_experts(pkg, torch, dev, mods, hs, args.kernel_rounds)
     achieved = B_EXPERTS_LAUNCH / (k_us * 1e-6) / 1e9
-    log(f"experts kernel: {k_us:.2f} us/launch (layer {k_layer:.2f} - router {k_router:.2f}, "
-        f"back-to-back) -> {achieved:.0f} GB/s")
+    log(f"experts kernel: {k_us:.2f} us/launch (events around each launch; layer {k_layer:.2f}, "
+        f"router alone {k_router:.2f}, back-to-back) -> {achieved:.0f} GB/s")
 
     # ---- other workloads of the same layer: M=32 (router from weights) and M=512 prefill
     # with Zipf(1.1)-skewed logits (MFMA tiles for hot experts), rotating over the layers
@@ -841,12 +841,13 @@ def main() -> int:
         "layer_GBps": round(B_LAYER / (us_layer * 1e-6) / 1e9, 1),
         "layer_hbm_frac": round(B_LAYER / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": "k_ct_moe_m1 (decode top-8 routing + gate/up + SiLU + down + combine, "
-                      "8 experts, one launch)",
+            "kernel": "k_ct_moe_m1x (decode top-8 routing + gate/up + SiLU + down of the 8 "
+                      "experts, one launch, each slot on its own XCD)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": EXPERTS_TRAFFIC_BYTES,
             "bytes_per_launch": B_EXPERTS_LAUNCH, "us_per_launch": round(k_us, 3),
-            "timing": "layer launches minus router launches, back to back over the 24 layers",
+            "timing": "HIP events around each experts launch, behind its router launch, over "
+                      "the 24 layers",
             "us_per_layer_launches": round(k_layer, 3), "us_per_router_launch": round(k_router, 3),
         },
         "cpu_baseline": cpu,

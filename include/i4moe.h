@@ -67,7 +67,7 @@
 extern "C" {
 #endif
 
-#define I4_ABI_VERSION 7
+#define I4_ABI_VERSION 8
 
 /* status codes */
 #define I4_OK               0
@@ -302,12 +302,52 @@ int    i4_moe_down_combine(const void* act, int x_dtype, const i4_qweight* down,
 
 /* The Thinker[0:24] MoE stack of src/duplex/streaming/clock.py:168-171 with
  * only the MoE blocks and residual adds kept: h <- h + moe_l(h) for
- * l < n_layers.  x and out are [T][H]; x is not modified. */
+ * l < n_layers.  x and out are [T][H]; x is not modified.  At T = 1 with top-8
+ * blocks of CT experts and H = 1024 or 2048 every layer runs the XCD-local
+ * pair of launches below (i4_moe_route_sum, i4_moe_experts_x; i4_moe_sum after
+ * the last layer), otherwise i4_moe_forward per layer; both give the same
+ * result bit for bit. */
 int    i4_moe_stack_forward(const void* x, int x_dtype, int T,
                             const i4_moe_weights* layers, int n_layers, int topk,
                             int renorm, void* out, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 size_t i4_moe_stack_workspace_bytes(int T, int H, int I, int E, int topk);
+
+/* The launches of one decode layer (T = 1) of i4_moe_stack_forward on an MI355X,
+ * the pieces of FusedPackedMoE.forward's Triton branch (src/duplex/streaming/
+ * fused_packed_moe.py:222-263) as that stack runs them.  The blocks: top-8 (one
+ * slot per XCD), CT experts, router_w present, H = 1024 or 2048, the shapes of
+ * i4_moe_forward's single-launch decode layer.  Slot j's gate_up and down
+ * workgroups all run on XCD j; the down workgroups take the slot's activations
+ * over through that XCD's L2 and write the slot's output rows, ypart[j][H]
+ * (x_dtype, 16-byte aligned), rounded to x_dtype as the reference rounds each
+ * expert's output (:262).  The routing-weighted sum is left to the next launch:
+ *   i4_moe_route_sum: the router launch of a layer (logits, RMSNorm, as
+ *     i4_moe_forward's) on res [H] when ypart is NULL; otherwise it first completes
+ *     the previous layer, h = res + sum_j w_j ypart[j] in fp32 in slot order,
+ *     rounded once (the arithmetic of i4_moe_forward's combine), writes h to h_out
+ *     and routes h.  w_j are the weights the previous i4_moe_experts_x call left in
+ *     the workspace.  reset_status = 1 clears the status word.
+ *   i4_moe_experts_x: the experts launch of that layer from the logits in the
+ *     workspace (every workgroup ranks them itself); it reads RMSNorm(h) from the
+ *     workspace, or h when the block has no norm.  down_only = 1 launches the down
+ *     workgroups alone: they wait for activations nobody writes, which the bound
+ *     max_polls turns into NaN rows and I4_ERR_HANDOFF in the status word (a test
+ *     of the bounded wait from the host; the stack passes 2^20).
+ *   i4_moe_sum: out = res + sum_j w_j ypart[j], the last layer's completion.
+ * The workspace is i4_moe_forward's T = 1 workspace (i4_moe_workspace_bytes(1, H,
+ * I, E, 8); the status word at i4_moe_status_offset); calls sharing it run in
+ * stream order and must not overlap. */
+int    i4_moe_route_sum(const void* res, int x_dtype, const void* ypart,
+                        const i4_moe_weights* weights, int topk, void* h_out,
+                        int reset_status, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+int    i4_moe_experts_x(const void* h, int x_dtype, const i4_moe_weights* weights, int topk,
+                        int renorm, void* ypart, int max_polls, int down_only,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream);
+int    i4_moe_sum(const void* res, int x_dtype, const void* ypart,
+                  const i4_moe_weights* weights, int topk, void* out,
+                  const void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Qwen3OmniMoeThinkerTextRMSNorm.forward (transformers modeling_qwen3_omni_moe.py:
  * 1388-1393, 5.15; the Thinker decoder layer's input_layernorm, which the clock

@@ -29,7 +29,7 @@ from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_down_wait
                   route, router_logits, unpack4, unpack_nibbles, Workspace, rmsnorm,
                   rmsnorm_linear, attn_decode, attn_decode_o, thinker_layer_decode,
                   thinker_layer_fits, thinker_layer_c, thinker_decode_step, dmoe_forward,
-                  dmoe_status, dmoe_down_wait)
+                  dmoe_status, dmoe_down_wait, StackLayerX)
 from .weights import QWeight, repack_awq_to_ct, repack_tile
 
 lib = _lib.lib
@@ -47,5 +47,5 @@ __all__ = [
     "thinker_decode_step",
     "ThinkerAttention", "ThinkerDecoderLayer", "ThinkerDecoder", "rope_inv_freq",
     "FusedMoE", "fuse_moe_blocks", "quantize_q8", "dmoe_forward", "dmoe_status",
-    "dmoe_down_wait",
+    "dmoe_down_wait", "StackLayerX",
 ]

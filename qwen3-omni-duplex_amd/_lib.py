@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libi4moe.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # element types and layouts (include/i4moe.h)
 F32, F16, BF16 = 0, 1, 2
@@ -113,6 +113,12 @@ SIGNATURES = {
     "i4_moe_stack_forward": (c_int, [c_void_p, c_int, c_int, POINTER(MoeWeightsC), c_int, c_int,
                                      c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "i4_moe_stack_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "i4_moe_route_sum": (c_int, [c_void_p, c_int, c_void_p, POINTER(MoeWeightsC), c_int, c_void_p,
+                                 c_int, c_void_p, c_size_t, c_void_p]),
+    "i4_moe_experts_x": (c_int, [c_void_p, c_int, POINTER(MoeWeightsC), c_int, c_int, c_void_p,
+                                 c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "i4_moe_sum": (c_int, [c_void_p, c_int, c_void_p, POINTER(MoeWeightsC), c_int, c_void_p,
+                           c_void_p, c_size_t, c_void_p]),
     "i4_rmsnorm_linear": (c_int, [c_void_p, c_int, c_int, c_void_p, ctypes.c_float,
                                   POINTER(QWeightC), c_void_p, c_void_p, c_int, c_void_p]),
     "i4_rmsnorm": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, ctypes.c_float, c_void_p,

@@ -294,7 +294,8 @@ struct MoeOps {
                    hipStream_t);
   int (*mfma_mixed)(bool, int, int, const void*, int, int, const int4*, const int*, const int4*,
                     const int*, const int32_t*, const TW&, int, void*, hipStream_t);
-  int (*moe_m1x_ct)(const GateUpArgs&, const TW&, const TW&, void*, int32_t*, int, hipStream_t);
+  int (*moe_m1x_ct)(const GateUpArgs&, const TW&, const TW&, void*, int32_t*, int, bool,
+                    hipStream_t);
 };
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
@@ -572,6 +573,49 @@ bool stack_xcd_local(const i4_moe_weights* layers, int n, int xt, int topk) {
   return true;
 }
 
+// One validated block of the XCD-local decode path.
+struct XBlock {
+  i4_qweight gu, dn;
+  MoeOps ops;
+  int H, I, E;
+};
+int xblock(const i4_moe_weights* mw, int xt, int topk, XBlock* b) {
+  i4_qweight tg, td;
+  int rc = check_moe(mw, xt, 1, topk, &b->gu, &b->dn, &tg, &td);
+  if (rc) return rc;
+  if (!mw->router_w) return I4_ERR_NULL;
+  if (b->gu.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  b->H = b->gu.K;
+  b->I = b->dn.K;
+  b->E = b->gu.E;
+  if ((b->H != 1024 && b->H != 2048) || !moe_m1x_ct_fits(topk, b->H, b->I)) return I4_ERR_SHAPE;
+  if (((uintptr_t)mw->router_w & 15) || ((uintptr_t)mw->norm_w & 15)) return I4_ERR_ALIGN;
+  if (!pick_ops(xt, b->gu.scale_dtype, b->dn.scale_dtype, &b->ops)) return I4_ERR_DTYPE;
+  return I4_OK;
+}
+
+// the router launch of a layer: on res itself (ypart == nullptr, the first layer), or
+// completing the previous layer first, h = res + sum_j w_j ypart[j] into h_out
+int x_route(const void* res, int xt, const void* ypart, const i4_moe_weights* mw,
+            const XBlock& b, int topk, void* h_out, const MoeWs& ws, bool reset, hipStream_t s) {
+  uint16_t* xn = mw->norm_w ? ws.xn : nullptr;
+  int32_t* st = reset ? ws.status : nullptr;
+  if (!ypart)
+    return i4_launch_router_logits(res, xt, 1, b.H, mw->router_w, b.E, mw->norm_w, mw->norm_eps,
+                                   xn, ws.logits, s, ws.act, topk * b.I / 8, st);
+  return i4_launch_router_sum(res, ypart, ws.w, topk, h_out, xt, b.H, mw->router_w, b.E,
+                              mw->norm_w, mw->norm_eps, xn, ws.logits, s, ws.act,
+                              topk * b.I / 8, st);
+}
+
+// the experts launch of a layer: h is the routed row (read when the block has no norm)
+int x_experts(const void* h, const i4_moe_weights* mw, const XBlock& b, int topk, int renorm,
+              void* ypart, const MoeWs& ws, int max_polls, bool down_only, hipStream_t s) {
+  const void* x = mw->norm_w ? (const void*)ws.xn : h;
+  const GateUpArgs a{true, topk, topk, b.E, renorm, x, ws.sel, ws.logits, ws.w, ws.act, nullptr};
+  return b.ops.moe_m1x_ct(a, to_tw(b.gu), to_tw(b.dn), ypart, ws.status, max_polls, down_only, s);
+}
+
 // T = 1 stack on the XCD-local experts launch.  Layer l's router launch first
 // completes layer l - 1 (h_l = h_{l-1} + sum_j w_j y_j, written to hb[l % 2]) and
 // routes h_l; the experts launch leaves its slot outputs in ypart and its routing
@@ -583,27 +627,14 @@ int stack_m1x(const void* x, int xt, const i4_moe_weights* layers, int n, int to
               hipStream_t s) {
   const void* h = x;  // h_l, the input of layer l
   for (int l = 0; l < n; ++l) {
-    const i4_moe_weights* mw = &layers[l];
-    i4_qweight gu, dn, tg, td;
-    int rc = check_moe(mw, xt, 1, topk, &gu, &dn, &tg, &td);
+    XBlock b;
+    int rc = xblock(&layers[l], xt, topk, &b);
     if (rc) return rc;
-    const int H = gu.K, I = dn.K, E = gu.E;
-    MoeOps ops;
-    if (!pick_ops(xt, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
-    uint16_t* xn = mw->norm_w ? ws.xn : nullptr;
-    if (l == 0) {
-      rc = i4_launch_router_logits(h, xt, 1, H, mw->router_w, E, mw->norm_w, mw->norm_eps, xn,
-                                   ws.logits, s, ws.act, topk * I / 8, ws.status);
-    } else {
-      uint16_t* hl = (l % 2) ? hb1 : hb0;
-      rc = i4_launch_router_sum(h, ypart, ws.w, topk, hl, xt, H, mw->router_w, E, mw->norm_w,
-                                mw->norm_eps, xn, ws.logits, s, ws.act, topk * I / 8, nullptr);
-      h = hl;
-    }
+    uint16_t* hl = (l % 2) ? hb1 : hb0;
+    rc = x_route(h, xt, l ? ypart : nullptr, &layers[l], b, topk, hl, ws, l == 0, s);
     if (rc) return rc;
-    const GateUpArgs a{true, topk, topk, E, renorm, xn ? (const void*)xn : h, ws.sel, ws.logits,
-                       ws.w, ws.act, nullptr};
-    rc = ops.moe_m1x_ct(a, to_tw(gu), to_tw(dn), ypart, ws.status, kHandoffPolls, s);
+    if (l) h = hl;
+    rc = x_experts(h, &layers[l], b, topk, renorm, ypart, ws, kHandoffPolls, false, s);
     if (rc) return rc;
   }
   return i4_launch_moe_sum(h, ypart, ws.w, topk, xt, layers[0].gate_up.K, out, s);
@@ -747,6 +778,55 @@ int i4_moe_stack_forward(const void* x, int x_dtype, int T, const i4_moe_weights
     h = dst;
   }
   return I4_OK;
+}
+
+
+int i4_moe_route_sum(const void* res, int x_dtype, const void* ypart,
+                     const i4_moe_weights* weights, int topk, void* h_out, int reset_status,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  XBlock b;
+  int rc = xblock(weights, x_dtype, topk, &b);
+  if (rc) return rc;
+  if (!res || (ypart && !h_out)) return I4_ERR_NULL;
+  if (((uintptr_t)res & 15) || ((uintptr_t)ypart & 15) || ((uintptr_t)h_out & 15))
+    return I4_ERR_ALIGN;
+  if (!workspace || workspace_bytes < carve(nullptr, 1, b.H, b.I, b.E, topk).bytes)
+    return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  const MoeWs ws = carve(workspace, 1, b.H, b.I, b.E, topk);
+  return x_route(res, x_dtype, ypart, weights, b, topk, h_out, ws, reset_status != 0, stream);
+}
+
+int i4_moe_experts_x(const void* h, int x_dtype, const i4_moe_weights* weights, int topk,
+                     int renorm, void* ypart, int max_polls, int down_only, void* workspace,
+                     size_t workspace_bytes, hipStream_t stream) {
+  XBlock b;
+  int rc = xblock(weights, x_dtype, topk, &b);
+  if (rc) return rc;
+  if (!ypart || (!weights->norm_w && !h)) return I4_ERR_NULL;
+  if (((uintptr_t)ypart & 15) || ((uintptr_t)h & 15)) return I4_ERR_ALIGN;
+  if (max_polls < 0) return I4_ERR_SHAPE;
+  if (!workspace || workspace_bytes < carve(nullptr, 1, b.H, b.I, b.E, topk).bytes)
+    return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  const MoeWs ws = carve(workspace, 1, b.H, b.I, b.E, topk);
+  return x_experts(h, weights, b, topk, renorm, ypart, ws, max_polls, down_only != 0, stream);
+}
+
+int i4_moe_sum(const void* res, int x_dtype, const void* ypart, const i4_moe_weights* weights,
+               int topk, void* out, const void* workspace, size_t workspace_bytes,
+               hipStream_t stream) {
+  XBlock b;
+  int rc = xblock(weights, x_dtype, topk, &b);
+  if (rc) return rc;
+  if (!res || !ypart || !out) return I4_ERR_NULL;
+  if (((uintptr_t)res & 15) || ((uintptr_t)ypart & 15) || ((uintptr_t)out & 15))
+    return I4_ERR_ALIGN;
+  if (!workspace || workspace_bytes < carve(nullptr, 1, b.H, b.I, b.E, topk).bytes)
+    return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  const MoeWs ws = carve(const_cast<void*>(workspace), 1, b.H, b.I, b.E, topk);
+  return i4_launch_moe_sum(res, ypart, ws.w, topk, x_dtype, b.H, out, stream);
 }
 
 }  // extern "C"

@@ -658,7 +658,7 @@ bool moe_m1x_ct_fits(int topk, int H, int I) {
 
 template <int XT, int ST>
 int launch_moe_m1x_ct(const GateUpArgs& ga, const TW& tgu, const TW& tdn, void* ypart,
-                      int32_t* status, int max_polls, hipStream_t s) {
+                      int32_t* status, int max_polls, bool down_only, hipStream_t s) {
   MoeM1xArgs a;
   a.gu = to_qw(tgu);
   a.dn = to_qw(tdn);
@@ -677,7 +677,7 @@ int launch_moe_m1x_ct(const GateUpArgs& ga, const TW& tgu, const TW& tdn, void* 
   a.status = status;
   a.max_polls = max_polls;
   const int rpw = WG / LG;
-  a.n_gate = ((I + rpw - 1) / rpw) * XCDS;
+  a.n_gate = down_only ? 0 : ((I + rpw - 1) / rpw) * XCDS;  // 0: the down workgroups alone
   constexpr int RWD = 64;  // (WG / LD) * (LD / 4) output rows per down workgroup
   const int n_down = ((H + RWD - 1) / RWD) * XCDS;
   const size_t lds_d = (size_t)I * 2 + (size_t)(I / 32) * 8;
@@ -702,7 +702,7 @@ int launch_moe_m1x_ct(const GateUpArgs& ga, const TW& tgu, const TW& tdn, void* 
   template int launch_moe_m1_ct<XT_, ST_>(const GateUpArgs&, const TW*, const TW&, const void*, \
                                           void*, int32_t*, int, hipStream_t);                  \
   template int launch_moe_m1x_ct<XT_, ST_>(const GateUpArgs&, const TW&, const TW&, void*,      \
-                                           int32_t*, int, hipStream_t);
+                                           int32_t*, int, bool, hipStream_t);
 I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
 I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)
 #undef I4_INST

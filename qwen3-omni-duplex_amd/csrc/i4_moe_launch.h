@@ -61,10 +61,11 @@ int launch_moe_m1_ct(const GateUpArgs& a, const TW* gate_up, const TW& down,
 // output rows ypart[j][H] (activation dtype); the routing-weighted sum and the
 // residual are left to the next launch (i4_launch_router_sum / i4_launch_moe_sum,
 // with the weights block 0 writes to a.wts).  act must hold the pending pattern.
+// down_only launches the down workgroups alone (act is then produced elsewhere).
 bool moe_m1x_ct_fits(int topk, int H, int I);
 template <int XT, int ST>
 int launch_moe_m1x_ct(const GateUpArgs& a, const TW& gate_up, const TW& down, void* ypart,
-                      int32_t* status, int max_polls, hipStream_t s);
+                      int32_t* status, int max_polls, bool down_only, hipStream_t s);
 
 // The T = 1 MoE block of a decoder layer whose router runs in an earlier launch
 // (i4_thinker_layer_decode, i4_attn.hip): that launch writes the logits and the

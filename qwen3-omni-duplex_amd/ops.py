@@ -427,6 +427,42 @@ def moe_stack(x: torch.Tensor, layers: list[tuple], top_k: int,
     return out.view(shape)
 
 
+class StackLayerX:
+    """The launches of one decode layer of the XCD-local stack path (i4_moe_route_sum,
+    i4_moe_experts_x, i4_moe_sum) on one block, given as a moe_stack layer tuple.  The
+    workspace is the block's T = 1 MoE workspace; slot outputs go to `ypart` [8, H]."""
+
+    def __init__(self, layer: tuple, top_k: int, dtype: torch.dtype,
+                 norm_topk_prob: bool = True, workspace: Workspace | None = None):
+        self.mw = moe_weights_c(*layer)
+        gu, dn = layer[0], layer[1]
+        self.top_k, self.renorm, self.xt = top_k, int(norm_topk_prob), _lib.half_code(dtype)
+        self.H = gu.K
+        dev = gu.packed.device
+        self.dev = dev
+        nbytes = _lib.lib().i4_moe_workspace_bytes(1, gu.K, dn.K, gu.E, top_k)
+        self.ws = (workspace or Workspace()).get(nbytes, dev)
+
+    def route(self, res: torch.Tensor, ypart: torch.Tensor | None = None,
+              h_out: torch.Tensor | None = None, reset_status: bool = False) -> None:
+        _lib.check(_lib.lib().i4_moe_route_sum(
+            res.data_ptr(), self.xt, _lib.ptr(ypart), ctypes.byref(self.mw), self.top_k,
+            _lib.ptr(h_out), int(reset_status), self.ws.data_ptr(), self.ws.numel(),
+            _lib.stream(self.dev)))
+
+    def experts(self, h: torch.Tensor | None, ypart: torch.Tensor, max_polls: int = 1 << 20,
+                down_only: bool = False) -> None:
+        _lib.check(_lib.lib().i4_moe_experts_x(
+            _lib.ptr(h), self.xt, ctypes.byref(self.mw), self.top_k, self.renorm,
+            ypart.data_ptr(), int(max_polls), int(down_only), self.ws.data_ptr(),
+            self.ws.numel(), _lib.stream(self.dev)))
+
+    def sum(self, res: torch.Tensor, ypart: torch.Tensor, out: torch.Tensor) -> None:
+        _lib.check(_lib.lib().i4_moe_sum(
+            res.data_ptr(), self.xt, ypart.data_ptr(), ctypes.byref(self.mw), self.top_k,
+            out.data_ptr(), self.ws.data_ptr(), self.ws.numel(), _lib.stream(self.dev)))
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """Qwen3OmniMoeThinkerTextRMSNorm over the last dim (i4_rmsnorm), in x.dtype."""
     dev = _lib.require_device(x, weight)

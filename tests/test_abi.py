@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported_and_bound(pkg):
 
 def test_version_and_errors(pkg):
     lib = pkg.lib()
-    assert lib.i4_abi_version() == 7
+    assert lib.i4_abi_version() == 8
     codes = {0: b"ok", -1: b"NULL", -2: b"dimension", -3: b"element type", -4: b"aligned",
              -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride",
              -10: b"gave up waiting", -11: b"static buffer"}

@@ -259,3 +259,72 @@ def test_moe_status_word_reads_ok_after_calls(pkg, dev):
     ws2 = pkg.Workspace()
     pkg.moe_stack(x, [moe.stack_entry()] * 3, K8, workspace=ws2)
     assert pkg.ops.moe_status(ws2, 1, H, I, 32, K8) == 0
+
+
+def test_stack_pieces_equal_the_stack(pkg, dev):
+    """The XCD-local decode path run launch by launch through the C ABI (i4_moe_route_sum,
+    i4_moe_experts_x, i4_moe_sum) equals i4_moe_stack_forward and the module loop bit for
+    bit, the layer outputs written by the router launches included."""
+    rng = np.random.default_rng(108)
+    mods = []
+    for _ in range(3):
+        m, _, _, _ = _awq_moe(pkg, dev, rng, E=32)
+        nw = rng.uniform(0.5, 1.5, H).astype(np.float16)
+        m.register_buffer("norm_weight", t_(nw, dev), persistent=False)
+        m.norm_eps = 1e-6
+        mods.append(m)
+    layers = [mods[i % 3].stack_entry() for i in range(5)]
+    x = t_(make_x(rng, (1, H), "f16"), dev)
+    ws = pkg.Workspace()
+    pieces = [pkg.StackLayerX(layer, K8, torch.float16, workspace=ws) for layer in layers]
+    ypart = torch.empty(K8, H, dtype=torch.float16, device=dev)
+    hbuf = [torch.empty(1, H, dtype=torch.float16, device=dev) for _ in range(2)]
+    h, hs = x, []
+    for li, p in enumerate(pieces):
+        if li == 0:
+            p.route(h, reset_status=True)
+        else:
+            p.route(h, ypart, hbuf[li % 2])
+            h = hbuf[li % 2]
+            hs.append(h.clone())
+        p.experts(h, ypart)
+    out = torch.empty_like(x)
+    pieces[-1].sum(h, ypart, out)
+    stack = pkg.moe_stack(x, layers, K8)
+    loop, ref_hs = x, []
+    for li in range(5):
+        loop = mods[li % 3](loop, residual=loop)
+        ref_hs.append(loop)
+    torch.cuda.synchronize()
+    assert torch.equal(out, stack) and torch.equal(out, loop)
+    for got, want in zip(hs, ref_hs[:-1]):
+        assert torch.equal(got, want)
+    assert pkg.ops.moe_status(ws, 1, H, I, 32, K8) == 0
+
+
+def test_stack_experts_wait_gives_up_visibly(pkg, dev):
+    """The down workgroups of the XCD-local experts launch run alone, with their bound on the
+    wait lowered from the host: the activations stay pending, so they give up, write NaN slot
+    rows and report I4_ERR_HANDOFF, and every kernel exits.  The next ordinary layer on the
+    same workspace (its router launch clears the status word) is correct again."""
+    rng = np.random.default_rng(109)
+    m, _, _, _ = _awq_moe(pkg, dev, rng, E=64)
+    layer = m.stack_entry()
+    x = t_(make_x(rng, (1, H), "f16"), dev)
+    ws = pkg.Workspace()
+    p = pkg.StackLayerX(layer, K8, torch.float16, workspace=ws)
+    ypart = torch.zeros(K8, H, dtype=torch.float16, device=dev)
+    for polls in (0, 3):
+        p.route(x, reset_status=True)  # arms the activations with the pending pattern
+        p.experts(x, ypart, max_polls=polls, down_only=True)
+        torch.cuda.synchronize()
+        assert pkg.ops.moe_status(ws, 1, H, I, 64, K8) == -10
+        assert torch.isnan(ypart).all()
+    p.route(x, reset_status=True)
+    p.experts(x, ypart)
+    out = torch.empty_like(x)
+    p.sum(x, ypart, out)
+    want = m(x, residual=x)
+    torch.cuda.synchronize()
+    assert pkg.ops.moe_status(ws, 1, H, I, 64, K8) == 0
+    assert torch.equal(out, want)
