@@ -20,16 +20,17 @@ Printed: one JSON line with value = us per layer (stack time / 24 for the faster
 the two ways to run a token -- one C call enqueueing the stack's 49 launches, or a
 hipGraph replay, which also copies the token's input into the captured buffer --
 both reported, median and p99 of that mode's per-token times beside them), plus the
-roofline of the dominant
-kernel (the decode experts launch: routing, gate/up, SiLU, down and combine of
-the 8 experts) timed with HIP events on the stream it runs on, and a CPU baseline (the reference's CPU expert path restated in
-torch, oracle/cpu_baseline.py) timed on this host.  Extra fields time the same
-layer at M = 32 (router from weights) and M = 512 (Zipf-skewed logits) with
-their realised expert histograms, HBM and MFMA fractions, the dequant-GEMV
-workloads (a 2048 -> 768 GEMV and the four attention projections, individually
-and back to back), the whole Thinker[0:24] decode step around the MoE stack
-(attention with a KV cache at --context positions + MoE per layer,
-thinker_decode_step), and the Talker's 16-bit / int8 MoE blocks (talker_moe).
+roofline of the dominant kernel (the decode experts launch: top-8 routing, gate/up,
+SiLU and down of the 8 experts) timed with HIP events on the stream it runs on, and a
+CPU baseline (the reference's CPU expert path restated in torch,
+oracle/cpu_baseline.py) timed on this host.  Extra fields time the same layer at
+M = 32 (router from weights) and M = 512 (Zipf-skewed logits) with their realised
+expert histograms, HBM and MFMA fractions; count the rows whose GPU top-8 differs
+from the host's exact ranking (routing_agreement); time the dequant-GEMV workloads
+(a 2048 -> 768 GEMV, also through the PackedLinear module, and the four attention
+projections, individually and back to back), the whole Thinker[0:24] decode step
+around the MoE stack (attention with a KV cache at --context positions + MoE per
+layer, thinker_decode_step), and the Talker's 16-bit / int8 MoE blocks (talker_moe).
 """
 from __future__ import annotations
 
@@ -137,52 +138,63 @@ def gpu_backlog(torch, dev, ms=20.0):
 def time_experts(pkg, torch, dev, mods, hs, rounds):
     """HIP-event timing of the dominant kernel, k_ct_moe_m1x: the experts launch of the
     stack's decode layer (top-8 routing, gate/up, SiLU and down of the 8 experts, each slot on
-    its own XCD, slot output rows out), on the stream it is launched on.  Every layer's
-    router launch (i4_moe_route_sum on the layer's own input) runs first, untimed; a pair of
-    events brackets each experts launch (i4_moe_experts_x) behind it, over `rounds` passes
-    of the 24 layers queued behind a backlog.  Also returned: the same loop's layer time
-    (router + experts, one pair of events around all of it) and the router launches alone.
-    Returns (experts us, layer us, router us) per launch."""
+    its own XCD, slot output rows out), on the stream it is launched on.  Each layer has its
+    own workspace, so the 24 router launches (i4_moe_route_sum on each layer's own input) can
+    run first and the 24 experts launches (i4_moe_experts_x) then run back to back between
+    one pair of events; `rounds` such passes behind a queued backlog.  Also returned: router +
+    experts interleaved layer by layer, and the router launches alone (each one pair of
+    events around all passes).  Returns (experts us, layer us, router us) per launch."""
     from qwen3_omni_duplex_amd import ops
 
     stream = torch.cuda.current_stream(dev)
     n = len(mods)
-    ws = pkg.Workspace()
-    pieces = [ops.StackLayerX(m.stack_entry(), TOPK, torch.float16, workspace=ws) for m in mods]
+    pieces = [ops.StackLayerX(m.stack_entry(), TOPK, torch.float16, workspace=pkg.Workspace())
+              for m in mods]
     ypart = torch.empty(TOPK, H, dtype=torch.float16, device=dev)
     ev = lambda: torch.cuda.Event(enable_timing=True)
 
-    def loop(experts, per_launch=None):
-        for li in range(n):  # warm
-            pieces[li].route(hs[li], reset_status=li == 0)
-            if experts:
-                pieces[li].experts(hs[li], ypart)
+    def warm():
+        for li in range(n):
+            pieces[li].route(hs[li], reset_status=True)
+            pieces[li].experts(hs[li], ypart)
         torch.cuda.synchronize()
         gpu_backlog(torch, dev)
+
+    def timed(body):
+        warm()
         e0, e1 = ev(), ev()
         e0.record(stream)
         for _ in range(rounds):
-            for li in range(n):
-                pieces[li].route(hs[li])
-                if experts:
-                    if per_launch is not None:
-                        a, b = ev(), ev()
-                        a.record(stream)
-                        pieces[li].experts(hs[li], ypart)
-                        b.record(stream)
-                        per_launch.append((a, b))
-                    else:
-                        pieces[li].experts(hs[li], ypart)
+            body()
         e1.record(stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (n * rounds)
 
-    us_layer, us_router = loop(True), loop(False)
-    pairs = []
-    loop(True, pairs)
-    us_experts = sum(a.elapsed_time(b) for a, b in pairs) * 1e3 / len(pairs)
-    if ops.moe_status(ws, 1, H, I, E, TOPK) != 0:
-        raise RuntimeError("a decode wait of the experts launch gave up")
+    def interleaved():
+        for li in range(n):
+            pieces[li].route(hs[li])
+            pieces[li].experts(hs[li], ypart)
+
+    def routers():
+        for li in range(n):
+            pieces[li].route(hs[li])
+
+    us_layer, us_router = timed(interleaved), timed(routers)
+    warm()
+    tot = 0.0
+    for _ in range(rounds):
+        routers()
+        e0, e1 = ev(), ev()
+        e0.record(stream)
+        for li in range(n):
+            pieces[li].experts(hs[li], ypart)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        tot += e0.elapsed_time(e1)
+    us_experts = tot * 1e3 / (n * rounds)
+    for p in pieces:
+        if ops.moe_status(p.ws_holder, 1, H, I, E, TOPK) != 0:
+            raise RuntimeError("a decode wait of the experts launch gave up")
     return us_experts, us_layer, us_router
 
 
@@ -397,8 +409,8 @@ def time_gemvs(pkg, torch, dev, replays=20):
             self.x = torch.randn(1, K, device=dev, generator=gen).half()
             self.y = torch.empty(1, N, dtype=torch.float16, device=dev)
             nb = lb.i4_linear_workspace_bytes(ctypes.byref(self.desc["awq"][0]), 1)
-            # AWQ split-K partials start (and stay) pending: every byte 0xFF
-            self.ws = torch.full((max(nb, 256),), 255, dtype=torch.uint8, device=dev)
+            # split-K workspace: its status word starts at 0, no other contents needed
+            self.ws = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev)
 
         def launch(self, layout, i):
             d = self.desc[layout][i]
@@ -424,6 +436,45 @@ def time_gemvs(pkg, torch, dev, replays=20):
         ts = graph_times(torch, lambda: [single.launch(layout, i) for i in range(n1)], replays)
         out[f"single_{layout}"] = stats(ts, n1, nbytes)
         log(f"GEMV 2048->768 ({layout}): {out[f'single_{layout}']['us']:.2f} us")
+    # the same GEMV through the Python module path (PackedLinear.forward -> ops.linear ->
+    # i4_linear, each module with its own kept workspace) on 64 of the copies: eager calls,
+    # host dispatch included, and the same calls captured in a hipGraph (what the module
+    # path enqueues on the device)
+    n_py = 64
+    py = {}
+    for li, layout in enumerate(("awq", "ct")):
+        w = single.keep[li]
+        lins = [pkg.PackedLinear.from_qweight(
+            pkg.QWeight(w.packed[i:i + 1], w.scale[i:i + 1], w.zeros[i:i + 1], w.layout, w.group,
+                        w.N, w.K), repack=False, tile=False) for i in range(n_py)]
+        xp = single.x
+
+        def calls(lins=lins, xp=xp):
+            for m in lins:
+                m(xp)
+
+        for _ in range(3):
+            calls()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(5):
+            calls()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e6 / (5 * n_py)
+        g = stats(graph_times(torch, calls, replays), n_py, nbytes)
+        py[layout] = {"us_eager": round(e0.elapsed_time(e1) * 1e3 / (5 * n_py), 3),
+                      "us_eager_wall": round(wall, 3), "us_graph": g["us"],
+                      "us_graph_p99": g["us_p99"]}
+        del lins
+    py["timing"] = ("PackedLinear.forward on 64 copies, eager (HIP events and wall clock "
+                    "around 5 passes) and as one hipGraph of the 64 calls (mean over replays)")
+    out["python_linear"] = py
+    log("PackedLinear 2048->768: " + ", ".join(
+        f"{k} eager {v['us_eager']:.2f} / graph {v['us_graph']:.2f} us"
+        for k, v in py.items() if k != "timing"))
     del single
     n2 = 64
     projs = {"q": Proj(2048, 4096, n2), "k": Proj(2048, 512, n2), "v": Proj(2048, 512, n2),
@@ -443,7 +494,7 @@ def time_gemvs(pkg, torch, dev, replays=20):
     qkv.x = projs["q"].x
     qkv.y = torch.empty(1, qkv.N, dtype=torch.float16, device=dev)
     nb = lb.i4_linear_workspace_bytes(ctypes.byref(qkv.desc["awq"][0]), 1)
-    qkv.ws = torch.full((max(nb, 256),), 255, dtype=torch.uint8, device=dev)
+    qkv.ws = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev)
     for layout in ("ct", "awq"):
         att = {}
         for name, p in projs.items():
@@ -531,6 +582,36 @@ def routing_stats(sels, per_expert_bytes, extra_bytes):
             "bytes": int(d * per_expert_bytes + extra_bytes)}
 
 
+def routing_agreement(torch, dev, mods, rows1, rows32):
+    """The GPU's top-8 from x against the exact ranking on the host, on the M = 1 decode
+    inputs and M = 32 batches of every layer: the router launch of ops.moe_forward (fp16 x
+    and the layer's fp16 router weight, no norm) against the float64 product rounded once to
+    fp16 and ranked value-descending with ties to the lower id (fused_packed_moe.py:195-197).
+    The GPU accumulates in fp32, so a logit within an ulp of a rounding boundary may round
+    to its neighbour and swap two near-tied experts.  Returns {M1, M32: rows, differ, rate}."""
+    from qwen3_omni_duplex_amd import ops
+
+    ws = ops.Workspace()
+    out = {}
+    for name, batches in (("M1", rows1), ("M32", rows32)):
+        n = bad = 0
+        for m in mods:
+            wr = m.router_w.detach().double().cpu()
+            tiles = dict(gate_up_tile=m.gate_up_tile, down_tile=m.down_tile)
+            for x in batches:
+                _, sel, _ = ops.moe_forward(x, m.gate_up, m.down, TOPK, router_w=m.router_w,
+                                            return_routing=True, workspace=ws, **tiles)
+                lg = (x.double().cpu() @ wr.T).half().double()
+                ref = torch.sort(lg, dim=1, descending=True, stable=True)[1][:, :TOPK]
+                bad += int((sel.long().cpu() != ref).any(dim=1).sum())
+                n += x.shape[0]
+        out[name] = {"rows": n, "differ": bad, "rate": round(bad / n, 5)}
+    out["reference"] = ("float64 x @ router_w.T rounded once to fp16, ranked on the host "
+                        "(value descending, ties to the lower id); a row differs if any of its "
+                        "8 ids, in order, differs")
+    return out
+
+
 def cpu_model_name() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -544,8 +625,8 @@ def cpu_model_name() -> str:
 def cpu_baseline(torch, first, xs, seconds):
     """The reference's CPU paths restated in torch (oracle/cpu_baseline.py), timed on this host
     over bounded samples: the M = 1 MoE layer on all threads (the reported value) and on one
-    thread, the M = 32 layer, and reference_gemv for the single 2048 -> 768 GEMV and the four
-    attention projections back to back.  The weights are layer 0's (MoE) and fresh seeded AWQ
+    thread, the M = 32 layer, 64-token slices of the M = 512 layer, and reference_gemv for
+    the single 2048 -> 768 GEMV and the four attention projections back to back.  The weights are layer 0's (MoE) and fresh seeded AWQ
     tensors of the workload's shapes (GEMVs); `seconds` bounds the whole leg."""
     from oracle import cpu_baseline as cb
 
@@ -555,17 +636,24 @@ def cpu_baseline(torch, first, xs, seconds):
     router = wr.detach().float().cpu()
     x = torch.stack([t.detach().float().cpu().reshape(-1) for t in xs[:64]])
     threads = torch.get_num_threads()
-    med, reps = cb.time_layer(x, router, gate, up, down, seconds=0.35 * seconds, top_k=TOPK,
+    med, reps = cb.time_layer(x, router, gate, up, down, seconds=0.3 * seconds, top_k=TOPK,
                               group=G)
     torch.set_num_threads(1)
     try:
-        med1, reps1 = cb.time_layer(x, router, gate, up, down, seconds=0.15 * seconds, top_k=TOPK,
+        med1, reps1 = cb.time_layer(x, router, gate, up, down, seconds=0.12 * seconds, top_k=TOPK,
                                     group=G)
     finally:
         torch.set_num_threads(threads)
     x32 = [x[i:i + 32] for i in (0, 32)]
     med32, reps32 = cb.time_calls(
-        lambda i: cb.moe_layer(x32[i % 2], router, gate, up, down, TOPK, G), 0.25 * seconds, 2)
+        lambda i: cb.moe_layer(x32[i % 2], router, gate, up, down, TOPK, G), 0.18 * seconds, 2)
+    # M = 512: the reference's CPU path loops over tokens (each dequantises its own 8
+    # experts), so a layer costs 512 tokens' worth; timed on 64-token slices of fresh rows
+    gen512 = torch.Generator().manual_seed(512)
+    x512 = torch.randn(128, H, generator=gen512)
+    med512, reps512 = cb.time_calls(
+        lambda i: cb.moe_layer(x512[64 * (i % 2):64 * (i % 2) + 64], router, gate, up, down,
+                               TOPK, G), 0.2 * seconds, 2)
 
     gen = torch.Generator().manual_seed(5)
 
@@ -577,7 +665,7 @@ def cpu_baseline(torch, first, xs, seconds):
     c1 = awq(H, I)
     xk = torch.randn(4, 4096, generator=gen).half()
     med_c1, reps_c1 = cb.time_calls(lambda i: cb.gemv(xk[i % 4, :H], *c1, group=G),
-                                    0.1 * seconds)
+                                    0.08 * seconds)
     proj = {"q": awq(2048, 4096), "k": awq(2048, 512), "v": awq(2048, 512), "o": awq(4096, 2048)}
 
     def attn(i):
@@ -586,7 +674,7 @@ def cpu_baseline(torch, first, xs, seconds):
             cb.gemv(xi[:2048], *proj[name], group=G)
         cb.gemv(xi, *proj["o"], group=G)
 
-    med_c2, reps_c2 = cb.time_calls(attn, 0.15 * seconds)
+    med_c2, reps_c2 = cb.time_calls(attn, 0.12 * seconds)
     model = cpu_model_name()
     return {
         "value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
@@ -602,6 +690,12 @@ def cpu_baseline(torch, first, xs, seconds):
             "moe_layer_M32": {"us_per_layer": round(med32 * 1e6, 1), "reps": reps32,
                               "tokens_per_s": round(32 / med32, 1),
                               "path": "CPU expert path, per token (fused_packed_moe.py:202-220)"},
+            "moe_layer_M512": {"us_per_layer": round(med512 * 512 / 64 * 1e6, 1),
+                               "us_per_token": round(med512 / 64 * 1e6, 1), "reps": reps512,
+                               "tokens_per_s": round(64 / med512, 1),
+                               "sample": "64-token slices of the 512 (x ~ N(0, 1)), median; "
+                                         "the per-token loop makes a layer 8 slices",
+                               "path": "CPU expert path, per token (fused_packed_moe.py:202-220)"},
         },
     }
 
@@ -733,8 +827,8 @@ def main() -> int:
     torch.cuda.synchronize()
     k_us, k_layer, k_router = time_experts(pkg, torch, dev, mods, hs, args.kernel_rounds)
     achieved = B_EXPERTS_LAUNCH / (k_us * 1e-6) / 1e9
-    log(f"experts kernel: {k_us:.2f} us/launch (events around each launch; layer {k_layer:.2f}, "
-        f"router alone {k_router:.2f}, back-to-back) -> {achieved:.0f} GB/s")
+    log(f"experts kernel: {k_us:.2f} us/launch (24 back to back; layer {k_layer:.2f}, "
+        f"router alone {k_router:.2f}) -> {achieved:.0f} GB/s")
 
     # ---- other workloads of the same layer: M=32 (router from weights) and M=512 prefill
     # with Zipf(1.1)-skewed logits (MFMA tiles for hot experts), rotating over the layers
@@ -791,6 +885,14 @@ def main() -> int:
             log(f"M={T}: {us_T:.1f} us/layer, {tf:.1f} TFLOP/s, {gbs:.0f} GB/s, "
                 f"{rs['experts_hit']} experts hit")
 
+    gen3 = torch.Generator(device=dev)
+    gen3.manual_seed(11)
+    rows32 = [torch.randn(32, H, device=dev, generator=gen3).half() for _ in range(4)]
+    routing = routing_agreement(torch, dev, mods, xs, rows32)
+    log(f"routing vs the host's exact top-8: M=1 {routing['M1']['differ']} of "
+        f"{routing['M1']['rows']} rows differ, M=32 {routing['M32']['differ']} of "
+        f"{routing['M32']['rows']}")
+
     gemv = time_gemvs(pkg, torch, dev, args.replays) if args.gemv else None
 
     decode = None
@@ -846,12 +948,13 @@ def main() -> int:
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": EXPERTS_TRAFFIC_BYTES,
             "bytes_per_launch": B_EXPERTS_LAUNCH, "us_per_launch": round(k_us, 3),
-            "timing": "HIP events around each experts launch, behind its router launch, over "
-                      "the 24 layers",
+            "timing": "HIP events around the 24 layers' experts launches back to back (their "
+                      "router launches run first, each layer with its own workspace)",
             "us_per_layer_launches": round(k_layer, 3), "us_per_router_launch": round(k_router, 3),
         },
         "cpu_baseline": cpu,
         "other_workloads": prefill,
+        "routing_agreement": routing,
         "gemv": gemv,
         "thinker_decode_step": decode,
         "talker_moe": talker,

@@ -148,11 +148,17 @@ const char* i4_strerror(int code);
  * (i4_dq_gemv_workspace_bytes() returns 0; NULL / 0 is accepted).  An AWQ
  * weight with N % 32 == 0 whose K-complete launch would stream more than 2048
  * rows per CU (K x ceil(N / 8 * k_sel / 256) > 2048, e.g. 2048 -> 4096 and
- * 4096 -> 2048) is split along K when the caller passes the workspace that
- * i4_dq_gemv_workspace_bytes() names: 256-byte aligned, every byte 0xFF before
- * its first call (each call leaves it so), one workspace per stream; with a
- * NULL workspace it runs K-complete, a smaller one is I4_ERR_WORKSPACE.  AWQ
- * scales must be 16-byte aligned (also between experts).
+ * 4096 -> 2048), with k_sel <= 8 and partials of at most 8 MiB, is split along K
+ * when the caller passes the workspace that i4_dq_gemv_workspace_bytes() names
+ * (256-byte aligned, one workspace per stream); with a NULL workspace it runs
+ * K-complete, a smaller one is I4_ERR_WORKSPACE.  The split launch hands each
+ * slice's partial sums to the last slice of its column strip inside the launch,
+ * tagged with a number the library gives every call, so the workspace needs no
+ * initial contents and a partial left by an earlier call is never taken.  Its
+ * first int32 is a status word: a call whose hand-over wait gave up (its outputs
+ * are NaN then) stores I4_ERR_HANDOFF there; calls never clear it, so zero it when
+ * the workspace is allocated and read it (after the stream) to learn of a failure.
+ * AWQ scales must be 16-byte aligned (also between experts).
  * A group at least as long as K is one scale per output row (the per-channel
  * branch of quant/dequant.py:75-76); a K that is not a multiple of the group
  * leaves a short last group (NG = ceil(K / group) scales per row). */
@@ -161,6 +167,16 @@ int    i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride,
                   void* out, int out_dtype,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t i4_dq_gemv_workspace_bytes(const i4_qweight* w, int k_sel);
+/* i4_dq_gemv with a caller bound on the split launch's hand-over wait (i4_dq_gemv
+ * uses 2^20 polls); reducers_only = 1 launches only the last slice of every strip,
+ * whose partials then never arrive: the wait gives up after max_polls polls (NaN
+ * outputs, I4_ERR_HANDOFF in the status word) and every kernel exits.  No reference
+ * counterpart: the host's way of testing the bounded wait.  I4_ERR_WORKSPACE /
+ * I4_ERR_LAYOUT when the call would not run split. */
+int    i4_dq_gemv_bounded(const void* x, int x_dtype, int64_t x_stride,
+                          const i4_qweight* w, const int32_t* sel, int k_sel,
+                          void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                          int max_polls, int reducers_only, hipStream_t stream);
 
 /* TritonPackedLinear.forward (src/duplex/streaming/triton_dequant_gemv.py:151-159):
  *   y[m][n] = sum_k W[n][k] * x[m][k] (+ bias[n]),  m < M, expert 0 of w.
@@ -171,8 +187,8 @@ size_t i4_dq_gemv_workspace_bytes(const i4_qweight* w, int k_sel);
  * (the path for prefill and other M > 1 batches); when that grid is small it
  * is split along K into fp32 partials in the workspace and summed in a fixed
  * order.  i4_linear_workspace_bytes gives the workspace (0: none needed); for
- * an AWQ weight it is i4_dq_gemv's split-K workspace, with the same 0xFF
- * contract. */
+ * an AWQ weight it is i4_dq_gemv's split-K workspace (M <= 8), with its status
+ * word. */
 int    i4_linear(const void* x, int x_dtype, int M, const i4_qweight* w,
                  const void* bias, void* y, int y_dtype,
                  void* workspace, size_t workspace_bytes, hipStream_t stream);
@@ -398,7 +414,10 @@ size_t i4_attn_decode_workspace_bytes(int n_heads, int head_dim, int max_len);
  * i4_attn_decode(_at) followed by i4_linear(o_w, bias = residual) bit for bit.
  * pos_dev (int32 on the device, nullable) overrides pos as in i4_attn_decode_at.
  * Workspace: i4_attn_decode_o_workspace_bytes(), no initial contents; calls sharing one
- * must not overlap. */
+ * must not overlap.  Its int32 at i4_attn_decode_o_status_offset() is a status word every
+ * call rewrites: I4_OK, or I4_ERR_HANDOFF when an o_proj workgroup gave up waiting for
+ * the merged heads of its own launch (its rows are then NaN; the wait is bounded at 2^20
+ * polls and only gives up if the launch's workgroups are not dispatched in block order). */
 int    i4_attn_decode_o(const void* qkv, int x_dtype, int n_heads, int n_kv_heads,
                         int head_dim, const void* q_norm_w, const void* k_norm_w, float eps,
                         const float* inv_freq, const int32_t* pos_dev, int pos, void* k_cache,
@@ -406,6 +425,7 @@ int    i4_attn_decode_o(const void* qkv, int x_dtype, int n_heads, int n_kv_head
                         const void* residual, void* y, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
 size_t i4_attn_decode_o_workspace_bytes(int n_heads, int head_dim, int max_len);
+size_t i4_attn_decode_o_status_offset(int n_heads, int head_dim, int max_len);
 
 /* One decode token through a whole Thinker decoder layer:
  * Qwen3OmniMoeThinkerTextDecoderLayer.forward (modeling_qwen3_omni_moe.py:1539-1565
@@ -551,12 +571,16 @@ int    i4_dmoe_down_wait(const void* x, int x_dtype, const i4_dmoe_weights* weig
  * routine.  A call whose i4_moe_workspace_bytes() exceeds the array returns
  * I4_ERR_SCRATCH without launching (8 MiB covers a decode token and batches of
  * up to ~160 tokens at hidden 2048, FFN 768, 128 experts, top-8).  Every call on
- * one GPU shares that GPU's array: calls that overlap on one GPU race. */
+ * one GPU shares that GPU's array: calls that overlap on one GPU race.  status_out
+ * (int32 on the device, 4-byte aligned, nullable) receives the status word that
+ * i4_moe_forward keeps in its workspace: I4_OK, or I4_ERR_HANDOFF when a decode wait
+ * gave up (NaN rows); the call rewrites it. */
 #define I4_NOALLOC_SCRATCH_BYTES (8u << 20)
 int    i4_moe_forward_noalloc(const void* x, int x_dtype, int T,
                               const i4_moe_weights* weights, int topk, int renorm,
                               const void* logits, const void* residual, void* out,
-                              int32_t* sel_out, float* w_out, hipStream_t stream);
+                              int32_t* sel_out, float* w_out, int32_t* status_out,
+                              hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -274,19 +274,40 @@ def silu(v: np.ndarray) -> np.ndarray:
     return v / (1.0 + np.exp(-v))
 
 
+def ref_combine(ys, w, dtype: str, residual=None) -> np.ndarray:
+    """The reference's own combine of one token (fused_packed_moe.py:199,262): the routing
+    weights rounded to the activation dtype (w.to(x.dtype)), each expert output rounded
+    (y.to(x.dtype)), their products rounded to the dtype (a 16-bit tensor multiply), the k
+    products summed in fp32 in slot order and rounded once (torch's 16-bit sum accumulates
+    in fp32); the decoder layer then adds the residual in the dtype.
+    ys [k, H], w [k] -> [H] (values of the dtype, as float64)."""
+    wr = round_half(np.asarray(w, np.float64), dtype)
+    prods = round_half(round_half(np.asarray(ys, np.float64), dtype) * wr[:, None], dtype)
+    acc = np.zeros(prods.shape[1], np.float32)
+    for p in prods:
+        acc = (acc + p.astype(np.float32)).astype(np.float32)
+    out = round_half(acc.astype(np.float64), dtype)
+    if residual is not None:
+        out = round_half(out + np.asarray(residual, np.float64), dtype)
+    return out
+
+
 def moe_layer(x, sel, w, Wgu, Wdn, act_dtype: str | None, residual=None,
-              out_dtype: str | None = None, y_dtype: str | None = None) -> np.ndarray:
+              out_dtype: str | None = None, y_dtype: str | None = None,
+              combine: str = "exact") -> np.ndarray:
     """x [T, H]; sel/w [T, k]; Wgu dense [E, 2I, H] (gate rows first); Wdn dense [E, H, I].
 
     y_dtype rounds each expert's output before the routing-weighted sum, the
-    reference's y.to(x.dtype) (fused_packed_moe.py:262); the sum itself stays
-    float64 here (the reference's bf16 product and sum are not modelled)."""
+    reference's y.to(x.dtype) (fused_packed_moe.py:262); with combine="exact" the sum
+    itself stays float64.  combine="reference" models the reference's own rounding of
+    the combine instead (ref_combine, in act_dtype), residual included."""
     x = np.asarray(x, np.float64)
     T = x.shape[0]
     I = Wgu.shape[1] // 2
     H = Wdn.shape[1]
     out = np.zeros((T, H), np.float64)
     for t in range(T):
+        ys = []
         for j in range(sel.shape[1]):
             e = int(sel[t, j])
             gu = Wgu[e] @ x[t]
@@ -296,7 +317,13 @@ def moe_layer(x, sel, w, Wgu, Wdn, act_dtype: str | None, residual=None,
             y = Wdn[e] @ a
             if y_dtype is not None:
                 y = round_half(y, y_dtype)
+            ys.append(y)
             out[t] += w[t, j] * y
+        if combine == "reference":
+            res_t = None if residual is None else np.asarray(residual, np.float64)[t]
+            out[t] = ref_combine(np.stack(ys), w[t], act_dtype, res_t)
+    if combine == "reference":
+        return out
     if residual is not None:
         out = out + np.asarray(residual, np.float64)
     if out_dtype is not None:

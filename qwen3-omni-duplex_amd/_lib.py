@@ -81,6 +81,8 @@ SIGNATURES = {
     "i4_dq_gemv": (c_int, [c_void_p, c_int, c_int64, POINTER(QWeightC), c_void_p, c_int,
                            c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
     "i4_dq_gemv_workspace_bytes": (c_size_t, [POINTER(QWeightC), c_int]),
+    "i4_dq_gemv_bounded": (c_int, [c_void_p, c_int, c_int64, POINTER(QWeightC), c_void_p, c_int,
+                                   c_void_p, c_int, c_void_p, c_size_t, c_int, c_int, c_void_p]),
     "i4_linear": (c_int, [c_void_p, c_int, c_int, POINTER(QWeightC), c_void_p, c_void_p, c_int,
                           c_void_p, c_size_t, c_void_p]),
     "i4_linear_workspace_bytes": (c_size_t, [POINTER(QWeightC), c_int]),
@@ -101,7 +103,7 @@ SIGNATURES = {
     "i4_moe_status_offset": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "i4_moe_forward_noalloc": (c_int, [c_void_p, c_int, c_int, POINTER(MoeWeightsC), c_int, c_int,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                       c_void_p]),
+                                       c_void_p, c_void_p]),
     "i4_moe_down_wait": (c_int, [c_void_p, c_int, POINTER(QWeightC), c_void_p, c_int, c_int, c_int,
                                  c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "i4_moe_gate_up": (c_int, [c_void_p, c_int, POINTER(QWeightC), c_void_p, c_int, c_void_p,
@@ -135,6 +137,7 @@ SIGNATURES = {
                                  c_int, POINTER(QWeightC), c_void_p, c_void_p, c_void_p,
                                  c_size_t, c_void_p]),
     "i4_attn_decode_o_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "i4_attn_decode_o_status_offset": (c_size_t, [c_int, c_int, c_int]),
     "i4_thinker_layer_decode": (c_int, [c_void_p, c_int, c_void_p, ctypes.c_float,
                                         POINTER(QWeightC), c_int, c_int, c_int, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,

@@ -38,6 +38,9 @@ class ThinkerAttention(nn.Module):
                  n_kv_heads: int, head_dim: int = 128, eps: float = 1e-6,
                  rope_theta: float = 1_000_000.0, max_len: int = 4096):
         super().__init__()
+        if qkv.lin.w.layout != "ct":
+            raise ValueError("the q|k|v weight must be in the CT layout: the input norm runs "
+                             "inside its GEMV (build PackedQKV with repack=True)")
         self.qkv, self.o_proj = qkv, o_proj
         self.n_heads, self.n_kv_heads, self.head_dim = int(n_heads), int(n_kv_heads), int(head_dim)
         self.eps = float(eps)
@@ -50,10 +53,30 @@ class ThinkerAttention(nn.Module):
         self.inv_freq = rope_inv_freq(head_dim, rope_theta)  # host table
         shape = (n_kv_heads, max_len, head_dim)
         dev = input_norm_w.device
-        self.register_buffer("k_cache", torch.zeros(shape, dtype=dt, device=dev), persistent=False)
-        self.register_buffer("v_cache", torch.zeros(shape, dtype=dt, device=dev), persistent=False)
+        self.register_buffer("_k_cache", torch.zeros(shape, dtype=dt, device=dev), persistent=False)
+        self.register_buffer("_v_cache", torch.zeros(shape, dtype=dt, device=dev), persistent=False)
         self.max_len = int(max_len)
         self.workspace = ops.Workspace()
+
+    # The caches are written in place by the kernels and their addresses are held by the
+    # decoder's layer structs, so they cannot be replaced: fill them in place
+    # (k_cache.copy_(...)) or clear them with reset_cache().
+    @property
+    def k_cache(self) -> torch.Tensor:
+        return self._k_cache
+
+    @property
+    def v_cache(self) -> torch.Tensor:
+        return self._v_cache
+
+    def reset_cache(self) -> None:
+        """Empty the KV cache in place (a new conversation)."""
+        self._k_cache.zero_()
+        self._v_cache.zero_()
+
+    def __setattr__(self, name, value):
+        super().__setattr__(name, value)
+        ops.weights_changed()
 
     def forward(self, h: torch.Tensor, pos: int | torch.Tensor) -> torch.Tensor:
         """h [1, H] (one token at cache position pos) -> h + o_proj(attn(norm(h))).
@@ -129,12 +152,27 @@ class ThinkerDecoder(nn.Module):
         self.layers = nn.ModuleList(layers)
         self.workspace = ops.Workspace()
         self._fused: bool | None = None
-        self._layers_c = None
+        self._layers_c, self._layers_refs, self._layers_gen = None, None, -1
 
     def _apply(self, fn, *args, **kwargs):
         # moved tensors: the layer structs hold their old addresses
         self._fused, self._layers_c = None, None
         return super()._apply(fn, *args, **kwargs)
+
+    def _structs(self):
+        """The layer structs (raw addresses of the layers' tensors), rebuilt when any tensor of
+        a ThinkerAttention or FusedPackedMoE was assigned since they were made; the tensors
+        they point at are kept referenced with them."""
+        gen = ops.weights_generation()
+        if self._layers_c is None or self._layers_gen != gen:
+            arr = _lib.ThinkerLayerC * len(self.layers)
+            self._layers_c = arr(*[ops.thinker_layer_c(l.attn, l.moe) for l in self.layers])
+            self._layers_refs = [(l.attn._k_cache, l.attn._v_cache, l.attn.input_norm_w,
+                                  l.attn.q_norm_w, l.attn.k_norm_w, l.attn.qkv.lin.w,
+                                  l.attn.o_proj.w, l.moe.gate_up, l.moe.down, l.moe.router_w,
+                                  l.moe.norm_weight) for l in self.layers]
+            self._layers_gen = gen
+        return self._layers_c
 
     def fused(self) -> bool:
         """Whether step runs as one i4_thinker_decode_step call: every layer takes
@@ -157,11 +195,8 @@ class ThinkerDecoder(nn.Module):
             a0, m0 = self.layers[0].attn, self.layers[0].moe
             if not isinstance(pos, torch.Tensor) and not 0 <= pos < a0.max_len:
                 raise ValueError(f"position {pos} outside the cache (max_len {a0.max_len})")
-            if self._layers_c is None:
-                arr = _lib.ThinkerLayerC * len(self.layers)
-                self._layers_c = arr(*[ops.thinker_layer_c(l.attn, l.moe) for l in self.layers])
             return ops.thinker_decode_step(
-                h, self._layers_c, len(self.layers), a0.n_heads, a0.n_kv_heads, a0.head_dim,
+                h, self._structs(), len(self.layers), a0.n_heads, a0.n_kv_heads, a0.head_dim,
                 a0.inv_freq, pos, a0.max_len, m0.hidden, m0.down.K, m0.gate_up.E, m0.top_k,
                 m0.norm_topk_prob, self.workspace)
         return self.unfused(h, pos)

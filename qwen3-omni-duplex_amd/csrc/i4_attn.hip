@@ -349,7 +349,8 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
                                                 const int32_t* __restrict__ pos_dev, int pos_host,
                                                 int max_len, uint16_t* __restrict__ att, OProj o,
                                                 const uint16_t* __restrict__ residual,
-                                                uint16_t* y, int max_polls, RFold r) {
+                                                uint16_t* y, int max_polls, RFold r,
+                                                int32_t* __restrict__ o_status) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int b = blockIdx.x, t = threadIdx.x;
   if (b < nq) {
@@ -381,11 +382,11 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     }
     gemv_ct_body<XT, ST, L, false, true, true>(b - nq, 0, att, 0, o.packed, 0, o.scale, 0,
                                                o.zeros, 0, nullptr, 1, o.N, o.K, o.gshift, y, XT,
-                                               residual, nullptr, 0.f, lds, max_polls);
+                                               residual, nullptr, 0.f, lds, max_polls, r.status);
   } else {
     gemv_ct_body<XT, ST, L, false, true>(b - nq, 0, att, 0, o.packed, 0, o.scale, 0, o.zeros, 0,
                                          nullptr, 1, o.N, o.K, o.gshift, y, XT, residual, nullptr,
-                                         0.f, lds, max_polls);
+                                         0.f, lds, max_polls, o_status);
   }
 }
 
@@ -397,8 +398,15 @@ size_t attn_ws(int nq, int max_len) {
   const size_t nch = ((size_t)max_len + ACH - 1) / ACH;
   return nch * nq * PSTR * sizeof(float);
 }
+// with o_proj: then (at a 256-byte boundary) the status word of the o_proj wait in a
+// 256-byte slot, then the attention output, which ends the workspace -- the router-fold
+// launch keeps its output y directly behind it, one pending span over both
+size_t attn_o_status_off(int nq, int max_len) {
+  return (attn_ws(nq, max_len) + 255) & ~(size_t)255;
+}
+size_t attn_o_att_off(int nq, int max_len) { return attn_o_status_off(nq, max_len) + 256; }
 size_t attn_o_ws(int nq, int max_len) {
-  return ((attn_ws(nq, max_len) + 255) & ~(size_t)255) + (size_t)nq * HD * 2;
+  return attn_o_att_off(nq, max_len) + (size_t)nq * HD * 2;
 }
 
 // o_proj behind the attention (k_attn_o), or none (o == nullptr: k_attn_combine);
@@ -411,6 +419,7 @@ struct OLaunch {
   void* y;
   const RFold* route = nullptr;
   bool reset_status = true;  // with route: the chunk launch clears route->status
+  int32_t* status = nullptr;  // without route: the o_proj wait's status, cleared likewise
 };
 
 template <int XT, int ST>
@@ -432,7 +441,7 @@ int launch_attn_o(const float* part, int nq, const int32_t* pos_dev, int pos, in
   if (L == L_ && rh == RH_) {                                                                 \
     hipLaunchKernelGGL((k_attn_o<XT, ST, L_, RH_>), grid, dim3(256), lds, s, part, nq,        \
                        pos_dev, pos, max_len, att, o.w, (const uint16_t*)o.residual,          \
-                       (uint16_t*)o.y, kHandoffPolls, r);                                     \
+                       (uint16_t*)o.y, kHandoffPolls, r, o.status);                           \
     return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                           \
   }
   I4_AO_CASE(8, 0) I4_AO_CASE(16, 0) I4_AO_CASE(32, 0) I4_AO_CASE(64, 0)
@@ -461,7 +470,8 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   // with o_proj, the attention output (and, with the router, y right behind it) start
   // pending
   const int n_pend = !o ? 0 : (nq * HD + (o->route ? o->w.N : 0)) / 8;
-  int32_t* st_reset = o && o->route && o->reset_status ? o->route->status : nullptr;
+  int32_t* st_reset = !o ? nullptr : o->route ? (o->reset_status ? o->route->status : nullptr)
+                                               : o->status;
 #define I4_AC_CASE(G_)                                                                        \
   if (gq / gsplit == G_)                                                                      \
     hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, (const uint16_t*)qkv,  \
@@ -555,8 +565,9 @@ static int attn_entry(const void* qkv, int x_dtype, int n_heads, int n_kv_heads,
   if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
   i4::RopeTab rt;
   for (int i = 0; i < i4::HD / 2; ++i) rt.inv_freq[i] = inv_freq[i];
-  // with o_proj the attention output lives in the workspace, after the partials
-  void* att = o ? (char*)workspace + ((i4::attn_ws(n_heads, max_len) + 255) & ~(size_t)255) : out;
+  // with o_proj the attention output lives in the workspace, after the partials and the
+  // status slot
+  void* att = o ? (char*)workspace + i4::attn_o_att_off(n_heads, max_len) : out;
   return x_dtype == I4_F16
              ? i4::attn_launch<I4_F16>(qkv, n_heads, n_kv_heads, q_norm_w, k_norm_w, eps, rt,
                                        pos_dev, pos, k_cache, v_cache, max_len, att, workspace,
@@ -605,9 +616,17 @@ int i4_attn_decode_o(const void* qkv, int x_dtype, int n_heads, int n_kv_heads, 
   o.st = nw.scale_dtype;
   o.residual = residual;
   o.y = y;
+  if (workspace && !((uintptr_t)workspace & 255) &&
+      workspace_bytes >= i4::attn_o_ws(n_heads, max_len))
+    o.status = (int32_t*)((char*)workspace + i4::attn_o_status_off(n_heads, max_len));
   return attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
                     inv_freq, pos_dev, pos, k_cache, v_cache, max_len, y, workspace,
                     workspace_bytes, stream, &o);
+}
+
+size_t i4_attn_decode_o_status_offset(int n_heads, int head_dim, int max_len) {
+  if (n_heads < 1 || head_dim != i4::HD || max_len < 1) return 0;
+  return i4::attn_o_status_off(n_heads, max_len);
 }
 
 size_t i4_thinker_layer_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len,

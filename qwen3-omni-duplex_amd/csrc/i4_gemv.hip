@@ -11,6 +11,8 @@
 //
 // The CT GEMV's work split is described with its body (i4_gemv_body.h); grid.y
 // is the selected-expert slot.
+#include <atomic>
+
 #include "i4_common.h"
 #include "i4_gemv_body.h"
 #include "i4_launch.h"
@@ -165,27 +167,34 @@ __global__ __launch_bounds__(WG) void k_gemv_awq(
 //   across the waves in LDS, and the slice's scale (loaded with the weights)
 //   is applied once per column: a slice lies inside one quantisation group.
 // Hand-over without atomics or fences: slices 0..P-2 of a strip store their
-// fp32 partials (1 KB) write-through and exit; slice P-1, dispatched after
-// them, reads the other partials from memory until none holds the pending
-// pattern (0xFFFFFFFF, a NaN no slice writes: NaNs are stored canonical),
-// sums them in a fixed order (slice classes s mod NWAVE, then its own slice),
-// writes y, and puts the pattern back.  The partials must hold the pattern
-// before the first launch; every launch leaves it there.  A reducer that
-// polls max_polls times without seeing every partial writes NaN.
+// fp32 partials (1 KB) write-through and exit, each column as one 8-byte store of
+// (value, tag) with the call's tag (a number the host gives every call, never 0);
+// slice P-1, dispatched after them, reads the other partials from memory until every
+// one carries the call's tag, sums them in a fixed order (slice classes s mod NWAVE,
+// then its own slice), writes y, and clears the tags it read (so a captured graph,
+// which replays one tag, finds them pending again).  A partial left by an earlier
+// call never carries this call's tag, so the workspace needs no initial contents.
+// A reducer that polls max_polls times without seeing every partial writes NaN,
+// clears the tags of its whole strip and stores I4_ERR_HANDOFF in the status word
+// (the workspace's first int32; only failures are stored, the caller clears it).
 static constexpr int SK_COLS = 256;  // columns per strip
-static constexpr u32 kPending32 = 0xFFFFFFFFu;
 static constexpr int kAwqPolls = 1 << 20;
+static constexpr size_t SK_HEAD = 256;  // workspace header: the status word, then partials
 
 template <int XT, int ST, int NWAVE, int PPT>
 __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
     const uint16_t* __restrict__ x, int64_t x_stride, const int32_t* __restrict__ qw, int64_t q_es,
     const void* __restrict__ scales, int64_t s_es, const int32_t* __restrict__ qz, int64_t z_es,
     const int32_t* __restrict__ sel, int E, int N, int gshift, int S, int P,
-    float* part, void* __restrict__ out, int ot, const void* __restrict__ bias, int max_polls) {
+    uint64_t* part, void* __restrict__ out, int ot, const void* __restrict__ bias, int max_polls,
+    u32 tag, int32_t* __restrict__ status, int only_last) {
   constexpr int NT = 64 * NWAVE, PASS = 16 * NWAVE, KS = PASS * PPT, CPT = SK_COLS / NT;
   __shared__ f32x4 red[NWAVE][64];
   __shared__ int s_gave_up;  // the reducer's wait gave up (set before the first barrier)
-  const int strip = (int)blockIdx.x / P, slice = (int)blockIdx.x % P;
+  // only_last: the reducers alone (grid S), whose partials then never arrive -- the host's
+  // way of making the wait give up in a test
+  const int strip = only_last ? (int)blockIdx.x : (int)blockIdx.x / P;
+  const int slice = only_last ? P - 1 : (int)blockIdx.x % P;
   const int j = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int q = t & 7, rp = t >> 3;
@@ -304,41 +313,44 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
     v *= scale_from_raw<ST>(sraw[c]);
     mine[c] = ev ? (v != v ? __builtin_nanf("") : v) : __builtin_nanf("");  // canonical NaN
   }
-  float* strip_part = part + (int64_t)(j * S + strip) * P * SK_COLS;
-  if (slice != P - 1) {  // a producer: hand the partial over and leave
+  uint64_t* strip_part = part + (int64_t)(j * S + strip) * P * SK_COLS;
+  if (slice != P - 1) {  // a producer: hand the partial over, tagged, and leave
 #pragma unroll
     for (int c = 0; c < CPT; ++c)
       if (ncol[c] >= 0)
-        __hip_atomic_store(strip_part + (int64_t)slice * SK_COLS + (ncol[c] & 255), mine[c],
+        __hip_atomic_store(strip_part + (int64_t)slice * SK_COLS + (ncol[c] & 255),
+                           (uint64_t)__builtin_bit_cast(u32, mine[c]) | ((uint64_t)tag << 32),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
 
   // the reducer: thread t reads columns 4 (t % 64) .. +3 of the slices
-  // s = t / 64 (mod NWAVE), up to 16 * NWAVE slices per round trip, until none
-  // is pending; the slice classes are then added in class order in LDS
+  // s = t / 64 (mod NWAVE) -- two 16-byte (value, tag) pairs each -- up to 8 * NWAVE
+  // slices per round trip, until every pair carries the call's tag; the slice classes
+  // are then added in class order in LDS
   __shared__ f32x4 red2[NWAVE][64];
   {
-    constexpr int MAXB = 16;
-    const rsrc_t pr = rsrc(strip_part, (u32)P * SK_COLS * 4u);
+    constexpr int MAXB = 8;
+    const rsrc_t pr = rsrc(strip_part, (u32)P * SK_COLS * 8u);
     const int cg = lane, so = wave;
     const bool cv = strip * SK_COLS + 4 * cg < N;  // whole column quads (N % 32 == 0)
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
     f32x4 a4 = {0.f, 0.f, 0.f, 0.f};
     bool gave_up = false;
-    for (int s0 = 0; s0 < P - 1; s0 += NWAVE * MAXB) {
-      u32x4 pv[MAXB];
+    for (int s0 = 0; s0 < P - 1 && !gave_up; s0 += NWAVE * MAXB) {
+      u32x4 pa[MAXB], pb[MAXB];  // columns (4 cg, 4 cg + 1) and (4 cg + 2, 4 cg + 3)
       for (int poll = 0;; ++poll) {
         bool pending = false;
 #pragma unroll
         for (int i = 0; i < MAXB; ++i) {  // past the last producer: re-read it, unused
-          const int sl = min(s0 + so + NWAVE * i, P - 2);
-          pv[i] = ld16_coherent(pr, (u32)(sl * SK_COLS + 4 * cg) * 4u);
+          const u32 o = (u32)(min(s0 + so + NWAVE * i, P - 2) * SK_COLS + 4 * cg) * 8u;
+          pa[i] = ld16_coherent(pr, o);
+          pb[i] = ld16_coherent(pr, o + 16u);
         }
 #pragma unroll
-        for (int i = 0; i < MAXB; ++i)  // only the slices this thread owns: an owner puts
-          pending |= cv && s0 + so + NWAVE * i < P - 1 &&  // the pattern back once it read one
-                     (pv[i].x == kPending32 || pv[i].y == kPending32 ||
-                      pv[i].z == kPending32 || pv[i].w == kPending32);
+        for (int i = 0; i < MAXB; ++i)  // only the slices this thread owns
+          pending |= cv && s0 + so + NWAVE * i < P - 1 &&
+                     (pa[i].y != tag || pa[i].w != tag || pb[i].y != tag || pb[i].w != tag);
         if (!pending) break;
         if (poll >= max_polls) {
           gave_up = true;
@@ -349,19 +361,32 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
         __builtin_amdgcn_s_sleep(1);
         asm volatile("" ::: "memory");
       }
+      if (gave_up) break;
 #pragma unroll
       for (int i = 0; i < MAXB; ++i) {
         const int sl = s0 + so + NWAVE * i;
         if (sl < P - 1 && cv) {
-          a4 += __builtin_bit_cast(f32x4, pv[i]);  // whole vector
-          const u32x4 pend = {kPending32, kPending32, kPending32, kPending32};
-          __builtin_amdgcn_raw_buffer_store_b128(pend, pr, (u32)(sl * SK_COLS + 4 * cg) * 4u, 0,
-                                                 kCoherent);  // pending again for the next launch
+          // value words through scalars: a bit cast applied to an ext-vector component
+          // directly reads component 0
+          const u32 va[4] = {pa[i].x, pa[i].y, pa[i].z, pa[i].w};
+          const u32 vb[4] = {pb[i].x, pb[i].y, pb[i].z, pb[i].w};
+          a4 += f32x4{__builtin_bit_cast(float, va[0]), __builtin_bit_cast(float, va[2]),
+                      __builtin_bit_cast(float, vb[0]), __builtin_bit_cast(float, vb[2])};
+          const u32 o = (u32)(sl * SK_COLS + 4 * cg) * 8u;  // tags cleared for a replay
+          __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o, 0, kCoherent);
+          __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o + 16u, 0, kCoherent);
         }
       }
     }
+    if (gave_up) {  // every tag of the strip cleared, including partials not seen yet
+      for (int sl = so; sl < P - 1; sl += NWAVE) {
+        const u32 o = (u32)(sl * SK_COLS + 4 * cg) * 8u;
+        __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o, 0, kCoherent);
+        __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o + 16u, 0, kCoherent);
+      }
+      s_gave_up = 1;
+    }
     red2[so][cg] = a4;
-    if (gave_up) s_gave_up = 1;
   }
   __syncthreads();
 #pragma unroll
@@ -376,7 +401,11 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
       v += i == 0 ? r.x : i == 1 ? r.y : i == 2 ? r.z : r.w;
     }
     v += mine[c];  // the last slice's own partial
-    if (s_gave_up) v = __builtin_nanf("");
+    if (s_gave_up) {
+      v = __builtin_nanf("");
+      if (t == 0 && c == 0) __hip_atomic_store(status, I4_ERR_HANDOFF, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+    }
     const int64_t o = (int64_t)j * N + n;
     if (ot == I4_F32) {
       if (bias) v += ((const float*)bias)[n];
@@ -721,15 +750,25 @@ static int launch_gemv_awq_t(const void* x, int64_t x_stride, const i4_qweight* 
 // K-complete, 6.5 / 6.8 at 2048 -> 4096 and 4096 -> 2048 against 8.5-9.6), so
 // the split is taken only where the K-complete launch fills more than 2048 rows
 // of lines per CU (K rows per workgroup, N / 8 workgroups per row of x over 256
-// CUs).  Its slice is the largest of 128 / 64 / 32 rows that divides K and the
-// group: a slice's loads are one round trip at any of these sizes, and fewer
-// slices make fewer partials to hand over.
+// CUs), and only for up to kSplitRows rows of x (decode: the plan was measured at
+// one row) whose partials fit kSplitBytes; more rows run K-complete.  Its slice is
+// the largest of 128 / 64 / 32 rows that divides K and the group: a slice's loads
+// are one round trip at any of these sizes, and fewer slices make fewer partials to
+// hand over.
+static constexpr int kSplitRows = 8;
+static constexpr size_t kSplitBytes = (size_t)8 << 20;
 struct AwqSplit {
   int nwave, ppt, S, P;
 };
+// workspace of a split-K plan: the header (status word), then the (value, tag)
+// partials [row][strip][slice][256] of 8 bytes
+static size_t awq_split_bytes(const AwqSplit& p, int k_sel) {
+  if (!p.nwave) return 0;
+  return SK_HEAD + (size_t)k_sel * p.S * p.P * SK_COLS * sizeof(uint64_t);
+}
 static AwqSplit awq_split_plan(const i4_qweight& w, int k_sel) {
   AwqSplit p{0, 0, 0, 0};
-  if (w.layout != I4_LAYOUT_AWQ || w.N % 32 != 0 || k_sel < 1) return p;
+  if (w.layout != I4_LAYOUT_AWQ || w.N % 32 != 0 || k_sel < 1 || k_sel > kSplitRows) return p;
   if (w.zeros && (((uintptr_t)w.zeros & 15) || (w.E > 1 && w.zeros_estride % 4))) return p;
   const int64_t rounds = ((int64_t)(w.N / 8) * k_sel + 255) / 256;
   if ((int64_t)w.K * rounds <= 2048) return p;
@@ -741,29 +780,36 @@ static AwqSplit awq_split_plan(const i4_qweight& w, int k_sel) {
     p = AwqSplit{o[0], o[1], S, w.K / ks};
     break;
   }
+  if (awq_split_bytes(p, k_sel) > kSplitBytes) p = AwqSplit{0, 0, 0, 0};
   return p;
 }
-// workspace of a split-K plan: the fp32 slice partials, [row][strip][slice][256],
-// every byte 0xFF (the pending pattern) before the first launch
-static size_t awq_split_bytes(const AwqSplit& p, int k_sel) {
-  if (!p.nwave) return 0;
-  return (size_t)k_sel * p.S * p.P * SK_COLS * sizeof(float);
+
+// the tag of one call of the split-K GEMV: a process-wide count, never 0
+static std::atomic<uint32_t> g_call_tag{0};
+static u32 next_call_tag() {
+  u32 t = ++g_call_tag;
+  while (t == 0) t = ++g_call_tag;
+  return t;
 }
 
 template <int XT, int ST>
 static int launch_gemv_awq_sk_t(const void* x, int64_t x_stride, const i4_qweight* w,
                                 const int32_t* sel, int k_sel, void* out, int ot,
-                                const void* bias, const AwqSplit& p, void* ws, hipStream_t s) {
+                                const void* bias, const AwqSplit& p, void* ws, int max_polls,
+                                bool reducers_only, hipStream_t s) {
   int gshift = 0;
   while ((1 << gshift) < w->group) ++gshift;
-  const dim3 grid(p.S * p.P, k_sel);
-  float* part = (float*)ws;
+  const dim3 grid(reducers_only ? p.S : p.S * p.P, k_sel);
+  int32_t* status = (int32_t*)ws;
+  uint64_t* part = (uint64_t*)((char*)ws + SK_HEAD);
+  const u32 tag = next_call_tag();
 #define I4_SK_CASE(NW_, PPT_)                                                                     \
   if (p.nwave == NW_ && p.ppt == PPT_) {                                                          \
     hipLaunchKernelGGL((k_gemv_awq_sk<XT, ST, NW_, PPT_>), grid, dim3(64 * NW_), 0, s,            \
                        (const uint16_t*)x, x_stride, w->packed, w->packed_estride, w->scale,      \
                        w->scale_estride, w->zeros, w->zeros_estride, sel, w->E, w->N, gshift,     \
-                       p.S, p.P, part, out, ot, bias, kAwqPolls);                                 \
+                       p.S, p.P, part, out, ot, bias, max_polls, tag, status,                     \
+                       (int)reducers_only);                                                       \
     return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                               \
   }
   I4_SK_CASE(4, 2) I4_SK_CASE(4, 1) I4_SK_CASE(2, 1)
@@ -775,19 +821,22 @@ static int launch_gemv_awq_sk_t(const void* x, int64_t x_stride, const i4_qweigh
 // the K-complete kernel (no workspace)
 static int launch_gemv_awq(const void* x, int xt, int64_t x_stride, const i4_qweight* w,
                            const int32_t* sel, int k_sel, void* out, int ot, const void* bias,
-                           void* ws, size_t ws_bytes, hipStream_t s) {
+                           void* ws, size_t ws_bytes, hipStream_t s, int max_polls = kAwqPolls,
+                           bool reducers_only = false) {
   const AwqSplit p = awq_split_plan(*w, k_sel);
   if (p.nwave && ws) {
     if (ws_bytes < awq_split_bytes(p, k_sel)) return I4_ERR_WORKSPACE;
     if ((uintptr_t)ws & 255) return I4_ERR_ALIGN;
 #define I4_AWQ_DT(XT_, ST_)                                                                   \
   if (xt == XT_ && w->scale_dtype == ST_)                                                     \
-    return launch_gemv_awq_sk_t<XT_, ST_>(x, x_stride, w, sel, k_sel, out, ot, bias, p, ws, s);
+    return launch_gemv_awq_sk_t<XT_, ST_>(x, x_stride, w, sel, k_sel, out, ot, bias, p, ws,   \
+                                          max_polls, reducers_only, s);
     I4_AWQ_DT(I4_F16, I4_F32) I4_AWQ_DT(I4_F16, I4_F16) I4_AWQ_DT(I4_F16, I4_BF16)
     I4_AWQ_DT(I4_BF16, I4_F32) I4_AWQ_DT(I4_BF16, I4_F16) I4_AWQ_DT(I4_BF16, I4_BF16)
 #undef I4_AWQ_DT
     return I4_ERR_DTYPE;
   }
+  if (reducers_only) return I4_ERR_WORKSPACE;  // only a split launch has reducers
 #define I4_AWQ_DT(XT_, ST_)                                                              \
   if (xt == XT_ && w->scale_dtype == ST_)                                                \
     return launch_gemv_awq_t<XT_, ST_>(x, x_stride, w, sel, k_sel, out, ot, bias, s);
@@ -808,6 +857,15 @@ size_t i4_dq_gemv_workspace_bytes(const i4_qweight* w, int k_sel) {
 int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w,
                const int32_t* sel, int k_sel, void* out, int out_dtype, void* workspace,
                size_t workspace_bytes, hipStream_t stream) {
+  return i4_dq_gemv_bounded(x, x_dtype, x_stride, w, sel, k_sel, out, out_dtype, workspace,
+                            workspace_bytes, kAwqPolls, 0, stream);
+}
+
+int i4_dq_gemv_bounded(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w,
+                       const int32_t* sel, int k_sel, void* out, int out_dtype, void* workspace,
+                       size_t workspace_bytes, int max_polls, int reducers_only,
+                       hipStream_t stream) {
+  if (max_polls < 0) return I4_ERR_SHAPE;
   i4_qweight nw;
   int rc = i4_check_weight(w, &nw);
   if (rc) return rc;
@@ -818,11 +876,13 @@ int i4_dq_gemv(const void* x, int x_dtype, int64_t x_stride, const i4_qweight* w
   if (!al16(x) || (x_stride * 2) % 16 != 0) return I4_ERR_ALIGN;
   if (nw.layout == I4_LAYOUT_TILE) return I4_ERR_LAYOUT;  // the MoE kernels' layout
   if (nw.layout == I4_LAYOUT_AWQ && !awq_scales_aligned(nw)) return I4_ERR_ALIGN;
-  if (nw.layout == I4_LAYOUT_CT)
+  if (nw.layout == I4_LAYOUT_CT) {
+    if (reducers_only) return I4_ERR_LAYOUT;  // only the AWQ split launch hands over
     return i4_launch_gemv_ct(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr,
                              stream);
+  }
   return launch_gemv_awq(x, x_dtype, x_stride, &nw, sel, k_sel, out, out_dtype, nullptr,
-                         workspace, workspace_bytes, stream);
+                         workspace, workspace_bytes, stream, max_polls, reducers_only != 0);
 }
 
 int i4_rmsnorm_linear(const void* x, int x_dtype, int M, const void* norm_w, float eps,

@@ -23,7 +23,8 @@ static constexpr int GEMV_ROUND = 4;  // chunks per lane whose loads are in flig
 // POLL: x (one row, K <= 8192) is written by earlier workgroups of the same
 // launch and holds the pending pattern until then; the workgroup issues its
 // first round of weight loads, then polls x (poll_rows) instead of loading it.
-// Rows of a workgroup whose wait gives up come out NaN.
+// Rows of a workgroup whose wait gives up come out NaN, and I4_ERR_HANDOFF goes to
+// *status (nullable).
 // HANDOFF: out (ot = XT) is read by later workgroups of the same launch: the
 // workgroup's rows are gathered in LDS and written through to memory as whole
 // 16-byte stores where they are aligned (else value by value), NaN in canonical form (so the pending
@@ -35,7 +36,7 @@ __device__ __forceinline__ void gemv_ct_body(
     int64_t s_es, const int32_t* __restrict__ zeros, int64_t z_es,
     const int32_t* __restrict__ sel, int E, int N, int K, int gshift, void* __restrict__ out,
     int ot, const void* __restrict__ bias, const uint16_t* __restrict__ nw, float eps,
-    unsigned char* lds, int max_polls) {
+    unsigned char* lds, int max_polls, int32_t* __restrict__ status = nullptr) {
   constexpr int WG = GEMV_WG, ROUND = GEMV_ROUND;
   static_assert(!(NORM && POLL), "a polled row is used as it arrives");
   constexpr int RPW = WG / L;
@@ -113,6 +114,10 @@ __device__ __forceinline__ void gemv_ct_body(
     }
   }
   row = group_sum<L>(row);
+  if constexpr (POLL) {  // a wait that gave up is reported (status nullable)
+    if (late && status && threadIdx.x == 0)
+      __hip_atomic_store(status, I4_ERR_HANDOFF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   if constexpr (HANDOFF) {
     __shared__ __align__(16) uint16_t s_y[RPW];
     if (rv && cl == 0) {

@@ -42,3 +42,12 @@ int i4_launch_router_sum(const void* res, const void* ypart, const float* wts, i
 // The completion alone: out = res + sum_k wts[k] ypart[k].
 int i4_launch_moe_sum(const void* res, const void* ypart, const float* wts, int kc, int xt,
                       int H, void* out, hipStream_t s);
+
+namespace i4 {
+// i4_moe_forward with its status word at `status` (device, 4-byte aligned; nullptr: in
+// the workspace), for i4_moe_forward_noalloc's status output
+int moe_forward_status(const void* x, int x_dtype, int T, const i4_moe_weights* weights,
+                       int topk, int renorm, const void* logits, const void* residual, void* out,
+                       int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
+                       int32_t* status, hipStream_t stream);
+}  // namespace i4

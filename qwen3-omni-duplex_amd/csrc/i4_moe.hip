@@ -474,7 +474,7 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
 int moe_forward_impl(const void* x, int x_dtype, int T, const i4_moe_weights* weights, int topk,
                      int renorm, const void* logits, const void* residual, void* out,
                      int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
-                     bool reset, hipStream_t stream) {
+                     bool reset, hipStream_t stream, int32_t* status = nullptr) {
   i4_qweight gu, dn, tg, td;
   int rc = check_moe(weights, x_dtype, T, topk, &gu, &dn, &tg, &td);
   if (rc) return rc;
@@ -488,7 +488,8 @@ int moe_forward_impl(const void* x, int x_dtype, int T, const i4_moe_weights* we
   const MoeWs need = carve(nullptr, T, H, I, E, topk);
   if (!workspace || workspace_bytes < need.bytes) return I4_ERR_WORKSPACE;
   if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
-  const MoeWs ws = carve(workspace, T, H, I, E, topk);
+  MoeWs ws = carve(workspace, T, H, I, E, topk);
+  if (status) ws.status = status;  // the caller's status word instead of the workspace's
   for (int t0 = 0; t0 < T; t0 += TCHUNK) {
     const int Tc = T - t0 < TCHUNK ? T - t0 : TCHUNK;
     const char* xs = (const char*)x + (size_t)t0 * H * 2;
@@ -546,6 +547,15 @@ int moe_decode_experts(const MoeDecodeBufs& b, int x_dtype, int topk, int renorm
   const GateUpArgs a{true, topk, topk, gu.E, renorm, w.xn, w.sel, w.logits, w.w, w.act, nullptr};
   const TW tg = to_tw(gu);
   return ops.moe_m1_ct(a, &tg, to_tw(dn), residual, out, w.status, kHandoffPolls, s);
+}
+
+int moe_forward_status(const void* x, int x_dtype, int T, const i4_moe_weights* weights,
+                       int topk, int renorm, const void* logits, const void* residual, void* out,
+                       int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
+                       int32_t* status, hipStream_t stream) {
+  if ((uintptr_t)status & 3) return I4_ERR_ALIGN;
+  return moe_forward_impl(x, x_dtype, T, weights, topk, renorm, logits, residual, out, sel_out,
+                          w_out, workspace, workspace_bytes, true, stream, status);
 }
 
 }  // namespace i4
@@ -662,6 +672,7 @@ int i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weig
   return moe_forward_impl(x, x_dtype, T, weights, topk, renorm, logits, residual, out, sel_out,
                           w_out, workspace, workspace_bytes, true, stream);
 }
+
 
 int i4_moe_down_wait(const void* act, int x_dtype, const i4_qweight* down, const void* logits,
                      int E_r, int topk, int renorm, const void* residual, void* out,

@@ -16,6 +16,7 @@
 #include <mutex>
 
 #include "i4moe.h"
+#include "i4_launch.h"
 
 static __device__ __align__(256) unsigned char scratch[I4_NOALLOC_SCRATCH_BYTES];
 
@@ -49,7 +50,8 @@ extern "C" {
 
 int i4_moe_forward_noalloc(const void* x, int x_dtype, int T, const i4_moe_weights* weights,
                            int topk, int renorm, const void* logits, const void* residual,
-                           void* out, int32_t* sel_out, float* w_out, hipStream_t stream) {
+                           void* out, int32_t* sel_out, float* w_out, int32_t* status_out,
+                           hipStream_t stream) {
   if (!weights) return I4_ERR_NULL;
   const size_t need = i4_moe_workspace_bytes(T, weights->gate_up.K, weights->down.K,
                                              weights->gate_up.E, topk);
@@ -64,8 +66,11 @@ int i4_moe_forward_noalloc(const void* x, int x_dtype, int T, const i4_moe_weigh
   void* ws = nullptr;
   const int rc = scratch_on(dev, &ws);
   if (rc) return rc;
-  return i4_moe_forward(x, x_dtype, T, weights, topk, renorm, logits, residual, out, sel_out,
-                        w_out, ws, (size_t)I4_NOALLOC_SCRATCH_BYTES, stream);
+  // the status word goes to status_out when given (the scratch's own copy is not
+  // reachable by the caller)
+  return i4::moe_forward_status(x, x_dtype, T, weights, topk, renorm, logits, residual, out,
+                                 sel_out, w_out, ws, (size_t)I4_NOALLOC_SCRATCH_BYTES,
+                                 status_out, stream);
 }
 
 }  // extern "C"

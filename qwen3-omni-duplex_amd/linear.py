@@ -57,6 +57,7 @@ class PackedLinear(nn.Module):
         self.register_buffer("scale", w.scale, persistent=False)
         self.register_buffer("zeros", w.zeros, persistent=False)
         self.register_buffer("bias", bias, persistent=False)
+        self.workspace = ops.Workspace()  # this module's split-K workspace, kept across calls
 
     @classmethod
     def from_qweight(cls, w: QWeight, bias: torch.Tensor | None = None,
@@ -71,8 +72,8 @@ class PackedLinear(nn.Module):
         rows = x.numel() // max(x.shape[-1], 1)
         if self.w_tile is not None and rows >= (TILE_ROWS if self.w.N >= 1024
                                                 else TILE_ROWS_NARROW):
-            return ops.linear(x, self.w_tile, self.bias)
-        return ops.linear(x, self.w, self.bias)
+            return ops.linear(x, self.w_tile, self.bias, workspace=self.workspace)
+        return ops.linear(x, self.w, self.bias, workspace=self.workspace)
 
 
 _SYM_ZEROS = -2004318072  # 0x88888888 as int32: every zero point 8

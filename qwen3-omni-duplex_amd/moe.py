@@ -43,8 +43,32 @@ def _stack_ct(linears, dtype, device):
     return packed, scale, out_f, in_f
 
 
+class _RouterGate(nn.Linear):
+    """The block's router Linear H -> E (FusedPackedMoE.gate, as the reference keeps
+    block.gate, fused_packed_moe.py:112).  Its weight is the router weight the library
+    reads; forward routes inside the library, so this module's own forward (and hooks on
+    it) run only when a caller invokes it.  Assigning its weight rebuilds the structs that
+    hold raw addresses of it."""
+
+    def __setattr__(self, name, value):
+        super().__setattr__(name, value)
+        ops.weights_changed()
+
+
 class FusedPackedMoE(nn.Module):
     """SparseMoeBlock replacement for int4-packed experts."""
+
+    def __setattr__(self, name, value):
+        if name == "router_w":  # the router weight is gate.weight
+            self.gate.weight = nn.Parameter(value.detach().contiguous(), requires_grad=False)
+        else:
+            super().__setattr__(name, value)
+        ops.weights_changed()
+
+    @property
+    def router_w(self) -> torch.Tensor:
+        """[E, H] router weight in the activation dtype: gate.weight (assignable)."""
+        return self.gate.weight
 
     def __init__(self, block: nn.Module | None = None, dtype=torch.bfloat16, device="cuda",
                  host_resident: bool = False, cpu_compute: bool = False, group: int = 32,
@@ -90,7 +114,9 @@ class FusedPackedMoE(nn.Module):
         self.inter = gate_up.N // 2
         self.hidden = gate_up.K
         self.hid_out, self.inter_in = down.N, down.K
-        self.register_buffer("router_w", router_w, persistent=False)
+        gate = _RouterGate(gate_up.K, gate_up.E, bias=False, device="meta")
+        gate.weight = nn.Parameter(router_w, requires_grad=False)
+        self.gate = gate
         self.register_buffer("norm_weight", norm_weight, persistent=False)
         self.norm_eps = float(norm_eps)
         bufs = [("gu_packed", gate_up.packed), ("gu_scale", gate_up.scale),

@@ -27,18 +27,37 @@ from . import _lib
 from .weights import QWeight
 
 
-def _ws(nbytes: int, device: torch.device, pending: bool = False) -> torch.Tensor | None:
-    """Per-call workspace; pending=True for the AWQ GEMV, whose split-K partials start as
-    the pending pattern (every byte 0xFF)."""
+def _gemv_ws(nbytes: int, device: torch.device, workspace: "Workspace | None",
+             kind: str = "awq"):
+    """The split-K workspace of an AWQ GEMV / linear call (None when the call needs none):
+    the caller's Workspace, else one kept per device and stream (the library takes one
+    workspace per stream).  Its status word must start at 0, so a workspace is zeroed when
+    it is allocated and never again: calls need no initial contents beyond that."""
     if nbytes == 0:
         return None
-    if pending:
-        return torch.full((nbytes,), 255, dtype=torch.uint8, device=device)
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if workspace is None:
+        key = (device.index, _lib.stream(device), kind)
+        workspace = _STREAM_WS.setdefault(key, Workspace())
+    return workspace.get(nbytes, device, zeroed=True)
+
+
+_STREAM_WS: dict = {}
+
+
+def gemv_status(workspace: "Workspace | None" = None, device: torch.device | None = None) -> int:
+    """The status word of an AWQ split-K GEMV workspace (the per-stream one when none is
+    given): 0, or the I4_ERR_HANDOFF code once a call on it gave up; synchronises."""
+    if workspace is None:
+        dev = device or torch.device("cuda", torch.cuda.current_device())
+        workspace = _STREAM_WS.get((dev.index, _lib.stream(dev), "awq"))
+    if workspace is None or workspace.buf is None:
+        return 0
+    torch.cuda.synchronize(workspace.buf.device)
+    return int(workspace.buf[:4].view(torch.int32).item())
 
 
 def dequant_gemv(x, packed, scale, sel, group=32, block_r=64, nw_blk=8, *, zeros=None,
-                 layout="ct", out_dtype=torch.float32):
+                 layout="ct", out_dtype=torch.float32, workspace=None):
     """y[j, r] = sum_c W[sel[j], r, c] * x[j, c], W dequantised from int4 on the fly.
 
     Same contract as the reference's dequant_gemv: x [K] (shared by every
@@ -69,7 +88,7 @@ def dequant_gemv(x, packed, scale, sel, group=32, block_r=64, nw_blk=8, *, zeros
     out = torch.empty(k, w.N, dtype=out_dtype, device=dev)
     lb = _lib.lib()
     cw = w.c()
-    ws = _ws(lb.i4_dq_gemv_workspace_bytes(ctypes.byref(cw), k), dev, pending=True)
+    ws = _gemv_ws(lb.i4_dq_gemv_workspace_bytes(ctypes.byref(cw), k), dev, workspace)
     _lib.check(lb.i4_dq_gemv(xc.data_ptr(), xt, s_x, ctypes.byref(cw), sel32.data_ptr(), k,
                              out.data_ptr(), _lib.dtype_code(out_dtype),
                              None if ws is None else ws.data_ptr(),
@@ -77,9 +96,34 @@ def dequant_gemv(x, packed, scale, sel, group=32, block_r=64, nw_blk=8, *, zeros
     return out
 
 
+def dequant_gemv_bounded(x: torch.Tensor, w: QWeight, sel: torch.Tensor, max_polls: int,
+                         reducers_only: bool, workspace: "Workspace",
+                         out_dtype=torch.float32) -> torch.Tensor:
+    """i4_dq_gemv_bounded: the AWQ split-K GEMV with a caller bound on its hand-over wait,
+    optionally only the reducing workgroups (whose partials then never arrive: the wait
+    gives up, NaN out, I4_ERR_HANDOFF in the workspace's status word).  x [k, K]."""
+    dev = _lib.require_device(x, w.packed, sel)
+    sel32 = sel.to(torch.int32).contiguous()
+    k = sel32.numel()
+    xc = x.reshape(k, w.K).contiguous()
+    out = torch.empty(k, w.N, dtype=out_dtype, device=dev)
+    lb = _lib.lib()
+    cw = w.c()
+    ws = _gemv_ws(lb.i4_dq_gemv_workspace_bytes(ctypes.byref(cw), k), dev, workspace)
+    _lib.check(lb.i4_dq_gemv_bounded(xc.data_ptr(), _lib.half_code(x.dtype), w.K,
+                                     ctypes.byref(cw), sel32.data_ptr(), k, out.data_ptr(),
+                                     _lib.dtype_code(out_dtype), _lib.ptr(ws),
+                                     0 if ws is None else ws.numel(), int(max_polls),
+                                     int(reducers_only), _lib.stream(dev)))
+    return out
+
+
 def linear(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
-           out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """y = x W^T (+ bias) for every row of x in one launch (E = 1 weight)."""
+           out_dtype: torch.dtype | None = None,
+           workspace: "Workspace | None" = None) -> torch.Tensor:
+    """y = x W^T (+ bias) for every row of x in one launch (E = 1 weight).  workspace: kept
+    by the caller for the calls that need one (an AWQ weight split along K, a tile weight
+    split along K); by default one per device and stream."""
     dev = _lib.require_device(x, w.packed, bias)
     xt = _lib.half_code(x.dtype)
     lead = x.shape[:-1]
@@ -96,7 +140,7 @@ def linear(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
             raise RuntimeError("bias length != out_features")
     lb = _lib.lib()
     cw = w.c()
-    ws = _ws(lb.i4_linear_workspace_bytes(ctypes.byref(cw), M), dev, pending=w.layout == "awq")
+    ws = _gemv_ws(lb.i4_linear_workspace_bytes(ctypes.byref(cw), M), dev, workspace, w.layout)
     _lib.check(lb.i4_linear(flat.data_ptr(), xt, M, ctypes.byref(cw), _lib.ptr(b), y.data_ptr(),
                             _lib.dtype_code(od), None if ws is None else ws.data_ptr(),
                             0 if ws is None else ws.numel(), _lib.stream(dev)))
@@ -231,9 +275,11 @@ class Workspace:
     def __init__(self) -> None:
         self.buf: torch.Tensor | None = None
 
-    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+    def get(self, nbytes: int, device: torch.device, zeroed: bool = False) -> torch.Tensor:
+        """At least nbytes; zeroed: a new buffer is allocated as zeros."""
         if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
-            self.buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+            make = torch.zeros if zeroed else torch.empty
+            self.buf = make(max(nbytes, 1), dtype=torch.uint8, device=device)
         return self.buf
 
 
@@ -321,12 +367,17 @@ def moe_forward_noalloc(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k:
                         norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
                         norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
                         gate_up_tile: QWeight | None = None, down_tile: QWeight | None = None,
-                        out: torch.Tensor | None = None) -> torch.Tensor:
+                        out: torch.Tensor | None = None,
+                        status: torch.Tensor | None = None) -> torch.Tensor:
     """moe_forward through i4_moe_forward_noalloc: the library's static per-GPU scratch
     replaces the workspace (no device allocation by the library; `out` may be given so that
-    nothing is allocated here either).  Calls that overlap on one GPU race."""
+    nothing is allocated here either).  Calls that overlap on one GPU race.  status (int32
+    device tensor of one element, optional) receives the call's status word: 0, or the
+    I4_ERR_HANDOFF code when a decode wait gave up."""
     dev = _lib.require_device(x, gate_up.packed, down.packed, router_w, logits, residual, norm_w,
-                              out)
+                              out, status)
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 1):
+        raise RuntimeError("status is an int32 device tensor")
     xt = _lib.half_code(x.dtype)
     xf = x.reshape(-1, x.shape[-1])
     if not xf.is_contiguous():
@@ -348,7 +399,7 @@ def moe_forward_noalloc(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k:
     _lib.check(_lib.lib().i4_moe_forward_noalloc(xf.data_ptr(), xt, T, ctypes.byref(mw), top_k,
                                                  int(norm_topk_prob), _lib.ptr(logits),
                                                  _lib.ptr(residual), out.data_ptr(), None, None,
-                                                 _lib.stream(dev)))
+                                                 _lib.ptr(status), _lib.stream(dev)))
     return out.view(x.shape)
 
 
@@ -441,7 +492,8 @@ class StackLayerX:
         dev = gu.packed.device
         self.dev = dev
         nbytes = _lib.lib().i4_moe_workspace_bytes(1, gu.K, dn.K, gu.E, top_k)
-        self.ws = (workspace or Workspace()).get(nbytes, dev)
+        self.ws_holder = workspace or Workspace()
+        self.ws = self.ws_holder.get(nbytes, dev)
 
     def route(self, res: torch.Tensor, ypart: torch.Tensor | None = None,
               h_out: torch.Tensor | None = None, reset_status: bool = False) -> None:
@@ -565,6 +617,16 @@ def attn_decode_o(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: to
     return y
 
 
+def attn_status(workspace: Workspace, n_heads: int, head_dim: int, max_len: int) -> int:
+    """The status word the last attn_decode_o call with this workspace left (0, or the
+    I4_ERR_HANDOFF code when an o_proj wait gave up); synchronises the device."""
+    off = _lib.lib().i4_attn_decode_o_status_offset(n_heads, head_dim, max_len)
+    if workspace.buf is None or workspace.buf.numel() < off + 4:
+        raise RuntimeError("the workspace has not served a call of these sizes")
+    torch.cuda.synchronize(workspace.buf.device)
+    return int(workspace.buf[off:off + 4].view(torch.int32).item())
+
+
 def thinker_layer_fits(n_heads: int, n_kv_heads: int, head_dim: int, max_len: int, H: int,
                       I: int, E: int, top_k: int) -> bool:
     """Whether i4_thinker_layer_decode takes a layer of these sizes."""
@@ -625,6 +687,19 @@ def thinker_layer_decode(h: torch.Tensor, in_norm_w: torch.Tensor, eps: float, q
         k_cache.data_ptr(), v_cache.data_ptr(), max_len, ctypes.byref(ow), ctypes.byref(mw),
         top_k, int(norm_topk_prob), out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(dev)))
     return out.view(h.shape)
+
+
+_WEIGHTS_GEN = [0]
+
+
+def weights_changed() -> None:
+    """Called when a tensor attribute of a decoder module is assigned: structs holding raw
+    addresses of the old tensors are rebuilt before their next use."""
+    _WEIGHTS_GEN[0] += 1
+
+
+def weights_generation() -> int:
+    return _WEIGHTS_GEN[0]
 
 
 def thinker_layer_c(attn, moe) -> _lib.ThinkerLayerC:

@@ -91,7 +91,13 @@ def test_call_validation_codes(pkg):
     # shapes, it runs K-complete workgroups; CT needs none; AWQ scales are read 16 bytes
     # at a time
     wa = _qw(_lib, layout=1, N=256, K=4096, group=128)
-    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wa), 8) == 8 * 1 * 32 * 256 * 4
+    # 256-byte header (the status word), then (value, tag) pairs of 8 bytes
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wa), 8) == 256 + 8 * 1 * 32 * 256 * 8
+    # more than 8 rows, or partials beyond 8 MiB, run K-complete: no workspace
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wa), 9) == 0
+    wbig = _qw(_lib, layout=1, N=4096, K=4096, group=128)
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wbig), 1) == 256 + 16 * 32 * 256 * 8
+    assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(wbig), 8) == 0
     assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(_qw(_lib, layout=1)), 8) == 0
     assert lib.i4_dq_gemv_workspace_bytes(ctypes.byref(_qw(_lib, layout=1, N=40, K=4096)),
                                           8) == 0
@@ -101,7 +107,7 @@ def test_call_validation_codes(pkg):
     assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(wa), 0x40000, 8, 0x50000, 0, 0x60010,
                           1 << 20, None) == -4
     assert lib.i4_linear_workspace_bytes(
-        ctypes.byref(_qw(_lib, layout=1, E=1, N=256, K=4096, group=128)), 1) == 32 * 256 * 4
+        ctypes.byref(_qw(_lib, layout=1, E=1, N=256, K=4096, group=128)), 1) == 256 + 32 * 256 * 8
     wa_odd = _qw(_lib, layout=1, scale=0x20008)
     assert lib.i4_dq_gemv(0x30000, 1, 0, ctypes.byref(wa_odd), 0x40000, 8, 0x50000, 0, None, 0,
                           None) == -4
@@ -232,7 +238,10 @@ def test_decode_attention_validation_codes(pkg):
     # with o_proj: a CT weight of K = n_heads * head_dim, and a larger workspace (the
     # merged heads live in it after the partials, at a 256-byte boundary)
     wso = lib.i4_attn_decode_o_workspace_bytes(32, 128, 4096)
-    assert wso == ((ws + 255) & ~255) + 32 * 128 * 2
+    # ... the o_proj wait's status word in a 256-byte slot in front of them (the router-fold
+    # launch of the decoder layer keeps its output directly behind the merged heads)
+    assert lib.i4_attn_decode_o_status_offset(32, 128, 4096) == (ws + 255) & ~255
+    assert wso == ((ws + 255) & ~255) + 256 + 32 * 128 * 2
     ow = _qw(_lib, E=1, N=2048, K=4096, group=32)
     callo = lambda **kw: lib.i4_attn_decode_o(
         0x30000, 2, kw.get("nh", 32), 4, 128, 0x40000, 0x50000, 1e-6, tab, kw.get("pd", None),

@@ -89,6 +89,23 @@ def test_fuse_packed_moe_blocks_replaces_the_block(pkg, dev, dtype):
     assert (m.num_experts, m.hidden, m.inter, m.top_k) == (E, H, I, K8)
     assert m.gate_up.layout == "ct" and m.gate_up_tile is not None
     assert m.router_w.dtype == dtype and m.gate_up.scale.dtype == dtype
+    # the router stays the block's `gate` Linear (fused_packed_moe.py:112), holding the
+    # router weight the library reads; a new gate weight changes the routing
+    assert isinstance(m.gate, nn.Linear) and m.gate.weight is m.router_w
+    assert torch.equal(m.gate.weight.float().cpu(),
+                       packed_block.gate.weight.detach().to(dtype).float())
+    xg = t_(make_x(np.random.default_rng(103), (1, H), "bf16" if dtype == torch.bfloat16
+                   else "f16"), dev)
+    lg_lib = pkg.router_logits(xg, m.router_w).float()
+    lg_torch = m.gate(xg.float().to(dtype)).float()
+    assert torch.allclose(lg_lib, lg_torch, rtol=2e-2, atol=2e-2)
+    saved = m.gate.weight
+    sel_before = m.route(xg)[1]
+    m.gate.weight = nn.Parameter(torch.flip(saved, dims=[0]), requires_grad=False)
+    # expert e's row is now E-1-e's: the same selection (equal logits, which bf16 makes
+    # common, may then rank in another order: ties go to the lower id)
+    assert torch.equal(m.route(xg)[1].sort().values, (E - 1 - sel_before).sort().values)
+    m.gate.weight = saved
     # the stacked gate | up rows are the experts' own words, gate rows first
     gp, _, up, _, dp, _ = packed_block.np
     for e in (0, 77, 127):
@@ -127,7 +144,7 @@ def test_routing_end_to_end_on_the_workload_inputs(pkg, dev):
     OWN fp16 logits (the exact product of the same fp16 x and router weight, rounded once):
     no mismatch on any row whose 8th / 9th logits are more than 1 ulp apart (the GPU's fp32
     accumulation may round a logit to its neighbour, so closer rows may legitimately differ);
-    the rate over all rows is reported."""
+    the count and rate over all rows are printed, and the rate is at most 5 %."""
     rng = np.random.default_rng(103)
     moe, _, _, wr = _awq_moe(pkg, dev, rng)
     rows = []
@@ -152,6 +169,7 @@ def test_routing_end_to_end_on_the_workload_inputs(pkg, dev):
           f"logits ({mismatch / len(rows):.2%}); {clear} rows with a > 1 ulp top-8 margin, "
           f"{clear_mismatch} of them differ")
     assert clear >= 0.9 * len(rows)
+    assert mismatch <= max(2, 0.05 * len(rows)), (mismatch, len(rows))
     # sel is in descending order: a swap inside the top 8 is a mismatch too unless the two
     # logits are within an ulp, which the margin rule does not cover, so allow exactly those
     for T, lg, got in rows:
@@ -328,3 +346,53 @@ def test_stack_experts_wait_gives_up_visibly(pkg, dev):
     torch.cuda.synchronize()
     assert pkg.ops.moe_status(ws, 1, H, I, 64, K8) == 0
     assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+def test_decode_layer_against_the_reference_rounding(pkg, dev, xdt):
+    """The decode layer (C3: 128 experts, top-8, 2048 / 768, AWQ g128, with the residual)
+    against the oracle in the reference's own rounding of the combine (routing weights and
+    expert outputs rounded to the activation dtype, 16-bit products, fp32 sum rounded once,
+    then the residual add; fused_packed_moe.py:199,262) as well as against the float64
+    combine.  The build keeps the weights and the weighted sum in fp32 and rounds once, so
+    it sits between the two; its distance from the reference's rounding is within the
+    parity bar (2e-2 of max |ref|) and, elementwise, within a few ulps of the largest
+    added term; the measured distances are printed."""
+    rng = np.random.default_rng(110 + (xdt == "bf16"))
+    sdt = "bf16" if xdt == "bf16" else np.float16
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, sdt=sdt)
+    tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    moe.router_w = moe.router_w.to(tdt)
+    hn = half_name(xdt)
+    worst_rel, worst_ulp = 0.0, 0.0
+    for rep in range(4):
+        x = make_x(rng, (1, H), xdt)
+        res = make_x(rng, (1, H), xdt)
+        out, sel, w = pkg.moe_forward(t_(x, dev), moe.gate_up, moe.down, K8,
+                                      router_w=moe.router_w, residual=t_(res, dev),
+                                      return_routing=True, gate_up_tile=moe.gate_up_tile,
+                                      down_tile=moe.down_tile)
+        lg = host(pkg.router_logits(t_(x, dev), moe.router_w))
+        sel_ref, w_ref = i4ref.route(lg, K8)
+        np.testing.assert_array_equal(sel.cpu().numpy(), sel_ref)
+        xin, r = f_(x)[0], f_(res)[0]
+        ys = []
+        for e in sel_ref[0]:
+            gu = dgu(int(e)) @ xin
+            a = i4ref.round_half(i4ref.silu(gu[:I]) * gu[I:], hn)
+            ys.append(i4ref.round_half(ddn(int(e)) @ a, hn))
+        ys = np.stack(ys)
+        ref_rounding = i4ref.ref_combine(ys, w_ref[0], hn, r)
+        exact = r + (w_ref[0][:, None] * ys).sum(0)
+        got = host(out)[0]
+        rel = i4ref.rel_err(got, ref_rounding)
+        scale = np.maximum(np.maximum(np.abs(r), np.abs(exact - r)),
+                           np.max(np.abs(w_ref[0][:, None] * ys), axis=0))
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(scale, 2.0 ** -14))) - (10 if hn == "f16" else 7))
+        worst_rel = max(worst_rel, rel)
+        worst_ulp = max(worst_ulp, float(np.max(np.abs(got - ref_rounding) / ulp)))
+        assert rel <= 2e-2, rel
+        assert i4ref.rel_err(got, exact) <= 2e-2
+    print(f"\n{xdt}: build vs the reference's rounding: max|err|/max|ref| {worst_rel:.2e}, "
+          f"{worst_ulp:.1f} ulps of the largest term")
+    assert worst_ulp <= 8, worst_ulp

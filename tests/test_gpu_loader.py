@@ -281,14 +281,19 @@ def test_attn_decode_o_equals_attention_then_o_proj(pkg, dev, xdt, nh, nkv, pos,
     kc, vc = cache[0].clone(), cache[1].clone()
     a = pkg.attn_decode(qkv, nh, nkv, qn, kn, 1e-6, inv, pos, kc, vc)
     want = pkg.linear(a.view(1, -1), w, bias=res).view(-1)
+    ws = pkg.Workspace()
     for dev_pos in (False, True):
         kc2, vc2 = cache[0].clone(), cache[1].clone()
         pp = torch.full((1,), pos, dtype=torch.int32, device=dev) if dev_pos else pos
-        got = pkg.attn_decode_o(qkv, nh, nkv, qn, kn, 1e-6, inv, pp, kc2, vc2, w, res)
+        if ws.buf is not None:
+            ws.buf.fill_(0xA5)  # the status word is rewritten by every call
+        got = pkg.attn_decode_o(qkv, nh, nkv, qn, kn, 1e-6, inv, pp, kc2, vc2, w, res,
+                                workspace=ws)
         torch.cuda.synchronize()
         assert torch.isfinite(got.float()).all()
         assert torch.equal(got, want), dev_pos
         assert torch.equal(kc2, kc) and torch.equal(vc2, vc)
+        assert pkg.ops.attn_status(ws, nh, hd, max_len) == 0
     # the o_proj GEMV itself against the oracle's fp32 product on the same attention output
     W = i4ref.ct_dequant(p, w.scale.float().cpu().numpy(), K, G, zeros=z)[0]
     ref = np.asarray(host(a), np.float64) @ W.T.astype(np.float64) + np.asarray(host(res), np.float64)

@@ -293,9 +293,10 @@ def test_dq_gemv_awq(pkg, dev, N, K, xdt, G):
 @pytest.mark.parametrize("N,K,G", [(768, 2048, 128), (4096, 2048, 128), (96, 8192, 64)])
 def test_dq_gemv_awq_split_k_handover(pkg, dev, N, K, G):
     """Both AWQ kernels through the C ABI: split along K (workspace given) and K-complete
-    (no workspace) each match the oracle.  The split launch's partials start as the pending
-    pattern and every call leaves them so, so five calls in a row on one workspace give
-    identical outputs (the last slice of a strip adds the partials in a fixed order)."""
+    (no workspace) each match the oracle.  The split launch's partials carry a tag of their
+    call, so a workspace of random bytes (status word zeroed) serves, and five calls in a row
+    on it give identical outputs (the last slice of a strip adds the partials in a fixed
+    order) and leave every tag cleared and the status word 0."""
     from qwen3_omni_duplex_amd import _lib
 
     lb = pkg.lib()
@@ -309,8 +310,9 @@ def test_dq_gemv_awq_split_k_handover(pkg, dev, N, K, G):
     xd, seld = t_(x, dev), t_(sel, dev)
     cw = w.c()
     nb = lb.i4_dq_gemv_workspace_bytes(ctypes.byref(cw), k)
-    assert nb > 0
-    ws = torch.full((nb,), 255, dtype=torch.uint8, device=dev)
+    assert nb > 256
+    ws = torch.from_numpy(rng.integers(0, 256, nb, dtype=np.uint8)).to(dev)
+    ws[:4] = 0
     stream = torch.cuda.current_stream().cuda_stream
 
     def run(wsp):
@@ -327,14 +329,58 @@ def test_dq_gemv_awq_split_k_handover(pkg, dev, N, K, G):
     for _ in range(5):
         outs.append(run(ws))
         torch.cuda.synchronize()
-        assert bool((ws == 255).all())
     for y in outs[1:]:
         assert torch.equal(y, outs[0])
     assert i4ref.rel_err(host(outs[0]), ref) <= 1e-4
+    assert pkg.ops.gemv_status(_WsView(ws)) == 0
+    # every (value, tag) pair a reducer read has its tag cleared for the next call
+    if N % 256 == 0:  # whole strips: every column of slices 0..P-2 was read
+        strips = ws[256:].view(torch.int32).view(k, N // 256, -1, 256, 2)
+        assert bool((strips[:, :, :-1, :, 1] == 0).all())
     # a workspace one byte short is refused before anything runs
     y = torch.empty(k, N, dtype=torch.float16, device=dev)
     assert lb.i4_dq_gemv(xd.data_ptr(), _lib.F16, K, ctypes.byref(cw), seld.data_ptr(), k,
                          y.data_ptr(), _lib.F16, ws.data_ptr(), nb - 1, stream) == -7
+
+
+class _WsView:
+    """A raw workspace tensor as the ops.Workspace the status readers take."""
+
+    def __init__(self, buf):
+        self.buf = buf
+
+
+@pytest.mark.parametrize("N,K", [(4096, 2048), (2048, 4096)])
+def test_dq_gemv_awq_split_k_wait_gives_up_visibly(pkg, dev, N, K):
+    """The split launch's reducers run alone (i4_dq_gemv_bounded, reducers_only) with the
+    bound on their wait lowered from the host: the partials never arrive, so every reducer
+    gives up, writes NaN, clears its strip's tags and stores I4_ERR_HANDOFF in the status
+    word; every kernel exits.  The next ordinary calls on the same workspace are correct."""
+    G, k = 128, 1
+    rng = np.random.default_rng(N + K)
+    qw, qz, sc = _gen.awq_weight(rng, 2, K, N, G)
+    w = pkg.QWeight(t_(qw, dev), t_(sc, dev), t_(qz, dev), "awq", G, N, K)
+    sel = t_(np.array([1], np.int32), dev)
+    x = make_x(rng, (k, K), "f16")
+    ref = i4ref.dq_gemv(f_(x), i4ref.awq_dequant(qw, qz, sc, G), np.array([1]))
+    ws = pkg.Workspace()
+    for polls in (0, 3):
+        y = pkg.ops.dequant_gemv_bounded(t_(x, dev), w, sel, polls, True, ws)
+        torch.cuda.synchronize()
+        assert torch.isnan(y).all()
+        assert pkg.ops.gemv_status(ws) == -10
+    y = pkg.ops.dequant_gemv_bounded(t_(x, dev), w, sel, 1 << 20, False, ws)
+    assert i4ref.rel_err(host(y), ref) <= 1e-4
+    assert pkg.ops.gemv_status(ws) == -10  # kept until the caller clears it
+    ws.buf[:4] = 0
+    y2 = pkg.dequant_gemv(t_(x, dev), w.packed, w.scale, sel, group=G, zeros=w.zeros,
+                          layout="awq", workspace=ws)
+    assert torch.equal(y2, y)
+    assert pkg.ops.gemv_status(ws) == 0
+    # only a split launch has reducers; a CT weight has no hand-over at all
+    wc = w.to_ct()
+    with pytest.raises(RuntimeError):
+        pkg.ops.dequant_gemv_bounded(t_(x, dev), wc, sel, 3, True, ws)
 
 
 @pytest.mark.parametrize("M", [1, 5])
@@ -768,7 +814,7 @@ def test_moe_mfma_tiles(pkg, dev, xdt):
     sdt = "bf16" if xdt == "bf16" else np.float16
     moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, E=E, sdt=sdt)
     if xdt == "bf16":
-        moe.register_buffer("router_w", moe.router_w.to(torch.bfloat16), persistent=False)
+        moe.router_w = moe.router_w.to(torch.bfloat16)
     x = make_x(rng, (T, H), xdt)
     lg = rng.standard_normal((T, E)).astype(np.float32)
     lg = i4ref.f32_to_bf16_bits(lg) if xdt == "bf16" else lg.astype(np.float16)
@@ -801,7 +847,7 @@ def test_moe_prefill_bf16_small_entries(pkg, dev):
     MFMA kernel's activation-sum correction."""
     rng = np.random.default_rng(35)
     moe, dgu, ddn, wr = _awq_moe(pkg, dev, rng, sdt="bf16")
-    moe.register_buffer("router_w", moe.router_w.to(torch.bfloat16), persistent=False)
+    moe.router_w = moe.router_w.to(torch.bfloat16)
     x = make_x(rng, (24, 2048), "bf16")
     _check_moe(pkg, moe, dgu, ddn, x, "bf16", dev)
 
@@ -859,7 +905,7 @@ def _stack_modules(pkg, dev, rng, xdt, norm, n_distinct=3):
     for _ in range(n_distinct):
         m, _, _, _ = _awq_moe(pkg, dev, rng, E=32, sdt=sdt)
         tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
-        m.register_buffer("router_w", m.router_w.to(tdt), persistent=False)
+        m.router_w = m.router_w.to(tdt)
         if norm:
             nw = torch.from_numpy(rng.uniform(0.5, 1.5, 2048).astype(np.float32)).to(dev, tdt)
             m.register_buffer("norm_weight", nw, persistent=False)

@@ -349,6 +349,55 @@ def test_moe_grouped_equals_per_token_with_output_rounding():
     assert 0 < np.max(np.abs(a - c)) <= 2.0 ** -8 * np.max(np.abs(c))
 
 
+@pytest.mark.parametrize("dt,tdt", [("bf16", torch.bfloat16), ("f16", torch.float16)])
+def test_ref_combine_matches_the_reference_expression(dt, tdt):
+    """ref_combine equals torch's own evaluation of the reference's combine,
+    (y.to(x.dtype) * w.to(x.dtype)[:, None]).sum(dim=0) then + residual in the activation
+    dtype (fused_packed_moe.py:199,262 and the decoder layer's residual add), bit for bit
+    on many columns; dropping the weights' rounding (a plausible slip) is caught."""
+    rng = np.random.default_rng(31)
+    for trial in range(6):
+        k, H = 8, 4096
+        ys = rng.standard_normal((k, H)) * (3.0 if trial % 2 else 0.05)
+        w = rng.dirichlet(np.ones(k))
+        res = rng.standard_normal(H)
+        y32 = torch.from_numpy(ys.astype(np.float32))
+        w32 = torch.from_numpy(w.astype(np.float32))
+        r16 = torch.from_numpy(res.astype(np.float32)).to(tdt)
+        want = r16 + (y32.to(tdt) * w32.to(tdt).unsqueeze(-1)).sum(dim=0)
+        want = want.float().double().numpy()
+        got = i4ref.ref_combine(y32.double().numpy(), w32.double().numpy(), dt,
+                                r16.float().double().numpy())
+        np.testing.assert_array_equal(got, want)
+        slip = i4ref.round_half(i4ref.round_half(
+            (i4ref.round_half(y32.double().numpy(), dt) * w32.double().numpy()[:, None]).sum(0),
+            dt) + r16.float().double().numpy(), dt)
+        assert not np.array_equal(slip, want)
+
+
+def test_moe_layer_reference_combine_is_near_the_exact_one():
+    """combine="reference" (the reference's own rounding) and the float64 combine of the
+    same layer differ by the 16-bit rounding of the products, the sum and the residual add
+    only: within a few units in the last place of the larger of the two added terms (the
+    residual and the MoE term; where they cancel the output's own ulp is smaller)."""
+    rng = np.random.default_rng(32)
+    E, H, I, k, T = 6, 64, 32, 4, 5
+    Wgu = rng.standard_normal((E, 2 * I, H)) * 0.1
+    Wdn = rng.standard_normal((E, H, I)) * 0.1
+    x = i4ref.round_half(rng.standard_normal((T, H)), "bf16")
+    res = i4ref.round_half(rng.standard_normal((T, H)), "bf16")
+    sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+    w = rng.dirichlet(np.ones(k), size=T)
+    exact = i4ref.moe_layer(x, sel, w, Wgu, Wdn, "bf16", residual=res, out_dtype="bf16",
+                            y_dtype="bf16")
+    ref = i4ref.moe_layer(x, sel, w, Wgu, Wdn, "bf16", residual=res, y_dtype="bf16",
+                          combine="reference")
+    scale = np.maximum(np.abs(res), np.abs(exact - res))
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(scale, 2.0 ** -14))) - 7)
+    assert np.all(np.abs(ref - exact) <= 4 * ulp)
+    assert not np.array_equal(ref, exact)
+
+
 def test_cpu_baseline_matches_the_oracle():
     """The timed CPU baseline (oracle/cpu_baseline.py, the reference's CPU expert path in torch
     fp32) computes the oracle's MoE layer on seeded AWQ inputs, and its reference_gemv

@@ -18,8 +18,10 @@ def _both(pkg, moe, x, res):
     kw = dict(router_w=moe.router_w, residual=res, gate_up_tile=moe.gate_up_tile,
               down_tile=moe.down_tile)
     want = pkg.moe_forward(x, moe.gate_up, moe.down, K8, **kw)
-    got = pkg.moe_forward_noalloc(x, moe.gate_up, moe.down, K8, **kw)
+    status = torch.full((1,), 12345, dtype=torch.int32, device=x.device)
+    got = pkg.moe_forward_noalloc(x, moe.gate_up, moe.down, K8, status=status, **kw)
     torch.cuda.synchronize()
+    assert int(status.item()) == 0  # the call rewrites the caller's status word
     return got, want
 
 
