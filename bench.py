@@ -437,10 +437,10 @@ def time_gemvs(pkg, torch, dev, replays=20):
         out[f"single_{layout}"] = stats(ts, n1, nbytes)
         log(f"GEMV 2048->768 ({layout}): {out[f'single_{layout}']['us']:.2f} us")
     # the same GEMV through the Python module path (PackedLinear.forward -> ops.linear ->
-    # i4_linear, each module with its own kept workspace) on 64 of the copies: eager calls,
+    # i4_linear, each module with its own kept workspace) on the same copies: eager calls,
     # host dispatch included, and the same calls captured in a hipGraph (what the module
     # path enqueues on the device)
-    n_py = 64
+    n_py = n1
     py = {}
     for li, layout in enumerate(("awq", "ct")):
         w = single.keep[li]
@@ -469,8 +469,9 @@ def time_gemvs(pkg, torch, dev, replays=20):
                       "us_eager_wall": round(wall, 3), "us_graph": g["us"],
                       "us_graph_p99": g["us_p99"]}
         del lins
-    py["timing"] = ("PackedLinear.forward on 64 copies, eager (HIP events and wall clock "
-                    "around 5 passes) and as one hipGraph of the 64 calls (mean over replays)")
+    py["timing"] = (f"PackedLinear.forward on the {n_py} copies, eager (HIP events and wall "
+                    f"clock around 5 passes) and as one hipGraph of the {n_py} calls (mean over "
+                    "replays)")
     out["python_linear"] = py
     log("PackedLinear 2048->768: " + ", ".join(
         f"{k} eager {v['us_eager']:.2f} / graph {v['us_graph']:.2f} us"

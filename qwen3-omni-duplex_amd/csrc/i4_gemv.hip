@@ -166,13 +166,14 @@ __global__ __launch_bounds__(WG) void k_gemv_awq(
 //   butterfly (xor 8, 16, 32: each step keeps half the columns) and then
 //   across the waves in LDS, and the slice's scale (loaded with the weights)
 //   is applied once per column: a slice lies inside one quantisation group.
-// Hand-over without atomics or fences: slices 0..P-2 of a strip store their
-// fp32 partials (1 KB) write-through and exit, each column as one 8-byte store of
-// (value, tag) with the call's tag (a number the host gives every call, never 0);
-// slice P-1, dispatched after them, reads the other partials from memory until every
-// one carries the call's tag, sums them in a fixed order (slice classes s mod NWAVE,
-// then its own slice), writes y, and clears the tags it read (so a captured graph,
-// which replays one tag, finds them pending again).  A partial left by an earlier
+// Hand-over without atomics or fences, inside one XCD: every slice of a strip runs on
+// the same XCD, slices 0..P-2 store their fp32 partials (1 KB) into that XCD's L2 and
+// exit, each column as one 8-byte store of (value, tag) with the call's tag (a number
+// the host gives every call, never 0); slice P-1, dispatched after them, reads the
+// other partials past its L1 (from the L2 that holds them) until every one carries the
+// call's tag, sums them in a fixed order (slice classes s mod NWAVE, then its own
+// slice), writes y, and clears the tags it read (so a captured graph, which replays one
+// tag, finds them pending again).  A partial left by an earlier
 // call never carries this call's tag, so the workspace needs no initial contents.
 // A reducer that polls max_polls times without seeing every partial writes NaN,
 // clears the tags of its whole strip and stores I4_ERR_HANDOFF in the status word
@@ -192,9 +193,19 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
   __shared__ f32x4 red[NWAVE][64];
   __shared__ int s_gave_up;  // the reducer's wait gave up (set before the first barrier)
   // only_last: the reducers alone (grid S), whose partials then never arrive -- the host's
-  // way of making the wait give up in a test
-  const int strip = only_last ? (int)blockIdx.x : (int)blockIdx.x / P;
-  const int slice = only_last ? P - 1 : (int)blockIdx.x % P;
+  // way of making the wait give up in a test.  Otherwise every slice of a strip runs on
+  // one XCD (block b on XCD b % 8; strip x + 8 l takes the P blocks b = 8 (l P + slice)
+  // + x, past S: none), so the partials are handed over through that XCD's L2
+  int strip, slice;
+  if (only_last) {
+    strip = (int)blockIdx.x;
+    slice = P - 1;
+  } else {
+    const int i = (int)blockIdx.x >> 3;
+    strip = ((int)blockIdx.x & 7) + 8 * (i / P);
+    slice = i % P;
+    if (strip >= S) return;
+  }
   const int j = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int q = t & 7, rp = t >> 3;
@@ -320,7 +331,7 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
       if (ncol[c] >= 0)
         __hip_atomic_store(strip_part + (int64_t)slice * SK_COLS + (ncol[c] & 255),
                            (uint64_t)__builtin_bit_cast(u32, mine[c]) | ((uint64_t)tag << 32),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return;
   }
 
@@ -373,16 +384,16 @@ __global__ __launch_bounds__(64 * NWAVE) void k_gemv_awq_sk(
           a4 += f32x4{__builtin_bit_cast(float, va[0]), __builtin_bit_cast(float, va[2]),
                       __builtin_bit_cast(float, vb[0]), __builtin_bit_cast(float, vb[2])};
           const u32 o = (u32)(sl * SK_COLS + 4 * cg) * 8u;  // tags cleared for a replay
-          __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o, 0, kCoherent);
-          __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o + 16u, 0, kCoherent);
+          __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o + 16u, 0, 0);
         }
       }
     }
     if (gave_up) {  // every tag of the strip cleared, including partials not seen yet
       for (int sl = so; sl < P - 1; sl += NWAVE) {
         const u32 o = (u32)(sl * SK_COLS + 4 * cg) * 8u;
-        __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o, 0, kCoherent);
-        __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o + 16u, 0, kCoherent);
+        __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(zero4, pr, o + 16u, 0, 0);
       }
       s_gave_up = 1;
     }
@@ -745,13 +756,15 @@ static int launch_gemv_awq_t(const void* x, int64_t x_stride, const i4_qweight* 
 
 // Split-K plan of the AWQ GEMV: waves per workgroup, row pairs per thread
 // (slice = 16 * waves * pairs rows), strips, slices; waves == 0: the shape
-// keeps the K-complete kernel.  The hand-over costs about 2 us (measured: the
-// split launch takes 5.5-6.0 us at 2048 -> 512 / 768 against 4.9 / 5.8
-// K-complete, 6.5 / 6.8 at 2048 -> 4096 and 4096 -> 2048 against 8.5-9.6), so
-// the split is taken only where the K-complete launch fills more than 2048 rows
-// of lines per CU (K rows per workgroup, N / 8 workgroups per row of x over 256
-// CUs), and only for up to kSplitRows rows of x (decode: the plan was measured at
-// one row) whose partials fit kSplitBytes; more rows run K-complete.  Its slice is
+// keeps the K-complete kernel.  Measured on one MI355X with the hand-over inside an
+// XCD (each GEMV one of 64 distinct weight copies, back to back in a graph): the split
+// launch takes 5.75 us at 2048 -> 4096 and 6.3 us at 4096 -> 2048 (through memory
+// across XCDs: 7.2 / 8.1; K-complete: 8.5-9.6), but 6.0 us at 2048 -> 768 and 5.5 at
+// 2048 -> 512 with at least 64 workgroups against 5.8 / 4.9 K-complete.  So the split
+// is taken only where the K-complete launch fills more than 2048 rows of lines per CU
+// (K rows per workgroup, N / 8 workgroups per row of x over 256 CUs), and only for up
+// to kSplitRows rows of x (decode: the plan was measured at one row) whose partials
+// fit kSplitBytes; more rows run K-complete.  Its slice is
 // the largest of 128 / 64 / 32 rows that divides K and the group: a slice's loads
 // are one round trip at any of these sizes, and fewer slices make fewer partials to
 // hand over.
@@ -799,7 +812,7 @@ static int launch_gemv_awq_sk_t(const void* x, int64_t x_stride, const i4_qweigh
                                 bool reducers_only, hipStream_t s) {
   int gshift = 0;
   while ((1 << gshift) < w->group) ++gshift;
-  const dim3 grid(reducers_only ? p.S : p.S * p.P, k_sel);
+  const dim3 grid(reducers_only ? p.S : 8 * ((p.S + 7) / 8) * p.P, k_sel);
   int32_t* status = (int32_t*)ws;
   uint64_t* part = (uint64_t*)((char*)ws + SK_HEAD);
   const u32 tag = next_call_tag();

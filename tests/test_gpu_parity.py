@@ -898,32 +898,33 @@ def test_stack_matches_layer_loop_and_oracle(pkg, dev):
     assert torch.equal(stack, h)
 
 
-def _stack_modules(pkg, dev, rng, xdt, norm, n_distinct=3):
-    """n_distinct small blocks (32 experts, H 2048, I 768) in the activation dtype xdt."""
+def _stack_modules(pkg, dev, rng, xdt, norm, n_distinct=3, H=2048, I=768):
+    """n_distinct small blocks (32 experts, H x I) in the activation dtype xdt."""
     sdt = "bf16" if xdt == "bf16" else np.float16
     mods = []
     for _ in range(n_distinct):
-        m, _, _, _ = _awq_moe(pkg, dev, rng, E=32, sdt=sdt)
+        m, _, _, _ = _awq_moe(pkg, dev, rng, E=32, H=H, I=I, sdt=sdt)
         tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
         m.router_w = m.router_w.to(tdt)
         if norm:
-            nw = torch.from_numpy(rng.uniform(0.5, 1.5, 2048).astype(np.float32)).to(dev, tdt)
+            nw = torch.from_numpy(rng.uniform(0.5, 1.5, H).astype(np.float32)).to(dev, tdt)
             m.register_buffer("norm_weight", nw, persistent=False)
             m.norm_eps = 1e-6
         mods.append(m)
     return mods
 
 
-@pytest.mark.parametrize("xdt,norm,n_layers", [("f16", True, 26), ("bf16", True, 5),
-                                               ("f16", False, 3), ("bf16", False, 1)])
-def test_stack_matches_layer_loop_variants(pkg, dev, xdt, norm, n_layers):
+@pytest.mark.parametrize("xdt,norm,n_layers,H,I", [
+    ("f16", True, 26, 2048, 768), ("bf16", True, 5, 2048, 768), ("f16", False, 3, 2048, 768),
+    ("bf16", False, 1, 2048, 768), ("bf16", True, 4, 1024, 384), ("f16", False, 2, 1024, 384)])
+def test_stack_matches_layer_loop_variants(pkg, dev, xdt, norm, n_layers, H, I):
     """The one-call decode stack equals the module-by-module loop bit for bit: an even and an
-    odd number of layers (the call alternates its outputs between the workspace and out), bf16,
-    and without the RMSNorm."""
+    odd number of layers (the call alternates its buffers by layer parity), bf16, without
+    the RMSNorm, and at hidden size 1024."""
     rng = np.random.default_rng(61 + n_layers)
-    mods = _stack_modules(pkg, dev, rng, xdt, norm)
+    mods = _stack_modules(pkg, dev, rng, xdt, norm, H=H, I=I)
     layers = [mods[i % len(mods)] for i in range(n_layers)]
-    x = make_x(rng, (1, 2048), "f16") * (1.0 if norm else 0.1)  # un-normalised layers grow
+    x = make_x(rng, (1, H), "f16") * (1.0 if norm else 0.1)  # un-normalised layers grow
     xt = t_(i4ref.f32_to_bf16_bits(x.astype(np.float32)) if xdt == "bf16" else x, dev)
     stack = pkg.moe_stack(xt, [m.stack_entry() for m in layers], 8)
     h = xt
@@ -934,7 +935,7 @@ def test_stack_matches_layer_loop_variants(pkg, dev, xdt, norm, n_layers):
     ws = pkg.Workspace()
     again = pkg.moe_stack(xt, [m.stack_entry() for m in layers], 8, workspace=ws)
     assert torch.equal(again, stack)
-    assert pkg.moe_status(ws, 1, 2048, 768, 32, 8) == 0
+    assert pkg.moe_status(ws, 1, H, I, 32, 8) == 0
 
 
 @pytest.mark.parametrize("norm,top_k,n_layers", [(True, 8, 4), (False, 4, 3)])
