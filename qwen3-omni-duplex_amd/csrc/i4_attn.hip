@@ -27,7 +27,10 @@
 namespace i4 {
 
 static constexpr int HD = 128;    // head_dim
-static constexpr int ACH = 64;    // cached positions per attention workgroup
+// cached positions per attention workgroup (32 gives 272 workgroups at the Thinker's
+// context 1024 instead of 136, but measured 819 against 814 us per decode step: the
+// merge's extra batch of chunk loads outweighs the shorter chunks)
+static constexpr int ACH = 64;
 static constexpr int GQMAX = 8;   // query heads per kv head
 static constexpr int PSTR = HD + 4;  // floats per chunk partial: m, l, pad, acc[HD] at 4
 
@@ -87,14 +90,20 @@ __device__ inline u32 head_norm_rope(u32 raw, u32 wraw, float eps, int pos, cons
 // have loaded.  Scores are v_dot2 products of the rounded half-precision q and
 // k pairs with fp32 accumulation; softmax statistics and P V in fp32.
 // part[(c * nq + head) * PSTR] = {chunk max m, sum l, -, -, acc[HD]}.
-template <int XT, int GQ>
-__global__ __launch_bounds__(256) void k_attn_chunk(
-    const uint16_t* __restrict__ qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
+// POLL: the q|k|v row is written by earlier workgroups of the same launch (the
+// projection of k_qkv_chunk) and holds the pending pattern until then: each wave first
+// issues its K / V loads, then reads its rows of it from memory (sc1) until none is
+// pending -- at most max_polls times; a wait that gives up makes the query NaN and
+// stores I4_ERR_HANDOFF to *o_status.  qkv is then not __restrict__ (the loads stay
+// inside the wait loop).
+template <int XT, int GQ, bool POLL>
+__device__ inline void chunk_body(
+    int c, int by, const uint16_t* qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, float eps, const int32_t* __restrict__ pos_dev,
-    int pos_host, int max_len, RopeTab rt, uint16_t* __restrict__ k_cache,
+    int pos_host, int max_len, const RopeTab& rt, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
     float* __restrict__ part, int gsplit, u32x4* __restrict__ pend, int n_pend,
-    int32_t* __restrict__ status) {
+    int32_t* __restrict__ status, int max_polls, int32_t* __restrict__ o_status) {
   __shared__ __align__(16) u32 s_q[GQ][HD / 2];  // rotated q pairs
   __shared__ u32 s_knew[HD / 2], s_vnew[HD / 2];
   __shared__ __align__(16) float s_p[GQ][ACH];
@@ -102,9 +111,9 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   __shared__ float s_stat[GQ][2];
   // kv head g; this workgroup's GQ query heads start at q0 (gsplit workgroups share a
   // kv head, each with GQ of its GQ * gsplit query heads)
-  const int c = blockIdx.x, g = blockIdx.y / gsplit, t = threadIdx.x;
-  const int q0 = g * GQ * gsplit + (blockIdx.y % gsplit) * GQ;
-  const bool writer = blockIdx.y % gsplit == 0;  // appends this token's k / v
+  const int g = by / gsplit, t = threadIdx.x;
+  const int q0 = g * GQ * gsplit + (by % gsplit) * GQ;
+  const bool writer = by % gsplit == 0;  // appends this token's k / v
   const int wave = t >> 6, lane = t & 63;
   // the position from device memory (a captured graph serves every token) or the
   // host; a grid sized for max_len leaves the chunks past it idle
@@ -113,7 +122,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   // it to o_proj inside the launch (k_attn_o), and the o_proj output when the MoE router
   // waits for it there, start as the pending pattern; status (nullable) is reset here,
   // before the launch whose router waves may report a wait that gave up
-  if (c == 0 && blockIdx.y == 0) {
+  if (c == 0 && by == 0) {
     for (int i = t; i < n_pend; i += 256) pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
     if (status && t == 0) *status = I4_OK;
   }
@@ -125,14 +134,18 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   // heads w and w + 4, and wave 0 of the last chunk this token's key and value
   constexpr int QPW = (GQ + 3) / 4;
   u32 qraw[QPW], qw = *(const u32*)(qn_w + 2 * lane), kraw = 0, kwn = 0, vraw = 0;
+  const u32 qoff = (u32)(2 * lane) * 2u, koff = (u32)((nq + g) * HD) * 2u + qoff,
+            voff = (u32)((nq + nkv + g) * HD) * 2u + qoff;
+  auto qrow = [&](int i) { return (u32)((q0 + min(wave + 4 * i, GQ - 1)) * HD) * 2u + qoff; };
+  if constexpr (!POLL) {
 #pragma unroll
-  for (int i = 0; i < QPW; ++i)
-    qraw[i] = *(const u32*)(qkv + (int64_t)(q0 + min(wave + 4 * i, GQ - 1)) * HD + 2 * lane);
-  if (last && wave == 0) {
-    kraw = *(const u32*)(qkv + (int64_t)(nq + g) * HD + 2 * lane);
-    vraw = *(const u32*)(qkv + (int64_t)(nq + nkv + g) * HD + 2 * lane);
-    kwn = *(const u32*)(kn_w + 2 * lane);
+    for (int i = 0; i < QPW; ++i) qraw[i] = *(const u32*)((const char*)qkv + qrow(i));
+    if (last && wave == 0) {
+      kraw = *(const u32*)((const char*)qkv + koff);
+      vraw = *(const u32*)((const char*)qkv + voff);
+    }
   }
+  if (last && wave == 0) kwn = *(const u32*)(kn_w + 2 * lane);
   // K: thread t reads dims [32 (t & 3), +32) of position c0 + (t >> 2), rows < pos
   const int j = t >> 2, qp = t & 3;
   const int kr = min(c0 + j, max(pos - 1, 0));
@@ -147,6 +160,36 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   for (int i = 0; i < 16; ++i)
     vv[i] = *(const u32*)(v_cache + kv0 + (int64_t)min(c0 + 16 * ks + i, max(pos - 1, 0)) * HD +
                           2 * d2);
+  if constexpr (POLL) {  // the K / V loads are in flight: now wait for this token's row
+    const rsrc_t rq = rsrc(qkv, (u32)((nq + 2 * nkv) * HD) * 2u);
+    auto pend16 = [](u32 v) { return (v & 0xFFFFu) == kPending16 || (v >> 16) == kPending16; };
+    bool late = false;
+    for (int it = 0;; ++it) {
+      bool p = false;
+#pragma unroll
+      for (int i = 0; i < QPW; ++i) {
+        qraw[i] = __builtin_amdgcn_raw_buffer_load_b32(rq, qrow(i), 0, kCoherent);
+        p |= pend16(qraw[i]);
+      }
+      if (last && wave == 0) {
+        kraw = __builtin_amdgcn_raw_buffer_load_b32(rq, koff, 0, kCoherent);
+        vraw = __builtin_amdgcn_raw_buffer_load_b32(rq, voff, 0, kCoherent);
+        p |= pend16(kraw) || pend16(vraw);
+      }
+      if (__builtin_amdgcn_ballot_w64(p) == 0) break;
+      if (it >= max_polls) {
+        late = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      asm volatile("" ::: "memory");
+    }
+    if (late) {
+#pragma unroll
+      for (int i = 0; i < QPW; ++i) qraw[i] = (u32)Half<XT>::QNAN * 0x10001u;
+      if (lane == 0 && o_status) *o_status = I4_ERR_HANDOFF;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < QPW; ++i)
     if (wave + 4 * i < GQ) s_q[wave + 4 * i][lane] = head_norm_rope<XT>(qraw[i], qw, eps, pos, rt);
@@ -245,6 +288,57 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
   }
 }
 
+template <int XT, int GQ>
+__global__ __launch_bounds__(256) void k_attn_chunk(
+    const uint16_t* __restrict__ qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, float eps, const int32_t* __restrict__ pos_dev,
+    int pos_host, int max_len, RopeTab rt, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
+    float* __restrict__ part, int gsplit, u32x4* __restrict__ pend, int n_pend,
+    int32_t* __restrict__ status) {
+  chunk_body<XT, GQ, false>(blockIdx.x, blockIdx.y, qkv, nq, nkv, qn_w, kn_w, eps, pos_dev,
+                            pos_host, max_len, rt, k_cache, v_cache, head_stride, scale, part,
+                            gsplit, pend, n_pend, status, 0, nullptr);
+}
+
+// The input RMSNorm + q|k|v projection and the attention chunks in one launch: blocks
+// [0, n_proj) are the projection's GEMV rows (gemv_ct_body with the norm, their rows
+// written through to qkv for the later blocks, qkv holding the pending pattern before the
+// launch), the later blocks the chunk workgroups (chunk c, kv head group by), which
+// issue their K / V loads and then poll qkv.  Only later blocks wait, and only for
+// earlier ones, so a launch whose workgroups are dispatched in block order completes.
+struct QkvProj {
+  const uint16_t* h;   // the layer's input row
+  const uint16_t* nw;  // input RMSNorm weight
+  float eps;
+  const int32_t* packed;
+  const void* scale;
+  const int32_t* zeros;
+  int N, K, gshift, n_proj;
+};
+
+template <int XT, int ST, int L, int GQ>
+__global__ __launch_bounds__(256) void k_qkv_chunk(
+    QkvProj pr, uint16_t* qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, float eps, const int32_t* __restrict__ pos_dev,
+    int pos_host, int max_len, RopeTab rt, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
+    float* __restrict__ part, int gsplit, int nch, u32x4* __restrict__ pend, int n_pend,
+    int32_t* __restrict__ status, int max_polls, int32_t* __restrict__ o_status) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int b = blockIdx.x;
+  if (b < pr.n_proj) {
+    gemv_ct_body<XT, ST, L, true, false, true>(b, 0, pr.h, 0, pr.packed, 0, pr.scale, 0,
+                                               pr.zeros, 0, nullptr, 1, pr.N, pr.K, pr.gshift,
+                                               qkv, XT, nullptr, pr.nw, pr.eps, lds, 0);
+    return;
+  }
+  const int cb = b - pr.n_proj;
+  chunk_body<XT, GQ, true>(cb % nch, cb / nch, qkv, nq, nkv, qn_w, kn_w, eps, pos_dev, pos_host,
+                           max_len, rt, k_cache, v_cache, head_stride, scale, part, gsplit, pend,
+                           n_pend, status, max_polls, o_status);
+}
+
 // One workgroup of HD threads per query head merges its chunks (flash-decoding):
 // out = o / L with a running maximum M over the chunks in chunk order,
 // L = sum_c l_c e^(m_c - M), o = sum_c acc_c e^(m_c - M).  Every load of a batch of
@@ -340,6 +434,8 @@ struct RFold {
   int32_t* status;
   int E;
   int n_o;  // o_proj workgroups
+  u32x4* qkv_next = nullptr;  // the next layer's q|k|v row to arm (its fused launch polls it)
+  int n_qkv_next = 0;
 };
 
 // y is not __restrict__: the router waves poll it, and a restrict pointer would let
@@ -373,6 +469,8 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     if (b >= nq + r.n_o) {
       const int rb = b - nq - r.n_o, nrb = (int)gridDim.x - nq - r.n_o;
       for (int i = rb * 256 + t; i < r.n_act; i += nrb * 256) r.act[i] = u32x4{~0u, ~0u, ~0u, ~0u};
+      for (int i = rb * 256 + t; i < r.n_qkv_next; i += nrb * 256)
+        r.qkv_next[i] = u32x4{~0u, ~0u, ~0u, ~0u};
       const int e = rb * 4 + (t >> 6);  // wave-uniform
       if (e >= r.E) return;
       bool late = false;
@@ -420,6 +518,10 @@ struct OLaunch {
   const RFold* route = nullptr;
   bool reset_status = true;  // with route: the chunk launch clears route->status
   int32_t* status = nullptr;  // without route: the o_proj wait's status, cleared likewise
+  // the input RMSNorm + q|k|v projection in the chunk launch (k_qkv_chunk): qkv holds the
+  // pending pattern before it; proj_st: its weight's scale dtype
+  const QkvProj* proj = nullptr;
+  int proj_st = 0;
 };
 
 template <int XT, int ST>
@@ -472,6 +574,24 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   const int n_pend = !o ? 0 : (nq * HD + (o->route ? o->w.N : 0)) / 8;
   int32_t* st_reset = !o ? nullptr : o->route ? (o->reset_status ? o->route->status : nullptr)
                                                : o->status;
+  if (o && o->proj) {  // projection rows first, then the chunks, polling qkv
+    const QkvProj& pr = *o->proj;
+    const size_t lds = (size_t)pr.K * 2 + (size_t)(pr.K / 32) * 8;
+    const dim3 fgrid(pr.n_proj + nch * nkv * gsplit);
+    int32_t* pst = o->route ? o->route->status : o->status;
+#define I4_QC_CASE(ST_, G_)                                                                   \
+  if (o->proj_st == ST_ && gq / gsplit == G_)                                                 \
+    hipLaunchKernelGGL((k_qkv_chunk<XT, ST_, 32, G_>), fgrid, dim3(256), lds, s, pr,          \
+                       (uint16_t*)qkv, nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w, \
+                       eps, pos_dev, pos, max_len, rt, (uint16_t*)k_cache, (uint16_t*)v_cache, \
+                       hs, scale, part, gsplit, nch, (u32x4*)out, n_pend, st_reset,           \
+                       kHandoffPolls, pst);                                                   \
+  else
+    I4_QC_CASE(I4_F32, 1) I4_QC_CASE(I4_F32, 2) I4_QC_CASE(I4_F32, 4)
+    I4_QC_CASE(I4_F16, 1) I4_QC_CASE(I4_F16, 2) I4_QC_CASE(I4_F16, 4)
+    I4_QC_CASE(I4_BF16, 1) I4_QC_CASE(I4_BF16, 2) I4_QC_CASE(I4_BF16, 4) return I4_ERR_SHAPE;
+#undef I4_QC_CASE
+  } else {
 #define I4_AC_CASE(G_)                                                                        \
   if (gq / gsplit == G_)                                                                      \
     hipLaunchKernelGGL((k_attn_chunk<XT, G_>), grid, dim3(256), 0, s, (const uint16_t*)qkv,  \
@@ -480,8 +600,9 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
                        (uint16_t*)k_cache, (uint16_t*)v_cache, hs, scale, part, gsplit,     \
                        (u32x4*)(o ? out : nullptr), n_pend, st_reset);                      \
   else
-  I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) return I4_ERR_SHAPE;
+    I4_AC_CASE(1) I4_AC_CASE(2) I4_AC_CASE(4) return I4_ERR_SHAPE;
 #undef I4_AC_CASE
+  }
   if (o) {  // out is the attention output buffer in the workspace
     if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
     if (o->st == I4_F32)
@@ -685,21 +806,47 @@ static int layer_check(const i4_thinker_layer& L, int x_dtype, int n_heads, int 
 }
 
 // h -> out through one layer; reset: the chunk launch clears the status word.
+// The layer's q|k|v projection can run inside its chunk launch (k_qkv_chunk: 32 lanes per
+// row, the GEMV shape of the Thinker's 2048 -> 5120 projection).
+static bool qkv_fusable(const LayerOk& c) {
+  return i4::gemv_lanes_per_row(c.qw.K / 32, c.qw.N) == 32 && c.qw.K <= 4096;
+}
+
+// h -> out through one layer; reset: the chunk launch clears the status word.
+// fused: the projection runs in the chunk launch, whose q|k|v row the previous layer's
+// o_proj launch armed with the pending pattern; arm_next: this layer's o_proj launch arms
+// it for the next layer.
 static int layer_launch(const i4_thinker_layer& L, const LayerOk& c, int x_dtype,
                         int n_heads, int n_kv_heads, const float* inv_freq,
                         const int32_t* pos_dev, int pos, int max_len, int topk, int renorm,
                         const void* h, bool reset, void* out, void* workspace,
-                        hipStream_t stream) {
+                        hipStream_t stream, bool fused = false, bool arm_next = false) {
   char* ws = (char*)workspace;
   void* qkv = ws + c.l.qkv;
   void* h2 = ws + c.l.h2;
-  int rc = i4_rmsnorm_linear(h, x_dtype, 1, L.in_norm_w, L.eps, &c.qw, nullptr, qkv, x_dtype,
-                             stream);
-  if (rc) return rc;
-  const i4::RFold r{(const uint16_t*)L.moe.router_w, (const uint16_t*)L.moe.norm_w,
-                    L.moe.norm_eps, c.mb.xn, c.mb.logits, c.mb.act, c.mb.n_act, c.mb.status,
-                    c.mb.E, 0};
+  int rc;
+  i4::QkvProj pr;
+  if (fused) {
+    const i4_qweight& qw = c.qw;
+    pr = i4::QkvProj{(const uint16_t*)h, (const uint16_t*)L.in_norm_w, L.eps, qw.packed,
+                     qw.scale, qw.zeros, qw.N, qw.K, i4_group_shift(qw.group), (qw.N + 7) / 8};
+  } else {
+    rc = i4_rmsnorm_linear(h, x_dtype, 1, L.in_norm_w, L.eps, &c.qw, nullptr, qkv, x_dtype,
+                           stream);
+    if (rc) return rc;
+  }
+  i4::RFold r{(const uint16_t*)L.moe.router_w, (const uint16_t*)L.moe.norm_w,
+              L.moe.norm_eps, c.mb.xn, c.mb.logits, c.mb.act, c.mb.n_act, c.mb.status,
+              c.mb.E, 0};
+  if (arm_next) {
+    r.qkv_next = (i4::u32x4*)qkv;
+    r.n_qkv_next = c.qw.N / 8;
+  }
   i4::OLaunch o;
+  if (fused) {
+    o.proj = &pr;
+    o.proj_st = c.qw.scale_dtype;
+  }
   const i4_qweight& ow = c.ow;
   o.w = i4::OProj{ow.packed, ow.scale, ow.zeros, ow.N, ow.K, i4_group_shift(ow.group)};
   o.st = ow.scale_dtype;
@@ -763,13 +910,17 @@ int i4_thinker_decode_step(const void* h, int x_dtype, const i4_thinker_layer* l
   if (workspace_bytes < c0.l.bytes + i4::al256((size_t)c0.mb.H * 2)) return I4_ERR_WORKSPACE;
   void* hbuf = (char*)workspace + c0.l.bytes;
   const void* cur = h;
+  // layers after the first run their projection inside the chunk launch (every layer
+  // shares the workspace and its shapes, so layer l - 1's o_proj launch arms layer l's row)
+  const bool fuse = qkv_fusable(c0);
   for (int l = 0; l < n_layers; ++l) {
     void* dst = l == n_layers - 1 ? out : hbuf;
     int rc = layer_check(layers[l], x_dtype, n_heads, n_kv_heads, head_dim, inv_freq, pos_dev,
                          pos, max_len, topk, workspace, workspace_bytes, 0, &c);
     if (rc) return rc;
     rc = layer_launch(layers[l], c, x_dtype, n_heads, n_kv_heads, inv_freq, pos_dev, pos,
-                      max_len, topk, renorm, cur, l == 0, dst, workspace, stream);
+                      max_len, topk, renorm, cur, l == 0, dst, workspace, stream, fuse && l > 0,
+                      fuse && l + 1 < n_layers);
     if (rc) return rc;
     cur = dst;
   }
