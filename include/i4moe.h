@@ -67,7 +67,7 @@
 extern "C" {
 #endif
 
-#define I4_ABI_VERSION 8
+#define I4_ABI_VERSION 9
 
 /* status codes */
 #define I4_OK               0
@@ -427,6 +427,33 @@ int    i4_attn_decode_o(const void* qkv, int x_dtype, int n_heads, int n_kv_head
 size_t i4_attn_decode_o_workspace_bytes(int n_heads, int head_dim, int max_len);
 size_t i4_attn_decode_o_status_offset(int n_heads, int head_dim, int max_len);
 
+/* The attention half of a Thinker decoder layer for one decode token, from the layer's
+ * input row h:
+ *   y = h + o_w attn(qkv_w rmsnorm(h; in_norm_w, eps)),
+ * the first lines of Qwen3OmniMoeThinkerTextDecoderLayer.forward
+ * (modeling_qwen3_omni_moe.py:1539-1552 in transformers 5.15) with q_proj / k_proj /
+ * v_proj and o_proj on TritonPackedLinear (triton_dequant_gemv.py:151-159).  qkv_w: one
+ * CT weight [(n_heads + 2 n_kv_heads) head_dim][H]; o_w: one CT weight [H][n_heads
+ * head_dim] (K <= 8192); the other arguments as in i4_attn_decode_o.  Where the q|k|v
+ * GEMV has 32 lanes per row and H <= 4096 (the Thinker's 2048 -> 5120), the input norm
+ * and the projection run inside the attention chunk launch, whose chunk workgroups take
+ * their q / k / v rows over as (value pair, tag) words; two launches in all.  Otherwise
+ * three (i4_rmsnorm_linear first).  Either way the result and the cache rows equal
+ * i4_rmsnorm_linear + i4_attn_decode_o(residual = h) bit for bit.  h: 16-byte aligned;
+ * y may be h.  Workspace: i4_attn_decode_qkv_o_workspace_bytes(), 256-byte aligned, the
+ * layout of i4_attn_decode_o's (status word at i4_attn_decode_o_status_offset(), also for
+ * a chunk workgroup whose wait for its rows gave up) then the q|k|v row; it needs no
+ * initial contents, and one zero-filled at allocation cannot agree with a hand-over tag
+ * by chance (the tags are odd); calls sharing one must not overlap. */
+int    i4_attn_decode_qkv_o(const void* h, int x_dtype, const void* in_norm_w, float eps,
+                            const i4_qweight* qkv_w, int n_heads, int n_kv_heads, int head_dim,
+                            const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                            const int32_t* pos_dev, int pos, void* k_cache, void* v_cache,
+                            int max_len, const i4_qweight* o_w, void* y, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+size_t i4_attn_decode_qkv_o_workspace_bytes(int n_heads, int n_kv_heads, int head_dim,
+                                            int max_len);
+
 /* One decode token through a whole Thinker decoder layer:
  * Qwen3OmniMoeThinkerTextDecoderLayer.forward (modeling_qwen3_omni_moe.py:1539-1565
  * in transformers 5.15), whose MoE block the reference replaces with
@@ -435,15 +462,18 @@ size_t i4_attn_decode_o_status_offset(int n_heads, int head_dim, int max_len);
  *   out = h2 + MoE(RMSNorm(h2; moe->norm_w, moe->norm_eps))
  * with the attention of i4_attn_decode_o (q_norm_w / k_norm_w also use eps) and the
  * MoE block of i4_moe_forward at T = 1 (router_w and norm_w required, CT experts).
- * Four launches: the q|k|v GEMV with the input norm, the attention chunks, the head
- * merge + o_proj + the MoE router (the router waves wait inside that launch for the
- * o_proj output), the experts.  The result, the cache rows and the MoE status word
+ * Three launches: the q|k|v GEMV with the input norm inside the attention chunk launch
+ * (as in i4_attn_decode_qkv_o; a separate launch first where its shape does not allow),
+ * the head merge + o_proj + the MoE router (the router waves wait inside that launch for
+ * the o_proj output), the experts.  The result, the cache rows and the MoE status word
  * equal i4_rmsnorm_linear + i4_attn_decode_o(residual = h) + i4_moe_forward(T = 1,
  * residual = h2) bit for bit.  qkv_w, o_w: one CT weight each, qkv_w [(n_heads +
  * 2 n_kv_heads) head_dim][H], o_w [H][n_heads head_dim]; H = 1024 or 2048.  h and
  * out ([H], x_dtype, 16-byte aligned) may be the same buffer.  pos_dev as in
  * i4_attn_decode_o.  Workspace: i4_thinker_layer_workspace_bytes(), no initial
- * contents, 256-byte aligned; it begins with i4_moe_forward's T = 1 workspace, so a
+ * contents (zero-filled at allocation rules out any chance agreement with the q|k|v
+ * hand-over tags, as for i4_attn_decode_qkv_o), 256-byte aligned; it begins with
+ * i4_moe_forward's T = 1 workspace, so a
  * router or expert wait that gave up leaves I4_ERR_HANDOFF at
  * i4_moe_status_offset(1, H, I, E, topk).  Calls sharing one must not overlap.
  * i4_thinker_layer_workspace_bytes returns 0 for sizes the entry does not take

@@ -27,7 +27,8 @@ from .moe import FusedPackedMoE, fuse_packed_moe_blocks
 from .ops import (dequant, dequant_gemv, linear, moe_down_combine, moe_down_wait, moe_forward,
                   moe_forward_noalloc, moe_gate_up, moe_route_gate_up, moe_stack, moe_status,
                   route, router_logits, unpack4, unpack_nibbles, Workspace, rmsnorm,
-                  rmsnorm_linear, attn_decode, attn_decode_o, thinker_layer_decode,
+                  rmsnorm_linear, attn_decode, attn_decode_o, attn_decode_qkv_o,
+                  thinker_layer_decode,
                   thinker_layer_fits, thinker_layer_c, thinker_decode_step, dmoe_forward,
                   dmoe_status, dmoe_down_wait, StackLayerX)
 from .weights import QWeight, repack_awq_to_ct, repack_tile
@@ -43,7 +44,8 @@ __all__ = [
     "concat_rows", "concat_cols_awq", "patch_attention", "TILE_ROWS", "lib",
     "Checkpoint", "read_moe_layer", "load_moe_layer", "load_thinker_moe_stack", "load_attention",
     "load_thinker_layer", "load_thinker_decoder", "rmsnorm", "rmsnorm_linear", "attn_decode",
-    "attn_decode_o", "thinker_layer_decode", "thinker_layer_fits", "thinker_layer_c",
+    "attn_decode_o", "attn_decode_qkv_o", "thinker_layer_decode", "thinker_layer_fits",
+    "thinker_layer_c",
     "thinker_decode_step",
     "ThinkerAttention", "ThinkerDecoderLayer", "ThinkerDecoder", "rope_inv_freq",
     "FusedMoE", "fuse_moe_blocks", "quantize_q8", "dmoe_forward", "dmoe_status",

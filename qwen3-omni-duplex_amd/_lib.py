@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libi4moe.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # element types and layouts (include/i4moe.h)
 F32, F16, BF16 = 0, 1, 2
@@ -138,6 +138,11 @@ SIGNATURES = {
                                  c_size_t, c_void_p]),
     "i4_attn_decode_o_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "i4_attn_decode_o_status_offset": (c_size_t, [c_int, c_int, c_int]),
+    "i4_attn_decode_qkv_o": (c_int, [c_void_p, c_int, c_void_p, ctypes.c_float,
+                                     POINTER(QWeightC), c_int, c_int, c_int, c_void_p, c_void_p,
+                                     c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int,
+                                     POINTER(QWeightC), c_void_p, c_void_p, c_size_t, c_void_p]),
+    "i4_attn_decode_qkv_o_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "i4_thinker_layer_decode": (c_int, [c_void_p, c_int, c_void_p, ctypes.c_float,
                                         POINTER(QWeightC), c_int, c_int, c_int, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,

@@ -8,9 +8,10 @@ i.e. transformers' Qwen3OmniMoeThinkerTextDecoderLayer.forward
     h = h + o_proj(attention(input_layernorm(h)))            ThinkerAttention
     h = h + moe(post_attention_layernorm(h))                  FusedPackedMoE (norm fused)
 
-with the projections on the library's int4 GEMVs (q|k|v as one launch with the input
-norm, o with the residual added in the launch that merges the attention heads), and
-q/k norm, rotary embedding, KV-cache append and GQA attention in i4_attn_decode_o.  The KV cache is preallocated
+with the projections on the library's int4 GEMVs (q|k|v with the input norm inside the
+attention chunk launch, o with the residual added in the launch that merges the attention
+heads), and q/k norm, rotary embedding, KV-cache append and GQA attention in
+i4_attn_decode_qkv_o.  The KV cache is preallocated
 ([n_kv_heads, max_len, head_dim] per layer, the activation dtype) instead of
 transformers' growing DynamicCache.
 """
@@ -88,14 +89,15 @@ class ThinkerAttention(nn.Module):
             raise ValueError("ThinkerAttention decodes one token")
         if not isinstance(pos, torch.Tensor) and not 0 <= pos < self.max_len:
             raise ValueError(f"position {pos} outside the cache (max_len {self.max_len})")
+        if self.o_proj.w.layout == "ct":
+            # input_layernorm + q|k|v inside the attention chunk launch, then the head
+            # merge and o_proj (+ the residual) in one more
+            return ops.attn_decode_qkv_o(h, self.input_norm_w, self.eps, self.qkv.lin.w,
+                                         self.n_heads, self.n_kv_heads, self.q_norm_w,
+                                         self.k_norm_w, self.inv_freq, pos, self.k_cache,
+                                         self.v_cache, self.o_proj.w, self.workspace)
         # input_layernorm folded into the q|k|v launch
         qkv = ops.rmsnorm_linear(h, self.input_norm_w, self.eps, self.qkv.lin.w)
-        if self.o_proj.w.layout == "ct":
-            # the head merge and o_proj (+ the residual) in one launch
-            return ops.attn_decode_o(qkv, self.n_heads, self.n_kv_heads, self.q_norm_w,
-                                     self.k_norm_w, self.eps, self.inv_freq, pos, self.k_cache,
-                                     self.v_cache, self.o_proj.w, h.reshape(-1),
-                                     self.workspace).view(h.shape)
         a = ops.attn_decode(qkv, self.n_heads, self.n_kv_heads, self.q_norm_w, self.k_norm_w,
                             self.eps, self.inv_freq, pos, self.k_cache, self.v_cache,
                             self.workspace)

@@ -91,11 +91,11 @@ __device__ inline u32 head_norm_rope(u32 raw, u32 wraw, float eps, int pos, cons
 // k pairs with fp32 accumulation; softmax statistics and P V in fp32.
 // part[(c * nq + head) * PSTR] = {chunk max m, sum l, -, -, acc[HD]}.
 // POLL: the q|k|v row is written by earlier workgroups of the same launch (the
-// projection of k_qkv_chunk) and holds the pending pattern until then: each wave first
-// issues its K / V loads, then reads its rows of it from memory (sc1) until none is
-// pending -- at most max_polls times; a wait that gives up makes the query NaN and
-// stores I4_ERR_HANDOFF to *o_status.  qkv is then not __restrict__ (the loads stay
-// inside the wait loop).
+// projection of k_qkv_chunk) as (value pair, tag) words, 8 bytes per two values: each
+// wave first issues its K / V loads, then reads its words from memory (sc1) until every
+// one carries this call's tag -- at most max_polls times; a wait that gives up makes the
+// query NaN and stores I4_ERR_HANDOFF to *o_status.  qkv is then not __restrict__ (the
+// loads stay inside the wait loop).
 template <int XT, int GQ, bool POLL>
 __device__ inline void chunk_body(
     int c, int by, const uint16_t* qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
@@ -103,7 +103,7 @@ __device__ inline void chunk_body(
     int pos_host, int max_len, const RopeTab& rt, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
     float* __restrict__ part, int gsplit, u32x4* __restrict__ pend, int n_pend,
-    int32_t* __restrict__ status, int max_polls, int32_t* __restrict__ o_status) {
+    int32_t* __restrict__ status, int max_polls, int32_t* __restrict__ o_status, u32 tag = 0) {
   __shared__ __align__(16) u32 s_q[GQ][HD / 2];  // rotated q pairs
   __shared__ u32 s_knew[HD / 2], s_vnew[HD / 2];
   __shared__ __align__(16) float s_p[GQ][ACH];
@@ -161,20 +161,22 @@ __device__ inline void chunk_body(
     vv[i] = *(const u32*)(v_cache + kv0 + (int64_t)min(c0 + 16 * ks + i, max(pos - 1, 0)) * HD +
                           2 * d2);
   if constexpr (POLL) {  // the K / V loads are in flight: now wait for this token's row
-    const rsrc_t rq = rsrc(qkv, (u32)((nq + 2 * nkv) * HD) * 2u);
-    auto pend16 = [](u32 v) { return (v & 0xFFFFu) == kPending16 || (v >> 16) == kPending16; };
+    // word of the pair at half-offset o: byte 2 o of the tagged row
+    const rsrc_t rq = rsrc(qkv, (u32)((nq + 2 * nkv) * HD) * 4u);
+    auto ld = [&](u32 o, u32& d) {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rq, 2u * o, 0, kCoherent);
+      const u32 dv = v.x, tv = v.y;
+      d = dv;
+      return tv != tag;
+    };
     bool late = false;
     for (int it = 0;; ++it) {
       bool p = false;
 #pragma unroll
-      for (int i = 0; i < QPW; ++i) {
-        qraw[i] = __builtin_amdgcn_raw_buffer_load_b32(rq, qrow(i), 0, kCoherent);
-        p |= pend16(qraw[i]);
-      }
+      for (int i = 0; i < QPW; ++i) p |= ld(qrow(i), qraw[i]);
       if (last && wave == 0) {
-        kraw = __builtin_amdgcn_raw_buffer_load_b32(rq, koff, 0, kCoherent);
-        vraw = __builtin_amdgcn_raw_buffer_load_b32(rq, voff, 0, kCoherent);
-        p |= pend16(kraw) || pend16(vraw);
+        p |= ld(koff, kraw);
+        p |= ld(voff, vraw);
       }
       if (__builtin_amdgcn_ballot_w64(p) == 0) break;
       if (it >= max_polls) {
@@ -301,12 +303,19 @@ __global__ __launch_bounds__(256) void k_attn_chunk(
                             gsplit, pend, n_pend, status, 0, nullptr);
 }
 
+// The hand-over tag of a q|k|v row written while the epoch word holds e: odd, so a
+// zero-filled buffer never carries one, and spread over the 32 bits.  The launch after
+// the chunks (k_attn_o) advances the epoch, so every call, a replayed graph's too,
+// waits for a tag that no earlier call wrote.
+__device__ inline u32 qkv_tag(u32 e) { return (2u * e + 1u) * 0x9E3779B1u; }
+
 // The input RMSNorm + q|k|v projection and the attention chunks in one launch: blocks
 // [0, n_proj) are the projection's GEMV rows (gemv_ct_body with the norm, their rows
-// written through to qkv for the later blocks, qkv holding the pending pattern before the
-// launch), the later blocks the chunk workgroups (chunk c, kv head group by), which
-// issue their K / V loads and then poll qkv.  Only later blocks wait, and only for
-// earlier ones, so a launch whose workgroups are dispatched in block order completes.
+// written through to qkv as (value pair, tag) words for the later blocks), the later
+// blocks the chunk workgroups (chunk c, kv head group by), which issue their K / V
+// loads and then poll qkv until their words carry this call's tag.  Only later blocks
+// wait, and only for earlier ones, so a launch whose workgroups are dispatched in
+// block order completes.
 struct QkvProj {
   const uint16_t* h;   // the layer's input row
   const uint16_t* nw;  // input RMSNorm weight
@@ -319,24 +328,25 @@ struct QkvProj {
 
 template <int XT, int ST, int L, int GQ>
 __global__ __launch_bounds__(256) void k_qkv_chunk(
-    QkvProj pr, uint16_t* qkv, int nq, int nkv, const uint16_t* __restrict__ qn_w,
-    const uint16_t* __restrict__ kn_w, float eps, const int32_t* __restrict__ pos_dev,
-    int pos_host, int max_len, RopeTab rt, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache, int64_t head_stride, float scale,
-    float* __restrict__ part, int gsplit, int nch, u32x4* __restrict__ pend, int n_pend,
-    int32_t* __restrict__ status, int max_polls, int32_t* __restrict__ o_status) {
+    QkvProj pr, u32* qkv, const u32* __restrict__ epoch, int nq, int nkv,
+    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, float eps,
+    const int32_t* __restrict__ pos_dev, int pos_host, int max_len, RopeTab rt,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t head_stride,
+    float scale, float* __restrict__ part, int gsplit, int nch, u32x4* __restrict__ pend,
+    int n_pend, int32_t* __restrict__ status, int max_polls, int32_t* __restrict__ o_status) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int b = blockIdx.x;
+  const u32 tag = qkv_tag(__builtin_amdgcn_readfirstlane(*epoch));
   if (b < pr.n_proj) {
-    gemv_ct_body<XT, ST, L, true, false, true>(b, 0, pr.h, 0, pr.packed, 0, pr.scale, 0,
-                                               pr.zeros, 0, nullptr, 1, pr.N, pr.K, pr.gshift,
-                                               qkv, XT, nullptr, pr.nw, pr.eps, lds, 0);
+    gemv_ct_body<XT, ST, L, true, false, true, true>(
+        b, 0, pr.h, 0, pr.packed, 0, pr.scale, 0, pr.zeros, 0, nullptr, 1, pr.N, pr.K,
+        pr.gshift, qkv, XT, nullptr, pr.nw, pr.eps, lds, 0, nullptr, tag);
     return;
   }
   const int cb = b - pr.n_proj;
-  chunk_body<XT, GQ, true>(cb % nch, cb / nch, qkv, nq, nkv, qn_w, kn_w, eps, pos_dev, pos_host,
-                           max_len, rt, k_cache, v_cache, head_stride, scale, part, gsplit, pend,
-                           n_pend, status, max_polls, o_status);
+  chunk_body<XT, GQ, true>(cb % nch, cb / nch, (const uint16_t*)qkv, nq, nkv, qn_w, kn_w, eps,
+                           pos_dev, pos_host, max_len, rt, k_cache, v_cache, head_stride, scale,
+                           part, gsplit, pend, n_pend, status, max_polls, o_status, tag);
 }
 
 // One workgroup of HD threads per query head merges its chunks (flash-decoding):
@@ -434,21 +444,25 @@ struct RFold {
   int32_t* status;
   int E;
   int n_o;  // o_proj workgroups
-  u32x4* qkv_next = nullptr;  // the next layer's q|k|v row to arm (its fused launch polls it)
-  int n_qkv_next = 0;
 };
 
 // y is not __restrict__: the router waves poll it, and a restrict pointer would let
-// the compiler take their loads out of the wait loop
+// the compiler take their loads out of the wait loop.  epoch (nullable): the q|k|v
+// hand-over epoch of k_qkv_chunk, advanced here, after the chunks that read it.
 template <int XT, int ST, int L, int RH>
 __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, int nq,
                                                 const int32_t* __restrict__ pos_dev, int pos_host,
                                                 int max_len, uint16_t* __restrict__ att, OProj o,
                                                 const uint16_t* __restrict__ residual,
                                                 uint16_t* y, int max_polls, RFold r,
-                                                int32_t* __restrict__ o_status) {
+                                                int32_t* __restrict__ o_status,
+                                                u32* __restrict__ epoch) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int b = blockIdx.x, t = threadIdx.x;
+  if (epoch && (b | t) == 0) {
+    const u32 e = *epoch;
+    __builtin_amdgcn_raw_buffer_store_b32(e + 1u, rsrc(epoch, 4u), 0u, 0, 0);
+  }
   if (b < nq) {
     __shared__ __align__(16) uint16_t s_o[HD];
     if (t < HD) {
@@ -469,8 +483,6 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     if (b >= nq + r.n_o) {
       const int rb = b - nq - r.n_o, nrb = (int)gridDim.x - nq - r.n_o;
       for (int i = rb * 256 + t; i < r.n_act; i += nrb * 256) r.act[i] = u32x4{~0u, ~0u, ~0u, ~0u};
-      for (int i = rb * 256 + t; i < r.n_qkv_next; i += nrb * 256)
-        r.qkv_next[i] = u32x4{~0u, ~0u, ~0u, ~0u};
       const int e = rb * 4 + (t >> 6);  // wave-uniform
       if (e >= r.E) return;
       bool late = false;
@@ -496,12 +508,15 @@ size_t attn_ws(int nq, int max_len) {
   const size_t nch = ((size_t)max_len + ACH - 1) / ACH;
   return nch * nq * PSTR * sizeof(float);
 }
-// with o_proj: then (at a 256-byte boundary) the status word of the o_proj wait in a
-// 256-byte slot, then the attention output, which ends the workspace -- the router-fold
-// launch keeps its output y directly behind it, one pending span over both
+// with o_proj: then (at a 256-byte boundary) a 256-byte slot holding the status word of
+// the o_proj wait and (128 bytes in) the q|k|v hand-over epoch, then the attention
+// output, which ends the workspace -- the router-fold launch keeps its output y directly
+// behind it, one pending span over both
 size_t attn_o_status_off(int nq, int max_len) {
   return (attn_ws(nq, max_len) + 255) & ~(size_t)255;
 }
+// the q|k|v hand-over epoch word, on its own line of the status slot
+size_t attn_o_epoch_off(int nq, int max_len) { return attn_o_status_off(nq, max_len) + 128; }
 size_t attn_o_att_off(int nq, int max_len) { return attn_o_status_off(nq, max_len) + 256; }
 size_t attn_o_ws(int nq, int max_len) {
   return attn_o_att_off(nq, max_len) + (size_t)nq * HD * 2;
@@ -518,15 +533,15 @@ struct OLaunch {
   const RFold* route = nullptr;
   bool reset_status = true;  // with route: the chunk launch clears route->status
   int32_t* status = nullptr;  // without route: the o_proj wait's status, cleared likewise
-  // the input RMSNorm + q|k|v projection in the chunk launch (k_qkv_chunk): qkv holds the
-  // pending pattern before it; proj_st: its weight's scale dtype
+  // the input RMSNorm + q|k|v projection in the chunk launch (k_qkv_chunk): qkv is then
+  // its (value pair, tag) row, N * 4 bytes; proj_st: its weight's scale dtype
   const QkvProj* proj = nullptr;
   int proj_st = 0;
 };
 
 template <int XT, int ST>
 int launch_attn_o(const float* part, int nq, const int32_t* pos_dev, int pos, int max_len,
-                  uint16_t* att, const OLaunch& o, hipStream_t s) {
+                  uint16_t* att, const OLaunch& o, u32* epoch, hipStream_t s) {
   const int C = o.w.K / 32, L = gemv_lanes_per_row(C, o.w.N), rpw = 256 / L;
   const int n_o = (o.w.N + rpw - 1) / rpw;
   RFold r{};
@@ -543,7 +558,7 @@ int launch_attn_o(const float* part, int nq, const int32_t* pos_dev, int pos, in
   if (L == L_ && rh == RH_) {                                                                 \
     hipLaunchKernelGGL((k_attn_o<XT, ST, L_, RH_>), grid, dim3(256), lds, s, part, nq,        \
                        pos_dev, pos, max_len, att, o.w, (const uint16_t*)o.residual,          \
-                       (uint16_t*)o.y, kHandoffPolls, r, o.status);                           \
+                       (uint16_t*)o.y, kHandoffPolls, r, o.status, epoch);                    \
     return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                           \
   }
   I4_AO_CASE(8, 0) I4_AO_CASE(16, 0) I4_AO_CASE(32, 0) I4_AO_CASE(64, 0)
@@ -574,6 +589,8 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   const int n_pend = !o ? 0 : (nq * HD + (o->route ? o->w.N : 0)) / 8;
   int32_t* st_reset = !o ? nullptr : o->route ? (o->reset_status ? o->route->status : nullptr)
                                                : o->status;
+  // with o_proj: the q|k|v hand-over epoch (k_qkv_chunk reads it, k_attn_o advances it)
+  u32* epoch = o ? (u32*)((char*)ws + attn_o_epoch_off(nq, max_len)) : nullptr;
   if (o && o->proj) {  // projection rows first, then the chunks, polling qkv
     const QkvProj& pr = *o->proj;
     const size_t lds = (size_t)pr.K * 2 + (size_t)(pr.K / 32) * 8;
@@ -582,7 +599,8 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
 #define I4_QC_CASE(ST_, G_)                                                                   \
   if (o->proj_st == ST_ && gq / gsplit == G_)                                                 \
     hipLaunchKernelGGL((k_qkv_chunk<XT, ST_, 32, G_>), fgrid, dim3(256), lds, s, pr,          \
-                       (uint16_t*)qkv, nq, nkv, (const uint16_t*)qn_w, (const uint16_t*)kn_w, \
+                       (u32*)qkv, epoch, nq, nkv, (const uint16_t*)qn_w,                      \
+                       (const uint16_t*)kn_w,                                                 \
                        eps, pos_dev, pos, max_len, rt, (uint16_t*)k_cache, (uint16_t*)v_cache, \
                        hs, scale, part, gsplit, nch, (u32x4*)out, n_pend, st_reset,           \
                        kHandoffPolls, pst);                                                   \
@@ -606,10 +624,13 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
   if (o) {  // out is the attention output buffer in the workspace
     if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
     if (o->st == I4_F32)
-      return launch_attn_o<XT, I4_F32>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, s);
+      return launch_attn_o<XT, I4_F32>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, epoch,
+                                       s);
     if (o->st == I4_F16)
-      return launch_attn_o<XT, I4_F16>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, s);
-    return launch_attn_o<XT, I4_BF16>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, s);
+      return launch_attn_o<XT, I4_F16>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, epoch,
+                                       s);
+    return launch_attn_o<XT, I4_BF16>(part, nq, pos_dev, pos, max_len, (uint16_t*)out, *o, epoch,
+                                      s);
   }
   hipLaunchKernelGGL(k_attn_combine<XT>, dim3(nq), dim3(HD), 0, s, part, nq, pos_dev, pos,
                      max_len, (uint16_t*)out);
@@ -622,10 +643,14 @@ inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 namespace {
 
+// the q|k|v row of a decode token: N = (nq + 2 nkv) HD values, as (value pair, tag)
+// words when the projection runs in the chunk launch (k_qkv_chunk), else as halves
+size_t qkv_row_bytes(int nq, int nkv) { return al256((size_t)(nq + 2 * nkv) * HD * 4); }
+
 // workspace of i4_thinker_layer_decode: i4_moe_forward's T = 1 workspace first (so its
 // status word sits at i4_moe_status_offset(1, H, I, E, topk)), then the attention's
-// (chunk partials, attention output) with the o_proj output h2 right behind it, then
-// the q|k|v projection
+// (chunk partials, status slot, attention output) with the o_proj output h2 right behind
+// it, then the q|k|v row
 struct LayerWs {
   size_t part, h2, qkv, bytes;
 };
@@ -634,8 +659,15 @@ LayerWs layer_ws(int nq, int nkv, int max_len, int H, int I, int E, int topk) {
   l.part = al256(i4_moe_workspace_bytes(1, H, I, E, topk));
   l.h2 = l.part + attn_o_ws(nq, max_len);
   l.qkv = al256(l.h2 + (size_t)H * 2);
-  l.bytes = l.qkv + al256((size_t)(nq + 2 * nkv) * HD * 2);
+  l.bytes = l.qkv + qkv_row_bytes(nq, nkv);
   return l;
+}
+
+// The q|k|v projection runs inside the chunk launch (k_qkv_chunk) when it has the GEMV
+// shape that launch is built for: 32 lanes per row (the Thinker's 2048 -> 5120) and the
+// input norm's one staging round (K <= 4096).
+bool qkv_fusable(const i4_qweight& qw) {
+  return gemv_lanes_per_row(qw.K / 32, qw.N) == 32 && qw.K <= 4096;
 }
 
 }  // namespace
@@ -750,6 +782,63 @@ size_t i4_attn_decode_o_status_offset(int n_heads, int head_dim, int max_len) {
   return i4::attn_o_status_off(n_heads, max_len);
 }
 
+// i4_attn_decode_qkv_o's workspace: i4_attn_decode_o's, then the q|k|v row
+size_t i4_attn_decode_qkv_o_workspace_bytes(int n_heads, int n_kv_heads, int head_dim,
+                                            int max_len) {
+  if (n_heads < 1 || n_kv_heads < 1 || head_dim != i4::HD || max_len < 1) return 0;
+  return i4::al256(i4::attn_o_ws(n_heads, max_len)) + i4::qkv_row_bytes(n_heads, n_kv_heads);
+}
+
+int i4_attn_decode_qkv_o(const void* h, int x_dtype, const void* in_norm_w, float eps,
+                         const i4_qweight* qkv_w, int n_heads, int n_kv_heads, int head_dim,
+                         const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                         const int32_t* pos_dev, int pos, void* k_cache, void* v_cache,
+                         int max_len, const i4_qweight* o_w, void* y, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
+  if (!h || !in_norm_w || !qkv_w || !o_w || !y) return I4_ERR_NULL;
+  if (x_dtype != I4_F16 && x_dtype != I4_BF16) return I4_ERR_DTYPE;
+  i4_qweight qw, ow;
+  int rc = i4_check_weight(qkv_w, &qw);
+  if (rc) return rc;
+  rc = i4_check_weight(o_w, &ow);
+  if (rc) return rc;
+  if (qw.layout != I4_LAYOUT_CT || ow.layout != I4_LAYOUT_CT) return I4_ERR_LAYOUT;
+  if (n_heads < 1 || n_kv_heads < 1 || head_dim != i4::HD) return I4_ERR_SHAPE;
+  const int H = ow.N;
+  if (qw.E != 1 || qw.K != H || qw.N != (n_heads + 2 * n_kv_heads) * i4::HD) return I4_ERR_SHAPE;
+  // o_proj: one staging round of the poll (K <= 8192)
+  if (ow.E != 1 || ow.K != n_heads * i4::HD || ow.K < 256 || ow.K > 8192) return I4_ERR_SHAPE;
+  if (((uintptr_t)h & 15) || ((uintptr_t)in_norm_w & 15) || ((uintptr_t)y & 1))
+    return I4_ERR_ALIGN;
+  const size_t need = i4_attn_decode_qkv_o_workspace_bytes(n_heads, n_kv_heads, head_dim, max_len);
+  if (!workspace || workspace_bytes < need) return I4_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 255) return I4_ERR_ALIGN;
+  char* ws = (char*)workspace;
+  void* qkv = ws + i4::al256(i4::attn_o_ws(n_heads, max_len));
+  rc = attn_check(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, inv_freq,
+                  pos_dev, pos, k_cache, v_cache, max_len, y);
+  if (rc) return rc;
+  i4::OLaunch o;
+  o.w = i4::OProj{ow.packed, ow.scale, ow.zeros, ow.N, ow.K, i4_group_shift(ow.group)};
+  o.st = ow.scale_dtype;
+  o.residual = h;
+  o.y = y;
+  o.status = (int32_t*)(ws + i4::attn_o_status_off(n_heads, max_len));
+  i4::QkvProj pr;
+  if (i4::qkv_fusable(qw)) {
+    pr = i4::QkvProj{(const uint16_t*)h, (const uint16_t*)in_norm_w, eps, qw.packed, qw.scale,
+                     qw.zeros, qw.N, qw.K, i4_group_shift(qw.group), (qw.N + 7) / 8};
+    o.proj = &pr;
+    o.proj_st = qw.scale_dtype;
+  } else {
+    rc = i4_rmsnorm_linear(h, x_dtype, 1, in_norm_w, eps, &qw, nullptr, qkv, x_dtype, stream);
+    if (rc) return rc;
+  }
+  return attn_entry(qkv, x_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, eps,
+                    inv_freq, pos_dev, pos, k_cache, v_cache, max_len, y, workspace,
+                    workspace_bytes, stream, &o);
+}
+
 size_t i4_thinker_layer_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len,
                                         int H, int I, int E, int topk) {
   if (n_heads < 1 || n_kv_heads < 1 || head_dim != i4::HD || max_len < 1) return 0;
@@ -805,26 +894,18 @@ static int layer_check(const i4_thinker_layer& L, int x_dtype, int n_heads, int 
                     ws + c->l.h2);
 }
 
-// h -> out through one layer; reset: the chunk launch clears the status word.
-// The layer's q|k|v projection can run inside its chunk launch (k_qkv_chunk: 32 lanes per
-// row, the GEMV shape of the Thinker's 2048 -> 5120 projection).
-static bool qkv_fusable(const LayerOk& c) {
-  return i4::gemv_lanes_per_row(c.qw.K / 32, c.qw.N) == 32 && c.qw.K <= 4096;
-}
-
-// h -> out through one layer; reset: the chunk launch clears the status word.
-// fused: the projection runs in the chunk launch, whose q|k|v row the previous layer's
-// o_proj launch armed with the pending pattern; arm_next: this layer's o_proj launch arms
-// it for the next layer.
+// h -> out through one layer; reset: the chunk launch clears the status word.  The
+// projection runs in the chunk launch where its shape allows (i4::qkv_fusable).
 static int layer_launch(const i4_thinker_layer& L, const LayerOk& c, int x_dtype,
                         int n_heads, int n_kv_heads, const float* inv_freq,
                         const int32_t* pos_dev, int pos, int max_len, int topk, int renorm,
                         const void* h, bool reset, void* out, void* workspace,
-                        hipStream_t stream, bool fused = false, bool arm_next = false) {
+                        hipStream_t stream) {
   char* ws = (char*)workspace;
   void* qkv = ws + c.l.qkv;
   void* h2 = ws + c.l.h2;
   int rc;
+  const bool fused = i4::qkv_fusable(c.qw);
   i4::QkvProj pr;
   if (fused) {
     const i4_qweight& qw = c.qw;
@@ -838,10 +919,6 @@ static int layer_launch(const i4_thinker_layer& L, const LayerOk& c, int x_dtype
   i4::RFold r{(const uint16_t*)L.moe.router_w, (const uint16_t*)L.moe.norm_w,
               L.moe.norm_eps, c.mb.xn, c.mb.logits, c.mb.act, c.mb.n_act, c.mb.status,
               c.mb.E, 0};
-  if (arm_next) {
-    r.qkv_next = (i4::u32x4*)qkv;
-    r.n_qkv_next = c.qw.N / 8;
-  }
   i4::OLaunch o;
   if (fused) {
     o.proj = &pr;
@@ -910,17 +987,13 @@ int i4_thinker_decode_step(const void* h, int x_dtype, const i4_thinker_layer* l
   if (workspace_bytes < c0.l.bytes + i4::al256((size_t)c0.mb.H * 2)) return I4_ERR_WORKSPACE;
   void* hbuf = (char*)workspace + c0.l.bytes;
   const void* cur = h;
-  // layers after the first run their projection inside the chunk launch (every layer
-  // shares the workspace and its shapes, so layer l - 1's o_proj launch arms layer l's row)
-  const bool fuse = qkv_fusable(c0);
   for (int l = 0; l < n_layers; ++l) {
     void* dst = l == n_layers - 1 ? out : hbuf;
     int rc = layer_check(layers[l], x_dtype, n_heads, n_kv_heads, head_dim, inv_freq, pos_dev,
                          pos, max_len, topk, workspace, workspace_bytes, 0, &c);
     if (rc) return rc;
     rc = layer_launch(layers[l], c, x_dtype, n_heads, n_kv_heads, inv_freq, pos_dev, pos,
-                      max_len, topk, renorm, cur, l == 0, dst, workspace, stream, fuse && l > 0,
-                      fuse && l + 1 < n_layers);
+                      max_len, topk, renorm, cur, l == 0, dst, workspace, stream);
     if (rc) return rc;
     cur = dst;
   }

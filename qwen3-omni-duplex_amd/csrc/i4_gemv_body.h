@@ -29,16 +29,21 @@ static constexpr int GEMV_ROUND = 4;  // chunks per lane whose loads are in flig
 // workgroup's rows are gathered in LDS and written through to memory as whole
 // 16-byte stores where they are aligned (else value by value), NaN in canonical form (so the pending
 // pattern never appears in finished values).  Same arithmetic as the plain store.
-template <int XT, int ST, int L, bool NORM, bool POLL, bool HANDOFF = false>
+// TAG (with HANDOFF): out is instead an array of (value pair, tag) words, 8 bytes per
+// two rows, every pair of the workgroup's rows stored with `tag` (N a multiple of the
+// workgroup's RPW rows): the readers wait for the tag of their call, so the buffer
+// needs no pending pattern.
+template <int XT, int ST, int L, bool NORM, bool POLL, bool HANDOFF = false, bool TAG = false>
 __device__ __forceinline__ void gemv_ct_body(
     int bx, int j, const uint16_t* __restrict__ x, int64_t x_stride,
     const int32_t* __restrict__ packed, int64_t p_es, const void* __restrict__ scale,
     int64_t s_es, const int32_t* __restrict__ zeros, int64_t z_es,
     const int32_t* __restrict__ sel, int E, int N, int K, int gshift, void* __restrict__ out,
     int ot, const void* __restrict__ bias, const uint16_t* __restrict__ nw, float eps,
-    unsigned char* lds, int max_polls, int32_t* __restrict__ status = nullptr) {
+    unsigned char* lds, int max_polls, int32_t* __restrict__ status = nullptr, u32 tag = 0) {
   constexpr int WG = GEMV_WG, ROUND = GEMV_ROUND;
   static_assert(!(NORM && POLL), "a polled row is used as it arrives");
+  static_assert(!TAG || HANDOFF, "tags belong to a hand-over");
   constexpr int RPW = WG / L;
   const int C = K >> 5, KW = K >> 3;
   const int NG = (C + (1 << gshift) - 1) >> gshift, NZW = (NG + 7) >> 3;
@@ -128,6 +133,18 @@ __device__ __forceinline__ void gemv_ct_body(
     }
     __syncthreads();
     const int n0 = bx * RPW, nv = min(RPW, N - n0);
+    if constexpr (TAG) {
+      static_assert(RPW % 4 == 0, "whole 16-byte stores of two (pair, tag) words");
+      // thread i: pairs 2i, 2i + 1 of the workgroup's rows as {pair, tag, pair, tag}
+      if ((int)threadIdx.x < RPW / 4) {
+        const u32* sp = (const u32*)s_y + 2 * threadIdx.x;
+        const u32 p0 = sp[0], p1 = sp[1];
+        const rsrc_t r = rsrc((u32*)out + ((int64_t)j * N + n0), (u32)RPW * 4u);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{p0, tag, p1, tag}, r, (u32)threadIdx.x * 16u,
+                                               0, kCoherent);
+      }
+      return;
+    }
     uint16_t* dst = (uint16_t*)out + (int64_t)j * N + n0;
     if (RPW % 8 == 0 && nv == RPW && ((uintptr_t)dst & 15) == 0) {
       if ((int)threadIdx.x < RPW / 8) {

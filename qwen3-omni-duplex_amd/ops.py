@@ -617,6 +617,55 @@ def attn_decode_o(qkv: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm_w: to
     return y
 
 
+def attn_decode_qkv_o(h: torch.Tensor, in_norm_w: torch.Tensor, eps: float, qkv_w: QWeight,
+                      n_heads: int, n_kv_heads: int, q_norm_w: torch.Tensor,
+                      k_norm_w: torch.Tensor, inv_freq: torch.Tensor, pos: int | torch.Tensor,
+                      k_cache: torch.Tensor, v_cache: torch.Tensor, o_w: QWeight,
+                      workspace: Workspace | None = None) -> torch.Tensor:
+    """The attention half of a decoder layer from its input row (i4_attn_decode_qkv_o):
+    h + o_w attn(qkv_w RMSNorm(h)), equal bit for bit to rmsnorm_linear followed by
+    attn_decode_o(residual=h).  qkv_w and o_w are CT weights; h is [..., H] holding one
+    token.  Where the q|k|v GEMV shape allows, its rows are computed inside the attention
+    chunk launch (two launches in all)."""
+    dev = _lib.require_device(h, in_norm_w, q_norm_w, k_norm_w, k_cache, v_cache, qkv_w.packed,
+                              o_w.packed)
+    if h.numel() != h.shape[-1]:
+        raise RuntimeError("attn_decode_qkv_o takes one token")
+    pos_dev = None
+    if isinstance(pos, torch.Tensor):
+        if pos.device != dev or pos.dtype != torch.int32 or pos.numel() != 1:
+            raise RuntimeError("a device position is one int32 on the tensors' device")
+        pos_dev = pos
+    xt = _lib.half_code(h.dtype)
+    for t, name in ((in_norm_w, "input norm"), (q_norm_w, "q norm"), (k_norm_w, "k norm")):
+        if t.dtype != h.dtype:
+            raise RuntimeError(f"the {name} weight must have the activation dtype")
+    nkv, max_len, hd = k_cache.shape
+    if k_cache.dtype != h.dtype or v_cache.shape != k_cache.shape or v_cache.dtype != h.dtype:
+        raise RuntimeError("the caches must be [n_kv_heads, max_len, head_dim] in the activation dtype")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or nkv != n_kv_heads:
+        raise RuntimeError("the caches must be contiguous [n_kv_heads, max_len, head_dim]")
+    tab = inv_freq.detach().to("cpu", torch.float32).contiguous()
+    if tab.numel() != hd // 2:
+        raise RuntimeError("inv_freq must hold head_dim / 2 values")
+    hf = h.reshape(-1).contiguous()
+    y = torch.empty_like(hf)
+    lb = _lib.lib()
+    nbytes = lb.i4_attn_decode_qkv_o_workspace_bytes(n_heads, n_kv_heads, hd, max_len)
+    # zero-filled when allocated: the q|k|v hand-over tags are odd, so no word of a new
+    # buffer can pass for a finished one
+    ws = (workspace or Workspace()).get(nbytes, dev, zeroed=True)
+    qw, ow = qkv_w.c(), o_w.c()
+    _lib.check(lb.i4_attn_decode_qkv_o(
+        hf.data_ptr(), xt, in_norm_w.contiguous().data_ptr(), float(eps), ctypes.byref(qw),
+        n_heads, n_kv_heads, hd, q_norm_w.contiguous().data_ptr(),
+        k_norm_w.contiguous().data_ptr(), tab.data_ptr(),
+        None if pos_dev is None else pos_dev.data_ptr(), 0 if pos_dev is not None else int(pos),
+        k_cache.data_ptr(), v_cache.data_ptr(), max_len, ctypes.byref(ow), y.data_ptr(),
+        ws.data_ptr(), ws.numel(), _lib.stream(dev)))
+    return y.view(h.shape)
+
+
 def attn_status(workspace: Workspace, n_heads: int, head_dim: int, max_len: int) -> int:
     """The status word the last attn_decode_o call with this workspace left (0, or the
     I4_ERR_HANDOFF code when an o_proj wait gave up); synchronises the device."""
@@ -642,8 +691,9 @@ def thinker_layer_decode(h: torch.Tensor, in_norm_w: torch.Tensor, eps: float, q
                          norm_w: torch.Tensor, norm_eps: float, norm_topk_prob: bool = True,
                          workspace: Workspace | None = None) -> torch.Tensor:
     """One decode token through a Thinker decoder layer (i4_thinker_layer_decode):
-    h2 = h + o_proj(attention(RMSNorm(h))), then h2 + MoE(RMSNorm(h2)), in four launches
-    (the MoE router runs in the o_proj launch, behind the workgroups producing h2).
+    h2 = h + o_proj(attention(RMSNorm(h))), then h2 + MoE(RMSNorm(h2)), in three launches
+    (the q|k|v GEMV inside the attention chunk launch, the MoE router in the o_proj
+    launch behind the workgroups producing h2, the experts).
     Equal bit for bit to rmsnorm_linear + attn_decode_o + moe_forward(residual=h2).
     qkv_w, o_w and the experts are CT weights; h is [..., H] holding one token."""
     dev = _lib.require_device(h, in_norm_w, q_norm_w, k_norm_w, k_cache, v_cache, o_w.packed,
@@ -676,7 +726,7 @@ def thinker_layer_decode(h: torch.Tensor, in_norm_w: torch.Tensor, eps: float, q
     nbytes = lb.i4_thinker_layer_workspace_bytes(n_heads, n_kv_heads, hd, max_len, H, I, E, top_k)
     if nbytes == 0:
         raise RuntimeError("unsupported Thinker layer shape")
-    ws = (workspace or Workspace()).get(nbytes, dev)
+    ws = (workspace or Workspace()).get(nbytes, dev, zeroed=True)  # see attn_decode_qkv_o
     qw, ow = qkv_w.c(), o_w.c()
     mw = moe_weights_c(gate_up, down, router_w, norm_w, norm_eps)
     _lib.check(lb.i4_thinker_layer_decode(
@@ -739,7 +789,7 @@ def thinker_decode_step(h: torch.Tensor, layers_c, n_layers: int, n_heads: int, 
                                                        H, I, E, top_k)
     if nbytes == 0:
         raise RuntimeError("unsupported Thinker layer shape")
-    ws = (workspace or Workspace()).get(nbytes, dev)
+    ws = (workspace or Workspace()).get(nbytes, dev, zeroed=True)  # see attn_decode_qkv_o
     _lib.check(lb.i4_thinker_decode_step(
         hf.data_ptr(), _lib.half_code(h.dtype), layers_c, n_layers, n_heads, n_kv_heads,
         head_dim, tab.data_ptr(), None if pos_dev is None else pos_dev.data_ptr(),

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported_and_bound(pkg):
 
 def test_version_and_errors(pkg):
     lib = pkg.lib()
-    assert lib.i4_abi_version() == 8
+    assert lib.i4_abi_version() == 9
     codes = {0: b"ok", -1: b"NULL", -2: b"dimension", -3: b"element type", -4: b"aligned",
              -5: b"layout", -6: b"group", -7: b"workspace", -8: b"launch", -9: b"stride",
              -10: b"gave up waiting", -11: b"static buffer"}
@@ -256,6 +256,34 @@ def test_decode_attention_validation_codes(pkg):
     assert callo(wsb=ws) == -7          # the partials alone do not hold the merged heads
     assert callo(pd=0x70002) == -4
 
+    # from the layer's input row: i4_attn_decode_o's workspace, then the q|k|v row as
+    # (value pair, tag) words from a 256-byte boundary
+    wsq = lib.i4_attn_decode_qkv_o_workspace_bytes(32, 4, 128, 4096)
+    assert wsq == ((wso + 255) & ~255) + 40 * 128 * 4
+    assert lib.i4_attn_decode_qkv_o_workspace_bytes(32, 4, 64, 4096) == 0
+    qw = _qw(_lib, E=1, N=5120, K=2048, group=32)
+    callq = lambda **kw: lib.i4_attn_decode_qkv_o(
+        kw.get("h", 0x30000), kw.get("xt", 2), kw.get("nw", 0x40000), 1e-6,
+        kw.get("qw", ctypes.byref(qw)), kw.get("nh", 32), 4, 128, 0x50000, 0x51000, tab,
+        kw.get("pd", None), kw.get("pos", 5), 0x100000, 0x200000, 4096,
+        kw.get("ow", ctypes.byref(ow)), kw.get("y", 0x90000), kw.get("ws", 0x300000),
+        kw.get("wsb", wsq), None)
+    assert callq(h=None) == -1
+    assert callq(qw=None) == -1
+    assert callq(y=None) == -1
+    assert callq(xt=0) == -3
+    assert callq(qw=ctypes.byref(_qw(_lib, E=1, N=5120, K=2048, group=128, layout=1))) == -5
+    assert callq(qw=ctypes.byref(_qw(_lib, E=1, N=4096, K=2048, group=32))) == -2  # not 40 heads
+    assert callq(qw=ctypes.byref(_qw(_lib, E=1, N=5120, K=1024, group=32))) == -2  # K != o_w.N
+    assert callq(nh=16) == -2           # o_w.K != 16 * 128
+    assert callq(h=0x30008) == -4
+    assert callq(nw=0x40008) == -4
+    assert callq(y=0x90001) == -4
+    assert callq(wsb=wso) == -7         # the q|k|v row does not fit
+    assert callq(ws=0x300080) == -4
+    assert callq(pos=4096) == -2
+    assert callq(pd=0x70002) == -4
+
 
 def test_thinker_layer_validation_codes(pkg):
     """i4_thinker_layer_decode rejects bad calls before its first launch (Thinker sizes:
@@ -266,9 +294,10 @@ def test_thinker_layer_validation_codes(pkg):
     lib = pkg.lib()
     tab = (ctypes.c_float * 64)()
     wsb = lib.i4_thinker_layer_workspace_bytes(32, 4, 128, 4096, 2048, 768, 128, 8)
-    # MoE workspace, attention workspace + h2, q|k|v, each from a 256-byte boundary
+    # MoE workspace, attention workspace + h2, the q|k|v row as (value pair, tag) words,
+    # each from a 256-byte boundary
     parts = (lib.i4_moe_workspace_bytes(1, 2048, 768, 128, 8),
-             lib.i4_attn_decode_o_workspace_bytes(32, 128, 4096) + 2048 * 2, 40 * 128 * 2)
+             lib.i4_attn_decode_o_workspace_bytes(32, 128, 4096) + 2048 * 2, 40 * 128 * 4)
     assert wsb == sum((b + 255) & ~255 for b in parts)
     fits = lambda **kw: lib.i4_thinker_layer_workspace_bytes(
         32, 4, kw.get("hd", 128), 4096, kw.get("H", 2048), kw.get("I", 768), 128, kw.get("k", 8))

@@ -306,6 +306,74 @@ def test_attn_decode_o_equals_attention_then_o_proj(pkg, dev, xdt, nh, nkv, pos,
     assert torch.equal(kc3, cache[0])
 
 
+@pytest.mark.parametrize("xdt,H,nh,nkv,G", [("f16", 2048, 32, 4, 32),    # the Thinker's
+                                             ("bf16", 2048, 32, 4, 128),
+                                             ("bf16", 1024, 16, 8, 32),   # 8 lanes per row
+                                             ("f16", 1024, 8, 2, 64)])
+def test_attn_decode_qkv_o_equals_norm_linear_then_attn_o(pkg, dev, xdt, H, nh, nkv, G):
+    """i4_attn_decode_qkv_o (the input norm + q|k|v GEMV inside the attention chunk launch,
+    its rows handed over as tagged words, where the GEMV has 32 lanes per row; three
+    launches otherwise) equals i4_rmsnorm_linear + i4_attn_decode_o(residual = h) bit for
+    bit, output and caches: consecutive tokens on one workspace (each call must take its
+    own rows, not the previous call's), host and device positions, then one hipGraph
+    replayed for several tokens with other work between the replays."""
+    rng = np.random.default_rng(700 + H + nh + G)
+    tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    hd, max_len = 128, 1024
+    N = (nh + 2 * nkv) * hd
+    from tests import _gen
+
+    def weight(n, k):
+        p, sc, z = _gen.ct_weight(rng, 1, n, k, G, zeros=G == 64)
+        return pkg.QWeight(t_(p, dev), t_(sc, dev).to(tdt), None if z is None else t_(z, dev),
+                           "ct", G, n, k)
+
+    qw, ow = weight(N, H), weight(H, nh * hd)
+    vec = lambda n: torch.from_numpy(rng.uniform(0.5, 1.5, n).astype(np.float32)).to(dev, tdt)
+    nw, qn, kn = vec(H), vec(hd), vec(hd)
+    inv = pkg.rope_inv_freq(hd, 1e6)
+    cache0 = [torch.randn(nkv, max_len, hd, device=dev).to(tdt) for _ in range(2)]
+    xs = [torch.from_numpy(rng.standard_normal(H).astype(np.float32)).to(dev, tdt)
+          for _ in range(6)]
+
+    def want_of(x, pos, kc, vc):
+        qkv = pkg.rmsnorm_linear(x.view(1, -1), nw, 1e-6, qw).view(-1)
+        return pkg.attn_decode_o(qkv, nh, nkv, qn, kn, 1e-6, inv, pos, kc, vc, ow, x)
+
+    kc_w, vc_w = cache0[0].clone(), cache0[1].clone()
+    kc_g, vc_g = cache0[0].clone(), cache0[1].clone()
+    ws = pkg.Workspace()
+    positions = (517, 518, 519, 63, 64, 1000)
+    for i, pos in enumerate(positions):
+        want = want_of(xs[i], pos, kc_w, vc_w)
+        pp = torch.full((1,), pos, dtype=torch.int32, device=dev) if i % 2 else pos
+        got = pkg.ops.attn_decode_qkv_o(xs[i], nw, 1e-6, qw, nh, nkv, qn, kn, inv, pp, kc_g,
+                                        vc_g, ow, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(got, want), pos
+        assert torch.equal(kc_g, kc_w) and torch.equal(vc_g, vc_w)
+        assert pkg.ops.attn_status(ws, nh, hd, max_len) == 0
+    # a captured graph: every replay runs with the tag its own epoch gives
+    h_buf = xs[0].clone()
+    pos_buf = torch.zeros(1, dtype=torch.int32, device=dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = pkg.ops.attn_decode_qkv_o(h_buf, nw, 1e-6, qw, nh, nkv, qn, kn, inv, pos_buf,
+                                        kc_g, vc_g, ow, workspace=ws)
+    for i, pos in enumerate((200, 201, 202, 203)):
+        x = xs[(i + 2) % len(xs)] * (1 + i)
+        h_buf.copy_(x)
+        pos_buf.fill_(pos)
+        g.replay()
+        want = want_of(x, pos, kc_w, vc_w)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), pos
+        assert torch.equal(kc_g, kc_w) and torch.equal(vc_g, vc_w)
+        _ = (torch.randn(256, 256, device=dev) @ torch.randn(256, 256, device=dev)).sum().item()
+    assert pkg.ops.attn_status(ws, nh, hd, max_len) == 0
+
+
 def _synthetic_layer(pkg, dev, tdt, H, E, I, top_k, nh, nkv, max_len, renorm, seed,
                      qkv_scales=None):
     """A Thinker decoder layer of random CT int4 weights (g32, scales in the activation
@@ -344,10 +412,11 @@ def _synthetic_layer(pkg, dev, tdt, H, E, I, top_k, nh, nkv, max_len, renorm, se
     ("f16", 1024, 32, 512, 6, 8, 2, True)])
 def test_thinker_layer_decode_equals_attention_then_moe(pkg, dev, xdt, H, E, I, top_k, nh, nkv,
                                                         renorm):
-    """i4_thinker_layer_decode (the MoE router inside the head merge + o_proj launch, its
-    waves waiting there for the o_proj output) equals the attention block followed by the
-    MoE block (i4_attn_decode_o, then i4_moe_forward with residual h2) bit for bit: output,
-    both caches and a status word left at 0; host and device positions, the last row of a
+    """i4_thinker_layer_decode (the q|k|v GEMV inside the attention chunk launch, the MoE
+    router inside the head merge + o_proj launch, its waves waiting there for the o_proj
+    output) equals the attention block followed by the MoE block (i4_rmsnorm_linear +
+    i4_attn_decode_o, then i4_moe_forward with residual h2) bit for bit: output, both
+    caches and a status word left at 0; host and device positions, the last row of a
     chunk, position 0; a device position past the cache gives NaN and leaves the cache."""
     tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
     max_len = 1024
@@ -364,7 +433,12 @@ def test_thinker_layer_decode_equals_attention_then_moe(pkg, dev, xdt, H, E, I, 
         for dev_pos in (False, True):
             a.k_cache.copy_(cache0[0])
             a.v_cache.copy_(cache0[1])
-            want = layer.unfused(x, pos)
+            # the three-launch attention (not ThinkerAttention's fused entry), then the MoE
+            qkv = pkg.rmsnorm_linear(x, a.input_norm_w, a.eps, a.qkv.lin.w).view(-1)
+            h2 = pkg.attn_decode_o(qkv, nh, nkv, a.q_norm_w, a.k_norm_w, a.eps, a.inv_freq,
+                                   pos, a.k_cache, a.v_cache, a.o_proj.w,
+                                   x.view(-1)).view(x.shape)
+            want = layer.moe(h2, residual=h2)
             kc, vc = a.k_cache.clone(), a.v_cache.clone()
             a.k_cache.copy_(cache0[0])
             a.v_cache.copy_(cache0[1])
