@@ -268,6 +268,22 @@ int    i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* w
  * share one workspace must not overlap. */
 size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
 
+/* i4_moe_forward for 2 <= T <= 64 tokens with the bound of its in-launch wait set by
+ * the caller (no reference counterpart: the reference runs the two projections as
+ * separate calls, fused_packed_moe.py:255-261).  At these sizes both expert
+ * projections run as one launch whose down workgroups wait, at most max_polls polls per
+ * 128-column block, for the activations that the launch's gate_up workgroups write
+ * (i4_moe_forward bounds it at 2^20, which a launch dispatched in block order never
+ * reaches).  down_only != 0 launches the down workgroups alone, so every wait gives up:
+ * the rows they own come out NaN (so does out) and the status word at
+ * i4_moe_status_offset(T, H, I, E, topk) holds I4_ERR_HANDOFF; every kernel still
+ * exits.  For testing the bounded wait from the host.  I4_ERR_SHAPE outside 2..64
+ * tokens or when gate_up and down use different group sizes (then nothing waits). */
+int    i4_moe_forward_bounded(const void* x, int x_dtype, int T, const i4_moe_weights* weights,
+                              int topk, int renorm, const void* logits, const void* residual,
+                              void* out, void* workspace, size_t workspace_bytes, int max_polls,
+                              int down_only, hipStream_t stream);
+
 /* Byte offset, inside the workspace of i4_moe_forward / i4_moe_stack_forward
  * with these sizes, of an int32 status word that every call rewrites on the
  * device: I4_OK, or I4_ERR_HANDOFF when a workgroup of the single-launch decode

@@ -100,6 +100,9 @@ SIGNATURES = {
                                c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                c_size_t, c_void_p]),
     "i4_moe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "i4_moe_forward_bounded": (c_int, [c_void_p, c_int, c_int, POINTER(MoeWeightsC), c_int,
+                                       c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                       c_int, c_int, c_void_p]),
     "i4_moe_status_offset": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "i4_moe_forward_noalloc": (c_int, [c_void_p, c_int, c_int, POINTER(MoeWeightsC), c_int, c_int,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -29,8 +29,11 @@ int i4_launch_gemv_ct(const void* x, int xt, int64_t x_stride, const i4_qweight*
 int i4_launch_router_logits(const void* x, int xt, int T, int H, const void* wr, int E,
                             const void* norm_w, float eps, void* xn, void* logits, hipStream_t s,
                             void* pend = nullptr, int n_pend = 0, int32_t* status = nullptr);
+// pend (16-byte aligned, n_pend 16-byte units, nullable) is filled with the pending
+// pattern for the fused grouped launch after it (k_tile_mfma_gd).
 int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
-                   float* wf, void* wh, int wht, hipStream_t s);
+                   float* wf, void* wh, int wht, hipStream_t s, void* pend = nullptr,
+                   int n_pend = 0);
 
 // T = 1 router launch that first completes the previous layer of an XCD-local experts
 // launch: h = res + sum_k wts[k] ypart[k] (kc == 8 slot rows of H values), written to

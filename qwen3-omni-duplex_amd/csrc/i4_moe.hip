@@ -296,6 +296,8 @@ struct MoeOps {
                     const int*, const int32_t*, const TW&, int, void*, hipStream_t);
   int (*moe_m1x_ct)(const GateUpArgs&, const TW&, const TW&, void*, int32_t*, int, bool,
                     hipStream_t);
+  int (*mfma_gd)(int, const void*, int, int, const int4*, const int*, const int32_t*, const TW&,
+                 const TW&, int, void*, void*, int32_t*, int, bool, hipStream_t);
 };
 
 template <int XT, int ST> constexpr MoeOps moe_ops() {
@@ -303,7 +305,7 @@ template <int XT, int ST> constexpr MoeOps moe_ops() {
                 &launch_gate_up_ct<XT, ST>,  &launch_down_m1_ct<XT, ST>,
                 &launch_mfma_gate_up<XT, ST>, &launch_mfma_down<XT, ST>,
                 &launch_moe_m1_ct<XT, ST>,   &launch_mfma_mixed<XT, ST>,
-                &launch_moe_m1x_ct<XT, ST>};
+                &launch_moe_m1x_ct<XT, ST>,  &launch_mfma_gd<XT, ST>};
 }
 
 bool pick_ops(int xt, int gst, int dst, MoeOps* ops) {
@@ -374,10 +376,13 @@ int check_moe(const i4_moe_weights* mw, int x_dtype, int T, int topk, i4_qweight
 
 // reset: this chunk's first kernel clears the status word (the first chunk of
 // a call, the first layer of a stack), so a later give-up is not overwritten
+// max_polls / down_only: the bound of the T <= 64 fused launch's wait, and that launch's
+// down workgroups alone (i4_moe_forward_bounded)
 int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_qweight& gu,
               const i4_qweight& dn, const i4_qweight& tg, const i4_qweight& td, int topk,
               int renorm, const void* logits, const void* residual, void* out, int32_t* sel_out,
-              float* w_out, const MoeWs& ws, bool reset, hipStream_t s) {
+              float* w_out, const MoeWs& ws, bool reset, hipStream_t s,
+              int max_polls = kHandoffPolls, bool down_only = false) {
   int32_t* st_reset = reset ? ws.status : nullptr;
   const int H = gu.K, I = dn.K, E = gu.E;
   MoeOps ops;
@@ -430,7 +435,11 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   // top-k on T / 4 workgroups (one token per wave), then the grouping: ranking every
   // token inside the one grouping workgroup queued the waves' scalar bisection steps on
   // one CU's scalar unit (5 us of the launch at T = 32; separate launches 1.5 us faster)
-  rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s);
+  // T <= 64 with one group size for both projections: gate_up and down share a launch
+  // whose down workgroups take act over inside it; the top-k launch sets act pending
+  const bool gd = one_list && tgu.gshift == tdn.gshift;
+  rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s, gd ? ws.act : nullptr,
+                      gd ? (int)((int64_t)Tk * I / 8) : 0);
   if (rc) return rc;
   hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E,
                      one_list ? T : MF_SMALL, MF_SMALL, ws.perm, ws.entries, ws.n_entries,
@@ -439,7 +448,11 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   // entry counts: sum over experts of ceil(n_e / 16) <= min(E, Tk) + Tk / 16
   const int max_s = (E < Tk ? E : Tk) + (one_list ? Tk / MF_SMALL : 0);
   const int max_b = (E < Tk / (MF_SMALL + 1) ? E : Tk / (MF_SMALL + 1)) + Tk / MF_TOK + 1;
-  if (one_list) {
+  if (gd) {
+    rc = ops.mfma_gd(max_s, x, T, topk, ws.entries, ws.n_entries, ws.perm, tgu, tdn, I, ws.act,
+                     ws.ys, ws.status, max_polls, down_only, s);
+    if (rc) return rc;
+  } else if (one_list) {
     rc = ops.mfma_gate_up(true, max_s, x, T, topk, ws.entries, ws.n_entries, ws.perm, tgu, I,
                           ws.act, s);
     if (rc) return rc;
@@ -474,7 +487,8 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
 int moe_forward_impl(const void* x, int x_dtype, int T, const i4_moe_weights* weights, int topk,
                      int renorm, const void* logits, const void* residual, void* out,
                      int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
-                     bool reset, hipStream_t stream, int32_t* status = nullptr) {
+                     bool reset, hipStream_t stream, int32_t* status = nullptr,
+                     int max_polls = kHandoffPolls, bool down_only = false) {
   i4_qweight gu, dn, tg, td;
   int rc = check_moe(weights, x_dtype, T, topk, &gu, &dn, &tg, &td);
   if (rc) return rc;
@@ -498,7 +512,8 @@ int moe_forward_impl(const void* x, int x_dtype, int T, const i4_moe_weights* we
     void* os = (char*)out + (size_t)t0 * H * 2;
     rc = moe_chunk(xs, x_dtype, Tc, weights, gu, dn, tg, td, topk, renorm, lg, rs, os,
                    sel_out ? sel_out + (size_t)t0 * topk : nullptr,
-                   w_out ? w_out + (size_t)t0 * topk : nullptr, ws, reset && t0 == 0, stream);
+                   w_out ? w_out + (size_t)t0 * topk : nullptr, ws, reset && t0 == 0, stream,
+                   max_polls, down_only);
     if (rc) return rc;
   }
   return I4_OK;
@@ -671,6 +686,21 @@ int i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* weig
                    hipStream_t stream) {
   return moe_forward_impl(x, x_dtype, T, weights, topk, renorm, logits, residual, out, sel_out,
                           w_out, workspace, workspace_bytes, true, stream);
+}
+
+int i4_moe_forward_bounded(const void* x, int x_dtype, int T, const i4_moe_weights* weights,
+                           int topk, int renorm, const void* logits, const void* residual,
+                           void* out, void* workspace, size_t workspace_bytes, int max_polls,
+                           int down_only, hipStream_t stream) {
+  if (!weights) return I4_ERR_NULL;
+  // only the fused T <= 64 launch waits: 2..64 tokens, one group size for both projections
+  if (T < 2 || T > ONE_LIST_T || max_polls < 0) return I4_ERR_SHAPE;
+  const i4_qweight& g = weights->gate_up_tile.packed ? weights->gate_up_tile : weights->gate_up;
+  const i4_qweight& d = weights->down_tile.packed ? weights->down_tile : weights->down;
+  if (g.group != d.group) return I4_ERR_SHAPE;
+  return moe_forward_impl(x, x_dtype, T, weights, topk, renorm, logits, residual, out, nullptr,
+                          nullptr, workspace, workspace_bytes, true, stream, nullptr, max_polls,
+                          down_only != 0);
 }
 
 

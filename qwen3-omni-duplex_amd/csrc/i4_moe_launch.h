@@ -111,6 +111,16 @@ int launch_mfma_mixed(bool gate_up, int max_large, int max_small, const void* sr
                       const int* n_small, const int32_t* perm, const TW& w, int I, void* out,
                       hipStream_t s);
 
+// Both projections of small entries (T <= 64) in one launch: the gate_up workgroups
+// first, then the down workgroups, which take act over inside the launch (it must hold
+// the pending pattern before it; a wait that gives up leaves NaN rows and
+// I4_ERR_HANDOFF in *status).  down_only: the down workgroups alone.
+template <int XT, int ST>
+int launch_mfma_gd(int max_entries, const void* x, int T, int topk, const int4* ent,
+                   const int* nent, const int32_t* perm, const TW& wg, const TW& wd, int I,
+                   void* act, void* ys, int32_t* status, int max_polls, bool down_only,
+                   hipStream_t s);
+
 // Dense linear layer on MFMA: y[M][N] = x[M][K] W^T (+ bias, dtype ot), W one
 // tile-layout weight (E = 1, N % 128 == 0).  Small grids are split along K
 // into fp32 partials in ws (linear_tile_workspace_bytes; 0 when not split).

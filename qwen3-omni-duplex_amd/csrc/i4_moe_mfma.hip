@@ -62,6 +62,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 __device__ inline u32x4 bload16(rsrc_t r, u32 voff, int soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
+// the same past the L1 (sc1): sees what other CUs of the launch wrote through
+__device__ inline u32x4 bload16_coherent(rsrc_t r, u32 voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kCoherent);
+}
 __device__ inline u32 bload4(rsrc_t r, u32 voff, int soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
 }
@@ -230,14 +234,23 @@ __device__ inline void correct(f32x4& res, const f32x4& d, u32 sraw, u32 zw, int
 // activation-sum buffers, XSUMB floats apart) from the kernel that runs it, so one
 // launch can serve entries of both sizes (k_tile_mfma_mixed).
 // RING: weight superchunks in flight per wave (2 or 3 register slots).
-template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN, int RING = 3>
+// HAND (one m-block, not LIN): the two projections share a launch (k_tile_mfma_gd).  The
+// gate_up workgroups write act through to memory, every NaN in canonical form; the down
+// workgroups read act past the L1 and, before staging each superchunk, reload it until
+// no value holds the pending pattern (act was set to it one launch earlier), at most
+// max_polls times: then their rows come out NaN and I4_ERR_HANDOFF goes to *status.
+// hsrc is act again, without __restrict__, so the reloads stay inside the wait loop.
+template <int XT, int ST, bool GB, bool GATEUP, int NB, int MB, bool LIN, int RING = 3,
+          bool HAND = false>
 __device__ inline void tile_mfma_body(
     int bx, int by, int bz, u32x4* __restrict__ xs0, int XSB, float* __restrict__ xsum0,
     int XSUMB, const uint16_t* __restrict__ src, u32 src_bytes, int topk,
     const int4* __restrict__ entries, const int* __restrict__ n_entries,
     const int32_t* __restrict__ perm, const TW& w, int I, uint16_t* __restrict__ act,
     float* __restrict__ ys, int M, const void* __restrict__ bias, int ot, int ksplit,
-    float* __restrict__ part) {
+    float* __restrict__ part, const uint16_t* hsrc = nullptr, int max_polls = 0,
+    int32_t* __restrict__ status = nullptr) {
+  static_assert(!HAND || (MB == 1 && !LIN), "the hand-over serves one-m-block entries");
   constexpr bool EXACT = XT == I4_F16;
   // fp16 with several m-blocks folds the scale into B (see the top); one
   // m-block keeps the exact form, whose extra registers fit its occupancy
@@ -285,10 +298,29 @@ __device__ inline void tile_mfma_body(
     u32x4 x;
   };
   u32x4 xd[WPT];
+  const rsrc_t hr = rsrc(HAND && !GATEUP ? hsrc : src, src_bytes);
   auto load_x = [&](int sc, u32x4* dst) {
     sc = scb + min(sc, SC - 1);
 #pragma unroll
-    for (int q = 0; q < WPT; ++q) dst[q] = bload16(xr, vx + 16u * q, sc * 256);
+    for (int q = 0; q < WPT; ++q)
+      dst[q] = HAND && !GATEUP ? bload16_coherent(hr, vx + 16u * q, sc * 256)
+                               : bload16(xr, vx + 16u * q, sc * 256);
+  };
+  // HAND down: reload superchunk sc's activation word until no thread holds a pending
+  // value (the workgroup decides together, so every thread runs the same passes)
+  bool late = false;
+  auto wait_x = [&](int sc, u32x4& x) {
+    sc = scb + min(sc, SC - 1);
+    for (int it = 0;; ++it) {
+      if (!__syncthreads_or(has_pending(x))) return;
+      if (it >= max_polls) {
+        late = true;
+        return;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      asm volatile("" ::: "memory");
+      x = bload16_coherent(hr, vx, sc * 256);
+    }
   };
   auto commit_x = [&](int buf, const u32x4* src_x) {
     float sm = 0.f, sm1 = 0.f;  // sm1: the second chunk of a two-chunk thread (MB = 8)
@@ -442,6 +474,7 @@ __device__ inline void tile_mfma_body(
     const int buf = DBUF ? sc & 1 : 0;
     if constexpr (!DBUF) __syncthreads();  // the previous superchunk's reads are done
     if constexpr (MB == 1) {
+      if constexpr (HAND && !GATEUP) wait_x(sc, sl.x);
       commit_x(buf, &sl.x);
     } else {
       commit_x(buf, xd);
@@ -488,7 +521,10 @@ __device__ inline void tile_mfma_body(
       step(sc + 1, s1);
     }
   }
-  // epilogue: lane holds rows m = 16 mb + 4 j + i of column r
+  // epilogue: lane holds rows m = 16 mb + 4 j + i of column r.  HAND gate_up gathers the
+  // workgroup's 16 x COLS values in LDS and writes each token's row through as 16-byte
+  // stores (2-byte write-through stores per lane reached the down workgroups later)
+  __shared__ __align__(16) uint16_t s_act[HAND && GATEUP ? 16 * COLS : 8];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
@@ -501,7 +537,10 @@ __device__ inline void tile_mfma_body(
             const int n = bx * COLS + 16 * (NB / 2) * wave + 16 * nb + ln;
             const float v =
                 ev ? silu(res[mb][nb][i]) * res[mb][nb + NB / 2][i] : __builtin_nanf("");
-            act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
+            if constexpr (HAND)
+              s_act[m * COLS + (n - bx * COLS)] = v != v ? Half<XT>::QNAN : Half<XT>::from_f32(v);
+            else
+              act[(int64_t)(pos0 + m) * I + n] = Half<XT>::from_f32(v);
           }
         } else if constexpr (LIN) {
           const int n0 = bx * COLS + 16 * NB * wave + ln;
@@ -532,11 +571,24 @@ __device__ inline void tile_mfma_body(
 #pragma unroll
           // the expert's output in the activation dtype (k_moe_combine sums the slots)
           for (int nb = 0; nb < NB; ++nb)
-            ((uint16_t*)ys)[o + 16 * nb] = Half<XT>::from_f32(ev ? res[mb][nb][i] : __builtin_nanf(""));
+            ((uint16_t*)ys)[o + 16 * nb] =
+                Half<XT>::from_f32(ev && !late ? res[mb][nb][i] : __builtin_nanf(""));
         }
       }
     }
   }
+  if constexpr (HAND && GATEUP) {
+    constexpr int WPR = COLS / 8;  // 16-byte words per token row
+    __syncthreads();
+    const int m = (int)threadIdx.x / WPR, q = (int)threadIdx.x % WPR;
+    if (m < cnt) {
+      const rsrc_t r = rsrc(act + (int64_t)(pos0 + m) * I + bx * COLS, (u32)COLS * 2u);
+      __builtin_amdgcn_raw_buffer_store_b128(((const u32x4*)s_act)[m * WPR + q], r, (u32)q * 16u,
+                                             0, kCoherent);
+    }
+  }
+  if constexpr (HAND && !GATEUP)  // a wait that gave up is reported (status nullable)
+    if (late && status && threadIdx.x == 0) *status = I4_ERR_HANDOFF;
 }
 
 // WPE: minimum waves per SIMD the register allocation must allow (1: no bound).  The
@@ -588,6 +640,36 @@ __global__ __launch_bounds__(256) void k_tile_mfma_mixed(
         src_bytes, topk, small, n_small, perm, w, I, act, ys, 0, nullptr, 0, 1, nullptr);
 }
 
+// Both projections of the small entries in one launch (T <= 64, every expert in entries
+// of <= 16 tokens): blocks [0, n_gu) are the gate_up workgroups (column tile b % gu_cols of
+// entry b / gu_cols), the later blocks the down workgroups (column tile d % dn_cols of
+// entry d / dn_cols), which stream their first weight superchunks at once and take each
+// superchunk of their entry's act over as its gate_up workgroups write it through (act
+// holds the pending pattern before the launch).  Only later blocks wait, and only for
+// earlier ones.  WPE: waves per SIMD the register allocation must allow; fp16 with one
+// group per superchunk fits six (80 VGPRs, no spill; 104 unbounded), the other forms
+// would spill and run unbounded.
+template <int XT, int ST, bool GB, int NB, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void k_tile_mfma_gd(
+    const uint16_t* __restrict__ x, u32 x_bytes, int topk, const int4* __restrict__ ent,
+    const int* __restrict__ nent, const int32_t* __restrict__ perm, TW wg, TW wd, int I,
+    uint16_t* act, u32 act_bytes, float* __restrict__ ys, int n_gu, int gu_cols, int dn_cols,
+    int max_polls, int32_t* __restrict__ status) {
+  __shared__ u32x4 xs[2 * 16 * MF_TSTRIDE];
+  __shared__ float xsum[2 * 16 * 4];
+  const int b = blockIdx.x;
+  if (b < n_gu) {
+    tile_mfma_body<XT, ST, GB, true, NB, 1, false, 2, true>(
+        b % gu_cols, b / gu_cols, 0, xs, 16 * MF_TSTRIDE, xsum, 16 * 4, x, x_bytes, topk, ent,
+        nent, perm, wg, I, act, nullptr, 0, nullptr, 0, 1, nullptr);
+  } else {
+    const int d = b - n_gu;
+    tile_mfma_body<XT, ST, GB, false, NB, 1, false, 2, true>(
+        d % dn_cols, d / dn_cols, 0, xs, 16 * MF_TSTRIDE, xsum, 16 * 4, act, act_bytes, 0, ent,
+        nent, perm, wd, 0, nullptr, ys, 0, nullptr, 0, 1, nullptr, act, max_polls, status);
+  }
+}
+
 // ---------------------------------------------------------------------------
 template <int XT, int ST, bool GB, bool GATEUP>
 static int mfma_t(bool small, int max_entries, const void* src, int src_rows, int topk,
@@ -634,6 +716,32 @@ int launch_mfma_down(bool small, int max_entries, const void* act, int rows, con
                                        nullptr, (float*)ys, s);
   return mfma_t<XT, ST, false, false>(small, max_entries, act, rows, 0, ent, nent, perm, w, 0,
                                       nullptr, (float*)ys, s);
+}
+
+template <int XT, int ST>
+int launch_mfma_gd(int max_entries, const void* x, int T, int topk, const int4* ent,
+                   const int* nent, const int32_t* perm, const TW& wg, const TW& wd, int I,
+                   void* act, void* ys, int32_t* status, int max_polls, bool down_only,
+                   hipStream_t s) {
+  const int64_t x_bytes = (int64_t)T * wg.K * 2, act_bytes = (int64_t)T * topk * I * 2;
+  if (act_bytes >= ((int64_t)1 << 31) || (int64_t)wg.N * wg.K / 2 >= ((int64_t)1 << 31) ||
+      (int64_t)wd.N * wd.K / 2 >= ((int64_t)1 << 31))
+    return I4_ERR_SHAPE;
+  if (wg.gshift != wd.gshift) return I4_ERR_SHAPE;  // one group size for both
+  const int gu_cols = I / (32 * MF_NB), dn_cols = wd.N / (64 * MF_NB);
+  // down_only: the down workgroups alone (their waits then give up after max_polls)
+  const int n_gu = down_only ? 0 : gu_cols * max_entries;
+  const dim3 grid(n_gu + dn_cols * max_entries);
+#define I4_GD_LAUNCH(GB_)                                                                     \
+  hipLaunchKernelGGL((k_tile_mfma_gd<XT, ST, GB_, MF_NB, (XT == I4_F16 && GB_) ? 6 : 1>),     \
+                     grid, dim3(256), 0, s,                                                   \
+                     (const uint16_t*)x, (u32)x_bytes, topk, ent, nent, perm, wg, wd, I,      \
+                     (uint16_t*)act, (u32)act_bytes, (float*)ys, n_gu, gu_cols, dn_cols,     \
+                     max_polls, status)
+  if (wg.gshift >= 2) I4_GD_LAUNCH(true);
+  else I4_GD_LAUNCH(false);
+#undef I4_GD_LAUNCH
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
 // both entry lists of one projection in one launch (k_tile_mfma_mixed)
@@ -752,7 +860,10 @@ int launch_mfma_linear(const void* x, int M, const TW& w, const void* bias, void
                                           hipStream_t);                                        \
   template int launch_mfma_mixed<XT_, ST_>(bool, int, int, const void*, int, int, const int4*, \
                                            const int*, const int4*, const int*, const int32_t*, \
-                                           const TW&, int, void*, hipStream_t);
+                                           const TW&, int, void*, hipStream_t);                \
+  template int launch_mfma_gd<XT_, ST_>(int, const void*, int, int, const int4*, const int*,   \
+                                        const int32_t*, const TW&, const TW&, int, void*, void*, \
+                                        int32_t*, int, bool, hipStream_t);
 I4_INST(I4_F16, I4_F32) I4_INST(I4_F16, I4_F16) I4_INST(I4_F16, I4_BF16)
 I4_INST(I4_BF16, I4_F32) I4_INST(I4_BF16, I4_F16) I4_INST(I4_BF16, I4_BF16)
 #undef I4_INST

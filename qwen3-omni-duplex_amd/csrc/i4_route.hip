@@ -325,12 +325,15 @@ __global__ __launch_bounds__(256) void k_router_t(const uint16_t* __restrict__ x
   }
 }
 
-// one wave per token
+// one wave per token; every thread also fills its share of pend (n_pend 16-byte units)
+// with the pending pattern
 template <int LT, int VPL>
 __global__ __launch_bounds__(256) void k_topk(const void* __restrict__ logits, int T, int E,
                                               int topk, int renorm, int32_t* __restrict__ sel,
                                               float* __restrict__ wf, void* __restrict__ wh,
-                                              int wht) {
+                                              int wht, u32x4* __restrict__ pend, int n_pend) {
+  for (int i = blockIdx.x * 256 + (int)threadIdx.x; i < n_pend; i += gridDim.x * 256)
+    pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   wave_topk_row<LT, VPL>(logits, t, E, topk, renorm, sel, wf, wh, wht);
@@ -431,12 +434,12 @@ int i4_launch_moe_sum(const void* res, const void* ypart, const float* wts, int 
 }
 
 int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renorm, int32_t* sel,
-                   float* wf, void* wh, int wht, hipStream_t s) {
+                   float* wf, void* wh, int wht, hipStream_t s, void* pend, int n_pend) {
   dim3 grid((T + 3) / 4);
 #define I4_TOPK_CASE(LT_, VPL_)                                                             \
   if (lt == LT_ && E <= 64 * VPL_) {                                                        \
     hipLaunchKernelGGL((k_topk<LT_, VPL_>), grid, dim3(256), 0, s, logits, T, E, topk,      \
-                       renorm, sel, wf, wh, wht);                                           \
+                       renorm, sel, wf, wh, wht, (u32x4*)pend, n_pend);                      \
     return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;                         \
   }
   I4_TOPK_CASE(I4_F16, 2) I4_TOPK_CASE(I4_F16, 8)

@@ -288,7 +288,8 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
                 norm_topk_prob: bool = True, residual: torch.Tensor | None = None,
                 return_routing: bool = False, workspace: Workspace | None = None,
                 norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
-                gate_up_tile: QWeight | None = None, down_tile: QWeight | None = None):
+                gate_up_tile: QWeight | None = None, down_tile: QWeight | None = None,
+                _bounded: tuple[int, bool] | None = None):
     """One int4 MoE block: out = residual + sum_j w_j down_e(silu(gate_e xn) * up_e xn).
 
     xn = x, or RMSNorm(x) with weight norm_w (the decoder's post-attention norm).
@@ -315,6 +316,12 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
     nbytes = lb.i4_moe_workspace_bytes(T, H, I, E, top_k)
     ws = (workspace or Workspace()).get(nbytes, dev)
     mw = moe_weights_c(gate_up, down, router_w, norm_w, norm_eps, gate_up_tile, down_tile)
+    if _bounded is not None:
+        _lib.check(lb.i4_moe_forward_bounded(
+            xf.data_ptr(), xt, T, ctypes.byref(mw), top_k, int(norm_topk_prob), _lib.ptr(lg),
+            _lib.ptr(rs), out.data_ptr(), ws.data_ptr(), ws.numel(), int(_bounded[0]),
+            int(_bounded[1]), _lib.stream(dev)))
+        return out.view(shape)
     _lib.check(lb.i4_moe_forward(xf.data_ptr(), xt, T, ctypes.byref(mw), top_k,
                                  int(norm_topk_prob), _lib.ptr(lg), _lib.ptr(rs), out.data_ptr(),
                                  _lib.ptr(sel), _lib.ptr(wts), ws.data_ptr(), ws.numel(),
@@ -323,6 +330,15 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
     if return_routing:
         return out, sel, wts
     return out
+
+
+def moe_forward_bounded(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
+                        max_polls: int, down_only: bool = False, **kw) -> torch.Tensor:
+    """moe_forward for 2..64 tokens with the bound of the fused launch's in-launch wait
+    given (i4_moe_forward_bounded); down_only launches its down workgroups alone, so
+    every wait gives up (NaN out, I4_ERR_HANDOFF in the status word).  For testing the
+    bounded wait from the host."""
+    return moe_forward(x, gate_up, down, top_k, _bounded=(max_polls, down_only), **kw)
 
 
 def moe_status(workspace: Workspace, T: int, H: int, I: int, E: int, top_k: int) -> int:

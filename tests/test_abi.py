@@ -189,6 +189,19 @@ def test_moe_validation_codes(pkg):
     assert lib.i4_moe_forward(0x30000, 1, 1, ctypes.byref(nrm), 8, 1, 0x90000, None, 0x70000,
                               None, None, 0x100000, ws, None) == -1
     assert lib.i4_moe_stack_workspace_bytes(1, 2048, 768, 128, 8) > ws
+    # the bounded form takes the fused 2..64-token launch only, checked before any launch
+    ws32 = lib.i4_moe_workspace_bytes(32, 2048, 768, 128, 8)
+    bnd = lambda **kw: lib.i4_moe_forward_bounded(
+        0x30000, 1, kw.get("T", 32), kw.get("mw", ctypes.byref(mw)), 8, 1, None, None, 0x70000,
+        0x100000, kw.get("wsb", ws32), kw.get("polls", 3), 1, None)
+    assert bnd(mw=None) == -1
+    assert bnd(T=1) == -2
+    assert bnd(T=65) == -2
+    assert bnd(polls=-1) == -2
+    assert bnd(wsb=ws32 - 1) == -7
+    g64 = _lib.MoeWeightsC(gate_up=gu, down=_qw(_lib, E=128, N=2048, K=768, group=64, layout=2),
+                           router_w=0x60000)
+    assert bnd(mw=ctypes.byref(g64)) == -2  # different group sizes: nothing waits
 
 
 def test_decode_attention_validation_codes(pkg):

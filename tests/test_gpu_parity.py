@@ -795,6 +795,45 @@ def test_moe_m32(pkg, dev):
     _check_moe(pkg, moe, dgu, ddn, x, "f16", dev, residual=x)
 
 
+def test_moe_m32_fused_wait_gives_up_visibly(pkg, dev):
+    """At T <= 64 both expert projections share one launch whose down workgroups wait for
+    the activations of its gate_up workgroups.  i4_moe_forward_bounded runs the down
+    workgroups alone with the bound lowered from the host: every wait gives up, the output
+    is NaN and the status word holds I4_ERR_HANDOFF, and every kernel exits.  The next
+    ordinary call on the same workspace is correct (against the oracle) and clears the
+    word; the bounded call with its producers present and the full bound equals it bit for
+    bit."""
+    rng = np.random.default_rng(29)
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng)
+    T = 32
+    x_np = make_x(rng, (T, 2048), "f16")
+    x = t_(x_np, dev)
+    tiles = dict(gate_up_tile=moe.gate_up_tile, down_tile=moe.down_tile)
+    ws = pkg.Workspace()
+    E, I = moe.gate_up.E, moe.down.K
+    for polls in (0, 3):
+        y = pkg.ops.moe_forward_bounded(x, moe.gate_up, moe.down, moe.top_k, polls, True,
+                                        router_w=moe.router_w, residual=x, workspace=ws, **tiles)
+        torch.cuda.synchronize()
+        assert torch.isnan(y.float()).all()
+        assert pkg.moe_status(ws, T, 2048, I, E, moe.top_k) == -10
+    got = pkg.moe_forward(x, moe.gate_up, moe.down, moe.top_k, router_w=moe.router_w,
+                          residual=x, workspace=ws, **tiles)
+    assert pkg.moe_status(ws, T, 2048, I, E, moe.top_k) == 0
+    checked, _ = _check_moe(pkg, moe, dgu, ddn, x_np, "f16", dev, residual=x_np)  # vs oracle
+    assert np.array_equal(host(got), checked)
+    again = pkg.ops.moe_forward_bounded(x, moe.gate_up, moe.down, moe.top_k, 1 << 20, False,
+                                        router_w=moe.router_w, residual=x, workspace=ws, **tiles)
+    assert torch.equal(again, got)
+    assert pkg.moe_status(ws, T, 2048, I, E, moe.top_k) == 0
+    # one token runs the decode path, more than 64 the two-list launches: nothing to bound
+    for bad_T in (1, 65):
+        xb = t_(make_x(rng, (bad_T, 2048), "f16"), dev)
+        with pytest.raises(RuntimeError):
+            pkg.ops.moe_forward_bounded(xb, moe.gate_up, moe.down, moe.top_k, 3, True,
+                                        router_w=moe.router_w, workspace=ws, **tiles)
+
+
 def test_moe_m512_zipf_logits(pkg, dev):
     rng = np.random.default_rng(24)
     moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng)
