@@ -289,13 +289,17 @@ __device__ inline void tile_mfma_body(
   const int row = GATEUP ? perm[pos0 + min(tk, cnt - 1)] / topk : pos0 + min(tk, cnt - 1);
   const rsrc_t xr = rsrc(src, src_bytes);
   const u32 vx = ((u32)row * (u32)K + 8u * (u32)kw) * 2u;
-  // Ring slot: the weights of one superchunk and, for MB = 1, its activation
-  // word too, issued right after the weights: the in-order wait for that word
-  // at staging time then only covers loads the step needs anyway.  With MB = 4
-  // (four words per thread) the activations are loaded one step ahead instead.
+  // Ring slot: the weights of one superchunk and (XR) its activation words too, issued
+  // right after the weights: the in-order wait for them at staging time then only covers
+  // loads the step needs anyway.  Two-slot rings carry them (one word per thread for one
+  // m-block, four for the large entries of the mixed launch: two superchunks of lead, 118
+  // VGPRs); the three-slot ring of the other multi-m-block forms loads them one step ahead
+  // instead (three slots of four words would cost occupancy).  Measured on the M=512
+  // layer: 118.9 / 119.4 -> 117.5 / 116.5 us for the large entries' two-slot form.
+  constexpr bool XR = MB == 1 || RING == 2;
   struct Slot {
     TSlot<GB> w[NB];
-    u32x4 x;
+    u32x4 x[XR ? WPT : 1];
   };
   u32x4 xd[WPT];
   const rsrc_t hr = rsrc(HAND && !GATEUP ? hsrc : src, src_bytes);
@@ -346,7 +350,7 @@ __device__ inline void tile_mfma_body(
   };
   auto issue = [&](int sc, Slot& sl) {
     wissue<ST, GB, NB>(wb, scb + min(sc, SC - 1), sl.w);
-    if constexpr (MB == 1) load_x(sc, &sl.x);
+    if constexpr (XR) load_x(sc, sl.x);
   };
   f32x4 res[MB][NB];
 #pragma unroll
@@ -473,14 +477,14 @@ __device__ inline void tile_mfma_body(
   auto step = [&](int sc, Slot& sl) {
     const int buf = DBUF ? sc & 1 : 0;
     if constexpr (!DBUF) __syncthreads();  // the previous superchunk's reads are done
-    if constexpr (MB == 1) {
-      if constexpr (HAND && !GATEUP) wait_x(sc, sl.x);
-      commit_x(buf, &sl.x);
+    if constexpr (XR) {
+      if constexpr (HAND && !GATEUP) wait_x(sc, sl.x[0]);
+      commit_x(buf, sl.x);
     } else {
       commit_x(buf, xd);
     }
     __syncthreads();
-    if constexpr (MB != 1) load_x(sc + 1, xd);  // unconditional (clamped), like every load
+    if constexpr (!XR) load_x(sc + 1, xd);  // unconditional (clamped), like every load
     if (sc < SC) compute(scb + sc, sl.w, buf);
     issue(sc + RING, sl);
   };
@@ -496,7 +500,7 @@ __device__ inline void tile_mfma_body(
     __builtin_amdgcn_sched_barrier(0);
     issue(2, s2);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (MB != 1) load_x(0, xd);
+    if constexpr (!XR) load_x(0, xd);
     __builtin_amdgcn_sched_barrier(0);
     step(0, s0);
     step(1, s1);
@@ -512,7 +516,7 @@ __device__ inline void tile_mfma_body(
     __builtin_amdgcn_sched_barrier(0);
     issue(1, s1);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (MB != 1) load_x(0, xd);
+    if constexpr (!XR) load_x(0, xd);
     __builtin_amdgcn_sched_barrier(0);
     step(0, s0);
     step(1, s1);
@@ -631,7 +635,7 @@ __global__ __launch_bounds__(256) void k_tile_mfma_mixed(
   __shared__ float xsum[NBUF * TOKL * 4];
   const int y = blockIdx.y, nl = *n_large;
   if (y < nl)
-    tile_mfma_body<XT, ST, GB, GATEUP, NB, MF_TOK / 16, false>(
+    tile_mfma_body<XT, ST, GB, GATEUP, NB, MF_TOK / 16, false, 2>(
         blockIdx.x, y, 0, xs, TOKL * MF_TSTRIDE, xsum, TOKL * 4, src, src_bytes,
         topk, large, n_large, perm, w, I, act, ys, 0, nullptr, 0, 1, nullptr);
   else
