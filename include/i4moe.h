@@ -287,8 +287,9 @@ int    i4_moe_forward_bounded(const void* x, int x_dtype, int T, const i4_moe_we
 /* Byte offset, inside the workspace of i4_moe_forward / i4_moe_stack_forward
  * with these sizes, of an int32 status word that every call rewrites on the
  * device: I4_OK, or I4_ERR_HANDOFF when a workgroup of the single-launch decode
- * layer gave up waiting for the activations of its own launch (its output rows
- * are then NaN).  The host reads it after the stream has finished the call; a
+ * layer, or a down workgroup of the 2..64-token launch that runs both expert
+ * projections, gave up waiting for the activations of its own launch (its output
+ * rows are then NaN).  The host reads it after the stream has finished the call; a
  * stack call reports a give-up in any of its layers.  The wait only ends that
  * way if the launch's workgroups are not dispatched in block order, which the
  * wait assumes (no reference counterpart: the reference faults instead,
