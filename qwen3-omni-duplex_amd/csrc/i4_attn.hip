@@ -356,7 +356,10 @@ __global__ __launch_bounds__(256) void k_qkv_chunk(
 // accumulator value) is issued before any is used, so a context of up to
 // 64 CMB_B positions costs one memory round trip.
 static constexpr int CMB = 1024;  // chunks per head at most (max_len <= 65536)
-static constexpr int CMB_B = 16;  // chunks per batch of loads
+// chunks per batch of loads: 32, so the Thinker's context 1024 (1025 positions with the
+// token, 17 chunks) is one round trip, not two (decode step 743-747 -> 740 us per token,
+// 126 VGPRs in the merge launch)
+static constexpr int CMB_B = 32;
 // Head h's output dimension t (bits in the activation dtype): the merge of the
 // chunks' (m, l, acc) partials.
 template <int XT>
