@@ -236,7 +236,7 @@ __device__ inline void correct(f32x4& res, const f32x4& d, u32 sraw, u32 zw, int
 // RING: weight superchunks in flight per wave (2 or 3 register slots).
 // HAND (one m-block, not LIN): the two projections share a launch (k_tile_mfma_gd).  The
 // gate_up workgroups write act through to memory, every NaN in canonical form; the down
-// workgroups read act past the L1 and, before staging each superchunk, reload it until
+// workgroups read act and, before staging each superchunk, reload it past the L1 until
 // no value holds the pending pattern (act was set to it one launch earlier), at most
 // max_polls times: then their rows come out NaN and I4_ERR_HANDOFF goes to *status.
 // hsrc is act again, without __restrict__, so the reloads stay inside the wait loop.
@@ -303,12 +303,13 @@ __device__ inline void tile_mfma_body(
   };
   u32x4 xd[WPT];
   const rsrc_t hr = rsrc(HAND && !GATEUP ? hsrc : src, src_bytes);
+  // HAND down reads act through the caches first (an entry's activations are read by
+  // every column tile of it); only a word that still holds the pending pattern, in memory
+  // or in a line the L2 took before its producer wrote it, is reloaded past them (wait_x)
   auto load_x = [&](int sc, u32x4* dst) {
     sc = scb + min(sc, SC - 1);
 #pragma unroll
-    for (int q = 0; q < WPT; ++q)
-      dst[q] = HAND && !GATEUP ? bload16_coherent(hr, vx + 16u * q, sc * 256)
-                               : bload16(xr, vx + 16u * q, sc * 256);
+    for (int q = 0; q < WPT; ++q) dst[q] = bload16(xr, vx + 16u * q, sc * 256);
   };
   // HAND down: reload superchunk sc's activation word until no thread holds a pending
   // value (the workgroup decides together, so every thread runs the same passes)
