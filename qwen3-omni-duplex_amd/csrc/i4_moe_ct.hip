@@ -115,11 +115,14 @@ __device__ inline void gate_up_body(int bx, int by, const uint16_t* __restrict__
       cu[i] = load_chunk<ST>(ru, c, w.gshift);
     }
   };
-  auto dot_round = [&](int r0) {
+  // FULL: every chunk of the round lies inside the row for every lane, so the round runs
+  // as one basic block without a per-lane test (same products in the same order)
+  auto dot_round = [&](int r0, auto full) {
+    constexpr bool FULL = decltype(full)::value;
 #pragma unroll
     for (int i = 0; i < ROUND; ++i) {
       const int c = cl + (r0 + i) * L;
-      if (c < C) {
+      if (FULL || c < C) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           if (t < cnt) {
@@ -135,14 +138,18 @@ __device__ inline void gate_up_body(int bx, int by, const uint16_t* __restrict__
   };
   // round 0 is peeled: a loop-header wait would hold its weight loads behind
   // the activation loads
+  auto dot_any = [&](int r0) {
+    if ((r0 + ROUND) * L <= C) dot_round(r0, std::true_type{});
+    else dot_round(r0, std::false_type{});
+  };
   load_round(0);
   st.commit(0, xs, sums);
   st.rest(row_of, xs, sums);
   __syncthreads();
-  dot_round(0);
+  dot_any(0);
   for (int r0 = ROUND; r0 < cpl; r0 += ROUND) {
     load_round(r0);
-    dot_round(r0);
+    dot_any(r0);
   }
   // HANDOFF: the workgroup's RPW activations (one token) are gathered in LDS and go out
   // as whole 16-byte stores written through to memory, NaN in canonical form.
@@ -217,7 +224,7 @@ __device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int t
                                  uint16_t* __restrict__ out, unsigned char* lds,
                                  int32_t* __restrict__ status = nullptr, int max_polls = 0) {
   constexpr int GPR = DownShape<L>::GPR, RW = DownShape<L>::RW;
-  constexpr int CR = 4;  // chunks per round
+  constexpr int CR = 3;  // chunks per round (FFN 768 at 8 lanes a row: one full round)
   const int I = w.K, H = w.N, C = I >> 5;
   const int cpl = (C + L - 1) / L;
   u32x4* xs = (u32x4*)lds;
@@ -279,21 +286,29 @@ __device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int t
         if (i == 0 || (r0 + i) * L < C)  // wave-uniform: skips rounds past the row's end
           ch[jj][i] = load_chunk<ST>(rp[jj], min(cl + (r0 + i) * L, C - 1), w.gshift);
   };
-  auto dot_round = [&](int r0) {
+  // FULL: every slot of the wave is selected and every chunk of the round lies inside the
+  // row for every lane, so the round runs as one basic block (its LDS reads all go out
+  // before the first product); per row the chunks add up in the same order either way
+  auto dot_round = [&](int r0, auto full) {
+    constexpr bool FULL = decltype(full)::value;
 #pragma unroll
     for (int jj = 0; jj < JMAX; ++jj) {
       const int j = jg + jj * GPR;
-      if (j < topk) {
+      if (FULL || j < topk) {
         const u32x4* xj = xs + (size_t)j * 4 * C;
 #pragma unroll
         for (int i = 0; i < CR; ++i) {
           const int c = cl + (r0 + i) * L;
-          if (c < C)
+          if (FULL || c < C)
             row[jj] += chunk_dot<XT, ST>(ch[jj][i], xj[c], xj[C + c], xj[2 * C + c], xj[3 * C + c],
                                          sums[j * C + c], c, w.gshift, mg);
         }
       }
     }
+  };
+  auto dot_any = [&](int r0) {
+    if (jg + (JMAX - 1) * GPR < topk && (r0 + CR) * L <= C) dot_round(r0, std::true_type{});
+    else dot_round(r0, std::false_type{});
   };
   // round 0 is peeled: a loop-header wait would hold its weight loads behind
   // the activation loads
@@ -304,10 +319,10 @@ __device__ inline void down_body(int bx, const uint16_t* __restrict__ act, int t
   if constexpr (!HANDOFF) st.rest(row_of, xs, sums);
   if ((int)threadIdx.x < topk) s_w[threadIdx.x] = wv;
   __syncthreads();
-  dot_round(0);
+  dot_any(0);
   for (int r0 = CR; r0 < cpl; r0 += CR) {
     load_round(r0);
-    dot_round(r0);
+    dot_any(r0);
   }
 #pragma unroll
   for (int jj = 0; jj < JMAX; ++jj) {
@@ -429,7 +444,7 @@ __device__ inline void down_slot_body(int j, int m, const uint16_t* __restrict__
                                       uint16_t* __restrict__ ypart, unsigned char* lds,
                                       int32_t* __restrict__ status, int max_polls) {
   constexpr int RP = WG / L, RWD = RP * JR;
-  constexpr int CR = 4;  // chunks per round
+  constexpr int CR = 3;  // chunks per round (FFN 768 at 8 lanes a row: one full round)
   const int I = w.K, H = w.N, C = I >> 5;
   const int cpl = (C + L - 1) / L;
   u32x4* xs = (u32x4*)lds;
@@ -463,16 +478,27 @@ __device__ inline void down_slot_body(int j, int m, const uint16_t* __restrict__
         if (i == 0 || (r0 + i) * L < C)  // wave-uniform: skips rounds past the row's end
           ch[jr][i] = load_chunk<ST>(rp[jr], min(cl + (r0 + i) * L, C - 1), w.gshift);
   };
-  auto dot_round = [&](int r0) {
+  // A round whose chunks all lie inside the row for every lane (FULL) runs without a
+  // per-lane test: one basic block, so the LDS reads of its chunks, shared by the JR rows,
+  // all go out before the first product (the guarded form waits on each chunk's reads in
+  // turn).  Per row, the chunks add up in the same order either way.
+  auto dot_round = [&](int r0, auto full) {
+    constexpr bool FULL = decltype(full)::value;
 #pragma unroll
-    for (int jr = 0; jr < JR; ++jr)
+    for (int i = 0; i < CR; ++i) {
+      const int c = cl + (r0 + i) * L;
+      if (FULL || c < C) {
+        const u32x4 x0 = xs[c], x1 = xs[C + c], x2 = xs[2 * C + c], x3 = xs[3 * C + c];
+        const float2 sm = sums[c];
 #pragma unroll
-      for (int i = 0; i < CR; ++i) {
-        const int c = cl + (r0 + i) * L;
-        if (c < C)
-          row[jr] += chunk_dot<XT, ST>(ch[jr][i], xs[c], xs[C + c], xs[2 * C + c], xs[3 * C + c],
-                                       sums[c], c, w.gshift, mg);
+        for (int jr = 0; jr < JR; ++jr)
+          row[jr] += chunk_dot<XT, ST>(ch[jr][i], x0, x1, x2, x3, sm, c, w.gshift, mg);
       }
+    }
+  };
+  auto dot_any = [&](int r0) {
+    if ((r0 + CR) * L <= C) dot_round(r0, std::true_type{});
+    else dot_round(r0, std::false_type{});
   };
   // the weight loads go out first; the activation row is polled behind them
   load_round(0);
@@ -480,10 +506,10 @@ __device__ inline void down_slot_body(int j, int m, const uint16_t* __restrict__
   const bool late = poll_row_xcd<XT>(st, act + (int64_t)j * I, max_polls);
   st.commit(0, xs, sums);
   __syncthreads();
-  dot_round(0);
+  dot_any(0);
   for (int r0 = CR; r0 < cpl; r0 += CR) {
     load_round(r0);
-    dot_round(r0);
+    dot_any(r0);
   }
 #pragma unroll
   for (int jr = 0; jr < JR; ++jr) {
