@@ -327,7 +327,7 @@ struct QkvProj {
 };
 
 template <int XT, int ST, int L, int GQ>
-__global__ __launch_bounds__(256) void k_qkv_chunk(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XT == I4_F16 ? 4 : 3))) void k_qkv_chunk(
     QkvProj pr, u32* qkv, const u32* __restrict__ epoch, int nq, int nkv,
     const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, float eps,
     const int32_t* __restrict__ pos_dev, int pos_host, int max_len, RopeTab rt,

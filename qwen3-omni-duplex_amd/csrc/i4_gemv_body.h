@@ -81,42 +81,63 @@ __device__ __forceinline__ void gemv_ct_body(
 
   bool late = false;
   float row = 0.f;
-  for (int r0 = 0; r0 < cpl; r0 += ROUND) {
-    Chunk ch[ROUND];
+  // A round takes R = ROUND chunks per lane, or 2 where at most 2 are left (a row of 2L
+  // chunks issues no dead loads).  A FULL round has every chunk inside the row for every
+  // lane: no per-lane test, so the round's dot is one basic block whose LDS reads all go
+  // out before the first product.  The chunks add up in the same order in every form.
+  // The activation row is staged once, after the first round's weight loads are issued.
+  auto stage = [&]() {
+    if constexpr (POLL) late = poll_rows<XT>(st, xrow, max_polls);
+    if constexpr (NORM) {
+      __shared__ float s_ss[WG / 64];
+      float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < ROUND; ++i) ch[i] = load_chunk<ST>(rp, min(cl + (r0 + i) * L, C - 1), gshift);
-    if (r0 == 0) {
-      if constexpr (POLL) late = poll_rows<XT>(st, xrow, max_polls);
-      if constexpr (NORM) {
-        __shared__ float s_ss[WG / 64];
-        float ss = 0.f;
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-          if (u * WG + (int)threadIdx.x < st.total) ss += sumsq8<XT>(st.d[u]);
-        ss = group_sum<64>(ss);
-        if ((threadIdx.x & 63) == 0) s_ss[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        const float r =
-            1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)K + eps);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          st.d[u].x = norm_pair<XT>(st.d[u].x, gv[u].x, r);
-          st.d[u].y = norm_pair<XT>(st.d[u].y, gv[u].y, r);
-          st.d[u].z = norm_pair<XT>(st.d[u].z, gv[u].z, r);
-          st.d[u].w = norm_pair<XT>(st.d[u].w, gv[u].w, r);
-        }
-      }
-      st.commit(0, xs, sums);
-      if constexpr (!POLL) st.rest(row_of, xs, sums);
+      for (int u = 0; u < 2; ++u)
+        if (u * WG + (int)threadIdx.x < st.total) ss += sumsq8<XT>(st.d[u]);
+      ss = group_sum<64>(ss);
+      if ((threadIdx.x & 63) == 0) s_ss[threadIdx.x >> 6] = ss;
       __syncthreads();
-    }
+      const float r =
+          1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) / (float)K + eps);
 #pragma unroll
-    for (int i = 0; i < ROUND; ++i) {
+      for (int u = 0; u < 2; ++u) {
+        st.d[u].x = norm_pair<XT>(st.d[u].x, gv[u].x, r);
+        st.d[u].y = norm_pair<XT>(st.d[u].y, gv[u].y, r);
+        st.d[u].z = norm_pair<XT>(st.d[u].z, gv[u].z, r);
+        st.d[u].w = norm_pair<XT>(st.d[u].w, gv[u].w, r);
+      }
+    }
+    st.commit(0, xs, sums);
+    if constexpr (!POLL) st.rest(row_of, xs, sums);
+    __syncthreads();
+  };
+  auto round = [&](int r0, auto rr, auto full) {
+    constexpr int R = decltype(rr)::value;
+    constexpr bool FULL = decltype(full)::value;
+    Chunk ch[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      ch[i] = load_chunk<ST>(rp, FULL ? cl + (r0 + i) * L : min(cl + (r0 + i) * L, C - 1), gshift);
+    if (r0 == 0) stage();
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
       const int c = cl + (r0 + i) * L;
-      if (c < C)
+      if (FULL || c < C)
         row += chunk_dot<XT, ST>(ch[i], xs[c], xs[C + c], xs[2 * C + c], xs[3 * C + c], sums[c], c,
                                  gshift, mg);
     }
+  };
+  using R2 = std::integral_constant<int, 2>;
+  using RF = std::integral_constant<int, ROUND>;
+  for (int r0 = 0; r0 < cpl;) {
+    // the shape of the round (wave-uniform)
+    const bool two = cpl - r0 <= 2;
+    const bool full = (r0 + (two ? 2 : ROUND)) * L <= C;
+    if (two && full) round(r0, R2{}, std::true_type{});
+    else if (two) round(r0, R2{}, std::false_type{});
+    else if (full) round(r0, RF{}, std::true_type{});
+    else round(r0, RF{}, std::false_type{});
+    r0 += two ? 2 : ROUND;
   }
   row = group_sum<L>(row);
   if constexpr (POLL) {  // a wait that gave up is reported (status nullable)
