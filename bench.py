@@ -61,7 +61,7 @@ B_EXPERTS_LAUNCH = (TOPK * (B_GATE_UP_EXPERT + B_DOWN_EXPERT) + H * 2 + 2 * TOPK
                     + TOPK * H * 2)                                                  # 19,673,088
 # HBM bytes per decode experts launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (calibrated against a device copy; summary under profiles/)
-EXPERTS_TRAFFIC_BYTES = 20_083_056
+EXPERTS_TRAFFIC_BYTES = 20_061_560
 
 
 def log(msg: str) -> None:
