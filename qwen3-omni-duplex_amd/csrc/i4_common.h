@@ -219,6 +219,16 @@ template <int XT> __device__ inline u32 magic_v() { return vgpr_const(Half<XT>::
 // hi-pair weight of the fp16 decode (its pairs carry 16q)
 template <int XT> constexpr float hi_scale() { return XT == I4_F16 ? 1.0f / 16.0f : 1.0f; }
 
+// the end of a chunk's dot: scale and zero applied to the decoded pair sums lo / hi
+template <int XT, int ST>
+__device__ inline float chunk_tail(float lo, float hi, u32 s, u32 zw, float2 sums, int c,
+                                   int gshift) {
+  const int g = c >> gshift;
+  const float z = (float)((zw >> (4 * (g & 7))) & 15u);
+  const float a = fmaf(hi, hi_scale<XT>(), lo);
+  return scale_from_raw<ST>(s) * (a - Half<XT>::MAGIC * sums.x - z * sums.y);
+}
+
 // sum over one chunk of (q - z) * s * x given the chunk's staged x words
 // (xw0..xw3, pair order) and its sums (Sb, S)
 template <int XT, int ST>
@@ -229,10 +239,63 @@ __device__ inline float chunk_dot(const Chunk& k, u32x4 xw0, u32x4 xw1, u32x4 xw
   dot8<XT>(k.w.y, xw1, lo, hi, mg);
   dot8<XT>(k.w.z, xw2, lo, hi, mg);
   dot8<XT>(k.w.w, xw3, lo, hi, mg);
-  const int g = c >> gshift;
-  const float z = (float)((k.z >> (4 * (g & 7))) & 15u);
-  const float a = fmaf(hi, hi_scale<XT>(), lo);
-  return scale_from_raw<ST>(k.s) * (a - Half<XT>::MAGIC * sums.x - z * sums.y);
+  return chunk_tail<XT, ST>(lo, hi, k.s, k.z, sums, c, gshift);
+}
+
+// A chunk with its nibbles already spread into the (nibble | magic) pairs that dot8
+// builds, four per word in dot8's order: for a projection whose weights land before its
+// activations, so the spreading runs while the activations are in flight.  xchunk_dot
+// then does chunk_dot's products in chunk_dot's order (the same result bit for bit).
+struct XChunk {
+  u32 p[16];
+  u32 s, z;
+};
+
+template <int XT> __device__ inline XChunk expand_chunk(const Chunk& k, u32 mg) {
+  constexpr u32 MK = 0x000F000Fu;
+  XChunk x;
+  const u32 w4[4] = {k.w.x, k.w.y, k.w.z, k.w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32 w = w4[i];
+    if constexpr (XT == I4_F16) {
+      const u32 t = w >> 8;
+      x.p[4 * i] = (w & MK) | mg;
+      x.p[4 * i + 1] = (w & 0x00F000F0u) | mg;
+      x.p[4 * i + 2] = (t & MK) | mg;
+      x.p[4 * i + 3] = (t & 0x00F000F0u) | mg;
+    } else {
+      x.p[4 * i] = (w & MK) | mg;
+      x.p[4 * i + 1] = ((w >> 4) & MK) | mg;
+      x.p[4 * i + 2] = ((w >> 8) & MK) | mg;
+      x.p[4 * i + 3] = ((w >> 12) & MK) | mg;
+    }
+  }
+  x.s = k.s;
+  x.z = k.z;
+  return x;
+}
+
+// keeps the spread pairs where they are computed: the compiler would otherwise move the
+// spreading next to its use, past the wait it is meant to overlap
+__device__ inline void pin(XChunk& x) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x.p[i]));
+}
+
+template <int XT, int ST>
+__device__ inline float xchunk_dot(const XChunk& k, u32x4 xw0, u32x4 xw1, u32x4 xw2, u32x4 xw3,
+                                   float2 sums, int c, int gshift) {
+  float lo = 0.f, hi = 0.f;
+  const u32x4 xw[4] = {xw0, xw1, xw2, xw3};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo = Half<XT>::dot2(k.p[4 * i], xw[i].x, lo);
+    hi = Half<XT>::dot2(k.p[4 * i + 1], xw[i].y, hi);
+    lo = Half<XT>::dot2(k.p[4 * i + 2], xw[i].z, lo);
+    hi = Half<XT>::dot2(k.p[4 * i + 3], xw[i].w, hi);
+  }
+  return chunk_tail<XT, ST>(lo, hi, k.s, k.z, sums, c, gshift);
 }
 
 // Permute 8 consecutive half-precision x values (one 16-byte load, dwords

@@ -415,23 +415,31 @@ static constexpr int XCDS = 8;
 // is served by a line their L2 holds dirty, elsewhere from memory.  Returns true if
 // max_polls passes went by without every value.  Thread t reads words t, t + 256, ...
 // of the row (st.d[u]), and only those; the barrier of each pass keeps the loads
-// inside the loop.
-template <int XT>
-__device__ inline bool poll_row_xcd(Stager<XT, 256>& st, const uint16_t* src, int max_polls) {
+// inside the loop.  mid() runs once, after the first pass's loads are issued and
+// before they are checked: work on data loaded earlier (loads retire in issue order,
+// so it waits for those alone) overlaps the first round trip.
+template <int XT, class Mid>
+__device__ inline bool poll_row_xcd(Stager<XT, 256>& st, const uint16_t* src, int max_polls,
+                                    Mid mid) {
   const rsrc_t r = rsrc(src, (u32)st.total * 16u);
-  for (int it = 0;; ++it) {
-    bool pend = false;
+  auto issue = [&]() {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int idx = u * 256 + (int)threadIdx.x;
       if (idx < st.total) st.d[u] = ld16_coherent(r, (u32)idx * 16u);
     }
+  };
+  issue();
+  mid();
+  for (int it = 0;; ++it) {
+    bool pend = false;
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       if (u * 256 + (int)threadIdx.x < st.total) pend |= has_pending(st.d[u]);
     if (!__syncthreads_or(pend)) return false;
     if (it >= max_polls) return true;
     __builtin_amdgcn_s_sleep(1);
+    issue();
   }
 }
 
@@ -482,6 +490,12 @@ __device__ inline void down_slot_body(int j, int m, const uint16_t* __restrict__
   // per-lane test: one basic block, so the LDS reads of its chunks, shared by the JR rows,
   // all go out before the first product (the guarded form waits on each chunk's reads in
   // turn).  Per row, the chunks add up in the same order either way.
+  // A full first round (below) keeps its first chunk of every row spread into decode
+  // pairs (XChunk), spread while the activation row is in flight: 12 more VGPRs a
+  // chunk, so one chunk of each row, within the four workgroups per CU the launch needs.
+  constexpr bool XP = JR <= 2;  // more rows per lane would cost the launch its occupancy
+  XChunk xc[XP ? JR : 1];
+  const bool full0 = XP && CR * L <= C;
   auto dot_round = [&](int r0, auto full) {
     constexpr bool FULL = decltype(full)::value;
 #pragma unroll
@@ -492,24 +506,34 @@ __device__ inline void down_slot_body(int j, int m, const uint16_t* __restrict__
         const float2 sm = sums[c];
 #pragma unroll
         for (int jr = 0; jr < JR; ++jr)
-          row[jr] += chunk_dot<XT, ST>(ch[jr][i], x0, x1, x2, x3, sm, c, w.gshift, mg);
+          row[jr] += XP && FULL && i == 0 && r0 == 0
+                         ? xchunk_dot<XT, ST>(xc[XP ? jr : 0], x0, x1, x2, x3, sm, c, w.gshift)
+                         : chunk_dot<XT, ST>(ch[jr][i], x0, x1, x2, x3, sm, c, w.gshift, mg);
       }
     }
-  };
-  auto dot_any = [&](int r0) {
-    if ((r0 + CR) * L <= C) dot_round(r0, std::true_type{});
-    else dot_round(r0, std::false_type{});
   };
   // the weight loads go out first; the activation row is polled behind them
   load_round(0);
   Stager<XT> st(1, I);
-  const bool late = poll_row_xcd<XT>(st, act + (int64_t)j * I, max_polls);
+  const bool late = poll_row_xcd<XT>(st, act + (int64_t)j * I, max_polls, [&]() {
+    if constexpr (XP) {
+      if (full0) {
+#pragma unroll
+        for (int jr = 0; jr < JR; ++jr) {
+          xc[jr] = expand_chunk<XT>(ch[jr][0], mg);
+          pin(xc[jr]);
+        }
+      }
+    }
+  });
   st.commit(0, xs, sums);
   __syncthreads();
-  dot_any(0);
+  if (full0) dot_round(0, std::true_type{});
+  else dot_round(0, std::false_type{});
   for (int r0 = CR; r0 < cpl; r0 += CR) {
     load_round(r0);
-    dot_any(r0);
+    if ((r0 + CR) * L <= C) dot_round(r0, std::true_type{});
+    else dot_round(r0, std::false_type{});
   }
 #pragma unroll
   for (int jr = 0; jr < JR; ++jr) {
