@@ -264,8 +264,13 @@ int    i4_moe_forward(const void* x, int x_dtype, int T, const i4_moe_weights* w
                       void* out, int32_t* sel_out, float* w_out,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* Workspace of i4_moe_forward (scratch for logits, routing, expert lists and
- * intermediate activations; no state is kept between calls).  Calls that
- * share one workspace must not overlap. */
+ * intermediate activations).  One word carries over from call to call: the first
+ * four bytes hold the epoch of the 2..64-token routing launch, whose router
+ * workgroups hand their logits to the ranking waves as (value pair, tag) words
+ * tagged with it and which a later launch of the call advances, so no word left by
+ * an earlier call can pass for this call's; any starting value works (no
+ * initialisation; a word left by something else passes with odds 2^-32).  Calls
+ * that share one workspace must not overlap. */
 size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
 
 /* i4_moe_forward for 2 <= T <= 64 tokens with the bound of its in-launch wait set by
@@ -289,7 +294,9 @@ int    i4_moe_forward_bounded(const void* x, int x_dtype, int T, const i4_moe_we
  * device: I4_OK, or I4_ERR_HANDOFF when a workgroup of the single-launch decode
  * layer, or a down workgroup of the 2..64-token launch that runs both expert
  * projections, gave up waiting for the activations of its own launch (its output
- * rows are then NaN).  The host reads it after the stream has finished the call; a
+ * rows are then NaN), or a ranking wave of the 2..64-token routing launch (router
+ * logits and top-k in one launch, E <= 128) gave up waiting for its token's logits
+ * (its routing weights, and so its output row, are then NaN).  The host reads it after the stream has finished the call; a
  * stack call reports a give-up in any of its layers.  The wait only ends that
  * way if the launch's workgroups are not dispatched in block order, which the
  * wait assumes (no reference counterpart: the reference faults instead,

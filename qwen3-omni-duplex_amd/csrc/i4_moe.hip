@@ -203,9 +203,12 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t* __restrict__ sel,
                                                 int* __restrict__ n_entries,
                                                 int4* __restrict__ mf_entries,
                                                 int* __restrict__ n_mf_entries,
-                                                int32_t* __restrict__ status) {
+                                                int32_t* __restrict__ status,
+                                                u32* __restrict__ epoch) {
   extern __shared__ __align__(16) unsigned char lds[];
-  if (status && threadIdx.x == 0) *status = I4_OK;  // nothing on this path waits
+  if (status && threadIdx.x == 0) *status = I4_OK;  // nothing before this launch waits
+  // the routing words of the next call carry another tag (k_router_topk_t)
+  if (epoch && threadIdx.x == 0) *epoch = *epoch + 1u;
   group_body(sel, T, topk, E, lo_max, lo_chunk, perm, entries, n_entries, mf_entries,
              n_mf_entries, lds);
 }
@@ -235,6 +238,7 @@ struct MoeWs {
   int4* mf_entries;  // large MFMA entries (<= MF_TOK tokens)
   int* n_mf_entries;
   int32_t* status;  // I4_OK or I4_ERR_HANDOFF (i4_moe_status_offset)
+  u32* epoch;
   size_t bytes;
 };
 
@@ -248,7 +252,11 @@ MoeWs carve(void* base, int T, int H, int I, int E, int topk) {
     o += al256(b);
     return p;
   };
-  m.logits = take((size_t)Tc * E * 2);
+  // the tag epoch of the fused routing's words first, at the same offset for every T, so
+  // that no other layout of the workspace writes over it
+  m.epoch = (u32*)take(4);
+  // [Tc][E] half logits, or [Tc][E / 2] (value pair, tag) words of the fused routing
+  m.logits = take((size_t)Tc * E * 4);
   m.xn = (uint16_t*)take((size_t)Tc * H * 2);
   m.sel = (int32_t*)take(Tk * 4);
   m.w = (float*)take(Tk * 4);
@@ -417,35 +425,49 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
     return (ct ? ops.down_m1_ct : ops.down_m1)(ws.act, topk, sel, wts, to_tw(dn), residual, out, s);
   }
   const TW tgu = to_tw(tg), tdn = to_tw(td);
+  const int Tk = T * topk;
+  const bool one_list = T <= ONE_LIST_T;
+  // T <= 64 with one group size for both projections: gate_up and down share a launch
+  // whose down workgroups take act over inside it; the routing launch sets act pending.
+  // (The same for both entry lists above 64 tokens measured no faster at M = 512: setting
+  // 6.3 MB pending and writing the activations through cost what the launch saved.)
+  const bool gd = one_list && tgu.gshift == tdn.gshift;
+  void* pend = gd ? ws.act : nullptr;
+  const int n_pend = gd ? (int)((int64_t)Tk * I / 8) : 0;
+  // 2..64 tokens with the router in the block: router and top-k as one launch whose
+  // ranking waves take the logits over inside it (k_router_topk_t)
+  const bool fused = mw->router_w && T >= 2 && T <= 64 && E <= 128 && E % 4 == 0;
   const void* lg = logits;
-  if (mw->router_w) {
+  if (fused) {
+    rc = i4_launch_router_topk(x, xt, T, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
+                               mw->norm_w ? ws.xn : nullptr, (u32*)ws.logits, ws.epoch, topk,
+                               renorm, sel, wts, pend, n_pend, st_reset, ws.status, kHandoffPolls,
+                               s);
+    if (rc) return rc;
+    if (mw->norm_w) x = ws.xn;
+    st_reset = nullptr;
+  } else if (mw->router_w) {
     rc = i4_launch_router_logits(x, xt, T, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
                                  mw->norm_w ? ws.xn : nullptr, ws.logits, s);
     if (rc) return rc;
     lg = ws.logits;
     if (mw->norm_w) x = ws.xn;
   }
-  const int Tk = T * topk;
   const int TW_ = (T + 31) / 32;
   const size_t glds = (size_t)2 * E * TW_ * 4 + (size_t)E * 4;
   // T <= MF_TOK: no expert has more tokens than one large entry holds, and
   // small entries of <= MF_SMALL tokens cover every expert in one launch per
-  // projection; above, experts with > MF_SMALL tokens take large entries
-  const bool one_list = T <= ONE_LIST_T;
-  // top-k on T / 4 workgroups (one token per wave), then the grouping: ranking every
-  // token inside the one grouping workgroup queued the waves' scalar bisection steps on
-  // one CU's scalar unit (5 us of the launch at T = 32; separate launches 1.5 us faster)
-  // T <= 64 with one group size for both projections: gate_up and down share a launch
-  // whose down workgroups take act over inside it; the top-k launch sets act pending.
-  // (The same for both entry lists above 64 tokens measured no faster at M = 512: setting
-  // 6.3 MB pending and writing the activations through cost what the launch saved.)
-  const bool gd = one_list && tgu.gshift == tdn.gshift;
-  rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s, gd ? ws.act : nullptr,
-                      gd ? (int)((int64_t)Tk * I / 8) : 0);
-  if (rc) return rc;
+  // projection; above, experts with > MF_SMALL tokens take large entries.
+  // Otherwise top-k on T / 4 workgroups (one token per wave), then the grouping: ranking
+  // every token inside the one grouping workgroup queued the waves' scalar bisection steps
+  // on one CU's scalar unit (5 us of the launch at T = 32; separate launches 1.5 us faster)
+  if (!fused) {
+    rc = i4_launch_topk(lg, xt, T, E, topk, renorm, sel, wts, nullptr, 0, s, pend, n_pend);
+    if (rc) return rc;
+  }
   hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), glds, s, sel, T, topk, E,
                      one_list ? T : MF_SMALL, MF_SMALL, ws.perm, ws.entries, ws.n_entries,
-                     ws.mf_entries, ws.n_mf_entries, st_reset);
+                     ws.mf_entries, ws.n_mf_entries, st_reset, fused ? ws.epoch : nullptr);
   if (hipGetLastError() != hipSuccess) return I4_ERR_LAUNCH;
   // entry counts: sum over experts of ceil(n_e / 16) <= min(E, Tk) + Tk / 16
   const int max_s = (E < Tk ? E : Tk) + (one_list ? Tk / MF_SMALL : 0);

@@ -259,16 +259,17 @@ __global__ __launch_bounds__(256) void k_rmsnorm_t(const uint16_t* __restrict__ 
 // k_router_m1, so a token's logits do not depend on the batch.  Wave w owns
 // experts EPW * w .. of the tile; the TT sums of one expert are formed
 // together so their wave reductions overlap.
-template <int XT, int TT, int EPW>
-__global__ __launch_bounds__(256) void k_router_t(const uint16_t* __restrict__ x, int T, int H,
-                                                  const uint16_t* __restrict__ wr, int E,
-                                                  uint16_t* __restrict__ logits) {
+// The body takes its tile (bx: expert group, by: token tile) and stores each finished
+// logit through store(token, expert, value), from lane 0 of the wave that made it.
+template <int XT, int TT, int EPW, class Store>
+__device__ inline void router_t_body(int bx, int by, const uint16_t* __restrict__ x, int T, int H,
+                                     const uint16_t* __restrict__ wr, int E, Store store) {
   constexpr int RL = 8;  // 512-element rounds of a router row (H <= 4096)
   extern __shared__ __align__(16) unsigned char lds[];
   u32x4* s_x = (u32x4*)lds;  // [TT][words]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int words = H >> 3, rounds = (H + 511) / 512;
-  const int t0 = blockIdx.y * TT, e0 = (blockIdx.x * 4 + wave) * EPW;
+  const int t0 = by * TT, e0 = (bx * 4 + wave) * EPW;
   u32x4 wv[EPW][RL];
 #pragma unroll
   for (int j = 0; j < EPW; ++j) {
@@ -320,8 +321,87 @@ __global__ __launch_bounds__(256) void k_router_t(const uint16_t* __restrict__ x
     if (lane == 0 && e < E) {
 #pragma unroll
       for (int tk = 0; tk < TT; ++tk)
-        if (t0 + tk < T) logits[(int64_t)(t0 + tk) * E + e] = Half<XT>::from_f32(a[tk]);
+        if (t0 + tk < T) store(t0 + tk, e, a[tk]);
     }
+  }
+}
+
+template <int XT, int TT, int EPW>
+__global__ __launch_bounds__(256) void k_router_t(const uint16_t* __restrict__ x, int T, int H,
+                                                  const uint16_t* __restrict__ wr, int E,
+                                                  uint16_t* __restrict__ logits) {
+  router_t_body<XT, TT, EPW>(blockIdx.x, blockIdx.y, x, T, H, wr, E, [&](int t, int e, float a) {
+    logits[(int64_t)t * E + e] = Half<XT>::from_f32(a);
+  });
+}
+
+// Tag of the routing words of one call at workspace epoch e: odd, so a zero-filled
+// buffer never matches.
+__device__ inline u32 route_tag(u32 e) { return (2u * e + 1u) * 0x9E3779B1u; }
+
+// Routing of 2..64 tokens (E <= 128, E % 4 == 0) as one launch.  Blocks [0, T E / 4) are
+// k_router_t<XT, 1, 1>'s workgroups (block b: token b / (E / 4), experts 4 (b % (E / 4))
+// .. + 3, one per wave; the same logits bit for bit); each writes its four logits as two
+// (value pair, tag) words, lgt [T][E / 2][2], in one 16-byte store written through.  The
+// ceil(T / 4) blocks after them rank one token per wave, as k_topk does, once every word
+// of the token's row holds this call's tag (loads past the L1, at most max_polls passes:
+// then the token's routing weights are NaN and I4_ERR_HANDOFF goes to *status), and set
+// pend (n_pend 16-byte units) to the pending pattern for the grouped launch.  Only the
+// later blocks wait, and only for earlier ones.  A later launch of the call (k_group)
+// advances *epoch, so the next call's words carry another tag and no pending pattern is
+// needed here.  status_reset (nullable) gets I4_OK from block 0 first.
+template <int XT>
+__global__ __launch_bounds__(256) void k_router_topk_t(
+    const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ wr, int E,
+    u32* lgt, const u32* __restrict__ epoch, int topk, int renorm,
+    int32_t* __restrict__ sel, float* __restrict__ wf, u32x4* __restrict__ pend, int n_pend,
+    int32_t* __restrict__ status_reset, int32_t* __restrict__ status, int max_polls) {
+  const int G = E >> 2, nr = G * T;
+  const int b = blockIdx.x;
+  const u32 tag = route_tag(__builtin_amdgcn_readfirstlane(*epoch));
+  if (b < nr) {
+    __shared__ uint16_t s_lg[4];
+    if (b == 0 && status_reset && threadIdx.x == 0) *status_reset = I4_OK;
+    const int t = b / G, g = b - t * G;
+    router_t_body<XT, 1, 1>(g, t, x, T, H, wr, E,
+                            [&](int, int e, float a) { s_lg[e & 3] = Half<XT>::from_f32(a); });
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const u32 p0 = (u32)s_lg[0] | ((u32)s_lg[1] << 16), p1 = (u32)s_lg[2] | ((u32)s_lg[3] << 16);
+      const rsrc_t r = rsrc(lgt, (u32)T * (u32)E * 4u);
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{p0, tag, p1, tag}, r,
+                                             (u32)t * (u32)E * 4u + (u32)g * 16u, 0, kCoherent);
+    }
+    return;
+  }
+  const int rb = b - nr, nrb = (int)gridDim.x - nr;
+  for (int i = rb * 256 + (int)threadIdx.x; i < n_pend; i += nrb * 256)
+    pend[i] = u32x4{~0u, ~0u, ~0u, ~0u};
+  const int t = rb * 4 + ((int)threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  // lane l ranks experts l and l + 64 (load_row's order), from words l / 2 and 32 + l / 2
+  // (lgt is not __restrict__, so the reloads stay inside the wait loop)
+  const rsrc_t r = rsrc(lgt, (u32)T * (u32)E * 4u);
+  const int ea = min(lane, E - 1), eb = min(lane + 64, E - 1);
+  const u32 ra = (u32)t * (u32)E * 4u;
+  u32x2 va, vb;
+  bool late = false;
+  for (int it = 0;; ++it) {
+    va = __builtin_amdgcn_raw_buffer_load_b64(r, ra + (u32)(ea >> 1) * 8u, 0, kCoherent);
+    vb = __builtin_amdgcn_raw_buffer_load_b64(r, ra + (u32)(eb >> 1) * 8u, 0, kCoherent);
+    if (__builtin_amdgcn_ballot_w64(va.y != tag || vb.y != tag) == 0) break;
+    if (it >= max_polls) {
+      late = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    asm volatile("" ::: "memory");
+  }
+  u32 raw[2] = {(va.x >> (16 * (ea & 1))) & 0xFFFFu, (vb.x >> (16 * (eb & 1))) & 0xFFFFu};
+  topk_row<XT, 2>(raw, t, E, topk, renorm, sel, wf, nullptr, 0);
+  if (late) {
+    if (lane < topk) wf[(int64_t)t * topk + lane] = __builtin_nanf("");
+    if (lane == 0 && status) *status = I4_ERR_HANDOFF;
   }
 }
 
@@ -447,6 +527,30 @@ int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renor
   I4_TOPK_CASE(I4_F32, 2) I4_TOPK_CASE(I4_F32, 8)
 #undef I4_TOPK_CASE
   return I4_ERR_SHAPE;
+}
+
+int i4_launch_router_topk(const void* x, int xt, int T, int H, const void* wr, int E,
+                          const void* norm_w, float eps, void* xn, u32* lgt, const u32* epoch,
+                          int topk, int renorm, int32_t* sel, float* wf, void* pend, int n_pend,
+                          int32_t* status_reset, int32_t* status, int max_polls, hipStream_t s) {
+  if (T < 2 || T > 64 || E > 128 || E % 4 != 0 || topk > E) return I4_ERR_SHAPE;
+  const uint16_t* xin = (const uint16_t*)x;
+  if (norm_w) {
+    if (xt == I4_F16)
+      hipLaunchKernelGGL(k_rmsnorm_t<I4_F16>, dim3(T), dim3(256), 0, s, xin, H,
+                         (const uint16_t*)norm_w, eps, (uint16_t*)xn);
+    else
+      hipLaunchKernelGGL(k_rmsnorm_t<I4_BF16>, dim3(T), dim3(256), 0, s, xin, H,
+                         (const uint16_t*)norm_w, eps, (uint16_t*)xn);
+    xin = (const uint16_t*)xn;
+  }
+  const dim3 grid((E / 4) * T + (T + 3) / 4);
+  const size_t lds = (size_t)(H / 8) * 16;
+#define I4_RTK_CASE(XT_)                                                                        hipLaunchKernelGGL((k_router_topk_t<XT_>), grid, dim3(256), lds, s, xin, T, H,                                  (const uint16_t*)wr, E, lgt, epoch, topk, renorm, sel, wf, (u32x4*)pend,                      n_pend, status_reset, status, max_polls)
+  if (xt == I4_F16) I4_RTK_CASE(I4_F16);
+  else I4_RTK_CASE(I4_BF16);
+#undef I4_RTK_CASE
+  return hipGetLastError() == hipSuccess ? I4_OK : I4_ERR_LAUNCH;
 }
 
 extern "C" {
