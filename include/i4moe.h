@@ -279,11 +279,16 @@ size_t i4_moe_workspace_bytes(int T, int H, int I, int E, int topk);
  * projections run as one launch whose down workgroups wait, at most max_polls polls per
  * 128-column block, for the activations that the launch's gate_up workgroups write
  * (i4_moe_forward bounds it at 2^20, which a launch dispatched in block order never
- * reaches).  down_only != 0 launches the down workgroups alone, so every wait gives up:
+ * reaches).  down_only = 1 launches the down workgroups alone, so every wait gives up:
  * the rows they own come out NaN (so does out) and the status word at
  * i4_moe_status_offset(T, H, I, E, topk) holds I4_ERR_HANDOFF; every kernel still
- * exits.  For testing the bounded wait from the host.  I4_ERR_SHAPE outside 2..64
- * tokens or when gate_up and down use different group sizes (then nothing waits). */
+ * exits.  down_only = 2 bounds the routing launch's wait instead (router logits and
+ * top-k in one launch, whose ranking waves wait for their token's logits; the router
+ * in the block, E <= 128, E % 4 == 0, else I4_ERR_SHAPE) and launches its ranking
+ * waves alone: every routing weight, and so out, is NaN and the status word (not
+ * cleared first in this mode) holds I4_ERR_HANDOFF.  For testing the bounded waits
+ * from the host.  I4_ERR_SHAPE outside 2..64 tokens, for other modes, or when gate_up
+ * and down use different group sizes (then nothing waits). */
 int    i4_moe_forward_bounded(const void* x, int x_dtype, int T, const i4_moe_weights* weights,
                               int topk, int renorm, const void* logits, const void* residual,
                               void* out, void* workspace, size_t workspace_bytes, int max_polls,

@@ -38,12 +38,13 @@ int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renor
 // E % 4 == 0, else I4_ERR_SHAPE): lgt holds T E 4 bytes of (value pair, tag) words, epoch
 // the workspace word a later launch of the call advances (k_group); the routing goes to
 // sel / wf, pend as in i4_launch_topk; a ranking wave that gave up writes NaN weights and
-// I4_ERR_HANDOFF to *status; status_reset (nullable) is set to I4_OK first.
+// I4_ERR_HANDOFF to *status; status_reset (nullable) is set to I4_OK first.  rank_only:
+// the ranking waves alone (their waits give up), for testing the bound.
 int i4_launch_router_topk(const void* x, int xt, int T, int H, const void* wr, int E,
                           const void* norm_w, float eps, void* xn, uint32_t* lgt,
                           const uint32_t* epoch, int topk, int renorm, int32_t* sel, float* wf,
                           void* pend, int n_pend, int32_t* status_reset, int32_t* status,
-                          int max_polls, hipStream_t s);
+                          int max_polls, bool rank_only, hipStream_t s);
 
 // T = 1 router launch that first completes the previous layer of an XCD-local experts
 // launch: h = res + sum_k wts[k] ypart[k] (kc == 8 slot rows of H values), written to

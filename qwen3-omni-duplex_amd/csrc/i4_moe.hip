@@ -384,14 +384,15 @@ int check_moe(const i4_moe_weights* mw, int x_dtype, int T, int topk, i4_qweight
 
 // reset: this chunk's first kernel clears the status word (the first chunk of
 // a call, the first layer of a stack), so a later give-up is not overwritten
-// max_polls / down_only: the bound of the T <= 64 fused launch's wait, and that launch's
-// down workgroups alone (i4_moe_forward_bounded)
+// max_polls / mode (i4_moe_forward_bounded): the bound of the T <= 64 waits; mode 1: the
+// grouped launch's down workgroups alone, 2: the routing launch's ranking waves alone
 int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_qweight& gu,
               const i4_qweight& dn, const i4_qweight& tg, const i4_qweight& td, int topk,
               int renorm, const void* logits, const void* residual, void* out, int32_t* sel_out,
               float* w_out, const MoeWs& ws, bool reset, hipStream_t s,
-              int max_polls = kHandoffPolls, bool down_only = false) {
-  int32_t* st_reset = reset ? ws.status : nullptr;
+              int max_polls = kHandoffPolls, int mode = 0) {
+  const bool down_only = mode == 1, rank_only = mode == 2;
+  int32_t* st_reset = reset && !rank_only ? ws.status : nullptr;
   const int H = gu.K, I = dn.K, E = gu.E;
   MoeOps ops;
   if (!pick_ops(xt, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
@@ -441,8 +442,8 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   if (fused) {
     rc = i4_launch_router_topk(x, xt, T, H, mw->router_w, E, mw->norm_w, mw->norm_eps,
                                mw->norm_w ? ws.xn : nullptr, (u32*)ws.logits, ws.epoch, topk,
-                               renorm, sel, wts, pend, n_pend, st_reset, ws.status, kHandoffPolls,
-                               s);
+                               renorm, sel, wts, pend, n_pend, st_reset, ws.status,
+                               rank_only ? max_polls : kHandoffPolls, rank_only, s);
     if (rc) return rc;
     if (mw->norm_w) x = ws.xn;
     st_reset = nullptr;
@@ -474,7 +475,7 @@ int moe_chunk(const void* x, int xt, int T, const i4_moe_weights* mw, const i4_q
   const int max_b = (E < Tk / (MF_SMALL + 1) ? E : Tk / (MF_SMALL + 1)) + Tk / MF_TOK + 1;
   if (gd) {
     rc = ops.mfma_gd(max_s, x, T, topk, ws.entries, ws.n_entries, ws.perm, tgu, tdn, I, ws.act,
-                     ws.ys, ws.status, max_polls, down_only, s);
+                     ws.ys, ws.status, rank_only ? kHandoffPolls : max_polls, down_only, s);
     if (rc) return rc;
   } else if (one_list) {
     rc = ops.mfma_gate_up(true, max_s, x, T, topk, ws.entries, ws.n_entries, ws.perm, tgu, I,
@@ -512,7 +513,7 @@ int moe_forward_impl(const void* x, int x_dtype, int T, const i4_moe_weights* we
                      int renorm, const void* logits, const void* residual, void* out,
                      int32_t* sel_out, float* w_out, void* workspace, size_t workspace_bytes,
                      bool reset, hipStream_t stream, int32_t* status = nullptr,
-                     int max_polls = kHandoffPolls, bool down_only = false) {
+                     int max_polls = kHandoffPolls, int mode = 0) {
   i4_qweight gu, dn, tg, td;
   int rc = check_moe(weights, x_dtype, T, topk, &gu, &dn, &tg, &td);
   if (rc) return rc;
@@ -537,7 +538,7 @@ int moe_forward_impl(const void* x, int x_dtype, int T, const i4_moe_weights* we
     rc = moe_chunk(xs, x_dtype, Tc, weights, gu, dn, tg, td, topk, renorm, lg, rs, os,
                    sel_out ? sel_out + (size_t)t0 * topk : nullptr,
                    w_out ? w_out + (size_t)t0 * topk : nullptr, ws, reset && t0 == 0, stream,
-                   max_polls, down_only);
+                   max_polls, mode);
     if (rc) return rc;
   }
   return I4_OK;
@@ -718,13 +719,17 @@ int i4_moe_forward_bounded(const void* x, int x_dtype, int T, const i4_moe_weigh
                            int down_only, hipStream_t stream) {
   if (!weights) return I4_ERR_NULL;
   // only the fused T <= 64 launch waits: 2..64 tokens, one group size for both projections
-  if (T < 2 || T > ONE_LIST_T || max_polls < 0) return I4_ERR_SHAPE;
+  if (T < 2 || T > ONE_LIST_T || max_polls < 0 || down_only < 0 || down_only > 2)
+    return I4_ERR_SHAPE;
   const i4_qweight& g = weights->gate_up_tile.packed ? weights->gate_up_tile : weights->gate_up;
   const i4_qweight& d = weights->down_tile.packed ? weights->down_tile : weights->down;
   if (g.group != d.group) return I4_ERR_SHAPE;
+  // mode 2 needs the fused routing launch: the router in the block, E <= 128, E % 4 == 0
+  if (down_only == 2 && (!weights->router_w || logits || g.E > 128 || g.E % 4 != 0))
+    return I4_ERR_SHAPE;
   return moe_forward_impl(x, x_dtype, T, weights, topk, renorm, logits, residual, out, nullptr,
                           nullptr, workspace, workspace_bytes, true, stream, nullptr, max_polls,
-                          down_only != 0);
+                          down_only);
 }
 
 

@@ -349,14 +349,17 @@ __device__ inline u32 route_tag(u32 e) { return (2u * e + 1u) * 0x9E3779B1u; }
 // pend (n_pend 16-byte units) to the pending pattern for the grouped launch.  Only the
 // later blocks wait, and only for earlier ones.  A later launch of the call (k_group)
 // advances *epoch, so the next call's words carry another tag and no pending pattern is
-// needed here.  status_reset (nullable) gets I4_OK from block 0 first.
+// needed here.  status_reset (nullable) gets I4_OK from block 0 first.  rank_only: the
+// ranking blocks alone (no router blocks; every wait then gives up), for testing the
+// bounded wait from the host.
 template <int XT>
 __global__ __launch_bounds__(256) void k_router_topk_t(
     const uint16_t* __restrict__ x, int T, int H, const uint16_t* __restrict__ wr, int E,
     u32* lgt, const u32* __restrict__ epoch, int topk, int renorm,
     int32_t* __restrict__ sel, float* __restrict__ wf, u32x4* __restrict__ pend, int n_pend,
-    int32_t* __restrict__ status_reset, int32_t* __restrict__ status, int max_polls) {
-  const int G = E >> 2, nr = G * T;
+    int32_t* __restrict__ status_reset, int32_t* __restrict__ status, int max_polls,
+    int rank_only) {
+  const int G = E >> 2, nr = rank_only ? 0 : G * T;
   const int b = blockIdx.x;
   const u32 tag = route_tag(__builtin_amdgcn_readfirstlane(*epoch));
   if (b < nr) {
@@ -532,7 +535,8 @@ int i4_launch_topk(const void* logits, int lt, int T, int E, int topk, int renor
 int i4_launch_router_topk(const void* x, int xt, int T, int H, const void* wr, int E,
                           const void* norm_w, float eps, void* xn, u32* lgt, const u32* epoch,
                           int topk, int renorm, int32_t* sel, float* wf, void* pend, int n_pend,
-                          int32_t* status_reset, int32_t* status, int max_polls, hipStream_t s) {
+                          int32_t* status_reset, int32_t* status, int max_polls, bool rank_only,
+                          hipStream_t s) {
   if (T < 2 || T > 64 || E > 128 || E % 4 != 0 || topk > E) return I4_ERR_SHAPE;
   const uint16_t* xin = (const uint16_t*)x;
   if (norm_w) {
@@ -544,9 +548,9 @@ int i4_launch_router_topk(const void* x, int xt, int T, int H, const void* wr, i
                          (const uint16_t*)norm_w, eps, (uint16_t*)xn);
     xin = (const uint16_t*)xn;
   }
-  const dim3 grid((E / 4) * T + (T + 3) / 4);
+  const dim3 grid((rank_only ? 0 : (E / 4) * T) + (T + 3) / 4);
   const size_t lds = (size_t)(H / 8) * 16;
-#define I4_RTK_CASE(XT_)                                                                        hipLaunchKernelGGL((k_router_topk_t<XT_>), grid, dim3(256), lds, s, xin, T, H,                                  (const uint16_t*)wr, E, lgt, epoch, topk, renorm, sel, wf, (u32x4*)pend,                      n_pend, status_reset, status, max_polls)
+#define I4_RTK_CASE(XT_)                                                                        hipLaunchKernelGGL((k_router_topk_t<XT_>), grid, dim3(256), lds, s, xin, T, H,                                  (const uint16_t*)wr, E, lgt, epoch, topk, renorm, sel, wf, (u32x4*)pend,                      n_pend, status_reset, status, max_polls, (int)rank_only)
   if (xt == I4_F16) I4_RTK_CASE(I4_F16);
   else I4_RTK_CASE(I4_BF16);
 #undef I4_RTK_CASE

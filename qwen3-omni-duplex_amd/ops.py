@@ -289,7 +289,7 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
                 return_routing: bool = False, workspace: Workspace | None = None,
                 norm_w: torch.Tensor | None = None, norm_eps: float = 1e-6,
                 gate_up_tile: QWeight | None = None, down_tile: QWeight | None = None,
-                _bounded: tuple[int, bool] | None = None):
+                _bounded: tuple[int, int] | None = None):
     """One int4 MoE block: out = residual + sum_j w_j down_e(silu(gate_e xn) * up_e xn).
 
     xn = x, or RMSNorm(x) with weight norm_w (the decoder's post-attention norm).
@@ -333,12 +333,15 @@ def moe_forward(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
 
 
 def moe_forward_bounded(x: torch.Tensor, gate_up: QWeight, down: QWeight, top_k: int,
-                        max_polls: int, down_only: bool = False, **kw) -> torch.Tensor:
-    """moe_forward for 2..64 tokens with the bound of the fused launch's in-launch wait
-    given (i4_moe_forward_bounded); down_only launches its down workgroups alone, so
-    every wait gives up (NaN out, I4_ERR_HANDOFF in the status word).  For testing the
-    bounded wait from the host."""
-    return moe_forward(x, gate_up, down, top_k, _bounded=(max_polls, down_only), **kw)
+                        max_polls: int, down_only: bool = False, rank_only: bool = False,
+                        **kw) -> torch.Tensor:
+    """moe_forward for 2..64 tokens with the bound of an in-launch wait given
+    (i4_moe_forward_bounded): the grouped experts launch's, whose down workgroups
+    down_only launches alone; or, with rank_only, the routing launch's, whose ranking waves
+    it launches alone.  Either way every wait gives up (NaN out, I4_ERR_HANDOFF in the
+    status word).  For testing the bounded waits from the host."""
+    mode = 2 if rank_only else (1 if down_only else 0)
+    return moe_forward(x, gate_up, down, top_k, _bounded=(max_polls, mode), **kw)
 
 
 def moe_status(workspace: Workspace, T: int, H: int, I: int, E: int, top_k: int) -> int:

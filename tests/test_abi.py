@@ -192,12 +192,15 @@ def test_moe_validation_codes(pkg):
     # the bounded form takes the fused 2..64-token launch only, checked before any launch
     ws32 = lib.i4_moe_workspace_bytes(32, 2048, 768, 128, 8)
     bnd = lambda **kw: lib.i4_moe_forward_bounded(
-        0x30000, 1, kw.get("T", 32), kw.get("mw", ctypes.byref(mw)), 8, 1, None, None, 0x70000,
-        0x100000, kw.get("wsb", ws32), kw.get("polls", 3), 1, None)
+        0x30000, 1, kw.get("T", 32), kw.get("mw", ctypes.byref(mw)), 8, 1, kw.get("lg"), None,
+        0x70000, 0x100000, kw.get("wsb", ws32), kw.get("polls", 3), kw.get("mode", 1), None)
     assert bnd(mw=None) == -1
     assert bnd(T=1) == -2
     assert bnd(T=65) == -2
     assert bnd(polls=-1) == -2
+    assert bnd(mode=3) == -2 and bnd(mode=-1) == -2
+    # mode 2 bounds the fused routing launch, which needs the router in the block
+    assert bnd(mode=2, lg=0x90000) == -2
     assert bnd(wsb=ws32 - 1) == -7
     g64 = _lib.MoeWeightsC(gate_up=gu, down=_qw(_lib, E=128, N=2048, K=768, group=64, layout=2),
                            router_w=0x60000)

@@ -797,9 +797,10 @@ def test_moe_m32(pkg, dev):
 
 def test_moe_m32_fused_wait_gives_up_visibly(pkg, dev):
     """At T <= 64 both expert projections share one launch whose down workgroups wait for
-    the activations of its gate_up workgroups.  i4_moe_forward_bounded runs the down
-    workgroups alone with the bound lowered from the host: every wait gives up, the output
-    is NaN and the status word holds I4_ERR_HANDOFF, and every kernel exits.  The next
+    the activations of its gate_up workgroups, and router and top-k share one whose ranking
+    waves wait for their token's logits.  i4_moe_forward_bounded runs the down workgroups
+    (or the ranking waves) alone with the bound lowered from the host: every wait gives up,
+    the output is NaN and the status word holds I4_ERR_HANDOFF, and every kernel exits.  The next
     ordinary call on the same workspace is correct (against the oracle) and clears the
     word; the bounded call with its producers present and the full bound equals it bit for
     bit."""
@@ -814,6 +815,14 @@ def test_moe_m32_fused_wait_gives_up_visibly(pkg, dev):
     for polls in (0, 3):
         y = pkg.ops.moe_forward_bounded(x, moe.gate_up, moe.down, moe.top_k, polls, True,
                                         router_w=moe.router_w, residual=x, workspace=ws, **tiles)
+        torch.cuda.synchronize()
+        assert torch.isnan(y.float()).all()
+        assert pkg.moe_status(ws, T, 2048, I, E, moe.top_k) == -10
+    # the routing launch's ranking waves alone: their waits for the logits give up too
+    for polls in (0, 3):
+        y = pkg.ops.moe_forward_bounded(x, moe.gate_up, moe.down, moe.top_k, polls,
+                                        rank_only=True, router_w=moe.router_w, residual=x,
+                                        workspace=ws, **tiles)
         torch.cuda.synchronize()
         assert torch.isnan(y.float()).all()
         assert pkg.moe_status(ws, T, 2048, I, E, moe.top_k) == -10
