@@ -430,6 +430,7 @@ __device__ inline bool poll_row_xcd(Stager<XT, 256>& st, const uint16_t* src, in
     }
   };
   issue();
+  __builtin_amdgcn_sched_barrier(0);  // the loads go out before mid()'s work
   mid();
   for (int it = 0;; ++it) {
     bool pend = false;
