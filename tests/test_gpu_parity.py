@@ -795,6 +795,23 @@ def test_moe_m32(pkg, dev):
     _check_moe(pkg, moe, dgu, ddn, x, "f16", dev, residual=x)
 
 
+@pytest.mark.parametrize("xdt,T,E", [("f16", 2, 128), ("bf16", 64, 128), ("f16", 9, 20)])
+def test_moe_fused_routing_edges(pkg, dev, xdt, T, E):
+    """Router and top-k as one launch (2..64 tokens, E <= 128, E % 4 == 0) at its
+    token-count edges and with E not a multiple of 8, after the block's input RMSNorm:
+    routing bit-exact against the oracle's top-k of the GPU's own logits, the normalised
+    input against the oracle's RMSNorm, outputs against the oracle."""
+    rng = np.random.default_rng(300 + T + E)
+    sdt = "bf16" if xdt == "bf16" else np.float16
+    moe, dgu, ddn, _ = _awq_moe(pkg, dev, rng, E=E, sdt=sdt)
+    if xdt == "bf16":
+        moe.router_w = moe.router_w.to(torch.bfloat16)
+    nw = rng.uniform(0.5, 1.5, 2048).astype(np.float32)
+    nw = i4ref.f32_to_bf16_bits(nw) if xdt == "bf16" else nw.astype(np.float16)
+    x = make_x(rng, (T, 2048), xdt)
+    _check_moe(pkg, moe, dgu, ddn, x, xdt, dev, residual=x, norm=(nw, 1e-6))
+
+
 def test_moe_m32_fused_wait_gives_up_visibly(pkg, dev):
     """At T <= 64 both expert projections share one launch whose down workgroups wait for
     the activations of its gate_up workgroups, and router and top-k share one whose ranking
