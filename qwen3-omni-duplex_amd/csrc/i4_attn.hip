@@ -317,16 +317,23 @@ __device__ inline u32 qkv_tag(u32 e) { return (2u * e + 1u) * 0x9E3779B1u; }
 // wait, and only for earlier ones, so a launch whose workgroups are dispatched in
 // block order completes.
 struct QkvProj {
-  const uint16_t* h;   // the layer's input row
+  const uint16_t* h;   // the layer's input row (with y: the previous layer's h2)
   const uint16_t* nw;  // input RMSNorm weight
   float eps;
   const int32_t* packed;
   const void* scale;
   const int32_t* zeros;
   int N, K, gshift, n_proj;
+  // nullable: the previous layer's slot outputs [8][K] and routing weights [8]; the input
+  // row is then h + sum_k w[k] y[k] (K = 2048), written to h_out by the first workgroup
+  const uint16_t* y = nullptr;
+  const float* w = nullptr;
+  uint16_t* h_out = nullptr;
 };
 
-template <int XT, int ST, int L, int GQ>
+// COMP: the projection rows complete their input first (QkvProj::y, the decode step's
+// XCD-local experts); a kernel of its own, so the plain form keeps its registers
+template <int XT, int ST, int L, int GQ, bool COMP = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XT == I4_F16 ? 4 : 3))) void k_qkv_chunk(
     QkvProj pr, u32* qkv, const u32* __restrict__ epoch, int nq, int nkv,
     const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, float eps,
@@ -338,9 +345,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XT == I4_F1
   const int b = blockIdx.x;
   const u32 tag = qkv_tag(__builtin_amdgcn_readfirstlane(*epoch));
   if (b < pr.n_proj) {
-    gemv_ct_body<XT, ST, L, true, false, true, true>(
-        b, 0, pr.h, 0, pr.packed, 0, pr.scale, 0, pr.zeros, 0, nullptr, 1, pr.N, pr.K,
-        pr.gshift, qkv, XT, nullptr, pr.nw, pr.eps, lds, 0, nullptr, tag);
+    if constexpr (COMP)
+      gemv_ct_body<XT, ST, L, true, false, true, true, true>(
+          b, 0, pr.h, 0, pr.packed, 0, pr.scale, 0, pr.zeros, 0, nullptr, 1, pr.N, pr.K,
+          pr.gshift, qkv, XT, nullptr, pr.nw, pr.eps, lds, 0, nullptr, tag, pr.y, pr.w,
+          pr.h_out);
+    else
+      gemv_ct_body<XT, ST, L, true, false, true, true>(
+          b, 0, pr.h, 0, pr.packed, 0, pr.scale, 0, pr.zeros, 0, nullptr, 1, pr.N, pr.K,
+          pr.gshift, qkv, XT, nullptr, pr.nw, pr.eps, lds, 0, nullptr, tag);
     return;
   }
   const int cb = b - pr.n_proj;
@@ -447,6 +460,7 @@ struct RFold {
   int32_t* status;
   int E;
   int n_o;  // o_proj workgroups
+  uint16_t* y_copy = nullptr;  // nullable: y as the router read it, for a later launch
 };
 
 // y is not __restrict__: the router waves poll it, and a restrict pointer would let
@@ -489,7 +503,8 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
       const int e = rb * 4 + (t >> 6);  // wave-uniform
       if (e >= r.E) return;
       bool late = false;
-      router_wave<XT, true, RH, true>(y, r.wr, e, r.nw, r.eps, r.xn, r.logits, max_polls, &late);
+      router_wave<XT, true, RH, true>(y, r.wr, e, r.nw, r.eps, r.xn, r.logits, max_polls, &late,
+                                      r.y_copy);
       if (late && (t & 63) == 0) *r.status = I4_ERR_HANDOFF;
       return;
     }
@@ -601,7 +616,9 @@ int attn_launch(const void* qkv, int nq, int nkv, const void* qn_w, const void* 
     int32_t* pst = o->route ? o->route->status : o->status;
 #define I4_QC_CASE(ST_, G_)                                                                   \
   if (o->proj_st == ST_ && gq / gsplit == G_)                                                 \
-    hipLaunchKernelGGL((k_qkv_chunk<XT, ST_, 32, G_>), fgrid, dim3(256), lds, s, pr,          \
+    hipLaunchKernelGGL(pr.y ? (k_qkv_chunk<XT, ST_, 32, G_, true>)                           \
+                            : (k_qkv_chunk<XT, ST_, 32, G_, false>),                          \
+                       fgrid, dim3(256), lds, s, pr,                                          \
                        (u32*)qkv, epoch, nq, nkv, (const uint16_t*)qn_w,                      \
                        (const uint16_t*)kn_w,                                                 \
                        eps, pos_dev, pos, max_len, rt, (uint16_t*)k_cache, (uint16_t*)v_cache, \
@@ -855,7 +872,9 @@ size_t i4_thinker_decode_step_workspace_bytes(int n_heads, int n_kv_heads, int h
                                               int max_len, int H, int I, int E, int topk) {
   const size_t b =
       i4_thinker_layer_workspace_bytes(n_heads, n_kv_heads, head_dim, max_len, H, I, E, topk);
-  return b ? b + i4::al256((size_t)H * 2) : 0;  // + the hidden state between layers
+  // + the hidden state between layers, a copy of the attention output and the slot
+  // outputs of the XCD-local experts launch
+  return b ? b + 2 * i4::al256((size_t)H * 2) + i4::al256((size_t)8 * H * 2) : 0;
 }
 
 // One layer's checks (every one made before any launch) and its launches.
@@ -899,21 +918,33 @@ static int layer_check(const i4_thinker_layer& L, int x_dtype, int n_heads, int 
 
 // h -> out through one layer; reset: the chunk launch clears the status word.  The
 // projection runs in the chunk launch where its shape allows (i4::qkv_fusable).
+// XCD-local form (decode step): with slot_y the layer's input is completed in the chunk
+// launch, h + sum_k slot_w[k] slot_y[k], and written to h_out (the attention's residual);
+// with ypart the experts launch is the XCD-local one, its slot outputs to ypart (the next
+// layer completes them) instead of out.
 static int layer_launch(const i4_thinker_layer& L, const LayerOk& c, int x_dtype,
                         int n_heads, int n_kv_heads, const float* inv_freq,
                         const int32_t* pos_dev, int pos, int max_len, int topk, int renorm,
                         const void* h, bool reset, void* out, void* workspace,
-                        hipStream_t stream) {
+                        hipStream_t stream, const void* slot_y = nullptr,
+                        const float* slot_w = nullptr, void* h_out = nullptr,
+                        void* ypart = nullptr, void* h2_copy = nullptr) {
   char* ws = (char*)workspace;
   void* qkv = ws + c.l.qkv;
   void* h2 = ws + c.l.h2;
   int rc;
   const bool fused = i4::qkv_fusable(c.qw);
+  if (slot_y && (!fused || c.qw.K != 2048)) return I4_ERR_SHAPE;
   i4::QkvProj pr;
   if (fused) {
     const i4_qweight& qw = c.qw;
     pr = i4::QkvProj{(const uint16_t*)h, (const uint16_t*)L.in_norm_w, L.eps, qw.packed,
                      qw.scale, qw.zeros, qw.N, qw.K, i4_group_shift(qw.group), (qw.N + 7) / 8};
+    if (slot_y) {
+      pr.y = (const uint16_t*)slot_y;
+      pr.w = slot_w;
+      pr.h_out = (uint16_t*)h_out;
+    }
   } else {
     rc = i4_rmsnorm_linear(h, x_dtype, 1, L.in_norm_w, L.eps, &c.qw, nullptr, qkv, x_dtype,
                            stream);
@@ -922,6 +953,7 @@ static int layer_launch(const i4_thinker_layer& L, const LayerOk& c, int x_dtype
   i4::RFold r{(const uint16_t*)L.moe.router_w, (const uint16_t*)L.moe.norm_w,
               L.moe.norm_eps, c.mb.xn, c.mb.logits, c.mb.act, c.mb.n_act, c.mb.status,
               c.mb.E, 0};
+  r.y_copy = (uint16_t*)h2_copy;  // the next layer completes its input from it
   i4::OLaunch o;
   if (fused) {
     o.proj = &pr;
@@ -930,7 +962,7 @@ static int layer_launch(const i4_thinker_layer& L, const LayerOk& c, int x_dtype
   const i4_qweight& ow = c.ow;
   o.w = i4::OProj{ow.packed, ow.scale, ow.zeros, ow.N, ow.K, i4_group_shift(ow.group)};
   o.st = ow.scale_dtype;
-  o.residual = h;
+  o.residual = slot_y ? h_out : h;
   o.y = h2;
   o.route = &r;
   o.reset_status = reset;
@@ -938,6 +970,7 @@ static int layer_launch(const i4_thinker_layer& L, const LayerOk& c, int x_dtype
                   inv_freq, pos_dev, pos, L.k_cache, L.v_cache, max_len, h2, ws + c.l.part,
                   c.l.h2 - c.l.part, stream, &o);
   if (rc) return rc;
+  if (ypart) return i4::moe_decode_experts_x(c.mb, x_dtype, topk, renorm, ypart, workspace, stream);
   return i4::moe_decode_experts(c.mb, x_dtype, topk, renorm, h2, out, workspace, stream);
 }
 
@@ -986,17 +1019,44 @@ int i4_thinker_decode_step(const void* h, int x_dtype, const i4_thinker_layer* l
     if (l && (c.mb.H != c0.mb.H || c.mb.I != c0.mb.I || c.mb.E != c0.mb.E)) return I4_ERR_SHAPE;
   }
   // the hidden state between layers: one buffer serves them all (a layer reads its input
-  // in its first three launches and writes its output in the fourth)
-  if (workspace_bytes < c0.l.bytes + i4::al256((size_t)c0.mb.H * 2)) return I4_ERR_WORKSPACE;
+  // in its first three launches and writes its output in the fourth); then the slot outputs
+  const size_t hb = i4::al256((size_t)c0.mb.H * 2);
+  if (workspace_bytes < c0.l.bytes + 2 * hb + i4::al256((size_t)8 * c0.mb.H * 2))
+    return I4_ERR_WORKSPACE;
   void* hbuf = (char*)workspace + c0.l.bytes;
-  const void* cur = h;
-  for (int l = 0; l < n_layers; ++l) {
-    void* dst = l == n_layers - 1 ? out : hbuf;
+  // the attention output h2 as the MoE router read it (the h2 buffer itself is set
+  // pending by the next layer's chunk launch, whose projection rows read this copy)
+  void* h2c = (char*)hbuf + hb;
+  void* ypart = (char*)h2c + hb;
+  // XCD-local experts launches (every slot's gate_up and down on one XCD, 1.2 us faster
+  // than the single-block launch) where every layer allows: each layer but the last leaves
+  // its slot outputs, and the next layer's chunk launch completes them into its input row
+  // before the input norm (the stack's completion arithmetic: the same h bit for bit)
+  bool xl = n_layers > 1 && topk <= 8 && c0.mb.H == 2048 &&
+            i4::moe_m1x_ct_fits(topk, c0.mb.H, c0.mb.I);
+  for (int l = 0; l < n_layers && xl; ++l) {
     int rc = layer_check(layers[l], x_dtype, n_heads, n_kv_heads, head_dim, inv_freq, pos_dev,
                          pos, max_len, topk, workspace, workspace_bytes, 0, &c);
     if (rc) return rc;
-    rc = layer_launch(layers[l], c, x_dtype, n_heads, n_kv_heads, inv_freq, pos_dev, pos,
-                      max_len, topk, renorm, cur, l == 0, dst, workspace, stream);
+    xl = i4::qkv_fusable(c.qw) && c.qw.K == 2048;
+  }
+  const void* cur = h;
+  for (int l = 0; l < n_layers; ++l) {
+    const bool last = l == n_layers - 1;
+    void* dst = last ? out : hbuf;
+    int rc = layer_check(layers[l], x_dtype, n_heads, n_kv_heads, head_dim, inv_freq, pos_dev,
+                         pos, max_len, topk, workspace, workspace_bytes, 0, &c);
+    if (rc) return rc;
+    if (xl) {
+      // layer l > 0 completes the previous layer's h2 (the copy its router wrote)
+      rc = layer_launch(layers[l], c, x_dtype, n_heads, n_kv_heads, inv_freq, pos_dev, pos,
+                        max_len, topk, renorm, l ? h2c : h, l == 0, out, workspace, stream,
+                        l ? ypart : nullptr, l ? c.mb.w : nullptr, l ? hbuf : nullptr,
+                        last ? nullptr : ypart, last ? nullptr : h2c);
+    } else {
+      rc = layer_launch(layers[l], c, x_dtype, n_heads, n_kv_heads, inv_freq, pos_dev, pos,
+                        max_len, topk, renorm, cur, l == 0, dst, workspace, stream);
+    }
     if (rc) return rc;
     cur = dst;
   }

@@ -11,6 +11,7 @@
 #pragma once
 
 #include "i4_common.h"
+#include "i4_router_body.h"
 
 namespace i4 {
 
@@ -33,15 +34,24 @@ static constexpr int GEMV_ROUND = 4;  // chunks per lane whose loads are in flig
 // two rows, every pair of the workgroup's rows stored with `tag` (N a multiple of the
 // workgroup's RPW rows): the readers wait for the tag of their call, so the buffer
 // needs no pending pattern.
-template <int XT, int ST, int L, bool NORM, bool POLL, bool HANDOFF = false, bool TAG = false>
+// COMP (with NORM, K = 2048): x is the residual row of a decode layer whose experts left
+// one output row per slot (slot_y [8][K], routing weights slot_w [8]); the row is
+// completed first, x + sum_k w[k] y[k] (slot_sum8: the single-launch combine's arithmetic,
+// so equal to it bit for bit), its loads issued ahead of the weight stream, and workgroup
+// bx = 0 writes the completed row to h_out.
+template <int XT, int ST, int L, bool NORM, bool POLL, bool HANDOFF = false, bool TAG = false,
+          bool COMP = false>
 __device__ __forceinline__ void gemv_ct_body(
     int bx, int j, const uint16_t* __restrict__ x, int64_t x_stride,
     const int32_t* __restrict__ packed, int64_t p_es, const void* __restrict__ scale,
     int64_t s_es, const int32_t* __restrict__ zeros, int64_t z_es,
     const int32_t* __restrict__ sel, int E, int N, int K, int gshift, void* __restrict__ out,
     int ot, const void* __restrict__ bias, const uint16_t* __restrict__ nw, float eps,
-    unsigned char* lds, int max_polls, int32_t* __restrict__ status = nullptr, u32 tag = 0) {
+    unsigned char* lds, int max_polls, int32_t* __restrict__ status = nullptr, u32 tag = 0,
+    const uint16_t* __restrict__ slot_y = nullptr, const float* __restrict__ slot_w = nullptr,
+    uint16_t* __restrict__ h_out = nullptr) {
   constexpr int WG = GEMV_WG, ROUND = GEMV_ROUND;
+  static_assert(!COMP || (NORM && !POLL), "the completed row is normalised as it is staged");
   static_assert(!(NORM && POLL), "a polled row is used as it arrives");
   static_assert(!TAG || HANDOFF, "tags belong to a hand-over");
   constexpr int RPW = WG / L;
@@ -72,7 +82,20 @@ __device__ __forceinline__ void gemv_ct_body(
   const u32 mg = magic_v<XT>();
   Stager<XT> st(1, K);  // activation loads first, weight loads behind them
   auto row_of = [&](int) { return xrow; };
-  if constexpr (!POLL) st.issue(row_of, 0);
+  // COMP: thread t's word of the residual row and of the 8 slot rows (K = 2048: one word)
+  u32x4 cres, cy[COMP ? 8 : 1];
+  float cw[COMP ? 8 : 1];
+  if constexpr (COMP) {
+    const int idx = (int)threadIdx.x;
+    cres = ldg16(xrow + 8 * idx);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      cy[k] = ldg16(slot_y + (int64_t)k * K + 8 * idx);
+      cw[k] = slot_w[k];
+    }
+  } else if constexpr (!POLL) {
+    st.issue(row_of, 0);
+  }
   u32x4 gv[2];
   if constexpr (NORM) {
 #pragma unroll
@@ -88,6 +111,11 @@ __device__ __forceinline__ void gemv_ct_body(
   // The activation row is staged once, after the first round's weight loads are issued.
   auto stage = [&]() {
     if constexpr (POLL) late = poll_rows<XT>(st, xrow, max_polls);
+    if constexpr (COMP) {
+      st.d[0] = slot_sum8<XT, 8>(cres, cy, cw);
+      st.d[1] = st.d[0];  // K = 2048: one word per thread
+      if (h_out && bx == 0) *(u32x4*)(h_out + 8 * (int)threadIdx.x) = st.d[0];
+    }
     if constexpr (NORM) {
       __shared__ float s_ss[WG / 64];
       float ss = 0.f;

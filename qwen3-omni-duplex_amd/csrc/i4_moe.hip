@@ -568,6 +568,7 @@ int moe_decode_bufs(const i4_moe_weights* mw, int x_dtype, int topk, void* ws, s
   b->act = (u32x4*)w.act;
   b->n_act = topk * I / 8;
   b->status = w.status;
+  b->w = w.w;
   b->H = H;
   b->I = I;
   b->E = E;
@@ -587,6 +588,18 @@ int moe_decode_experts(const MoeDecodeBufs& b, int x_dtype, int topk, int renorm
   const GateUpArgs a{true, topk, topk, gu.E, renorm, w.xn, w.sel, w.logits, w.w, w.act, nullptr};
   const TW tg = to_tw(gu);
   return ops.moe_m1_ct(a, &tg, to_tw(dn), residual, out, w.status, kHandoffPolls, s);
+}
+
+int moe_decode_experts_x(const MoeDecodeBufs& b, int x_dtype, int topk, int renorm, void* ypart,
+                         void* ws, hipStream_t s) {
+  const i4_qweight& gu = b.gate_up;
+  const i4_qweight& dn = b.down;
+  if (!moe_m1x_ct_fits(topk, gu.K, dn.K)) return I4_ERR_SHAPE;
+  const MoeWs w = carve(ws, 1, gu.K, dn.K, gu.E, topk);
+  MoeOps ops;
+  if (!pick_ops(x_dtype, gu.scale_dtype, dn.scale_dtype, &ops)) return I4_ERR_DTYPE;
+  const GateUpArgs a{true, topk, topk, gu.E, renorm, w.xn, w.sel, w.logits, w.w, w.act, nullptr};
+  return ops.moe_m1x_ct(a, to_tw(gu), to_tw(dn), ypart, w.status, kHandoffPolls, false, s);
 }
 
 int moe_forward_status(const void* x, int x_dtype, int T, const i4_moe_weights* weights,

@@ -77,6 +77,7 @@ struct MoeDecodeBufs {
   u32x4* act;        // [topk * I] activations, n_act 16-byte words
   int n_act;
   int32_t* status;
+  float* w;          // [topk] routing weights the experts launch writes
   int H, I, E;
   i4_qweight gate_up, down;  // validated (i4_check_weight) CT weights
 };
@@ -87,6 +88,11 @@ int moe_decode_bufs(const i4_moe_weights* mw, int x_dtype, int topk, void* ws, s
 // The experts launch of that block: out = residual + MoE(xn) from the logits.
 int moe_decode_experts(const MoeDecodeBufs& b, int x_dtype, int topk, int renorm,
                        const void* residual, void* out, void* ws, hipStream_t s);
+// The XCD-local experts launch of that block (moe_m1x_ct_fits): the slot outputs to
+// ypart [topk][H] and the routing weights to b.w; a later launch completes the layer,
+// residual + sum_k w[k] ypart[k] (slot_sum8).
+int moe_decode_experts_x(const MoeDecodeBufs& b, int x_dtype, int topk, int renorm, void* ypart,
+                         void* ws, hipStream_t s);
 
 // Grouped (T > 1) expert projections on MFMA.  entries[i] = {expert, first
 // position, tokens, 0} of the expert-sorted (token, slot) list perm; small

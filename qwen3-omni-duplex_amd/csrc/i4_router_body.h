@@ -60,11 +60,13 @@ __device__ __forceinline__ void router_finish(u32x4 (&xv)[H / 512], const u32x4 
 // until no word is pending (at most max_polls times: then *late is set and the
 // logit is computed from whatever was read).  x is not __restrict__ here: the memory
 // clobber in the wait loop then keeps the loads inside it.
+// x_copy (nullable, POLL): expert 0's wave also writes the row as it read it there.
 template <int XT, bool NORM, int H, bool POLL>
 __device__ __forceinline__ void router_wave(const uint16_t* x, const uint16_t* __restrict__ wr, int e,
                                    const uint16_t* __restrict__ nw, float eps,
                                    uint16_t* __restrict__ xn_out, uint16_t* __restrict__ logits,
-                                   int max_polls = 0, bool* late = nullptr) {
+                                   int max_polls = 0, bool* late = nullptr,
+                                   uint16_t* __restrict__ x_copy = nullptr) {
   static_assert(H == 1024 || H == 2048, "one 512-value round per 64 lanes, 2 or 4 rounds");
   constexpr int NR = H / 512;  // lane l owns words l + 64 i, i < NR
   const int lane = threadIdx.x & 63;
@@ -87,6 +89,10 @@ __device__ __forceinline__ void router_wave(const uint16_t* x, const uint16_t* _
       }
       __builtin_amdgcn_s_sleep(1);
       asm volatile("" ::: "memory");
+    }
+    if (x_copy && e == 0) {
+#pragma unroll
+      for (int i = 0; i < NR; ++i) *(u32x4*)(x_copy + 8 * (lane + 64 * i)) = xv[i];
     }
   }
   router_finish<XT, NORM, H>(xv, gv, wv, e, eps, xn_out, logits);

@@ -357,7 +357,7 @@ def test_thinker_layer_validation_codes(pkg):
     # the decode step: the layer's workspace and the hidden state between layers; every
     # layer is checked before the first launch
     wss = lib.i4_thinker_decode_step_workspace_bytes(32, 4, 128, 4096, 2048, 768, 128, 8)
-    assert wss == wsb + 4096
+    assert wss == wsb + 2 * 4096 + 8 * 4096
     assert lib.i4_thinker_decode_step_workspace_bytes(32, 4, 128, 4096, 3072, 768, 128, 8) == 0
 
     def layer(**kw):
