@@ -537,7 +537,11 @@ typedef struct i4_thinker_layer {
  * in one call (the hidden state between layers stays in the workspace).  The
  * result and the caches equal i4_thinker_layer_decode applied layer by layer bit
  * for bit.  Every layer has the same head counts, H, I, E; the checks of all
- * layers come before the first launch.
+ * layers come before the first launch.  At H = 2048 with the stack's XCD-local
+ * experts launch available (top-8 or less), every layer but the last runs that
+ * launch instead of the single-block one (its slot outputs stay in the workspace)
+ * and the next layer's q|k|v launch completes them into its input row first, with
+ * the single-block combine's arithmetic: the same result bit for bit.
  * Workspace: i4_thinker_decode_step_workspace_bytes(), no initial contents,
  * 256-byte aligned; it begins with i4_moe_forward's T = 1 workspace, whose status
  * word (i4_moe_status_offset(1, H, I, E, topk)) is cleared by the first layer and
