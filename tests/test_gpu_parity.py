@@ -1054,6 +1054,37 @@ def test_stack_graph_replays_match_eager(pkg, dev):
         _ = (torch.randn(256, 256, device=dev) @ torch.randn(256, 256, device=dev)).sum().item()
 
 
+def test_moe_m32_graph_replays_match_eager(pkg, dev):
+    """The 32-token block (routing launch whose ranking waves wait for tagged logits, grouping,
+    the grouped experts launch, combine) captured in a hipGraph gives the eager result on
+    every replay, with other work and new inputs between replays: the tag epoch the
+    grouping launch advances makes each replay wait for its own logits."""
+    rng = np.random.default_rng(72)
+    moe, _, _, _ = _awq_moe(pkg, dev, rng)
+    tiles = dict(gate_up_tile=moe.gate_up_tile, down_tile=moe.down_tile)
+    ws = pkg.Workspace()
+    xs = [t_(make_x(rng, (32, 2048), "f16"), dev) for _ in range(3)]
+    run = lambda x: pkg.moe_forward(x, moe.gate_up, moe.down, moe.top_k, router_w=moe.router_w,
+                                    residual=x, workspace=ws, **tiles)
+    eager = [run(x).clone() for x in xs]
+    static_x = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(static_x)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = run(static_x)
+    for r in range(6):
+        static_x.copy_(xs[r % 3])
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[r % 3])
+        assert pkg.moe_status(ws, 32, 2048, moe.down.K, moe.gate_up.E, moe.top_k) == 0
+        _ = (torch.randn(256, 256, device=dev) @ torch.randn(256, 256, device=dev)).sum().item()
+
+
 @pytest.mark.parametrize("T", [1, 9])
 def test_router_logits_with_norm(pkg, dev, T):
     rng = np.random.default_rng(29 + T)
